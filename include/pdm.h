@@ -1,0 +1,205 @@
+/*
+ * pdm.h — C ABI of the MI355X (gfx950) embedding-lookup and OneTrans
+ * interaction forward path.
+ *
+ * Every entry point is extern "C", takes plain pointers and sizes, never
+ * throws, and returns a pdm_status (0 = OK, < 0 = error).  The text of the
+ * last error on the calling thread is available through pdm_last_error().
+ * All device work is enqueued on the caller's HIP stream; no entry point
+ * synchronises the host with the device except where stated.
+ *
+ * Pointers documented as "device" must point at memory of the current HIP
+ * device.  Inputs are never written.  Outputs are written completely.
+ */
+#ifndef PDM_H_
+#define PDM_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* pdm_stream_t; /* == hipStream_t */
+
+typedef enum {
+  PDM_OK = 0,
+  PDM_ERR_INVALID = -1,     /* bad argument (shape, dtype, null pointer, size) */
+  PDM_ERR_UNSUPPORTED = -2, /* valid but not implemented combination */
+  PDM_ERR_HIP = -3,         /* a HIP runtime call failed */
+  PDM_ERR_WORKSPACE = -4    /* workspace too small */
+} pdm_status;
+
+typedef enum {
+  PDM_F32 = 0,
+  PDM_F16 = 1,
+  PDM_BF16 = 2,
+  /* int8 rowwise: each row is [fp16 scale][fp16 bias][dim x uint8], the row
+   * stride is row_bytes (>= 4 + dim, multiple of 4).  Decode of element d:
+   * float(q[d]) * float(scale) rounded to fp32, then + float(bias) rounded
+   * to fp32 (two roundings, no fused multiply-add). */
+  PDM_I8_SB_F16 = 3
+} pdm_dtype;
+
+typedef enum { PDM_POOL_SUM = 0, PDM_POOL_MEAN = 1 } pdm_pooling;
+
+/* Version of this ABI (major * 10000 + minor * 100 + patch). */
+int32_t pdm_abi_version(void);
+
+/* Copies the last error message of the calling thread into buf (NUL
+ * terminated, truncated to n bytes).  Returns the full message length. */
+size_t pdm_last_error(char* buf, size_t n);
+
+/* ------------------------------------------------------------------------
+ * Table-batched pooled embedding forward.
+ *
+ * Replaces the forward of TorchRec EmbeddingBagCollection
+ * (primus_dlrm/models/embedding.py:118-120,151; primus_dlrm/models/dlrm.py:147)
+ * and of FBGEMM's table-batched embedding op op(indices, offsets) -> [B, sum D]
+ * (tests/test_fbgemm_tbe.py:23-35,52-65), including the masked sum/mean
+ * pooling written out at primus_dlrm/models/sharded_embedding.py:220-227 and
+ * the padding-id filter of _build_pooled_kjt (embedding.py:179-204).
+ * ------------------------------------------------------------------------ */
+
+typedef struct {
+  int64_t rows;           /* number of rows in the table */
+  int64_t weights_offset; /* byte offset of row 0 inside the weights buffer */
+  int32_t dim;            /* embedding dim (multiple of 4) */
+  int32_t dtype;          /* pdm_dtype of the stored rows */
+  int32_t pooling;        /* pdm_pooling */
+  int32_t row_bytes;      /* byte stride between rows; 0 = dense default */
+  int32_t out_offset;     /* first output column of this table */
+  int32_t reserved;
+} pdm_table_desc;
+
+typedef struct pdm_tbe_plan_s* pdm_tbe_plan;
+
+/* Validates the table list, uploads its metadata to the current device and
+ * groups tables by (dtype, dim) for launch.  Synchronous (one small copy). */
+int pdm_tbe_plan_create(const pdm_table_desc* tables, int32_t num_tables,
+                        pdm_tbe_plan* plan_out);
+int pdm_tbe_plan_destroy(pdm_tbe_plan plan);
+/* Sum of dims = number of output columns the plan writes (max out_offset+dim). */
+int64_t pdm_tbe_plan_total_dim(pdm_tbe_plan plan);
+
+/* weights:     device, base of all tables (byte addressed by weights_offset)
+ * indices:     device, int32 or int64 (index_bits = 32 | 64), num_indices long
+ * offsets:     device, int64 [T * B + 1], table-major: bag (t, b) is
+ *              indices[offsets[t*B+b] : offsets[t*B+b+1]]
+ * padding_idx: an index equal to it is skipped and not counted (-1 = none)
+ * out:         device, [B, out_row_stride] of out_dtype (F32 | F16 | BF16)
+ * err_flag:    optional device int32; set to 1 when an index is outside
+ *              [0, rows) (such indices are skipped, never read) or a bag's
+ *              offsets are not monotone / exceed num_indices.
+ * An empty bag (or one holding only padding) pools to 0 for sum and mean.
+ * Mean divides the fp32 sum by the count of pooled indices. */
+int pdm_tbe_pooled_fwd(pdm_tbe_plan plan, const void* weights,
+                       const void* indices, int32_t index_bits,
+                       int64_t num_indices, const int64_t* offsets,
+                       int64_t batch_size, int64_t padding_idx, void* out,
+                       int32_t out_dtype, int64_t out_row_stride,
+                       int32_t* err_flag, pdm_stream_t stream);
+
+/* Quantizes fp32 rows [rows, dim] (device) into int8 rowwise rows
+ * (PDM_I8_SB_F16 layout, row stride row_bytes) on the device:
+ * bias = fp16(min row), scale = fp16((max - bias) / 255) (1 when the range is
+ * 0), q = clamp(rint((x - bias) * (1 / scale)), 0, 255). */
+int pdm_int8_rowwise_quantize(const float* src, int64_t rows, int32_t dim,
+                              void* dst, int32_t row_bytes,
+                              pdm_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Jagged -> padded S-token sequence gather.
+ *
+ * Replaces the unpooled lookup TorchRec EmbeddingCollection.forward
+ * (embedding.py:156-172, onetrans.py:480-509), the per-pool concat of
+ * item|artist|album embeddings (onetrans.py:515-520) and the pool concat
+ * along the sequence (onetrans.py:553-558), with the host-side jagged->padded
+ * step of the data loader (primus_dlrm/data/dataset.py:604-636) moved onto
+ * the device.  A pool keeps its last min(len, max_len) events.
+ * ------------------------------------------------------------------------ */
+
+#define PDM_SEQ_MAX_POOLS 8
+#define PDM_SEQ_MAX_FEATURES 8
+
+typedef enum { PDM_PAD_ROW0 = 0, PDM_PAD_ZERO = 1 } pdm_pad_mode;
+typedef enum { PDM_ALIGN_RIGHT = 0, PDM_ALIGN_LEFT = 1 } pdm_align;
+
+typedef struct {
+  int32_t num_pools;    /* P <= PDM_SEQ_MAX_POOLS */
+  int32_t num_features; /* F <= PDM_SEQ_MAX_FEATURES (tables per event) */
+  int32_t dtype;        /* PDM_F32 | PDM_F16 | PDM_BF16, tables and output */
+  int32_t pad_mode;     /* pdm_pad_mode; ROW0 = reference (id 0 lookup) */
+  int32_t align;        /* pdm_align; RIGHT = reference (left padded) */
+  int32_t reserved;
+  int64_t batch_size;                         /* B */
+  int32_t max_len[PDM_SEQ_MAX_POOLS];         /* padded length per pool */
+  int32_t dim[PDM_SEQ_MAX_FEATURES];          /* dim per feature table */
+  int64_t rows[PDM_SEQ_MAX_FEATURES];         /* rows per feature table */
+  int64_t num_ids[PDM_SEQ_MAX_POOLS];         /* entries in each id array of
+                                                 pool p (offsets[p][B] <= it) */
+} pdm_seq_desc;
+
+/* tables:  [F] device pointers, dense row-major [rows, dim] of dtype
+ * ids:     [P * F] device pointers, int64, pool-major; ids[p*F+f] has
+ *          offsets[p][B] entries
+ * offsets: [P] device pointers, int64 [B + 1] per pool
+ * out:     device, [B, sum_p max_len[p], sum_f dim[f]] of dtype
+ * mask:    device, uint8 [B, sum_p max_len[p]] (1 = event, 0 = padding); may
+ *          be NULL
+ * err_flag: optional device int32, set to 1 on an id outside [0, rows)
+ *          (that slot is written as zeros) or bad offsets. */
+int pdm_seq_gather_fwd(const pdm_seq_desc* desc, const void* const* tables,
+                       const int64_t* const* ids,
+                       const int64_t* const* offsets, void* out,
+                       uint8_t* mask, int32_t* err_flag, pdm_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * OneTrans mixed-parameter interaction block forward (bf16 MFMA).
+ *
+ * Replaces OneTransBlock.forward(x, mask, q_len, n_s_tokens)
+ * (primus_dlrm/models/onetrans.py:207-231) run under autocast(bf16), with
+ * RMSNorm (:74-82), MixedAttention (:85-169) and MixedFFN (:172-204).  The
+ * mask must be the bottom-right causal pyramid mask of build_pyramid_mask
+ * (:62-67), which is the only mask the reference passes (:581-582).
+ * ------------------------------------------------------------------------ */
+
+typedef struct {
+  int32_t batch;    /* B */
+  int32_t d_model;  /* D (256 supported) */
+  int32_t n_heads;  /* H (D / H = 64 supported) */
+  int32_t n_ns;     /* NS tokens at the end of the sequence */
+  int32_t ffn_dim;  /* FFN hidden (multiple of 256) */
+  int32_t kv_len;   /* tokens in x */
+  int32_t q_len;    /* tokens kept (tail of x), n_ns <= q_len <= kv_len */
+  int32_t reserved;
+} pdm_block_desc;
+
+typedef struct {
+  const float* norm1_w;   /* fp32 [D] */
+  const void* s_qkv_w;    /* bf16 [3D, D]  (nn.Linear weight) */
+  const void* ns_qkv_w;   /* bf16 [NS, 3D, D] */
+  const void* out_w;      /* bf16 [D, D] */
+  const float* norm2_w;   /* fp32 [D] */
+  const void* s_w1;       /* bf16 [F, D] */
+  const void* s_w2;       /* bf16 [D, F] */
+  const void* ns_w1;      /* bf16 [NS, F, D] */
+  const void* ns_w2;      /* bf16 [NS, D, F] */
+} pdm_block_weights;
+
+/* Bytes of device workspace pdm_onetrans_block_fwd needs for desc. */
+int64_t pdm_onetrans_block_workspace_size(const pdm_block_desc* desc);
+
+/* x: device fp32 [B, kv_len, D] (the residual stream); y: device fp32
+ * [B, q_len, D]; workspace: device, >= pdm_onetrans_block_workspace_size. */
+int pdm_onetrans_block_fwd(const pdm_block_desc* desc, const float* x,
+                           const pdm_block_weights* w, float* y,
+                           void* workspace, int64_t workspace_bytes,
+                           pdm_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PDM_H_ */

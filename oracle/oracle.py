@@ -1,0 +1,220 @@
+"""NumPy front end of the C oracle (pdm_oracle.c).  TEST INFRASTRUCTURE ONLY.
+
+Only the parity tests, ``__graft_entry__.smoke()`` and the CPU-baseline leg
+of ``bench.py`` use this module, as the checker.  It restates the
+reference's lookup semantics on the CPU:
+
+* ``tbe_pooled``      pooled sum / mean per (table, bag) — primus_dlrm/models/
+                      sharded_embedding.py:220-227, padding filter embedding.py:188-194,
+                      table-major offsets tests/test_fbgemm_tbe.py:33-35.
+* ``int8_quantize``   int8 rowwise rows ([fp16 scale][fp16 bias][q]); the reference has
+                      no quantized path, so this restates FBGEMM's fused rowwise SB-half
+                      quantizer (fbgemm_gpu 1.5.0, absent here).
+* ``seq_gather``      jagged -> padded pools: data/dataset.py:604-626 (last L events,
+                      left pad with id 0), onetrans.py:515-520 (feature concat),
+                      onetrans.py:553-558 (pool concat).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import List, Optional, Sequence
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "_build", "liboracle.so")
+_lib = None
+
+F32, F16, BF16, I8 = 0, 1, 2, 3
+_DT = {"fp32": F32, "fp16": F16, "bf16": BF16, "int8": I8}
+_POOL = {"sum": 0, "mean": 1}
+
+
+class _Table(ctypes.Structure):
+    _fields_ = [("rows", ctypes.c_int64), ("weights_offset", ctypes.c_int64), ("dim", ctypes.c_int32),
+                ("dtype", ctypes.c_int32), ("pooling", ctypes.c_int32), ("row_bytes", ctypes.c_int32),
+                ("out_offset", ctypes.c_int32), ("reserved", ctypes.c_int32)]
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            raise RuntimeError(f"{_LIB_PATH} missing: run `make -C oracle`")
+        h = ctypes.CDLL(_LIB_PATH)
+        vp, i32, i64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64
+        h.oracle_f16_to_f32.restype = ctypes.c_float
+        h.oracle_f16_to_f32.argtypes = [ctypes.c_uint16]
+        h.oracle_f32_to_f16.restype = ctypes.c_uint16
+        h.oracle_f32_to_f16.argtypes = [ctypes.c_float]
+        h.oracle_f32_to_bf16.restype = ctypes.c_uint16
+        h.oracle_f32_to_bf16.argtypes = [ctypes.c_float]
+        h.oracle_tbe_pooled.restype = i64
+        h.oracle_tbe_pooled.argtypes = [ctypes.POINTER(_Table), i32, i64, vp, vp, i32, i64, vp, i64, vp, i32,
+                                        i64, i32]
+        h.oracle_int8_quantize.restype = None
+        h.oracle_int8_quantize.argtypes = [vp, i64, i32, vp, i32, i32]
+        h.oracle_seq_gather.restype = i64
+        h.oracle_seq_gather.argtypes = [i32, i32, i32, i64, vp, vp, vp, vp, vp, vp, vp, i32, i32, vp, vp]
+        _lib = h
+    return _lib
+
+
+def _p(a: np.ndarray) -> int:
+    return a.ctypes.data
+
+
+# ---- conversions -------------------------------------------------------------
+
+def f32_to_f16_bits(x) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32).ravel()
+    return np.array([lib().oracle_f32_to_f16(float(v)) for v in x], dtype=np.uint16)
+
+
+def f32_to_bf16_bits(x) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32).ravel()
+    return np.array([lib().oracle_f32_to_bf16(float(v)) for v in x], dtype=np.uint16)
+
+
+def f16_bits_to_f32(h) -> np.ndarray:
+    h = np.ascontiguousarray(h, dtype=np.uint16).ravel()
+    return np.array([lib().oracle_f16_to_f32(int(v)) for v in h], dtype=np.float32)
+
+
+def offsets_np(lengths) -> np.ndarray:
+    lengths = np.asarray(lengths, dtype=np.int64).ravel()
+    out = np.zeros(lengths.size + 1, dtype=np.int64)
+    np.cumsum(lengths, out=out[1:])
+    return out
+
+
+# ---- pooled lookup -----------------------------------------------------------
+
+def default_row_bytes(dtype: str, dim: int) -> int:
+    return {"fp32": 4 * dim, "fp16": 2 * dim, "bf16": 2 * dim}.get(dtype, (4 + dim + 3) & ~3)
+
+
+def tbe_pooled(flat: np.ndarray, slots: Sequence[dict], indices: np.ndarray, offsets: np.ndarray, batch: int,
+               padding_idx: int = -1, out_dtype: str = "fp32", out_stride: Optional[int] = None,
+               threads: int = 1, return_bad: bool = False):
+    """flat: uint8 bytes of every table; slots: dicts rows, weights_offset, dim, dtype ("fp32" | "fp16" |
+    "bf16" | "int8"), pooling ("sum" | "mean"), row_bytes (0 = default), out_offset.
+    Returns [B, out_stride] float32 (out_dtype fp32) or uint16 bit patterns (fp16 / bf16)."""
+    T = len(slots)
+    arr = (_Table * T)()
+    total = 0
+    for i, s in enumerate(slots):
+        arr[i] = _Table(int(s["rows"]), int(s["weights_offset"]), int(s["dim"]), _DT[s["dtype"]],
+                        _POOL[s["pooling"]], int(s.get("row_bytes", 0)), int(s["out_offset"]), 0)
+        total = max(total, int(s["out_offset"]) + int(s["dim"]))
+    out_stride = total if out_stride is None else out_stride
+    flat = np.ascontiguousarray(flat, dtype=np.uint8)
+    indices = np.ascontiguousarray(indices)
+    if indices.dtype not in (np.int32, np.int64):
+        indices = indices.astype(np.int64)
+    offsets = np.ascontiguousarray(offsets, dtype=np.int64)
+    assert offsets.size == T * batch + 1
+    out = np.zeros((batch, out_stride), dtype=np.float32 if out_dtype == "fp32" else np.uint16)
+    bad = lib().oracle_tbe_pooled(arr, T, batch, _p(flat), _p(indices) if indices.size else None,
+                                  32 if indices.dtype == np.int32 else 64, indices.size, _p(offsets),
+                                  padding_idx, _p(out), _DT[out_dtype], out_stride, threads)
+    return (out, int(bad)) if return_bad else out
+
+
+def table_bytes(w) -> np.ndarray:
+    """Raw bytes of a table given as a torch tensor (any dtype) or numpy array."""
+    try:
+        import torch
+        if isinstance(w, torch.Tensor):
+            w = w.detach().cpu().contiguous()
+            if w.dtype in (torch.bfloat16, torch.float16):
+                return w.view(torch.int16).numpy().view(np.uint8).reshape(-1)
+            return w.numpy().view(np.uint8).reshape(-1)
+    except ImportError:
+        pass
+    return np.ascontiguousarray(w).view(np.uint8).reshape(-1)
+
+
+def _dtype_name(w) -> str:
+    try:
+        import torch
+        if isinstance(w, torch.Tensor):
+            return {torch.float32: "fp32", torch.float16: "fp16", torch.bfloat16: "bf16",
+                    torch.uint8: "int8"}[w.dtype]
+    except ImportError:
+        pass
+    return {np.dtype(np.float32): "fp32", np.dtype(np.float16): "fp16", np.dtype(np.uint8): "int8"}[w.dtype]
+
+
+def tbe_pooled_from_tables(tables: Sequence, poolings: Sequence[str], indices, offsets, batch: int,
+                           out_dtype: str = "fp32", padding_idx: int = -1, dims: Optional[Sequence[int]] = None,
+                           threads: int = 1):
+    """Convenience form: one 2-D table per slot (int8 tables as uint8 [rows, row_bytes] with ``dims``)."""
+    chunks, slots, off, col = [], [], 0, 0
+    for i, w in enumerate(tables):
+        b = table_bytes(w)
+        dt = _dtype_name(w)
+        rows = int(w.shape[0])
+        dim = int(dims[i]) if dims is not None else int(w.shape[1])
+        rb = int(w.shape[1]) if dt == "int8" else 0
+        pad = (-off) % 16
+        if pad:
+            chunks.append(np.zeros(pad, dtype=np.uint8))
+            off += pad
+        slots.append(dict(rows=rows, weights_offset=off, dim=dim, dtype=dt, pooling=poolings[i], row_bytes=rb,
+                          out_offset=col))
+        chunks.append(b)
+        off += b.size
+        col += dim
+    flat = np.concatenate(chunks) if chunks else np.zeros(1, np.uint8)
+    return tbe_pooled(flat, slots, np.asarray(indices), np.asarray(offsets), batch, padding_idx, out_dtype,
+                      threads=threads)
+
+
+# ---- int8 rowwise ------------------------------------------------------------
+
+def int8_quantize(src: np.ndarray, row_bytes: int = 0, threads: int = 1) -> np.ndarray:
+    src = np.ascontiguousarray(src, dtype=np.float32)
+    rows, dim = src.shape
+    rb = row_bytes or (4 + dim + 3) & ~3
+    out = np.zeros((rows, rb), dtype=np.uint8)
+    lib().oracle_int8_quantize(_p(src), rows, dim, _p(out), rb, threads)
+    return out
+
+
+def int8_decode(q: np.ndarray, dim: int) -> np.ndarray:
+    """Row decode x = float(q) * scale (fp32 rounding) + bias (fp32 rounding)."""
+    q = np.ascontiguousarray(q, dtype=np.uint8)
+    sb = q[:, :4].copy().view(np.float16).astype(np.float32)  # [rows, 2]
+    scale, bias = sb[:, 0:1], sb[:, 1:2]
+    prod = (q[:, 4:4 + dim].astype(np.float32) * scale).astype(np.float32)
+    return (prod + bias).astype(np.float32)
+
+
+# ---- sequence gather ---------------------------------------------------------
+
+def seq_gather(tables: Sequence[np.ndarray], ids: Sequence[Sequence[np.ndarray]], offsets: Sequence[np.ndarray],
+               max_len: Sequence[int], pad_mode: int = 0, align: int = 0, return_bad: bool = False):
+    """tables[f]: [rows, dim] uint16 (bf16 / fp16 bits) or float32; ids[p][f] int64; offsets[p] int64 [B+1].
+    Returns (out [B, S, sum dim] in the table dtype, mask uint8 [B, S])."""
+    P, F = len(offsets), len(tables)
+    tables = [np.ascontiguousarray(t) for t in tables]
+    esize = tables[0].dtype.itemsize
+    B = offsets[0].size - 1
+    S = int(sum(max_len))
+    Dt = int(sum(t.shape[1] for t in tables))
+    out = np.zeros((B, S, Dt), dtype=tables[0].dtype)
+    mask = np.zeros((B, S), dtype=np.uint8)
+    ml = np.asarray(max_len, dtype=np.int32)
+    dims = np.asarray([t.shape[1] for t in tables], dtype=np.int32)
+    rows = np.asarray([t.shape[0] for t in tables], dtype=np.int64)
+    ids_c = [np.ascontiguousarray(ids[p][f], dtype=np.int64) for p in range(P) for f in range(F)]
+    offs_c = [np.ascontiguousarray(o, dtype=np.int64) for o in offsets]
+    num_ids = np.asarray([ids_c[p * F].size for p in range(P)], dtype=np.int64)
+    tab_ptrs = (ctypes.c_void_p * F)(*[_p(t) for t in tables])
+    id_ptrs = (ctypes.c_void_p * (P * F))(*[_p(a) for a in ids_c])
+    off_ptrs = (ctypes.c_void_p * P)(*[_p(o) for o in offs_c])
+    bad = lib().oracle_seq_gather(P, F, esize, B, _p(ml), _p(dims), _p(rows), tab_ptrs, id_ptrs, off_ptrs,
+                                  _p(num_ids), pad_mode, align, _p(out), _p(mask))
+    return (out, mask, int(bad)) if return_bad else (out, mask)

@@ -1,0 +1,172 @@
+"""ctypes binding of libpdm.so, the C ABI declared in include/pdm.h.
+
+The library is built in-tree (``primus-dlrm_amd/libpdm.so``).  Every op of
+this package goes through it; there is no fallback implementation, so a
+missing or stale library raises instead of silently computing elsewhere.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libpdm.so")
+
+PDM_OK = 0
+PDM_ERR_INVALID = -1
+PDM_ERR_UNSUPPORTED = -2
+PDM_ERR_HIP = -3
+PDM_ERR_WORKSPACE = -4
+
+PDM_F32, PDM_F16, PDM_BF16, PDM_I8_SB_F16 = 0, 1, 2, 3
+PDM_POOL_SUM, PDM_POOL_MEAN = 0, 1
+PDM_PAD_ROW0, PDM_PAD_ZERO = 0, 1
+PDM_ALIGN_RIGHT, PDM_ALIGN_LEFT = 0, 1
+PDM_SEQ_MAX_POOLS = 8
+PDM_SEQ_MAX_FEATURES = 8
+
+# Every symbol include/pdm.h declares (checked by the ABI test).
+EXPORTED_SYMBOLS = (
+    "pdm_abi_version",
+    "pdm_last_error",
+    "pdm_tbe_plan_create",
+    "pdm_tbe_plan_destroy",
+    "pdm_tbe_plan_total_dim",
+    "pdm_tbe_pooled_fwd",
+    "pdm_int8_rowwise_quantize",
+    "pdm_seq_gather_fwd",
+    "pdm_onetrans_block_workspace_size",
+    "pdm_onetrans_block_fwd",
+)
+
+
+class PdmError(RuntimeError):
+    """A C ABI call returned a non-zero pdm_status."""
+
+    def __init__(self, status: int, func: str, message: str):
+        super().__init__(f"{func} failed with status {status}: {message}")
+        self.status = status
+
+
+class TableDesc(ctypes.Structure):
+    _fields_ = [
+        ("rows", ctypes.c_int64),
+        ("weights_offset", ctypes.c_int64),
+        ("dim", ctypes.c_int32),
+        ("dtype", ctypes.c_int32),
+        ("pooling", ctypes.c_int32),
+        ("row_bytes", ctypes.c_int32),
+        ("out_offset", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+    ]
+
+
+class SeqDesc(ctypes.Structure):
+    _fields_ = [
+        ("num_pools", ctypes.c_int32),
+        ("num_features", ctypes.c_int32),
+        ("dtype", ctypes.c_int32),
+        ("pad_mode", ctypes.c_int32),
+        ("align", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+        ("batch_size", ctypes.c_int64),
+        ("max_len", ctypes.c_int32 * PDM_SEQ_MAX_POOLS),
+        ("dim", ctypes.c_int32 * PDM_SEQ_MAX_FEATURES),
+        ("rows", ctypes.c_int64 * PDM_SEQ_MAX_FEATURES),
+        ("num_ids", ctypes.c_int64 * PDM_SEQ_MAX_POOLS),
+    ]
+
+
+class BlockDesc(ctypes.Structure):
+    _fields_ = [
+        ("batch", ctypes.c_int32),
+        ("d_model", ctypes.c_int32),
+        ("n_heads", ctypes.c_int32),
+        ("n_ns", ctypes.c_int32),
+        ("ffn_dim", ctypes.c_int32),
+        ("kv_len", ctypes.c_int32),
+        ("q_len", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+    ]
+
+
+class BlockWeights(ctypes.Structure):
+    _fields_ = [
+        ("norm1_w", ctypes.c_void_p),
+        ("s_qkv_w", ctypes.c_void_p),
+        ("ns_qkv_w", ctypes.c_void_p),
+        ("out_w", ctypes.c_void_p),
+        ("norm2_w", ctypes.c_void_p),
+        ("s_w1", ctypes.c_void_p),
+        ("s_w2", ctypes.c_void_p),
+        ("ns_w1", ctypes.c_void_p),
+        ("ns_w2", ctypes.c_void_p),
+    ]
+
+
+_lib = None
+_lock = threading.Lock()
+
+
+def _declare(lib: ctypes.CDLL) -> None:
+    vp, i32, i64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64
+    lib.pdm_abi_version.restype = i32
+    lib.pdm_abi_version.argtypes = []
+    lib.pdm_last_error.restype = ctypes.c_size_t
+    lib.pdm_last_error.argtypes = [ctypes.c_char_p, ctypes.c_size_t]
+    lib.pdm_tbe_plan_create.restype = ctypes.c_int
+    lib.pdm_tbe_plan_create.argtypes = [ctypes.POINTER(TableDesc), i32, ctypes.POINTER(vp)]
+    lib.pdm_tbe_plan_destroy.restype = ctypes.c_int
+    lib.pdm_tbe_plan_destroy.argtypes = [vp]
+    lib.pdm_tbe_plan_total_dim.restype = i64
+    lib.pdm_tbe_plan_total_dim.argtypes = [vp]
+    lib.pdm_tbe_pooled_fwd.restype = ctypes.c_int
+    lib.pdm_tbe_pooled_fwd.argtypes = [vp, vp, vp, i32, i64, vp, i64, i64, vp, i32, i64, vp, vp]
+    lib.pdm_int8_rowwise_quantize.restype = ctypes.c_int
+    lib.pdm_int8_rowwise_quantize.argtypes = [vp, i64, i32, vp, i32, vp]
+    lib.pdm_seq_gather_fwd.restype = ctypes.c_int
+    lib.pdm_seq_gather_fwd.argtypes = [ctypes.POINTER(SeqDesc), ctypes.POINTER(vp), ctypes.POINTER(vp),
+                                       ctypes.POINTER(vp), vp, vp, vp, vp]
+    lib.pdm_onetrans_block_workspace_size.restype = i64
+    lib.pdm_onetrans_block_workspace_size.argtypes = [ctypes.POINTER(BlockDesc)]
+    lib.pdm_onetrans_block_fwd.restype = ctypes.c_int
+    lib.pdm_onetrans_block_fwd.argtypes = [ctypes.POINTER(BlockDesc), vp, ctypes.POINTER(BlockWeights), vp,
+                                           vp, i64, vp]
+
+
+def lib() -> ctypes.CDLL:
+    """Returns the loaded library, loading it on first use.
+
+    Raises RuntimeError when libpdm.so has not been built.
+    """
+    global _lib
+    if _lib is None:
+        with _lock:
+            if _lib is None:
+                if not os.path.exists(LIB_PATH):
+                    raise RuntimeError(
+                        f"{LIB_PATH} is missing: build it with `python -c 'import __graft_entry__ as g; g.build()'` "
+                        "or `make -C primus-dlrm_amd/csrc`")
+                handle = ctypes.CDLL(LIB_PATH, mode=ctypes.RTLD_LOCAL)
+                _declare(handle)
+                _lib = handle
+    return _lib
+
+
+def last_error() -> str:
+    buf = ctypes.create_string_buffer(1024)
+    lib().pdm_last_error(buf, len(buf))
+    return buf.value.decode(errors="replace")
+
+
+def check(status: int, func: str) -> None:
+    if status != PDM_OK:
+        raise PdmError(status, func, last_error())
+
+
+def stream_ptr(device) -> int:
+    """Raw hipStream_t of torch's current stream on ``device``."""
+    import torch
+
+    return torch.cuda.current_stream(device).cuda_stream

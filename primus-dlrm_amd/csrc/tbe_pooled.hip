@@ -1,0 +1,554 @@
+// Table-batched pooled embedding forward for gfx950.
+//
+// Semantics follow the reference's pooled lookup: TorchRec
+// EmbeddingBagCollection / FBGEMM TBE forward over table-major offsets
+// (tests/test_fbgemm_tbe.py:23-35), masked sum / mean with
+// mean = sum / max(count, 1) (primus_dlrm/models/sharded_embedding.py:220-227),
+// padding ids dropped before pooling (primus_dlrm/models/embedding.py:188-194).
+//
+// Design: a bag (table t, sample b) is owned by a group of `lpb` lanes of one
+// wavefront (lpb = row payload / vector width, so a row is read by one
+// coalesced vector load per lane).  A group loads up to lpb indices of its bag
+// with one coalesced load, broadcasts them with cross-lane permutes, issues the
+// row loads of U indices before accumulating them, and adds rows in bag order
+// so every output element is the same fp32 sum the sequential CPU restatement
+// produces.  The kernel never reads outside [0, rows) of a table or outside
+// [0, num_indices) of the index array: offending entries are skipped and
+// reported through an optional device flag.
+#include <algorithm>
+#include <memory>
+#include <vector>
+
+#include "pdm_common.h"
+
+#pragma clang fp contract(off)
+
+namespace pdm {
+
+struct TbeMeta {
+  int64_t rows;
+  int64_t w_off;  // byte offset of row 0 inside the weights buffer
+  int32_t row_bytes;
+  int32_t out_col;
+  int32_t pooling;
+  int32_t dim;
+};
+
+struct TbeArgs {
+  const char* weights;
+  const void* indices;
+  const int64_t* offsets;
+  const TbeMeta* meta;
+  const int32_t* group_tables;
+  void* out;
+  int32_t* err;
+  int64_t num_indices;
+  int64_t B;
+  int64_t num_bags;
+  int64_t padding_idx;
+  int64_t out_stride;  // elements
+  int32_t lpb_shift;
+  int32_t payload_vecs;  // payload bytes / VB
+  int32_t out_vec_ok;    // output rows aligned for vector stores
+  int32_t index_bits;
+};
+
+template <int VB>
+struct VecT;
+template <>
+struct VecT<16> { using T = uint4; };
+template <>
+struct VecT<8> { using T = uint2; };
+template <>
+struct VecT<4> { using T = uint32_t; };
+
+template <int VB>
+__device__ __forceinline__ void load_words(const char* p, uint32_t (&w)[VB / 4]) {
+  using T = typename VecT<VB>::T;
+  const T v = *reinterpret_cast<const T*>(p);
+  if constexpr (VB == 16) { w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w; }
+  else if constexpr (VB == 8) { w[0] = v.x; w[1] = v.y; }
+  else { w[0] = v; }
+}
+
+// Elements per VB-byte vector of the stored dtype.
+template <int WT, int VB>
+constexpr int epv() {
+  return WT == PDM_F32 ? VB / 4 : (WT == PDM_I8_SB_F16 ? VB : VB / 2);
+}
+
+template <int WT, int VB>
+__device__ __forceinline__ void accumulate(float* acc, const uint32_t (&w)[VB / 4],
+                                           float scale, float bias) {
+  constexpr int W = VB / 4;
+#pragma unroll
+  for (int i = 0; i < W; ++i) {
+    if constexpr (WT == PDM_F32) {
+      acc[i] += __uint_as_float(w[i]);
+    } else if constexpr (WT == PDM_BF16) {
+      acc[2 * i] += __uint_as_float(w[i] << 16);
+      acc[2 * i + 1] += __uint_as_float(w[i] & 0xffff0000u);
+    } else if constexpr (WT == PDM_F16) {
+      acc[2 * i] += f16_bits_to_f32(w[i] & 0xffffu);
+      acc[2 * i + 1] += f16_bits_to_f32(w[i] >> 16);
+    } else {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const float q = (float)((w[i] >> (8 * k)) & 0xffu);
+        const float prod = __fmul_rn(q, scale);
+        acc[4 * i + k] += __fadd_rn(prod, bias);
+      }
+    }
+  }
+}
+
+template <int OT, int N>
+__device__ __forceinline__ void store_out(char* dst, const float* v, bool vec_ok) {
+  constexpr int OS = OT == PDM_F32 ? 4 : 2;
+  constexpr int BYTES = N * OS;
+  if constexpr (OT == PDM_F32) {
+    if (vec_ok && BYTES % 16 == 0) {
+#pragma unroll
+      for (int i = 0; i < N / 4; ++i)
+        reinterpret_cast<float4*>(dst)[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < N; ++i) reinterpret_cast<float*>(dst)[i] = v[i];
+    }
+  } else {
+    uint32_t h[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) h[i] = OT == PDM_F16 ? f32_to_f16_bits(v[i]) : f32_to_bf16_bits(v[i]);
+    if constexpr (N % 2 == 0) {
+      uint32_t p[N / 2];
+#pragma unroll
+      for (int i = 0; i < N / 2; ++i) p[i] = h[2 * i] | (h[2 * i + 1] << 16);
+      if (vec_ok && BYTES % 16 == 0) {
+#pragma unroll
+        for (int i = 0; i < N / 8; ++i)
+          reinterpret_cast<uint4*>(dst)[i] = make_uint4(p[4 * i], p[4 * i + 1], p[4 * i + 2], p[4 * i + 3]);
+      } else if (vec_ok && BYTES % 8 == 0) {
+#pragma unroll
+        for (int i = 0; i < N / 4; ++i) reinterpret_cast<uint2*>(dst)[i] = make_uint2(p[2 * i], p[2 * i + 1]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < N / 2; ++i) reinterpret_cast<uint32_t*>(dst)[i] = p[i];
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < N; ++i) reinterpret_cast<uint16_t*>(dst)[i] = (uint16_t)h[i];
+    }
+  }
+}
+
+__device__ __forceinline__ int64_t shfl64(int64_t v, int src) {
+  const int lo = __shfl((int)(uint32_t)v, src, 64);
+  const int hi = __shfl((int)(uint32_t)((uint64_t)v >> 32), src, 64);
+  return (int64_t)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
+}
+
+template <int WT, int OT, int VB, int NC>
+__global__ __launch_bounds__(256) void tbe_pooled_kernel(TbeArgs a) {
+  constexpr int W = VB / 4;
+  constexpr int EPV = epv<WT, VB>();
+  constexpr int U = 4;  // row loads issued before the first is accumulated
+  const int lane = threadIdx.x & 63;
+  const int lpb = 1 << a.lpb_shift;
+  const int j = lane & (lpb - 1);
+  const int gbase = lane & ~(lpb - 1);
+  const int64_t wave = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const int64_t g = (wave << (6 - a.lpb_shift)) + (lane >> a.lpb_shift);
+  if (g >= a.num_bags) return;  // all lanes of a group share g
+
+  const int64_t tl = g / a.B;
+  const int64_t b = g - tl * a.B;
+  const int t = a.group_tables[tl];
+  const TbeMeta m = a.meta[t];
+  const int64_t bag = (int64_t)t * a.B + b;
+  int64_t start = a.offsets[bag];
+  int64_t end = a.offsets[bag + 1];
+  bool bad = false;
+  if (start < 0 || end < start || end > a.num_indices) {
+    bad = true;
+    start = end = 0;
+  }
+  const char* wbase = a.weights + m.w_off + (WT == PDM_I8_SB_F16 ? 4 : 0);
+
+  float acc[NC][EPV];
+#pragma unroll
+  for (int c = 0; c < NC; ++c)
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) acc[c][e] = 0.0f;
+  int count = 0;
+
+  for (int64_t base = start; base < end; base += lpb) {
+    const int n = (int)min((int64_t)lpb, end - base);
+    int64_t my = -1;
+    if (j < n) {
+      my = a.index_bits == 32 ? (int64_t)reinterpret_cast<const int32_t*>(a.indices)[base + j]
+                              : reinterpret_cast<const int64_t*>(a.indices)[base + j];
+    }
+    for (int k = 0; k < n; k += U) {
+      int64_t idx[U];
+      bool ok[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        idx[u] = shfl64(my, gbase + ((k + u) & (lpb - 1)));
+        const bool live = (k + u) < n && idx[u] != a.padding_idx;
+        ok[u] = live && idx[u] >= 0 && idx[u] < m.rows;
+        bad |= live && !ok[u];
+      }
+      uint32_t v[U][NC][W];
+      uint32_t sb[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (ok[u]) {
+          const char* row = wbase + idx[u] * (int64_t)m.row_bytes;
+          if constexpr (WT == PDM_I8_SB_F16) sb[u] = *reinterpret_cast<const uint32_t*>(row - 4);
+#pragma unroll
+          for (int c = 0; c < NC; ++c) {
+            const int vi = c * lpb + j;
+            if (vi < a.payload_vecs) load_words<VB>(row + vi * VB, v[u][c]);
+          }
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (ok[u]) {
+          float scale = 0.0f, bias = 0.0f;
+          if constexpr (WT == PDM_I8_SB_F16) {
+            scale = f16_bits_to_f32(sb[u] & 0xffffu);
+            bias = f16_bits_to_f32(sb[u] >> 16);
+          }
+#pragma unroll
+          for (int c = 0; c < NC; ++c) accumulate<WT, VB>(acc[c], v[u][c], scale, bias);
+          ++count;
+        }
+      }
+    }
+  }
+
+  if (m.pooling == PDM_POOL_MEAN && count > 0) {
+    const float cf = (float)count;
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int e = 0; e < EPV; ++e) acc[c][e] = __fdiv_rn(acc[c][e], cf);
+  }
+
+  constexpr int OS = OT == PDM_F32 ? 4 : 2;
+  char* orow = reinterpret_cast<char*>(a.out) + (b * a.out_stride + m.out_col) * OS;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int vi = c * lpb + j;
+    if (vi < a.payload_vecs) store_out<OT, EPV>(orow + (int64_t)vi * EPV * OS, acc[c], a.out_vec_ok != 0);
+  }
+  if (bad && a.err) a.err[0] = 1;
+}
+
+// ---- quantizer -------------------------------------------------------------
+
+// One group of 32 lanes per row; dim <= 32 * 8 * 4.
+template <int PER>
+__global__ __launch_bounds__(256) void int8_quantize_kernel(const float* __restrict__ src, int64_t rows,
+                                                            int dim, char* __restrict__ dst, int row_bytes) {
+  const int lane = threadIdx.x & 63;
+  const int j = lane & 31;
+  const int64_t r = ((int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) * 2 + (lane >> 5);
+  if (r >= rows) return;
+  const float* x = src + r * dim;
+  float v[PER];
+  float mn = INFINITY, mx = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int d = i * 32 + j;
+    v[i] = d < dim ? x[d] : 0.0f;
+    if (d < dim) {
+      mn = fminf(mn, v[i]);
+      mx = fmaxf(mx, v[i]);
+    }
+  }
+#pragma unroll
+  for (int s = 16; s >= 1; s >>= 1) {
+    mn = fminf(mn, __shfl_xor(mn, s, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, s, 64));
+  }
+  const uint32_t bias16 = f32_to_f16_bits(mn);
+  const float bias = f16_bits_to_f32(bias16);
+  const float range = mx - bias;
+  uint32_t scale16 = f32_to_f16_bits(range == 0.0f ? 1.0f : range / 255.0f);
+  float scale = f16_bits_to_f32(scale16);
+  if (scale == 0.0f || isinf(1.0f / scale)) {
+    scale16 = 0x3c00u;
+    scale = 1.0f;
+  }
+  const float inv = 1.0f / scale;
+  char* o = dst + r * (int64_t)row_bytes;
+  if (j == 0) *reinterpret_cast<uint32_t*>(o) = scale16 | (bias16 << 16);
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int d = i * 32 + j;
+    if (d < dim) {
+      float q = rintf((v[i] - bias) * inv);
+      q = fminf(fmaxf(q, 0.0f), 255.0f);
+      reinterpret_cast<uint8_t*>(o)[4 + d] = (uint8_t)q;
+    }
+  }
+  for (int d = 4 + dim + j; d < row_bytes; d += 32) reinterpret_cast<uint8_t*>(o)[d] = 0;
+}
+
+}  // namespace pdm
+
+// ---- C ABI -------------------------------------------------------------------
+
+using namespace pdm;
+
+struct TbeGroup {
+  int32_t dtype;
+  int32_t dim;
+  int32_t row_bytes_all;  // common row stride, -1 if tables differ
+  int32_t first;          // index into the grouped table list
+  int32_t count;
+  int64_t min_w_off_align;  // gcd-like alignment of all weights_offsets (power of 2)
+  int32_t out_col_align;    // alignment (elements) of all out_offsets
+};
+
+struct pdm_tbe_plan_s {
+  int device = 0;
+  std::vector<pdm_table_desc> tables;
+  std::vector<TbeGroup> groups;
+  TbeMeta* d_meta = nullptr;
+  int32_t* d_group_tables = nullptr;
+  int64_t total_dim = 0;
+  ~pdm_tbe_plan_s();
+};
+
+static int32_t default_row_bytes(int dtype, int dim) {
+  switch (dtype) {
+    case PDM_F32: return 4 * dim;
+    case PDM_F16:
+    case PDM_BF16: return 2 * dim;
+    default: return (4 + dim + 3) & ~3;
+  }
+}
+
+static int64_t pow2_align(int64_t v) {  // largest power of two dividing v (v == 0 -> large)
+  if (v == 0) return int64_t(1) << 40;
+  return v & -v;
+}
+
+extern "C" int pdm_tbe_plan_create(const pdm_table_desc* tables, int32_t num_tables, pdm_tbe_plan* plan_out) {
+  clear_error();
+  PDM_CHECK_ARG(tables != nullptr && plan_out != nullptr, "null argument");
+  PDM_CHECK_ARG(num_tables > 0, "num_tables must be > 0");
+  std::unique_ptr<pdm_tbe_plan_s> plan(new pdm_tbe_plan_s());
+  std::vector<TbeMeta> meta(num_tables);
+  for (int t = 0; t < num_tables; ++t) {
+    pdm_table_desc d = tables[t];
+    PDM_CHECK_ARG(d.rows >= 0, "table " + std::to_string(t) + ": rows < 0");
+    PDM_CHECK_ARG(d.dim > 0 && d.dim % 4 == 0 && d.dim <= 4096,
+                  "table " + std::to_string(t) + ": dim must be a positive multiple of 4, <= 4096");
+    PDM_CHECK_ARG(d.dtype >= PDM_F32 && d.dtype <= PDM_I8_SB_F16, "table " + std::to_string(t) + ": bad dtype");
+    PDM_CHECK_ARG(d.pooling == PDM_POOL_SUM || d.pooling == PDM_POOL_MEAN,
+                  "table " + std::to_string(t) + ": bad pooling");
+    PDM_CHECK_ARG(d.weights_offset >= 0, "table " + std::to_string(t) + ": weights_offset < 0");
+    PDM_CHECK_ARG(d.out_offset >= 0, "table " + std::to_string(t) + ": out_offset < 0");
+    const int32_t payload = d.dtype == PDM_I8_SB_F16 ? d.dim : d.dim * dtype_size(d.dtype);
+    const int32_t min_rb = d.dtype == PDM_I8_SB_F16 ? 4 + d.dim : payload;
+    if (d.row_bytes == 0) d.row_bytes = default_row_bytes(d.dtype, d.dim);
+    PDM_CHECK_ARG(d.row_bytes >= min_rb && d.row_bytes % 4 == 0,
+                  "table " + std::to_string(t) + ": row_bytes must be >= the row payload and a multiple of 4");
+    PDM_CHECK_ARG(d.weights_offset % 4 == 0, "table " + std::to_string(t) + ": weights_offset must be 4-byte aligned");
+    plan->tables.push_back(d);
+    meta[t] = TbeMeta{d.rows, d.weights_offset, d.row_bytes, d.out_offset, d.pooling, d.dim};
+    plan->total_dim = std::max<int64_t>(plan->total_dim, (int64_t)d.out_offset + d.dim);
+  }
+  // Group tables sharing (dtype, dim); order inside a group keeps table order.
+  std::vector<int32_t> order;
+  for (int t = 0; t < num_tables; ++t) {
+    const auto& d = plan->tables[t];
+    bool found = false;
+    for (auto& g : plan->groups)
+      if (g.dtype == d.dtype && g.dim == d.dim) found = true;
+    if (found) continue;
+    TbeGroup g{d.dtype, d.dim, d.row_bytes, (int32_t)order.size(), 0, int64_t(1) << 40, 1 << 20};
+    for (int u = t; u < num_tables; ++u) {
+      const auto& e = plan->tables[u];
+      if (e.dtype != d.dtype || e.dim != d.dim) continue;
+      order.push_back(u);
+      ++g.count;
+      if (e.row_bytes != g.row_bytes_all) g.row_bytes_all = -1;
+      g.min_w_off_align = std::min(g.min_w_off_align, std::min(pow2_align(e.weights_offset), pow2_align(e.row_bytes)));
+      g.out_col_align = (int32_t)std::min<int64_t>(g.out_col_align, pow2_align(e.out_offset));
+    }
+    plan->groups.push_back(g);
+  }
+  PDM_CHECK_HIP(hipGetDevice(&plan->device));
+  PDM_CHECK_HIP(hipMalloc(&plan->d_meta, sizeof(TbeMeta) * num_tables));
+  PDM_CHECK_HIP(hipMalloc(&plan->d_group_tables, sizeof(int32_t) * num_tables));
+  PDM_CHECK_HIP(hipMemcpy(plan->d_meta, meta.data(), sizeof(TbeMeta) * num_tables, hipMemcpyHostToDevice));
+  PDM_CHECK_HIP(hipMemcpy(plan->d_group_tables, order.data(), sizeof(int32_t) * num_tables, hipMemcpyHostToDevice));
+  *plan_out = plan.release();
+  return PDM_OK;
+}
+
+pdm_tbe_plan_s::~pdm_tbe_plan_s() {
+  if (!d_meta && !d_group_tables) return;
+  int cur = 0;
+  (void)hipGetDevice(&cur);
+  (void)hipSetDevice(device);
+  if (d_meta) (void)hipFree(d_meta);
+  if (d_group_tables) (void)hipFree(d_group_tables);
+  (void)hipSetDevice(cur);
+}
+
+extern "C" int pdm_tbe_plan_destroy(pdm_tbe_plan plan) {
+  clear_error();
+  delete plan;
+  return PDM_OK;
+}
+
+extern "C" int64_t pdm_tbe_plan_total_dim(pdm_tbe_plan plan) { return plan ? plan->total_dim : -1; }
+
+namespace {
+
+using KernelFn = void (*)(TbeArgs);
+
+template <int WT, int OT, int VB>
+KernelFn pick_nc(int nc) {
+  switch (nc) {
+    case 1: return tbe_pooled_kernel<WT, OT, VB, 1>;
+    case 2: return tbe_pooled_kernel<WT, OT, VB, 2>;
+    case 4: return tbe_pooled_kernel<WT, OT, VB, 4>;
+    default: return nullptr;
+  }
+}
+
+template <int WT, int OT>
+KernelFn pick_vb(int vb, int nc) {
+  if constexpr (WT == PDM_I8_SB_F16) {
+    return vb == 4 ? pick_nc<WT, OT, 4>(nc) : nullptr;
+  } else {
+    switch (vb) {
+      case 16: return pick_nc<WT, OT, 16>(nc);
+      case 8: return pick_nc<WT, OT, 8>(nc);
+      case 4: return pick_nc<WT, OT, 4>(nc);
+      default: return nullptr;
+    }
+  }
+}
+
+template <int WT>
+KernelFn pick_ot(int ot, int vb, int nc) {
+  switch (ot) {
+    case PDM_F32: return pick_vb<WT, PDM_F32>(vb, nc);
+    case PDM_F16: return pick_vb<WT, PDM_F16>(vb, nc);
+    case PDM_BF16: return pick_vb<WT, PDM_BF16>(vb, nc);
+    default: return nullptr;
+  }
+}
+
+KernelFn pick_kernel(int wt, int ot, int vb, int nc) {
+  switch (wt) {
+    case PDM_F32: return pick_ot<PDM_F32>(ot, vb, nc);
+    case PDM_F16: return pick_ot<PDM_F16>(ot, vb, nc);
+    case PDM_BF16: return pick_ot<PDM_BF16>(ot, vb, nc);
+    case PDM_I8_SB_F16: return pick_ot<PDM_I8_SB_F16>(ot, vb, nc);
+    default: return nullptr;
+  }
+}
+
+}  // namespace
+
+extern "C" int pdm_tbe_pooled_fwd(pdm_tbe_plan plan, const void* weights, const void* indices, int32_t index_bits,
+                                  int64_t num_indices, const int64_t* offsets, int64_t batch_size,
+                                  int64_t padding_idx, void* out, int32_t out_dtype, int64_t out_row_stride,
+                                  int32_t* err_flag, pdm_stream_t stream) {
+  clear_error();
+  PDM_CHECK_ARG(plan != nullptr, "null plan");
+  PDM_CHECK_ARG(index_bits == 32 || index_bits == 64, "index_bits must be 32 or 64");
+  PDM_CHECK_ARG(num_indices >= 0 && batch_size >= 0, "negative size");
+  PDM_CHECK_ARG(out_dtype == PDM_F32 || out_dtype == PDM_F16 || out_dtype == PDM_BF16, "bad out_dtype");
+  PDM_CHECK_ARG(out_row_stride >= plan->total_dim, "out_row_stride smaller than the plan's total dim");
+  const int64_t T = (int64_t)plan->tables.size();
+  if (batch_size == 0) return PDM_OK;
+  PDM_CHECK_ARG(weights && offsets && out, "null device pointer");
+  PDM_CHECK_ARG(indices != nullptr || num_indices == 0, "null indices");
+  PDM_CHECK_ARG(((uintptr_t)weights & 3) == 0, "weights must be 4-byte aligned");
+  PDM_CHECK_ARG(((uintptr_t)offsets & 7) == 0, "offsets must be 8-byte aligned");
+  const int osize = out_dtype == PDM_F32 ? 4 : 2;
+  for (const auto& g : plan->groups) {
+    const int payload = g.dtype == PDM_I8_SB_F16 ? g.dim : g.dim * dtype_size(g.dtype);
+    // widest vector that divides the payload and keeps every row aligned
+    const int64_t base_align = std::min(pow2_align((int64_t)(uintptr_t)weights), g.min_w_off_align);
+    int vb = 4;
+    if (g.dtype != PDM_I8_SB_F16) {
+      for (int c : {16, 8}) {
+        if (payload % c == 0 && base_align % c == 0) { vb = c; break; }
+      }
+    }
+    const int vecs = payload / vb;
+    int lpb = 1;
+    while (lpb < vecs && lpb < 64) lpb <<= 1;
+    const int nc = (vecs + lpb - 1) / lpb;
+    int ncp = 1;
+    while (ncp < nc) ncp <<= 1;
+    KernelFn fn = pick_kernel(g.dtype, out_dtype, vb, ncp);
+    if (!fn) {
+      set_error("pdm_tbe_pooled_fwd: unsupported combination (dtype " + std::to_string(g.dtype) + ", dim " +
+                std::to_string(g.dim) + ")");
+      return PDM_ERR_UNSUPPORTED;
+    }
+    const int epv_ = g.dtype == PDM_F32 ? vb / 4 : (g.dtype == PDM_I8_SB_F16 ? vb : vb / 2);
+    const int64_t store_bytes = std::min<int64_t>(16, (int64_t)epv_ * osize);
+    const bool out_vec_ok = pow2_align((int64_t)(uintptr_t)out) >= store_bytes &&
+                            pow2_align(out_row_stride * osize) >= store_bytes &&
+                            pow2_align((int64_t)g.out_col_align * osize) >= store_bytes;
+    int lpb_shift = 0;
+    while ((1 << lpb_shift) < lpb) ++lpb_shift;
+    TbeArgs a;
+    a.weights = reinterpret_cast<const char*>(weights);
+    a.indices = indices;
+    a.offsets = offsets;
+    a.meta = plan->d_meta;
+    a.group_tables = plan->d_group_tables + g.first;
+    a.out = out;
+    a.err = err_flag;
+    a.num_indices = num_indices;
+    a.B = batch_size;
+    a.num_bags = (int64_t)g.count * batch_size;
+    a.padding_idx = padding_idx;
+    a.out_stride = out_row_stride;
+    a.lpb_shift = lpb_shift;
+    a.payload_vecs = vecs;
+    a.out_vec_ok = out_vec_ok ? 1 : 0;
+    a.index_bits = index_bits;
+    const int64_t bags_per_block = 4 * (64 / lpb);
+    const int64_t blocks = (a.num_bags + bags_per_block - 1) / bags_per_block;
+    PDM_CHECK_ARG(blocks < (int64_t(1) << 31), "too many bags for one launch");
+    hipLaunchKernelGGL(fn, dim3((unsigned)blocks), dim3(256), 0, reinterpret_cast<hipStream_t>(stream), a);
+    PDM_CHECK_LAUNCH();
+  }
+  (void)T;
+  return PDM_OK;
+}
+
+extern "C" int pdm_int8_rowwise_quantize(const float* src, int64_t rows, int32_t dim, void* dst, int32_t row_bytes,
+                                         pdm_stream_t stream) {
+  clear_error();
+  PDM_CHECK_ARG(rows >= 0, "rows < 0");
+  PDM_CHECK_ARG(dim > 0 && dim <= 1024, "dim must be in [1, 1024]");
+  PDM_CHECK_ARG(row_bytes >= 4 + dim && row_bytes % 4 == 0, "row_bytes must be >= 4 + dim and a multiple of 4");
+  if (rows == 0) return PDM_OK;
+  PDM_CHECK_ARG(src && dst, "null device pointer");
+  PDM_CHECK_ARG(pow2_align((int64_t)(uintptr_t)dst) >= 4, "dst must be 4-byte aligned");
+  const int64_t blocks = (rows + 7) / 8;  // 8 rows per 256-thread block
+  const int per = (dim + 31) / 32;
+  auto s = reinterpret_cast<hipStream_t>(stream);
+  if (per <= 4) hipLaunchKernelGGL(int8_quantize_kernel<4>, dim3((unsigned)blocks), dim3(256), 0, s, src, rows, dim, (char*)dst, row_bytes);
+  else if (per <= 8) hipLaunchKernelGGL(int8_quantize_kernel<8>, dim3((unsigned)blocks), dim3(256), 0, s, src, rows, dim, (char*)dst, row_bytes);
+  else if (per <= 16) hipLaunchKernelGGL(int8_quantize_kernel<16>, dim3((unsigned)blocks), dim3(256), 0, s, src, rows, dim, (char*)dst, row_bytes);
+  else hipLaunchKernelGGL(int8_quantize_kernel<32>, dim3((unsigned)blocks), dim3(256), 0, s, src, rows, dim, (char*)dst, row_bytes);
+  PDM_CHECK_LAUNCH();
+  return PDM_OK;
+}

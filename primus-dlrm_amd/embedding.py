@@ -1,0 +1,545 @@
+"""Drop-in embedding modules over the gfx950 lookup kernels.
+
+* ``EmbeddingBagCollection``  — TorchRec EBC surface: ``EmbeddingBagCollection(tables=[EmbeddingBagConfig],
+  device)``, ``forward(KeyedJaggedTensor) -> KeyedTensor`` (reference call sites:
+  primus_dlrm/models/embedding.py:50-57,118-120,151; primus_dlrm/models/dlrm.py:147).
+  State dict keys ``embedding_bags.<table>.weight`` as in TorchRec.
+* ``EmbeddingCollection``     — TorchRec EC surface: ``forward(KJT) -> Dict[str, JaggedTensor]``
+  (embedding.py:60-66,122-124,161; onetrans.py:496).  Keys ``embeddings.<table>.weight``.
+* ``SequenceGather``          — jagged ids of the behaviour pools -> padded S-token rows ``[B, S, sum D]``
+  plus mask, on the device (replaces EC lookup + view + cat at onetrans.py:501-520,553-558 and the
+  host padding at data/dataset.py:604-636).
+* ``TorchRecEmbeddings``      — the reference's tensor-in/tensor-out wrapper (embedding.py:72-174):
+  ``forward({feat: ids[B] | ids[B, L]}, padding_idx=0) -> {feat: [B, D] | [B, L, D]}``.
+
+Every table of a collection lives in ONE device allocation (rows of table t start at a 256-byte
+aligned byte offset); the per-table ``weight`` parameters are typed views of it, so one pointer plus
+per-table offsets describe all tables to the kernels.
+"""
+from __future__ import annotations
+
+import enum
+import math
+from dataclasses import dataclass, field
+from typing import Callable, Dict, List, Optional, Sequence, Tuple
+
+import torch
+import torch.nn as nn
+
+from . import _lib as L
+from . import ops
+from .kjt import JaggedTensor, KeyedJaggedTensor, KeyedTensor
+
+
+class PoolingType(enum.Enum):
+    SUM = "SUM"
+    MEAN = "MEAN"
+    NONE = "NONE"
+
+
+class DataType(enum.Enum):
+    FP32 = "FP32"
+    FP16 = "FP16"
+    BF16 = "BF16"
+    INT8 = "INT8"  # rowwise: [fp16 scale][fp16 bias][dim x uint8] per row
+
+
+_DT_TORCH = {DataType.FP32: torch.float32, DataType.FP16: torch.float16, DataType.BF16: torch.bfloat16}
+_DT_PDM = {DataType.FP32: L.PDM_F32, DataType.FP16: L.PDM_F16, DataType.BF16: L.PDM_BF16,
+           DataType.INT8: L.PDM_I8_SB_F16}
+_POOL_PDM = {PoolingType.SUM: L.PDM_POOL_SUM, PoolingType.MEAN: L.PDM_POOL_MEAN}
+
+
+@dataclass
+class EmbeddingBagConfig:
+    """Mirrors torchrec.EmbeddingBagConfig as the reference builds it (embedding.py:50-57)."""
+    num_embeddings: int
+    embedding_dim: int
+    name: str = ""
+    data_type: DataType = DataType.FP32
+    feature_names: List[str] = field(default_factory=list)
+    pooling: PoolingType = PoolingType.SUM
+    init_fn: Optional[Callable[[torch.Tensor], None]] = None
+    row_bytes: int = 0  # INT8 only: row stride (0 = 4 + dim rounded up to 4)
+
+
+@dataclass
+class EmbeddingConfig:
+    """Mirrors torchrec.EmbeddingConfig (embedding.py:60-66)."""
+    num_embeddings: int
+    embedding_dim: int
+    name: str = ""
+    data_type: DataType = DataType.FP32
+    feature_names: List[str] = field(default_factory=list)
+    init_fn: Optional[Callable[[torch.Tensor], None]] = None
+    pooling: PoolingType = PoolingType.NONE
+
+
+@dataclass
+class EmbeddingTableConfig:
+    """Mirrors primus_dlrm.config.EmbeddingTableConfig (config.py:101-113)."""
+    name: str = ""
+    features: List[str] = field(default_factory=list)
+    num_embeddings: int = 0
+    embedding_dim: int = 0
+    pooling: str = "none"
+
+
+def _row_bytes(cfg) -> int:
+    if cfg.data_type == DataType.INT8:
+        rb = cfg.row_bytes if getattr(cfg, "row_bytes", 0) else (4 + cfg.embedding_dim + 3) & ~3
+        if rb < 4 + cfg.embedding_dim or rb % 4:
+            raise ValueError(f"table {cfg.name}: bad INT8 row_bytes {rb}")
+        return rb
+    return cfg.embedding_dim * torch.tensor([], dtype=_DT_TORCH[cfg.data_type]).element_size()
+
+
+def _default_init(w: torch.Tensor) -> None:
+    # TorchRec's default table init: U(-sqrt(1/rows), sqrt(1/rows)).
+    bound = math.sqrt(1.0 / max(w.shape[0], 1))
+    w.uniform_(-bound, bound)
+
+
+class _TableWeight(nn.Module):
+    def __init__(self, weight: torch.Tensor):
+        super().__init__()
+        self.weight = nn.Parameter(weight, requires_grad=False)
+
+
+class _FlatTables(nn.Module):
+    """All tables of a collection in one uint8 device buffer, exposed as typed
+    per-table ``weight`` views under ``<prefix>.<table>.weight``."""
+
+    ALIGN = 256
+
+    def __init__(self, configs: Sequence, prefix: str, device: torch.device, init_chunk_rows: int = 1 << 20):
+        super().__init__()
+        self._configs = list(configs)
+        self._prefix = prefix
+        self.offsets: List[int] = []
+        off = 0
+        for cfg in self._configs:
+            off = (off + self.ALIGN - 1) // self.ALIGN * self.ALIGN
+            self.offsets.append(off)
+            off += cfg.num_embeddings * _row_bytes(cfg)
+        self.total_bytes = max(off, 1)
+        flat = torch.empty(self.total_bytes, dtype=torch.uint8, device=device)
+        self.register_buffer("_flat", flat, persistent=False)
+        setattr(self, prefix, nn.ModuleDict())
+        self._make_views()
+        self._initialise(init_chunk_rows)
+
+    def _view(self, i: int) -> torch.Tensor:
+        cfg = self._configs[i]
+        rb = _row_bytes(cfg)
+        raw = self._flat.narrow(0, self.offsets[i], cfg.num_embeddings * rb)
+        if cfg.data_type == DataType.INT8:
+            return raw.view(cfg.num_embeddings, rb)
+        return raw.view(_DT_TORCH[cfg.data_type]).view(cfg.num_embeddings, cfg.embedding_dim)
+
+    def _make_views(self) -> None:
+        md = getattr(self, self._prefix)
+        for i, cfg in enumerate(self._configs):
+            md[cfg.name] = _TableWeight(self._view(i))
+
+    @torch.no_grad()
+    def _initialise(self, chunk: int) -> None:
+        for i, cfg in enumerate(self._configs):
+            init = cfg.init_fn or _default_init
+            w = self._view(i)
+            rows = cfg.num_embeddings
+            if rows == 0:
+                continue
+            if cfg.data_type == DataType.FP32 and cfg.init_fn is not None:
+                init(w)
+                continue
+            for r0 in range(0, rows, chunk):
+                n = min(chunk, rows - r0)
+                tmp = torch.empty((n, cfg.embedding_dim), dtype=torch.float32, device=w.device)
+                if cfg.init_fn is None:
+                    bound = math.sqrt(1.0 / rows)
+                    tmp.uniform_(-bound, bound)
+                else:
+                    init(tmp)
+                if cfg.data_type == DataType.INT8:
+                    if w.device.type == "cuda":
+                        w[r0:r0 + n].copy_(ops.int8_rowwise_quantize(tmp, _row_bytes(cfg)))
+                    else:
+                        w[r0:r0 + n].zero_()  # CPU construction: quantize after moving to the GPU
+                else:
+                    w[r0:r0 + n].copy_(tmp)
+
+    def _apply(self, fn, recurse=True):
+        # Keep the per-table parameters views of the (moved) flat buffer.
+        self._flat = fn(self._flat)
+        self._make_views()
+        return self
+
+    @property
+    def flat(self) -> torch.Tensor:
+        return self._flat
+
+    def weight(self, name: str) -> torch.Tensor:
+        return getattr(self, self._prefix)[name].weight
+
+
+def _kjt_slot_offsets(kjt, order: List[str]) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Returns (values, offsets) with bags laid out key-major in ``order``.
+
+    Zero copy when the KJT already holds exactly ``order``; otherwise values
+    are gathered on the device into the requested key order (TorchRec permutes
+    the KJT the same way before its lookup)."""
+    keys = list(kjt.keys())
+    values = kjt.values()
+    B = kjt.stride()
+    offsets = kjt.offsets().to(torch.int64)
+    if keys == order:
+        return values, offsets
+    pos = {k: i for i, k in enumerate(keys)}
+    missing = [k for k in order if k not in pos]
+    if missing:
+        raise KeyError(f"KeyedJaggedTensor lacks features {missing}")
+    dev = values.device
+    lengths = kjt.lengths().to(torch.int64).view(len(keys), B)
+    perm = torch.tensor([pos[k] for k in order], device=dev)
+    new_lengths = lengths.index_select(0, perm).reshape(-1)
+    new_offsets = torch.zeros(new_lengths.numel() + 1, dtype=torch.int64, device=dev)
+    torch.cumsum(new_lengths, 0, out=new_offsets[1:])
+    if sorted(order) == sorted(keys):
+        total = values.numel()
+    else:
+        total = int(new_offsets[-1].item())  # a subset of keys: the output size needs one sync
+    i = torch.arange(total, device=dev)
+    seg = torch.searchsorted(new_offsets, i, right=True) - 1
+    old_starts = offsets[:-1].view(len(keys), B).index_select(0, perm).reshape(-1)
+    src = old_starts[seg] + (i - new_offsets[seg])
+    return values[src], new_offsets
+
+
+class EmbeddingBagCollection(nn.Module):
+    """Pooled lookups of several tables in one table-batched launch per
+    (dtype, dim) group.  Output ``KeyedTensor`` columns follow table order,
+    then feature order inside a table (TorchRec's order)."""
+
+    def __init__(self, tables: List[EmbeddingBagConfig], device: Optional[torch.device] = None,
+                 output_dtype: torch.dtype = torch.float32, is_weighted: bool = False):
+        super().__init__()
+        if is_weighted:
+            raise NotImplementedError("per-sample weights are not on this path")
+        if device is None:
+            device = torch.device("cuda")
+        device = torch.device(device)
+        names = [t.name for t in tables]
+        if len(set(names)) != len(names):
+            raise ValueError("table names must be unique")
+        for t in tables:
+            if t.pooling not in (PoolingType.SUM, PoolingType.MEAN):
+                raise ValueError(f"table {t.name}: EmbeddingBagCollection needs SUM or MEAN pooling")
+            if t.embedding_dim % 4:
+                raise ValueError(f"table {t.name}: embedding_dim must be a multiple of 4")
+        self._tables = list(tables)
+        self._output_dtype = output_dtype
+        self._store = _FlatTables(tables, "embedding_bags", device)
+        self._feature_names: List[str] = []
+        self._dims: List[int] = []
+        self._slots: List[dict] = []
+        col = 0
+        for i, t in enumerate(tables):
+            for f in t.feature_names:
+                self._feature_names.append(f)
+                self._dims.append(t.embedding_dim)
+                self._slots.append(dict(rows=t.num_embeddings, weights_offset=self._store.offsets[i],
+                                        dim=t.embedding_dim, dtype=_DT_PDM[t.data_type],
+                                        pooling=_POOL_PDM[t.pooling], row_bytes=_row_bytes(t), out_offset=col))
+                col += t.embedding_dim
+        self._total_dim = col
+        self._plan: Optional[ops.TbePlan] = None
+        self._plan_device: Optional[torch.device] = None
+
+    # TorchRec-style accessors
+    @property
+    def embedding_bags(self) -> nn.ModuleDict:
+        return self._store.embedding_bags
+
+    def embedding_bag_configs(self) -> List[EmbeddingBagConfig]:
+        return self._tables
+
+    def feature_names(self) -> List[str]:
+        return self._feature_names
+
+    def state_dict(self, *args, **kwargs):
+        sd = super().state_dict(*args, **kwargs)
+        prefix = kwargs.get("prefix", args[1] if len(args) > 1 else "")
+        return {k.replace(prefix + "_store.", prefix, 1): v for k, v in sd.items()}
+
+    def load_state_dict(self, state_dict, strict: bool = True, assign: bool = False):
+        with torch.no_grad():
+            for t in self._tables:
+                key = f"embedding_bags.{t.name}.weight"
+                if key in state_dict:
+                    self._store.weight(t.name).copy_(state_dict[key])
+                elif strict:
+                    raise KeyError(f"missing key {key}")
+        return None
+
+    def _get_plan(self) -> ops.TbePlan:
+        dev = self._store.flat.device
+        if self._plan is None or self._plan_device != dev:
+            self._plan = ops.TbePlan(self._slots, dev)
+            self._plan_device = dev
+        return self._plan
+
+    def pooled(self, values: torch.Tensor, offsets: torch.Tensor, batch_size: int,
+               padding_idx: int = -1, err_flag: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """Raw table-batched call: ``offsets`` is ``[T*B+1]`` over this
+        collection's feature order; returns ``[B, sum D]``."""
+        return ops.tbe_pooled_raw(self._get_plan(), self._store.flat, values, offsets, batch_size,
+                                  self._output_dtype, padding_idx, err_flag=err_flag)
+
+    def forward(self, features) -> KeyedTensor:
+        values, offsets = _kjt_slot_offsets(features, self._feature_names)
+        plan = self._get_plan()
+        code = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}[self._output_dtype]
+        out = torch.ops.pdm.tbe_pooled_fwd(self._store.flat, values, offsets, plan.plan_id, plan.num_slots,
+                                           self._total_dim, code, -1)
+        return KeyedTensor(self._feature_names, self._dims, out)
+
+
+class EmbeddingCollection(nn.Module):
+    """Unpooled lookups: every id of feature f becomes row ``weight[id]`` of
+    f's table, bit-exact (a one-id bag summed in fp32 and written in the
+    table's dtype is the stored value)."""
+
+    def __init__(self, tables: List[EmbeddingConfig], device: Optional[torch.device] = None):
+        super().__init__()
+        if device is None:
+            device = torch.device("cuda")
+        device = torch.device(device)
+        for t in tables:
+            if t.data_type == DataType.INT8:
+                raise ValueError("EmbeddingCollection tables must be FP32, FP16 or BF16")
+            if t.embedding_dim % 4:
+                raise ValueError(f"table {t.name}: embedding_dim must be a multiple of 4")
+        self._tables = list(tables)
+        self._store = _FlatTables(tables, "embeddings", device)
+        self._feature_names: List[str] = []
+        self._feature_table: Dict[str, int] = {}
+        for i, t in enumerate(tables):
+            for f in t.feature_names:
+                self._feature_names.append(f)
+                self._feature_table[f] = i
+        self._plans: Dict[Tuple[int, str], ops.TbePlan] = {}
+
+    @property
+    def embeddings(self) -> nn.ModuleDict:
+        return self._store.embeddings
+
+    def embedding_configs(self) -> List[EmbeddingConfig]:
+        return self._tables
+
+    def feature_names(self) -> List[str]:
+        return self._feature_names
+
+    def table_of(self, feature: str) -> torch.Tensor:
+        return self._store.weight(self._tables[self._feature_table[feature]].name)
+
+    def state_dict(self, *args, **kwargs):
+        sd = super().state_dict(*args, **kwargs)
+        prefix = kwargs.get("prefix", args[1] if len(args) > 1 else "")
+        return {k.replace(prefix + "_store.", prefix, 1): v for k, v in sd.items()}
+
+    def load_state_dict(self, state_dict, strict: bool = True, assign: bool = False):
+        with torch.no_grad():
+            for t in self._tables:
+                key = f"embeddings.{t.name}.weight"
+                if key in state_dict:
+                    self._store.weight(t.name).copy_(state_dict[key])
+                elif strict:
+                    raise KeyError(f"missing key {key}")
+        return None
+
+    def _plan_for(self, ti: int) -> ops.TbePlan:
+        dev = self._store.flat.device
+        key = (ti, str(dev))
+        if key not in self._plans:
+            t = self._tables[ti]
+            self._plans[key] = ops.TbePlan([dict(rows=t.num_embeddings, weights_offset=self._store.offsets[ti],
+                                                 dim=t.embedding_dim, dtype=_DT_PDM[t.data_type],
+                                                 pooling=L.PDM_POOL_SUM, row_bytes=_row_bytes(t),
+                                                 out_offset=0)], dev)
+        return self._plans[key]
+
+    def gather(self, feature: str, ids: torch.Tensor) -> torch.Tensor:
+        """``weight[ids]`` for a flat id vector of ``feature``: ``[n, D]``."""
+        ti = self._feature_table[feature]
+        t = self._tables[ti]
+        ids = ids.reshape(-1)
+        if not ids.is_contiguous():
+            ids = ids.contiguous()
+        n = ids.numel()
+        offsets = torch.arange(n + 1, dtype=torch.int64, device=ids.device)
+        return ops.tbe_pooled_raw(self._plan_for(ti), self._store.flat, ids, offsets, n, _DT_TORCH[t.data_type])
+
+    def forward(self, features) -> Dict[str, JaggedTensor]:
+        keys = list(features.keys())
+        B = features.stride()
+        offsets = features.offsets().to(torch.int64)
+        bounds = offsets.view(-1)[:: B] if B > 0 else offsets[:1]
+        starts = bounds.tolist()  # per-key value ranges: one host sync, as TorchRec's length_per_key()
+        out: Dict[str, JaggedTensor] = {}
+        values = features.values()
+        for k, name in enumerate(keys):
+            if name not in self._feature_table:
+                continue
+            lo, hi = starts[k], starts[k + 1]
+            seg = values[lo:hi]
+            rows = self.gather(name, seg)
+            seg_off = offsets[k * B:(k + 1) * B + 1] - lo
+            out[name] = JaggedTensor(rows, offsets=seg_off)
+        return out
+
+
+class SequenceGather(nn.Module):
+    """Jagged behaviour-pool ids -> padded S-token rows on the device.
+
+    ``sequence_groups`` maps a pool name to its features (concat order per
+    event, e.g. ``{"hist_lp": ["hist_lp_item", "hist_lp_artist", "hist_lp_album"], ...}``,
+    reference: configs/bench_onetrans_v6.yaml:33-35, onetrans.py:515-520).
+    Feature ``f`` is looked up in ``tables[feature_table[f]]`` (an
+    ``EmbeddingCollection``'s tables).  Pools are laid out along the sequence
+    in ``sequence_groups`` order, each padded to ``max_len[pool]``.
+
+    ``pad_mode="row0"`` with ``align="right"`` reproduces the reference
+    exactly (left padding with id 0, whose lookup is table row 0);
+    ``pad_mode="zero"`` writes zero rows instead.
+    """
+
+    def __init__(self, ec: EmbeddingCollection, sequence_groups: Dict[str, List[str]],
+                 max_len: Dict[str, int] | int, pad_mode: str = "row0", align: str = "right"):
+        super().__init__()
+        self.ec = ec
+        self.groups = {g: list(fs) for g, fs in sequence_groups.items()}
+        nfeat = {len(fs) for fs in self.groups.values()}
+        if len(nfeat) != 1:
+            raise ValueError("every pool must list the same number of features")
+        self.max_len = {g: (max_len if isinstance(max_len, int) else int(max_len[g])) for g in self.groups}
+        self.pad_mode = {"row0": L.PDM_PAD_ROW0, "zero": L.PDM_PAD_ZERO}[pad_mode]
+        self.align = {"right": L.PDM_ALIGN_RIGHT, "left": L.PDM_ALIGN_LEFT}[align]
+        first = next(iter(self.groups.values()))
+        # the k-th feature of every pool must use the same table as the first pool's
+        for fs in self.groups.values():
+            for a, b in zip(fs, first):
+                if self.ec._feature_table[a] != self.ec._feature_table[b]:
+                    raise ValueError("the k-th feature of every pool must share one table")
+        self._feature_tables = [ec._feature_table[f] for f in first]
+
+    def slot_ranges(self) -> Dict[str, Tuple[int, int]]:
+        out, s = {}, 0
+        for g in self.groups:
+            out[g] = (s, self.max_len[g])
+            s += self.max_len[g]
+        return out
+
+    def forward(self, batch: Dict[str, torch.Tensor]) -> Tuple[torch.Tensor, torch.Tensor]:
+        """``batch[f]`` is the flat int64 id vector of feature f and
+        ``batch[f + "__lengths"]`` its per-sample lengths (the pipeline-batch
+        convention of primus_dlrm/data/synthetic.py:224-228); every feature of
+        a pool shares its lengths.  Returns (tokens ``[B, S, sum D]``,
+        mask bool ``[B, S]``)."""
+        tables = [self.ec._store.weight(self.ec._tables[ti].name) for ti in self._feature_tables]
+        ids, offsets, max_len = [], [], []
+        for g, fs in self.groups.items():
+            lengths = batch[fs[0] + "__lengths"]
+            off = torch.zeros(lengths.numel() + 1, dtype=torch.int64, device=lengths.device)
+            torch.cumsum(lengths.to(torch.int64), 0, out=off[1:])
+            offsets.append(off)
+            ids.append([batch[f].reshape(-1).to(torch.int64).contiguous() for f in fs])
+            max_len.append(self.max_len[g])
+        flat_ids = [t for row in ids for t in row]
+        out, mask = torch.ops.pdm.seq_gather_fwd(tables, flat_ids, offsets, max_len, self.pad_mode, self.align)
+        return out, mask.view(torch.bool)
+
+
+class TorchRecEmbeddings(nn.Module):
+    """Tensor-in / tensor-out lookup wrapper with the reference's constructor
+    and forward (primus_dlrm/models/embedding.py:72-174).
+
+    Pooled features: ``[B, L] -> [B, D]`` with ids equal to ``padding_idx``
+    skipped on the device (the reference removes them with boolean indexing
+    and a host sync in _build_pooled_kjt, embedding.py:179-204; here no sync).
+    Unpooled: ``[B] -> [B, D]``, ``[B, L] -> [B, L, D]``.
+    """
+
+    _POOLING = {"sum": PoolingType.SUM, "mean": PoolingType.MEAN}
+
+    def __init__(self, table_specs: List[EmbeddingTableConfig], device: Optional[torch.device] = None,
+                 embedding_init: str = "uniform", scalar_feature_names: Optional[set] = None,
+                 data_type: DataType = DataType.FP32):
+        super().__init__()
+        if device is None:
+            device = torch.device("cuda")
+        init_fn = None
+        if embedding_init == "normal":
+            def init_fn(w: torch.Tensor) -> None:
+                nn.init.normal_(w, mean=0.0, std=1.0)
+        pooled, unpooled = [], []
+        self._pooled_features: List[str] = []
+        self._unpooled_features: List[str] = []
+        self._feature_dims: Dict[str, int] = {}
+        for spec in table_specs:
+            for feat in spec.features:
+                self._feature_dims[feat] = spec.embedding_dim
+            if spec.pooling in self._POOLING:
+                pooled.append(EmbeddingBagConfig(spec.num_embeddings, spec.embedding_dim, spec.name, data_type,
+                                                 list(spec.features), self._POOLING[spec.pooling], init_fn))
+                self._pooled_features.extend(spec.features)
+            else:
+                unpooled.append(EmbeddingConfig(spec.num_embeddings, spec.embedding_dim, spec.name, data_type,
+                                                list(spec.features), init_fn))
+                self._unpooled_features.extend(spec.features)
+        self._pooled_set = set(self._pooled_features)
+        self._unpooled_set = set(self._unpooled_features)
+        self._scalar_features = (set(scalar_feature_names) & self._unpooled_set) if scalar_feature_names else set()
+        self.ebc = EmbeddingBagCollection(pooled, device) if pooled else None
+        self.ec = EmbeddingCollection(unpooled, device) if unpooled else None
+
+    def forward(self, features: Dict[str, torch.Tensor], padding_idx: int = 0) -> Dict[str, torch.Tensor]:
+        results: Dict[str, torch.Tensor] = {}
+        if self.ebc is not None:
+            present = [f for f in self._pooled_features if f in features]
+            if present:
+                if len(present) != len(self._pooled_features):
+                    raise KeyError(f"pooled lookup needs every pooled feature, missing "
+                                   f"{sorted(self._pooled_set - set(present))}")
+                B = features[present[0]].shape[0]
+                vals, offs, base = [], [], 0
+                for f in present:
+                    ids = features[f]
+                    if ids.dim() == 1:
+                        ids = ids.unsqueeze(1)
+                    if ids.shape[0] != B:
+                        raise ValueError("pooled features must share the batch size")
+                    Lf = ids.shape[1]
+                    vals.append(ids.reshape(-1))
+                    offs.append(torch.arange(B, device=ids.device, dtype=torch.int64) * Lf + base)
+                    base += B * Lf
+                offs.append(torch.full((1,), base, dtype=torch.int64, device=vals[0].device))
+                values = torch.cat(vals) if len(vals) > 1 else vals[0].contiguous()
+                if values.dtype not in (torch.int32, torch.int64):
+                    values = values.to(torch.int64)
+                out = self.ebc.pooled(values, torch.cat(offs), B, padding_idx)
+                col = 0
+                for f in self._pooled_features:
+                    D = self._feature_dims[f]
+                    results[f] = out[:, col:col + D]
+                    col += D
+        if self.ec is not None:
+            for f in self._unpooled_features:
+                if f not in features:
+                    continue
+                ids = features[f]
+                D = self._feature_dims[f]
+                rows = self.ec.gather(f, ids)
+                B = ids.shape[0]
+                results[f] = rows.view(B, D) if f in self._scalar_features else rows.view(B, -1, D)
+        return results

@@ -1,0 +1,160 @@
+"""OneTrans interaction block with the reference's module surface.
+
+``OneTransBlock(d_model, n_heads, n_ns_tokens, ffn_mult=4, dropout=0.0, attention_impl=...)``
+and ``forward(x, mask, q_len, n_s_tokens) -> [B, q_len, D]`` follow
+primus_dlrm/models/onetrans.py:207-231; parameter names and shapes
+(``norm1.weight``, ``attn.s_qkv.weight``, ``attn.ns_qkv_weight``,
+``attn.out_proj.weight``, ``norm2.weight``, ``ffn.s_w1.weight``,
+``ffn.s_w2.weight``, ``ffn.ns_w1``, ``ffn.ns_w2``; :77,111-113,180-184,214-218)
+match so reference state dicts load unchanged.  Forward runs the fused gfx950
+kernels in the numerics the reference gets under ``autocast(bf16)``
+(primus_dlrm/training/dist_trainer.py:471): bf16 GEMM operands with fp32
+accumulation, fp32 RMSNorm, exact-erf GELU, fp32 residual stream.
+
+``pyramid_schedule`` and ``build_pyramid_mask`` restate onetrans.py:50-67.
+"""
+from __future__ import annotations
+
+from typing import List, Optional, Sequence
+
+import torch
+import torch.nn as nn
+
+from . import ops
+
+
+def pyramid_schedule(l_s: int, l_ns: int, n_layers: int) -> List[int]:
+    """S-token queries kept per layer, shrinking linearly from l_s to l_ns
+    (onetrans.py:50-59; Python's round-half-even, floor at l_ns)."""
+    if n_layers == 1:
+        return [l_ns]
+    out = []
+    for layer in range(n_layers):
+        q = l_s - layer * (l_s - l_ns) / (n_layers - 1)
+        out.append(max(int(round(q)), l_ns))
+    return out
+
+
+def build_pyramid_mask(q_len: int, kv_len: int, device: torch.device) -> torch.Tensor:
+    """Bottom-right causal mask ``[q_len, kv_len]``: query i sees keys
+    j <= i + (kv_len - q_len) (onetrans.py:62-67)."""
+    offset = kv_len - q_len
+    q_idx = torch.arange(q_len, device=device).unsqueeze(1) + offset
+    kv_idx = torch.arange(kv_len, device=device).unsqueeze(0)
+    return kv_idx <= q_idx
+
+
+class RMSNorm(nn.Module):
+    """Parameter container with the reference's RMSNorm surface (onetrans.py:74-82)."""
+
+    def __init__(self, d: int, eps: float = 1e-6):
+        super().__init__()
+        self.weight = nn.Parameter(torch.ones(d))
+        self.eps = eps
+
+
+class MixedAttention(nn.Module):
+    """Parameters of the reference MixedAttention (onetrans.py:85-121)."""
+
+    def __init__(self, d_model: int, n_heads: int, n_ns_tokens: int, dropout: float = 0.0,
+                 attention_impl: str = "pdm"):
+        super().__init__()
+        if d_model % n_heads:
+            raise ValueError("d_model must be divisible by n_heads")
+        self.d_model, self.n_heads, self.d_head, self.n_ns = d_model, n_heads, d_model // n_heads, n_ns_tokens
+        self.attention_impl = attention_impl
+        self.s_qkv = nn.Linear(d_model, 3 * d_model, bias=False)
+        self.ns_qkv_weight = nn.Parameter(torch.empty(n_ns_tokens, 3 * d_model, d_model))
+        self.out_proj = nn.Linear(d_model, d_model, bias=False)
+        self.attn_drop = dropout
+        nn.init.xavier_uniform_(self.s_qkv.weight)
+        nn.init.xavier_uniform_(self.out_proj.weight)
+        for i in range(n_ns_tokens):
+            nn.init.xavier_uniform_(self.ns_qkv_weight.data[i])
+
+
+class MixedFFN(nn.Module):
+    """Parameters of the reference MixedFFN (onetrans.py:172-193)."""
+
+    def __init__(self, d_model: int, ffn_dim: int, n_ns_tokens: int, dropout: float = 0.0):
+        super().__init__()
+        self.n_ns, self.d_model = n_ns_tokens, d_model
+        self.s_w1 = nn.Linear(d_model, ffn_dim, bias=False)
+        self.s_w2 = nn.Linear(ffn_dim, d_model, bias=False)
+        self.ns_w1 = nn.Parameter(torch.empty(n_ns_tokens, ffn_dim, d_model))
+        self.ns_w2 = nn.Parameter(torch.empty(n_ns_tokens, d_model, ffn_dim))
+        self.dropout = nn.Dropout(dropout)
+        nn.init.xavier_uniform_(self.s_w1.weight)
+        nn.init.xavier_uniform_(self.s_w2.weight)
+        for i in range(n_ns_tokens):
+            nn.init.xavier_uniform_(self.ns_w1.data[i])
+            nn.init.xavier_uniform_(self.ns_w2.data[i])
+
+
+class OneTransBlock(nn.Module):
+    """Pre-norm causal block with shared S-token and per-token NS weights.
+
+    Forward only (inference / evaluation); dropout must be inactive.  ``x``
+    is the fp32 residual stream ``[B, kv_len, D]`` whose last ``n_ns`` tokens
+    are the NS-tokens; ``mask`` must be ``build_pyramid_mask(q_len, kv_len)``
+    (only its shape is checked, so no host sync happens).
+    """
+
+    def __init__(self, d_model: int, n_heads: int, n_ns_tokens: int, ffn_mult: int = 4,
+                 dropout: float = 0.0, attention_impl: str = "pdm"):
+        super().__init__()
+        self.norm1 = RMSNorm(d_model)
+        self.attn = MixedAttention(d_model, n_heads, n_ns_tokens, dropout, attention_impl)
+        self.norm2 = RMSNorm(d_model)
+        self.ffn = MixedFFN(d_model, d_model * ffn_mult, n_ns_tokens, dropout)
+        self._bf16_cache: Optional[tuple] = None
+
+    def _bf16_weights(self):
+        params = (self.attn.s_qkv.weight, self.attn.ns_qkv_weight, self.attn.out_proj.weight,
+                  self.ffn.s_w1.weight, self.ffn.s_w2.weight, self.ffn.ns_w1, self.ffn.ns_w2)
+        key = tuple((p.data_ptr(), p._version, p.device) for p in params)
+        if self._bf16_cache is None or self._bf16_cache[0] != key:
+            # autocast casts fp32 weights to bf16 for every matmul; cast once per weight version
+            conv = tuple(p.detach().to(torch.bfloat16).contiguous() for p in params)
+            self._bf16_cache = (key, conv)
+        return self._bf16_cache[1]
+
+    def forward(self, x: torch.Tensor, mask: torch.Tensor, q_len: int, n_s_tokens: int) -> torch.Tensor:
+        if self.training and (self.attn.attn_drop > 0 or self.ffn.dropout.p > 0):
+            raise RuntimeError("OneTransBlock forward kernels do not implement dropout; call .eval()")
+        kv_len = x.shape[1]
+        if n_s_tokens != kv_len - self.attn.n_ns:
+            raise ValueError(f"n_s_tokens ({n_s_tokens}) must equal kv_len - n_ns ({kv_len - self.attn.n_ns})")
+        if mask is not None and tuple(mask.shape) != (q_len, kv_len):
+            raise ValueError(f"mask must be [q_len, kv_len] = [{q_len}, {kv_len}]")
+        if x.dtype != torch.float32:
+            raise TypeError("the residual stream x must be fp32 (the reference's stream with positional "
+                            "embeddings under autocast)")
+        s_qkv, ns_qkv, out_w, s_w1, s_w2, ns_w1, ns_w2 = self._bf16_weights()
+        return torch.ops.pdm.onetrans_block_fwd(
+            x.contiguous(), self.norm1.weight.detach().float().contiguous(), s_qkv, ns_qkv, out_w,
+            self.norm2.weight.detach().float().contiguous(), s_w1, s_w2, ns_w1, ns_w2,
+            self.attn.n_heads, int(q_len))
+
+
+class OneTransStack(nn.Module):
+    """The block loop of OneTransModel._backbone (onetrans.py:568-582): layer
+    l keeps ``schedule[l] + n_ns`` query tokens of the previous output."""
+
+    def __init__(self, d_model: int, n_heads: int, n_ns_tokens: int, n_layers: int, ffn_mult: int = 4,
+                 schedule: Optional[Sequence[int]] = None):
+        super().__init__()
+        self.n_ns = n_ns_tokens
+        self.schedule = list(schedule) if schedule is not None else None
+        self.blocks = nn.ModuleList([OneTransBlock(d_model, n_heads, n_ns_tokens, ffn_mult)
+                                     for _ in range(n_layers)])
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        L_S = x.shape[1] - self.n_ns
+        schedule = self.schedule or pyramid_schedule(L_S, self.n_ns, len(self.blocks))
+        for layer, block in enumerate(self.blocks):
+            q_len = schedule[layer] + self.n_ns
+            kv_len = x.shape[1]
+            mask = build_pyramid_mask(q_len, kv_len, x.device)
+            x = block(x, mask=mask, q_len=q_len, n_s_tokens=kv_len - self.n_ns)
+        return x

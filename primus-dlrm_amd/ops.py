@@ -1,0 +1,285 @@
+"""PyTorch custom ops over the C ABI (include/pdm.h).
+
+Each op validates shapes, dtypes and devices on the host, then enqueues the
+HIP kernels of libpdm.so on torch's current stream.  Ops are registered with
+``torch.library.custom_op`` and carry fake (meta) kernels, so FX tracing and
+``torch.compile(dynamic=True)`` see them as single opaque nodes (the
+reference compiles its blocks that way: primus_dlrm/models/onetrans.py:382-390).
+
+There is no CPU implementation: called with CPU tensors these ops raise.
+"""
+from __future__ import annotations
+
+import ctypes
+import itertools
+import threading
+from typing import Dict, List, Optional, Sequence, Tuple
+
+import torch
+
+from . import _lib as L
+
+TORCH_TO_PDM = {torch.float32: L.PDM_F32, torch.float16: L.PDM_F16, torch.bfloat16: L.PDM_BF16}
+PDM_TO_TORCH = {v: k for k, v in TORCH_TO_PDM.items()}
+
+
+def _require_cuda(*tensors: torch.Tensor) -> torch.device:
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise RuntimeError(f"pdm ops run on the GPU only; got a tensor on {t.device}")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise RuntimeError(f"tensors on different devices: {dev} and {t.device}")
+    return dev
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+# ---------------------------------------------------------------------------
+# Pooled TBE
+# ---------------------------------------------------------------------------
+
+class TbePlan:
+    """A pdm_tbe_plan: per-slot table metadata resident on one device.
+
+    ``slots`` are dicts with keys rows, weights_offset, dim, dtype (pdm
+    dtype), pooling (pdm pooling), row_bytes, out_offset.  A slot is one
+    pooled output (one feature); several slots may share a table.
+    """
+
+    _registry: Dict[int, "TbePlan"] = {}
+    _ids = itertools.count(1)
+    _lock = threading.Lock()
+
+    def __init__(self, slots: Sequence[dict], device: torch.device):
+        if not slots:
+            raise ValueError("a TBE plan needs at least one table slot")
+        arr = (L.TableDesc * len(slots))()
+        for i, s in enumerate(slots):
+            arr[i] = L.TableDesc(int(s["rows"]), int(s["weights_offset"]), int(s["dim"]), int(s["dtype"]),
+                                 int(s["pooling"]), int(s.get("row_bytes", 0)), int(s["out_offset"]), 0)
+        handle = ctypes.c_void_p()
+        with torch.cuda.device(device):
+            L.check(L.lib().pdm_tbe_plan_create(arr, len(slots), ctypes.byref(handle)), "pdm_tbe_plan_create")
+        self.handle = handle
+        self.device = torch.device(device)
+        self.num_slots = len(slots)
+        self.total_dim = int(L.lib().pdm_tbe_plan_total_dim(handle))
+        with TbePlan._lock:
+            self.plan_id = next(TbePlan._ids)
+            TbePlan._registry[self.plan_id] = self
+
+    def release(self) -> None:
+        if self.handle is not None and self.handle.value:
+            with TbePlan._lock:
+                TbePlan._registry.pop(self.plan_id, None)
+            L.lib().pdm_tbe_plan_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.release()
+        except Exception:
+            pass
+
+    @staticmethod
+    def get(plan_id: int) -> "TbePlan":
+        try:
+            return TbePlan._registry[plan_id]
+        except KeyError:
+            raise RuntimeError(f"TBE plan {plan_id} does not exist (released?)") from None
+
+
+def tbe_pooled_raw(plan: TbePlan, weights: torch.Tensor, indices: torch.Tensor, offsets: torch.Tensor,
+                   batch_size: int, out_dtype: torch.dtype = torch.float32, padding_idx: int = -1,
+                   out: Optional[torch.Tensor] = None, err_flag: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Launches pdm_tbe_pooled_fwd; returns ``out`` ([B, total_dim])."""
+    dev = _require_cuda(weights, indices, offsets, out, err_flag)
+    if indices.dtype not in (torch.int32, torch.int64):
+        raise TypeError(f"indices must be int32 or int64, got {indices.dtype}")
+    if offsets.dtype != torch.int64:
+        raise TypeError(f"offsets must be int64, got {offsets.dtype}")
+    if not (weights.is_contiguous() and indices.is_contiguous() and offsets.is_contiguous()):
+        raise ValueError("weights, indices and offsets must be contiguous")
+    if offsets.numel() != plan.num_slots * batch_size + 1:
+        raise ValueError(f"offsets has {offsets.numel()} entries, expected T*B+1 = "
+                         f"{plan.num_slots * batch_size + 1}")
+    if out_dtype not in TORCH_TO_PDM:
+        raise TypeError(f"unsupported output dtype {out_dtype}")
+    if out is None:
+        out = torch.empty((batch_size, plan.total_dim), dtype=out_dtype, device=dev)
+    elif out.dim() != 2 or out.shape[0] != batch_size or out.stride(1) != 1 or out.dtype != out_dtype:
+        raise ValueError("out must be [B, >=total_dim] with unit column stride and the requested dtype")
+    if out.shape[1] < plan.total_dim:
+        raise ValueError("out has fewer columns than the plan writes")
+    if err_flag is not None and (err_flag.dtype != torch.int32 or err_flag.numel() < 1):
+        raise ValueError("err_flag must be an int32 tensor with at least one element")
+    status = L.lib().pdm_tbe_pooled_fwd(
+        plan.handle, weights.data_ptr(), indices.data_ptr() if indices.numel() else None,
+        32 if indices.dtype == torch.int32 else 64, indices.numel(), offsets.data_ptr(), batch_size,
+        padding_idx, out.data_ptr(), TORCH_TO_PDM[out_dtype], out.stride(0), _ptr(err_flag),
+        L.stream_ptr(dev))
+    L.check(status, "pdm_tbe_pooled_fwd")
+    return out
+
+
+_DTYPE_CODES = {0: torch.float32, 1: torch.float16, 2: torch.bfloat16}
+
+
+@torch.library.custom_op("pdm::tbe_pooled_fwd", mutates_args=())
+def tbe_pooled_fwd(weights: torch.Tensor, indices: torch.Tensor, offsets: torch.Tensor, plan_id: int,
+                   num_slots: int, total_dim: int, out_dtype_code: int, padding_idx: int) -> torch.Tensor:
+    plan = TbePlan.get(plan_id)
+    batch = (offsets.numel() - 1) // num_slots
+    return tbe_pooled_raw(plan, weights, indices, offsets, batch, _DTYPE_CODES[out_dtype_code], padding_idx)
+
+
+@tbe_pooled_fwd.register_fake
+def _(weights, indices, offsets, plan_id, num_slots, total_dim, out_dtype_code, padding_idx):
+    batch = (offsets.shape[0] - 1) // num_slots
+    return weights.new_empty((batch, total_dim), dtype=_DTYPE_CODES[out_dtype_code])
+
+
+def int8_rowwise_quantize(src: torch.Tensor, row_bytes: int = 0) -> torch.Tensor:
+    """fp32 [rows, dim] -> uint8 [rows, row_bytes] int8-rowwise rows
+    ([fp16 scale][fp16 bias][dim x uint8], padded to row_bytes)."""
+    dev = _require_cuda(src)
+    if src.dtype != torch.float32 or src.dim() != 2 or not src.is_contiguous():
+        raise ValueError("src must be a contiguous fp32 [rows, dim] tensor")
+    rows, dim = src.shape
+    if row_bytes == 0:
+        row_bytes = (4 + dim + 3) & ~3
+    dst = torch.empty((rows, row_bytes), dtype=torch.uint8, device=dev)
+    L.check(L.lib().pdm_int8_rowwise_quantize(src.data_ptr(), rows, dim, dst.data_ptr(), row_bytes,
+                                              L.stream_ptr(dev)), "pdm_int8_rowwise_quantize")
+    return dst
+
+
+# ---------------------------------------------------------------------------
+# Jagged -> padded S-token gather
+# ---------------------------------------------------------------------------
+
+def seq_gather_raw(tables: Sequence[torch.Tensor], ids: Sequence[Sequence[torch.Tensor]],
+                   offsets: Sequence[torch.Tensor], max_len: Sequence[int], pad_mode: int = L.PDM_PAD_ROW0,
+                   align: int = L.PDM_ALIGN_RIGHT, want_mask: bool = True,
+                   err_flag: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
+    """tables[f]: [rows_f, dim_f]; ids[p][f]: int64 [n_p]; offsets[p]: int64 [B+1].
+    Returns out [B, sum(max_len), sum(dim)] and mask uint8 [B, sum(max_len)]."""
+    P, F = len(offsets), len(tables)
+    if not (1 <= P <= L.PDM_SEQ_MAX_POOLS and 1 <= F <= L.PDM_SEQ_MAX_FEATURES):
+        raise ValueError(f"need 1..{L.PDM_SEQ_MAX_POOLS} pools and 1..{L.PDM_SEQ_MAX_FEATURES} features")
+    if len(ids) != P or any(len(r) != F for r in ids) or len(max_len) != P:
+        raise ValueError("ids must be [pools][features] and max_len one per pool")
+    flat_ids = [t for row in ids for t in row]
+    dev = _require_cuda(*tables, *flat_ids, *offsets, err_flag)
+    dtype = tables[0].dtype
+    if dtype not in TORCH_TO_PDM:
+        raise TypeError(f"unsupported table dtype {dtype}")
+    B = offsets[0].numel() - 1
+    desc = L.SeqDesc()
+    desc.num_pools, desc.num_features = P, F
+    desc.dtype, desc.pad_mode, desc.align = TORCH_TO_PDM[dtype], pad_mode, align
+    desc.batch_size = B
+    for f, t in enumerate(tables):
+        if t.dtype != dtype or t.dim() != 2 or not t.is_contiguous():
+            raise ValueError("tables must be contiguous 2-D tensors of one dtype")
+        desc.dim[f] = t.shape[1]
+        desc.rows[f] = t.shape[0]
+    for p in range(P):
+        o = offsets[p]
+        if o.dtype != torch.int64 or o.dim() != 1 or o.numel() != B + 1 or not o.is_contiguous():
+            raise ValueError("offsets must be contiguous int64 [B+1], the same B for every pool")
+        n = ids[p][0].numel()
+        for t in ids[p]:
+            if t.dtype != torch.int64 or t.dim() != 1 or not t.is_contiguous() or t.numel() != n:
+                raise ValueError("ids of one pool must be contiguous int64 vectors of equal length")
+        desc.num_ids[p] = n
+        if int(max_len[p]) < 0:
+            raise ValueError("max_len must be >= 0")
+        desc.max_len[p] = int(max_len[p])
+    S = sum(int(m) for m in max_len)
+    Dtot = sum(t.shape[1] for t in tables)
+    out = torch.empty((B, S, Dtot), dtype=dtype, device=dev)
+    mask = torch.empty((B, S), dtype=torch.uint8, device=dev) if want_mask else None
+    tab_arr = (ctypes.c_void_p * F)(*[t.data_ptr() for t in tables])
+    ids_arr = (ctypes.c_void_p * (P * F))(*[t.data_ptr() if t.numel() else None for t in flat_ids])
+    off_arr = (ctypes.c_void_p * P)(*[o.data_ptr() for o in offsets])
+    status = L.lib().pdm_seq_gather_fwd(ctypes.byref(desc), tab_arr, ids_arr, off_arr, out.data_ptr(),
+                                        _ptr(mask), _ptr(err_flag), L.stream_ptr(dev))
+    L.check(status, "pdm_seq_gather_fwd")
+    return out, mask
+
+
+@torch.library.custom_op("pdm::seq_gather_fwd", mutates_args=())
+def seq_gather_fwd(tables: List[torch.Tensor], ids: List[torch.Tensor], offsets: List[torch.Tensor],
+                   max_len: List[int], pad_mode: int, align: int) -> Tuple[torch.Tensor, torch.Tensor]:
+    F = len(tables)
+    grid = [ids[p * F:(p + 1) * F] for p in range(len(offsets))]
+    out, mask = seq_gather_raw(tables, grid, offsets, max_len, pad_mode, align, want_mask=True)
+    return out, mask
+
+
+@seq_gather_fwd.register_fake
+def _(tables, ids, offsets, max_len, pad_mode, align):
+    B = offsets[0].shape[0] - 1
+    S = sum(max_len)
+    D = sum(t.shape[1] for t in tables)
+    return (tables[0].new_empty((B, S, D)), tables[0].new_empty((B, S), dtype=torch.uint8))
+
+
+# ---------------------------------------------------------------------------
+# OneTrans block
+# ---------------------------------------------------------------------------
+
+def onetrans_block_raw(x: torch.Tensor, w: Dict[str, torch.Tensor], n_heads: int, q_len: int,
+                       out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """x: fp32 [B, kv, D]; w: norm1_w/norm2_w fp32 [D], the GEMM weights bf16
+    in nn.Linear layout.  Returns fp32 [B, q_len, D]."""
+    names = ("norm1_w", "s_qkv_w", "ns_qkv_w", "out_w", "norm2_w", "s_w1", "s_w2", "ns_w1", "ns_w2")
+    dev = _require_cuda(x, *[w[k] for k in names])
+    if x.dtype != torch.float32 or x.dim() != 3 or not x.is_contiguous():
+        raise ValueError("x must be a contiguous fp32 [B, kv_len, D] tensor")
+    B, kv, D = x.shape
+    n_ns = w["ns_qkv_w"].shape[0]
+    Fd = w["s_w1"].shape[0]
+    shapes = {"norm1_w": (D,), "s_qkv_w": (3 * D, D), "ns_qkv_w": (n_ns, 3 * D, D), "out_w": (D, D),
+              "norm2_w": (D,), "s_w1": (Fd, D), "s_w2": (D, Fd), "ns_w1": (n_ns, Fd, D), "ns_w2": (n_ns, D, Fd)}
+    for k in names:
+        t = w[k]
+        want = torch.float32 if k.startswith("norm") else torch.bfloat16
+        if tuple(t.shape) != shapes[k] or t.dtype != want or not t.is_contiguous():
+            raise ValueError(f"{k}: expected contiguous {want} {shapes[k]}, got {t.dtype} {tuple(t.shape)}")
+    if not (n_ns <= q_len <= kv):
+        raise ValueError(f"need n_ns <= q_len <= kv_len, got n_ns={n_ns} q_len={q_len} kv_len={kv}")
+    desc = L.BlockDesc(B, D, n_heads, n_ns, Fd, kv, q_len, 0)
+    ws_bytes = int(L.lib().pdm_onetrans_block_workspace_size(ctypes.byref(desc)))
+    if ws_bytes < 0:
+        raise L.PdmError(ws_bytes, "pdm_onetrans_block_workspace_size", L.last_error())
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    if out is None:
+        out = torch.empty((B, q_len, D), dtype=torch.float32, device=dev)
+    bw = L.BlockWeights(*[w[k].data_ptr() for k in names])
+    status = L.lib().pdm_onetrans_block_fwd(ctypes.byref(desc), x.data_ptr(), ctypes.byref(bw), out.data_ptr(),
+                                            ws.data_ptr(), ws_bytes, L.stream_ptr(dev))
+    L.check(status, "pdm_onetrans_block_fwd")
+    return out
+
+
+@torch.library.custom_op("pdm::onetrans_block_fwd", mutates_args=())
+def onetrans_block_fwd(x: torch.Tensor, norm1_w: torch.Tensor, s_qkv_w: torch.Tensor, ns_qkv_w: torch.Tensor,
+                       out_w: torch.Tensor, norm2_w: torch.Tensor, s_w1: torch.Tensor, s_w2: torch.Tensor,
+                       ns_w1: torch.Tensor, ns_w2: torch.Tensor, n_heads: int, q_len: int) -> torch.Tensor:
+    w = dict(norm1_w=norm1_w, s_qkv_w=s_qkv_w, ns_qkv_w=ns_qkv_w, out_w=out_w, norm2_w=norm2_w,
+             s_w1=s_w1, s_w2=s_w2, ns_w1=ns_w1, ns_w2=ns_w2)
+    return onetrans_block_raw(x, w, n_heads, q_len)
+
+
+@onetrans_block_fwd.register_fake
+def _(x, norm1_w, s_qkv_w, ns_qkv_w, out_w, norm2_w, s_w1, s_w2, ns_w1, ns_w2, n_heads, q_len):
+    return x.new_empty((x.shape[0], q_len, x.shape[2]))

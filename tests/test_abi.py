@@ -1,0 +1,70 @@
+"""The C ABI library loads, exports every symbol include/pdm.h declares, and
+rejects bad arguments with a status code and message before touching a GPU."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _header_functions():
+    text = open(os.path.join(ROOT, "include", "pdm.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(pdm_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_functions_match_binding_list(pdm):
+    assert _header_functions() == sorted(pdm._lib.EXPORTED_SYMBOLS)
+
+
+def test_library_exports_every_declared_symbol(pdm):
+    lib = pdm._lib.lib()
+    for name in _header_functions():
+        assert hasattr(lib, name), name
+    assert lib.pdm_abi_version() == 10000
+
+
+def test_struct_layouts_match_header(pdm):
+    L = pdm._lib
+    assert ctypes.sizeof(L.TableDesc) == 40
+    assert ctypes.sizeof(L.BlockDesc) == 32
+    assert ctypes.sizeof(L.BlockWeights) == 72
+    assert L.SeqDesc.max_len.offset == 32
+    assert ctypes.sizeof(L.SeqDesc) == 32 + 4 * 8 + 4 * 8 + 8 * 8 + 8 * 8
+
+
+def test_argument_errors_are_reported_not_raised(pdm):
+    L = pdm._lib
+    lib = L.lib()
+    h = ctypes.c_void_p()
+    assert lib.pdm_tbe_plan_create(None, 1, ctypes.byref(h)) == L.PDM_ERR_INVALID
+    assert "null" in L.last_error()
+    bad = (L.TableDesc * 1)(L.TableDesc(10, 0, 6, L.PDM_F32, L.PDM_POOL_SUM, 0, 0, 0))
+    assert lib.pdm_tbe_plan_create(bad, 1, ctypes.byref(h)) == L.PDM_ERR_INVALID
+    assert "multiple of 4" in L.last_error()
+    bad = (L.TableDesc * 1)(L.TableDesc(10, 0, 8, 9, L.PDM_POOL_SUM, 0, 0, 0))
+    assert lib.pdm_tbe_plan_create(bad, 1, ctypes.byref(h)) == L.PDM_ERR_INVALID
+    assert lib.pdm_tbe_pooled_fwd(None, None, None, 64, 0, None, 1, -1, None, 0, 8, None, None) == L.PDM_ERR_INVALID
+    d = L.SeqDesc()
+    d.num_pools = 0
+    assert lib.pdm_seq_gather_fwd(ctypes.byref(d), None, None, None, None, None, None, None) == L.PDM_ERR_INVALID
+    assert lib.pdm_int8_rowwise_quantize(None, 10, 0, None, 8, None) == L.PDM_ERR_INVALID
+
+
+def test_ops_refuse_cpu_tensors(pdm):
+    import torch
+
+    with pytest.raises(RuntimeError, match="GPU only"):
+        pdm.ops.int8_rowwise_quantize(torch.zeros(4, 8))
+    with pytest.raises(RuntimeError, match="GPU only"):
+        pdm.ops.seq_gather_raw([torch.zeros(4, 8, dtype=torch.bfloat16)], [[torch.zeros(1, dtype=torch.long)]],
+                               [torch.zeros(2, dtype=torch.long)], [1])
+
+
+def test_custom_ops_registered(pdm):
+    import torch
+
+    for name in ("tbe_pooled_fwd", "seq_gather_fwd", "onetrans_block_fwd"):
+        assert hasattr(torch.ops.pdm, name)
