@@ -87,7 +87,8 @@ int64_t pdm_tbe_plan_total_dim(pdm_tbe_plan plan);
  * indices:     device, int32 or int64 (index_bits = 32 | 64), num_indices long
  * offsets:     device, int64 [T * B + 1], table-major: bag (t, b) is
  *              indices[offsets[t*B+b] : offsets[t*B+b+1]]
- * padding_idx: an index equal to it is skipped and not counted (-1 = none)
+ * padding_idx: an index equal to it is skipped and not counted (negative =
+ *              no padding id: every index is pooled or flagged)
  * out:         device, [B, out_row_stride] of out_dtype (F32 | F16 | BF16)
  * err_flag:    optional device int32; set to 1 when an index is outside
  *              [0, rows) (such indices are skipped, never read) or a bag's

@@ -152,7 +152,7 @@ int64_t oracle_tbe_pooled(const oracle_table* tables, int32_t T, int64_t B,
     for (int64_t i = start; i < end; ++i) {
       const int64_t idx = index_bits == 32 ? (int64_t)((const int32_t*)indices)[i]
                                            : ((const int64_t*)indices)[i];
-      if (idx == padding_idx) continue;
+      if (padding_idx >= 0 && idx == padding_idx) continue;
       if (idx < 0 || idx >= tb->rows) { ++bad; continue; }
       const uint8_t* row = weights + tb->weights_offset + (size_t)idx * (size_t)rb;
       for (int32_t d = 0; d < D; ++d) acc[d] += decode(row, tb->dtype, d);

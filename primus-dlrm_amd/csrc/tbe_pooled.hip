@@ -194,7 +194,7 @@ __global__ __launch_bounds__(256) void tbe_pooled_kernel(TbeArgs a) {
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         idx[u] = shfl64(my, gbase + ((k + u) & (lpb - 1)));
-        const bool live = (k + u) < n && idx[u] != a.padding_idx;
+        const bool live = (k + u) < n && !(a.padding_idx >= 0 && idx[u] == a.padding_idx);
         ok[u] = live && idx[u] >= 0 && idx[u] < m.rows;
         bad |= live && !ok[u];
       }
