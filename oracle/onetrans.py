@@ -1,0 +1,166 @@
+"""CPU oracle of the OneTrans interaction block.  TEST INFRASTRUCTURE ONLY:
+used by tests/, ``__graft_entry__.smoke()`` and bench.py's CPU-baseline leg
+as the checker, never by the product package.
+
+Restates primus_dlrm/models/onetrans.py in PyTorch on the CPU:
+
+* ``pyramid_schedule``   onetrans.py:50-59
+* ``pyramid_mask``       onetrans.py:62-67  (bottom-right causal: key j <= i + kv - q)
+* ``rmsnorm``            onetrans.py:74-82  (fp32, eps 1e-6, ``(x * rms) * w``)
+* ``block_forward``      OneTransBlock.forward onetrans.py:220-231 with
+                         MixedAttention.forward :124-169 and MixedFFN.forward :195-204
+
+``mode="autocast"`` reproduces the rounding points the reference has under
+``torch.autocast(bf16)`` (primus_dlrm/training/dist_trainer.py:471) with an
+fp32 residual stream: every Linear / einsum takes bf16-rounded operands,
+accumulates in fp32 and rounds its output to bf16; attention takes bf16
+q/k/v, runs the softmax in fp32 and rounds its output to bf16; GELU (exact
+erf) runs in fp32 on the bf16 GEMM output and rounds to bf16; RMSNorm and the
+residual additions stay fp32.  ``mode="fp64"`` runs the same graph in float64
+without any rounding (ground truth).
+
+Weights use the reference's parameter names (onetrans.py:111-113,180-184,214-218):
+norm1, s_qkv [3D, D], ns_qkv [NS, 3D, D], out [D, D], norm2, s_w1 [F, D],
+s_w2 [D, F], ns_w1 [NS, F, D], ns_w2 [NS, D, F].
+"""
+from __future__ import annotations
+
+import math
+from typing import Dict, List
+
+import torch
+
+WEIGHT_NAMES = ("norm1", "s_qkv", "ns_qkv", "out", "norm2", "s_w1", "s_w2", "ns_w1", "ns_w2")
+
+
+def pyramid_schedule(l_s: int, l_ns: int, n_layers: int) -> List[int]:
+    """onetrans.py:50-59."""
+    if n_layers == 1:
+        return [l_ns]
+    out = []
+    for layer in range(n_layers):
+        q = l_s - layer * (l_s - l_ns) / (n_layers - 1)
+        out.append(max(int(round(q)), l_ns))
+    return out
+
+
+def pyramid_mask(q_len: int, kv_len: int) -> torch.Tensor:
+    """onetrans.py:62-67: mask[i, j] = j <= i + (kv_len - q_len)."""
+    i = torch.arange(q_len).unsqueeze(1) + (kv_len - q_len)
+    j = torch.arange(kv_len).unsqueeze(0)
+    return j <= i
+
+
+def _bf16(t: torch.Tensor) -> torch.Tensor:
+    return t.to(torch.bfloat16).to(torch.float32)
+
+
+class _Num:
+    """Arithmetic of one mode: ``lin`` is an autocast Linear / einsum."""
+
+    def __init__(self, mode: str):
+        if mode not in ("autocast", "fp64"):
+            raise ValueError(mode)
+        self.mode = mode
+        self.dt = torch.float64 if mode == "fp64" else torch.float32
+
+    def round(self, t: torch.Tensor) -> torch.Tensor:
+        return _bf16(t) if self.mode == "autocast" else t
+
+    def lin(self, x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+        """x [..., K] . w[N, K]^T"""
+        return self.round(torch.matmul(self.round(x), self.round(w.to(self.dt)).transpose(-1, -2)))
+
+
+def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """onetrans.py:80-82 (x is the fp32 or fp64 residual stream, so ``.to(x.dtype)`` keeps it)."""
+    rms = x.pow(2).mean(-1, keepdim=True).add(eps).rsqrt()
+    return (x * rms) * w.to(x.dtype)
+
+
+def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, num: _Num) -> torch.Tensor:
+    """Causal bottom-right softmax attention on BSHD tensors, scale 1/sqrt(dh)
+    (onetrans.py:148-161; the flash/SDPA default scale)."""
+    B, Lq, H, dh = q.shape
+    Lk = k.shape[1]
+    qt, kt, vt = (num.round(t).transpose(1, 2) for t in (q, k, v))  # [B, H, L, dh]
+    s = torch.matmul(qt, kt.transpose(-1, -2)) / math.sqrt(dh)
+    s = s.masked_fill(~pyramid_mask(Lq, Lk), float("-inf"))
+    p = torch.softmax(s, dim=-1)
+    o = torch.matmul(p, vt)
+    return num.round(o.transpose(1, 2))  # [B, Lq, H, dh]
+
+
+def block_forward(x: torch.Tensor, w: Dict[str, torch.Tensor], q_len: int, n_heads: int,
+                  mode: str = "autocast", return_parts: bool = False):
+    """OneTransBlock.forward (onetrans.py:220-231) for x [B, kv, D]; the last
+    ``w['ns_qkv'].shape[0]`` tokens of x are the NS-tokens.  With
+    ``return_parts`` also returns the intermediates (h1, q, k, v, o, z, h2, g)."""
+    num = _Num(mode)
+    x = x.to(num.dt)
+    B, kv, D = x.shape
+    n_ns = w["ns_qkv"].shape[0]
+    n_s = kv - n_ns
+    dh = D // n_heads
+    # MixedAttention (:124-169)
+    h = rmsnorm(x, w["norm1"])
+    s_qkv = num.lin(h[:, :n_s], w["s_qkv"]).reshape(B, n_s, 3, n_heads, dh)
+    ns_qkv = torch.stack([num.lin(h[:, n_s + t], w["ns_qkv"][t]) for t in range(n_ns)], dim=1) if n_ns else \
+        h.new_zeros(B, 0, 3 * D)
+    ns_qkv = ns_qkv.reshape(B, n_ns, 3, n_heads, dh)
+    q = torch.cat([s_qkv[:, :, 0], ns_qkv[:, :, 0]], dim=1)
+    k = torch.cat([s_qkv[:, :, 1], ns_qkv[:, :, 1]], dim=1)
+    v = torch.cat([s_qkv[:, :, 2], ns_qkv[:, :, 2]], dim=1)
+    q = q[:, kv - q_len:]
+    o = attention(q, k, v, num).reshape(B, q_len, D)
+    z = num.lin(o, w["out"]) + x[:, kv - q_len:]
+    # MixedFFN (:195-204) on the pre-normed stream, n_s = q_len - n_ns
+    h2 = rmsnorm(z, w["norm2"])
+    n_s_out = q_len - n_ns
+    gelu = lambda t: num.round(torch.nn.functional.gelu(t))  # noqa: E731  exact erf
+    g_s = gelu(num.lin(h2[:, :n_s_out], w["s_w1"]))
+    g_ns = [gelu(num.lin(h2[:, n_s_out + t], w["ns_w1"][t])) for t in range(n_ns)]
+    s_out = num.lin(g_s, w["s_w2"])
+    ns_out = [num.lin(g_ns[t], w["ns_w2"][t]) for t in range(n_ns)]
+    ffn = torch.cat([s_out] + [t.unsqueeze(1) for t in ns_out], dim=1)
+    y = z + ffn
+    if return_parts:
+        g = torch.cat([g_s] + [t.unsqueeze(1) for t in g_ns], dim=1)
+        return y, dict(h1=h, q=q.reshape(B, q_len, D), k=k.reshape(B, kv, D), v=v.reshape(B, kv, D), o=o, z=z,
+                       h2=h2, g=g)
+    return y
+
+
+def stack_forward(x: torch.Tensor, layers: List[Dict[str, torch.Tensor]], schedule: List[int], n_heads: int,
+                  mode: str = "autocast") -> torch.Tensor:
+    """The block loop of OneTransModel._backbone (onetrans.py:568-582)."""
+    n_ns = layers[0]["ns_qkv"].shape[0]
+    for w, q_s in zip(layers, schedule):
+        x = block_forward(x, w, q_s + n_ns, n_heads, mode)
+    return x
+
+
+def random_weights(D: int, F: int, n_ns: int, std: float = 0.02, seed: int = 0,
+                   norm_std: float = 0.0) -> Dict[str, torch.Tensor]:
+    """N(0, std) weights (bf16-representable, fp32 storage); RMSNorm weights
+    1 + N(0, norm_std) (the reference initialises them to ones, onetrans.py:77)."""
+    g = torch.Generator().manual_seed(seed)
+    r = lambda *shape: _bf16(torch.randn(*shape, generator=g) * std)  # noqa: E731
+    return {
+        "norm1": 1.0 + torch.randn(D, generator=g) * norm_std,
+        "s_qkv": r(3 * D, D), "ns_qkv": r(n_ns, 3 * D, D), "out": r(D, D),
+        "norm2": 1.0 + torch.randn(D, generator=g) * norm_std,
+        "s_w1": r(F, D), "s_w2": r(D, F), "ns_w1": r(n_ns, F, D), "ns_w2": r(n_ns, D, F),
+    }
+
+
+def block_flops(B: int, kv: int, q_len: int, D: int, F: int, n_ns: int) -> float:
+    """Forward FLOPs of one block by the reference's convention
+    (onetrans.py:392-474 without the backward factor): S-token QKV on every kv
+    S-token, attention counted full (no causal discount)."""
+    n_s = kv - n_ns
+    f = 2 * n_s * D * 3 * D + 2 * n_ns * 3 * D * D
+    f += 4 * q_len * kv * D
+    f += 2 * q_len * D * D
+    f += 4 * q_len * D * F
+    return float(f) * B

@@ -1,16 +1,598 @@
-// OneTrans block forward (placeholder until the MFMA kernels land).
+// OneTrans mixed-parameter block forward for gfx950 (bf16 MFMA).
+//
+// Semantics: OneTransBlock.forward(x, mask, q_len, n_s_tokens)
+// (primus_dlrm/models/onetrans.py:207-231) under autocast(bf16)
+// (primus_dlrm/training/dist_trainer.py:471) with an fp32 residual stream:
+//   h1 = RMSNorm1(x)                         fp32 math, eps 1e-6     (:74-82)
+//   qkv = h1 @ Wqkv^T  (shared for S-tokens, per-token for NS-tokens) (:124-139)
+//   q  = q[:, kv - q_len:]                  pyramid tail              (:141-144)
+//   o  = causal bottom-right softmax(q k^T / sqrt(dh)) v              (:62-67,148-161)
+//   z  = o @ Wout^T + x[:, kv - q_len:]                               (:168-169,226-227)
+//   y  = z + FFN(RMSNorm2(z)), FFN = W2 gelu_erf(W1 .), S shared / NS per token (:172-204)
+// Every GEMM takes bf16 operands, accumulates in fp32 and rounds its output
+// to bf16 (autocast), GELU runs in fp32 on the bf16 GEMM output and rounds
+// to bf16, the residual additions run in fp32.
+//
+// Launches per block: rmsnorm, QKV GEMM (writes Q tail rows, K, and V
+// transposed per head), attention, out-proj GEMM (+x tail -> z in y),
+// rmsnorm, FFN-up GEMM (+GELU), FFN-down GEMM (+z -> y).
+//
+// GEMM design: C[128x128] tiles of A[M,K] . W[N,K]^T (both K-contiguous, the
+// nn.Linear layout), 4 waves in a 2x2 arrangement, each wave 2x2
+// v_mfma_f32_32x32x16_bf16 tiles, K streamed in 64-wide slices through a
+// double-buffered LDS ring.  Rows are (sample, token) pairs; S-token rows use
+// the shared weight and NS-token rows the weight of their token, so one
+// launch covers the shared GEMM and the 16 per-token GEMMs.
+//
+// Attention design: one wave owns 32 queries of one (sample, head).  It
+// computes S^T = K Q^T so that each lane holds one query's scores; the
+// online softmax then needs a single cross-half exchange, and the fp32
+// accumulator layout of S^T is already the B-operand layout of
+// O^T = V^T P^T, so P never leaves registers.
+#include <algorithm>
+#include <cmath>
+
 #include "pdm_common.h"
+
+namespace pdm {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ f32x16_t mfma32x32x16(u32x4_t a, u32x4_t b, f32x16_t c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
+                                                 c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float bf16_round(float v) { return bf16_bits_to_f32(f32_to_bf16_bits(v)); }
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+}
+
+// ---------------------------------------------------------------------------
+// RMSNorm -> bf16 rows.  One wave per row, D = 64 * VPL.
+// out row r = bf16((x * rsqrt(mean(x^2) + eps)) * w), fp32 arithmetic in the
+// reference's order (onetrans.py:80-82).
+// ---------------------------------------------------------------------------
+template <int VPL>
+__global__ __launch_bounds__(256) void rmsnorm_bf16_kernel(const float* __restrict__ x, int64_t x_bstride,
+                                                           int T, int64_t rows, const float* __restrict__ w,
+                                                           uint16_t* __restrict__ out, float eps) {
+  constexpr int D = 64 * VPL;
+  const int lane = threadIdx.x & 63;
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= rows) return;
+  const int64_t b = r / T;
+  const int t = (int)(r - b * T);
+  const float* xr = x + b * x_bstride + (int64_t)t * D + lane * VPL;
+  float v[VPL];
+  if constexpr (VPL % 4 == 0) {
+#pragma unroll
+    for (int i = 0; i < VPL / 4; ++i) {
+      const float4 f = reinterpret_cast<const float4*>(xr)[i];
+      v[4 * i] = f.x; v[4 * i + 1] = f.y; v[4 * i + 2] = f.z; v[4 * i + 3] = f.w;
+    }
+  } else if constexpr (VPL % 2 == 0) {
+#pragma unroll
+    for (int i = 0; i < VPL / 2; ++i) {
+      const float2 f = reinterpret_cast<const float2*>(xr)[i];
+      v[2 * i] = f.x; v[2 * i + 1] = f.y;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) v[i] = xr[i];
+  }
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) ss += v[i] * v[i];
+#pragma unroll
+  for (int s = 32; s >= 1; s >>= 1) ss += __shfl_xor(ss, s, 64);
+  const float rms = 1.0f / sqrtf(ss / (float)D + eps);
+  uint16_t* o = out + r * D + lane * VPL;
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const float wv = w[lane * VPL + i];
+    const float n = v[i] * rms;
+    o[i] = (uint16_t)f32_to_bf16_bits(n * wv);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Grouped GEMM  C = A . W^T  over (sample, token) rows.
+// ---------------------------------------------------------------------------
+enum { EPI_BF16 = 0, EPI_QKV = 1, EPI_RESID = 2, EPI_GELU = 3 };
+
+constexpr int GBM = 128, GBN = 128, GBK = 64, GPAD = 8;
+
+struct GemmArgs {
+  const uint16_t* A;  // bf16 rows: row (b, t) at A + b * a_bstride + t * K
+  int64_t a_bstride;  // elements between samples
+  const uint16_t* W;     // [N, K] shared (S-token) weight
+  const uint16_t* W_ns;  // [n_ns, N, K] per-token weights, or null when shared by all rows
+  int B;
+  int n_s;    // tokens of the shared group per sample (tokens 0 .. n_s-1)
+  int n_ns;   // per-token groups (tokens n_s .. n_s+n_ns-1); 0 when W_ns is null
+  int N, K;
+  int tiles_s;  // ceil(B * n_s / GBM)
+  int tiles_b;  // ceil(B / GBM)
+  int n_tiles;  // ceil(N / GBN)
+  int64_t total_blocks;
+  // epilogue
+  void* out;            // EPI_BF16 / EPI_GELU: bf16 [B, T, N]; EPI_RESID: fp32 [B, T, N]
+  int64_t out_bstride;  // elements between samples of out
+  const float* res;     // EPI_RESID: residual fp32, row (b, t) at res + b * res_bstride + (t + res_toff) * N
+  int64_t res_bstride;
+  int res_toff;
+  // EPI_QKV: N = 3D.  Q [B, q_len, D] (tokens t >= kv - q_len), K [B, kv, D], VT [B, H, 64, kv_pad]
+  uint16_t* q;
+  uint16_t* k;
+  uint16_t* vt;
+  int kv, q_len, kv_pad, D;
+};
+
+__device__ __forceinline__ float gelu_erf(float v) { return 0.5f * v * (1.0f + erff(v * 0.70710678118654752f)); }
+
+template <int EPI>
+__global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
+  __shared__ __attribute__((aligned(16))) uint16_t sA[2][GBM][GBK + GPAD];
+  __shared__ __attribute__((aligned(16))) uint16_t sB[2][GBN][GBK + GPAD];
+  __shared__ int s_rb[GBM];  // sample of tile row i, -1 = no row
+  __shared__ int s_rt[GBM];  // token of tile row i
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+
+  // blocks sharing an M tile run on one XCD (block ids are dealt to the 8 XCDs round robin)
+  int64_t bid = blockIdx.x;
+  const int64_t full = a.total_blocks & ~int64_t(7);
+  if (bid < full) bid = (bid & 7) * (full >> 3) + (bid >> 3);
+  const int mt = (int)(bid / a.n_tiles);
+  const int n0 = (int)(bid - (int64_t)mt * a.n_tiles) * GBN;
+
+  const uint16_t* W = a.W;
+  if (tid < GBM) {
+    int b = -1, t = 0;
+    if (mt < a.tiles_s) {
+      const int64_t r = (int64_t)mt * GBM + tid;
+      if (r < (int64_t)a.B * a.n_s) {
+        b = (int)(r / a.n_s);
+        t = (int)(r - (int64_t)b * a.n_s);
+      }
+    } else {
+      const int g = (mt - a.tiles_s) / a.tiles_b;
+      const int bb = (mt - a.tiles_s) - g * a.tiles_b;
+      const int r = bb * GBM + tid;
+      if (r < a.B) {
+        b = r;
+        t = a.n_s + g;
+      }
+    }
+    s_rb[tid] = b;
+    s_rt[tid] = t;
+  }
+  if (mt >= a.tiles_s) W = a.W_ns + (int64_t)((mt - a.tiles_s) / a.tiles_b) * a.N * a.K;
+  __syncthreads();
+
+  if constexpr (EPI == EPI_QKV) {
+    // Q columns of S-token rows outside the kept tail are never read: skip the tile
+    if (n0 < a.D) {
+      const int thr = a.kv - a.q_len;
+      const int need = (tid < GBM && s_rb[tid] >= 0 && s_rt[tid] >= thr) ? 1 : 0;
+      if (!__syncthreads_or(need)) return;
+    }
+  }
+
+  // global -> LDS assignment: 8 threads x 16 B per 64-element row slice, 32 rows per pass
+  const int lr = tid >> 3, lc = (tid & 7) * 8;
+  const uint16_t* arow[4];
+  const uint16_t* wrow[4];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const int i = p * 32 + lr;
+    const int b = s_rb[i];
+    arow[p] = b >= 0 ? a.A + (int64_t)b * a.a_bstride + (int64_t)s_rt[i] * a.K + lc : nullptr;
+    const int n = n0 + i;
+    wrow[p] = n < a.N ? W + (int64_t)n * a.K + lc : nullptr;
+  }
+
+  u32x4_t ra[4], rb[4];
+  auto gload = [&](int k0) {
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      ra[p] = arow[p] ? *reinterpret_cast<const u32x4_t*>(arow[p] + k0) : u32x4_t{0, 0, 0, 0};
+      rb[p] = wrow[p] ? *reinterpret_cast<const u32x4_t*>(wrow[p] + k0) : u32x4_t{0, 0, 0, 0};
+    }
+  };
+  auto sstore = [&](int buf) {
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      *reinterpret_cast<u32x4_t*>(&sA[buf][p * 32 + lr][lc]) = ra[p];
+      *reinterpret_cast<u32x4_t*>(&sB[buf][p * 32 + lr][lc]) = rb[p];
+    }
+  };
+
+  f32x16_t acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+  const int nk = a.K / GBK;
+  gload(0);
+  sstore(0);
+  __syncthreads();
+  const int fr = lane & 31, fk = (lane >> 5) * 8;
+  for (int kt = 0; kt < nk; ++kt) {
+    const int buf = kt & 1;
+    if (kt + 1 < nk) gload((kt + 1) * GBK);
+#pragma unroll
+    for (int ks = 0; ks < GBK / 16; ++ks) {
+      u32x4_t af[2], bf[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) af[i] = *reinterpret_cast<const u32x4_t*>(&sA[buf][wm * 64 + i * 32 + fr][ks * 16 + fk]);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) bf[j] = *reinterpret_cast<const u32x4_t*>(&sB[buf][wn * 64 + j * 32 + fr][ks * 16 + fk]);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = mfma32x32x16(af[i], bf[j], acc[i][j]);
+    }
+    if (kt + 1 < nk) sstore(buf ^ 1);
+    __syncthreads();
+  }
+
+  // epilogue: acc[i][j][e] is row wm*64 + i*32 + (e/4)*8 + (lane/32)*4 + e%4, column n0 + wn*64 + j*32 + lane%32
+  const int hf = lane >> 5;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int row = wm * 64 + i * 32 + (e >> 2) * 8 + hf * 4 + (e & 3);
+      const int b = s_rb[row];
+      if (b < 0) continue;
+      const int t = s_rt[row];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int n = n0 + wn * 64 + j * 32 + fr;
+        if (n >= a.N) continue;
+        const float v = acc[i][j][e];
+        if constexpr (EPI == EPI_BF16) {
+          reinterpret_cast<uint16_t*>(a.out)[(int64_t)b * a.out_bstride + (int64_t)t * a.N + n] =
+              (uint16_t)f32_to_bf16_bits(v);
+        } else if constexpr (EPI == EPI_GELU) {
+          reinterpret_cast<uint16_t*>(a.out)[(int64_t)b * a.out_bstride + (int64_t)t * a.N + n] =
+              (uint16_t)f32_to_bf16_bits(gelu_erf(bf16_round(v)));
+        } else if constexpr (EPI == EPI_RESID) {
+          const float r = a.res[(int64_t)b * a.res_bstride + (int64_t)(t + a.res_toff) * a.N + n];
+          reinterpret_cast<float*>(a.out)[(int64_t)b * a.out_bstride + (int64_t)t * a.N + n] = bf16_round(v) + r;
+        } else {  // EPI_QKV
+          const uint16_t bits = (uint16_t)f32_to_bf16_bits(v);
+          const int D = a.D;
+          if (n < D) {
+            const int tq = t - (a.kv - a.q_len);
+            if (tq >= 0) a.q[((int64_t)b * a.q_len + tq) * D + n] = bits;
+          } else if (n < 2 * D) {
+            a.k[((int64_t)b * a.kv + t) * D + (n - D)] = bits;
+          } else {
+            const int c = n - 2 * D;
+            const int h = c >> 6, d = c & 63;
+            const int H = D >> 6;
+            a.vt[(((int64_t)b * H + h) * 64 + d) * a.kv_pad + t] = bits;
+          }
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Causal bottom-right attention, head dim 64.
+// Q [B, q_len, H*64], K [B, kv, H*64], VT [B, H, 64, kv_pad] (bf16) -> O [B, q_len, H*64] bf16.
+// Query i (0-based in the kept tail) sees keys j <= i + (kv - q_len).
+// ---------------------------------------------------------------------------
+struct AttnArgs {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* vt;
+  uint16_t* o;
+  int B, H, q_len, kv, kv_pad;
+  float scale_log2;  // log2(e) / sqrt(64)
+};
+
+__global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int bh = blockIdx.y;
+  const int b = bh / a.H, h = bh - (bh / a.H) * a.H;
+  const int D = a.H * 64;
+  const int qi0 = blockIdx.x * 128 + wave * 32;
+  if (qi0 >= a.q_len) return;
+  const int fr = lane & 31, hf = lane >> 5;
+  const int off = a.kv - a.q_len;
+  const int qi = qi0 + fr;
+  const bool qvalid = qi < a.q_len;
+  const int p = qi + off;  // last key this query sees
+
+  u32x4_t qf[4];
+  const uint16_t* qrow = a.q + ((int64_t)b * a.q_len + qi) * D + h * 64 + hf * 8;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) qf[c] = qvalid ? *reinterpret_cast<const u32x4_t*>(qrow + c * 16) : u32x4_t{0, 0, 0, 0};
+
+  const int q_last = min(qi0 + 31, a.q_len - 1);
+  const int kv_end = min(a.kv, q_last + off + 1);
+
+  f32x16_t o[2];
+#pragma unroll
+  for (int e = 0; e < 16; ++e) { o[0][e] = 0.0f; o[1][e] = 0.0f; }
+  float m = -INFINITY, l = 0.0f;
+
+  const uint16_t* kbase = a.k + (int64_t)b * a.kv * D + h * 64 + hf * 8;
+  const uint16_t* vbase = a.vt + ((int64_t)b * a.H + h) * 64 * a.kv_pad;
+
+  for (int j0 = 0; j0 < kv_end; j0 += 32) {
+    // S^T[kv][q] = K . Q^T
+    f32x16_t s;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) s[e] = 0.0f;
+    const int jr = j0 + fr;
+    const uint16_t* krow = kbase + (int64_t)jr * D;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const u32x4_t kf = jr < a.kv ? *reinterpret_cast<const u32x4_t*>(krow + c * 16) : u32x4_t{0, 0, 0, 0};
+      s = mfma32x32x16(kf, qf[c], s);
+    }
+    // s[e] is key j0 + (e/4)*8 + hf*4 + e%4 of query qi
+    float mx = -INFINITY;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int j = j0 + (e >> 2) * 8 + hf * 4 + (e & 3);
+      const float t = (j <= p && j < a.kv) ? s[e] * a.scale_log2 : -INFINITY;
+      s[e] = t;
+      mx = fmaxf(mx, t);
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m, mx);
+    const float alpha = exp2f(m - m_new);
+    m = m_new;
+    float ps = 0.0f;
+    uint32_t pk[8];
+#pragma unroll
+    for (int e = 0; e < 16; e += 2) {
+      const float p0 = exp2f(s[e] - m_new);
+      const float p1 = exp2f(s[e + 1] - m_new);
+      ps += p0 + p1;
+      pk[e >> 1] = pack_bf16x2(p0, p1);
+    }
+    l = l * alpha + ps;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) { o[0][e] *= alpha; o[1][e] *= alpha; }
+    // O^T[d][q] += V^T . P^T; P^T chunk c2 holds keys j0 + 16*c2 + (e/4)*8 + hf*4 + e%4, e = 0..7
+    const bool tail = j0 + 32 > a.kv;
+#pragma unroll
+    for (int c2 = 0; c2 < 2; ++c2) {
+      const u32x4_t pb = {pk[4 * c2], pk[4 * c2 + 1], pk[4 * c2 + 2], pk[4 * c2 + 3]};
+      const int jb = j0 + 16 * c2 + hf * 4;
+#pragma unroll
+      for (int db = 0; db < 2; ++db) {
+        const uint16_t* vrow = vbase + (int64_t)(db * 32 + fr) * a.kv_pad + jb;
+        u32x2_t lo = *reinterpret_cast<const u32x2_t*>(vrow);
+        u32x2_t hi = *reinterpret_cast<const u32x2_t*>(vrow + 8);
+        if (tail) {
+          // keys at or past kv hold no value: zero them so 0 * garbage cannot appear
+#pragma unroll
+          for (int w = 0; w < 2; ++w) {
+            const int j = jb + 2 * w;
+            if (j >= a.kv) lo[w] = 0u;
+            else if (j + 1 >= a.kv) lo[w] &= 0xffffu;
+            const int j2 = jb + 8 + 2 * w;
+            if (j2 >= a.kv) hi[w] = 0u;
+            else if (j2 + 1 >= a.kv) hi[w] &= 0xffffu;
+          }
+        }
+        const u32x4_t vf = {lo[0], lo[1], hi[0], hi[1]};
+        o[db] = mfma32x32x16(vf, pb, o[db]);
+      }
+    }
+  }
+  l += __shfl_xor(l, 32, 64);
+  if (!qvalid) return;
+  const float inv = 1.0f / l;
+  uint16_t* orow = a.o + ((int64_t)b * a.q_len + qi) * D + h * 64;
+  // o[db][e] is d = db*32 + (e/4)*8 + hf*4 + e%4
+#pragma unroll
+  for (int db = 0; db < 2; ++db)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int d = db * 32 + g * 8 + hf * 4;
+      u32x2_t w;
+      w[0] = pack_bf16x2(o[db][4 * g] * inv, o[db][4 * g + 1] * inv);
+      w[1] = pack_bf16x2(o[db][4 * g + 2] * inv, o[db][4 * g + 3] * inv);
+      *reinterpret_cast<u32x2_t*>(orow + d) = w;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+
+struct BlockLayout {
+  int64_t h = 0, q = 0, k = 0, vt = 0, g = 0, total = 0;
+  int kv_pad = 0;
+};
+
+static int64_t align256(int64_t v) { return (v + 255) & ~int64_t(255); }
+
+static BlockLayout block_layout(const pdm_block_desc& d) {
+  BlockLayout L;
+  const int64_t B = d.batch, D = d.d_model;
+  L.kv_pad = (d.kv_len + 31) & ~31;
+  int64_t off = 0;
+  L.h = off; off = align256(off + B * d.kv_len * D * 2);                // h1, later h2
+  L.q = off; off = align256(off + B * d.q_len * D * 2);                 // Q, later attention output
+  L.k = off; off = align256(off + B * d.kv_len * D * 2);                // K
+  L.vt = off; off = align256(off + B * (D / 64) * 64 * (int64_t)L.kv_pad * 2);  // V^T per head
+  L.g = off; off = align256(off + B * d.q_len * (int64_t)d.ffn_dim * 2);  // GELU(FFN-up)
+  L.total = off;
+  return L;
+}
+
+static const char* check_desc(const pdm_block_desc* d) {
+  if (!d) return "null desc";
+  if (d->batch < 1) return "batch must be >= 1";
+  if (d->d_model < 128 || d->d_model > 512 || d->d_model % 128) return "d_model must be 128, 256, 384 or 512";
+  if (d->n_heads * 64 != d->d_model) return "head dim must be 64 (n_heads = d_model / 64)";
+  if (d->ffn_dim < 128 || d->ffn_dim % 128) return "ffn_dim must be a positive multiple of 128";
+  if (d->n_ns < 0) return "n_ns must be >= 0";
+  if (!(d->n_ns <= d->q_len && d->q_len <= d->kv_len)) return "need n_ns <= q_len <= kv_len";
+  if (d->q_len < 1) return "q_len must be >= 1";
+  return nullptr;
+}
+
+static void gemm_tiles(GemmArgs& g) {
+  g.tiles_s = (int)(((int64_t)g.B * g.n_s + GBM - 1) / GBM);
+  g.tiles_b = (g.B + GBM - 1) / GBM;
+  g.n_tiles = (g.N + GBN - 1) / GBN;
+  g.total_blocks = ((int64_t)g.tiles_s + (int64_t)g.n_ns * g.tiles_b) * g.n_tiles;
+}
+
+template <int EPI>
+static int launch_gemm(GemmArgs& g, hipStream_t s) {
+  gemm_tiles(g);
+  if (g.total_blocks == 0) return PDM_OK;
+  PDM_CHECK_ARG(g.total_blocks < (int64_t(1) << 31), "GEMM grid too large");
+  hipLaunchKernelGGL(gemm_kernel<EPI>, dim3((unsigned)g.total_blocks), dim3(256), 0, s, g);
+  PDM_CHECK_LAUNCH();
+  return PDM_OK;
+}
+
+static int launch_rmsnorm(const float* x, int64_t x_bstride, int T, int64_t B, int D, const float* w, uint16_t* out,
+                          hipStream_t s) {
+  const int64_t rows = B * T;
+  if (rows == 0) return PDM_OK;
+  const int64_t blocks = (rows + 3) / 4;
+  switch (D / 64) {
+    case 2: hipLaunchKernelGGL(rmsnorm_bf16_kernel<2>, dim3((unsigned)blocks), dim3(256), 0, s, x, x_bstride, T, rows, w, out, 1e-6f); break;
+    case 4: hipLaunchKernelGGL(rmsnorm_bf16_kernel<4>, dim3((unsigned)blocks), dim3(256), 0, s, x, x_bstride, T, rows, w, out, 1e-6f); break;
+    case 6: hipLaunchKernelGGL(rmsnorm_bf16_kernel<6>, dim3((unsigned)blocks), dim3(256), 0, s, x, x_bstride, T, rows, w, out, 1e-6f); break;
+    case 8: hipLaunchKernelGGL(rmsnorm_bf16_kernel<8>, dim3((unsigned)blocks), dim3(256), 0, s, x, x_bstride, T, rows, w, out, 1e-6f); break;
+    default: set_error("rmsnorm: unsupported d_model"); return PDM_ERR_UNSUPPORTED;
+  }
+  PDM_CHECK_LAUNCH();
+  return PDM_OK;
+}
+
+static bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+}  // namespace pdm
 
 using namespace pdm;
 
 extern "C" int64_t pdm_onetrans_block_workspace_size(const pdm_block_desc* desc) {
-  (void)desc;
-  return 0;
+  clear_error();
+  if (const char* e = check_desc(desc)) {
+    set_error(std::string("pdm_onetrans_block_workspace_size: ") + e);
+    return PDM_ERR_INVALID;
+  }
+  return block_layout(*desc).total;
 }
 
 extern "C" int pdm_onetrans_block_fwd(const pdm_block_desc* desc, const float* x, const pdm_block_weights* w,
                                       float* y, void* workspace, int64_t workspace_bytes, pdm_stream_t stream) {
-  (void)desc; (void)x; (void)w; (void)y; (void)workspace; (void)workspace_bytes; (void)stream;
-  set_error("pdm_onetrans_block_fwd: not built yet");
-  return PDM_ERR_UNSUPPORTED;
+  clear_error();
+  if (const char* e = check_desc(desc)) {
+    set_error(std::string("pdm_onetrans_block_fwd: ") + e);
+    return PDM_ERR_INVALID;
+  }
+  const pdm_block_desc& d = *desc;
+  PDM_CHECK_ARG(x && w && y && workspace, "null pointer");
+  PDM_CHECK_ARG(w->norm1_w && w->s_qkv_w && w->out_w && w->norm2_w && w->s_w1 && w->s_w2, "null weight pointer");
+  PDM_CHECK_ARG(d.n_ns == 0 || (w->ns_qkv_w && w->ns_w1 && w->ns_w2), "null per-token weight pointer");
+  const BlockLayout L = block_layout(d);
+  if (workspace_bytes < L.total) {
+    set_error("pdm_onetrans_block_fwd: workspace of " + std::to_string(workspace_bytes) + " bytes, need " +
+              std::to_string(L.total));
+    return PDM_ERR_WORKSPACE;
+  }
+  const void* ptrs[] = {x, y, workspace, w->s_qkv_w, w->out_w, w->s_w1, w->s_w2,
+                        d.n_ns ? w->ns_qkv_w : w->s_qkv_w, d.n_ns ? w->ns_w1 : w->s_w1,
+                        d.n_ns ? w->ns_w2 : w->s_w2, w->norm1_w, w->norm2_w};
+  for (const void* p : ptrs) PDM_CHECK_ARG(aligned16(p), "every tensor must be 16-byte aligned");
+  PDM_CHECK_ARG((const void*)y != (const void*)x, "y must not alias x");
+
+  auto s = reinterpret_cast<hipStream_t>(stream);
+  char* ws = reinterpret_cast<char*>(workspace);
+  uint16_t* h = reinterpret_cast<uint16_t*>(ws + L.h);
+  uint16_t* q = reinterpret_cast<uint16_t*>(ws + L.q);
+  uint16_t* k = reinterpret_cast<uint16_t*>(ws + L.k);
+  uint16_t* vt = reinterpret_cast<uint16_t*>(ws + L.vt);
+  uint16_t* g = reinterpret_cast<uint16_t*>(ws + L.g);
+  const int B = d.batch, D = d.d_model, H = d.n_heads, F = d.ffn_dim;
+  const int kv = d.kv_len, ql = d.q_len, nns = d.n_ns;
+  int st;
+
+  // 1. h1 = RMSNorm1(x)  [B, kv, D]
+  if ((st = launch_rmsnorm(x, (int64_t)kv * D, kv, B, D, w->norm1_w, h, s)) != PDM_OK) return st;
+
+  // 2. Q (tail rows), K, V^T
+  {
+    GemmArgs g0{};
+    g0.A = h; g0.a_bstride = (int64_t)kv * D;
+    g0.W = reinterpret_cast<const uint16_t*>(w->s_qkv_w);
+    g0.W_ns = reinterpret_cast<const uint16_t*>(w->ns_qkv_w);
+    g0.B = B; g0.n_s = kv - nns; g0.n_ns = nns; g0.N = 3 * D; g0.K = D;
+    g0.q = q; g0.k = k; g0.vt = vt; g0.kv = kv; g0.q_len = ql; g0.kv_pad = L.kv_pad; g0.D = D;
+    if ((st = launch_gemm<EPI_QKV>(g0, s)) != PDM_OK) return st;
+  }
+  // 3. attention -> O (written over Q: each wave reads its Q rows before writing them)
+  {
+    AttnArgs aa{};
+    aa.q = q; aa.k = k; aa.vt = vt; aa.o = q;
+    aa.B = B; aa.H = H; aa.q_len = ql; aa.kv = kv; aa.kv_pad = L.kv_pad;
+    aa.scale_log2 = 1.4426950408889634f / 8.0f;
+    const int64_t gy = (int64_t)B * H;
+    PDM_CHECK_ARG(gy < 65536, "batch * heads must be < 65536");
+    hipLaunchKernelGGL(attn_kernel, dim3((unsigned)((ql + 127) / 128), (unsigned)gy), dim3(256), 0, s, aa);
+    PDM_CHECK_LAUNCH();
+  }
+  // 4. z = bf16(O . Wout^T) + x[:, kv - q_len:]  -> y
+  {
+    GemmArgs g1{};
+    g1.A = q; g1.a_bstride = (int64_t)ql * D;
+    g1.W = reinterpret_cast<const uint16_t*>(w->out_w);
+    g1.B = B; g1.n_s = ql; g1.n_ns = 0; g1.N = D; g1.K = D;
+    g1.out = y; g1.out_bstride = (int64_t)ql * D;
+    g1.res = x; g1.res_bstride = (int64_t)kv * D; g1.res_toff = kv - ql;
+    if ((st = launch_gemm<EPI_RESID>(g1, s)) != PDM_OK) return st;
+  }
+  // 5. h2 = RMSNorm2(z)  [B, q_len, D]
+  if ((st = launch_rmsnorm(y, (int64_t)ql * D, ql, B, D, w->norm2_w, h, s)) != PDM_OK) return st;
+  // 6. g = bf16(gelu(bf16(h2 . W1^T)))  [B, q_len, F]
+  {
+    GemmArgs g2{};
+    g2.A = h; g2.a_bstride = (int64_t)ql * D;
+    g2.W = reinterpret_cast<const uint16_t*>(w->s_w1);
+    g2.W_ns = reinterpret_cast<const uint16_t*>(w->ns_w1);
+    g2.B = B; g2.n_s = ql - nns; g2.n_ns = nns; g2.N = F; g2.K = D;
+    g2.out = g; g2.out_bstride = (int64_t)ql * F;
+    if ((st = launch_gemm<EPI_GELU>(g2, s)) != PDM_OK) return st;
+  }
+  // 7. y = z + bf16(g . W2^T)
+  {
+    GemmArgs g3{};
+    g3.A = g; g3.a_bstride = (int64_t)ql * F;
+    g3.W = reinterpret_cast<const uint16_t*>(w->s_w2);
+    g3.W_ns = reinterpret_cast<const uint16_t*>(w->ns_w2);
+    g3.B = B; g3.n_s = ql - nns; g3.n_ns = nns; g3.N = D; g3.K = F;
+    g3.out = y; g3.out_bstride = (int64_t)ql * D;
+    g3.res = y; g3.res_bstride = (int64_t)ql * D; g3.res_toff = 0;
+    if ((st = launch_gemm<EPI_RESID>(g3, s)) != PDM_OK) return st;
+  }
+  return PDM_OK;
 }

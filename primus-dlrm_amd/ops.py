@@ -237,10 +237,32 @@ def _(tables, ids, offsets, max_len, pad_mode, align):
 # OneTrans block
 # ---------------------------------------------------------------------------
 
+def onetrans_workspace_layout(B: int, kv: int, q_len: int, D: int, F: int) -> Dict[str, Tuple[int, int]]:
+    """Byte (offset, size) of each region of the block workspace, as laid out by
+    pdm_onetrans_block_fwd: h (RMSNorm1 rows [B, kv, D] bf16, later RMSNorm2
+    rows [B, q_len, D]), q (Q tail rows [B, q_len, D] bf16, later the attention
+    output), k ([B, kv, D] bf16), vt (V transposed per head [B, D/64, 64,
+    kv_pad] bf16, kv_pad = kv rounded up to 32), g (GELU of the FFN-up GEMM
+    [B, q_len, F] bf16)."""
+    a = lambda v: (v + 255) // 256 * 256  # noqa: E731
+    kv_pad = (kv + 31) // 32 * 32
+    sizes = [("h", B * kv * D * 2), ("q", B * q_len * D * 2), ("k", B * kv * D * 2),
+             ("vt", B * D * kv_pad * 2), ("g", B * q_len * F * 2)]
+    out, off = {}, 0
+    for name, n in sizes:
+        out[name] = (off, n)
+        off = a(off + n)
+    out["total"] = (off, 0)
+    return out
+
+
 def onetrans_block_raw(x: torch.Tensor, w: Dict[str, torch.Tensor], n_heads: int, q_len: int,
-                       out: Optional[torch.Tensor] = None) -> torch.Tensor:
+                       out: Optional[torch.Tensor] = None, workspace: Optional[torch.Tensor] = None
+                       ) -> torch.Tensor:
     """x: fp32 [B, kv, D]; w: norm1_w/norm2_w fp32 [D], the GEMM weights bf16
-    in nn.Linear layout.  Returns fp32 [B, q_len, D]."""
+    in nn.Linear layout.  Returns fp32 [B, q_len, D].  ``workspace`` (uint8,
+    at least pdm_onetrans_block_workspace_size bytes) is allocated when not
+    given."""
     names = ("norm1_w", "s_qkv_w", "ns_qkv_w", "out_w", "norm2_w", "s_w1", "s_w2", "ns_w1", "ns_w2")
     dev = _require_cuda(x, *[w[k] for k in names])
     if x.dtype != torch.float32 or x.dim() != 3 or not x.is_contiguous():
@@ -261,7 +283,11 @@ def onetrans_block_raw(x: torch.Tensor, w: Dict[str, torch.Tensor], n_heads: int
     ws_bytes = int(L.lib().pdm_onetrans_block_workspace_size(ctypes.byref(desc)))
     if ws_bytes < 0:
         raise L.PdmError(ws_bytes, "pdm_onetrans_block_workspace_size", L.last_error())
-    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    if workspace is None:
+        workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    elif workspace.dtype != torch.uint8 or workspace.numel() < ws_bytes or workspace.device != dev:
+        raise ValueError(f"workspace must be a uint8 tensor of >= {ws_bytes} bytes on {dev}")
+    ws = workspace
     if out is None:
         out = torch.empty((B, q_len, D), dtype=torch.float32, device=dev)
     bw = L.BlockWeights(*[w[k].data_ptr() for k in names])

@@ -68,3 +68,16 @@ def test_custom_ops_registered(pdm):
 
     for name in ("tbe_pooled_fwd", "seq_gather_fwd", "onetrans_block_fwd"):
         assert hasattr(torch.ops.pdm, name)
+
+
+def test_block_workspace_size_matches_python_layout(pdm):
+    L = pdm._lib
+    for B, kv, q, ns, D, Fd in ((1024, 400, 272, 16, 256, 1024), (3, 33, 16, 16, 128, 384), (7, 9, 9, 0, 512, 128)):
+        d = L.BlockDesc(B, D, D // 64, ns, Fd, kv, q, 0)
+        got = L.lib().pdm_onetrans_block_workspace_size(ctypes.byref(d))
+        assert got == pdm.ops.onetrans_workspace_layout(B, kv, q, D, Fd)["total"][0]
+    bad = L.BlockDesc(4, 256, 2, 1, 1024, 10, 5, 0)  # head dim 128
+    assert L.lib().pdm_onetrans_block_workspace_size(ctypes.byref(bad)) == L.PDM_ERR_INVALID
+    assert "head dim" in L.last_error()
+    bad = L.BlockDesc(4, 256, 4, 6, 1024, 10, 5, 0)  # q_len < n_ns
+    assert L.lib().pdm_onetrans_block_workspace_size(ctypes.byref(bad)) == L.PDM_ERR_INVALID
