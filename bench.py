@@ -2,12 +2,20 @@
 
 Default workload: the single-hot pooled lookup (26 tables, rows log-uniform
 in [1e3, 4e7], dim 128 bf16, one Zipf(1.05) id per bag, batch 65,536, sum,
-fp32 out).  ``--workload`` selects another of the five workloads.  A step is
-one forward of the path over one batch already resident in HBM.
+fp32 out).  ``--workload`` selects another:
 
+  ebc_fp32    8 tables x 100,000 x 64 fp32, sum, Poisson(10) bags, B=2048
+  single_hot  (default, above)
+  int8_mean   64 tables x 5,000,000 x 128 int8 rowwise, mean, Poisson(20) bags, B=16,384, fp16 out
+  seq_gather  3 behaviour pools, item 10M x 256 + artist 1M x 64 + album 2M x 64 bf16, B=1024
+  onetrans    4-layer OneTrans block stack, B=1024, 384 S + 16 NS tokens, d 256, schedule 384/256/128/64
+  copy_1gib   calibration only: a 1 GiB device-to-device copy (the HBM counters' reference kernel)
+
+A step is one forward of the path over one batch already resident in HBM.
 Prints ONE JSON line with the throughput, the roofline of the dominant kernel
 (algorithmic bytes or FLOPs per launch over its HIP-event-timed average
-duration) and a CPU baseline (the C oracle on the host cores, bounded sample).
+duration on the launch stream) and a CPU baseline (the oracle on the host
+cores, bounded sample).
 """
 from __future__ import annotations
 
@@ -68,11 +76,11 @@ def time_cpu(fn, reps: int = 5) -> float:
 
 
 # ----------------------------------------------------------------------------------------------
-# pooled workloads
+# pooled workloads (ebc_fp32, single_hot, int8_mean)
 # ----------------------------------------------------------------------------------------------
 
 def setup_pooled(pdm, torch, dev, w, weight_std: float):
-    """Builds the tables of workload ``w`` on the device and returns the step closure."""
+    """Builds the tables of workload ``w`` on the device; returns (step, algorithmic bytes, keepalive)."""
     L = pdm._lib
     dt_code = {"fp32": L.PDM_F32, "bf16": L.PDM_BF16, "int8": L.PDM_I8_SB_F16}[w.dtype]
     pool = {"sum": L.PDM_POOL_SUM, "mean": L.PDM_POOL_MEAN}[w.pooling]
@@ -123,8 +131,8 @@ def setup_pooled(pdm, torch, dev, w, weight_std: float):
 
 
 def cpu_pooled(orc, w, threads: int, row_cap: int, weight_std: float):
-    """The oracle over the same ids on tables capped at ``row_cap`` rows (ids of a
-    capped table are drawn with the same distribution over the capped rows)."""
+    """The oracle over the same bags on tables capped at ``row_cap`` rows (ids of a
+    capped table are redrawn over the capped rows with the same distribution)."""
     import primus_dlrm_amd.synthetic as syn
 
     g = np.random.default_rng(5)
@@ -148,25 +156,118 @@ def cpu_pooled(orc, w, threads: int, row_cap: int, weight_std: float):
         col += w.dim
     flat = np.concatenate(chunks)
     idx = w.indices.copy()
+    alpha = {"bf16": 1.05, "int8": 1.2}.get(w.dtype, None)
     for t, r in enumerate(w.rows):
         if r > row_cap:
             seg = slice(w.offsets[t * w.batch], w.offsets[(t + 1) * w.batch])
-            idx[seg] = syn.zipf_rows(syn.rng(99, t), idx[seg].size, row_cap, 1.05) if w.dtype != "int8" \
-                else idx[seg] % row_cap
+            n = int(w.offsets[(t + 1) * w.batch] - w.offsets[t * w.batch])
+            idx[seg] = syn.zipf_rows(syn.rng(99, t), n, row_cap, alpha) if alpha else \
+                syn.rng(99, t).integers(0, row_cap, n)
     od = "fp32" if w.out_dtype == "fp32" else "fp16"
     sec = time_cpu(lambda: orc.tbe_pooled(flat, slots, idx, w.offsets, w.batch, -1, od, threads=threads))
     return w.num_lookups / sec, sec
 
 
 # ----------------------------------------------------------------------------------------------
+# S-token gather
+# ----------------------------------------------------------------------------------------------
+
+def setup_seq(pdm, torch, dev, w):
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(1004)
+    tables = []
+    for rows, dim in zip(w.table_rows, w.table_dims):
+        t = torch.empty((rows, dim), dtype=torch.bfloat16, device=dev)
+        for r0 in range(0, rows, 1 << 20):
+            n = min(1 << 20, rows - r0)
+            t[r0:r0 + n].copy_(torch.empty((n, dim), device=dev).normal_(0.0, 0.02, generator=gen))
+        tables.append(t)
+    ids = [[torch.from_numpy(a).to(dev) for a in row] for row in w.ids]
+    offs = [torch.from_numpy(o).to(dev) for o in w.offsets]
+
+    def step():
+        pdm.ops.seq_gather_raw(tables, ids, offs, w.max_len)
+
+    S = sum(w.max_len)
+    row_bytes = sum(w.table_dims) * 2
+    events = w.num_events
+    kept = sum(int(np.minimum(np.diff(o), m).sum()) for o, m in zip(w.offsets, w.max_len))
+    # rows read for kept events + row 0 per padded slot (cached) counted once per slot is ignored;
+    # ids read (3 x int64 per kept event), offsets, padded output and mask written
+    alg_bytes = kept * row_bytes + kept * 3 * 8 + sum(o.size * 8 for o in w.offsets) + \
+        w.batch * S * row_bytes + w.batch * S
+    return step, alg_bytes, kept, (tables, ids, offs)
+
+
+def cpu_seq(orc, w, row_cap: int):
+    g = np.random.default_rng(6)
+    tabs = [g.integers(0, 1 << 16, (min(r, row_cap), d), dtype=np.uint16) for r, d in zip(w.table_rows,
+                                                                                          w.table_dims)]
+    ids = [[a % min(r, row_cap) for a, r in zip(row, w.table_rows)] for row in w.ids]
+    sec = time_cpu(lambda: orc.seq_gather(tabs, ids, w.offsets, w.max_len))
+    return sec
+
+
+# ----------------------------------------------------------------------------------------------
+# OneTrans block stack
+# ----------------------------------------------------------------------------------------------
+
+def setup_onetrans(pdm, torch, dev, w):
+    from oracle import onetrans as ot  # noqa: F401  (flop convention lives with the oracle)
+
+    D, F, n_ns = w.d_model, w.d_model * w.ffn_mult, w.n_ns
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(1005)
+    layers = []
+    for _ in w.schedule:
+        r = lambda *s: (torch.randn(*s, device=dev, generator=gen) * 0.02).to(torch.bfloat16)  # noqa: E731
+        layers.append(dict(norm1_w=torch.ones(D, device=dev), s_qkv_w=r(3 * D, D), ns_qkv_w=r(n_ns, 3 * D, D),
+                           out_w=r(D, D), norm2_w=torch.ones(D, device=dev), s_w1=r(F, D), s_w2=r(D, F),
+                           ns_w1=r(n_ns, F, D), ns_w2=r(n_ns, D, F)))
+    kv0 = w.l_s + n_ns
+    x = torch.randn(w.batch, kv0, D, device=dev, generator=gen) * 0.02
+    ws_size = pdm.ops.onetrans_workspace_layout(w.batch, kv0, kv0, D, F)["total"][0]
+    ws = torch.empty(ws_size, dtype=torch.uint8, device=dev)
+    outs = []
+    kv = kv0
+    for q_s in w.schedule:
+        outs.append(torch.empty(w.batch, q_s + n_ns, D, device=dev))
+    H = D // 64
+
+    def step():
+        cur = x
+        for layer, q_s in enumerate(w.schedule):
+            pdm.ops.onetrans_block_raw(cur, layers[layer], H, q_s + n_ns, out=outs[layer], workspace=ws)
+            cur = outs[layer]
+
+    flops = 0.0
+    for q_s in w.schedule:
+        flops += ot.block_flops(w.batch, kv, q_s + n_ns, D, F, n_ns)
+        kv = q_s + n_ns
+    return step, flops, (x, layers, ws, outs)
+
+
+def cpu_onetrans(w, threads: int, batch: int):
+    import torch
+    from oracle import onetrans as ot
+
+    torch.set_num_threads(threads)
+    D, F = w.d_model, w.d_model * w.ffn_mult
+    layers = [ot.random_weights(D, F, w.n_ns, seed=i) for i in range(len(w.schedule))]
+    x = torch.randn(batch, w.l_s + w.n_ns, D) * 0.02
+    sec = time_cpu(lambda: ot.stack_forward(x, layers, w.schedule, D // 64), reps=3)
+    return sec
+
+
+# ----------------------------------------------------------------------------------------------
 
 def main() -> int:
-    ap = argparse.ArgumentParser(description=__doc__)
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="single_hot",
-                    choices=["single_hot", "ebc_fp32", "int8_mean", "seq_gather", "onetrans"])
+                    choices=["single_hot", "ebc_fp32", "int8_mean", "seq_gather", "onetrans", "copy_1gib"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
 
@@ -185,8 +286,8 @@ def main() -> int:
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     threads = cpu_threads()
+    cpu_fn = None
 
-    cfg = {}
     if args.workload in ("single_hot", "ebc_fp32", "int8_mean"):
         if args.workload == "single_hot":
             w, std, cap = syn.single_hot_bf16(), 0.02, 500_000
@@ -194,22 +295,62 @@ def main() -> int:
             w, std, cap = syn.ebc_fp32(), 0.01, 100_000
         else:
             w, std, cap = syn.int8_mean(), 0.05, 200_000
-        step, alg_bytes, keep = setup_pooled(pdm, torch, dev, w, std)
-        units_per_step, unit = w.num_lookups, "lookups/s"
+        step, alg, keep = setup_pooled(pdm, torch, dev, w, std)
+        units, unit, bound = w.num_lookups, "lookups/s", "hbm"
         dtype = {"bf16": "bf16->f32", "fp32": "f32", "int8": "u8->f32"}[w.dtype]
         cfg = {"workload": w.name, "tables": w.num_tables, "rows_total": int(sum(w.rows)), "dim": w.dim,
                "batch": w.batch, "lookups_per_batch": w.num_lookups, "pooling": w.pooling,
                "weights": w.dtype, "out": w.out_dtype}
-        bound = "hbm"
+
+        def cpu_fn():
+            val, sec = cpu_pooled(orc, w, threads, cap, std)
+            return {"value": round(val, 1), "unit": unit, "cores": threads, "kind": "port",
+                    "sample": f"C oracle, full batch of {w.num_lookups} lookups on tables capped at {cap} rows "
+                              f"(ids redrawn over the capped rows), median of 5 reps = {sec:.3f} s"}
+    elif args.workload == "seq_gather":
+        w = syn.seq_gather()
+        step, alg, kept, keep = setup_seq(pdm, torch, dev, w)
+        units, unit, bound, dtype = kept, "events/s", "hbm", "bf16"
+        cfg = {"workload": w.name, "batch": w.batch, "pools": len(w.max_len), "max_len": w.max_len,
+               "tables": {"rows": w.table_rows, "dims": w.table_dims}, "events_kept": kept,
+               "out": [w.batch, sum(w.max_len), sum(w.table_dims)]}
+
+        def cpu_fn():
+            sec = cpu_seq(orc, w, 1_000_000)
+            return {"value": round(kept / sec, 1), "unit": unit, "cores": 1, "kind": "port",
+                    "sample": f"C oracle (one thread), full batch of {kept} kept events, item table capped at "
+                              f"1,000,000 rows (ids taken modulo), median of 5 reps = {sec:.3f} s"}
+    elif args.workload == "copy_1gib":
+        # calibration: a plain device copy of 1 GiB (reads 1 GiB, writes 1 GiB) for the HBM counters
+        src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        keep = (src, dst)
+
+        def step():
+            dst.copy_(src)
+
+        alg, units, unit, bound, dtype = 2 << 30, 2 << 30, "bytes/s", "hbm", "f32"
+        cfg = {"workload": "device_copy_1gib"}
     else:
-        raise SystemExit(f"workload {args.workload} is not wired into bench.py yet")
+        w = syn.onetrans_block()
+        step, alg, keep = setup_onetrans(pdm, torch, dev, w)
+        units, unit, bound, dtype = w.batch, "samples/s", "mfma", "bf16"
+        cfg = {"workload": w.name, "batch": w.batch, "l_s": w.l_s, "n_ns": w.n_ns, "d_model": w.d_model,
+               "n_heads": w.n_heads, "ffn": w.d_model * w.ffn_mult, "schedule": w.schedule,
+               "gflop_per_step": round(alg / 1e9, 1)}
+        cpu_batch = 8
+
+        def cpu_fn():
+            sec = cpu_onetrans(w, threads, cpu_batch)
+            return {"value": round(cpu_batch / sec, 2), "unit": unit, "cores": threads, "kind": "port",
+                    "sample": f"PyTorch-CPU oracle (autocast emulation, fp32) of the 4-layer stack at batch "
+                              f"{cpu_batch}, median of 3 reps = {sec:.3f} s"}
 
     stream = torch.cuda.current_stream(dev)
     log(f"warmup {args.warmup} steps")
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    # per-launch HIP events on the launch stream give the kernel's average duration
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -221,21 +362,23 @@ def main() -> int:
     elapsed = time.perf_counter() - t0
     kernel_ms = statistics.mean(a.elapsed_time(b) for a, b in ev)
     ms_per_step = elapsed * 1e3 / args.steps
-    value = units_per_step * args.steps / elapsed
-    achieved = alg_bytes / (kernel_ms * 1e-3) / 1e9
-    traffic = traffic_from_profiles(args.workload)
-    roofline = {"bound": bound, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                "algorithmic_bytes": int(alg_bytes), "kernel_ms": round(kernel_ms, 5)}
-    log(f"{value:.4g} {unit}, kernel {kernel_ms:.4f} ms, {achieved:.1f} GB/s")
+    value = units * args.steps / elapsed
+    if bound == "hbm":
+        achieved = alg / (kernel_ms * 1e-3) / 1e9
+        roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles(args.workload),
+                    "algorithmic_bytes": int(alg), "kernel_ms": round(kernel_ms, 5)}
+    else:
+        achieved = alg / (kernel_ms * 1e-3) / 1e12
+        roofline = {"bound": "mfma", "achieved": round(achieved, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                    "frac": round(achieved / BF16_PEAK_TFLOPS, 4), "traffic": traffic_from_profiles(args.workload),
+                    "algorithmic_flops": alg, "kernel_ms": round(kernel_ms, 5)}
+    log(f"{value:.4g} {unit}, step {kernel_ms:.4f} ms, {achieved:.1f} {roofline['unit']}")
 
     cpu = None
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and cpu_fn is not None:
         log(f"cpu baseline on {threads} threads")
-        cpu_val, sec = cpu_pooled(orc, w, threads, cap, std)
-        cpu = {"value": round(cpu_val, 1), "unit": unit, "cores": threads, "kind": "port",
-               "sample": f"C oracle, full batch of {w.num_lookups} lookups on tables capped at {cap} rows "
-                         f"(ids redrawn over the capped rows), median of 5 reps = {sec:.3f} s"}
+        cpu = cpu_fn()
 
     line = {"metric": METRIC, "value": round(value, 1), "unit": unit, "n_gpus": 1, "steps": args.steps,
             "warmup": args.warmup, "ms_per_step": round(ms_per_step, 5), "higher_is_better": True,
