@@ -44,7 +44,9 @@ struct TbeArgs {
   int32_t* err;
   int64_t num_indices;
   int64_t B;
-  int64_t num_bags;
+  int64_t num_groups;        // groups of lpb lanes; each pools lpb consecutive bags of one table
+  int64_t chunks_per_table;  // ceil(B / R)
+  int64_t group_count;       // tables of this launch
   int64_t padding_idx;
   int64_t out_stride;  // elements
   int32_t lpb_shift;
@@ -53,22 +55,15 @@ struct TbeArgs {
   int32_t index_bits;
 };
 
-template <int VB>
-struct VecT;
-template <>
-struct VecT<16> { using T = uint4; };
-template <>
-struct VecT<8> { using T = uint2; };
-template <>
-struct VecT<4> { using T = uint32_t; };
-
+// Loads VB bytes from a 4-byte aligned address (rows are only guaranteed
+// 4-byte alignment, e.g. int8 rows of 132 bytes).  Written as dword loads,
+// which the compiler merges into one global_load_dwordx{2,4}: gfx950 vector
+// memory instructions need dword alignment only.
 template <int VB>
 __device__ __forceinline__ void load_words(const char* p, uint32_t (&w)[VB / 4]) {
-  using T = typename VecT<VB>::T;
-  const T v = *reinterpret_cast<const T*>(p);
-  if constexpr (VB == 16) { w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w; }
-  else if constexpr (VB == 8) { w[0] = v.x; w[1] = v.y; }
-  else { w[0] = v; }
+  const uint32_t* q = reinterpret_cast<const uint32_t*>(p);
+#pragma unroll
+  for (int i = 0; i < VB / 4; ++i) w[i] = q[i];
 }
 
 // Elements per VB-byte vector of the stored dtype.
@@ -102,6 +97,12 @@ __device__ __forceinline__ void accumulate(float* acc, const uint32_t (&w)[VB / 
   }
 }
 
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+
+// Stores N pooled values; vec_ok says the destination is aligned for the
+// widest vector stores (native vector types keep them single instructions).
 template <int OT, int N>
 __device__ __forceinline__ void store_out(char* dst, const float* v, bool vec_ok) {
   constexpr int OS = OT == PDM_F32 ? 4 : 2;
@@ -110,7 +111,7 @@ __device__ __forceinline__ void store_out(char* dst, const float* v, bool vec_ok
     if (vec_ok && BYTES % 16 == 0) {
 #pragma unroll
       for (int i = 0; i < N / 4; ++i)
-        reinterpret_cast<float4*>(dst)[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+        reinterpret_cast<f32x4_t*>(dst)[i] = f32x4_t{v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]};
     } else {
 #pragma unroll
       for (int i = 0; i < N; ++i) reinterpret_cast<float*>(dst)[i] = v[i];
@@ -126,10 +127,10 @@ __device__ __forceinline__ void store_out(char* dst, const float* v, bool vec_ok
       if (vec_ok && BYTES % 16 == 0) {
 #pragma unroll
         for (int i = 0; i < N / 8; ++i)
-          reinterpret_cast<uint4*>(dst)[i] = make_uint4(p[4 * i], p[4 * i + 1], p[4 * i + 2], p[4 * i + 3]);
+          reinterpret_cast<u32x4_t*>(dst)[i] = u32x4_t{p[4 * i], p[4 * i + 1], p[4 * i + 2], p[4 * i + 3]};
       } else if (vec_ok && BYTES % 8 == 0) {
 #pragma unroll
-        for (int i = 0; i < N / 4; ++i) reinterpret_cast<uint2*>(dst)[i] = make_uint2(p[2 * i], p[2 * i + 1]);
+        for (int i = 0; i < N / 4; ++i) reinterpret_cast<u32x2_t*>(dst)[i] = u32x2_t{p[2 * i], p[2 * i + 1]};
       } else {
 #pragma unroll
         for (int i = 0; i < N / 2; ++i) reinterpret_cast<uint32_t*>(dst)[i] = p[i];
@@ -147,87 +148,39 @@ __device__ __forceinline__ int64_t shfl64(int64_t v, int src) {
   return (int64_t)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
 }
 
+// Bags pooled at once by one lane group (their accumulators live in registers):
+// about 32 accumulator floats per lane.
+template <int WT, int VB, int NC>
+constexpr int bags_per_group() {
+  constexpr int r = 32 / (NC * epv<WT, VB>());
+  return r < 1 ? 1 : (r > 8 ? 8 : r);
+}
+
+// Row loads issued back to back before the first is accumulated.
+#ifndef PDM_TBE_MAX_ROWS_IN_FLIGHT
+#define PDM_TBE_MAX_ROWS_IN_FLIGHT 4
+#endif
+template <int VB, int NC>
+constexpr int rows_in_flight() {
+  constexpr int u = 32 / (NC * (VB / 4));
+  return u < 2 ? 2 : (u > PDM_TBE_MAX_ROWS_IN_FLIGHT ? PDM_TBE_MAX_ROWS_IN_FLIGHT : u);
+}
+
+// Loads that would fall outside a table read this zero block instead, so the
+// row loads of a batch need no branches; their values are never used.
+constexpr int kSafeBytes = 16 * 1024 + 64;
+__device__ __attribute__((aligned(256))) unsigned char g_safe_row[kSafeBytes];
+
+__device__ __forceinline__ int64_t load_index(const TbeArgs& a, int64_t pos) {
+  return a.index_bits == 32 ? (int64_t)reinterpret_cast<const int32_t*>(a.indices)[pos]
+                            : reinterpret_cast<const int64_t*>(a.indices)[pos];
+}
+
+// Writes one pooled bag (mean divides by the count of pooled rows).
 template <int WT, int OT, int VB, int NC>
-__global__ __launch_bounds__(256) void tbe_pooled_kernel(TbeArgs a) {
-  constexpr int W = VB / 4;
+__device__ __forceinline__ void store_bag(const TbeArgs& a, const TbeMeta& m, int64_t b, int lpb, int j,
+                                          float (&acc)[NC][epv<WT, VB>()], int count) {
   constexpr int EPV = epv<WT, VB>();
-  constexpr int U = 4;  // row loads issued before the first is accumulated
-  const int lane = threadIdx.x & 63;
-  const int lpb = 1 << a.lpb_shift;
-  const int j = lane & (lpb - 1);
-  const int gbase = lane & ~(lpb - 1);
-  const int64_t wave = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-  const int64_t g = (wave << (6 - a.lpb_shift)) + (lane >> a.lpb_shift);
-  if (g >= a.num_bags) return;  // all lanes of a group share g
-
-  const int64_t tl = g / a.B;
-  const int64_t b = g - tl * a.B;
-  const int t = a.group_tables[tl];
-  const TbeMeta m = a.meta[t];
-  const int64_t bag = (int64_t)t * a.B + b;
-  int64_t start = a.offsets[bag];
-  int64_t end = a.offsets[bag + 1];
-  bool bad = false;
-  if (start < 0 || end < start || end > a.num_indices) {
-    bad = true;
-    start = end = 0;
-  }
-  const char* wbase = a.weights + m.w_off + (WT == PDM_I8_SB_F16 ? 4 : 0);
-
-  float acc[NC][EPV];
-#pragma unroll
-  for (int c = 0; c < NC; ++c)
-#pragma unroll
-    for (int e = 0; e < EPV; ++e) acc[c][e] = 0.0f;
-  int count = 0;
-
-  for (int64_t base = start; base < end; base += lpb) {
-    const int n = (int)min((int64_t)lpb, end - base);
-    int64_t my = -1;
-    if (j < n) {
-      my = a.index_bits == 32 ? (int64_t)reinterpret_cast<const int32_t*>(a.indices)[base + j]
-                              : reinterpret_cast<const int64_t*>(a.indices)[base + j];
-    }
-    for (int k = 0; k < n; k += U) {
-      int64_t idx[U];
-      bool ok[U];
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        idx[u] = shfl64(my, gbase + ((k + u) & (lpb - 1)));
-        const bool live = (k + u) < n && !(a.padding_idx >= 0 && idx[u] == a.padding_idx);
-        ok[u] = live && idx[u] >= 0 && idx[u] < m.rows;
-        bad |= live && !ok[u];
-      }
-      uint32_t v[U][NC][W];
-      uint32_t sb[U];
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        if (ok[u]) {
-          const char* row = wbase + idx[u] * (int64_t)m.row_bytes;
-          if constexpr (WT == PDM_I8_SB_F16) sb[u] = *reinterpret_cast<const uint32_t*>(row - 4);
-#pragma unroll
-          for (int c = 0; c < NC; ++c) {
-            const int vi = c * lpb + j;
-            if (vi < a.payload_vecs) load_words<VB>(row + vi * VB, v[u][c]);
-          }
-        }
-      }
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        if (ok[u]) {
-          float scale = 0.0f, bias = 0.0f;
-          if constexpr (WT == PDM_I8_SB_F16) {
-            scale = f16_bits_to_f32(sb[u] & 0xffffu);
-            bias = f16_bits_to_f32(sb[u] >> 16);
-          }
-#pragma unroll
-          for (int c = 0; c < NC; ++c) accumulate<WT, VB>(acc[c], v[u][c], scale, bias);
-          ++count;
-        }
-      }
-    }
-  }
-
   if (m.pooling == PDM_POOL_MEAN && count > 0) {
     const float cf = (float)count;
 #pragma unroll
@@ -235,7 +188,6 @@ __global__ __launch_bounds__(256) void tbe_pooled_kernel(TbeArgs a) {
 #pragma unroll
       for (int e = 0; e < EPV; ++e) acc[c][e] = __fdiv_rn(acc[c][e], cf);
   }
-
   constexpr int OS = OT == PDM_F32 ? 4 : 2;
   char* orow = reinterpret_cast<char*>(a.out) + (b * a.out_stride + m.out_col) * OS;
 #pragma unroll
@@ -243,8 +195,194 @@ __global__ __launch_bounds__(256) void tbe_pooled_kernel(TbeArgs a) {
     const int vi = c * lpb + j;
     if (vi < a.payload_vecs) store_out<OT, EPV>(orow + (int64_t)vi * EPV * OS, acc[c], a.out_vec_ok != 0);
   }
+}
+
+// A group of lpb lanes pools R consecutive bags of one table (R = 1 for
+// multi-hot bags; R > 1 for bags of about one index, so that a group keeps
+// several rows in flight).  Their indices
+// form one contiguous range of the index array (table-major offsets), which
+// the group walks U positions at a time: the U row loads are issued back to
+// back (positions without a valid row read a zero block), then each row is
+// added to the accumulator of the bag its position falls in.  The next chunk
+// of lpb indices is fetched while the current one is pooled.  Rows of a bag
+// are added in bag order, so every sum is the sequential fp32 sum.
+template <int WT, int OT, int VB, int NC, int R>
+__global__ __launch_bounds__(256) void tbe_pooled_kernel(TbeArgs a) {
+  constexpr int EPV = epv<WT, VB>();
+  constexpr int W = VB / 4;
+  constexpr int U = rows_in_flight<VB, NC>();
+  const int lane = threadIdx.x & 63;
+  const int lpb = 1 << a.lpb_shift;
+  const int j = lane & (lpb - 1);
+  const int gbase = lane & ~(lpb - 1);
+  const int64_t wave = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const int64_t grp = (wave << (6 - a.lpb_shift)) + (lane >> a.lpb_shift);
+  if (grp >= a.num_groups) return;  // all lanes of a group share grp
+
+  const int64_t tl = grp / a.chunks_per_table;
+  const int64_t b0 = (grp - tl * a.chunks_per_table) * R;
+  const int nb = (int)min((int64_t)R, a.B - b0);
+  const int t = a.group_tables[tl];
+  const TbeMeta m = a.meta[t];
+  const int64_t bag0 = (int64_t)t * a.B + b0;
+  const char* wbase = a.weights + m.w_off + (WT == PDM_I8_SB_F16 ? 4 : 0);
+  const char* safe = reinterpret_cast<const char*>(g_safe_row) + 16;
+
+  // bag r of the group spans [off[r], off[r + 1]) (every lane of the group loads the same R + 1 offsets)
+  int64_t off[R + 1];
+#pragma unroll
+  for (int r = 0; r <= R; ++r) off[r] = a.offsets[bag0 + (r <= nb ? r : nb)];
+  bool valid = off[0] >= 0 && off[nb] <= a.num_indices;
+#pragma unroll
+  for (int r = 0; r < R; ++r) valid = valid && (r >= nb || off[r + 1] >= off[r]);
+
+  float acc[R][NC][EPV];
+  int count[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    count[r] = 0;
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int e = 0; e < EPV; ++e) acc[r][c][e] = 0.0f;
+  }
+  bool bad = !valid;
+
+  if (valid) {
+    const int64_t s = off[0], e = off[nb];
+    int32_t rel_end[R];  // end of bag r relative to s
+#pragma unroll
+    for (int r = 0; r < R; ++r) rel_end[r] = (int32_t)(off[r < nb ? r + 1 : nb] - s);
+    int64_t next = (j < min((int64_t)lpb, e - s)) ? load_index(a, s + j) : -1;
+    for (int64_t base = s; base < e; base += lpb) {
+      const int n = (int)min((int64_t)lpb, e - base);
+      const int64_t my = next;
+      if (base + lpb < e) next = (j < min((int64_t)lpb, e - base - lpb)) ? load_index(a, base + lpb + j) : -1;
+      const int32_t rel_base = (int32_t)(base - s);
+      for (int k = 0; k < n; k += U) {
+        uint32_t v[U][NC][W];
+        uint32_t sb[U];
+        bool ok[U];
+        int64_t idxs[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) idxs[u] = shfl64(my, gbase + ((k + u) & (lpb - 1)));
+        if constexpr (R == 1) {
+          // one bag: guarded loads, rows added straight into its accumulator
+#pragma unroll
+          for (int u = 0; u < U; ++u) {
+            const int64_t idx = idxs[u];
+            const bool live = (k + u) < n && !(a.padding_idx >= 0 && idx == a.padding_idx);
+            ok[u] = live && idx >= 0 && idx < m.rows;
+            bad |= live && !ok[u];
+            if (ok[u]) {
+              const char* row = wbase + idx * (int64_t)m.row_bytes;
+              if constexpr (WT == PDM_I8_SB_F16) sb[u] = *reinterpret_cast<const uint32_t*>(row - 4);
+#pragma unroll
+              for (int c = 0; c < NC; ++c) {
+                const int vi = c * lpb + j;
+                if (vi < a.payload_vecs) load_words<VB>(row + vi * VB, v[u][c]);
+              }
+            }
+          }
+#pragma unroll
+          for (int u = 0; u < U; ++u) {
+            if (!ok[u]) continue;
+            float scale = 0.0f, bias = 0.0f;
+            if constexpr (WT == PDM_I8_SB_F16) {
+              scale = f16_bits_to_f32(sb[u] & 0xffffu);
+              bias = f16_bits_to_f32(sb[u] >> 16);
+            }
+#pragma unroll
+            for (int c = 0; c < NC; ++c) accumulate<WT, VB>(acc[0][c], v[u][c], scale, bias);
+            ++count[0];
+          }
+          continue;
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int64_t idx = idxs[u];
+          const bool live = (k + u) < n && !(a.padding_idx >= 0 && idx == a.padding_idx);
+          ok[u] = live && idx >= 0 && idx < m.rows;
+          bad |= live && !ok[u];
+          const char* row = ok[u] ? wbase + idx * (int64_t)m.row_bytes : safe;
+          if constexpr (WT == PDM_I8_SB_F16) sb[u] = *reinterpret_cast<const uint32_t*>(row - 4);
+#pragma unroll
+          for (int c = 0; c < NC; ++c) {
+            const int vi = c * lpb + j;
+            load_words<VB>((vi < a.payload_vecs ? row : safe) + vi * VB, v[u][c]);
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int32_t p = rel_base + k + u;
+          int rb = 0;  // bag of position p: number of bag ends at or before p
+#pragma unroll
+          for (int r = 0; r < R; ++r) rb += p >= rel_end[r] ? 1 : 0;
+          float scale = 0.0f, bias = 0.0f;
+          if constexpr (WT == PDM_I8_SB_F16) {
+            scale = f16_bits_to_f32(sb[u] & 0xffffu);
+            bias = f16_bits_to_f32(sb[u] >> 16);
+          }
+          float row_v[NC][EPV];
+#pragma unroll
+          for (int c = 0; c < NC; ++c) {
+#pragma unroll
+            for (int e2 = 0; e2 < EPV; ++e2) row_v[c][e2] = 0.0f;
+            accumulate<WT, VB>(row_v[c], v[u][c], scale, bias);  // decode: 0 + x == x exactly
+          }
+#pragma unroll
+          for (int r = 0; r < R; ++r) {
+            const bool mine = ok[u] && rb == r;
+#pragma unroll
+            for (int c = 0; c < NC; ++c)
+#pragma unroll
+              for (int e2 = 0; e2 < EPV; ++e2) acc[r][c][e2] = mine ? acc[r][c][e2] + row_v[c][e2] : acc[r][c][e2];
+            count[r] += mine ? 1 : 0;
+          }
+        }
+      }
+    }
+  } else {
+    // some bag has an invalid range: it pools to 0 and is reported; the others are pooled one row at a time
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      if (r >= nb) continue;
+      int64_t s0 = off[r], e0 = off[r + 1];
+      if (s0 < 0 || e0 < s0 || e0 > a.num_indices) s0 = e0 = 0;
+      for (int64_t pos = s0; pos < e0; ++pos) {
+        const int64_t idx = load_index(a, pos);
+        const bool live = !(a.padding_idx >= 0 && idx == a.padding_idx);
+        if (!live) continue;
+        if (idx < 0 || idx >= m.rows) continue;
+        const char* row = wbase + idx * (int64_t)m.row_bytes;
+        float scale = 0.0f, bias = 0.0f;
+        if constexpr (WT == PDM_I8_SB_F16) {
+          const uint32_t sbw = *reinterpret_cast<const uint32_t*>(row - 4);
+          scale = f16_bits_to_f32(sbw & 0xffffu);
+          bias = f16_bits_to_f32(sbw >> 16);
+        }
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          const int vi = c * lpb + j;
+          if (vi < a.payload_vecs) {
+            uint32_t w[W];
+            load_words<VB>(row + vi * VB, w);
+            accumulate<WT, VB>(acc[r][c], w, scale, bias);
+          }
+        }
+        ++count[r];
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+    if (r < nb) store_bag<WT, OT, VB, NC>(a, m, b0 + r, lpb, j, acc[r], count[r]);
   if (bad && a.err) a.err[0] = 1;
 }
+
+}  // namespace pdm
+
+namespace pdm {
 
 // ---- quantizer -------------------------------------------------------------
 
@@ -309,7 +447,6 @@ struct TbeGroup {
   int32_t row_bytes_all;  // common row stride, -1 if tables differ
   int32_t first;          // index into the grouped table list
   int32_t count;
-  int64_t min_w_off_align;  // gcd-like alignment of all weights_offsets (power of 2)
   int32_t out_col_align;    // alignment (elements) of all out_offsets
 };
 
@@ -371,14 +508,13 @@ extern "C" int pdm_tbe_plan_create(const pdm_table_desc* tables, int32_t num_tab
     for (auto& g : plan->groups)
       if (g.dtype == d.dtype && g.dim == d.dim) found = true;
     if (found) continue;
-    TbeGroup g{d.dtype, d.dim, d.row_bytes, (int32_t)order.size(), 0, int64_t(1) << 40, 1 << 20};
+    TbeGroup g{d.dtype, d.dim, d.row_bytes, (int32_t)order.size(), 0, 1 << 20};
     for (int u = t; u < num_tables; ++u) {
       const auto& e = plan->tables[u];
       if (e.dtype != d.dtype || e.dim != d.dim) continue;
       order.push_back(u);
       ++g.count;
       if (e.row_bytes != g.row_bytes_all) g.row_bytes_all = -1;
-      g.min_w_off_align = std::min(g.min_w_off_align, std::min(pow2_align(e.weights_offset), pow2_align(e.row_bytes)));
       g.out_col_align = (int32_t)std::min<int64_t>(g.out_col_align, pow2_align(e.out_offset));
     }
     plan->groups.push_back(g);
@@ -414,46 +550,56 @@ namespace {
 
 using KernelFn = void (*)(TbeArgs);
 
+template <int WT, int OT, int VB, int NC>
+KernelFn pick_r(bool multi) {
+  constexpr int RM = bags_per_group<WT, VB, NC>();
+  return multi && RM > 1 ? tbe_pooled_kernel<WT, OT, VB, NC, RM> : tbe_pooled_kernel<WT, OT, VB, NC, 1>;
+}
+
 template <int WT, int OT, int VB>
-KernelFn pick_nc(int nc) {
+KernelFn pick_nc(int nc, bool multi) {
   switch (nc) {
-    case 1: return tbe_pooled_kernel<WT, OT, VB, 1>;
-    case 2: return tbe_pooled_kernel<WT, OT, VB, 2>;
-    case 4: return tbe_pooled_kernel<WT, OT, VB, 4>;
+    case 1: return pick_r<WT, OT, VB, 1>(multi);
+    case 2: return pick_r<WT, OT, VB, 2>(multi);
+    case 4: return pick_r<WT, OT, VB, 4>(multi);
     default: return nullptr;
   }
 }
 
 template <int WT, int OT>
-KernelFn pick_vb(int vb, int nc) {
-  if constexpr (WT == PDM_I8_SB_F16) {
-    return vb == 4 ? pick_nc<WT, OT, 4>(nc) : nullptr;
-  } else {
-    switch (vb) {
-      case 16: return pick_nc<WT, OT, 16>(nc);
-      case 8: return pick_nc<WT, OT, 8>(nc);
-      case 4: return pick_nc<WT, OT, 4>(nc);
-      default: return nullptr;
-    }
-  }
-}
-
-template <int WT>
-KernelFn pick_ot(int ot, int vb, int nc) {
-  switch (ot) {
-    case PDM_F32: return pick_vb<WT, PDM_F32>(vb, nc);
-    case PDM_F16: return pick_vb<WT, PDM_F16>(vb, nc);
-    case PDM_BF16: return pick_vb<WT, PDM_BF16>(vb, nc);
+KernelFn pick_vb(int vb, int nc, bool multi) {
+  switch (vb) {
+    case 16: return pick_nc<WT, OT, 16>(nc, multi);
+    case 8: return pick_nc<WT, OT, 8>(nc, multi);
+    case 4: return pick_nc<WT, OT, 4>(nc, multi);
     default: return nullptr;
   }
 }
 
-KernelFn pick_kernel(int wt, int ot, int vb, int nc) {
+template <int WT>
+KernelFn pick_ot(int ot, int vb, int nc, bool multi) {
+  switch (ot) {
+    case PDM_F32: return pick_vb<WT, PDM_F32>(vb, nc, multi);
+    case PDM_F16: return pick_vb<WT, PDM_F16>(vb, nc, multi);
+    case PDM_BF16: return pick_vb<WT, PDM_BF16>(vb, nc, multi);
+    default: return nullptr;
+  }
+}
+
+// Bags per lane group the kernel picked by pick_kernel pools (mirrors bags_per_group).
+int bags_per_group_rt(int wt, int vb, int nc, bool multi) {
+  if (!multi) return 1;
+  const int e = wt == PDM_F32 ? vb / 4 : (wt == PDM_I8_SB_F16 ? vb : vb / 2);
+  const int r = 32 / (nc * e);
+  return r < 1 ? 1 : (r > 8 ? 8 : r);
+}
+
+KernelFn pick_kernel(int wt, int ot, int vb, int nc, bool multi) {
   switch (wt) {
-    case PDM_F32: return pick_ot<PDM_F32>(ot, vb, nc);
-    case PDM_F16: return pick_ot<PDM_F16>(ot, vb, nc);
-    case PDM_BF16: return pick_ot<PDM_BF16>(ot, vb, nc);
-    case PDM_I8_SB_F16: return pick_ot<PDM_I8_SB_F16>(ot, vb, nc);
+    case PDM_F32: return pick_ot<PDM_F32>(ot, vb, nc, multi);
+    case PDM_F16: return pick_ot<PDM_F16>(ot, vb, nc, multi);
+    case PDM_BF16: return pick_ot<PDM_BF16>(ot, vb, nc, multi);
+    case PDM_I8_SB_F16: return pick_ot<PDM_I8_SB_F16>(ot, vb, nc, multi);
     default: return nullptr;
   }
 }
@@ -479,13 +625,10 @@ extern "C" int pdm_tbe_pooled_fwd(pdm_tbe_plan plan, const void* weights, const 
   const int osize = out_dtype == PDM_F32 ? 4 : 2;
   for (const auto& g : plan->groups) {
     const int payload = g.dtype == PDM_I8_SB_F16 ? g.dim : g.dim * dtype_size(g.dtype);
-    // widest vector that divides the payload and keeps every row aligned
-    const int64_t base_align = std::min(pow2_align((int64_t)(uintptr_t)weights), g.min_w_off_align);
+    // widest load that divides the row payload (loads need 4-byte alignment only)
     int vb = 4;
-    if (g.dtype != PDM_I8_SB_F16) {
-      for (int c : {16, 8}) {
-        if (payload % c == 0 && base_align % c == 0) { vb = c; break; }
-      }
+    for (int c : {16, 8}) {
+      if (payload % c == 0) { vb = c; break; }
     }
     const int vecs = payload / vb;
     int lpb = 1;
@@ -493,7 +636,9 @@ extern "C" int pdm_tbe_pooled_fwd(pdm_tbe_plan plan, const void* weights, const 
     const int nc = (vecs + lpb - 1) / lpb;
     int ncp = 1;
     while (ncp < nc) ncp <<= 1;
-    KernelFn fn = pick_kernel(g.dtype, out_dtype, vb, ncp);
+    // bags of about one index: a lane group pools several bags to keep several rows in flight
+    const bool multi = num_indices <= 2 * T * batch_size;
+    KernelFn fn = pick_kernel(g.dtype, out_dtype, vb, ncp, multi);
     if (!fn) {
       set_error("pdm_tbe_pooled_fwd: unsupported combination (dtype " + std::to_string(g.dtype) + ", dim " +
                 std::to_string(g.dim) + ")");
@@ -516,20 +661,21 @@ extern "C" int pdm_tbe_pooled_fwd(pdm_tbe_plan plan, const void* weights, const 
     a.err = err_flag;
     a.num_indices = num_indices;
     a.B = batch_size;
-    a.num_bags = (int64_t)g.count * batch_size;
+    a.chunks_per_table = (batch_size + bags_per_group_rt(g.dtype, vb, ncp, multi) - 1) / bags_per_group_rt(g.dtype, vb, ncp, multi);
+    a.group_count = g.count;
+    a.num_groups = (int64_t)g.count * a.chunks_per_table;
     a.padding_idx = padding_idx;
     a.out_stride = out_row_stride;
     a.lpb_shift = lpb_shift;
     a.payload_vecs = vecs;
     a.out_vec_ok = out_vec_ok ? 1 : 0;
     a.index_bits = index_bits;
-    const int64_t bags_per_block = 4 * (64 / lpb);
-    const int64_t blocks = (a.num_bags + bags_per_block - 1) / bags_per_block;
+    const int64_t groups_per_block = 4 * (64 / lpb);
+    const int64_t blocks = (a.num_groups + groups_per_block - 1) / groups_per_block;
     PDM_CHECK_ARG(blocks < (int64_t(1) << 31), "too many bags for one launch");
     hipLaunchKernelGGL(fn, dim3((unsigned)blocks), dim3(256), 0, reinterpret_cast<hipStream_t>(stream), a);
     PDM_CHECK_LAUNCH();
   }
-  (void)T;
   return PDM_OK;
 }
 

@@ -145,6 +145,39 @@ def test_pooled_misaligned_weights_base_uses_narrow_loads(pdm, dev):
     _assert_bits(got, want)
 
 
+@pytest.mark.parametrize("dtype", ["fp32", "fp16", "bf16", "int8"])
+@pytest.mark.parametrize("pooling", ["sum", "mean"])
+def test_pooled_short_bags_bitexact(pdm, dev, dtype, pooling):
+    """Bags of 0-3 indices (average <= 2: the kernel pools several bags per lane group),
+    with padding ids, out-of-range ids and ragged batch tails."""
+    g = np.random.default_rng(12)
+    specs = [(700, 64, dtype, pooling), (90, 16, dtype, pooling), (300, 128, dtype, pooling), (50, 12, dtype, pooling)]
+    if dtype == "int8":
+        specs[3] = (50, 20, dtype, pooling)
+    flat, host, slots = _make_tables(g, specs, dev)
+    B = 203
+    lens = g.integers(0, 4, 4 * B)
+    lens[:7] = [0, 1, 0, 3, 1, 1, 2]
+    idx = np.concatenate([g.integers(0, specs[t][0], lens[t * B:(t + 1) * B].sum()) for t in range(4)])
+    idx[g.random(idx.size) < 0.1] = 3  # padding id
+    bad_pos = g.choice(idx.size, 5, replace=False)
+    idx[bad_pos[:3]] = 10 ** 6
+    idx[bad_pos[3:]] = -2
+    got, want, err, bad = _run(pdm, dev, flat, host, slots, idx, o.offsets_np(lens), B, padding_idx=3)
+    _assert_bits(got, want)
+    assert err == 1 and bad == 5
+
+
+def test_pooled_short_bags_bad_offsets(pdm, dev):
+    g = np.random.default_rng(13)
+    flat, host, slots = _make_tables(g, [(40, 64, "bf16", "sum")], dev)
+    idx = g.integers(0, 40, 12)
+    off = np.array([0, 1, 2, 2, 9, 3, 4, 5, 6, 7, 12], dtype=np.int64)  # one bag runs backwards
+    got, want, err, bad = _run(pdm, dev, flat, host, slots, idx, off, 10)
+    _assert_bits(got, want)
+    assert err == 1 and bad >= 1
+
+
 def test_pooled_batch_zero_and_no_indices(pdm, dev):
     g = np.random.default_rng(8)
     flat, host, slots = _make_tables(g, [(10, 8, "fp32", "sum")], dev)
