@@ -40,17 +40,20 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ f32x16_t mfma32x32x16(u32x4_t a, u32x4_t b, f32x16_t c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
                                                  c, 0, 0, 0);
 }
 
-__device__ __forceinline__ float bf16_round(float v) { return bf16_bits_to_f32(f32_to_bf16_bits(v)); }
+// bf16 rounding of the block kernels: the hardware conversion (v_cvt_pk_bf16_f32,
+// round to nearest even), branch free.
+__device__ __forceinline__ uint32_t bf16_bits(float v) { return __builtin_bit_cast(uint16_t, (__bf16)v); }
 
-__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
-}
+__device__ __forceinline__ float bf16_round(float v) { return (float)(__bf16)v; }
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) { return bf16_bits(lo) | (bf16_bits(hi) << 16); }
 
 // ---------------------------------------------------------------------------
 // RMSNorm -> bf16 rows.  One wave per row, D = 64 * VPL.
@@ -96,7 +99,7 @@ __global__ __launch_bounds__(256) void rmsnorm_bf16_kernel(const float* __restri
   for (int i = 0; i < VPL; ++i) {
     const float wv = w[lane * VPL + i];
     const float n = v[i] * rms;
-    o[i] = (uint16_t)f32_to_bf16_bits(n * wv);
+    o[i] = (uint16_t)bf16_bits(n * wv);
   }
 }
 
@@ -104,6 +107,23 @@ __global__ __launch_bounds__(256) void rmsnorm_bf16_kernel(const float* __restri
 // Grouped GEMM  C = A . W^T  over (sample, token) rows.
 // ---------------------------------------------------------------------------
 enum { EPI_BF16 = 0, EPI_QKV = 1, EPI_RESID = 2, EPI_GELU = 3 };
+
+// GELU with the error function, 0.5 x (1 + erf(x / sqrt 2)) (the reference's
+// exact-erf F.gelu), branch free.  erfc(|z|) follows Abramowitz & Stegun,
+// Handbook of Mathematical Functions, formula 7.1.26 (|error| <= 1.5e-7):
+// erfc(a) = t (a1 + t (a2 + t (a3 + t (a4 + t a5)))) exp(-a^2), t = 1 / (1 + p a).
+// 1 + erf(z) is 2 - erfc(z) for z >= 0 and erfc(-z) otherwise, so the
+// negative tail carries no cancellation.  After the bf16 rounding of the
+// result it agrees with the exact-erf GELU except in the far negative tail
+// (x < -3.5, |GELU| < 1e-3), where the two can differ by one bf16 step.
+__device__ __forceinline__ float gelu_erf(float v) {
+  const float z = v * 0.70710678118654752f;
+  const float az = fabsf(z);
+  const float t = __builtin_amdgcn_rcpf(1.0f + 0.3275911f * az);
+  const float poly = t * (0.254829592f + t * (-0.284496736f + t * (1.421413741f + t * (-1.453152027f + t * 1.061405429f))));
+  const float e = poly * __builtin_amdgcn_exp2f(-(az * az) * 1.4426950408889634f);
+  return 0.5f * v * (z >= 0.0f ? 2.0f - e : e);
+}
 
 constexpr int GBM = 128, GBN = 128, GBK = 64, GPAD = 8;
 
@@ -131,9 +151,63 @@ struct GemmArgs {
   uint16_t* k;
   uint16_t* vt;
   int kv, q_len, kv_pad, D;
+  // row-stationary kernels: fp32 A rows normalised on load (RMSNorm weight norm_w), FFN weights
+  const float* A32;
+  const float* norm_w;
+  const uint16_t* W2;     // FFN-down [D, F] shared
+  const uint16_t* W2_ns;  // [n_ns, D, F]
 };
 
-__device__ __forceinline__ float gelu_erf(float v) { return 0.5f * v * (1.0f + erff(v * 0.70710678118654752f)); }
+// Stores one GEMM output element (b, t, n) with the epilogue EPI.
+template <int EPI>
+__device__ __forceinline__ void epilogue_store(const GemmArgs& a, int b, int t, int n, float v) {
+  if constexpr (EPI == EPI_BF16) {
+    reinterpret_cast<uint16_t*>(a.out)[(int64_t)b * a.out_bstride + (int64_t)t * a.N + n] =
+        (uint16_t)bf16_bits(v);
+  } else if constexpr (EPI == EPI_GELU) {
+    reinterpret_cast<uint16_t*>(a.out)[(int64_t)b * a.out_bstride + (int64_t)t * a.N + n] =
+        (uint16_t)bf16_bits(gelu_erf(bf16_round(v)));
+  } else if constexpr (EPI == EPI_RESID) {
+    const float r = a.res[(int64_t)b * a.res_bstride + (int64_t)(t + a.res_toff) * a.N + n];
+    reinterpret_cast<float*>(a.out)[(int64_t)b * a.out_bstride + (int64_t)t * a.N + n] = bf16_round(v) + r;
+  } else {  // EPI_QKV
+    const uint16_t bits = (uint16_t)bf16_bits(v);
+    const int D = a.D;
+    if (n < D) {
+      const int tq = t - (a.kv - a.q_len);
+      if (tq >= 0) a.q[((int64_t)b * a.q_len + tq) * D + n] = bits;
+    } else if (n < 2 * D) {
+      a.k[((int64_t)b * a.kv + t) * D + (n - D)] = bits;
+    } else {
+      const int c = n - 2 * D;
+      const int h = c >> 6, d = c & 63;
+      const int H = D >> 6;
+      a.vt[(((int64_t)b * H + h) * 64 + d) * a.kv_pad + t] = bits;
+    }
+  }
+}
+
+// (sample, token) of row i of GEMM row tile mt, or b = -1 past the end.  Tiles
+// 0 .. tiles_s-1 hold the shared group's rows (sample-major, token minor), the
+// following tiles_b tiles per NS token hold that token's rows of every sample.
+__device__ __forceinline__ void tile_row(const GemmArgs& a, int mt, int rows_per_tile, int i, int& b, int& t) {
+  b = -1;
+  t = 0;
+  if (mt < a.tiles_s) {
+    const int64_t r = (int64_t)mt * rows_per_tile + i;
+    if (r < (int64_t)a.B * a.n_s) {
+      b = (int)(r / a.n_s);
+      t = (int)(r - (int64_t)b * a.n_s);
+    }
+  } else {
+    const int g = (mt - a.tiles_s) / a.tiles_b;
+    const int r = ((mt - a.tiles_s) - g * a.tiles_b) * rows_per_tile + i;
+    if (r < a.B) {
+      b = r;
+      t = a.n_s + g;
+    }
+  }
+}
 
 template <int EPI>
 __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
@@ -155,26 +229,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
   const int n0 = (int)(bid - (int64_t)mt * a.n_tiles) * GBN;
 
   const uint16_t* W = a.W;
-  if (tid < GBM) {
-    int b = -1, t = 0;
-    if (mt < a.tiles_s) {
-      const int64_t r = (int64_t)mt * GBM + tid;
-      if (r < (int64_t)a.B * a.n_s) {
-        b = (int)(r / a.n_s);
-        t = (int)(r - (int64_t)b * a.n_s);
-      }
-    } else {
-      const int g = (mt - a.tiles_s) / a.tiles_b;
-      const int bb = (mt - a.tiles_s) - g * a.tiles_b;
-      const int r = bb * GBM + tid;
-      if (r < a.B) {
-        b = r;
-        t = a.n_s + g;
-      }
-    }
-    s_rb[tid] = b;
-    s_rt[tid] = t;
-  }
+  if (tid < GBM) tile_row(a, mt, GBM, tid, s_rb[tid], s_rt[tid]);
   if (mt >= a.tiles_s) W = a.W_ns + (int64_t)((mt - a.tiles_s) / a.tiles_b) * a.N * a.K;
   __syncthreads();
 
@@ -262,34 +317,374 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
       for (int j = 0; j < 2; ++j) {
         const int n = n0 + wn * 64 + j * 32 + fr;
         if (n >= a.N) continue;
-        const float v = acc[i][j][e];
-        if constexpr (EPI == EPI_BF16) {
-          reinterpret_cast<uint16_t*>(a.out)[(int64_t)b * a.out_bstride + (int64_t)t * a.N + n] =
-              (uint16_t)f32_to_bf16_bits(v);
-        } else if constexpr (EPI == EPI_GELU) {
-          reinterpret_cast<uint16_t*>(a.out)[(int64_t)b * a.out_bstride + (int64_t)t * a.N + n] =
-              (uint16_t)f32_to_bf16_bits(gelu_erf(bf16_round(v)));
-        } else if constexpr (EPI == EPI_RESID) {
-          const float r = a.res[(int64_t)b * a.res_bstride + (int64_t)(t + a.res_toff) * a.N + n];
-          reinterpret_cast<float*>(a.out)[(int64_t)b * a.out_bstride + (int64_t)t * a.N + n] = bf16_round(v) + r;
-        } else {  // EPI_QKV
-          const uint16_t bits = (uint16_t)f32_to_bf16_bits(v);
-          const int D = a.D;
-          if (n < D) {
-            const int tq = t - (a.kv - a.q_len);
-            if (tq >= 0) a.q[((int64_t)b * a.q_len + tq) * D + n] = bits;
-          } else if (n < 2 * D) {
-            a.k[((int64_t)b * a.kv + t) * D + (n - D)] = bits;
-          } else {
-            const int c = n - 2 * D;
-            const int h = c >> 6, d = c & 63;
-            const int H = D >> 6;
-            a.vt[(((int64_t)b * H + h) * 64 + d) * a.kv_pad + t] = bits;
-          }
-        }
+        epilogue_store<EPI>(a, b, t, n, acc[i][j][e]);
       }
     }
   }
+}
+
+// ---------------------------------------------------------------------------
+// Row-stationary GEMM for K = d_model:  out[rows, N] = A[rows, D] . W[N, D]^T.
+//
+// Each wave keeps RB x 32 rows of A for the whole K = D in registers as MFMA
+// A fragments (lane l holds row l%32, k-slots (l/32)*8 .. +8 of every
+// 16-wide k step).  With NORM the rows are fp32 residual-stream rows,
+// normalised on load: a first pass takes the sum of squares (the two lanes of
+// a row each hold half of it), a second re-reads the row (an L2 hit), scales
+// it by rsqrt(mean + eps) and the RMSNorm weight in fp32 and rounds to bf16,
+// exactly the autocast path of the reference (onetrans.py:80-82).  The
+// weight streams global -> LDS (no register staging) through a double
+// buffer in chunks of 32 output columns; each weight fragment read from LDS
+// feeds RB MFMAs.
+// ---------------------------------------------------------------------------
+template <int D, int RB, bool NORM>
+__device__ __forceinline__ void load_row_fragments(const GemmArgs& a, const int* s_rb, const int* s_rt, int wave,
+                                                   int fr, int hf, u32x4_t (&af)[RB][D / 16]) {
+  constexpr int KS = D / 16;
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    const int row = wave * RB * 32 + rb * 32 + fr;
+    const int b = s_rb[row];
+    if (b < 0) {
+#pragma unroll
+      for (int s = 0; s < KS; ++s) af[rb][s] = u32x4_t{0, 0, 0, 0};
+      continue;
+    }
+    const int64_t base = (int64_t)b * a.a_bstride + (int64_t)s_rt[row] * D + hf * 8;
+    if constexpr (NORM) {
+      const float* xr = a.A32 + base;
+      float ss = 0.0f;
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        const f32x4_t v0 = *reinterpret_cast<const f32x4_t*>(xr + s * 16);
+        const f32x4_t v1 = *reinterpret_cast<const f32x4_t*>(xr + s * 16 + 4);
+        ss += v0.x * v0.x + v0.y * v0.y + v0.z * v0.z + v0.w * v0.w;
+        ss += v1.x * v1.x + v1.y * v1.y + v1.z * v1.z + v1.w * v1.w;
+      }
+      ss += __shfl_xor(ss, 32, 64);
+      const float rms = 1.0f / sqrtf(ss / (float)D + 1e-6f);
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        const f32x4_t v0 = *reinterpret_cast<const f32x4_t*>(xr + s * 16);
+        const f32x4_t v1 = *reinterpret_cast<const f32x4_t*>(xr + s * 16 + 4);
+        const f32x4_t w0 = *reinterpret_cast<const f32x4_t*>(a.norm_w + s * 16 + hf * 8);
+        const f32x4_t w1 = *reinterpret_cast<const f32x4_t*>(a.norm_w + s * 16 + hf * 8 + 4);
+        af[rb][s] = u32x4_t{pack_bf16x2((v0.x * rms) * w0.x, (v0.y * rms) * w0.y),
+                            pack_bf16x2((v0.z * rms) * w0.z, (v0.w * rms) * w0.w),
+                            pack_bf16x2((v1.x * rms) * w1.x, (v1.y * rms) * w1.y),
+                            pack_bf16x2((v1.z * rms) * w1.z, (v1.w * rms) * w1.w)};
+      }
+    } else {
+      const uint16_t* ar = reinterpret_cast<const uint16_t*>(a.A) + base;
+#pragma unroll
+      for (int s = 0; s < KS; ++s) af[rb][s] = *reinterpret_cast<const u32x4_t*>(ar + s * 16);
+    }
+  }
+}
+
+// Weight chunks live in LDS as rows of 2*D bytes; 16-byte piece v of row r
+// sits at position v ^ (r & 15), so the 32 lanes reading piece v of rows
+// 0..31 hit distinct banks.
+template <int D>
+__device__ __forceinline__ u32x4_t read_w_frag(const char* lds, int r, int piece) {
+  return *reinterpret_cast<const u32x4_t*>(lds + r * (2 * D) + ((piece ^ (r & 15)) << 4));
+}
+
+template <int D, int RB, int EPI, bool NORM>
+__global__ __launch_bounds__(256, 2) void rowgemm_kernel(GemmArgs a) {
+  constexpr int KS = D / 16;
+  constexpr int TROWS = 4 * RB * 32;
+  constexpr int CHUNK_BYTES = 32 * D * 2;
+  __shared__ __attribute__((aligned(16))) char sW[2][CHUNK_BYTES];
+  __shared__ int s_rb[TROWS];
+  __shared__ int s_rt[TROWS];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int fr = lane & 31, hf = lane >> 5;
+  const int mt = blockIdx.x;
+  for (int i = tid; i < TROWS; i += 256) tile_row(a, mt, TROWS, i, s_rb[i], s_rt[i]);
+  const uint16_t* W = mt < a.tiles_s ? a.W : a.W_ns + (int64_t)((mt - a.tiles_s) / a.tiles_b) * a.N * D;
+  __syncthreads();
+
+  int c0 = 0;
+  if constexpr (EPI == EPI_QKV) {
+    // Q columns are needed only for the kept tail tokens
+    int need = 0;
+    for (int i = tid; i < TROWS; i += 256) need |= (s_rb[i] >= 0 && s_rt[i] >= a.kv - a.q_len) ? 1 : 0;
+    if (!__syncthreads_or(need)) c0 = D / 32;
+  }
+  const int nchunks = a.N / 32;
+  // weight chunk c: 32 rows x D as 32 LDS rows, 16-byte piece v of row r at v ^ (r & 15);
+  // loaded into registers at the top of an iteration, written to LDS at its bottom
+  constexpr int CPR = D / 8;
+  constexpr int WL = 32 * CPR / 256;  // 16-byte pieces per thread
+  u32x4_t wr[WL];
+  auto gload = [&](int c) {
+#pragma unroll
+    for (int p = 0; p < WL; ++p) {
+      const int q = p * 256 + tid;
+      const int r = q / CPR, pos = q - (q / CPR) * CPR;
+      wr[p] = *reinterpret_cast<const u32x4_t*>(W + (int64_t)(c * 32 + r) * D + (pos ^ (r & 15)) * 8);
+    }
+  };
+  auto sstore = [&](int buf) {
+#pragma unroll
+    for (int p = 0; p < WL; ++p) *reinterpret_cast<u32x4_t*>(sW[buf] + (p * 256 + tid) * 16) = wr[p];
+  };
+  gload(c0);
+  sstore(0);
+
+  u32x4_t af[RB][KS];
+  load_row_fragments<D, RB, NORM>(a, s_rb, s_rt, wave, fr, hf, af);
+
+  for (int c = c0; c < nchunks; ++c) {
+    const int buf = (c - c0) & 1;
+    __syncthreads();  // chunk c is in LDS; every wave is done with chunk c - 1
+    const bool more = c + 1 < nchunks;
+    if (more) gload(c + 1);
+    // V columns of the QKV GEMM are computed transposed (weight rows on the
+    // accumulator rows) so that a lane holds consecutive tokens of V^T
+    const bool transposed = EPI == EPI_QKV && c * 32 >= 2 * a.D;
+    float res[RB][16];
+    if constexpr (EPI == EPI_RESID) {
+      // issue the residual loads before the MFMAs
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int row = wave * RB * 32 + rb * 32 + (e >> 2) * 8 + hf * 4 + (e & 3);
+          const int b = s_rb[row];
+          res[rb][e] = b >= 0 ? a.res[(int64_t)b * a.res_bstride + (int64_t)(s_rt[row] + a.res_toff) * a.N + c * 32 + fr]
+                              : 0.0f;
+        }
+    }
+    f32x16_t acc[RB];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[rb][e] = 0.0f;
+    if (transposed) {
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        const u32x4_t wf = read_w_frag<D>(sW[buf], fr, 2 * s + hf);
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) acc[rb] = mfma32x32x16(wf, af[rb][s], acc[rb]);
+      }
+      // acc[rb][e]: weight row (e/4)*8 + hf*4 + e%4 of the chunk, token row rb*32 + fr of the wave
+      const int D_ = a.D, H = D_ >> 6;
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
+        const int row = wave * RB * 32 + rb * 32 + fr;
+        const int b = s_rb[row];
+        if (b < 0) continue;
+        const int t = s_rt[row];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int cv = c * 32 + (e >> 2) * 8 + hf * 4 + (e & 3) - 2 * D_;
+          a.vt[(((int64_t)b * H + (cv >> 6)) * 64 + (cv & 63)) * a.kv_pad + t] =
+              (uint16_t)bf16_bits(acc[rb][e]);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        const u32x4_t wf = read_w_frag<D>(sW[buf], fr, 2 * s + hf);
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) acc[rb] = mfma32x32x16(af[rb][s], wf, acc[rb]);
+      }
+      // acc[rb][e]: row wave*RB*32 + rb*32 + (e/4)*8 + hf*4 + e%4 of the tile, column c*32 + fr
+      const int n = c * 32 + fr;
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int row = wave * RB * 32 + rb * 32 + (e >> 2) * 8 + hf * 4 + (e & 3);
+          const int b = s_rb[row];
+          if (b < 0) continue;
+          if constexpr (EPI == EPI_RESID) {
+            reinterpret_cast<float*>(a.out)[(int64_t)b * a.out_bstride + (int64_t)s_rt[row] * a.N + n] =
+                bf16_round(acc[rb][e]) + res[rb][e];
+          } else {
+            epilogue_store<EPI>(a, b, s_rt[row], n, acc[rb][e]);
+          }
+        }
+    }
+    if (more) sstore(buf ^ 1);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Fused FFN:  y = z + W2 . gelu(W1 . RMSNorm2(z))  for K = d_model = D, hidden F.
+//
+// Each wave owns 32 rows.  RMSNorm2(z) rows stay in registers (same layout
+// as rowgemm's A fragments).  The hidden dimension is walked in chunks of
+// 32 units: U^T = W1_c . h^T puts hidden units on the accumulator rows and
+// token rows on the columns, so lane l holds token row l%32 and 16 hidden
+// units of it.  After GELU (fp32 on the bf16-rounded value, then bf16) those
+// values are the B operand of y^T += W2[:, c] . G^T without leaving
+// registers.  The accumulator row e/4*8 + (l/32)*4 + e%4 of a 16-unit half
+// must meet hidden unit (l/32)*8 + e%8 for the W2 operand to be one
+// contiguous 16-byte read, so LDS row r of the W1 chunk holds hidden unit
+// r with bits 2 and 3 swapped.  W1 and W2 chunks stream global -> LDS
+// directly, double buffered.  The epilogue adds z (fp32) to the
+// bf16-rounded FFN output.
+// ---------------------------------------------------------------------------
+template <int D>
+__global__ __launch_bounds__(256, 1) void ffn_kernel(GemmArgs a) {
+  constexpr int KS = D / 16;
+  constexpr int DB = D / 32;                 // 32-row blocks of the output (d)
+  constexpr int W1_BYTES = 32 * D * 2;       // 32 hidden units x D
+  constexpr int W2_BYTES = D * 64;           // D outputs x 32 hidden units
+  constexpr int W2_PER_WAVE = D * 4 / 256;   // 64-lane copies per wave of a W2 chunk
+  constexpr int NST = 3;                     // LDS ring stages
+  __shared__ __attribute__((aligned(16))) char sW1[NST][W1_BYTES];
+  __shared__ __attribute__((aligned(16))) char sW2[NST][W2_BYTES];
+  __shared__ int s_rb[128];
+  __shared__ int s_rt[128];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int fr = lane & 31, hf = lane >> 5;
+  const int mt = blockIdx.x;
+  if (tid < 128) tile_row(a, mt, 128, tid, s_rb[tid], s_rt[tid]);
+  const int F = a.N;
+  const int64_t gsel = mt < a.tiles_s ? -1 : (mt - a.tiles_s) / a.tiles_b;
+  const uint16_t* W1 = gsel < 0 ? a.W : a.W_ns + gsel * (int64_t)F * D;
+  const uint16_t* W2 = gsel < 0 ? a.W2 : a.W2_ns + gsel * (int64_t)D * F;
+  __syncthreads();
+
+  // Weight chunk c: W1 rows c*32 + swap23(r) (all D columns) as 32 LDS rows with
+  // 16-byte piece v of row r at v ^ (r & 15); W2[d, c*32 .. c*32+32) as D LDS
+  // rows of 64 bytes with piece v of row d at v ^ ((d >> 2) & 3).  Loaded into
+  // registers at the top of an iteration, written to LDS at its bottom, so the
+  // global latency hides behind a whole iteration of compute.
+  constexpr int CPR = D / 8;
+  constexpr int L1 = 32 * CPR / 256;  // 16-byte pieces per thread of a W1 chunk
+  constexpr int L2 = D * 4 / 256;     // and of a W2 chunk
+  u32x4_t r1[L1], r2[L2];
+  auto gload = [&](int c) {
+#pragma unroll
+    for (int p = 0; p < L1; ++p) {
+      const int q = p * 256 + tid;
+      const int r = q / CPR, pos = q - (q / CPR) * CPR;
+      const int v = pos ^ (r & 15);
+      const int hid = c * 32 + ((r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1));
+      r1[p] = *reinterpret_cast<const u32x4_t*>(W1 + (int64_t)hid * D + v * 8);
+    }
+#pragma unroll
+    for (int p = 0; p < L2; ++p) {
+      const int q = p * 256 + tid;
+      const int d = q >> 2, v = (q & 3) ^ ((d >> 2) & 3);
+      r2[p] = *reinterpret_cast<const u32x4_t*>(W2 + (int64_t)d * F + c * 32 + v * 8);
+    }
+  };
+  auto sstore = [&](int buf) {
+#pragma unroll
+    for (int p = 0; p < L1; ++p) *reinterpret_cast<u32x4_t*>(sW1[buf] + (p * 256 + tid) * 16) = r1[p];
+#pragma unroll
+    for (int p = 0; p < L2; ++p) *reinterpret_cast<u32x4_t*>(sW2[buf] + (p * 256 + tid) * 16) = r2[p];
+  };
+  const int nchunks = F / 32;
+  gload(0);
+  sstore(0);
+  if (nchunks > 1) {
+    gload(1);
+    sstore(1);
+  }
+
+  u32x4_t hfr[1][KS];
+  load_row_fragments<D, 1, true>(a, s_rb, s_rt, wave, fr, hf, hfr);
+
+  f32x16_t y[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) y[db][e] = 0.0f;
+
+  // Software pipeline: iteration c issues the FFN-up MFMAs of chunk c + 1
+  // interleaved with the GELU of chunk c (VALU work overlapping the matrix
+  // cores), then the FFN-down MFMAs of chunk c.  Chunks c and c + 1 are
+  // resident in the ring; chunk c + 2 is loaded during the iteration and
+  // written to the stage chunk c - 1 used.
+  constexpr int GPS = 16 / KS;  // GELU evaluations per k step
+  auto up = [&](const char* w1, int s, f32x16_t acc) { return mfma32x32x16(read_w_frag<D>(w1, fr, 2 * s + hf), hfr[0][s], acc); };
+  auto down = [&](const char* w2, const uint32_t (&gp)[8]) {
+    u32x4_t w2f[2][DB];
+#pragma unroll
+    for (int c2 = 0; c2 < 2; ++c2)
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        const int d = db * 32 + fr;
+        w2f[c2][db] = *reinterpret_cast<const u32x4_t*>(w2 + d * 64 + (((2 * c2 + hf) ^ ((d >> 2) & 3)) << 4));
+      }
+#pragma unroll
+    for (int c2 = 0; c2 < 2; ++c2) {
+      const u32x4_t gb = {gp[4 * c2], gp[4 * c2 + 1], gp[4 * c2 + 2], gp[4 * c2 + 3]};
+#pragma unroll
+      for (int db = 0; db < DB; ++db) y[db] = mfma32x32x16(w2f[c2][db], gb, y[db]);
+    }
+  };
+
+  __syncthreads();
+  f32x16_t u;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) u[e] = 0.0f;
+#pragma unroll
+  for (int s = 0; s < KS; ++s) u = up(sW1[0], s, u);
+
+  for (int c = 0; c + 1 < nchunks; ++c) {
+    // chunk c + 1 is in LDS, and every wave is done with chunk c - 1, whose stage receives chunk c + 2
+    __syncthreads();
+    const bool more = c + 2 < nchunks;
+    if (more) gload(c + 2);
+    const char* w1n = sW1[(c + 1) % NST];
+    u32x4_t w1f[KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) w1f[s] = read_w_frag<D>(w1n, fr, 2 * s + hf);
+    f32x16_t un;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) un[e] = 0.0f;
+    uint32_t gp[8];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      un = mfma32x32x16(w1f[s], hfr[0][s], un);
+#pragma unroll
+      for (int q = 0; q < GPS; ++q) {
+        const int e = s * GPS + q;  // G = bf16(gelu(bf16(U))): u[e] is hidden (e/4)*8 + hf*4 + e%4
+        const uint32_t gbits = bf16_bits(gelu_erf(bf16_round(u[e])));
+        if (e & 1) gp[e >> 1] |= gbits << 16;
+        else gp[e >> 1] = gbits;
+      }
+    }
+    down(sW2[c % NST], gp);
+    u = un;
+    if (more) sstore((c + 2) % NST);
+  }
+  {
+    uint32_t gp[8];
+#pragma unroll
+    for (int e = 0; e < 16; e += 2) gp[e >> 1] = pack_bf16x2(gelu_erf(bf16_round(u[e])), gelu_erf(bf16_round(u[e + 1])));
+    down(sW2[(nchunks - 1) % NST], gp);
+  }
+
+  // y[db][e] is output d = db*32 + (e/4)*8 + hf*4 + e%4 of this lane's row
+  const int row = wave * 32 + fr;
+  const int b = s_rb[row];
+  if (b < 0) return;
+  const int64_t off = (int64_t)b * a.out_bstride + (int64_t)s_rt[row] * D;
+  float* out = reinterpret_cast<float*>(a.out) + off;
+  const float* zr = a.res + off;
+#pragma unroll
+  for (int db = 0; db < DB; ++db)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int d = db * 32 + g * 8 + hf * 4;
+      const f32x4_t z = *reinterpret_cast<const f32x4_t*>(zr + d);
+      *reinterpret_cast<f32x4_t*>(out + d) =
+          f32x4_t{z.x + bf16_round(y[db][4 * g]), z.y + bf16_round(y[db][4 * g + 1]),
+                  z.z + bf16_round(y[db][4 * g + 2]), z.w + bf16_round(y[db][4 * g + 3])};
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -429,16 +824,24 @@ struct BlockLayout {
 
 static int64_t align256(int64_t v) { return (v + 255) & ~int64_t(255); }
 
+// d_model 128 and 256 run the fused kernels (RMSNorm inside the GEMMs, FFN in
+// registers); other widths run the tiled GEMM path, which also needs the
+// normalised rows (h) and the GELU activations (g) in the workspace.
+static bool fused_path(const pdm_block_desc& d) { return d.d_model == 128 || d.d_model == 256; }
+
 static BlockLayout block_layout(const pdm_block_desc& d) {
   BlockLayout L;
   const int64_t B = d.batch, D = d.d_model;
+  const bool fused = fused_path(d);
   L.kv_pad = (d.kv_len + 31) & ~31;
   int64_t off = 0;
-  L.h = off; off = align256(off + B * d.kv_len * D * 2);                // h1, later h2
   L.q = off; off = align256(off + B * d.q_len * D * 2);                 // Q, later attention output
   L.k = off; off = align256(off + B * d.kv_len * D * 2);                // K
   L.vt = off; off = align256(off + B * (D / 64) * 64 * (int64_t)L.kv_pad * 2);  // V^T per head
-  L.g = off; off = align256(off + B * d.q_len * (int64_t)d.ffn_dim * 2);  // GELU(FFN-up)
+  if (!fused) {
+    L.h = off; off = align256(off + B * d.kv_len * D * 2);                // h1, later h2
+    L.g = off; off = align256(off + B * d.q_len * (int64_t)d.ffn_dim * 2);  // GELU(FFN-up)
+  }
   L.total = off;
   return L;
 }
@@ -468,6 +871,36 @@ static int launch_gemm(GemmArgs& g, hipStream_t s) {
   if (g.total_blocks == 0) return PDM_OK;
   PDM_CHECK_ARG(g.total_blocks < (int64_t(1) << 31), "GEMM grid too large");
   hipLaunchKernelGGL(gemm_kernel<EPI>, dim3((unsigned)g.total_blocks), dim3(256), 0, s, g);
+  PDM_CHECK_LAUNCH();
+  return PDM_OK;
+}
+
+// Row tiles of rows_per_tile rows: the shared group's tiles, then tiles_b per NS token.
+static int64_t row_tiles(GemmArgs& g, int rows_per_tile) {
+  g.tiles_s = (int)(((int64_t)g.B * g.n_s + rows_per_tile - 1) / rows_per_tile);
+  g.tiles_b = (g.B + rows_per_tile - 1) / rows_per_tile;
+  return (int64_t)g.tiles_s + (int64_t)g.n_ns * g.tiles_b;
+}
+
+template <int EPI, bool NORM>
+static int launch_rowgemm(GemmArgs& g, int D, hipStream_t s) {
+  // the residual epilogue keeps 16 loaded residual values per row block in registers: one row block per wave
+  constexpr int RB = EPI == EPI_RESID ? 1 : 2;
+  const int64_t tiles = row_tiles(g, 4 * RB * 32);
+  if (tiles == 0) return PDM_OK;
+  PDM_CHECK_ARG(tiles < (int64_t(1) << 31), "GEMM grid too large");
+  if (D == 256) hipLaunchKernelGGL((rowgemm_kernel<256, RB, EPI, NORM>), dim3((unsigned)tiles), dim3(256), 0, s, g);
+  else hipLaunchKernelGGL((rowgemm_kernel<128, RB, EPI, NORM>), dim3((unsigned)tiles), dim3(256), 0, s, g);
+  PDM_CHECK_LAUNCH();
+  return PDM_OK;
+}
+
+static int launch_ffn(GemmArgs& g, int D, hipStream_t s) {
+  const int64_t tiles = row_tiles(g, 128);
+  if (tiles == 0) return PDM_OK;
+  PDM_CHECK_ARG(tiles < (int64_t(1) << 31), "FFN grid too large");
+  if (D == 256) hipLaunchKernelGGL(ffn_kernel<256>, dim3((unsigned)tiles), dim3(256), 0, s, g);
+  else hipLaunchKernelGGL(ffn_kernel<128>, dim3((unsigned)tiles), dim3(256), 0, s, g);
   PDM_CHECK_LAUNCH();
   return PDM_OK;
 }
@@ -537,11 +970,19 @@ extern "C" int pdm_onetrans_block_fwd(const pdm_block_desc* desc, const float* x
   const int kv = d.kv_len, ql = d.q_len, nns = d.n_ns;
   int st;
 
-  // 1. h1 = RMSNorm1(x)  [B, kv, D]
-  if ((st = launch_rmsnorm(x, (int64_t)kv * D, kv, B, D, w->norm1_w, h, s)) != PDM_OK) return st;
-
-  // 2. Q (tail rows), K, V^T
-  {
+  if (fused_path(d)) {
+    // 1. Q (tail rows), K, V^T = RMSNorm1(x) . Wqkv^T  (norm fused into the GEMM)
+    GemmArgs g0{};
+    g0.A32 = x; g0.a_bstride = (int64_t)kv * D; g0.norm_w = w->norm1_w;
+    g0.W = reinterpret_cast<const uint16_t*>(w->s_qkv_w);
+    g0.W_ns = reinterpret_cast<const uint16_t*>(w->ns_qkv_w);
+    g0.B = B; g0.n_s = kv - nns; g0.n_ns = nns; g0.N = 3 * D; g0.K = D;
+    g0.q = q; g0.k = k; g0.vt = vt; g0.kv = kv; g0.q_len = ql; g0.kv_pad = L.kv_pad; g0.D = D;
+    if ((st = launch_rowgemm<EPI_QKV, true>(g0, D, s)) != PDM_OK) return st;
+  } else {
+    // 1. h1 = RMSNorm1(x)  [B, kv, D]
+    if ((st = launch_rmsnorm(x, (int64_t)kv * D, kv, B, D, w->norm1_w, h, s)) != PDM_OK) return st;
+    // 2. Q (tail rows), K, V^T
     GemmArgs g0{};
     g0.A = h; g0.a_bstride = (int64_t)kv * D;
     g0.W = reinterpret_cast<const uint16_t*>(w->s_qkv_w);
@@ -569,7 +1010,23 @@ extern "C" int pdm_onetrans_block_fwd(const pdm_block_desc* desc, const float* x
     g1.B = B; g1.n_s = ql; g1.n_ns = 0; g1.N = D; g1.K = D;
     g1.out = y; g1.out_bstride = (int64_t)ql * D;
     g1.res = x; g1.res_bstride = (int64_t)kv * D; g1.res_toff = kv - ql;
-    if ((st = launch_gemm<EPI_RESID>(g1, s)) != PDM_OK) return st;
+    if (fused_path(d)) {
+      if ((st = launch_rowgemm<EPI_RESID, false>(g1, D, s)) != PDM_OK) return st;
+    } else if ((st = launch_gemm<EPI_RESID>(g1, s)) != PDM_OK) {
+      return st;
+    }
+  }
+  if (fused_path(d)) {
+    // 5. y = z + bf16(W2 . gelu(W1 . RMSNorm2(z)))  (norm, both GEMMs and GELU in one kernel)
+    GemmArgs g2{};
+    g2.A32 = y; g2.a_bstride = (int64_t)ql * D; g2.norm_w = w->norm2_w;
+    g2.W = reinterpret_cast<const uint16_t*>(w->s_w1);
+    g2.W_ns = reinterpret_cast<const uint16_t*>(w->ns_w1);
+    g2.W2 = reinterpret_cast<const uint16_t*>(w->s_w2);
+    g2.W2_ns = reinterpret_cast<const uint16_t*>(w->ns_w2);
+    g2.B = B; g2.n_s = ql - nns; g2.n_ns = nns; g2.N = F; g2.K = D;
+    g2.out = y; g2.out_bstride = (int64_t)ql * D; g2.res = y;
+    return launch_ffn(g2, D, s);
   }
   // 5. h2 = RMSNorm2(z)  [B, q_len, D]
   if ((st = launch_rmsnorm(y, (int64_t)ql * D, ql, B, D, w->norm2_w, h, s)) != PDM_OK) return st;

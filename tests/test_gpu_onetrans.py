@@ -59,13 +59,14 @@ def _run_case(pdm, dev, B, kv, q_len, n_ns, D=256, F=1024, seed=0, x_std=1.0, w_
     vt = _ws_view(ws, layout, "vt", (B, H, 64, kv_pad))[..., :kv]
     v = vt.permute(0, 3, 1, 2).reshape(B, kv, D)
     o = _ws_view(ws, layout, "q", (B, q_len, D))
-    g = _ws_view(ws, layout, "g", (B, q_len, F))
-    h2 = _ws_view(ws, layout, "h", (B, q_len, D))
     _close("k", k, parts["k"])
     _close("v", v, parts["v"])
     _close("attention out", o, parts["o"])
-    _close("rmsnorm2", h2, parts["h2"].to(torch.bfloat16))
-    _close("gelu(ffn up)", g, parts["g"])
+    if "g" in layout:  # the unfused path keeps RMSNorm2 rows and GELU activations in the workspace
+        g = _ws_view(ws, layout, "g", (B, q_len, F))
+        h2 = _ws_view(ws, layout, "h", (B, q_len, D))
+        _close("rmsnorm2", h2, parts["h2"].to(torch.bfloat16))
+        _close("gelu(ffn up)", g, parts["g"])
     x_tail = x[:, kv - q_len:]
     _close("block update y - x_tail", got.cpu() - x_tail, want - x_tail)
     _close("block output y", got.cpu(), want)
@@ -85,6 +86,11 @@ def test_block_matches_oracle(pdm, dev, B, kv, q_len, n_ns):
 
 def test_block_d128_ffn384_and_norm_weights(pdm, dev):
     _run_case(pdm, dev, 6, 50, 30, 5, D=128, F=384, seed=7, norm_std=0.3, w_std=0.05)
+
+
+def test_block_d384_tiled_path(pdm, dev):
+    """d_model 384 (the reference's OneTransL width) runs the tiled GEMM path."""
+    _run_case(pdm, dev, 5, 45, 21, 3, D=384, F=1536, seed=8, norm_std=0.2)
 
 
 def test_block_baseline_shape_reduced_batch(pdm, dev):
