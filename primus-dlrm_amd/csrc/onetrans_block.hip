@@ -31,6 +31,7 @@
 // O^T = V^T P^T, so P never leaves registers.
 #include <algorithm>
 #include <cmath>
+#include <mutex>
 
 #include "pdm_common.h"
 
@@ -814,6 +815,149 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// Causal attention with K and V^T of one (sample, head) resident in LDS.
+//
+// One workgroup of 8 waves per (sample, head).  K rows and V^T rows of the
+// head are copied to LDS once; each wave then sweeps its 32-query tiles
+// (tiles w, w + 8, ...) over the key tiles up to its causal limit with no
+// further barriers.  Same math as attn_kernel: S^T = K Q^T puts a query per
+// lane, online softmax in fp32, O^T += V^T P^T with P^T in registers.  Keys
+// are stored in LDS with bits 2 and 3 of their index inside each group of
+// 16 swapped, so that the accumulator rows of S^T a lane holds for a 16-key
+// step are 8 consecutive keys: the V^T operand is then one 16-byte read.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int swap23(int m) { return (m & ~12) | ((m & 4) << 1) | ((m & 8) >> 1); }
+
+__global__ __launch_bounds__(512) void attn_lds_kernel(AttnArgs a) {
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  const int kvp = a.kv_pad;                  // keys held (multiple of 32)
+  char* sK = smem;                           // kvp rows x 128 bytes
+  char* sV = smem + (int64_t)kvp * 128;      // 64 rows x 2*kvp bytes
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int fr = lane & 31, hf = lane >> 5;
+  const int bh = blockIdx.x;
+  const int b = bh / a.H, h = bh - (bh / a.H) * a.H;
+  const int D = a.H * 64;
+  const int off = a.kv - a.q_len;
+
+  // K: LDS row m holds key (m & ~15) | swap23(m & 15); piece p of a row sits at p ^ ((m >> 1) & 7)
+  for (int q = tid; q < kvp * 8; q += 512) {
+    const int m = q >> 3, p = q & 7;
+    const int key = (m & ~15) | swap23(m & 15);
+    u32x4_t v = {0, 0, 0, 0};
+    if (key < a.kv) v = *reinterpret_cast<const u32x4_t*>(a.k + ((int64_t)b * a.kv + key) * D + h * 64 + p * 8);
+    *reinterpret_cast<u32x4_t*>(sK + m * 128 + ((p ^ ((m >> 1) & 7)) << 4)) = v;
+  }
+  // V^T: row d holds keys 0..kvp-1; piece p of a row sits at p ^ ((d >> 2) & 3); keys >= kv are zero
+  const int ppr = kvp >> 3;
+  const uint16_t* vsrc = a.vt + ((int64_t)b * a.H + h) * 64 * kvp;
+  for (int q = tid; q < 64 * ppr; q += 512) {
+    const int d = q / ppr, p = q - (q / ppr) * ppr;
+    u32x4_t v = *reinterpret_cast<const u32x4_t*>(vsrc + (int64_t)d * kvp + p * 8);
+    if (p * 8 + 8 > a.kv) {
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const int k0 = p * 8 + 2 * w;
+        if (k0 >= a.kv) v[w] = 0u;
+        else if (k0 + 1 >= a.kv) v[w] &= 0xffffu;
+      }
+    }
+    *reinterpret_cast<u32x4_t*>(sV + d * (2 * kvp) + ((p ^ ((d >> 2) & 3)) << 4)) = v;
+  }
+  __syncthreads();
+
+  const int ntiles = (a.q_len + 31) >> 5;
+  for (int qt = wave; qt < ntiles; qt += 8) {
+    const int qi0 = qt * 32;
+    const int qi = qi0 + fr;
+    const bool qvalid = qi < a.q_len;
+    const int p_last = qi + off;  // last key this query sees
+    u32x4_t qf[4];
+    const uint16_t* qrow = a.q + ((int64_t)b * a.q_len + qi) * D + h * 64 + hf * 8;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) qf[c] = qvalid ? *reinterpret_cast<const u32x4_t*>(qrow + c * 16) : u32x4_t{0, 0, 0, 0};
+    const int q_last = min(qi0 + 31, a.q_len - 1);
+    const int kv_end = min(a.kv, q_last + off + 1);
+
+    f32x16_t o[2];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) { o[0][e] = 0.0f; o[1][e] = 0.0f; }
+    float m = -INFINITY, l = 0.0f;
+
+    for (int j0 = 0; j0 < kv_end; j0 += 32) {
+      // S^T[key][q] = K . Q^T over the 32 LDS rows j0 .. j0+31
+      const int mrow = j0 + fr;
+      const char* krow = sK + mrow * 128;
+      f32x16_t s;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) s[e] = 0.0f;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const u32x4_t kf = *reinterpret_cast<const u32x4_t*>(krow + (((2 * c + hf) ^ ((mrow >> 1) & 7)) << 4));
+        s = mfma32x32x16(kf, qf[c], s);
+      }
+      // s[e] is LDS row j0 + (e/4)*8 + hf*4 + e%4, i.e. key j0 + 16*(e/8) + hf*8 + e%8
+      const bool diag = j0 + 31 > p_last || j0 + 32 > a.kv;  // some key of the tile is masked for this query
+      float mx = -INFINITY;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        float t = s[e] * a.scale_log2;
+        if (diag) {
+          const int key = j0 + 16 * (e >> 3) + hf * 8 + (e & 7);
+          t = (key <= p_last && key < a.kv) ? t : -INFINITY;
+        }
+        s[e] = t;
+        mx = fmaxf(mx, t);
+      }
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float m_new = fmaxf(m, mx);
+      const float alpha = exp2f(m - m_new);
+      m = m_new;
+      float ps = 0.0f;
+      uint32_t pk[8];
+#pragma unroll
+      for (int e = 0; e < 16; e += 2) {
+        const float p0 = exp2f(s[e] - m_new);
+        const float p1 = exp2f(s[e + 1] - m_new);
+        ps += p0 + p1;
+        pk[e >> 1] = pack_bf16x2(p0, p1);
+      }
+      l = l * alpha + ps;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) { o[0][e] *= alpha; o[1][e] *= alpha; }
+      // O^T[d][q] += V^T . P^T; chunk c2 of P^T holds keys j0 + 16*c2 + hf*8 + 0..7
+#pragma unroll
+      for (int c2 = 0; c2 < 2; ++c2) {
+        const u32x4_t pb = {pk[4 * c2], pk[4 * c2 + 1], pk[4 * c2 + 2], pk[4 * c2 + 3]};
+        const int piece = (j0 >> 3) + 2 * c2 + hf;
+#pragma unroll
+        for (int db = 0; db < 2; ++db) {
+          const int d = db * 32 + fr;
+          const u32x4_t vf = *reinterpret_cast<const u32x4_t*>(sV + d * (2 * kvp) + ((piece ^ ((d >> 2) & 3)) << 4));
+          o[db] = mfma32x32x16(vf, pb, o[db]);
+        }
+      }
+    }
+    l += __shfl_xor(l, 32, 64);
+    if (qvalid) {
+      const float inv = 1.0f / l;
+      uint16_t* orow = a.o + ((int64_t)b * a.q_len + qi) * D + h * 64;
+#pragma unroll
+      for (int db = 0; db < 2; ++db)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int d = db * 32 + g * 8 + hf * 4;
+          u32x2_t w;
+          w[0] = pack_bf16x2(o[db][4 * g] * inv, o[db][4 * g + 1] * inv);
+          w[1] = pack_bf16x2(o[db][4 * g + 2] * inv, o[db][4 * g + 3] * inv);
+          *reinterpret_cast<u32x2_t*>(orow + d) = w;
+        }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
 
@@ -923,6 +1067,25 @@ static int launch_rmsnorm(const float* x, int64_t x_bstride, int T, int64_t B, i
 
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
+// Largest LDS footprint of attn_lds_kernel (keys up to 608 per head); longer
+// sequences run attn_kernel, which streams K and V^T from memory.
+constexpr int64_t kAttnLdsMax = 608 * 256;
+
+// Allows attn_lds_kernel more than the default 64 KiB of dynamic LDS (once per process and device).
+static int attn_lds_prepare() {
+  static std::once_flag once[64];
+  static hipError_t err[64];
+  int dev = 0;
+  PDM_CHECK_HIP(hipGetDevice(&dev));
+  if (dev < 0 || dev >= 64) return PDM_OK;
+  std::call_once(once[dev], [&] {
+    err[dev] = hipFuncSetAttribute(reinterpret_cast<const void*>(attn_lds_kernel),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)kAttnLdsMax);
+  });
+  PDM_CHECK_HIP(err[dev]);
+  return PDM_OK;
+}
+
 }  // namespace pdm
 
 using namespace pdm;
@@ -998,8 +1161,15 @@ extern "C" int pdm_onetrans_block_fwd(const pdm_block_desc* desc, const float* x
     aa.B = B; aa.H = H; aa.q_len = ql; aa.kv = kv; aa.kv_pad = L.kv_pad;
     aa.scale_log2 = 1.4426950408889634f / 8.0f;
     const int64_t gy = (int64_t)B * H;
-    PDM_CHECK_ARG(gy < 65536, "batch * heads must be < 65536");
-    hipLaunchKernelGGL(attn_kernel, dim3((unsigned)((ql + 127) / 128), (unsigned)gy), dim3(256), 0, s, aa);
+    const int64_t lds = (int64_t)L.kv_pad * 256;  // K rows (128 B) + V^T rows (2 B per key) of one head
+    if (lds <= kAttnLdsMax) {
+      if ((st = attn_lds_prepare()) != PDM_OK) return st;
+      PDM_CHECK_ARG(gy < (int64_t(1) << 31), "batch * heads too large");
+      hipLaunchKernelGGL(attn_lds_kernel, dim3((unsigned)gy), dim3(512), (unsigned)lds, s, aa);
+    } else {
+      PDM_CHECK_ARG(gy < 65536, "batch * heads must be < 65536");
+      hipLaunchKernelGGL(attn_kernel, dim3((unsigned)((ql + 127) / 128), (unsigned)gy), dim3(256), 0, s, aa);
+    }
     PDM_CHECK_LAUNCH();
   }
   // 4. z = bf16(O . Wout^T) + x[:, kv - q_len:]  -> y
