@@ -17,6 +17,7 @@
 // reported through an optional device flag.
 #include <algorithm>
 #include <memory>
+#include <type_traits>
 #include <vector>
 
 #include "pdm_common.h"
@@ -380,6 +381,150 @@ __global__ __launch_bounds__(256) void tbe_pooled_kernel(TbeArgs a) {
   if (bad && a.err) a.err[0] = 1;
 }
 
+// Bags of at most one index (single-hot lookups): a group of LPB lanes owns
+// LPB consecutive bags of one table.  Lane j loads the offsets and the index
+// of bag j, the group then issues the LPB row loads back to back (lane j
+// reads pieces j, LPB + j, ... of every row) and writes each row out
+// converted, with no accumulators; the output value is 0 + row (the
+// sequential fp32 sum of one row, so -0 becomes +0 as in the oracle), and a
+// mean over one row is the row.  The piece width is picked so that a lane's
+// output for one piece is at most 16 bytes: each store instruction of a group
+// then writes one contiguous run.  A group holding a longer bag or an invalid
+// range pools its bags one at a time instead.
+template <int WT, int OT, int VB, int LPB, int NC>
+__global__ __launch_bounds__(256) void tbe_short_kernel(TbeArgs a) {
+  constexpr int EPV = epv<WT, VB>();
+  constexpr int W = VB / 4;
+  constexpr int U = 4;
+  const int lane = threadIdx.x & 63;
+  const int j = lane & (LPB - 1);
+  const int gbase = lane & ~(LPB - 1);
+  const int64_t wave = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const int64_t grp = wave * (64 / LPB) + lane / LPB;
+  if (grp >= a.num_groups) return;  // all lanes of a group share grp
+
+  const int64_t tl = grp / a.chunks_per_table;
+  const int64_t b0 = (grp - tl * a.chunks_per_table) * LPB;
+  const int nb = (int)min((int64_t)LPB, a.B - b0);
+  const int t = a.group_tables[tl];
+  const TbeMeta m = a.meta[t];
+  const int64_t bag0 = (int64_t)t * a.B + b0;
+  const char* wbase = a.weights + m.w_off + (WT == PDM_I8_SB_F16 ? 4 : 0);
+  const char* safe = reinterpret_cast<const char*>(g_safe_row) + 16;
+
+  constexpr int OS = OT == PDM_F32 ? 4 : 2;
+
+  int64_t st = 0, en = 0;
+  if (j < nb) {
+    st = a.offsets[bag0 + j];
+    en = a.offsets[bag0 + j + 1];
+  }
+  const bool short_ok = j >= nb || (st >= 0 && en >= st && en <= a.num_indices && en - st <= 1);
+  const uint64_t gmask = (LPB == 64 ? ~0ull : ((1ull << LPB) - 1ull)) << gbase;
+  bool bad = false;
+
+  if ((__ballot(!short_ok) & gmask) == 0) {
+    int64_t idx = -1;
+    bool live = false;
+    if (j < nb && en - st == 1) {
+      idx = load_index(a, st);
+      live = !(a.padding_idx >= 0 && idx == a.padding_idx);
+    }
+    const bool ok = live && idx >= 0 && idx < m.rows;
+    bad = live && !ok;
+    uint32_t v[LPB][NC][W];
+    uint32_t sb[LPB];
+    bool okr[LPB];
+#pragma unroll
+    for (int r = 0; r < LPB; ++r) {
+      const int64_t ir = shfl64(idx, gbase + r);
+      okr[r] = __shfl(ok ? 1 : 0, gbase + r, 64) != 0;
+      const char* row = okr[r] ? wbase + ir * (int64_t)m.row_bytes : safe;
+      if constexpr (WT == PDM_I8_SB_F16) sb[r] = *reinterpret_cast<const uint32_t*>(row - 4);
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const int vi = c * LPB + j;
+        load_words<VB>((vi < a.payload_vecs ? row : safe) + vi * VB, v[r][c]);
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < LPB; ++r) {
+      if (r >= nb) continue;
+      float acc[NC][EPV];
+#pragma unroll
+      for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int e = 0; e < EPV; ++e) acc[c][e] = 0.0f;
+      if (okr[r]) {
+        float scale = 0.0f, bias = 0.0f;
+        if constexpr (WT == PDM_I8_SB_F16) {
+          scale = f16_bits_to_f32(sb[r] & 0xffffu);
+          bias = f16_bits_to_f32(sb[r] >> 16);
+        }
+#pragma unroll
+        for (int c = 0; c < NC; ++c) accumulate<WT, VB>(acc[c], v[r][c], scale, bias);
+      }
+      char* orow = reinterpret_cast<char*>(a.out) + ((b0 + r) * a.out_stride + m.out_col) * OS;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const int vi = c * LPB + j;
+        if (vi < a.payload_vecs) store_out<OT, EPV>(orow + (int64_t)vi * EPV * OS, acc[c], a.out_vec_ok != 0);
+      }
+    }
+  } else {
+    for (int r = 0; r < nb; ++r) {
+      int64_t s0 = shfl64(st, gbase + r), e0 = shfl64(en, gbase + r);
+      if (s0 < 0 || e0 < s0 || e0 > a.num_indices) {
+        bad = true;
+        s0 = e0 = 0;
+      }
+      float acc[NC][EPV];
+#pragma unroll
+      for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int e = 0; e < EPV; ++e) acc[c][e] = 0.0f;
+      int count = 0;
+      for (int64_t base = s0; base < e0; base += LPB) {
+        const int n = (int)min((int64_t)LPB, e0 - base);
+        const int64_t my = j < n ? load_index(a, base + j) : -1;
+        for (int k = 0; k < n; k += U) {
+          uint32_t v[U][NC][W];
+          uint32_t sb[U];
+          bool ok[U];
+#pragma unroll
+          for (int u = 0; u < U; ++u) {
+            const int64_t idx = shfl64(my, gbase + ((k + u) & (LPB - 1)));
+            const bool live = (k + u) < n && !(a.padding_idx >= 0 && idx == a.padding_idx);
+            ok[u] = live && idx >= 0 && idx < m.rows;
+            bad |= live && !ok[u];
+            const char* row = ok[u] ? wbase + idx * (int64_t)m.row_bytes : safe;
+            if constexpr (WT == PDM_I8_SB_F16) sb[u] = *reinterpret_cast<const uint32_t*>(row - 4);
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+              const int vi = c * LPB + j;
+              load_words<VB>((vi < a.payload_vecs ? row : safe) + vi * VB, v[u][c]);
+            }
+          }
+#pragma unroll
+          for (int u = 0; u < U; ++u) {
+            if (!ok[u]) continue;
+            float scale = 0.0f, bias = 0.0f;
+            if constexpr (WT == PDM_I8_SB_F16) {
+              scale = f16_bits_to_f32(sb[u] & 0xffffu);
+              bias = f16_bits_to_f32(sb[u] >> 16);
+            }
+#pragma unroll
+            for (int c = 0; c < NC; ++c) accumulate<WT, VB>(acc[c], v[u][c], scale, bias);
+            ++count;
+          }
+        }
+      }
+      store_bag<WT, OT, VB, NC>(a, m, b0 + r, LPB, j, acc, count);
+    }
+  }
+  if (bad && a.err) a.err[0] = 1;
+}
+
 }  // namespace pdm
 
 namespace pdm {
@@ -551,37 +696,96 @@ namespace {
 using KernelFn = void (*)(TbeArgs);
 
 template <int WT, int OT, int VB, int NC>
-KernelFn pick_r(bool multi) {
-  constexpr int RM = bags_per_group<WT, VB, NC>();
-  return multi && RM > 1 ? tbe_pooled_kernel<WT, OT, VB, NC, RM> : tbe_pooled_kernel<WT, OT, VB, NC, 1>;
-}
-
-template <int WT, int OT, int VB>
-KernelFn pick_nc(int nc, bool multi) {
-  switch (nc) {
-    case 1: return pick_r<WT, OT, VB, 1>(multi);
-    case 2: return pick_r<WT, OT, VB, 2>(multi);
-    case 4: return pick_r<WT, OT, VB, 4>(multi);
+KernelFn pick_short_lpb(int lpb) {
+  switch (lpb) {
+    case 2: return tbe_short_kernel<WT, OT, VB, 2, NC>;
+    case 4: return tbe_short_kernel<WT, OT, VB, 4, NC>;
+    case 8: return tbe_short_kernel<WT, OT, VB, 8, NC>;
+    case 16: return tbe_short_kernel<WT, OT, VB, 16, NC>;
     default: return nullptr;
   }
 }
 
 template <int WT, int OT>
-KernelFn pick_vb(int vb, int nc, bool multi) {
+KernelFn pick_short(int vb, int nc, int lpb) {
+  switch (vb * 8 + nc) {
+    case 16 * 8 + 1: return pick_short_lpb<WT, OT, 16, 1>(lpb);
+    case 8 * 8 + 1: return pick_short_lpb<WT, OT, 8, 1>(lpb);
+    case 8 * 8 + 2: return pick_short_lpb<WT, OT, 8, 2>(lpb);
+    case 4 * 8 + 1: return pick_short_lpb<WT, OT, 4, 1>(lpb);
+    case 4 * 8 + 2: return pick_short_lpb<WT, OT, 4, 2>(lpb);
+    default: return nullptr;
+  }
+}
+
+// Kernel for bags of about one index per bag (tbe_pooled_kernel with several bags per group; the
+// single-hot kernel is picked separately).
+template <int WT, int OT, int VB, int NC>
+KernelFn pick_r(bool multi, int lpb, bool& short_path) {
+  constexpr int RM = bags_per_group<WT, VB, NC>();
+  short_path = false;
+  (void)lpb;
+  return multi && RM > 1 ? tbe_pooled_kernel<WT, OT, VB, NC, RM> : tbe_pooled_kernel<WT, OT, VB, NC, 1>;
+}
+
+// Single-hot kernel for a table group: piece width vb so that a lane's output per piece is <= 16 bytes,
+// lane groups of at most 16 lanes with one or two pieces per lane.  Returns null when no such shape fits.
+KernelFn pick_short_kernel(int wt, int ot, int payload, int osize, int& vb, int& lpb, int& nc) {
+  const int in_bytes = wt == PDM_I8_SB_F16 ? 1 : dtype_size(wt);
+  const int cap = std::max(4, 16 * in_bytes / osize);
+  vb = 0;
+  for (int c : {16, 8, 4})
+    if (c <= cap && payload % c == 0) { vb = c; break; }
+  if (vb == 0) return nullptr;
+  const int vecs = payload / vb;
+  lpb = 1;
+  while (lpb < vecs && lpb < 16) lpb <<= 1;
+  if (lpb < 2 || vecs % lpb != 0 || vecs / lpb > 2) return nullptr;
+  nc = vecs / lpb;
+  auto by_ot = [&](auto wt_tag) -> KernelFn {
+    constexpr int WT = decltype(wt_tag)::value;
+    switch (ot) {
+      case PDM_F32: return pick_short<WT, PDM_F32>(vb, nc, lpb);
+      case PDM_F16: return pick_short<WT, PDM_F16>(vb, nc, lpb);
+      case PDM_BF16: return pick_short<WT, PDM_BF16>(vb, nc, lpb);
+      default: return nullptr;
+    }
+  };
+  switch (wt) {
+    case PDM_F32: return by_ot(std::integral_constant<int, PDM_F32>{});
+    case PDM_F16: return by_ot(std::integral_constant<int, PDM_F16>{});
+    case PDM_BF16: return by_ot(std::integral_constant<int, PDM_BF16>{});
+    case PDM_I8_SB_F16: return by_ot(std::integral_constant<int, PDM_I8_SB_F16>{});
+    default: return nullptr;
+  }
+}
+
+template <int WT, int OT, int VB>
+KernelFn pick_nc(int nc, bool multi, int lpb, bool& sp) {
+  switch (nc) {
+    case 1: return pick_r<WT, OT, VB, 1>(multi, lpb, sp);
+    case 2: return pick_r<WT, OT, VB, 2>(multi, lpb, sp);
+    case 4: return pick_r<WT, OT, VB, 4>(multi, lpb, sp);
+    default: return nullptr;
+  }
+}
+
+template <int WT, int OT>
+KernelFn pick_vb(int vb, int nc, bool multi, int lpb, bool& sp) {
   switch (vb) {
-    case 16: return pick_nc<WT, OT, 16>(nc, multi);
-    case 8: return pick_nc<WT, OT, 8>(nc, multi);
-    case 4: return pick_nc<WT, OT, 4>(nc, multi);
+    case 16: return pick_nc<WT, OT, 16>(nc, multi, lpb, sp);
+    case 8: return pick_nc<WT, OT, 8>(nc, multi, lpb, sp);
+    case 4: return pick_nc<WT, OT, 4>(nc, multi, lpb, sp);
     default: return nullptr;
   }
 }
 
 template <int WT>
-KernelFn pick_ot(int ot, int vb, int nc, bool multi) {
+KernelFn pick_ot(int ot, int vb, int nc, bool multi, int lpb, bool& sp) {
   switch (ot) {
-    case PDM_F32: return pick_vb<WT, PDM_F32>(vb, nc, multi);
-    case PDM_F16: return pick_vb<WT, PDM_F16>(vb, nc, multi);
-    case PDM_BF16: return pick_vb<WT, PDM_BF16>(vb, nc, multi);
+    case PDM_F32: return pick_vb<WT, PDM_F32>(vb, nc, multi, lpb, sp);
+    case PDM_F16: return pick_vb<WT, PDM_F16>(vb, nc, multi, lpb, sp);
+    case PDM_BF16: return pick_vb<WT, PDM_BF16>(vb, nc, multi, lpb, sp);
     default: return nullptr;
   }
 }
@@ -594,12 +798,12 @@ int bags_per_group_rt(int wt, int vb, int nc, bool multi) {
   return r < 1 ? 1 : (r > 8 ? 8 : r);
 }
 
-KernelFn pick_kernel(int wt, int ot, int vb, int nc, bool multi) {
+KernelFn pick_kernel(int wt, int ot, int vb, int nc, bool multi, int lpb, bool& sp) {
   switch (wt) {
-    case PDM_F32: return pick_ot<PDM_F32>(ot, vb, nc, multi);
-    case PDM_F16: return pick_ot<PDM_F16>(ot, vb, nc, multi);
-    case PDM_BF16: return pick_ot<PDM_BF16>(ot, vb, nc, multi);
-    case PDM_I8_SB_F16: return pick_ot<PDM_I8_SB_F16>(ot, vb, nc, multi);
+    case PDM_F32: return pick_ot<PDM_F32>(ot, vb, nc, multi, lpb, sp);
+    case PDM_F16: return pick_ot<PDM_F16>(ot, vb, nc, multi, lpb, sp);
+    case PDM_BF16: return pick_ot<PDM_BF16>(ot, vb, nc, multi, lpb, sp);
+    case PDM_I8_SB_F16: return pick_ot<PDM_I8_SB_F16>(ot, vb, nc, multi, lpb, sp);
     default: return nullptr;
   }
 }
@@ -638,7 +842,19 @@ extern "C" int pdm_tbe_pooled_fwd(pdm_tbe_plan plan, const void* weights, const 
     while (ncp < nc) ncp <<= 1;
     // bags of about one index: a lane group pools several bags to keep several rows in flight
     const bool multi = num_indices <= 2 * T * batch_size;
-    KernelFn fn = pick_kernel(g.dtype, out_dtype, vb, ncp, multi);
+    bool short_path = false;
+    KernelFn fn = nullptr;
+    if (multi) {
+      int svb = 0, slpb = 0, snc = 0;
+      if ((fn = pick_short_kernel(g.dtype, out_dtype, payload, osize, svb, slpb, snc)) != nullptr) {
+        short_path = true;
+        vb = svb;
+        lpb = slpb;
+        ncp = snc;
+      }
+    }
+    if (!fn) fn = pick_kernel(g.dtype, out_dtype, vb, ncp, multi, lpb, short_path);
+    (void)vecs;
     if (!fn) {
       set_error("pdm_tbe_pooled_fwd: unsupported combination (dtype " + std::to_string(g.dtype) + ", dim " +
                 std::to_string(g.dim) + ")");
@@ -661,13 +877,14 @@ extern "C" int pdm_tbe_pooled_fwd(pdm_tbe_plan plan, const void* weights, const 
     a.err = err_flag;
     a.num_indices = num_indices;
     a.B = batch_size;
-    a.chunks_per_table = (batch_size + bags_per_group_rt(g.dtype, vb, ncp, multi) - 1) / bags_per_group_rt(g.dtype, vb, ncp, multi);
+    const int bags = short_path ? lpb : bags_per_group_rt(g.dtype, vb, ncp, multi);
+    a.chunks_per_table = (batch_size + bags - 1) / bags;
     a.group_count = g.count;
     a.num_groups = (int64_t)g.count * a.chunks_per_table;
     a.padding_idx = padding_idx;
     a.out_stride = out_row_stride;
     a.lpb_shift = lpb_shift;
-    a.payload_vecs = vecs;
+    a.payload_vecs = payload / vb;
     a.out_vec_ok = out_vec_ok ? 1 : 0;
     a.index_bits = index_bits;
     const int64_t groups_per_block = 4 * (64 / lpb);

@@ -168,6 +168,43 @@ def test_pooled_short_bags_bitexact(pdm, dev, dtype, pooling):
     assert err == 1 and bad == 5
 
 
+@pytest.mark.parametrize("dtype", ["fp32", "fp16", "bf16", "int8"])
+@pytest.mark.parametrize("pooling", ["sum", "mean"])
+@pytest.mark.parametrize("out_dtype", ["fp32", "bf16"])
+def test_pooled_single_hot_fast_path_bitexact(pdm, dev, dtype, pooling, out_dtype):
+    """Mostly one index per bag: lane groups whose bags all hold <= 1 index take the
+    direct row-conversion path, groups with a longer bag fall back to pooling bag by
+    bag; rows of -0.0 must come out as +0.0 (0 + row)."""
+    g = np.random.default_rng(14)
+    dims = {"fp32": (8, 16, 32, 64), "fp16": (16, 32, 64, 128), "bf16": (16, 32, 64, 128),
+            "int8": (32, 64, 128, 128)}[dtype]
+    specs = [(r, d, dtype, pooling) for r, d in zip((300, 90, 5000, 777), dims)]
+    flat, host, slots = _make_tables(g, specs, dev)
+    if dtype != "int8":
+        # a row of negative zeros in table 0
+        w = host[slots[0]["weights_offset"]:].view(np.uint8)
+        rb = dims[0] * {"fp32": 4, "fp16": 2, "bf16": 2}[dtype]
+        neg0 = np.zeros(dims[0], {"fp32": np.float32, "fp16": np.float16, "bf16": np.uint16}[dtype])
+        if dtype == "bf16":
+            neg0[:] = 0x8000
+        else:
+            neg0[:] = -0.0
+        w[5 * rb:6 * rb] = neg0.view(np.uint8)
+        flat = torch.from_numpy(host).to(dev)
+    B = 517
+    lens = np.ones(4 * B, dtype=np.int64)
+    lens[g.random(4 * B) < 0.05] = 0
+    lens[g.choice(4 * B, 6, replace=False)] = 2  # a few groups take the fallback
+    idx = np.concatenate([g.integers(0, specs[t][0], lens[t * B:(t + 1) * B].sum()) for t in range(4)])
+    idx[:40:7] = 5  # the -0.0 row
+    idx[g.random(idx.size) < 0.03] = 7  # padding id
+    idx[g.choice(idx.size, 3, replace=False)] = 10 ** 7
+    got, want, err, bad = _run(pdm, dev, flat, host, slots, idx, o.offsets_np(lens), B, out_dtype=out_dtype,
+                               padding_idx=7)
+    _assert_bits(got, want)
+    assert err == 1 and bad == 3
+
+
 def test_pooled_short_bags_bad_offsets(pdm, dev):
     g = np.random.default_rng(13)
     flat, host, slots = _make_tables(g, [(40, 64, "bf16", "sum")], dev)
