@@ -44,13 +44,50 @@ struct SeqArgs {
 template <int VB>
 struct SVec;
 template <>
-struct SVec<16> { using T = uint4; };
+struct SVec<16> { typedef unsigned int T __attribute__((ext_vector_type(4))); };
 template <>
 struct SVec<4> { using T = uint32_t; };
+
+// Loads through a pointer known to address global memory (pointers read back
+// from LDS are generic, which would otherwise make these flat loads).
+template <class T>
+__device__ __forceinline__ T load_global(const void* p) {
+  return *reinterpret_cast<const __attribute__((address_space(1))) T*>(reinterpret_cast<uintptr_t>(p));
+}
 
 template <int VB, int NCH>
 __global__ __launch_bounds__(256) void seq_gather_kernel(SeqArgs a) {
   using T = typename SVec<VB>::T;
+  // The per-pool and per-feature tables are indexed with per-lane values; kept in
+  // kernel arguments, every such access would be a vector memory load, so a
+  // workgroup copies them to LDS once.
+  __shared__ const int64_t* s_ids[PDM_SEQ_MAX_POOLS * PDM_SEQ_MAX_FEATURES];
+  __shared__ const int64_t* s_off[PDM_SEQ_MAX_POOLS];
+  __shared__ const char* s_tab[PDM_SEQ_MAX_FEATURES];
+  __shared__ int64_t s_rows[PDM_SEQ_MAX_FEATURES];
+  __shared__ int64_t s_nid[PDM_SEQ_MAX_POOLS];
+  __shared__ int32_t s_fb[PDM_SEQ_MAX_FEATURES];
+  __shared__ int32_t s_fc[PDM_SEQ_MAX_FEATURES + 1];
+  __shared__ int32_t s_lmax[PDM_SEQ_MAX_POOLS];
+  __shared__ int32_t s_soff[PDM_SEQ_MAX_POOLS + 1];
+  {
+    const int i = threadIdx.x;
+    if (i < PDM_SEQ_MAX_POOLS * PDM_SEQ_MAX_FEATURES) s_ids[i] = a.ids[i];
+    if (i < PDM_SEQ_MAX_POOLS) {
+      s_off[i] = a.offsets[i];
+      s_nid[i] = a.num_ids[i];
+      s_lmax[i] = a.lmax[i];
+    }
+    if (i < PDM_SEQ_MAX_FEATURES) {
+      s_tab[i] = a.tables[i];
+      s_rows[i] = a.rows[i];
+      s_fb[i] = a.feat_bytes[i];
+    }
+    if (i < PDM_SEQ_MAX_FEATURES + 1) s_fc[i] = a.feat_col[i];
+    if (i < PDM_SEQ_MAX_POOLS + 1) s_soff[i] = a.soff[i];
+  }
+  __syncthreads();
+
   const int lane = threadIdx.x & 63;
   const int lpb = 1 << a.lpb_shift;
   const int j = lane & (lpb - 1);
@@ -60,13 +97,13 @@ __global__ __launch_bounds__(256) void seq_gather_kernel(SeqArgs a) {
   const int64_t b = tok / a.S;
   const int s = (int)(tok - b * a.S);
   int p = 0;
-  while (p + 1 < a.P && s >= a.soff[p + 1]) ++p;
-  const int pos = s - a.soff[p];
-  const int L = a.lmax[p];
-  const int64_t* off = a.offsets[p];
-  int64_t beg = off[b], end = off[b + 1];
+  while (p + 1 < a.P && s >= s_soff[p + 1]) ++p;
+  const int pos = s - s_soff[p];
+  const int L = s_lmax[p];
+  const int64_t* off = s_off[p];
+  int64_t beg = load_global<int64_t>(off + b), end = load_global<int64_t>(off + b + 1);
   bool bad = false;
-  if (beg < 0 || end < beg || end > a.num_ids[p]) {
+  if (beg < 0 || end < beg || end > s_nid[p]) {
     bad = true;
     beg = end = 0;
   }
@@ -89,16 +126,16 @@ __global__ __launch_bounds__(256) void seq_gather_kernel(SeqArgs a) {
     if (ch < a.chunks) {
       const int o = ch * VB;
       int f = 0;
-      while (f + 1 < a.F && o >= a.feat_col[f + 1]) ++f;
+      while (f + 1 < a.F && o >= s_fc[f + 1]) ++f;
       int64_t id = 0;
       bool zero = ev < 0 && a.pad_zero;
-      if (ev >= 0) id = a.ids[p * PDM_SEQ_MAX_FEATURES + f][ev];
-      if (id < 0 || id >= a.rows[f]) {
+      if (ev >= 0) id = load_global<int64_t>(s_ids[p * PDM_SEQ_MAX_FEATURES + f] + ev);
+      if (id < 0 || id >= s_rows[f]) {
         bad = true;
         zero = true;
       }
       if (!zero) {
-        v[c] = *reinterpret_cast<const T*>(a.tables[f] + id * a.feat_bytes[f] + (o - a.feat_col[f]));
+        v[c] = load_global<T>(s_tab[f] + id * s_fb[f] + (o - s_fc[f]));
         z[c] = false;
       }
     }
