@@ -9,10 +9,12 @@
 // concatenated per event (onetrans.py:515-520) and pools along the sequence
 // (onetrans.py:553-558).  The mask marks real events.
 //
-// Design: pure copy, HBM bound.  A group of `lpb` lanes owns one output
-// token; the token row (sum of feature bytes) is cut into VB-byte chunks and
-// lane j moves chunks j, j + lpb, ...  Loads of all chunks are issued before
-// the stores so each lane keeps several row reads in flight.
+// Design: pure copy, HBM bound.  A group of `lpb` lanes owns TPG consecutive
+// output tokens; a token row (sum of feature bytes) is cut into VB-byte
+// chunks and lane j moves chunks j, j + lpb, ... of each token.  Each phase's
+// loads (pool offsets, event ids, table rows) are issued for all TPG tokens
+// before the next phase, so the three dependent memory round trips are paid
+// once per TPG tokens.
 #include <algorithm>
 
 #include "pdm_common.h"
@@ -55,7 +57,11 @@ __device__ __forceinline__ T load_global(const void* p) {
   return *reinterpret_cast<const __attribute__((address_space(1))) T*>(reinterpret_cast<uintptr_t>(p));
 }
 
-template <int VB, int NCH>
+#ifndef PDM_SEQ_TOKENS_PER_GROUP
+#define PDM_SEQ_TOKENS_PER_GROUP 8
+#endif
+
+template <int VB, int NCH, int TPG>
 __global__ __launch_bounds__(256) void seq_gather_kernel(SeqArgs a) {
   using T = typename SVec<VB>::T;
   // The per-pool and per-feature tables are indexed with per-lane values; kept in
@@ -92,63 +98,85 @@ __global__ __launch_bounds__(256) void seq_gather_kernel(SeqArgs a) {
   const int lpb = 1 << a.lpb_shift;
   const int j = lane & (lpb - 1);
   const int64_t wave = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-  const int64_t tok = (wave << (6 - a.lpb_shift)) + (lane >> a.lpb_shift);
-  if (tok >= a.num_tokens) return;
-  const int64_t b = tok / a.S;
-  const int s = (int)(tok - b * a.S);
-  int p = 0;
-  while (p + 1 < a.P && s >= s_soff[p + 1]) ++p;
-  const int pos = s - s_soff[p];
-  const int L = s_lmax[p];
-  const int64_t* off = s_off[p];
-  int64_t beg = load_global<int64_t>(off + b), end = load_global<int64_t>(off + b + 1);
+  const int64_t tok0 = ((wave << (6 - a.lpb_shift)) + (lane >> a.lpb_shift)) * TPG;
+  if (tok0 >= a.num_tokens) return;  // all lanes of a group share tok0
   bool bad = false;
-  if (beg < 0 || end < beg || end > s_nid[p]) {
-    bad = true;
-    beg = end = 0;
-  }
-  const int64_t len = end - beg;
-  const int n = (int)min(len, (int64_t)L);
-  int64_t ev = -1;
-  if (!a.align_left) {
-    if (pos >= L - n) ev = end - n + (pos - (L - n));
-  } else if (pos < n) {
-    ev = end - n + pos;
-  }
-  if (j == 0 && a.mask) a.mask[tok] = ev >= 0 ? 1 : 0;
 
-  T v[NCH];
-  bool z[NCH];
+  // event of each of the group's TPG tokens (-1: padding slot) and its pool
+  int64_t ev[TPG];
+  int pool[TPG];
+  int64_t b = tok0 / a.S;
+  int s = (int)(tok0 - b * a.S);
+#pragma unroll
+  for (int i = 0; i < TPG; ++i) {
+    ev[i] = -1;
+    pool[i] = 0;
+    if (tok0 + i < a.num_tokens) {
+      int p = 0;
+      while (p + 1 < a.P && s >= s_soff[p + 1]) ++p;
+      pool[i] = p;
+      const int pos = s - s_soff[p];
+      const int L = s_lmax[p];
+      const int64_t* off = s_off[p];
+      int64_t beg = load_global<int64_t>(off + b), end = load_global<int64_t>(off + b + 1);
+      if (beg < 0 || end < beg || end > s_nid[p]) {
+        bad = true;
+        beg = end = 0;
+      }
+      const int n = (int)min(end - beg, (int64_t)L);
+      if (!a.align_left) {
+        if (pos >= L - n) ev[i] = end - n + (pos - (L - n));
+      } else if (pos < n) {
+        ev[i] = end - n + pos;
+      }
+      if (j == 0 && a.mask) a.mask[tok0 + i] = ev[i] >= 0 ? 1 : 0;
+    }
+    if (++s == a.S) {
+      s = 0;
+      ++b;
+    }
+  }
+
+  // feature, table row piece offset of each chunk this lane moves
+  int feat[NCH];
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
-    const int ch = c * lpb + j;
-    z[c] = true;
-    if (ch < a.chunks) {
-      const int o = ch * VB;
-      int f = 0;
-      while (f + 1 < a.F && o >= s_fc[f + 1]) ++f;
-      int64_t id = 0;
-      bool zero = ev < 0 && a.pad_zero;
-      if (ev >= 0) id = load_global<int64_t>(s_ids[p * PDM_SEQ_MAX_FEATURES + f] + ev);
-      if (id < 0 || id >= s_rows[f]) {
+    const int o = (c * lpb + j) * VB;
+    int f = 0;
+    while (f + 1 < a.F && o >= s_fc[f + 1]) ++f;
+    feat[c] = f;
+  }
+  int64_t id[TPG][NCH];
+#pragma unroll
+  for (int i = 0; i < TPG; ++i)
+#pragma unroll
+    for (int c = 0; c < NCH; ++c)
+      id[i][c] = (ev[i] >= 0 && c * lpb + j < a.chunks)
+                     ? load_global<int64_t>(s_ids[pool[i] * PDM_SEQ_MAX_FEATURES + feat[c]] + ev[i]) : 0;
+  T v[TPG][NCH];
+#pragma unroll
+  for (int i = 0; i < TPG; ++i)
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      const int ch = c * lpb + j;
+      v[i][c] = T{};
+      if (tok0 + i >= a.num_tokens || ch >= a.chunks) continue;
+      const int f = feat[c];
+      bool zero = ev[i] < 0 && a.pad_zero;  // padding: row 0 (ROW0) or zeros (ZERO)
+      if (id[i][c] < 0 || id[i][c] >= s_rows[f]) {
         bad = true;
         zero = true;
       }
-      if (!zero) {
-        v[c] = load_global<T>(s_tab[f] + id * s_fb[f] + (o - s_fc[f]));
-        z[c] = false;
-      }
+      if (!zero) v[i][c] = load_global<T>(s_tab[f] + id[i][c] * s_fb[f] + (ch * VB - s_fc[f]));
     }
-  }
-  char* dst = a.out + tok * a.tok_bytes;
 #pragma unroll
-  for (int c = 0; c < NCH; ++c) {
-    const int ch = c * lpb + j;
-    if (ch < a.chunks) {
-      T w;
-      if (z[c]) w = T{};
-      else w = v[c];
-      *reinterpret_cast<T*>(dst + ch * VB) = w;
+  for (int i = 0; i < TPG; ++i) {
+    if (tok0 + i >= a.num_tokens) continue;
+    char* dst = a.out + (tok0 + i) * a.tok_bytes;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      const int ch = c * lpb + j;
+      if (ch < a.chunks) *reinterpret_cast<T*>(dst + ch * VB) = v[i][c];
     }
   }
   if (bad && a.err) a.err[0] = 1;
@@ -160,14 +188,15 @@ using namespace pdm;
 
 namespace {
 using SeqFn = void (*)(SeqArgs);
+constexpr int kTpg = PDM_SEQ_TOKENS_PER_GROUP;
 template <int VB>
 SeqFn pick_seq(int nch) {
   switch (nch) {
-    case 1: return seq_gather_kernel<VB, 1>;
-    case 2: return seq_gather_kernel<VB, 2>;
-    case 3: return seq_gather_kernel<VB, 3>;
-    case 4: return seq_gather_kernel<VB, 4>;
-    case 8: return seq_gather_kernel<VB, 8>;
+    case 1: return seq_gather_kernel<VB, 1, kTpg>;
+    case 2: return seq_gather_kernel<VB, 2, kTpg>;
+    case 3: return seq_gather_kernel<VB, 3, kTpg>;
+    case 4: return seq_gather_kernel<VB, 4, kTpg>;
+    case 8: return seq_gather_kernel<VB, 8, kTpg>;
     default: return nullptr;
   }
 }
@@ -247,7 +276,7 @@ extern "C" int pdm_seq_gather_fwd(const pdm_seq_desc* desc, const void* const* t
   int sh = 0;
   while ((1 << sh) < lpb) ++sh;
   a.lpb_shift = sh;
-  const int64_t tok_per_block = 4 * (64 / lpb);
+  const int64_t tok_per_block = 4 * (64 / lpb) * kTpg;
   const int64_t blocks = (a.num_tokens + tok_per_block - 1) / tok_per_block;
   PDM_CHECK_ARG(blocks < (int64_t(1) << 31), "too many tokens for one launch");
   hipLaunchKernelGGL(fn, dim3((unsigned)blocks), dim3(256), 0, reinterpret_cast<hipStream_t>(stream), a);
