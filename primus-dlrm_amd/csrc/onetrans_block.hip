@@ -42,6 +42,8 @@ typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ f32x16_t mfma32x32x16(u32x4_t a, u32x4_t b, f32x16_t c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
@@ -54,7 +56,10 @@ __device__ __forceinline__ uint32_t bf16_bits(float v) { return __builtin_bit_ca
 
 __device__ __forceinline__ float bf16_round(float v) { return (float)(__bf16)v; }
 
-__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) { return bf16_bits(lo) | (bf16_bits(hi) << 16); }
+// two values in one conversion: lo in bits 0..15, hi in bits 16..31
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, bf16x2_t));
+}
 
 // ---------------------------------------------------------------------------
 // RMSNorm -> bf16 rows.  One wave per row, D = 64 * VPL.
@@ -815,145 +820,242 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Causal attention with K and V^T of one (sample, head) resident in LDS.
-//
-// One workgroup of 8 waves per (sample, head).  K rows and V^T rows of the
-// head are copied to LDS once; each wave then sweeps its 32-query tiles
-// (tiles w, w + 8, ...) over the key tiles up to its causal limit with no
-// further barriers.  Same math as attn_kernel: S^T = K Q^T puts a query per
-// lane, online softmax in fp32, O^T += V^T P^T with P^T in registers.  Keys
-// are stored in LDS with bits 2 and 3 of their index inside each group of
-// 16 swapped, so that the accumulator rows of S^T a lane holds for a 16-key
-// step are 8 consecutive keys: the V^T operand is then one 16-byte read.
+// Persistent attention with the keys and values of a head resident in LDS.
+// Each workgroup of 8 waves walks the (sample, head) pairs blockIdx.x,
+// blockIdx.x + gridDim.x, ...  K rows and V^T rows of a head are read from
+// memory into registers while the previous head is computed, and written to
+// LDS between two barriers, so the copy hides behind the attention math.
+// Each wave sweeps 32-query tiles over the key tiles up to its causal limit
+// with no further barriers.  Query tiles go to waves in snake order of
+// decreasing cost (the causal sweep of tile t covers t + 1 key tiles), so the
+// waves of a head finish close together.  S^T = K Q^T puts a query per lane,
+// online softmax in fp32, O^T += V^T P^T with P^T in registers.  Keys are
+// stored in LDS with bits 2 and 3 of their index inside each group of 16
+// swapped, so that the accumulator rows of S^T a lane holds for a 16-key step
+// are 8 consecutive keys: the V^T operand is then one 16-byte read.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ int swap23(int m) { return (m & ~12) | ((m & 4) << 1) | ((m & 8) >> 1); }
 
+// Largest key count held in LDS (K 128 B + V^T 128 B per key).
+constexpr int kAttnLdsMaxKeys = 608;
+
+// NP: 16-byte pieces per thread of K (and of V^T), kv_pad * 8 <= NP * 512.
+template <int NP>
 __global__ __launch_bounds__(512) void attn_lds_kernel(AttnArgs a) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
-  const int kvp = a.kv_pad;                  // keys held (multiple of 32)
+  const int kvp = a.kv_pad;                  // keys held (multiple of 32, <= kAttnLdsMaxKeys)
   char* sK = smem;                           // kvp rows x 128 bytes
   char* sV = smem + (int64_t)kvp * 128;      // 64 rows x 2*kvp bytes
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int fr = lane & 31, hf = lane >> 5;
-  const int bh = blockIdx.x;
-  const int b = bh / a.H, h = bh - (bh / a.H) * a.H;
   const int D = a.H * 64;
   const int off = a.kv - a.q_len;
+  const int BH = a.B * a.H;
 
-  // K: LDS row m holds key (m & ~15) | swap23(m & 15); piece p of a row sits at p ^ ((m >> 1) & 7)
-  for (int q = tid; q < kvp * 8; q += 512) {
-    const int m = q >> 3, p = q & 7;
-    const int key = (m & ~15) | swap23(m & 15);
-    u32x4_t v = {0, 0, 0, 0};
-    if (key < a.kv) v = *reinterpret_cast<const u32x4_t*>(a.k + ((int64_t)b * a.kv + key) * D + h * 64 + p * 8);
-    *reinterpret_cast<u32x4_t*>(sK + m * 128 + ((p ^ ((m >> 1) & 7)) << 4)) = v;
-  }
-  // V^T: row d holds keys 0..kvp-1; piece p of a row sits at p ^ ((d >> 2) & 3); keys >= kv are zero
-  const int ppr = kvp >> 3;
-  const uint16_t* vsrc = a.vt + ((int64_t)b * a.H + h) * 64 * kvp;
-  for (int q = tid; q < 64 * ppr; q += 512) {
-    const int d = q / ppr, p = q - (q / ppr) * ppr;
-    u32x4_t v = *reinterpret_cast<const u32x4_t*>(vsrc + (int64_t)d * kvp + p * 8);
-    if (p * 8 + 8 > a.kv) {
+  // Copy of one head, NP rounds of 512 16-byte pieces for K and for V^T:
+  //  K: thread t holds LDS row m = 64 i + t / 8 (key (m & ~15) | swap23(m & 15)) and piece t % 8 of it,
+  //     stored at piece position (t % 8) ^ ((m >> 1) & 7);
+  //  V^T: thread t holds row d = t / 8 and piece 8 i + t % 8 of it (keys 64 i + 8 (t % 8) ..), stored at
+  //     piece position (8 i + t % 8) ^ ((d >> 2) & 3).
+  // Every per-round address is a fixed stride from round 0's.
+  const int m0 = tid >> 3, p0 = tid & 7;
+  const int key0 = (m0 & ~15) | swap23(m0 & 15);
+  const int ppr = kvp >> 3;                  // pieces per V^T row
+  char* const sk0 = sK + m0 * 128 + ((p0 ^ ((m0 >> 1) & 7)) << 4);
+  char* const sv0 = sV + m0 * (2 * kvp) + ((p0 ^ ((m0 >> 2) & 3)) << 4);
+  // Every read below is unconditional (out-of-range pieces read an in-range address and are zeroed
+  // or skipped when stored), so that waits on the in-order memory counters never depend on a branch.
+  u32x4_t kr[NP], vr[NP];
+  auto gload = [&](int bh) {
+    const int b = bh / a.H, h = bh - (bh / a.H) * a.H;
+    const uint16_t* ksrc = a.k + (int64_t)b * a.kv * D + h * 64 + p0 * 8;
+    const uint16_t* vsrc = a.vt + ((int64_t)bh * 64 + m0) * kvp;
 #pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        const int k0 = p * 8 + 2 * w;
-        if (k0 >= a.kv) v[w] = 0u;
-        else if (k0 + 1 >= a.kv) v[w] &= 0xffffu;
+    for (int i = 0; i < NP; ++i) {
+      kr[i] = *reinterpret_cast<const u32x4_t*>(ksrc + (int64_t)min(64 * i + key0, a.kv - 1) * D);
+      vr[i] = *reinterpret_cast<const u32x4_t*>(vsrc + min(8 * i + p0, ppr - 1) * 8);
+    }
+  };
+  auto sstore = [&]() {
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+      if (64 * i + m0 < kvp)
+        *reinterpret_cast<u32x4_t*>(sk0 + 64 * i * 128) = 64 * i + key0 < a.kv ? kr[i] : u32x4_t{0, 0, 0, 0};
+      const int pv = 8 * i + p0;
+      if (pv < ppr) {
+        u32x4_t v = vr[i];
+        if (pv * 8 + 8 > a.kv) {  // V^T beyond key kv - 1 is padding the QKV GEMM never wrote
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            const int k0 = pv * 8 + 2 * w;
+            if (k0 >= a.kv) v[w] = 0u;
+            else if (k0 + 1 >= a.kv) v[w] &= 0xffffu;
+          }
+        }
+        *reinterpret_cast<u32x4_t*>(sv0 + 128 * i) = v;
       }
     }
-    *reinterpret_cast<u32x4_t*>(sV + d * (2 * kvp) + ((p ^ ((d >> 2) & 3)) << 4)) = v;
-  }
-  __syncthreads();
+  };
 
   const int ntiles = (a.q_len + 31) >> 5;
-  for (int qt = wave; qt < ntiles; qt += 8) {
-    const int qi0 = qt * 32;
-    const int qi = qi0 + fr;
-    const bool qvalid = qi < a.q_len;
-    const int p_last = qi + off;  // last key this query sees
+  // k-th tile of this wave in snake order (index into tiles sorted by decreasing cost), or -1
+  auto tile_of = [&](int k) {
+    const int idx = 8 * k + ((k & 1) ? 7 - wave : wave);
+    return idx < ntiles ? ntiles - 1 - idx : -1;
+  };
+
+  int bh = blockIdx.x;
+  gload(bh);
+  for (;;) {
+    __syncthreads();  // every wave is done with the previous head's LDS
+    sstore();
+    __syncthreads();
+    const int b = bh / a.H, h = bh - (bh / a.H) * a.H;
+    const int next = bh + (int)gridDim.x;
+    const uint16_t* qbase = a.q + (int64_t)b * a.q_len * D + h * 64 + hf * 8;
     u32x4_t qf[4];
-    const uint16_t* qrow = a.q + ((int64_t)b * a.q_len + qi) * D + h * 64 + hf * 8;
+    // rows past q_len read row q_len - 1 (their outputs are never stored)
+    auto qload = [&](int qt, u32x4_t (&f)[4]) {
+      const int qi = min(qt * 32 + fr, a.q_len - 1);
 #pragma unroll
-    for (int c = 0; c < 4; ++c) qf[c] = qvalid ? *reinterpret_cast<const u32x4_t*>(qrow + c * 16) : u32x4_t{0, 0, 0, 0};
-    const int q_last = min(qi0 + 31, a.q_len - 1);
-    const int kv_end = min(a.kv, q_last + off + 1);
+      for (int c = 0; c < 4; ++c) f[c] = *reinterpret_cast<const u32x4_t*>(qbase + (int64_t)qi * D + c * 16);
+    };
+    // One 32-query tile: S^T, online softmax and O^T over the key tiles up to its causal limit.
+    auto process_tile = [&](const int qt, const u32x4_t (&qf)[4]) {
+      const int qi0 = qt * 32;
+      const int qi = qi0 + fr;
+      const int p_last = qi + off;  // last key this query sees
+      const int q_last = min(qi0 + 31, a.q_len - 1);
+      const int kv_end = min(a.kv, q_last + off + 1);
 
-    f32x16_t o[2];
+      f32x16_t o[2];
 #pragma unroll
-    for (int e = 0; e < 16; ++e) { o[0][e] = 0.0f; o[1][e] = 0.0f; }
-    float m = -INFINITY, l = 0.0f;
+      for (int e = 0; e < 16; ++e) { o[0][e] = 0.0f; o[1][e] = 0.0f; }
+      // m: the shift of the exponentials (log2 units), shared by the two lanes of a query; l: this lane's
+      // share of the softmax denominator.  m is raised only when a score exceeds it by more than 8, so
+      // every exponential stays <= 2^8 and the rescale of O is skipped for most key tiles; the
+      // normalised output does not depend on the shift.
+      float m = -INFINITY, l = 0.0f;
+      // key j0 + 16*(e/8) + hf*8 + e%8 of element e is visible iff 16*(e/8) + e%8 <= lim - j0
+      const int lim = min(p_last, a.kv - 1) - hf * 8;
+      const char* kp = sK + fr * 128;
+      const char* vp0 = sV + fr * (2 * kvp);
+      const char* vp1 = sV + (32 + fr) * (2 * kvp);
+      int kofs[4], vofs[2];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) kofs[c] = ((2 * c + hf) ^ ((fr >> 1) & 7)) << 4;
+#pragma unroll
+      for (int c2 = 0; c2 < 2; ++c2) vofs[c2] = ((2 * c2 + hf) ^ ((fr >> 2) & 3)) << 4;  // (d >> 2) & 3, d = fr or 32 + fr
 
-    for (int j0 = 0; j0 < kv_end; j0 += 32) {
-      // S^T[key][q] = K . Q^T over the 32 LDS rows j0 .. j0+31
-      const int mrow = j0 + fr;
-      const char* krow = sK + mrow * 128;
-      f32x16_t s;
+      // K and V^T fragments of a key tile are read one tile ahead of their MFMAs
+      u32x4_t kf[4], vf[4];
+      auto kread = [&](int j0, u32x4_t (&f)[4]) {
 #pragma unroll
-      for (int e = 0; e < 16; ++e) s[e] = 0.0f;
+        for (int c = 0; c < 4; ++c) f[c] = *reinterpret_cast<const u32x4_t*>(kp + j0 * 128 + kofs[c]);
+      };
+      // O^T[d][q] += V^T . P^T; chunk c2 of P^T holds keys j0 + 16*c2 + hf*8 + 0..7, which sit in
+      // piece j0/8 + 2*c2 + hf of V^T row d, at position (j0/8) + ((2*c2 + hf) ^ ((d >> 2) & 3))
+      auto vread = [&](int j0, u32x4_t (&f)[4]) {
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const u32x4_t kf = *reinterpret_cast<const u32x4_t*>(krow + (((2 * c + hf) ^ ((mrow >> 1) & 7)) << 4));
-        s = mfma32x32x16(kf, qf[c], s);
-      }
-      // s[e] is LDS row j0 + (e/4)*8 + hf*4 + e%4, i.e. key j0 + 16*(e/8) + hf*8 + e%8
-      const bool diag = j0 + 31 > p_last || j0 + 32 > a.kv;  // some key of the tile is masked for this query
-      float mx = -INFINITY;
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        float t = s[e] * a.scale_log2;
-        if (diag) {
-          const int key = j0 + 16 * (e >> 3) + hf * 8 + (e & 7);
-          t = (key <= p_last && key < a.kv) ? t : -INFINITY;
+        for (int c2 = 0; c2 < 2; ++c2) {
+          f[2 * c2] = *reinterpret_cast<const u32x4_t*>(vp0 + j0 * 2 + vofs[c2]);
+          f[2 * c2 + 1] = *reinterpret_cast<const u32x4_t*>(vp1 + j0 * 2 + vofs[c2]);
         }
-        s[e] = t;
-        mx = fmaxf(mx, t);
-      }
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float m_new = fmaxf(m, mx);
-      const float alpha = exp2f(m - m_new);
-      m = m_new;
-      float ps = 0.0f;
-      uint32_t pk[8];
+      };
+      kread(0, kf);
+      vread(0, vf);
+      for (int j0 = 0; j0 < kv_end; j0 += 32) {
+        const int jn = j0 + 32 < kv_end ? j0 + 32 : j0;  // the last tile re-reads itself
+        // S^T[key][q] = K . Q^T over the 32 LDS rows j0 .. j0+31 (row j0 + fr: piece p at p ^ ((fr >> 1) & 7))
+        f32x16_t s;
 #pragma unroll
-      for (int e = 0; e < 16; e += 2) {
-        const float p0 = exp2f(s[e] - m_new);
-        const float p1 = exp2f(s[e + 1] - m_new);
-        ps += p0 + p1;
-        pk[e >> 1] = pack_bf16x2(p0, p1);
-      }
-      l = l * alpha + ps;
+        for (int e = 0; e < 16; ++e) s[e] = 0.0f;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) { o[0][e] *= alpha; o[1][e] *= alpha; }
-      // O^T[d][q] += V^T . P^T; chunk c2 of P^T holds keys j0 + 16*c2 + hf*8 + 0..7
+        for (int c = 0; c < 4; ++c) s = mfma32x32x16(kf[c], qf[c], s);
+        kread(jn, kf);
+        // s[e] is LDS row j0 + (e/4)*8 + hf*4 + e%4, i.e. key j0 + 16*(e/8) + hf*8 + e%8
+        if (j0 + 31 > qi0 + off || j0 + 32 > a.kv) {  // some key of the tile is masked for some query
+          const int r = lim - j0;
 #pragma unroll
-      for (int c2 = 0; c2 < 2; ++c2) {
-        const u32x4_t pb = {pk[4 * c2], pk[4 * c2 + 1], pk[4 * c2 + 2], pk[4 * c2 + 3]};
-        const int piece = (j0 >> 3) + 2 * c2 + hf;
-#pragma unroll
-        for (int db = 0; db < 2; ++db) {
-          const int d = db * 32 + fr;
-          const u32x4_t vf = *reinterpret_cast<const u32x4_t*>(sV + d * (2 * kvp) + ((piece ^ ((d >> 2) & 3)) << 4));
-          o[db] = mfma32x32x16(vf, pb, o[db]);
+          for (int e = 0; e < 16; ++e) s[e] = (16 * (e >> 3) + (e & 7) <= r) ? s[e] : -INFINITY;
         }
+        float mx = fmaxf(fmaxf(s[0], s[1]), s[2]);
+#pragma unroll
+        for (int e = 3; e < 15; e += 2) mx = fmaxf(fmaxf(mx, s[e]), s[e + 1]);
+        mx = fmaxf(mx, s[15]);
+        {  // max with the other half of the wave (lane l ^ 32 holds the same query)
+          const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+          mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+        }
+        const float mt = mx * a.scale_log2;  // tile max in log2 units (scale_log2 > 0)
+        if (__builtin_amdgcn_ballot_w64(mt > m + 8.0f)) {
+          const float m_new = fmaxf(m, mt);
+          const float alpha = __builtin_amdgcn_exp2f(m - m_new);  // 0 on the first tile (m = -inf)
+          m = m_new;
+          l *= alpha;
+#pragma unroll
+          for (int e = 0; e < 16; ++e) { o[0][e] *= alpha; o[1][e] *= alpha; }
+        }
+        float ps = 0.0f;
+        uint32_t pk[8];
+#pragma unroll
+        for (int e = 0; e < 16; e += 2) {
+          const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[e], a.scale_log2, -m));
+          const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[e + 1], a.scale_log2, -m));
+          ps += p0 + p1;
+          pk[e >> 1] = pack_bf16x2(p0, p1);
+        }
+        l += ps;
+#pragma unroll
+        for (int c2 = 0; c2 < 2; ++c2) {
+          const u32x4_t pb = {pk[4 * c2], pk[4 * c2 + 1], pk[4 * c2 + 2], pk[4 * c2 + 3]};
+          o[0] = mfma32x32x16(vf[2 * c2], pb, o[0]);
+          o[1] = mfma32x32x16(vf[2 * c2 + 1], pb, o[1]);
+        }
+        vread(jn, vf);
       }
+      {
+        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(l), __float_as_uint(l), false, false);
+        l = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+      }
+      if (qi < a.q_len) {
+        // O is written over Q: this wave has read every Q row of this tile, and no other wave reads them
+        const float inv = 1.0f / l;
+        uint16_t* orow = a.o + ((int64_t)b * a.q_len + qi) * D + h * 64;
+#pragma unroll
+        for (int db = 0; db < 2; ++db)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const int d = db * 32 + g * 8 + hf * 4;
+            u32x2_t w;
+            w[0] = pack_bf16x2(o[db][4 * g] * inv, o[db][4 * g + 1] * inv);
+            w[1] = pack_bf16x2(o[db][4 * g + 2] * inv, o[db][4 * g + 3] * inv);
+            *reinterpret_cast<u32x2_t*>(orow + d) = w;
+          }
+      }
+    };
+    // Q of a tile is read one tile ahead.  The first two tiles' Q is requested before the next
+    // head's copy, and the copy after the first tile: memory reads complete in issue order for the
+    // wait counter, so no wait for Q inside a tile also waits for the copy.
+    int qt = tile_of(0);
+    const int qt1 = tile_of(1);
+    u32x4_t qn[4];
+    qload(max(qt, 0), qf);
+    qload(qt1 >= 0 ? qt1 : max(qt, 0), qn);
+    if (qt >= 0) process_tile(qt, qf);
+    gload(next < BH ? next : bh);  // in flight while this head is computed (the last head re-reads itself)
+    qt = qt1;
+    for (int kt = 1; qt >= 0; ++kt) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) qf[c] = qn[c];
+      const int qt_next = tile_of(kt + 1);
+      qload(qt_next >= 0 ? qt_next : qt, qn);
+      process_tile(qt, qf);
+      qt = qt_next;
     }
-    l += __shfl_xor(l, 32, 64);
-    if (qvalid) {
-      const float inv = 1.0f / l;
-      uint16_t* orow = a.o + ((int64_t)b * a.q_len + qi) * D + h * 64;
-#pragma unroll
-      for (int db = 0; db < 2; ++db)
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int d = db * 32 + g * 8 + hf * 4;
-          u32x2_t w;
-          w[0] = pack_bf16x2(o[db][4 * g] * inv, o[db][4 * g + 1] * inv);
-          w[1] = pack_bf16x2(o[db][4 * g + 2] * inv, o[db][4 * g + 3] * inv);
-          *reinterpret_cast<u32x2_t*>(orow + d) = w;
-        }
-    }
+    if (next >= BH) break;
+    bh = next;
   }
 }
 
@@ -1067,22 +1169,34 @@ static int launch_rmsnorm(const float* x, int64_t x_bstride, int T, int64_t B, i
 
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
-// Largest LDS footprint of attn_lds_kernel (keys up to 608 per head); longer
-// sequences run attn_kernel, which streams K and V^T from memory.
-constexpr int64_t kAttnLdsMax = 608 * 256;
+// Largest LDS footprint of attn_lds_kernel; longer sequences run attn_kernel,
+// which streams K and V^T from memory.
+constexpr int64_t kAttnLdsMax = (int64_t)kAttnLdsMaxKeys * 256;
 
-// Allows attn_lds_kernel more than the default 64 KiB of dynamic LDS (once per process and device).
-static int attn_lds_prepare() {
+// Launches attn_lds_kernel<NP> on a persistent grid: as many workgroups as fit
+// on the device at once, each walking (sample, head) pairs.  The LDS limit is
+// raised above the default 64 KiB once per process, device and instance.
+template <int NP>
+static int launch_attn_lds(const AttnArgs& aa, int64_t lds, hipStream_t s) {
   static std::once_flag once[64];
   static hipError_t err[64];
+  static int ncu[64];
   int dev = 0;
   PDM_CHECK_HIP(hipGetDevice(&dev));
-  if (dev < 0 || dev >= 64) return PDM_OK;
+  PDM_CHECK_ARG(dev >= 0 && dev < 64, "device index out of range");
   std::call_once(once[dev], [&] {
-    err[dev] = hipFuncSetAttribute(reinterpret_cast<const void*>(attn_lds_kernel),
+    err[dev] = hipFuncSetAttribute(reinterpret_cast<const void*>(attn_lds_kernel<NP>),
                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)kAttnLdsMax);
+    if (err[dev] == hipSuccess) err[dev] = hipDeviceGetAttribute(&ncu[dev], hipDeviceAttributeMultiprocessorCount, dev);
   });
   PDM_CHECK_HIP(err[dev]);
+  int per_cu = 0;
+  PDM_CHECK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, attn_lds_kernel<NP>, 512, (size_t)lds));
+  const int64_t bh = (int64_t)aa.B * aa.H;
+  PDM_CHECK_ARG(bh < (int64_t(1) << 31), "batch * heads too large");
+  const int64_t grid = std::min<int64_t>(bh, (int64_t)std::max(ncu[dev], 1) * std::max(per_cu, 1));
+  hipLaunchKernelGGL(attn_lds_kernel<NP>, dim3((unsigned)grid), dim3(512), (unsigned)lds, s, aa);
+  PDM_CHECK_LAUNCH();
   return PDM_OK;
 }
 
@@ -1163,9 +1277,12 @@ extern "C" int pdm_onetrans_block_fwd(const pdm_block_desc* desc, const float* x
     const int64_t gy = (int64_t)B * H;
     const int64_t lds = (int64_t)L.kv_pad * 256;  // K rows (128 B) + V^T rows (2 B per key) of one head
     if (lds <= kAttnLdsMax) {
-      if ((st = attn_lds_prepare()) != PDM_OK) return st;
-      PDM_CHECK_ARG(gy < (int64_t(1) << 31), "batch * heads too large");
-      hipLaunchKernelGGL(attn_lds_kernel, dim3((unsigned)gy), dim3(512), (unsigned)lds, s, aa);
+      const int np = (L.kv_pad * 8 + 511) / 512;
+      if (np <= 2) st = launch_attn_lds<2>(aa, lds, s);
+      else if (np <= 4) st = launch_attn_lds<4>(aa, lds, s);
+      else if (np <= 7) st = launch_attn_lds<7>(aa, lds, s);
+      else st = launch_attn_lds<(kAttnLdsMaxKeys * 8 + 511) / 512>(aa, lds, s);
+      if (st != PDM_OK) return st;
     } else {
       PDM_CHECK_ARG(gy < 65536, "batch * heads must be < 65536");
       hipLaunchKernelGGL(attn_kernel, dim3((unsigned)((ql + 127) / 128), (unsigned)gy), dim3(256), 0, s, aa);
