@@ -444,77 +444,120 @@ __global__ __launch_bounds__(256, 2) void rowgemm_kernel(GemmArgs a) {
   u32x4_t af[RB][KS];
   load_row_fragments<D, RB, NORM>(a, s_rb, s_rt, wave, fr, hf, af);
 
+  // Two accumulator layouts, chosen per chunk so that every store writes 4 consecutive outputs:
+  //  rows on lanes (acc = W . A^T): lane fr holds row rb*32 + fr and columns c*32 + (e/4)*8 + hf*4 + e%4
+  //    (Q, K and the residual epilogue: outputs are row-major);
+  //  columns on lanes (acc = A . W^T): lane fr holds column c*32 + fr and rows rb*32 + (e/4)*8 + hf*4 + e%4
+  //    (V, stored transposed as V^T[b, h, d, token]: consecutive tokens are consecutive outputs).
+  // vgrp bit rb*4 + g: rows rb*32 + g*8 + hf*4 .. +3 of this wave are 4 consecutive tokens of one
+  // sample starting at a multiple of 4, so their V^T outputs form one aligned 8-byte store.
+  int vgrp = 0;
+  if constexpr (EPI == EPI_QKV) {
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int r0 = wave * RB * 32 + rb * 32 + g * 8 + hf * 4;
+        const int b0 = s_rb[r0], t0 = s_rt[r0];
+        bool ok = b0 >= 0 && (t0 & 3) == 0;
+#pragma unroll
+        for (int i = 1; i < 4; ++i) ok = ok && s_rb[r0 + i] == b0 && s_rt[r0 + i] == t0 + i;
+        vgrp |= ok ? 1 << (rb * 4 + g) : 0;
+      }
+  }
+  const int my_row = wave * RB * 32 + fr;  // + rb * 32: this lane's row in the rows-on-lanes layout
+
   for (int c = c0; c < nchunks; ++c) {
     const int buf = (c - c0) & 1;
     __syncthreads();  // chunk c is in LDS; every wave is done with chunk c - 1
     const bool more = c + 1 < nchunks;
     if (more) gload(c + 1);
-    // V columns of the QKV GEMM are computed transposed (weight rows on the
-    // accumulator rows) so that a lane holds consecutive tokens of V^T
-    const bool transposed = EPI == EPI_QKV && c * 32 >= 2 * a.D;
-    float res[RB][16];
+    const bool cols_on_lanes = EPI == EPI_QKV && c * 32 >= 2 * a.D;
+    f32x4_t res[RB][4];
     if constexpr (EPI == EPI_RESID) {
       // issue the residual loads before the MFMAs
 #pragma unroll
-      for (int rb = 0; rb < RB; ++rb)
+      for (int rb = 0; rb < RB; ++rb) {
+        const int b = s_rb[my_row + rb * 32];
+        const float* rr = a.res + (int64_t)max(b, 0) * a.res_bstride +
+                          (int64_t)(s_rt[my_row + rb * 32] + a.res_toff) * a.N + c * 32 + hf * 4;
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int row = wave * RB * 32 + rb * 32 + (e >> 2) * 8 + hf * 4 + (e & 3);
-          const int b = s_rb[row];
-          res[rb][e] = b >= 0 ? a.res[(int64_t)b * a.res_bstride + (int64_t)(s_rt[row] + a.res_toff) * a.N + c * 32 + fr]
-                              : 0.0f;
-        }
+        for (int g = 0; g < 4; ++g)
+          res[rb][g] = b >= 0 ? *reinterpret_cast<const f32x4_t*>(rr + g * 8) : f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+      }
     }
     f32x16_t acc[RB];
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[rb][e] = 0.0f;
-    if (transposed) {
-#pragma unroll
-      for (int s = 0; s < KS; ++s) {
-        const u32x4_t wf = read_w_frag<D>(sW[buf], fr, 2 * s + hf);
-#pragma unroll
-        for (int rb = 0; rb < RB; ++rb) acc[rb] = mfma32x32x16(wf, af[rb][s], acc[rb]);
-      }
-      // acc[rb][e]: weight row (e/4)*8 + hf*4 + e%4 of the chunk, token row rb*32 + fr of the wave
-      const int D_ = a.D, H = D_ >> 6;
-#pragma unroll
-      for (int rb = 0; rb < RB; ++rb) {
-        const int row = wave * RB * 32 + rb * 32 + fr;
-        const int b = s_rb[row];
-        if (b < 0) continue;
-        const int t = s_rt[row];
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int cv = c * 32 + (e >> 2) * 8 + hf * 4 + (e & 3) - 2 * D_;
-          a.vt[(((int64_t)b * H + (cv >> 6)) * 64 + (cv & 63)) * a.kv_pad + t] =
-              (uint16_t)bf16_bits(acc[rb][e]);
-        }
-      }
-    } else {
+    if (cols_on_lanes) {
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
         const u32x4_t wf = read_w_frag<D>(sW[buf], fr, 2 * s + hf);
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) acc[rb] = mfma32x32x16(af[rb][s], wf, acc[rb]);
       }
-      // acc[rb][e]: row wave*RB*32 + rb*32 + (e/4)*8 + hf*4 + e%4 of the tile, column c*32 + fr
-      const int n = c * 32 + fr;
+      // V^T[b, h, d, token]: column cv = c*32 + fr - 2D of V is head cv / 64, d = cv % 64
+      const int cv = c * 32 + fr - 2 * a.D;
+      uint16_t* vrow = a.vt + ((int64_t)(cv >> 6) * 64 + (cv & 63)) * a.kv_pad;
+      const int64_t vbs = (int64_t)(a.D >> 6) * 64 * a.kv_pad;  // per sample
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int row = wave * RB * 32 + rb * 32 + (e >> 2) * 8 + hf * 4 + (e & 3);
-          const int b = s_rb[row];
-          if (b < 0) continue;
-          if constexpr (EPI == EPI_RESID) {
-            reinterpret_cast<float*>(a.out)[(int64_t)b * a.out_bstride + (int64_t)s_rt[row] * a.N + n] =
-                bf16_round(acc[rb][e]) + res[rb][e];
+        for (int g = 0; g < 4; ++g) {
+          const int r0 = wave * RB * 32 + rb * 32 + g * 8 + hf * 4;
+          const float v[4] = {acc[rb][4 * g], acc[rb][4 * g + 1], acc[rb][4 * g + 2], acc[rb][4 * g + 3]};
+          if (vgrp & (1 << (rb * 4 + g))) {
+            *reinterpret_cast<u32x2_t*>(vrow + s_rb[r0] * vbs + s_rt[r0]) =
+                u32x2_t{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
           } else {
-            epilogue_store<EPI>(a, b, s_rt[row], n, acc[rb][e]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const int b = s_rb[r0 + i];
+              if (b >= 0) vrow[b * vbs + s_rt[r0 + i]] = (uint16_t)bf16_bits(v[i]);
+            }
           }
         }
+    } else {
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        const u32x4_t wf = read_w_frag<D>(sW[buf], fr, 2 * s + hf);
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) acc[rb] = mfma32x32x16(wf, af[rb][s], acc[rb]);
+      }
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
+        const int b = s_rb[my_row + rb * 32];
+        if (b < 0) continue;
+        const int t = s_rt[my_row + rb * 32];
+        const int col = c * 32 + hf * 4;  // + g * 8
+        if constexpr (EPI == EPI_RESID) {
+          float* o = reinterpret_cast<float*>(a.out) + (int64_t)b * a.out_bstride + (int64_t)t * a.N + col;
+#pragma unroll
+          for (int g = 0; g < 4; ++g)
+            *reinterpret_cast<f32x4_t*>(o + g * 8) =
+                f32x4_t{bf16_round(acc[rb][4 * g]) + res[rb][g].x, bf16_round(acc[rb][4 * g + 1]) + res[rb][g].y,
+                        bf16_round(acc[rb][4 * g + 2]) + res[rb][g].z, bf16_round(acc[rb][4 * g + 3]) + res[rb][g].w};
+        } else if constexpr (EPI == EPI_QKV) {
+          uint16_t* o;
+          if (col < a.D) {  // Q: kept tail tokens only
+            const int tq = t - (a.kv - a.q_len);
+            if (tq < 0) continue;
+            o = a.q + ((int64_t)b * a.q_len + tq) * a.D + col;
+          } else {
+            o = a.k + ((int64_t)b * a.kv + t) * a.D + (col - a.D);
+          }
+#pragma unroll
+          for (int g = 0; g < 4; ++g)
+            *reinterpret_cast<u32x2_t*>(o + g * 8) = u32x2_t{pack_bf16x2(acc[rb][4 * g], acc[rb][4 * g + 1]),
+                                                             pack_bf16x2(acc[rb][4 * g + 2], acc[rb][4 * g + 3])};
+        } else {
+#pragma unroll
+          for (int e = 0; e < 16; ++e)
+            epilogue_store<EPI>(a, b, t, col + (e >> 2) * 8 + (e & 3), acc[rb][e]);
+        }
+      }
     }
     if (more) sstore(buf ^ 1);
   }
