@@ -50,6 +50,20 @@ __device__ __forceinline__ f32x16_t mfma32x32x16(u32x4_t a, u32x4_t b, f32x16_t 
                                                  c, 0, 0, 0);
 }
 
+// Pins the instruction order of a fully unrolled loop of N MFMAs, each fed by
+// one LDS read: the first LEAD reads are issued up front, then one MFMA and
+// the next read alternate, so every read has LEAD MFMAs of latency slack.
+template <int N, int LEAD>
+__device__ __forceinline__ void sched_mfma_ds_pipeline() {
+  __builtin_amdgcn_sched_group_barrier(0x100, LEAD, 0);  // DS reads
+#pragma unroll
+  for (int i = 0; i < N - LEAD; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+  }
+  __builtin_amdgcn_sched_group_barrier(0x008, LEAD, 0);
+}
+
 // bf16 rounding of the block kernels: the hardware conversion (v_cvt_pk_bf16_f32,
 // round to nearest even), branch free.
 __device__ __forceinline__ uint32_t bf16_bits(float v) { return __builtin_bit_cast(uint16_t, (__bf16)v); }
@@ -115,20 +129,22 @@ __global__ __launch_bounds__(256) void rmsnorm_bf16_kernel(const float* __restri
 enum { EPI_BF16 = 0, EPI_QKV = 1, EPI_RESID = 2, EPI_GELU = 3 };
 
 // GELU with the error function, 0.5 x (1 + erf(x / sqrt 2)) (the reference's
-// exact-erf F.gelu), branch free.  erfc(|z|) follows Abramowitz & Stegun,
-// Handbook of Mathematical Functions, formula 7.1.26 (|error| <= 1.5e-7):
-// erfc(a) = t (a1 + t (a2 + t (a3 + t (a4 + t a5)))) exp(-a^2), t = 1 / (1 + p a).
-// 1 + erf(z) is 2 - erfc(z) for z >= 0 and erfc(-z) otherwise, so the
-// negative tail carries no cancellation.  After the bf16 rounding of the
-// result it agrees with the exact-erf GELU except in the far negative tail
-// (x < -3.5, |GELU| < 1e-3), where the two can differ by one bf16 step.
+// exact-erf F.gelu), branch free.  erfc(a) for a = |x| / sqrt 2 follows
+// Abramowitz & Stegun, Handbook of Mathematical Functions, formula 7.1.26
+// (|error| <= 1.5e-7): erfc(a) = t (a1 + t (a2 + t (a3 + t (a4 + t a5)))) exp(-a^2),
+// t = 1 / (1 + p a).  With e = erfc(a) / 2, GELU(x) = x - x e for x >= 0 and
+// x e = -|x| e for x < 0, i.e. max(x, 0) - |x| e in both cases, so the
+// negative tail carries no cancellation.  After the bf16 rounding of the result
+// it agrees with the exact-erf GELU except in the far negative tail (x < -3.5,
+// |GELU| < 1e-3), where the two can differ by one bf16 step.
 __device__ __forceinline__ float gelu_erf(float v) {
-  const float z = v * 0.70710678118654752f;
-  const float az = fabsf(z);
-  const float t = __builtin_amdgcn_rcpf(1.0f + 0.3275911f * az);
-  const float poly = t * (0.254829592f + t * (-0.284496736f + t * (1.421413741f + t * (-1.453152027f + t * 1.061405429f))));
-  const float e = poly * __builtin_amdgcn_exp2f(-(az * az) * 1.4426950408889634f);
-  return 0.5f * v * (z >= 0.0f ? 2.0f - e : e);
+  const float ax = fabsf(v);
+  // p / sqrt 2 with p = 0.3275911; coefficients a_i / 2
+  const float t = __builtin_amdgcn_rcpf(__builtin_fmaf(ax, 0.23164189619f, 1.0f));
+  const float poly = t * (0.127414796f + t * (-0.142248368f + t * (0.7107068705f + t * (-0.7265760135f + t * 0.5307027145f))));
+  // exp(-x^2 / 2) = 2^(-x^2 log2(e) / 2)
+  const float e = poly * __builtin_amdgcn_exp2f((v * v) * -0.72134752044448170f);
+  return __builtin_fmaf(-ax, e, fmaxf(v, 0.0f));
 }
 
 constexpr int GBM = 128, GBN = 128, GBK = 64, GPAD = 8;
@@ -388,19 +404,23 @@ __device__ __forceinline__ void load_row_fragments(const GemmArgs& a, const int*
   }
 }
 
-// Weight chunks live in LDS as rows of 2*D bytes; 16-byte piece v of row r
-// sits at position v ^ (r & 15), so the 32 lanes reading piece v of rows
-// 0..31 hit distinct banks.
+// Weight chunks live in LDS as rows of 2*D bytes padded to a stride of
+// 2*D + 16, so rows r and r + 1 start 16 bytes apart in the banks: the lanes
+// reading one 16-byte piece of 16 consecutive rows hit distinct banks, and a
+// lane's piece offsets are immediates.
+template <int D>
+constexpr int w_stride() { return 2 * D + 16; }
+
 template <int D>
 __device__ __forceinline__ u32x4_t read_w_frag(const char* lds, int r, int piece) {
-  return *reinterpret_cast<const u32x4_t*>(lds + r * (2 * D) + ((piece ^ (r & 15)) << 4));
+  return *reinterpret_cast<const u32x4_t*>(lds + r * w_stride<D>() + (piece << 4));
 }
 
 template <int D, int RB, int EPI, bool NORM>
 __global__ __launch_bounds__(256, 2) void rowgemm_kernel(GemmArgs a) {
   constexpr int KS = D / 16;
   constexpr int TROWS = 4 * RB * 32;
-  constexpr int CHUNK_BYTES = 32 * D * 2;
+  constexpr int CHUNK_BYTES = 32 * w_stride<D>();
   __shared__ __attribute__((aligned(16))) char sW[2][CHUNK_BYTES];
   __shared__ int s_rb[TROWS];
   __shared__ int s_rt[TROWS];
@@ -425,18 +445,18 @@ __global__ __launch_bounds__(256, 2) void rowgemm_kernel(GemmArgs a) {
   // loaded into registers at the top of an iteration, written to LDS at its bottom
   constexpr int CPR = D / 8;
   constexpr int WL = 32 * CPR / 256;  // 16-byte pieces per thread
+  constexpr int RPP = 256 / CPR;      // chunk rows covered by one piece round
+  const int wr0 = tid / CPR, wp0 = tid - (tid / CPR) * CPR;
   u32x4_t wr[WL];
   auto gload = [&](int c) {
 #pragma unroll
-    for (int p = 0; p < WL; ++p) {
-      const int q = p * 256 + tid;
-      const int r = q / CPR, pos = q - (q / CPR) * CPR;
-      wr[p] = *reinterpret_cast<const u32x4_t*>(W + (int64_t)(c * 32 + r) * D + (pos ^ (r & 15)) * 8);
-    }
+    for (int p = 0; p < WL; ++p)
+      wr[p] = *reinterpret_cast<const u32x4_t*>(W + (int64_t)(c * 32 + p * RPP + wr0) * D + wp0 * 8);
   };
   auto sstore = [&](int buf) {
 #pragma unroll
-    for (int p = 0; p < WL; ++p) *reinterpret_cast<u32x4_t*>(sW[buf] + (p * 256 + tid) * 16) = wr[p];
+    for (int p = 0; p < WL; ++p)
+      *reinterpret_cast<u32x4_t*>(sW[buf] + (p * RPP + wr0) * w_stride<D>() + wp0 * 16) = wr[p];
   };
   gload(c0);
   sstore(0);
@@ -566,174 +586,183 @@ __global__ __launch_bounds__(256, 2) void rowgemm_kernel(GemmArgs a) {
 // ---------------------------------------------------------------------------
 // Fused FFN:  y = z + W2 . gelu(W1 . RMSNorm2(z))  for K = d_model = D, hidden F.
 //
-// Each wave owns 32 rows.  RMSNorm2(z) rows stay in registers (same layout
-// as rowgemm's A fragments).  The hidden dimension is walked in chunks of
-// 32 units: U^T = W1_c . h^T puts hidden units on the accumulator rows and
-// token rows on the columns, so lane l holds token row l%32 and 16 hidden
-// units of it.  After GELU (fp32 on the bf16-rounded value, then bf16) those
-// values are the B operand of y^T += W2[:, c] . G^T without leaving
-// registers.  The accumulator row e/4*8 + (l/32)*4 + e%4 of a 16-unit half
-// must meet hidden unit (l/32)*8 + e%8 for the W2 operand to be one
-// contiguous 16-byte read, so LDS row r of the W1 chunk holds hidden unit
-// r with bits 2 and 3 swapped.  W1 and W2 chunks stream global -> LDS
-// directly, double buffered.  The epilogue adds z (fp32) to the
-// bf16-rounded FFN output.
+// Each of the NW waves owns RB x 32 rows; with RB = 1 and 8 waves, two waves
+// share a SIMD and one's GELU (VALU) overlaps the other's MFMAs, which the
+// hardware does not do within a wave.  RMSNorm2(z) rows stay in registers
+// (same layout as rowgemm's A fragments) and so do the D fp32 outputs of the
+// wave's rows.  The hidden dimension is walked in chunks of 32 units:
+// U^T = W1_c . h^T puts hidden units on the accumulator rows and token rows
+// on the columns, so lane l holds token row l%32 of each row block and 16
+// hidden units of it.  After GELU (fp32 on the bf16-rounded value, then bf16)
+// those values are the B operand of y^T += W2[:, c] . G^T without leaving
+// registers.  Every weight fragment read from LDS feeds RB MFMAs.  The
+// accumulator row e/4*8 + (l/32)*4 + e%4 of a 16-unit half must meet hidden
+// unit (l/32)*8 + e%8 for the W2 operand to be one contiguous 16-byte read,
+// so LDS row r of the W1 chunk holds hidden unit r with bits 2 and 3 swapped.
+// W1 and W2 chunks stream through an NST-stage LDS ring: chunk c + NST - 1 is
+// read into registers in two halves (W1 during the FFN-up MFMAs, W2 during
+// GELU and FFN-down) and written to the stage chunk c - 1 used.  The
+// epilogue adds z (fp32) to the bf16-rounded FFN output.
 // ---------------------------------------------------------------------------
-template <int D>
-__global__ __launch_bounds__(256, 1) void ffn_kernel(GemmArgs a) {
+template <int D, int RB, int NW, int NST, int WPS>
+__global__ __launch_bounds__(NW * 64, WPS) void ffn_kernel(GemmArgs a) {
+  constexpr int NT = NW * 64;                // threads
+  constexpr int PF = NST - 1;                // chunks read ahead
   constexpr int KS = D / 16;
   constexpr int DB = D / 32;                 // 32-row blocks of the output (d)
-  constexpr int W1_BYTES = 32 * D * 2;       // 32 hidden units x D
+  constexpr int TROWS = NW * RB * 32;
+  constexpr int W1_BYTES = 32 * w_stride<D>();  // 32 hidden units x D (padded rows)
   constexpr int W2_BYTES = D * 64;           // D outputs x 32 hidden units
-  constexpr int W2_PER_WAVE = D * 4 / 256;   // 64-lane copies per wave of a W2 chunk
-  constexpr int NST = 3;                     // LDS ring stages
   __shared__ __attribute__((aligned(16))) char sW1[NST][W1_BYTES];
   __shared__ __attribute__((aligned(16))) char sW2[NST][W2_BYTES];
-  __shared__ int s_rb[128];
-  __shared__ int s_rt[128];
+  __shared__ int s_rb[TROWS];
+  __shared__ int s_rt[TROWS];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int fr = lane & 31, hf = lane >> 5;
   const int mt = blockIdx.x;
-  if (tid < 128) tile_row(a, mt, 128, tid, s_rb[tid], s_rt[tid]);
+  for (int i = tid; i < TROWS; i += NT) tile_row(a, mt, TROWS, i, s_rb[i], s_rt[i]);
   const int F = a.N;
   const int64_t gsel = mt < a.tiles_s ? -1 : (mt - a.tiles_s) / a.tiles_b;
   const uint16_t* W1 = gsel < 0 ? a.W : a.W_ns + gsel * (int64_t)F * D;
   const uint16_t* W2 = gsel < 0 ? a.W2 : a.W2_ns + gsel * (int64_t)D * F;
   __syncthreads();
 
-  // Weight chunk c: W1 rows c*32 + swap23(r) (all D columns) as 32 LDS rows with
-  // 16-byte piece v of row r at v ^ (r & 15); W2[d, c*32 .. c*32+32) as D LDS
-  // rows of 64 bytes with piece v of row d at v ^ ((d >> 2) & 3).  Loaded into
-  // registers at the top of an iteration, written to LDS at its bottom, so the
-  // global latency hides behind a whole iteration of compute.
+  // Weight chunk c: W1 rows c*32 + swap23(r) (all D columns) as 32 padded LDS
+  // rows; W2[d, c*32 .. c*32+32) as D LDS rows of 64 bytes with piece v of row
+  // d at v ^ ((d >> 2) & 3).
   constexpr int CPR = D / 8;
-  constexpr int L1 = 32 * CPR / 256;  // 16-byte pieces per thread of a W1 chunk
-  constexpr int L2 = D * 4 / 256;     // and of a W2 chunk
+  constexpr int L1 = 32 * CPR / NT;   // 16-byte pieces per thread of a W1 chunk
+  constexpr int L2 = D * 4 / NT;      // and of a W2 chunk
   u32x4_t r1[L1], r2[L2];
-  auto gload = [&](int c) {
+  constexpr int RPP = NT / CPR;       // W1 chunk rows covered by one piece round
+  const int w1r0 = tid / CPR, w1p0 = tid - (tid / CPR) * CPR;
+  auto gload1 = [&](int c) {
 #pragma unroll
     for (int p = 0; p < L1; ++p) {
-      const int q = p * 256 + tid;
-      const int r = q / CPR, pos = q - (q / CPR) * CPR;
-      const int v = pos ^ (r & 15);
+      const int r = p * RPP + w1r0;
       const int hid = c * 32 + ((r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1));
-      r1[p] = *reinterpret_cast<const u32x4_t*>(W1 + (int64_t)hid * D + v * 8);
+      r1[p] = *reinterpret_cast<const u32x4_t*>(W1 + (int64_t)hid * D + w1p0 * 8);
     }
+  };
+  auto gload2 = [&](int c) {
 #pragma unroll
     for (int p = 0; p < L2; ++p) {
-      const int q = p * 256 + tid;
+      const int q = p * NT + tid;
       const int d = q >> 2, v = (q & 3) ^ ((d >> 2) & 3);
       r2[p] = *reinterpret_cast<const u32x4_t*>(W2 + (int64_t)d * F + c * 32 + v * 8);
     }
   };
-  auto sstore = [&](int buf) {
+  auto sstore1 = [&](int buf) {
 #pragma unroll
-    for (int p = 0; p < L1; ++p) *reinterpret_cast<u32x4_t*>(sW1[buf] + (p * 256 + tid) * 16) = r1[p];
+    for (int p = 0; p < L1; ++p)
+      *reinterpret_cast<u32x4_t*>(sW1[buf] + (p * RPP + w1r0) * w_stride<D>() + w1p0 * 16) = r1[p];
+  };
+  auto sstore2 = [&](int buf) {
 #pragma unroll
-    for (int p = 0; p < L2; ++p) *reinterpret_cast<u32x4_t*>(sW2[buf] + (p * 256 + tid) * 16) = r2[p];
+    for (int p = 0; p < L2; ++p) *reinterpret_cast<u32x4_t*>(sW2[buf] + (p * NT + tid) * 16) = r2[p];
   };
   const int nchunks = F / 32;
-  gload(0);
-  sstore(0);
-  if (nchunks > 1) {
-    gload(1);
-    sstore(1);
-  }
-
-  u32x4_t hfr[1][KS];
-  load_row_fragments<D, 1, true>(a, s_rb, s_rt, wave, fr, hf, hfr);
-
-  f32x16_t y[DB];
+  gload1(0); gload2(0);
+  sstore1(0); sstore2(0);
 #pragma unroll
-  for (int db = 0; db < DB; ++db)
-#pragma unroll
-    for (int e = 0; e < 16; ++e) y[db][e] = 0.0f;
-
-  // Software pipeline: iteration c issues the FFN-up MFMAs of chunk c + 1
-  // interleaved with the GELU of chunk c (VALU work overlapping the matrix
-  // cores), then the FFN-down MFMAs of chunk c.  Chunks c and c + 1 are
-  // resident in the ring; chunk c + 2 is loaded during the iteration and
-  // written to the stage chunk c - 1 used.
-  constexpr int GPS = 16 / KS;  // GELU evaluations per k step
-  auto up = [&](const char* w1, int s, f32x16_t acc) { return mfma32x32x16(read_w_frag<D>(w1, fr, 2 * s + hf), hfr[0][s], acc); };
-  auto down = [&](const char* w2, const uint32_t (&gp)[8]) {
-    u32x4_t w2f[2][DB];
-#pragma unroll
-    for (int c2 = 0; c2 < 2; ++c2)
-#pragma unroll
-      for (int db = 0; db < DB; ++db) {
-        const int d = db * 32 + fr;
-        w2f[c2][db] = *reinterpret_cast<const u32x4_t*>(w2 + d * 64 + (((2 * c2 + hf) ^ ((d >> 2) & 3)) << 4));
-      }
-#pragma unroll
-    for (int c2 = 0; c2 < 2; ++c2) {
-      const u32x4_t gb = {gp[4 * c2], gp[4 * c2 + 1], gp[4 * c2 + 2], gp[4 * c2 + 3]};
-#pragma unroll
-      for (int db = 0; db < DB; ++db) y[db] = mfma32x32x16(w2f[c2][db], gb, y[db]);
+  for (int c = 1; c < PF; ++c)
+    if (c < nchunks) {
+      gload1(c); gload2(c);
+      sstore1(c); sstore2(c);
     }
-  };
 
-  __syncthreads();
-  f32x16_t u;
-#pragma unroll
-  for (int e = 0; e < 16; ++e) u[e] = 0.0f;
-#pragma unroll
-  for (int s = 0; s < KS; ++s) u = up(sW1[0], s, u);
+  u32x4_t hfr[RB][KS];
+  load_row_fragments<D, RB, true>(a, s_rb, s_rt, wave, fr, hf, hfr);
 
-  for (int c = 0; c + 1 < nchunks; ++c) {
-    // chunk c + 1 is in LDS, and every wave is done with chunk c - 1, whose stage receives chunk c + 2
+  f32x16_t y[RB][DB];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) y[rb][db][e] = 0.0f;
+
+  for (int c = 0; c < nchunks; ++c) {
+    // chunks c .. c + PF - 1 are in LDS, and every wave is done with chunk c - 1, whose stage receives chunk c + PF
     __syncthreads();
-    const bool more = c + 2 < nchunks;
-    if (more) gload(c + 2);
-    const char* w1n = sW1[(c + 1) % NST];
-    u32x4_t w1f[KS];
+    const bool more = c + PF < nchunks;
+    const int st = c % NST, st2 = (c + PF) % NST;
+    if (more) gload1(c + PF);
+    // FFN-up: U^T[rb] = W1_c . h[rb]^T, each W1 fragment feeding RB MFMAs
+    const char* w1 = sW1[st];
+    f32x16_t u[RB];
 #pragma unroll
-    for (int s = 0; s < KS; ++s) w1f[s] = read_w_frag<D>(w1n, fr, 2 * s + hf);
-    f32x16_t un;
+    for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-    for (int e = 0; e < 16; ++e) un[e] = 0.0f;
-    uint32_t gp[8];
+      for (int e = 0; e < 16; ++e) u[rb][e] = 0.0f;
+    {
+      u32x4_t wf[KS];
 #pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      un = mfma32x32x16(w1f[s], hfr[0][s], un);
+      for (int s = 0; s < KS; ++s) wf[s] = read_w_frag<D>(w1, fr, 2 * s + hf);
 #pragma unroll
-      for (int q = 0; q < GPS; ++q) {
-        const int e = s * GPS + q;  // G = bf16(gelu(bf16(U))): u[e] is hidden (e/4)*8 + hf*4 + e%4
-        const uint32_t gbits = bf16_bits(gelu_erf(bf16_round(u[e])));
-        if (e & 1) gp[e >> 1] |= gbits << 16;
-        else gp[e >> 1] = gbits;
-      }
+      for (int s = 0; s < KS; ++s)
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) u[rb] = mfma32x32x16(wf[s], hfr[rb][s], u[rb]);
+      if constexpr (RB == 1) sched_mfma_ds_pipeline<KS, 4>();
     }
-    down(sW2[c % NST], gp);
-    u = un;
-    if (more) sstore((c + 2) % NST);
-  }
-  {
-    uint32_t gp[8];
+    if (more) {
+      sstore1(st2);
+      gload2(c + PF);
+    }
+    // G = bf16(gelu(bf16(U))): u[rb][e] is hidden unit (e/4)*8 + hf*4 + e%4 (LDS row order) of token fr
+    uint32_t gp[RB][8];
 #pragma unroll
-    for (int e = 0; e < 16; e += 2) gp[e >> 1] = pack_bf16x2(gelu_erf(bf16_round(u[e])), gelu_erf(bf16_round(u[e + 1])));
-    down(sW2[(nchunks - 1) % NST], gp);
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+      for (int e = 0; e < 16; e += 2)
+        gp[rb][e >> 1] = pack_bf16x2(gelu_erf(bf16_round(u[rb][e])), gelu_erf(bf16_round(u[rb][e + 1])));
+    // FFN-down: y^T[rb][db] += W2[db rows, chunk c] . G[rb]^T; chunk c2 of G^T holds hidden units
+    // 16*c2 + hf*8 + 0..7, piece 2*c2 + hf of W2 row d, stored at (2*c2 + hf) ^ ((d >> 2) & 3)
+    const char* w2 = sW2[st];
+    {
+      // (d >> 2) & 3 = (fr >> 2) & 3 for d = db*32 + fr
+      u32x4_t wf[DB * 2];
+#pragma unroll
+      for (int c2 = 0; c2 < 2; ++c2)
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+          wf[c2 * DB + db] = *reinterpret_cast<const u32x4_t*>(w2 + (db * 32 + fr) * 64 + (((2 * c2 + hf) ^ ((fr >> 2) & 3)) << 4));
+#pragma unroll
+      for (int c2 = 0; c2 < 2; ++c2)
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+          for (int rb = 0; rb < RB; ++rb) {
+            const u32x4_t gb = {gp[rb][4 * c2], gp[rb][4 * c2 + 1], gp[rb][4 * c2 + 2], gp[rb][4 * c2 + 3]};
+            y[rb][db] = mfma32x32x16(wf[c2 * DB + db], gb, y[rb][db]);
+          }
+      if constexpr (RB == 1) sched_mfma_ds_pipeline<DB * 2, 4>();
+    }
+    if (more) sstore2(st2);
   }
 
-  // y[db][e] is output d = db*32 + (e/4)*8 + hf*4 + e%4 of this lane's row
-  const int row = wave * 32 + fr;
-  const int b = s_rb[row];
-  if (b < 0) return;
-  const int64_t off = (int64_t)b * a.out_bstride + (int64_t)s_rt[row] * D;
-  float* out = reinterpret_cast<float*>(a.out) + off;
-  const float* zr = a.res + off;
+  // y[rb][db][e] is output d = db*32 + (e/4)*8 + hf*4 + e%4 of row wave*RB*32 + rb*32 + fr
 #pragma unroll
-  for (int db = 0; db < DB; ++db)
+  for (int rb = 0; rb < RB; ++rb) {
+    const int row = wave * RB * 32 + rb * 32 + fr;
+    const int b = s_rb[row];
+    if (b < 0) continue;
+    const int64_t off = (int64_t)b * a.out_bstride + (int64_t)s_rt[row] * D;
+    float* out = reinterpret_cast<float*>(a.out) + off;
+    const float* zr = a.res + off;
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int d = db * 32 + g * 8 + hf * 4;
-      const f32x4_t z = *reinterpret_cast<const f32x4_t*>(zr + d);
-      *reinterpret_cast<f32x4_t*>(out + d) =
-          f32x4_t{z.x + bf16_round(y[db][4 * g]), z.y + bf16_round(y[db][4 * g + 1]),
-                  z.z + bf16_round(y[db][4 * g + 2]), z.w + bf16_round(y[db][4 * g + 3])};
-    }
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d = db * 32 + g * 8 + hf * 4;
+        const f32x4_t z = *reinterpret_cast<const f32x4_t*>(zr + d);
+        *reinterpret_cast<f32x4_t*>(out + d) =
+            f32x4_t{z.x + bf16_round(y[rb][db][4 * g]), z.y + bf16_round(y[rb][db][4 * g + 1]),
+                    z.z + bf16_round(y[rb][db][4 * g + 2]), z.w + bf16_round(y[rb][db][4 * g + 3])};
+      }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -1184,12 +1213,28 @@ static int launch_rowgemm(GemmArgs& g, int D, hipStream_t s) {
   return PDM_OK;
 }
 
+// FFN launch shape: RB * 32 rows per wave, NW waves per workgroup, an NST-stage
+// weight ring, WPS workgroups per CU.  Eight waves of 32 rows (two per SIMD:
+// one wave's GELU runs beside the other's MFMAs) measured fastest at d_model 256.
+#ifndef PDM_FFN_RB
+#define PDM_FFN_RB 1
+#endif
+#ifndef PDM_FFN_NW
+#define PDM_FFN_NW 8
+#endif
+#ifndef PDM_FFN_NST
+#define PDM_FFN_NST 3
+#endif
+#ifndef PDM_FFN_WPS
+#define PDM_FFN_WPS 1
+#endif
 static int launch_ffn(GemmArgs& g, int D, hipStream_t s) {
-  const int64_t tiles = row_tiles(g, 128);
+  constexpr int RB = PDM_FFN_RB, NW = PDM_FFN_NW, NST = PDM_FFN_NST, WPS = PDM_FFN_WPS;
+  const int64_t tiles = row_tiles(g, NW * RB * 32);
   if (tiles == 0) return PDM_OK;
   PDM_CHECK_ARG(tiles < (int64_t(1) << 31), "FFN grid too large");
-  if (D == 256) hipLaunchKernelGGL(ffn_kernel<256>, dim3((unsigned)tiles), dim3(256), 0, s, g);
-  else hipLaunchKernelGGL(ffn_kernel<128>, dim3((unsigned)tiles), dim3(256), 0, s, g);
+  if (D == 256) hipLaunchKernelGGL((ffn_kernel<256, RB, NW, NST, WPS>), dim3((unsigned)tiles), dim3(NW * 64), 0, s, g);
+  else hipLaunchKernelGGL((ffn_kernel<128, RB, NW, NST, WPS>), dim3((unsigned)tiles), dim3(NW * 64), 0, s, g);
   PDM_CHECK_LAUNCH();
   return PDM_OK;
 }
