@@ -107,34 +107,57 @@ __global__ __launch_bounds__(256) void seq_gather_kernel(SeqArgs a) {
   int pool[TPG];
   int64_t b = tok0 / a.S;
   int s = (int)(tok0 - b * a.S);
+  int p0 = 0;
+  while (p0 + 1 < a.P && s >= s_soff[p0 + 1]) ++p0;
+  // slot s of sample b at position pos of pool p holds event end - n + (pos - (L - n)) (right aligned)
+  // or end - n + pos (left aligned) when that position is filled
+  auto event_of = [&](int64_t beg, int64_t end, int p, int pos) -> int64_t {
+    const int L = s_lmax[p];
+    const int n = (int)min(end - beg, (int64_t)L);
+    if (!a.align_left) return pos >= L - n ? end - n + (pos - (L - n)) : -1;
+    return pos < n ? end - n + pos : -1;
+  };
+  if (tok0 + TPG <= a.num_tokens && s - s_soff[p0] + TPG <= s_lmax[p0]) {
+    // all TPG tokens are slots of one pool of one sample: one pair of offsets
+    const int64_t* off = s_off[p0];
+    int64_t beg = load_global<int64_t>(off + b), end = load_global<int64_t>(off + b + 1);
+    if (beg < 0 || end < beg || end > s_nid[p0]) {
+      bad = true;
+      beg = end = 0;
+    }
 #pragma unroll
-  for (int i = 0; i < TPG; ++i) {
-    ev[i] = -1;
-    pool[i] = 0;
-    if (tok0 + i < a.num_tokens) {
-      int p = 0;
-      while (p + 1 < a.P && s >= s_soff[p + 1]) ++p;
-      pool[i] = p;
-      const int pos = s - s_soff[p];
-      const int L = s_lmax[p];
-      const int64_t* off = s_off[p];
-      int64_t beg = load_global<int64_t>(off + b), end = load_global<int64_t>(off + b + 1);
-      if (beg < 0 || end < beg || end > s_nid[p]) {
-        bad = true;
-        beg = end = 0;
-      }
-      const int n = (int)min(end - beg, (int64_t)L);
-      if (!a.align_left) {
-        if (pos >= L - n) ev[i] = end - n + (pos - (L - n));
-      } else if (pos < n) {
-        ev[i] = end - n + pos;
-      }
-      if (j == 0 && a.mask) a.mask[tok0 + i] = ev[i] >= 0 ? 1 : 0;
+    for (int i = 0; i < TPG; ++i) {
+      pool[i] = p0;
+      ev[i] = event_of(beg, end, p0, s - s_soff[p0] + i);
     }
-    if (++s == a.S) {
-      s = 0;
-      ++b;
+  } else {
+#pragma unroll
+    for (int i = 0; i < TPG; ++i) {
+      ev[i] = -1;
+      pool[i] = 0;
+      if (tok0 + i < a.num_tokens) {
+        int p = 0;
+        while (p + 1 < a.P && s >= s_soff[p + 1]) ++p;
+        pool[i] = p;
+        const int64_t* off = s_off[p];
+        int64_t beg = load_global<int64_t>(off + b), end = load_global<int64_t>(off + b + 1);
+        if (beg < 0 || end < beg || end > s_nid[p]) {
+          bad = true;
+          beg = end = 0;
+        }
+        ev[i] = event_of(beg, end, p, s - s_soff[p]);
+      }
+      if (++s == a.S) {
+        s = 0;
+        ++b;
+      }
     }
+  }
+  // mask byte of token i written by lane i % lpb of the group
+  if (a.mask) {
+#pragma unroll
+    for (int i = 0; i < TPG; ++i)
+      if (j == (i & (lpb - 1)) && tok0 + i < a.num_tokens) a.mask[tok0 + i] = ev[i] >= 0 ? 1 : 0;
   }
 
   // feature, table row piece offset of each chunk this lane moves
@@ -146,13 +169,19 @@ __global__ __launch_bounds__(256) void seq_gather_kernel(SeqArgs a) {
     while (f + 1 < a.F && o >= s_fc[f + 1]) ++f;
     feat[c] = f;
   }
+  // id of each (token, chunk); chunks of one feature share the id, which is read once
   int64_t id[TPG][NCH];
 #pragma unroll
   for (int i = 0; i < TPG; ++i)
 #pragma unroll
-    for (int c = 0; c < NCH; ++c)
-      id[i][c] = (ev[i] >= 0 && c * lpb + j < a.chunks)
-                     ? load_global<int64_t>(s_ids[pool[i] * PDM_SEQ_MAX_FEATURES + feat[c]] + ev[i]) : 0;
+    for (int c = 0; c < NCH; ++c) {
+      if (c > 0 && feat[c] == feat[c - 1]) {
+        id[i][c] = id[i][c - 1];
+      } else {
+        id[i][c] = (ev[i] >= 0 && c * lpb + j < a.chunks)
+                       ? load_global<int64_t>(s_ids[pool[i] * PDM_SEQ_MAX_FEATURES + feat[c]] + ev[i]) : 0;
+      }
+    }
   T v[TPG][NCH];
 #pragma unroll
   for (int i = 0; i < TPG; ++i)
@@ -169,6 +198,8 @@ __global__ __launch_bounds__(256) void seq_gather_kernel(SeqArgs a) {
       }
       if (!zero) v[i][c] = load_global<T>(s_tab[f] + id[i][c] * s_fb[f] + (ch * VB - s_fc[f]));
     }
+  // token rows are written once: non-temporal stores stream them to memory without allocating in the
+  // caches (1.5x the store bandwidth of cached stores here)
 #pragma unroll
   for (int i = 0; i < TPG; ++i) {
     if (tok0 + i >= a.num_tokens) continue;
@@ -176,7 +207,7 @@ __global__ __launch_bounds__(256) void seq_gather_kernel(SeqArgs a) {
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
       const int ch = c * lpb + j;
-      if (ch < a.chunks) *reinterpret_cast<T*>(dst + ch * VB) = v[i][c];
+      if (ch < a.chunks) __builtin_nontemporal_store(v[i][c], reinterpret_cast<T*>(dst + ch * VB));
     }
   }
   if (bad && a.err) a.err[0] = 1;
