@@ -1107,24 +1107,25 @@ __global__ __launch_bounds__(512) void attn_lds_kernel(AttnArgs a) {
           }
       }
     };
-    // Q of a tile is read one tile ahead.  The first two tiles' Q is requested before the next
-    // head's copy, and the copy after the first tile: memory reads complete in issue order for the
-    // wait counter, so no wait for Q inside a tile also waits for the copy.
-    int qt = tile_of(0);
-    const int qt1 = tile_of(1);
+    // A wave's first two tiles (all of them while q_len <= 512) have their Q requested before the next
+    // head's copy, which then overlaps the whole head: memory reads complete in issue order for the
+    // wait counter, so waiting for Q does not wait for the copy.  The code is straight-line up to the
+    // second tile so that the compiler's waits count exactly; scheduling barriers keep the issue order.
+    const int qt0 = tile_of(0), qt1 = tile_of(1);
     u32x4_t qn[4];
-    qload(max(qt, 0), qf);
-    qload(qt1 >= 0 ? qt1 : max(qt, 0), qn);
-    if (qt >= 0) process_tile(qt, qf);
+    qload(max(qt0, 0), qf);
+    qload(qt1 >= 0 ? qt1 : max(qt0, 0), qn);
+    __builtin_amdgcn_sched_barrier(0);
     gload(next < BH ? next : bh);  // in flight while this head is computed (the last head re-reads itself)
-    qt = qt1;
-    for (int kt = 1; qt >= 0; ++kt) {
-#pragma unroll
-      for (int c = 0; c < 4; ++c) qf[c] = qn[c];
-      const int qt_next = tile_of(kt + 1);
-      qload(qt_next >= 0 ? qt_next : qt, qn);
+    __builtin_amdgcn_sched_barrier(0);
+    if (qt0 >= 0) process_tile(qt0, qf);
+    if (qt1 >= 0) process_tile(qt1, qn);
+    // tiles past the second (q_len > 512): Q read at the start of the tile
+    for (int kt = 2;; ++kt) {
+      const int qt = tile_of(kt);
+      if (qt < 0) break;
+      qload(qt, qf);
       process_tile(qt, qf);
-      qt = qt_next;
     }
     if (next >= BH) break;
     bh = next;
