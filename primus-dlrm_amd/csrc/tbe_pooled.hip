@@ -40,7 +40,7 @@ struct TbeArgs {
   const void* indices;
   const int64_t* offsets;
   const TbeMeta* meta;
-  const int32_t* group_tables;
+  const int32_t* group_tables;  // tables of this launch, in group order
   void* out;
   int32_t* err;
   int64_t num_indices;
@@ -54,6 +54,7 @@ struct TbeArgs {
   int32_t payload_vecs;  // payload bytes / VB
   int32_t out_vec_ok;    // output rows aligned for vector stores
   int32_t index_bits;
+  int32_t table_base;  // >= 0: the launch's tables are table_base, table_base + 1, ... (no table list read)
 };
 
 // Loads VB bytes from a 4-byte aligned address (rows are only guaranteed
@@ -229,7 +230,7 @@ __global__ __launch_bounds__(256) void tbe_pooled_kernel(TbeArgs a) {
   const int64_t tl = grp / a.chunks_per_table;
   const int64_t b0 = (grp - tl * a.chunks_per_table) * R;
   const int nb = (int)min((int64_t)R, a.B - b0);
-  const int t = a.group_tables[tl];
+  const int t = a.table_base >= 0 ? a.table_base + (int)tl : a.group_tables[tl];
   const TbeMeta m = a.meta[t];
   const int64_t bag0 = (int64_t)t * a.B + b0;
   const char* wbase = a.weights + m.w_off + (WT == PDM_I8_SB_F16 ? 4 : 0);
@@ -412,7 +413,7 @@ __global__ __launch_bounds__(256) void tbe_short_kernel(TbeArgs a) {
   const int64_t tl = grp / a.chunks_per_table;
   const int64_t b0 = (grp - tl * a.chunks_per_table) * LPB;
   const int nb = (int)min((int64_t)LPB, a.B - b0);
-  const int t = a.group_tables[tl];
+  const int t = a.table_base >= 0 ? a.table_base + (int)tl : a.group_tables[tl];
   const TbeMeta m = a.meta[t];
   const int64_t bag0 = (int64_t)t * a.B + b0;
   const char* wbase = a.weights + m.w_off + (WT == PDM_I8_SB_F16 ? 4 : 0);
@@ -599,6 +600,7 @@ struct TbeGroup {
   int32_t first;          // index into the grouped table list
   int32_t count;
   int32_t out_col_align;    // alignment (elements) of all out_offsets
+  int32_t table_base;       // first table if the group's tables are consecutive, else -1
 };
 
 struct pdm_tbe_plan_s {
@@ -659,10 +661,11 @@ extern "C" int pdm_tbe_plan_create(const pdm_table_desc* tables, int32_t num_tab
     for (auto& g : plan->groups)
       if (g.dtype == d.dtype && g.dim == d.dim) found = true;
     if (found) continue;
-    TbeGroup g{d.dtype, d.dim, d.row_bytes, (int32_t)order.size(), 0, 1 << 20};
+    TbeGroup g{d.dtype, d.dim, d.row_bytes, (int32_t)order.size(), 0, 1 << 20, t};
     for (int u = t; u < num_tables; ++u) {
       const auto& e = plan->tables[u];
       if (e.dtype != d.dtype || e.dim != d.dim) continue;
+      if (u != t + g.count) g.table_base = -1;
       order.push_back(u);
       ++g.count;
       if (e.row_bytes != g.row_bytes_all) g.row_bytes_all = -1;
@@ -879,6 +882,7 @@ extern "C" int pdm_tbe_pooled_fwd(pdm_tbe_plan plan, const void* weights, const 
     a.offsets = offsets;
     a.meta = plan->d_meta;
     a.group_tables = plan->d_group_tables + g.first;
+    a.table_base = g.table_base;
     a.out = out;
     a.err = err_flag;
     a.num_indices = num_indices;
