@@ -613,8 +613,11 @@ __global__ __launch_bounds__(NW * 64, WPS) void ffn_kernel(GemmArgs a) {
   constexpr int TROWS = NW * RB * 32;
   constexpr int W1_BYTES = 32 * w_stride<D>();  // 32 hidden units x D (padded rows)
   constexpr int W2_BYTES = D * 64;           // D outputs x 32 hidden units
-  __shared__ __attribute__((aligned(16))) char sW1[NST][W1_BYTES];
-  __shared__ __attribute__((aligned(16))) char sW2[NST][W2_BYTES];
+  // one LDS block: the weight ring, reused by the epilogue's staging tile
+  constexpr int RING_BYTES = NST * (W1_BYTES + W2_BYTES);
+  __shared__ __attribute__((aligned(16))) char sRing[RING_BYTES];
+  char (*sW1)[W1_BYTES] = reinterpret_cast<char (*)[W1_BYTES]>(sRing);
+  char (*sW2)[W2_BYTES] = reinterpret_cast<char (*)[W2_BYTES]>(sRing + NST * W1_BYTES);
   __shared__ int s_rb[TROWS];
   __shared__ int s_rt[TROWS];
 
@@ -743,25 +746,42 @@ __global__ __launch_bounds__(NW * 64, WPS) void ffn_kernel(GemmArgs a) {
     if (more) sstore2(st2);
   }
 
-  // y[rb][db][e] is output d = db*32 + (e/4)*8 + hf*4 + e%4 of row wave*RB*32 + rb*32 + fr
+  // Epilogue y = z + bf16(FFN).  y[rb][db][e] is output d = db*32 + (e/4)*8 + hf*4 + e%4 of row
+  // wave*RB*32 + rb*32 + fr.  The values go through LDS (the weight ring is free now) SEG outputs at a
+  // time, so that z is read and y written as whole row segments of SEG outputs, with
+  // non-temporal stores (y is streamed to memory; the next kernel reads it from there).
+  __syncthreads();
+  constexpr int SEG = NW * RB * 32 * (64 * 4 + 16) <= RING_BYTES ? 64 : 32;  // outputs per pass
+  constexpr int SROW = SEG * 4 + 16;       // LDS row stride (bytes), padded against bank conflicts
+  static_assert(NW * RB * 32 * SROW <= RING_BYTES, "epilogue staging must fit the weight ring");
+  char* stage = sRing + wave * (RB * 32 * SROW);
 #pragma unroll
-  for (int rb = 0; rb < RB; ++rb) {
-    const int row = wave * RB * 32 + rb * 32 + fr;
-    const int b = s_rb[row];
-    if (b < 0) continue;
-    const int64_t off = (int64_t)b * a.out_bstride + (int64_t)s_rt[row] * D;
-    float* out = reinterpret_cast<float*>(a.out) + off;
-    const float* zr = a.res + off;
+  for (int q = 0; q < D / SEG; ++q) {
 #pragma unroll
-    for (int db = 0; db < DB; ++db)
+    for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int d = db * 32 + g * 8 + hf * 4;
-        const f32x4_t z = *reinterpret_cast<const f32x4_t*>(zr + d);
-        *reinterpret_cast<f32x4_t*>(out + d) =
-            f32x4_t{z.x + bf16_round(y[rb][db][4 * g]), z.y + bf16_round(y[rb][db][4 * g + 1]),
-                    z.z + bf16_round(y[rb][db][4 * g + 2]), z.w + bf16_round(y[rb][db][4 * g + 3])};
+      for (int db2 = 0; db2 < SEG / 32; ++db2) {
+        const int db = q * (SEG / 32) + db2;
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          *reinterpret_cast<f32x4_t*>(stage + (rb * 32 + fr) * SROW + (db2 * 32 + g * 8 + hf * 4) * 4) =
+              f32x4_t{bf16_round(y[rb][db][4 * g]), bf16_round(y[rb][db][4 * g + 1]),
+                      bf16_round(y[rb][db][4 * g + 2]), bf16_round(y[rb][db][4 * g + 3])};
       }
+    // each wave reads back only its own tile; a wave's LDS accesses execute in order, so no barrier
+#pragma unroll
+    for (int k = 0; k < RB * 32 * (SEG / 4) / 64; ++k) {
+      const int piece = k * 64 + lane;     // 16-byte piece of the wave's RB*32 x SEG tile
+      const int r = piece / (SEG / 4), c4 = piece - (piece / (SEG / 4)) * (SEG / 4);
+      const int row = wave * RB * 32 + r;
+      const int b = s_rb[row];
+      if (b < 0) continue;
+      const int64_t off = (int64_t)b * a.out_bstride + (int64_t)s_rt[row] * D + q * SEG + c4 * 4;
+      const f32x4_t z = *reinterpret_cast<const f32x4_t*>(a.res + off);
+      const f32x4_t v = *reinterpret_cast<const f32x4_t*>(stage + r * SROW + c4 * 16);
+      __builtin_nontemporal_store(f32x4_t{z.x + v.x, z.y + v.y, z.z + v.z, z.w + v.w},
+                                  reinterpret_cast<f32x4_t*>(reinterpret_cast<float*>(a.out) + off));
+    }
   }
 }
 
