@@ -1224,7 +1224,10 @@ static int64_t row_tiles(GemmArgs& g, int rows_per_tile) {
 template <int EPI, bool NORM>
 static int launch_rowgemm(GemmArgs& g, int D, hipStream_t s) {
   // the residual epilogue keeps 16 loaded residual values per row block in registers: one row block per wave
-  constexpr int RB = EPI == EPI_RESID ? 1 : 2;
+#ifndef PDM_QKV_RB
+#define PDM_QKV_RB 1
+#endif
+  constexpr int RB = EPI == EPI_RESID ? 1 : PDM_QKV_RB;
   const int64_t tiles = row_tiles(g, 4 * RB * 32);
   if (tiles == 0) return PDM_OK;
   PDM_CHECK_ARG(tiles < (int64_t(1) << 31), "GEMM grid too large");
