@@ -9,6 +9,7 @@ fp32 out).  ``--workload`` selects another:
   int8_mean   64 tables x 5,000,000 x 128 int8 rowwise, mean, Poisson(20) bags, B=16,384, fp16 out
   seq_gather  3 behaviour pools, item 10M x 256 + artist 1M x 64 + album 2M x 64 bf16, B=1024
   onetrans    4-layer OneTrans block stack, B=1024, 384 S + 16 NS tokens, d 256, schedule 384/256/128/64
+  cross_hash  cross-feature ids: xxHash64 of (uid, artist_id) int64 pairs % 100,000,000, 16,777,216 rows
   copy_1gib   calibration only: a 1 GiB device-to-device copy (the HBM counters' reference kernel)
 
 A step is one forward of the path over one batch already resident in HBM.
@@ -267,7 +268,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="single_hot",
-                    choices=["single_hot", "ebc_fp32", "int8_mean", "seq_gather", "onetrans", "copy_1gib"])
+                    choices=["single_hot", "ebc_fp32", "int8_mean", "seq_gather", "onetrans", "cross_hash",
+                             "copy_1gib"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
 
@@ -320,6 +322,27 @@ def main() -> int:
             return {"value": round(kept / sec, 1), "unit": unit, "cores": 1, "kind": "port",
                     "sample": f"C oracle (one thread), full batch of {kept} kept events, item table capped at "
                               f"1,000,000 rows (ids taken modulo), median of 5 reps = {sec:.3f} s"}
+    elif args.workload == "cross_hash":
+        # user_x_artist cross ids (config.py:151): one (uid, artist_id) pair per row, 100M buckets, salt 0
+        n_rows, table_size = 1 << 24, 100_000_000
+        rng = np.random.default_rng(1006)
+        uid = rng.integers(0, 1_000_000, n_rows, dtype=np.int64)
+        artist = rng.integers(0, 1_290_000, n_rows, dtype=np.int64)
+        keys = [torch.from_numpy(uid).to(dev), torch.from_numpy(artist).to(dev)]
+        out = torch.empty(n_rows, dtype=torch.int64, device=dev)
+        keep = (keys, out)
+
+        def step():
+            pdm.ops.cross_hash_raw(keys, table_size, 0, out=out)
+
+        alg, units, unit, bound, dtype = n_rows * 24, n_rows, "hashes/s", "hbm", "int64"
+        cfg = {"workload": "cross_hash_uid_x_artist_16m", "rows": n_rows, "keys": 2, "table_size": table_size,
+               "salt": 0}
+
+        def cpu_fn():
+            sec = time_cpu(lambda: orc.cross_hash([uid, artist], table_size, 0))
+            return {"value": round(n_rows / sec, 1), "unit": unit, "cores": threads, "kind": "port",
+                    "sample": f"C oracle (XXH64 per row, OpenMP), all {n_rows} rows, median of 5 reps = {sec:.3f} s"}
     elif args.workload == "copy_1gib":
         # calibration: a plain device copy of 1 GiB (reads 1 GiB, writes 1 GiB) for the HBM counters
         src = torch.ones(1 << 28, dtype=torch.float32, device=dev)

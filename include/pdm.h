@@ -168,10 +168,10 @@ int pdm_seq_gather_fwd(const pdm_seq_desc* desc, const void* const* tables,
 
 typedef struct {
   int32_t batch;    /* B */
-  int32_t d_model;  /* D (256 supported) */
+  int32_t d_model;  /* D: 128 or 256 (fused kernels), 384 or 512 (tiled kernels) */
   int32_t n_heads;  /* H (D / H = 64 supported) */
   int32_t n_ns;     /* NS tokens at the end of the sequence */
-  int32_t ffn_dim;  /* FFN hidden (multiple of 256) */
+  int32_t ffn_dim;  /* FFN hidden (multiple of 128) */
   int32_t kv_len;   /* tokens in x */
   int32_t q_len;    /* tokens kept (tail of x), n_ns <= q_len <= kv_len */
   int32_t reserved;
@@ -198,6 +198,27 @@ int pdm_onetrans_block_fwd(const pdm_block_desc* desc, const float* x,
                            const pdm_block_weights* w, float* y,
                            void* workspace, int64_t workspace_bytes,
                            pdm_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Cross-feature ids: xxHash64 of the little-endian concatenation of n int64
+ * keys, seeded with salt, modulo table_size (an unsigned 64-bit remainder).
+ *
+ * Replaces cross_hash_nway / cross_hash_int64 / cross_hash_batch
+ * (primus_dlrm/data/hashing.py:23-52,55-69,72-112), which the dataset calls
+ * once per event and cross spec (primus_dlrm/data/dataset.py:586-602); the
+ * result is the row id of the spec's EmbeddingCollection table
+ * (primus_dlrm/config.py:124-160).
+ * ------------------------------------------------------------------------ */
+
+#define PDM_CROSS_MAX_KEYS 8
+
+/* keys: host array of num_keys device pointers (2 <= num_keys <= 8), key k of
+ * row i at keys[k][i * key_strides[k]]; a stride of 0 broadcasts one value
+ * to every row.  out: device int64 [n], every value in [0, table_size).
+ * table_size >= 1. */
+int pdm_cross_hash_fwd(const int64_t* const* keys, const int64_t* key_strides,
+                       int32_t num_keys, int64_t n, uint64_t table_size,
+                       uint64_t salt, int64_t* out, pdm_stream_t stream);
 
 #ifdef __cplusplus
 }

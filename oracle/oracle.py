@@ -13,6 +13,8 @@ reference's lookup semantics on the CPU:
 * ``seq_gather``      jagged -> padded pools: data/dataset.py:604-626 (last L events,
                       left pad with id 0), onetrans.py:515-520 (feature concat),
                       onetrans.py:553-558 (pool concat).
+* ``cross_hash``      cross-feature ids: data/hashing.py:23-52 (XXH64 of the "<{n}q"
+                      packed keys, seed = salt, % table_size); ``xxh64`` is the digest.
 """
 from __future__ import annotations
 
@@ -57,6 +59,10 @@ def lib() -> ctypes.CDLL:
         h.oracle_int8_quantize.argtypes = [vp, i64, i32, vp, i32, i32]
         h.oracle_seq_gather.restype = i64
         h.oracle_seq_gather.argtypes = [i32, i32, i32, i64, vp, vp, vp, vp, vp, vp, vp, i32, i32, vp, vp]
+        h.oracle_xxh64.restype = ctypes.c_uint64
+        h.oracle_xxh64.argtypes = [vp, ctypes.c_size_t, ctypes.c_uint64]
+        h.oracle_cross_hash.restype = None
+        h.oracle_cross_hash.argtypes = [vp, vp, i32, i64, ctypes.c_uint64, ctypes.c_uint64, vp]
         _lib = h
     return _lib
 
@@ -218,3 +224,26 @@ def seq_gather(tables: Sequence[np.ndarray], ids: Sequence[Sequence[np.ndarray]]
     bad = lib().oracle_seq_gather(P, F, esize, B, _p(ml), _p(dims), _p(rows), tab_ptrs, id_ptrs, off_ptrs,
                                   _p(num_ids), pad_mode, align, _p(out), _p(mask))
     return (out, mask, int(bad)) if return_bad else (out, mask)
+
+
+def xxh64(data: bytes, seed: int = 0) -> int:
+    """XXH64 digest of ``data`` (the C restatement, any length)."""
+    buf = np.frombuffer(bytes(data), dtype=np.uint8).copy() if len(data) else np.zeros(1, np.uint8)
+    return int(lib().oracle_xxh64(_p(buf), len(data), seed & (2**64 - 1)))
+
+
+def cross_hash(keys: Sequence[np.ndarray], table_size: int, salt: int = 0) -> np.ndarray:
+    """Cross-feature ids: per row, XXH64(seed=salt) of the little-endian int64 keys, % table_size.
+
+    ``keys`` are int64 arrays of one length or of length 1 (broadcast), as in
+    primus_dlrm/data/hashing.py:23-52 (n-way) and :72-112 (batch)."""
+    ks = [np.ascontiguousarray(np.asarray(k, dtype=np.int64).ravel()) for k in keys]
+    n = max(k.shape[0] for k in ks)
+    strides = np.array([0 if (k.shape[0] == 1 and n != 1) else 1 for k in ks], dtype=np.int64)
+    for k, st in zip(ks, strides):
+        assert st == 0 or k.shape[0] == n, "key arrays must have one length (or length 1)"
+    out = np.empty(n, dtype=np.int64)
+    ptrs = (ctypes.c_void_p * len(ks))(*[_p(k) for k in ks])
+    lib().oracle_cross_hash(ctypes.addressof(ptrs), _p(strides), len(ks), n, table_size, salt & (2**64 - 1),
+                            _p(out))
+    return out

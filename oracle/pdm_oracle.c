@@ -24,6 +24,14 @@
  *                          every feature table and concat per event
  *                          (primus_dlrm/models/onetrans.py:515-520), pools
  *                          concatenated along the sequence (:553-558).
+ *   oracle_cross_hash      cross-feature ids: xxHash64 (seed = salt) of the
+ *                          little-endian concatenation of n int64 keys,
+ *                          modulo table_size (primus_dlrm/data/hashing.py:
+ *                          23-52, struct "<{n}q" pack + xxhash.xxh64 +
+ *                          intdigest() % table_size).  XXH64 is restated
+ *                          from its published specification, byte by byte
+ *                          over the packed buffer (any length), not from
+ *                          the word structure the GPU kernel uses.
  *   f32_to_f16 / f32_to_bf16 / f16_to_f32: IEEE round-to-nearest-even.
  */
 #include <math.h>
@@ -253,4 +261,82 @@ int64_t oracle_seq_gather(int32_t P, int32_t F, int32_t esize, int64_t B,
     }
   }
   return bad;
+}
+
+/* ---- cross-feature ids (xxHash64) --------------------------------------- */
+
+static const uint64_t XP1 = 0x9E3779B185EBCA87ull, XP2 = 0xC2B2AE3D27D4EB4Full,
+                      XP3 = 0x165667B19E3779F9ull, XP4 = 0x85EBCA77C2B2AE63ull,
+                      XP5 = 0x27D4EB2F165667C5ull;
+
+static inline uint64_t xrotl(uint64_t x, int r) { return (x << r) | (x >> (64 - r)); }
+static inline uint64_t xread64(const uint8_t* p) {
+  uint64_t v = 0;
+  for (int i = 7; i >= 0; --i) v = (v << 8) | p[i];  /* little endian */
+  return v;
+}
+static inline uint32_t xread32(const uint8_t* p) {
+  return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
+}
+static inline uint64_t xround(uint64_t acc, uint64_t lane) { return xrotl(acc + lane * XP2, 31) * XP1; }
+static inline uint64_t xmerge(uint64_t acc, uint64_t v) { return (acc ^ xround(0, v)) * XP1 + XP4; }
+
+/* XXH64 of len bytes at p with seed (the specification's algorithm). */
+uint64_t oracle_xxh64(const uint8_t* p, size_t len, uint64_t seed) {
+  const uint8_t* end = p + len;
+  uint64_t acc;
+  if (len >= 32) {
+    uint64_t v1 = seed + XP1 + XP2, v2 = seed + XP2, v3 = seed, v4 = seed - XP1;
+    const uint8_t* limit = end - 32;
+    do {
+      v1 = xround(v1, xread64(p));
+      v2 = xround(v2, xread64(p + 8));
+      v3 = xround(v3, xread64(p + 16));
+      v4 = xround(v4, xread64(p + 24));
+      p += 32;
+    } while (p <= limit);
+    acc = xrotl(v1, 1) + xrotl(v2, 7) + xrotl(v3, 12) + xrotl(v4, 18);
+    acc = xmerge(acc, v1);
+    acc = xmerge(acc, v2);
+    acc = xmerge(acc, v3);
+    acc = xmerge(acc, v4);
+  } else {
+    acc = seed + XP5;
+  }
+  acc += (uint64_t)len;
+  while (p + 8 <= end) {
+    acc ^= xround(0, xread64(p));
+    acc = xrotl(acc, 27) * XP1 + XP4;
+    p += 8;
+  }
+  if (p + 4 <= end) {
+    acc ^= (uint64_t)xread32(p) * XP1;
+    acc = xrotl(acc, 23) * XP2 + XP3;
+    p += 4;
+  }
+  while (p < end) {
+    acc ^= (uint64_t)(*p) * XP5;
+    acc = xrotl(acc, 11) * XP1;
+    ++p;
+  }
+  acc ^= acc >> 33;
+  acc *= XP2;
+  acc ^= acc >> 29;
+  acc *= XP3;
+  acc ^= acc >> 32;
+  return acc;
+}
+
+/* out[i] = xxh64(pack("<nq", keys[0][i*s0], ..., keys[n-1][i*s_{n-1}]), salt) % table_size. */
+void oracle_cross_hash(const int64_t* const* keys, const int64_t* strides, int32_t n_keys, int64_t n,
+                       uint64_t table_size, uint64_t salt, int64_t* out) {
+#pragma omp parallel for schedule(static) if (n > 65536)
+  for (int64_t i = 0; i < n; ++i) {
+    uint8_t buf[8 * 64];
+    for (int32_t k = 0; k < n_keys; ++k) {
+      uint64_t v = (uint64_t)keys[k][i * strides[k]];
+      for (int b = 0; b < 8; ++b) buf[8 * k + b] = (uint8_t)(v >> (8 * b));
+    }
+    out[i] = (int64_t)(oracle_xxh64(buf, (size_t)(8 * n_keys), salt) % table_size);
+  }
 }

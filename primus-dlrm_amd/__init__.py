@@ -1,8 +1,9 @@
 """MI355X (gfx950) embedding-lookup and OneTrans interaction forward path.
 
 Drop-ins for the reference's TorchRec EmbeddingBagCollection /
-EmbeddingCollection lookups, the OneTrans S-token build and the OneTrans
-block, running hand-written HIP kernels through the C ABI of libpdm.so.
+EmbeddingCollection lookups, the OneTrans S-token build, the OneTrans
+block and the cross-feature id hashing, running hand-written HIP kernels
+through the C ABI of libpdm.so.
 """
 from . import _lib
 from .embedding import (DataType, EmbeddingBagCollection, EmbeddingBagConfig, EmbeddingCollection,
@@ -11,10 +12,11 @@ from .kjt import JaggedTensor, KeyedJaggedTensor, KeyedTensor
 from .onetrans import (MixedAttention, MixedFFN, OneTransBlock, OneTransStack, RMSNorm, build_pyramid_mask,
                        pyramid_schedule)
 from . import ops
+from . import hashing
 
 __all__ = [
     "DataType", "EmbeddingBagCollection", "EmbeddingBagConfig", "EmbeddingCollection", "EmbeddingConfig",
     "EmbeddingTableConfig", "PoolingType", "SequenceGather", "TorchRecEmbeddings", "JaggedTensor",
     "KeyedJaggedTensor", "KeyedTensor", "MixedAttention", "MixedFFN", "OneTransBlock", "OneTransStack",
-    "RMSNorm", "build_pyramid_mask", "pyramid_schedule", "ops",
+    "RMSNorm", "build_pyramid_mask", "pyramid_schedule", "ops", "hashing",
 ]

@@ -12,6 +12,7 @@ import threading
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libpdm.so")
+PDM_CROSS_MAX_KEYS = 8
 
 PDM_OK = 0
 PDM_ERR_INVALID = -1
@@ -36,6 +37,7 @@ EXPORTED_SYMBOLS = (
     "pdm_tbe_pooled_fwd",
     "pdm_int8_rowwise_quantize",
     "pdm_seq_gather_fwd",
+    "pdm_cross_hash_fwd",
     "pdm_onetrans_block_workspace_size",
     "pdm_onetrans_block_fwd",
 )
@@ -133,6 +135,9 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.pdm_onetrans_block_fwd.restype = ctypes.c_int
     lib.pdm_onetrans_block_fwd.argtypes = [ctypes.POINTER(BlockDesc), vp, ctypes.POINTER(BlockWeights), vp,
                                            vp, i64, vp]
+    lib.pdm_cross_hash_fwd.restype = ctypes.c_int
+    lib.pdm_cross_hash_fwd.argtypes = [ctypes.POINTER(vp), ctypes.POINTER(i64), i32, i64, ctypes.c_uint64,
+                                       ctypes.c_uint64, vp, vp]
 
 
 def lib() -> ctypes.CDLL:

@@ -310,3 +310,56 @@ def onetrans_block_fwd(x: torch.Tensor, norm1_w: torch.Tensor, s_qkv_w: torch.Te
 @onetrans_block_fwd.register_fake
 def _(x, norm1_w, s_qkv_w, ns_qkv_w, out_w, norm2_w, s_w1, s_w2, ns_w1, ns_w2, n_heads, q_len):
     return x.new_empty((x.shape[0], q_len, x.shape[2]))
+
+
+# ---------------------------------------------------------------------------
+# Cross-feature ids (xxHash64)
+# ---------------------------------------------------------------------------
+
+def cross_hash_raw(keys: Sequence[torch.Tensor], table_size: int, salt: int = 0,
+                   out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """``out[i] = xxh64(le int64 keys[0][i] .. keys[n-1][i], seed=salt) % table_size`` on the GPU.
+
+    Each key is an int64 device tensor of N values, or of one value broadcast
+    to every row (primus_dlrm/data/hashing.py:23-52 n-way, :72-112 batch)."""
+    n_keys = len(keys)
+    if not 2 <= n_keys <= L.PDM_CROSS_MAX_KEYS:
+        raise ValueError(f"cross hash needs 2..{L.PDM_CROSS_MAX_KEYS} keys, got {n_keys}")
+    if table_size < 1:
+        raise ValueError("table_size must be >= 1")
+    ks = [k.reshape(-1) for k in keys]
+    dev = _require_cuda(*ks)
+    for k in ks:
+        if k.dtype != torch.int64:
+            raise TypeError(f"keys must be int64, got {k.dtype}")
+    n = max(k.numel() for k in ks)
+    strides = []
+    for k in ks:
+        if k.numel() == n:
+            strides.append(1)
+        elif k.numel() == 1:
+            strides.append(0)
+        else:
+            raise ValueError("key tensors must have one length (or length 1)")
+    ks = [k.contiguous() for k in ks]
+    if out is None:
+        out = torch.empty(n, dtype=torch.int64, device=dev)
+    elif out.dtype != torch.int64 or out.numel() != n or not out.is_contiguous() or out.device != dev:
+        raise ValueError("out must be a contiguous int64 tensor of N rows on the keys' device")
+    ptrs = (ctypes.c_void_p * n_keys)(*[k.data_ptr() for k in ks])
+    st = (ctypes.c_int64 * n_keys)(*strides)
+    with torch.cuda.device(dev):
+        L.check(L.lib().pdm_cross_hash_fwd(ptrs, st, n_keys, n, table_size, salt & (2**64 - 1), _ptr(out),
+                                           L.stream_ptr(dev)), "pdm_cross_hash_fwd")
+    return out
+
+
+@torch.library.custom_op("pdm::cross_hash_fwd", mutates_args=())
+def cross_hash_fwd(keys: List[torch.Tensor], table_size: int, salt: int) -> torch.Tensor:
+    return cross_hash_raw(keys, table_size, salt)
+
+
+@cross_hash_fwd.register_fake
+def _(keys, table_size, salt):
+    n = max(k.numel() for k in keys)
+    return keys[0].new_empty(n, dtype=torch.int64)

@@ -51,6 +51,12 @@ def test_argument_errors_are_reported_not_raised(pdm):
     d.num_pools = 0
     assert lib.pdm_seq_gather_fwd(ctypes.byref(d), None, None, None, None, None, None, None) == L.PDM_ERR_INVALID
     assert lib.pdm_int8_rowwise_quantize(None, 10, 0, None, 8, None) == L.PDM_ERR_INVALID
+    one = (ctypes.c_int64 * 1)(1)
+    assert lib.pdm_cross_hash_fwd(None, one, 1, 4, 10, 0, None, None) == L.PDM_ERR_INVALID
+    assert "num_keys" in L.last_error()
+    two = (ctypes.c_int64 * 2)(1, 1)
+    assert lib.pdm_cross_hash_fwd(None, two, 2, 4, 0, 0, None, None) == L.PDM_ERR_INVALID
+    assert "table_size" in L.last_error()
 
 
 def test_ops_refuse_cpu_tensors(pdm):
