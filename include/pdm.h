@@ -111,6 +111,100 @@ int pdm_int8_rowwise_quantize(const float* src, int64_t rows, int32_t dim,
                               pdm_stream_t stream);
 
 /* ------------------------------------------------------------------------
+ * Pooled TBE backward with the embedding optimizer fused in.
+ *
+ * Replaces the backward of the fused-optimizer table-batched embedding that
+ * TorchRec builds for an EmbeddingBagCollection whose weights were tagged by
+ * _apply_optimizer_in_backward (primus_dlrm/distributed/wrapper.py:151-174):
+ * FBGEMM's EmbOptimType.ADAM for torch.optim.Adam (the default,
+ * primus_dlrm/config.py:411-418) and EXACT_ROWWISE_ADAGRAD for
+ * torchrec.optim.RowWiseAdagrad with WeightDecayMode.L2
+ * (fbgemm_gpu 2026.4.29, scripts/launch_slurm_docker.sh:402, not vendored).
+ *
+ * The gradient of a table row is the sum, over every lookup of that row in
+ * the batch, of grad_out[b, out_offset : out_offset + dim] of the lookup's bag
+ * (times 1 / count for mean pooling, count = pooled indices of the bag);
+ * padding ids and out-of-range ids contribute nothing.  Only rows looked up
+ * in the batch are updated (sparse update), each exactly once.
+ *
+ * Row space: the plan's distinct tables (slots with equal weights_offset,
+ * rows, dim, dtype and row_bytes are one table) are numbered group by group
+ * ((dtype, dim) groups in first-appearance order) and in table order inside a
+ * group; row r of a table has row id pdm_tbe_plan_row_offset(slot) + r.
+ * Row-wise optimizer state is one fp32 per row id.
+ * ------------------------------------------------------------------------ */
+
+typedef enum {
+  PDM_OPT_ADAM = 0,            /* FBGEMM ADAM: per-element m, v */
+  PDM_OPT_ROWWISE_ADAGRAD = 1, /* FBGEMM EXACT_ROWWISE_ADAGRAD: one sum per row */
+  PDM_OPT_NONE = 2             /* gradient only (pdm_tbe_backward_sparse_grad) */
+} pdm_optimizer;
+
+typedef enum { PDM_WD_NONE = 0, PDM_WD_L2 = 1 } pdm_weight_decay_mode;
+
+typedef struct {
+  int32_t optimizer;         /* pdm_optimizer */
+  int32_t weight_decay_mode; /* row-wise Adagrad: PDM_WD_NONE | PDM_WD_L2 */
+  float learning_rate;
+  float eps;
+  float beta1;               /* Adam */
+  float beta2;               /* Adam */
+  float weight_decay;        /* Adam: decoupled term lr * wd * w */
+  int32_t reserved;
+  int64_t step;              /* Adam: 1-based count of this update */
+} pdm_optim_params;
+
+/* Rows of the plan's row space, and the row id of row 0 of a slot's table
+ * (-1 on a bad argument). */
+int64_t pdm_tbe_plan_total_rows(pdm_tbe_plan plan);
+int64_t pdm_tbe_plan_row_offset(pdm_tbe_plan plan, int32_t slot);
+
+/* Device workspace bytes the backward needs for num_indices lookups. */
+int64_t pdm_tbe_backward_workspace_size(pdm_tbe_plan plan, int64_t num_indices);
+
+/* Fused backward + optimizer update, in place.
+ * weights:   device fp32 base (every slot PDM_F32, row_bytes == 4 * dim,
+ *            weights_offset a multiple of 16)
+ * momentum1: Adam: fp32 buffer laid out like weights (same byte offsets);
+ *            row-wise Adagrad: fp32 [pdm_tbe_plan_total_rows]
+ * momentum2: Adam: like momentum1; row-wise Adagrad: unused (may be NULL)
+ * indices, index_bits, num_indices, offsets, batch_size, padding_idx: as in
+ *            pdm_tbe_pooled_fwd for the same batch
+ * grad_out:  device fp32 [B, grad_row_stride], d(loss)/d(pooled output)
+ *            (grad_row_stride and every out_offset multiples of 4,
+ *            16-byte aligned base)
+ * workspace: device, >= pdm_tbe_backward_workspace_size bytes
+ * err_flag:  optional device int32, set to 1 on an out-of-range index or
+ *            malformed offsets (those entries and bags are skipped; where
+ *            non-monotone offsets make two bags share a lookup, that lookup
+ *            counts for one of them).
+ * The update is deterministic: the same inputs give the same bits. */
+int pdm_tbe_backward_fused(pdm_tbe_plan plan, float* weights, float* momentum1,
+                           float* momentum2, const void* indices,
+                           int32_t index_bits, int64_t num_indices,
+                           const int64_t* offsets, int64_t batch_size,
+                           int64_t padding_idx, const float* grad_out,
+                           int64_t grad_row_stride,
+                           const pdm_optim_params* opt, void* workspace,
+                           int64_t workspace_bytes, int32_t* err_flag,
+                           pdm_stream_t stream);
+
+/* The deduplicated row gradients the fused update consumes (all slots of
+ * the plan must share one dim D):
+ * row_ids:   device int64 [num_indices]; first *num_unique entries = the
+ *            distinct row ids looked up, ascending
+ * grad_rows: device fp32 [num_indices, D]; row u = gradient of row_ids[u]
+ * num_unique: device int64 scalar. */
+int pdm_tbe_backward_sparse_grad(pdm_tbe_plan plan, const void* indices,
+                                 int32_t index_bits, int64_t num_indices,
+                                 const int64_t* offsets, int64_t batch_size,
+                                 int64_t padding_idx, const float* grad_out,
+                                 int64_t grad_row_stride, int64_t* row_ids,
+                                 float* grad_rows, int64_t* num_unique,
+                                 void* workspace, int64_t workspace_bytes,
+                                 int32_t* err_flag, pdm_stream_t stream);
+
+/* ------------------------------------------------------------------------
  * Jagged -> padded S-token sequence gather.
  *
  * Replaces the unpooled lookup TorchRec EmbeddingCollection.forward

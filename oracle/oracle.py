@@ -15,6 +15,12 @@ reference's lookup semantics on the CPU:
                       onetrans.py:553-558 (pool concat).
 * ``cross_hash``      cross-feature ids: data/hashing.py:23-52 (XXH64 of the "<{n}q"
                       packed keys, seed = salt, % table_size); ``xxh64`` is the digest.
+* ``tbe_backward``    pooled-lookup backward + the fused embedding optimizer TorchRec maps the
+                      reference's choice to (distributed/wrapper.py:151-174): row gradients
+                      summed in lookup order, then FBGEMM's ADAM or EXACT_ROWWISE_ADAGRAD
+                      update per distinct row (fbgemm_gpu 2026.4.29, absent here; rules
+                      restated at oracle_tbe_backward in pdm_oracle.c).  ``row_space``
+                      numbers the distinct tables the way the library documents it.
 """
 from __future__ import annotations
 
@@ -39,6 +45,12 @@ class _Table(ctypes.Structure):
                 ("out_offset", ctypes.c_int32), ("reserved", ctypes.c_int32)]
 
 
+class _Optim(ctypes.Structure):
+    _fields_ = [("optimizer", ctypes.c_int32), ("wd_mode", ctypes.c_int32), ("lr", ctypes.c_float),
+                ("eps", ctypes.c_float), ("beta1", ctypes.c_float), ("beta2", ctypes.c_float),
+                ("weight_decay", ctypes.c_float), ("reserved", ctypes.c_int32), ("step", ctypes.c_int64)]
+
+
 def lib() -> ctypes.CDLL:
     global _lib
     if _lib is None:
@@ -61,6 +73,9 @@ def lib() -> ctypes.CDLL:
         h.oracle_seq_gather.argtypes = [i32, i32, i32, i64, vp, vp, vp, vp, vp, vp, vp, i32, i32, vp, vp]
         h.oracle_xxh64.restype = ctypes.c_uint64
         h.oracle_xxh64.argtypes = [vp, ctypes.c_size_t, ctypes.c_uint64]
+        h.oracle_tbe_backward.restype = i64
+        h.oracle_tbe_backward.argtypes = [ctypes.POINTER(_Table), vp, i32, i64, vp, i32, i64, vp, i64, vp, i64,
+                                          vp, vp, i32, ctypes.POINTER(_Optim), vp, vp, vp, vp, vp]
         h.oracle_cross_hash.restype = None
         h.oracle_cross_hash.argtypes = [vp, vp, i32, i64, ctypes.c_uint64, ctypes.c_uint64, vp]
         _lib = h
@@ -247,3 +262,78 @@ def cross_hash(keys: Sequence[np.ndarray], table_size: int, salt: int = 0) -> np
     lib().oracle_cross_hash(ctypes.addressof(ptrs), _p(strides), len(ks), n, table_size, salt & (2**64 - 1),
                             _p(out))
     return out
+
+
+# ---- pooled backward + fused optimizer ----------------------------------------
+
+ADAM, ROWWISE_ADAGRAD, GRAD_ONLY = 0, 1, 2
+WD_NONE, WD_L2 = 0, 1
+
+
+def row_space(slots: Sequence[dict]):
+    """Row id of row 0 of each slot's table and the total row count: distinct tables (equal
+    weights_offset, rows, dim, dtype, row_bytes) numbered group by group ((dtype, dim) groups in
+    first-appearance order), in slot order inside a group."""
+    def ident(s):
+        return (int(s["weights_offset"]), int(s["rows"]), int(s["dim"]), s["dtype"],
+                int(s.get("row_bytes", 0)) or default_row_bytes(s["dtype"], int(s["dim"])))
+    groups: List[tuple] = []
+    for s in slots:
+        g = (s["dtype"], int(s["dim"]))
+        if g not in groups:
+            groups.append(g)
+    row_off = [0] * len(slots)
+    seen = {}
+    total = 0
+    for g in groups:
+        for i, s in enumerate(slots):
+            if (s["dtype"], int(s["dim"])) != g:
+                continue
+            k = ident(s)
+            if k in seen:
+                row_off[i] = seen[k]
+            else:
+                seen[k] = row_off[i] = total
+                total += int(s["rows"])
+    return row_off, total
+
+
+def tbe_backward(slots: Sequence[dict], indices: np.ndarray, offsets: np.ndarray, batch: int, grad: np.ndarray,
+                 padding_idx: int = -1, optimizer: int = GRAD_ONLY, weights: Optional[np.ndarray] = None,
+                 m1: Optional[np.ndarray] = None, m2: Optional[np.ndarray] = None, lr: float = 0.01,
+                 eps: float = 1e-8, beta1: float = 0.9, beta2: float = 0.999, weight_decay: float = 0.0,
+                 wd_mode: int = WD_NONE, step: int = 1, row_off: Optional[Sequence[int]] = None):
+    """slots as for ``tbe_pooled`` (fp32 tables); grad: float32 [B, grad_stride].
+    weights / m1 / m2: float32 arrays updated in place (weights and Adam state indexed by
+    weights_offset / 4 + row * dim; row-wise state by row id).
+    Returns (row_ids, row_grads [U, max dim] (a row of a narrower table is zero past its dim), bad)."""
+    T = len(slots)
+    arr = (_Table * T)()
+    for i, s in enumerate(slots):
+        arr[i] = _Table(int(s["rows"]), int(s["weights_offset"]), int(s["dim"]), _DT[s["dtype"]],
+                        _POOL[s["pooling"]], int(s.get("row_bytes", 0)), int(s["out_offset"]), 0)
+    if row_off is None:
+        row_off, _ = row_space(slots)
+    ro = np.ascontiguousarray(row_off, dtype=np.int64)
+    indices = np.ascontiguousarray(indices)
+    if indices.dtype not in (np.int32, np.int64):
+        indices = indices.astype(np.int64)
+    offsets = np.ascontiguousarray(offsets, dtype=np.int64)
+    assert offsets.size == T * batch + 1
+    grad = np.ascontiguousarray(grad, dtype=np.float32)
+    n = max(indices.size, 1)
+    D = max(int(s["dim"]) for s in slots)
+    ids = np.zeros(n, dtype=np.int64)
+    rows = np.zeros((n, D), dtype=np.float32)
+    entries = np.zeros(n * 40, dtype=np.uint8)
+    bad = ctypes.c_int64(0)
+    opt = _Optim(optimizer, wd_mode, lr, eps, beta1, beta2, weight_decay, 0, step)
+    for a in (weights, m1, m2):
+        assert a is None or (a.dtype == np.float32 and a.flags.c_contiguous)
+    u = lib().oracle_tbe_backward(arr, _p(ro), T, batch, _p(indices) if indices.size else None,
+                                  32 if indices.dtype == np.int32 else 64, indices.size, _p(offsets), padding_idx,
+                                  _p(grad) if grad.size else None, grad.shape[1] if grad.ndim == 2 else 0,
+                                  _p(ids), _p(rows), D, ctypes.byref(opt),
+                                  _p(weights) if weights is not None else None, _p(m1) if m1 is not None else None,
+                                  _p(m2) if m2 is not None else None, _p(entries), ctypes.byref(bad))
+    return ids[:u], rows[:u], int(bad.value)

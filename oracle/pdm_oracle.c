@@ -32,10 +32,18 @@
  *                          from its published specification, byte by byte
  *                          over the packed buffer (any length), not from
  *                          the word structure the GPU kernel uses.
+ *   oracle_tbe_backward    pooled-lookup backward with the fused embedding
+ *                          optimizer TorchRec substitutes for the
+ *                          reference's choice (primus_dlrm/distributed/
+ *                          wrapper.py:151-174): the row gradient summed in
+ *                          lookup order, then FBGEMM's ADAM or
+ *                          EXACT_ROWWISE_ADAGRAD update rule per distinct
+ *                          row (formulas at the function).
  *   f32_to_f16 / f32_to_bf16 / f16_to_f32: IEEE round-to-nearest-even.
  */
 #include <math.h>
 #include <stdint.h>
+#include <stdlib.h>
 #include <string.h>
 
 enum { O_F32 = 0, O_F16 = 1, O_BF16 = 2, O_I8 = 3 };
@@ -339,4 +347,136 @@ void oracle_cross_hash(const int64_t* const* keys, const int64_t* strides, int32
     }
     out[i] = (int64_t)(oracle_xxh64(buf, (size_t)(8 * n_keys), salt) % table_size);
   }
+}
+
+/* ---- pooled TBE backward + fused optimizer ---------------------------- */
+
+/* Same field layout as the library's pdm_optim_params. */
+typedef struct {
+  int32_t optimizer; /* 0 Adam, 1 row-wise Adagrad, 2 gradient only */
+  int32_t wd_mode;   /* row-wise Adagrad: 0 none, 1 L2 */
+  float lr, eps, beta1, beta2, weight_decay;
+  int32_t reserved;
+  int64_t step;
+} oracle_optim;
+
+typedef struct {
+  int64_t key;   /* row id: row_off[slot] + index */
+  int64_t pos;   /* lookup position (tie order) */
+  int64_t goff;  /* first grad element of the lookup's bag slice */
+  float scale;   /* 1, or 1 / pooled count for mean */
+  int32_t slot;
+} bwd_entry;
+
+static int cmp_bwd_entry(const void* pa, const void* pb) {
+  const bwd_entry* a = (const bwd_entry*)pa;
+  const bwd_entry* b = (const bwd_entry*)pb;
+  if (a->key != b->key) return a->key < b->key ? -1 : 1;
+  return a->pos < b->pos ? -1 : (a->pos > b->pos ? 1 : 0);
+}
+
+/* The gradient of each looked-up row is the sum, in lookup-position order,
+ * of scale * grad[b, out_offset + d] over the row's lookups (fmaf per term);
+ * padding ids and out-of-range ids contribute nothing; the mean scale is
+ * 1 / (pooled ids of the bag), the derivative of the pooled mean
+ * (primus_dlrm/models/sharded_embedding.py:220-227).  The optimizer is then
+ * applied once per distinct row (sparse update), with the formulas of the
+ * fused FBGEMM optimizers TorchRec maps the reference's choice to
+ * (primus_dlrm/distributed/wrapper.py:151-174; fbgemm_gpu 2026.4.29, absent
+ * here, restated from its published update rules):
+ *   Adam (EmbOptimType.ADAM, the reference's default optimizer):
+ *     m = b1 m + (1 - b1) g;  v = b2 v + (1 - b2) g^2
+ *     w = w - lr ((m / (1 - b1^t)) / (sqrt(v / (1 - b2^t)) + eps) + wd w)
+ *   row-wise Adagrad (EXACT_ROWWISE_ADAGRAD, weight_decay_mode L2 or none):
+ *     g' = g + wd w (L2);  G = G + mean_d(g'^2)
+ *     mu = lr / (sqrt(G) + eps);  w = (1 - mu wd) w - mu g   (L2)
+ *                                 w = w - mu g              (none)
+ * row_off[t]: row id of row 0 of slot t's table (slots of one table share
+ * it).  Adam state m1/m2 is laid out like the fp32 weights; row-wise state
+ * m1 is indexed by row id.  ids_out / grads_out (optional; rows of
+ * grads_stride floats) receive the distinct row ids, ascending, and their
+ * gradients.  Returns the
+ * number of distinct rows; *bad counts skipped entries (out-of-range ids,
+ * bags with malformed offsets).  entries is scratch of num_indices. */
+int64_t oracle_tbe_backward(const oracle_table* tables, const int64_t* row_off, int32_t T, int64_t B,
+                            const void* indices, int32_t index_bits, int64_t num_indices,
+                            const int64_t* offsets, int64_t padding_idx, const float* grad, int64_t grad_stride,
+                            int64_t* ids_out, float* grads_out, int32_t grads_stride, const oracle_optim* opt,
+                            float* weights,
+                            float* m1, float* m2, bwd_entry* entries, int64_t* bad) {
+  int64_t n = 0, nbad = 0;
+  for (int64_t g = 0; g < (int64_t)T * B; ++g) {
+    const int32_t t = (int32_t)(g / B);
+    const int64_t b = g % B;
+    const oracle_table* tb = &tables[t];
+    const int64_t start = offsets[g], end = offsets[g + 1];
+    if (start < 0 || end < start || end > num_indices) {
+      ++nbad;
+      continue;
+    }
+    int64_t count = 0;
+    for (int64_t i = start; i < end; ++i) {
+      const int64_t idx = index_bits == 32 ? (int64_t)((const int32_t*)indices)[i] : ((const int64_t*)indices)[i];
+      if (padding_idx >= 0 && idx == padding_idx) continue;
+      if (idx < 0 || idx >= tb->rows) {
+        ++nbad;
+        continue;
+      }
+      ++count;
+    }
+    const float scale = tb->pooling == 1 ? 1.0f / (float)count : 1.0f;
+    for (int64_t i = start; i < end; ++i) {
+      const int64_t idx = index_bits == 32 ? (int64_t)((const int32_t*)indices)[i] : ((const int64_t*)indices)[i];
+      if ((padding_idx >= 0 && idx == padding_idx) || idx < 0 || idx >= tb->rows) continue;
+      bwd_entry e = {row_off[t] + idx, i, b * grad_stride + tb->out_offset, scale, t};
+      entries[n++] = e;
+    }
+  }
+  if (bad) *bad = nbad;
+  qsort(entries, (size_t)n, sizeof(bwd_entry), cmp_bwd_entry);
+  int64_t u = 0;
+  float gsum[4096];
+  for (int64_t i = 0; i < n;) {
+    int64_t j = i;
+    const oracle_table* tb = &tables[entries[i].slot];
+    const int32_t D = tb->dim;
+    for (int32_t d = 0; d < D; ++d) gsum[d] = 0.0f;
+    for (; j < n && entries[j].key == entries[i].key; ++j)
+      for (int32_t d = 0; d < D; ++d) gsum[d] = fmaf(entries[j].scale, grad[entries[j].goff + d], gsum[d]);
+    const int64_t key = entries[i].key;
+    if (ids_out) ids_out[u] = key;
+    if (grads_out)
+      for (int32_t d = 0; d < D; ++d) grads_out[u * grads_stride + d] = gsum[d];
+    if (opt && opt->optimizer != 2) {
+      const int64_t e0 = tb->weights_offset / 4 + (key - row_off[entries[i].slot]) * D;
+      float* w = weights + e0;
+      if (opt->optimizer == 0) {
+        const float b1 = opt->beta1, b2 = opt->beta2, omb1 = 1.0f - b1, omb2 = 1.0f - b2;
+        const float bc1 = 1.0f - powf(b1, (float)opt->step), bc2 = 1.0f - powf(b2, (float)opt->step);
+        float* m = m1 + e0;
+        float* v = m2 + e0;
+        for (int32_t d = 0; d < D; ++d) {
+          const float g = gsum[d];
+          m[d] = fmaf(g, omb1, m[d] * b1);
+          v[d] = fmaf(g * g, omb2, v[d] * b2);
+          w[d] = w[d] - opt->lr * ((m[d] / bc1) / (sqrtf(v[d] / bc2) + opt->eps) + opt->weight_decay * w[d]);
+        }
+      } else {
+        const int l2 = opt->wd_mode == 1;
+        float ss = 0.0f;
+        for (int32_t d = 0; d < D; ++d) {
+          const float gg = l2 ? gsum[d] + opt->weight_decay * w[d] : gsum[d];
+          ss += gg * gg;
+        }
+        const float state = m1[key] + ss / (float)D;
+        const float mult = opt->lr / (sqrtf(state) + opt->eps);
+        const float corr = l2 ? 1.0f - mult * opt->weight_decay : 1.0f;
+        for (int32_t d = 0; d < D; ++d) w[d] = corr * w[d] - mult * gsum[d];
+        m1[key] = state;
+      }
+    }
+    ++u;
+    i = j;
+  }
+  return u;
 }

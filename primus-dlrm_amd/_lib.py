@@ -26,6 +26,8 @@ PDM_PAD_ROW0, PDM_PAD_ZERO = 0, 1
 PDM_ALIGN_RIGHT, PDM_ALIGN_LEFT = 0, 1
 PDM_SEQ_MAX_POOLS = 8
 PDM_SEQ_MAX_FEATURES = 8
+PDM_OPT_ADAM, PDM_OPT_ROWWISE_ADAGRAD, PDM_OPT_NONE = 0, 1, 2
+PDM_WD_NONE, PDM_WD_L2 = 0, 1
 
 # Every symbol include/pdm.h declares (checked by the ABI test).
 EXPORTED_SYMBOLS = (
@@ -36,6 +38,11 @@ EXPORTED_SYMBOLS = (
     "pdm_tbe_plan_total_dim",
     "pdm_tbe_pooled_fwd",
     "pdm_int8_rowwise_quantize",
+    "pdm_tbe_plan_total_rows",
+    "pdm_tbe_plan_row_offset",
+    "pdm_tbe_backward_workspace_size",
+    "pdm_tbe_backward_fused",
+    "pdm_tbe_backward_sparse_grad",
     "pdm_seq_gather_fwd",
     "pdm_cross_hash_fwd",
     "pdm_onetrans_block_workspace_size",
@@ -61,6 +68,20 @@ class TableDesc(ctypes.Structure):
         ("row_bytes", ctypes.c_int32),
         ("out_offset", ctypes.c_int32),
         ("reserved", ctypes.c_int32),
+    ]
+
+
+class OptimParams(ctypes.Structure):
+    _fields_ = [
+        ("optimizer", ctypes.c_int32),
+        ("weight_decay_mode", ctypes.c_int32),
+        ("learning_rate", ctypes.c_float),
+        ("eps", ctypes.c_float),
+        ("beta1", ctypes.c_float),
+        ("beta2", ctypes.c_float),
+        ("weight_decay", ctypes.c_float),
+        ("reserved", ctypes.c_int32),
+        ("step", ctypes.c_int64),
     ]
 
 
@@ -135,6 +156,18 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.pdm_onetrans_block_fwd.restype = ctypes.c_int
     lib.pdm_onetrans_block_fwd.argtypes = [ctypes.POINTER(BlockDesc), vp, ctypes.POINTER(BlockWeights), vp,
                                            vp, i64, vp]
+    lib.pdm_tbe_plan_total_rows.restype = i64
+    lib.pdm_tbe_plan_total_rows.argtypes = [vp]
+    lib.pdm_tbe_plan_row_offset.restype = i64
+    lib.pdm_tbe_plan_row_offset.argtypes = [vp, i32]
+    lib.pdm_tbe_backward_workspace_size.restype = i64
+    lib.pdm_tbe_backward_workspace_size.argtypes = [vp, i64]
+    lib.pdm_tbe_backward_fused.restype = ctypes.c_int
+    lib.pdm_tbe_backward_fused.argtypes = [vp, vp, vp, vp, vp, i32, i64, vp, i64, i64, vp, i64,
+                                           ctypes.POINTER(OptimParams), vp, i64, vp, vp]
+    lib.pdm_tbe_backward_sparse_grad.restype = ctypes.c_int
+    lib.pdm_tbe_backward_sparse_grad.argtypes = [vp, vp, i32, i64, vp, i64, i64, vp, i64, vp, vp, vp, vp, i64,
+                                                 vp, vp]
     lib.pdm_cross_hash_fwd.restype = ctypes.c_int
     lib.pdm_cross_hash_fwd.argtypes = [ctypes.POINTER(vp), ctypes.POINTER(i64), i32, i64, ctypes.c_uint64,
                                        ctypes.c_uint64, vp, vp]

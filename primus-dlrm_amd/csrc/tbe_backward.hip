@@ -1,0 +1,816 @@
+// Pooled TBE backward with the embedding optimizer fused in, for gfx950.
+//
+// Semantics: the fused-optimizer table-batched embedding TorchRec builds for
+// an EmbeddingBagCollection whose weights carry _apply_optimizer_in_backward
+// (primus_dlrm/distributed/wrapper.py:151-174): torch.optim.Adam maps to
+// FBGEMM's ADAM, torchrec.optim.RowWiseAdagrad (WeightDecayMode.L2) to
+// EXACT_ROWWISE_ADAGRAD.  The row gradient is the sum over the batch's
+// lookups of that row of the bag's output gradient (scaled by 1 / count for
+// mean pooling); every looked-up row is updated once, untouched rows keep
+// their weights and state.
+//
+// Design (one stream, no host synchronisation, deterministic):
+//  1. linearise: each lookup becomes a 32-bit row-space key (sentinel for
+//     padding / invalid ids) and an 8-byte record {gradient row, scale};
+//  2. stable LSD radix sort of (key, lookup position), 8 bits per pass over
+//     only the bits the row space needs.  A tile of 4096 keys is ranked per
+//     wavefront with ballots (stable: lanes and rounds follow positions),
+//     then staged in LDS in sorted order so the scatter writes contiguous
+//     runs per digit;
+//  3. accumulate: a wavefront owns 64 consecutive sorted entries; lane groups
+//     of D/4 lanes (one float4 of the row per lane) sum the runs of equal keys
+//     in position order and apply the optimizer to the row in registers.  A
+//     run that crosses a chunk boundary leaves per-chunk partial sums, which a
+//     second kernel adds in chunk order before applying the optimizer, so a
+//     hot row costs no atomics and the summation order never depends on
+//     scheduling.
+#include <algorithm>
+#include <vector>
+
+#include "pdm_common.h"
+#include "tbe_plan.h"
+
+#pragma clang fp contract(off)
+
+namespace pdm {
+
+namespace {
+
+constexpr int kSortThreads = 256;
+constexpr int kSortItems = 16;
+constexpr int kTile = kSortThreads * kSortItems;  // keys per sort tile
+constexpr int kBins = 256;                         // 8-bit digits
+constexpr int kChunk = 64;                         // sorted entries per accumulating wavefront
+constexpr uint32_t kSentinel = 0xFFFFFFFFu;
+
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint64_t lanemask_lt(int lane) { return (uint64_t(1) << lane) - 1; }
+
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v, int lane) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t t = __shfl_up(v, o);
+    if (lane >= o) v += t;
+  }
+  return v;
+}
+
+// Exclusive scan of one value per thread over a 256-thread block; tmp holds 4
+// words.  The caller synchronises before tmp is written again.
+__device__ __forceinline__ uint32_t block_excl_scan256(uint32_t v, uint32_t* tmp, uint32_t& total) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const uint32_t incl = wave_incl_scan(v, lane);
+  if (lane == 63) tmp[w] = incl;
+  __syncthreads();
+  uint32_t pre = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) pre += i < w ? tmp[i] : 0u;
+  total = tmp[0] + tmp[1] + tmp[2] + tmp[3];
+  return pre + incl - v;
+}
+
+// ---- 1. linearisation ---------------------------------------------------------
+
+__global__ __launch_bounds__(256) void fill_u32_kernel(uint32_t* __restrict__ p, int64_t n4, uint32_t v) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n4) reinterpret_cast<uint4*>(p)[i] = make_uint4(v, v, v, v);
+}
+
+struct LinArgs {
+  const void* indices;
+  const int64_t* offsets;
+  const BwdSlot* slots;
+  uint32_t* keys;  // [n_pad], pre-filled with the sentinel
+  uint2* info;     // [num_indices] {gradient float4 index, scale bits}
+  int32_t* err;
+  int64_t num_indices;
+  int64_t B;
+  int64_t num_bags;
+  int64_t padding_idx;
+  int64_t grad_stride;
+};
+
+// One thread per bag: counts the bag's pooled ids (mean scale), then writes a
+// key and a record for each of them.  A bag whose offsets are malformed is
+// skipped and flagged; an id outside [0, rows) is skipped and flagged.
+template <typename IdxT>
+__global__ __launch_bounds__(256) void bwd_linearize_kernel(LinArgs a) {
+  const int64_t bag = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (bag >= a.num_bags) return;
+  const int64_t t = bag / a.B;
+  const int64_t b = bag - t * a.B;
+  const BwdSlot s = a.slots[t];
+  const int64_t lo = a.offsets[bag], hi = a.offsets[bag + 1];
+  if (lo < 0 || hi < lo || hi > a.num_indices) {
+    if (a.err) *a.err = 1;
+    return;
+  }
+  const IdxT* idx = reinterpret_cast<const IdxT*>(a.indices);
+  int64_t cnt = 0;
+  bool bad = false;
+  const bool has_pad = a.padding_idx >= 0;
+  for (int64_t p = lo; p < hi; ++p) {
+    const int64_t v = (int64_t)idx[p];
+    if (has_pad && v == a.padding_idx) continue;
+    if (v < 0 || v >= s.rows) {
+      bad = true;
+      continue;
+    }
+    ++cnt;
+  }
+  if (bad && a.err) *a.err = 1;
+  if (cnt == 0) return;
+  const float scale = s.pooling == PDM_POOL_MEAN ? 1.0f / (float)cnt : 1.0f;
+  const uint2 rec = make_uint2((uint32_t)((b * a.grad_stride + s.out_col) >> 2), __float_as_uint(scale));
+  for (int64_t p = lo; p < hi; ++p) {
+    const int64_t v = (int64_t)idx[p];
+    if ((has_pad && v == a.padding_idx) || v < 0 || v >= s.rows) continue;
+    a.keys[p] = (uint32_t)(s.row_off + v);
+    a.info[p] = rec;
+  }
+}
+
+// ---- 2. radix sort ---------------------------------------------------------------
+
+// Per-tile digit counts, stored digit-major: hist[d * num_tiles + tile].
+__global__ __launch_bounds__(kSortThreads) void radix_count_kernel(const uint32_t* __restrict__ keys,
+                                                                   uint32_t* __restrict__ hist, int shift,
+                                                                   uint32_t mask, int64_t num_tiles) {
+  __shared__ uint32_t cnt[4][kBins];
+  const int tid = threadIdx.x, w = tid >> 6;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) cnt[i][tid] = 0;
+  __syncthreads();
+  const uint4* k4 = reinterpret_cast<const uint4*>(keys + (int64_t)blockIdx.x * kTile);
+  uint4 k[kSortItems / 4];
+#pragma unroll
+  for (int i = 0; i < kSortItems / 4; ++i) k[i] = k4[i * kSortThreads + tid];
+#pragma unroll
+  for (int i = 0; i < kSortItems / 4; ++i) {
+    atomicAdd(&cnt[w][(k[i].x >> shift) & mask], 1u);
+    atomicAdd(&cnt[w][(k[i].y >> shift) & mask], 1u);
+    atomicAdd(&cnt[w][(k[i].z >> shift) & mask], 1u);
+    atomicAdd(&cnt[w][(k[i].w >> shift) & mask], 1u);
+  }
+  __syncthreads();
+  hist[(int64_t)tid * num_tiles + blockIdx.x] = cnt[0][tid] + cnt[1][tid] + cnt[2][tid] + cnt[3][tid];
+}
+
+// Exclusive scan of each row of rows[gridDim.x][len] in place; totals[row] =
+// the row's sum.
+__global__ __launch_bounds__(256) void scan_rows_kernel(uint32_t* __restrict__ rows, uint32_t* __restrict__ totals,
+                                                        int64_t len) {
+  __shared__ uint32_t tmp[4];
+  uint32_t* row = rows + (int64_t)blockIdx.x * len;
+  uint32_t carry = 0;
+  for (int64_t base = 0; base < len; base += 256 * 4) {
+    const int64_t i0 = base + threadIdx.x * 4;
+    uint32_t v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = i0 + j < len ? row[i0 + j] : 0u;
+    uint32_t total;
+    uint32_t run = carry + block_excl_scan256(v[0] + v[1] + v[2] + v[3], tmp, total);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (i0 + j < len) row[i0 + j] = run;
+      run += v[j];
+    }
+    carry += total;
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) totals[blockIdx.x] = carry;
+}
+
+// Stable scatter of one tile.  Wave w ranks the keys at tile positions
+// w*1024 + j*64 + lane, j = 0..15 (position order = (j, lane) order): lanes
+// with equal digits are found with one ballot per digit bit, and a per-wave
+// LDS counter per digit carries ranks across rounds.  Keys (and values) are
+// then placed in LDS in tile-sorted order and written out in that order, so
+// the global writes of a digit are contiguous.  FIRST: the values are the
+// key positions.
+template <bool FIRST>
+__global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
+    const uint32_t* __restrict__ keys_in, const uint32_t* __restrict__ vals_in, uint32_t* __restrict__ keys_out,
+    uint32_t* __restrict__ vals_out, const uint32_t* __restrict__ hist, const uint32_t* __restrict__ totals,
+    int shift, int nbits, int64_t num_tiles, uint32_t n_pad) {
+  __shared__ uint32_t cnt[4][kBins];
+  __shared__ uint32_t tstart[kBins];
+  __shared__ uint32_t gbase[kBins];
+  __shared__ uint32_t tmp[4];
+  __shared__ uint32_t sk[kTile];
+  __shared__ uint32_t sv[kTile];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const uint32_t mask = (1u << nbits) - 1u;
+  const int64_t tile = blockIdx.x;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) cnt[i][tid] = 0;
+  {
+    uint32_t total;
+    const uint32_t dpre = block_excl_scan256(totals[tid], tmp, total);
+    gbase[tid] = dpre + hist[(int64_t)tid * num_tiles + tile];
+  }
+  const int64_t p0 = tile * kTile + w * (kTile / 4);
+  uint32_t key[kSortItems], val[kSortItems], rank[kSortItems];
+#pragma unroll
+  for (int j = 0; j < kSortItems; ++j) {
+    key[j] = keys_in[p0 + j * 64 + lane];
+    val[j] = FIRST ? (uint32_t)(p0 + j * 64 + lane) : vals_in[p0 + j * 64 + lane];
+  }
+  __syncthreads();  // cnt zeroed, tmp free
+  const uint64_t lt = lanemask_lt(lane);
+#pragma unroll
+  for (int j = 0; j < kSortItems; ++j) {
+    const uint32_t d = (key[j] >> shift) & mask;
+    uint64_t peers = ~uint64_t(0);
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+      if (b < nbits) {
+        const bool bit = (d >> b) & 1u;
+        const uint64_t bal = __ballot(bit);
+        peers &= bit ? bal : ~bal;
+      }
+    }
+    const uint32_t before = cnt[w][d];
+    rank[j] = before + (uint32_t)__popcll(peers & lt);
+    if ((peers & lt) == 0) cnt[w][d] = before + (uint32_t)__popcll(peers);
+  }
+  __syncthreads();
+  {
+    const uint32_t c0 = cnt[0][tid], c1 = cnt[1][tid], c2 = cnt[2][tid], c3 = cnt[3][tid];
+    cnt[0][tid] = 0;
+    cnt[1][tid] = c0;
+    cnt[2][tid] = c0 + c1;
+    cnt[3][tid] = c0 + c1 + c2;
+    uint32_t total;
+    tstart[tid] = block_excl_scan256(c0 + c1 + c2 + c3, tmp, total);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < kSortItems; ++j) {
+    const uint32_t d = (key[j] >> shift) & mask;
+    const uint32_t lpos = tstart[d] + cnt[w][d] + rank[j];
+    if (lpos < (uint32_t)kTile) {
+      sk[lpos] = key[j];
+      sv[lpos] = val[j];
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < kSortItems; ++i) {
+    const uint32_t idx = i * kSortThreads + tid;
+    const uint32_t k = sk[idx];
+    const uint32_t d = (k >> shift) & mask;
+    const uint32_t g = gbase[d] + idx - tstart[d];
+    if (g < n_pad) {
+      keys_out[g] = k;
+      vals_out[g] = sv[idx];
+    }
+  }
+}
+
+// ---- 3. accumulate + optimizer ---------------------------------------------------
+
+struct AccArgs {
+  const uint32_t* keys;  // sorted keys [n_pad]
+  const uint32_t* vals;  // lookup positions, in key order
+  const uint2* info;     // per lookup position
+  const float* grad;
+  float* w;
+  float* m1;
+  float* m2;
+  float* part_first;  // [num_chunks, D]: sum of a chunk's first run when it began in an earlier chunk
+  float* part_last;   // [num_chunks, D]: sum of a chunk's last run when it began there and continues
+  const BwdTable* tabs;
+  int32_t ntab;
+  int32_t D;
+  uint32_t key_lo;
+  uint32_t key_hi;
+  int64_t n_pad;
+  int64_t num_chunks;
+  int64_t num_indices;
+  // optimizer
+  int32_t wd_mode;
+  float lr, eps, b1, b2, omb1, omb2, bc1, bc2, wd;
+  // gradient output
+  int64_t* out_ids;
+  float* out_rows;
+  const uint32_t* head_prefix;  // per chunk: distinct rows that begin in earlier chunks
+  const uint32_t* num_heads;
+  int64_t* out_count;
+};
+
+enum { MODE_ADAM = 0, MODE_ADAGRAD = 1, MODE_GRAD = 2 };
+
+// Applies the update of row `key` from its summed gradient g (lane gl of a
+// group of G lanes holds float4 columns gl, gl + G, ...).
+template <int G, int VEC, int MODE>
+__device__ __forceinline__ void apply_row(const AccArgs& a, uint32_t key, const f32x4_t (&g)[VEC], int gl,
+                                          int64_t slot) {
+  const int D4 = a.D >> 2;
+  if constexpr (MODE == MODE_GRAD) {
+    if (gl == 0) a.out_ids[slot] = (int64_t)key;
+    f32x4_t* o = reinterpret_cast<f32x4_t*>(a.out_rows + slot * a.D);
+#pragma unroll
+    for (int v = 0; v < VEC; ++v)
+      if (gl + v * G < D4) o[gl + v * G] = g[v];
+    return;
+  } else {
+    int lo = 0, hi = a.ntab - 1;  // last table whose first row id <= key
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (a.tabs[mid].row_off <= (int64_t)key) lo = mid;
+      else hi = mid - 1;
+    }
+    const BwdTable tb = a.tabs[lo];
+    const int64_t e0 = tb.w_elem + ((int64_t)key - tb.row_off) * a.D;
+    f32x4_t* W = reinterpret_cast<f32x4_t*>(a.w + e0);
+    if constexpr (MODE == MODE_ADAM) {
+      f32x4_t* M = reinterpret_cast<f32x4_t*>(a.m1 + e0);
+      f32x4_t* V = reinterpret_cast<f32x4_t*>(a.m2 + e0);
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) {
+        const int c = gl + v * G;
+        if (c >= D4) continue;
+        f32x4_t w = W[c], m = M[c], s = V[c];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          m[e] = fmaf(g[v][e], a.omb1, m[e] * a.b1);
+          s[e] = fmaf(g[v][e] * g[v][e], a.omb2, s[e] * a.b2);
+          w[e] = w[e] - a.lr * ((m[e] / a.bc1) / (sqrtf(s[e] / a.bc2) + a.eps) + a.wd * w[e]);
+        }
+        W[c] = w;
+        M[c] = m;
+        V[c] = s;
+      }
+    } else {
+      f32x4_t w[VEC];
+      float ss = 0.0f;
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) {
+        const int c = gl + v * G;
+        w[v] = c < D4 ? W[c] : f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        f32x4_t gg = g[v];
+        if (a.wd_mode == PDM_WD_L2) gg = gg + a.wd * w[v];
+        ss += gg[0] * gg[0] + gg[1] * gg[1] + gg[2] * gg[2] + gg[3] * gg[3];
+      }
+#pragma unroll
+      for (int o = G / 2; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+      const float gavg = ss / (float)a.D;
+      const float state = a.m1[key] + gavg;
+      const float mult = a.lr / (sqrtf(state) + a.eps);
+      const float corr = a.wd_mode == PDM_WD_L2 ? 1.0f - mult * a.wd : 1.0f;
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) {
+        const int c = gl + v * G;
+        if (c < D4) W[c] = corr * w[v] - mult * g[v];
+      }
+      if (gl == 0) a.m1[key] = state;
+    }
+  }
+}
+
+template <int G, int VEC, int MODE>
+__global__ __launch_bounds__(256) void bwd_accumulate_kernel(AccArgs a) {
+  constexpr int NG = 64 / G;
+  __shared__ uint32_t s_off[4][kChunk];
+  __shared__ float s_sc[4][kChunk];
+  __shared__ uint32_t s_key[4][kChunk];
+  __shared__ uint8_t s_head[4][kChunk];
+  __shared__ uint8_t s_tail[4][kChunk];
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  if constexpr (MODE == MODE_GRAD) {
+    if (blockIdx.x == 0 && threadIdx.x == 0) *a.out_count = (int64_t)a.num_heads[0];
+  }
+  const int64_t chunk = (int64_t)blockIdx.x * 4 + w;
+  if (chunk >= a.num_chunks) return;
+  const int64_t base = chunk * kChunk;
+  const uint32_t k = a.keys[base + lane];
+  const uint32_t pos = a.vals[base + lane];
+  const bool mine = k >= a.key_lo && k < a.key_hi && pos < a.num_indices;
+  if (__ballot(mine) == 0) return;
+  uint32_t kp = __shfl_up(k, 1), kn = __shfl_down(k, 1);
+  if (lane == 0) kp = base > 0 ? a.keys[base - 1] : ~k;
+  if (lane == 63) kn = base + kChunk < a.n_pad ? a.keys[base + kChunk] : ~k;
+  const bool pstart = mine && (lane == 0 || k != kp);
+  const bool pend = mine && (lane == 63 || k != kn);
+  const uint64_t starts = __ballot(pstart), ends = __ballot(pend);
+  const bool cont_first = __ballot(lane == 0 && mine && k == kp) != 0;
+  const bool cont_last = __ballot(lane == 63 && mine && k == kn) != 0;
+  uint2 rec = make_uint2(0u, 0u);
+  if (mine) rec = a.info[pos];
+  s_off[w][lane] = rec.x;
+  s_sc[w][lane] = __uint_as_float(rec.y);
+  const uint64_t lt = lanemask_lt(lane);
+  if (pstart) {
+    const int j = __popcll(starts & lt);
+    s_head[w][j] = (uint8_t)lane;
+    s_key[w][j] = k;
+  }
+  if (pend) s_tail[w][__popcll(ends & lt)] = (uint8_t)lane;
+  __builtin_amdgcn_wave_barrier();
+  const int nparts = __popcll(starts);
+  const int gl = lane % G;
+  const f32x4_t* grad4 = reinterpret_cast<const f32x4_t*>(a.grad);
+  const int D4 = a.D >> 2;
+  for (int j = lane / G; j < nparts; j += NG) {
+    const int h = s_head[w][j], e = s_tail[w][j];
+    f32x4_t acc[VEC];
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) acc[v] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    int i = h;
+    for (; i + 3 <= e; i += 4) {
+      f32x4_t gv[4][VEC];
+      float sc[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const uint32_t off = s_off[w][i + u];
+        sc[u] = s_sc[w][i + u];
+#pragma unroll
+        for (int v = 0; v < VEC; ++v)
+          gv[u][v] = gl + v * G < D4 ? grad4[off + gl + v * G] : f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int v = 0; v < VEC; ++v)
+#pragma unroll
+          for (int c = 0; c < 4; ++c) acc[v][c] = fmaf(sc[u], gv[u][v][c], acc[v][c]);
+    }
+    for (; i <= e; ++i) {
+      const uint32_t off = s_off[w][i];
+      const float sc = s_sc[w][i];
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) {
+        if (gl + v * G >= D4) continue;
+        const f32x4_t gv = grad4[off + gl + v * G];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[v][c] = fmaf(sc, gv[c], acc[v][c]);
+      }
+    }
+    const bool first_cont = j == 0 && cont_first;
+    const bool last_cont = j == nparts - 1 && cont_last;
+    if (first_cont || last_cont) {
+      f32x4_t* p = reinterpret_cast<f32x4_t*>((first_cont ? a.part_first : a.part_last) + chunk * a.D);
+#pragma unroll
+      for (int v = 0; v < VEC; ++v)
+        if (gl + v * G < D4) p[gl + v * G] = acc[v];
+    } else {
+      const int64_t slot = MODE == MODE_GRAD ? (int64_t)a.head_prefix[chunk] + j - (cont_first ? 1 : 0) : 0;
+      apply_row<G, VEC, MODE>(a, s_key[w][j], acc, gl, slot);
+    }
+  }
+}
+
+// Finishes the runs that cross chunk boundaries: the chunk holding a run's
+// first entry adds the partial sums of the following chunks in order.
+template <int G, int VEC, int MODE>
+__global__ __launch_bounds__(256) void bwd_fixup_kernel(AccArgs a) {
+  constexpr int NG = 64 / G;
+  const int lane = threadIdx.x & 63, gl = lane % G;
+  const int64_t chunk = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * NG + lane / G;
+  if (chunk >= a.num_chunks) return;
+  const int64_t base = chunk * kChunk, end = base + kChunk;
+  if (end >= a.n_pad) return;
+  const uint32_t key = a.keys[end - 1];
+  if (key < a.key_lo || key >= a.key_hi || a.keys[end] != key) return;
+  if (base > 0 && a.keys[base] == key && a.keys[base - 1] == key) return;  // began in an earlier chunk
+  const int D4 = a.D >> 2;
+  f32x4_t acc[VEC];
+  const f32x4_t* pl = reinterpret_cast<const f32x4_t*>(a.part_last + chunk * a.D);
+#pragma unroll
+  for (int v = 0; v < VEC; ++v) acc[v] = gl + v * G < D4 ? pl[gl + v * G] : f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int64_t c = chunk + 1;; ++c) {
+    const f32x4_t* pf = reinterpret_cast<const f32x4_t*>(a.part_first + c * a.D);
+#pragma unroll
+    for (int v = 0; v < VEC; ++v)
+      if (gl + v * G < D4) acc[v] = acc[v] + pf[gl + v * G];
+    const int64_t ce = (c + 1) * kChunk;
+    if (ce >= a.n_pad || a.keys[ce] != key) break;
+  }
+  const int64_t slot = MODE == MODE_GRAD ? (int64_t)a.head_prefix[chunk + 1] - 1 : 0;
+  apply_row<G, VEC, MODE>(a, key, acc, gl, slot);
+}
+
+// Distinct rows (of the key range) whose first entry lies in each chunk.
+__global__ __launch_bounds__(256) void bwd_count_heads_kernel(const uint32_t* __restrict__ keys,
+                                                              uint32_t* __restrict__ cnt, int64_t num_chunks,
+                                                              uint32_t key_lo, uint32_t key_hi) {
+  const int lane = threadIdx.x & 63;
+  const int64_t chunk = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (chunk >= num_chunks) return;
+  const int64_t base = chunk * kChunk;
+  const uint32_t k = keys[base + lane];
+  uint32_t kp = __shfl_up(k, 1);
+  if (lane == 0) kp = base > 0 ? keys[base - 1] : ~k;
+  const uint64_t heads = __ballot(k >= key_lo && k < key_hi && k != kp);
+  if (lane == 0) cnt[chunk] = (uint32_t)__popcll(heads);
+}
+
+__global__ void write_i64_kernel(int64_t* p, int64_t v) {
+  if (threadIdx.x == 0) *p = v;
+}
+
+// ---- host side --------------------------------------------------------------------
+
+struct BwdLayout {
+  int64_t n_pad, num_tiles, num_chunks, dmax;
+  int64_t keys_a, keys_b, vals_a, vals_b, info, hist, totals, part_first, part_last, total;
+};
+
+int64_t align256(int64_t v) { return (v + 255) & ~int64_t(255); }
+
+BwdLayout bwd_layout(const pdm_tbe_plan_s* plan, int64_t n) {
+  BwdLayout L{};
+  L.n_pad = (std::max<int64_t>(n, 1) + kTile - 1) / kTile * kTile;
+  L.num_tiles = L.n_pad / kTile;
+  L.num_chunks = L.n_pad / kChunk;
+  L.dmax = 4;
+  for (const auto& g : plan->bwd_groups) L.dmax = std::max<int64_t>(L.dmax, g.dim);
+  int64_t off = 0;
+  auto take = [&](int64_t bytes) {
+    const int64_t at = off;
+    off += align256(bytes);
+    return at;
+  };
+  L.keys_a = take(L.n_pad * 4);
+  L.keys_b = take(L.n_pad * 4);
+  L.vals_a = take(L.n_pad * 4);
+  L.vals_b = take(L.n_pad * 4);
+  L.info = take(std::max<int64_t>(n, 1) * 8);
+  L.hist = take(kBins * L.num_tiles * 4);
+  L.totals = take(kBins * 4);
+  L.part_first = take(L.num_chunks * L.dmax * 4);
+  L.part_last = take(L.num_chunks * L.dmax * 4);
+  L.total = off;
+  return L;
+}
+
+using AccFn = void (*)(AccArgs);
+
+template <int MODE>
+bool pick_acc(int D, AccFn& acc, AccFn& fix, int& ng) {
+  const int d4 = D / 4;
+#define PDM_ACC_CASE(G_, V_)                            \
+  {                                                     \
+    acc = bwd_accumulate_kernel<G_, V_, MODE>;          \
+    fix = bwd_fixup_kernel<G_, V_, MODE>;               \
+    ng = 64 / G_;                                       \
+    return true;                                        \
+  }
+  if (d4 <= 1) PDM_ACC_CASE(1, 1)
+  if (d4 <= 2) PDM_ACC_CASE(2, 1)
+  if (d4 <= 4) PDM_ACC_CASE(4, 1)
+  if (d4 <= 8) PDM_ACC_CASE(8, 1)
+  if (d4 <= 16) PDM_ACC_CASE(16, 1)
+  if (d4 <= 32) PDM_ACC_CASE(32, 1)
+  if (d4 <= 64) PDM_ACC_CASE(64, 1)
+  if (d4 <= 128) PDM_ACC_CASE(64, 2)
+  if (d4 <= 256) PDM_ACC_CASE(64, 4)
+#undef PDM_ACC_CASE
+  return false;
+}
+
+bool pick_acc_mode(int mode, int D, AccFn& acc, AccFn& fix, int& ng) {
+  switch (mode) {
+    case MODE_ADAM: return pick_acc<MODE_ADAM>(D, acc, fix, ng);
+    case MODE_ADAGRAD: return pick_acc<MODE_ADAGRAD>(D, acc, fix, ng);
+    default: return pick_acc<MODE_GRAD>(D, acc, fix, ng);
+  }
+}
+
+struct BwdCall {
+  pdm_tbe_plan plan;
+  int mode;
+  float* weights;
+  float* m1;
+  float* m2;
+  const void* indices;
+  int32_t index_bits;
+  int64_t num_indices;
+  const int64_t* offsets;
+  int64_t B;
+  int64_t padding_idx;
+  const float* grad;
+  int64_t grad_stride;
+  const pdm_optim_params* opt;
+  int64_t* out_ids;
+  float* out_rows;
+  int64_t* out_count;
+  void* ws;
+  int64_t ws_bytes;
+  int32_t* err;
+  hipStream_t stream;
+};
+
+int run_backward(const BwdCall& c) {
+  const pdm_tbe_plan_s* plan = c.plan;
+  PDM_CHECK_ARG(plan != nullptr, "null plan");
+  PDM_CHECK_ARG(c.index_bits == 32 || c.index_bits == 64, "index_bits must be 32 or 64");
+  PDM_CHECK_ARG(c.num_indices >= 0 && c.B >= 0, "negative size");
+  PDM_CHECK_ARG(c.num_indices < (int64_t)kSentinel - kTile, "num_indices must be < 2^32 - 4097");
+  PDM_CHECK_ARG(plan->total_rows < (int64_t)kSentinel, "the plan's row space must hold < 2^32 - 1 rows");
+  for (const auto& d : plan->tables) {
+    PDM_CHECK_ARG(d.dtype == PDM_F32 && d.row_bytes == 4 * d.dim, "the backward needs dense fp32 tables");
+    PDM_CHECK_ARG(d.weights_offset % 16 == 0, "the backward needs weights_offset a multiple of 16");
+    PDM_CHECK_ARG(d.out_offset % 4 == 0, "the backward needs out_offset a multiple of 4");
+    PDM_CHECK_ARG(d.dim <= 1024, "the backward supports dim <= 1024");
+  }
+  const int64_t T = (int64_t)plan->tables.size();
+  if (c.mode == MODE_GRAD) {
+    PDM_CHECK_ARG(plan->bwd_groups.size() == 1, "the sparse gradient needs one dim across the plan");
+    PDM_CHECK_ARG(c.out_ids && c.out_rows && c.out_count, "null output");
+    PDM_CHECK_ARG(((uintptr_t)c.out_rows & 15) == 0, "grad_rows must be 16-byte aligned");
+  } else {
+    const pdm_optim_params& o = *c.opt;
+    PDM_CHECK_ARG(c.weights && c.m1, "null weights or momentum1");
+    PDM_CHECK_ARG(((uintptr_t)c.weights & 15) == 0, "weights must be 16-byte aligned");
+    if (c.mode == MODE_ADAM) {
+      PDM_CHECK_ARG(c.m2 != nullptr, "Adam needs momentum2");
+      PDM_CHECK_ARG(((uintptr_t)c.m1 & 15) == 0 && ((uintptr_t)c.m2 & 15) == 0,
+                    "momentum buffers must be 16-byte aligned");
+      PDM_CHECK_ARG(o.step >= 1, "Adam step must be >= 1");
+      PDM_CHECK_ARG(o.beta1 >= 0.0f && o.beta1 < 1.0f && o.beta2 >= 0.0f && o.beta2 < 1.0f,
+                    "Adam betas must be in [0, 1)");
+    } else {
+      PDM_CHECK_ARG(o.weight_decay_mode == PDM_WD_NONE || o.weight_decay_mode == PDM_WD_L2,
+                    "weight_decay_mode must be PDM_WD_NONE or PDM_WD_L2");
+    }
+  }
+  const BwdLayout L = bwd_layout(plan, c.num_indices);
+  if (c.B == 0 || c.num_indices == 0) {
+    if (c.mode == MODE_GRAD) {
+      hipLaunchKernelGGL(write_i64_kernel, dim3(1), dim3(64), 0, c.stream, c.out_count, (int64_t)0);
+      PDM_CHECK_LAUNCH();
+    }
+    return PDM_OK;
+  }
+  PDM_CHECK_ARG(c.grad_stride >= plan->total_dim && c.grad_stride % 4 == 0,
+                "grad_row_stride must be >= the plan's total dim and a multiple of 4");
+  PDM_CHECK_ARG(c.B * c.grad_stride < (int64_t(1) << 34), "grad_out holds too many elements (>= 2^34)");
+  PDM_CHECK_ARG(c.indices && c.offsets && c.grad, "null device pointer");
+  PDM_CHECK_ARG(((uintptr_t)c.grad & 15) == 0, "grad_out must be 16-byte aligned");
+  PDM_CHECK_ARG(c.ws != nullptr && c.ws_bytes >= L.total,
+                "workspace smaller than pdm_tbe_backward_workspace_size");
+  PDM_CHECK_ARG(((uintptr_t)c.ws & 255) == 0, "workspace must be 256-byte aligned");
+  char* ws = reinterpret_cast<char*>(c.ws);
+  uint32_t* keys_a = reinterpret_cast<uint32_t*>(ws + L.keys_a);
+  uint32_t* keys_b = reinterpret_cast<uint32_t*>(ws + L.keys_b);
+  uint32_t* vals_a = reinterpret_cast<uint32_t*>(ws + L.vals_a);
+  uint32_t* vals_b = reinterpret_cast<uint32_t*>(ws + L.vals_b);
+  uint2* info = reinterpret_cast<uint2*>(ws + L.info);
+  uint32_t* hist = reinterpret_cast<uint32_t*>(ws + L.hist);
+  uint32_t* totals = reinterpret_cast<uint32_t*>(ws + L.totals);
+
+  // 1. keys and records
+  const int64_t n4 = L.n_pad / 4;
+  hipLaunchKernelGGL(fill_u32_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, c.stream, keys_a, n4,
+                     kSentinel);
+  PDM_CHECK_LAUNCH();
+  LinArgs la{c.indices, c.offsets, plan->d_bwd_slots, keys_a, info, c.err, c.num_indices, c.B, T * c.B,
+             c.padding_idx, c.grad_stride};
+  const int64_t lin_blocks = (T * c.B + 255) / 256;
+  PDM_CHECK_ARG(lin_blocks < (int64_t(1) << 31), "too many bags for one launch");
+  if (c.index_bits == 32)
+    hipLaunchKernelGGL(bwd_linearize_kernel<int32_t>, dim3((unsigned)lin_blocks), dim3(256), 0, c.stream, la);
+  else
+    hipLaunchKernelGGL(bwd_linearize_kernel<int64_t>, dim3((unsigned)lin_blocks), dim3(256), 0, c.stream, la);
+  PDM_CHECK_LAUNCH();
+
+  // 2. sort (key, position) on the bits the row space needs
+  int bits = 1;
+  while (bits < 32 && (int64_t(1) << bits) < plan->total_rows + 1) ++bits;
+  const int passes = (bits + 7) / 8;
+  uint32_t *kin = keys_a, *kout = keys_b, *vin = vals_a, *vout = vals_b;
+  for (int p = 0; p < passes; ++p) {
+    const int shift = 8 * p;
+    const int nb = std::min(8, bits - shift);
+    const uint32_t mask = (1u << nb) - 1u;
+    hipLaunchKernelGGL(radix_count_kernel, dim3((unsigned)L.num_tiles), dim3(kSortThreads), 0, c.stream, kin, hist,
+                       shift, mask, L.num_tiles);
+    PDM_CHECK_LAUNCH();
+    hipLaunchKernelGGL(scan_rows_kernel, dim3(kBins), dim3(256), 0, c.stream, hist, totals, L.num_tiles);
+    PDM_CHECK_LAUNCH();
+    if (p == 0)
+      hipLaunchKernelGGL(radix_scatter_kernel<true>, dim3((unsigned)L.num_tiles), dim3(kSortThreads), 0, c.stream,
+                         kin, (const uint32_t*)nullptr, kout, vout, hist, totals, shift, nb, L.num_tiles,
+                         (uint32_t)L.n_pad);
+    else
+      hipLaunchKernelGGL(radix_scatter_kernel<false>, dim3((unsigned)L.num_tiles), dim3(kSortThreads), 0, c.stream,
+                         kin, vin, kout, vout, hist, totals, shift, nb, L.num_tiles, (uint32_t)L.n_pad);
+    PDM_CHECK_LAUNCH();
+    std::swap(kin, kout);
+    std::swap(vin, vout);
+  }
+  // sorted data now in kin / vin
+
+  // 3. per dim group: accumulate runs, apply the optimizer
+  AccArgs a{};
+  a.keys = kin;
+  a.vals = vin;
+  a.info = info;
+  a.grad = c.grad;
+  a.w = c.weights;
+  a.m1 = c.m1;
+  a.m2 = c.m2;
+  a.part_first = reinterpret_cast<float*>(ws + L.part_first);
+  a.part_last = reinterpret_cast<float*>(ws + L.part_last);
+  a.n_pad = L.n_pad;
+  a.num_chunks = L.num_chunks;
+  a.num_indices = c.num_indices;
+  if (c.mode != MODE_GRAD) {
+    const pdm_optim_params& o = *c.opt;
+    a.wd_mode = o.weight_decay_mode;
+    a.lr = o.learning_rate;
+    a.eps = o.eps;
+    a.wd = o.weight_decay;
+    a.b1 = o.beta1;
+    a.b2 = o.beta2;
+    a.omb1 = 1.0f - o.beta1;
+    a.omb2 = 1.0f - o.beta2;
+    if (c.mode == MODE_ADAM) {
+      a.bc1 = 1.0f - powf(o.beta1, (float)o.step);
+      a.bc2 = 1.0f - powf(o.beta2, (float)o.step);
+    }
+  }
+  a.out_ids = c.out_ids;
+  a.out_rows = c.out_rows;
+  a.out_count = c.out_count;
+  const int64_t acc_blocks = L.num_chunks / 4;
+  for (const auto& g : plan->bwd_groups) {
+    if (g.num_tables == 0) {
+      if (c.mode == MODE_GRAD) {
+        hipLaunchKernelGGL(write_i64_kernel, dim3(1), dim3(64), 0, c.stream, c.out_count, (int64_t)0);
+        PDM_CHECK_LAUNCH();
+      }
+      continue;
+    }
+    AccFn acc = nullptr, fix = nullptr;
+    int ng = 1;
+    if (!pick_acc_mode(c.mode, g.dim, acc, fix, ng)) {
+      set_error("pdm_tbe_backward: unsupported dim " + std::to_string(g.dim));
+      return PDM_ERR_UNSUPPORTED;
+    }
+    a.tabs = plan->d_bwd_tables + g.first_table;
+    a.ntab = g.num_tables;
+    a.D = g.dim;
+    a.key_lo = (uint32_t)g.row_lo;
+    a.key_hi = (uint32_t)g.row_hi;
+    if (c.mode == MODE_GRAD) {
+      hipLaunchKernelGGL(bwd_count_heads_kernel, dim3((unsigned)acc_blocks), dim3(256), 0, c.stream, kin, hist,
+                         L.num_chunks, a.key_lo, a.key_hi);
+      PDM_CHECK_LAUNCH();
+      hipLaunchKernelGGL(scan_rows_kernel, dim3(1), dim3(256), 0, c.stream, hist, totals, L.num_chunks);
+      PDM_CHECK_LAUNCH();
+      a.head_prefix = hist;
+      a.num_heads = totals;
+    }
+    hipLaunchKernelGGL(acc, dim3((unsigned)acc_blocks), dim3(256), 0, c.stream, a);
+    PDM_CHECK_LAUNCH();
+    const int64_t fix_blocks = (L.num_chunks + 4 * ng - 1) / (4 * ng);
+    hipLaunchKernelGGL(fix, dim3((unsigned)fix_blocks), dim3(256), 0, c.stream, a);
+    PDM_CHECK_LAUNCH();
+  }
+  return PDM_OK;
+}
+
+}  // namespace
+
+}  // namespace pdm
+
+using namespace pdm;
+
+extern "C" int64_t pdm_tbe_backward_workspace_size(pdm_tbe_plan plan, int64_t num_indices) {
+  if (!plan || num_indices < 0) return -1;
+  return bwd_layout(plan, num_indices).total;
+}
+
+extern "C" int pdm_tbe_backward_fused(pdm_tbe_plan plan, float* weights, float* momentum1, float* momentum2,
+                                      const void* indices, int32_t index_bits, int64_t num_indices,
+                                      const int64_t* offsets, int64_t batch_size, int64_t padding_idx,
+                                      const float* grad_out, int64_t grad_row_stride, const pdm_optim_params* opt,
+                                      void* workspace, int64_t workspace_bytes, int32_t* err_flag,
+                                      pdm_stream_t stream) {
+  clear_error();
+  PDM_CHECK_ARG(opt != nullptr, "null optimizer parameters");
+  PDM_CHECK_ARG(opt->optimizer == PDM_OPT_ADAM || opt->optimizer == PDM_OPT_ROWWISE_ADAGRAD,
+                "optimizer must be PDM_OPT_ADAM or PDM_OPT_ROWWISE_ADAGRAD");
+  BwdCall c{plan, opt->optimizer == PDM_OPT_ADAM ? MODE_ADAM : MODE_ADAGRAD, weights, momentum1, momentum2,
+            indices, index_bits, num_indices, offsets, batch_size, padding_idx, grad_out, grad_row_stride, opt,
+            nullptr, nullptr, nullptr, workspace, workspace_bytes, err_flag,
+            reinterpret_cast<hipStream_t>(stream)};
+  return run_backward(c);
+}
+
+extern "C" int pdm_tbe_backward_sparse_grad(pdm_tbe_plan plan, const void* indices, int32_t index_bits,
+                                            int64_t num_indices, const int64_t* offsets, int64_t batch_size,
+                                            int64_t padding_idx, const float* grad_out, int64_t grad_row_stride,
+                                            int64_t* row_ids, float* grad_rows, int64_t* num_unique,
+                                            void* workspace, int64_t workspace_bytes, int32_t* err_flag,
+                                            pdm_stream_t stream) {
+  clear_error();
+  BwdCall c{plan, MODE_GRAD, nullptr, nullptr, nullptr, indices, index_bits, num_indices, offsets, batch_size,
+            padding_idx, grad_out, grad_row_stride, nullptr, row_ids, grad_rows, num_unique, workspace,
+            workspace_bytes, err_flag, reinterpret_cast<hipStream_t>(stream)};
+  return run_backward(c);
+}

@@ -21,19 +21,11 @@
 #include <vector>
 
 #include "pdm_common.h"
+#include "tbe_plan.h"
 
 #pragma clang fp contract(off)
 
 namespace pdm {
-
-struct TbeMeta {
-  int64_t rows;
-  int64_t w_off;  // byte offset of row 0 inside the weights buffer
-  int32_t row_bytes;
-  int32_t out_col;
-  int32_t pooling;
-  int32_t dim;
-};
 
 struct TbeArgs {
   const char* weights;
@@ -593,26 +585,6 @@ __global__ __launch_bounds__(256) void int8_quantize_kernel(const float* __restr
 
 using namespace pdm;
 
-struct TbeGroup {
-  int32_t dtype;
-  int32_t dim;
-  int32_t row_bytes_all;  // common row stride, -1 if tables differ
-  int32_t first;          // index into the grouped table list
-  int32_t count;
-  int32_t out_col_align;    // alignment (elements) of all out_offsets
-  int32_t table_base;       // first table if the group's tables are consecutive, else -1
-};
-
-struct pdm_tbe_plan_s {
-  int device = 0;
-  std::vector<pdm_table_desc> tables;
-  std::vector<TbeGroup> groups;
-  TbeMeta* d_meta = nullptr;
-  int32_t* d_group_tables = nullptr;
-  int64_t total_dim = 0;
-  ~pdm_tbe_plan_s();
-};
-
 static int32_t default_row_bytes(int dtype, int dim) {
   switch (dtype) {
     case PDM_F32: return 4 * dim;
@@ -673,23 +645,73 @@ extern "C" int pdm_tbe_plan_create(const pdm_table_desc* tables, int32_t num_tab
     }
     plan->groups.push_back(g);
   }
+  // Row space (backward keys, row-wise optimizer state): the distinct tables,
+  // numbered group by group and in table order inside a group.  Slots with the
+  // same (weights_offset, rows, dim, dtype, row_bytes) read one table and
+  // share its rows.
+  std::vector<BwdTable> btabs;
+  std::vector<BwdSlot> bslots(num_tables);
+  plan->slot_row_off.assign(num_tables, 0);
+  for (const auto& g : plan->groups) {
+    BwdGroup bg{g.dim, g.dtype, (int32_t)btabs.size(), 0, 1, 0, plan->total_rows, 0};
+    for (int i = 0; i < g.count; ++i) {
+      const int t = order[g.first + i];
+      const auto& d = plan->tables[t];
+      int same = -1;
+      for (int u = 0; u < t && same < 0; ++u) {
+        const auto& e = plan->tables[u];
+        if (e.weights_offset == d.weights_offset && e.rows == d.rows && e.dim == d.dim && e.dtype == d.dtype &&
+            e.row_bytes == d.row_bytes)
+          same = u;
+      }
+      if (same >= 0) {
+        plan->slot_row_off[t] = plan->slot_row_off[same];
+      } else {
+        plan->slot_row_off[t] = plan->total_rows;
+        if (d.rows > 0) {
+          btabs.push_back(BwdTable{plan->total_rows, d.weights_offset / 4});
+          ++bg.num_tables;
+        }
+        plan->total_rows += d.rows;
+      }
+      if (d.row_bytes != 4 * d.dim) bg.dense_rows = 0;
+      bslots[t] = BwdSlot{d.rows, plan->slot_row_off[t], d.out_offset, d.pooling};
+    }
+    bg.row_hi = plan->total_rows;
+    plan->bwd_groups.push_back(bg);
+  }
+  if (btabs.empty()) btabs.push_back(BwdTable{0, 0});
   PDM_CHECK_HIP(hipGetDevice(&plan->device));
   PDM_CHECK_HIP(hipMalloc(&plan->d_meta, sizeof(TbeMeta) * num_tables));
   PDM_CHECK_HIP(hipMalloc(&plan->d_group_tables, sizeof(int32_t) * num_tables));
+  PDM_CHECK_HIP(hipMalloc(&plan->d_bwd_slots, sizeof(BwdSlot) * num_tables));
+  PDM_CHECK_HIP(hipMalloc(&plan->d_bwd_tables, sizeof(BwdTable) * btabs.size()));
   PDM_CHECK_HIP(hipMemcpy(plan->d_meta, meta.data(), sizeof(TbeMeta) * num_tables, hipMemcpyHostToDevice));
   PDM_CHECK_HIP(hipMemcpy(plan->d_group_tables, order.data(), sizeof(int32_t) * num_tables, hipMemcpyHostToDevice));
+  PDM_CHECK_HIP(hipMemcpy(plan->d_bwd_slots, bslots.data(), sizeof(BwdSlot) * num_tables, hipMemcpyHostToDevice));
+  PDM_CHECK_HIP(
+      hipMemcpy(plan->d_bwd_tables, btabs.data(), sizeof(BwdTable) * btabs.size(), hipMemcpyHostToDevice));
   *plan_out = plan.release();
   return PDM_OK;
 }
 
 pdm_tbe_plan_s::~pdm_tbe_plan_s() {
-  if (!d_meta && !d_group_tables) return;
+  if (!d_meta && !d_group_tables && !d_bwd_slots && !d_bwd_tables) return;
   int cur = 0;
   (void)hipGetDevice(&cur);
   (void)hipSetDevice(device);
   if (d_meta) (void)hipFree(d_meta);
   if (d_group_tables) (void)hipFree(d_group_tables);
+  if (d_bwd_slots) (void)hipFree(d_bwd_slots);
+  if (d_bwd_tables) (void)hipFree(d_bwd_tables);
   (void)hipSetDevice(cur);
+}
+
+extern "C" int64_t pdm_tbe_plan_total_rows(pdm_tbe_plan plan) { return plan ? plan->total_rows : -1; }
+
+extern "C" int64_t pdm_tbe_plan_row_offset(pdm_tbe_plan plan, int32_t slot) {
+  if (!plan || slot < 0 || slot >= (int32_t)plan->slot_row_off.size()) return -1;
+  return plan->slot_row_off[slot];
 }
 
 extern "C" int pdm_tbe_plan_destroy(pdm_tbe_plan plan) {

@@ -70,7 +70,11 @@ class TbePlan:
         self.handle = handle
         self.device = torch.device(device)
         self.num_slots = len(slots)
+        self.dims = [int(s["dim"]) for s in slots]
+        self.fp32_extent = max(int(s["weights_offset"]) + int(s["rows"]) * 4 * int(s["dim"]) for s in slots)
         self.total_dim = int(L.lib().pdm_tbe_plan_total_dim(handle))
+        self.total_rows = int(L.lib().pdm_tbe_plan_total_rows(handle))
+        self.row_offsets = [int(L.lib().pdm_tbe_plan_row_offset(handle, i)) for i in range(len(slots))]
         with TbePlan._lock:
             self.plan_id = next(TbePlan._ids)
             TbePlan._registry[self.plan_id] = self
@@ -127,6 +131,98 @@ def tbe_pooled_raw(plan: TbePlan, weights: torch.Tensor, indices: torch.Tensor, 
         L.stream_ptr(dev))
     L.check(status, "pdm_tbe_pooled_fwd")
     return out
+
+
+def tbe_backward_workspace(plan: TbePlan, num_indices: int, device=None) -> torch.Tensor:
+    """Device workspace for pdm_tbe_backward_fused / _sparse_grad over ``num_indices`` lookups."""
+    n = int(L.lib().pdm_tbe_backward_workspace_size(plan.handle, int(num_indices)))
+    if n < 0:
+        raise ValueError("bad plan or num_indices")
+    return torch.empty(n, dtype=torch.uint8, device=device if device is not None else plan.device)
+
+
+def _check_bwd_inputs(plan: TbePlan, indices, offsets, batch_size, grad_out, workspace):
+    if indices.dtype not in (torch.int32, torch.int64):
+        raise TypeError(f"indices must be int32 or int64, got {indices.dtype}")
+    if offsets.dtype != torch.int64:
+        raise TypeError(f"offsets must be int64, got {offsets.dtype}")
+    if not (indices.is_contiguous() and offsets.is_contiguous()):
+        raise ValueError("indices and offsets must be contiguous")
+    if offsets.numel() != plan.num_slots * batch_size + 1:
+        raise ValueError(f"offsets has {offsets.numel()} entries, expected T*B+1 = "
+                         f"{plan.num_slots * batch_size + 1}")
+    if grad_out.dtype != torch.float32 or grad_out.dim() != 2 or grad_out.shape[0] != batch_size \
+            or (grad_out.numel() and grad_out.stride(1) != 1) or grad_out.shape[1] < plan.total_dim:
+        raise ValueError("grad_out must be float32 [B, >= total_dim] with unit column stride")
+    if workspace is None:
+        workspace = tbe_backward_workspace(plan, indices.numel(), grad_out.device)
+    if workspace.dtype != torch.uint8 or not workspace.is_contiguous():
+        raise ValueError("workspace must be a contiguous uint8 tensor")
+    return workspace
+
+
+def tbe_backward_fused_raw(plan: TbePlan, weights: torch.Tensor, momentum1: torch.Tensor,
+                           momentum2: Optional[torch.Tensor], indices: torch.Tensor, offsets: torch.Tensor,
+                           batch_size: int, grad_out: torch.Tensor, optimizer: int = L.PDM_OPT_ADAM,
+                           learning_rate: float = 0.01, eps: float = 1e-8, beta1: float = 0.9,
+                           beta2: float = 0.999, weight_decay: float = 0.0, weight_decay_mode: int = L.PDM_WD_NONE,
+                           step: int = 1, padding_idx: int = -1, workspace: Optional[torch.Tensor] = None,
+                           err_flag: Optional[torch.Tensor] = None) -> None:
+    """Launches pdm_tbe_backward_fused: updates ``weights`` (the plan's fp32 table buffer) and the
+    optimizer state in place from d(loss)/d(pooled output) ``grad_out`` [B, >= total_dim]."""
+    dev = _require_cuda(weights, momentum1, momentum2, indices, offsets, grad_out, workspace, err_flag)
+    workspace = _check_bwd_inputs(plan, indices, offsets, batch_size, grad_out, workspace)
+    for name, t in (("weights", weights), ("momentum1", momentum1), ("momentum2", momentum2)):
+        if t is not None and not t.is_contiguous():
+            raise ValueError(f"{name} must be contiguous")
+    if momentum1.dtype != torch.float32 or (momentum2 is not None and momentum2.dtype != torch.float32):
+        raise TypeError("optimizer state must be float32")
+
+    def nbytes(t):
+        return t.numel() * t.element_size()
+
+    if nbytes(weights) < plan.fp32_extent:
+        raise ValueError("weights is smaller than the plan's fp32 tables")
+    if optimizer == L.PDM_OPT_ADAM:
+        if momentum2 is None or nbytes(momentum1) < plan.fp32_extent or nbytes(momentum2) < plan.fp32_extent:
+            raise ValueError("Adam state must be laid out like the weights (as many bytes)")
+    elif momentum1.numel() < plan.total_rows:
+        raise ValueError(f"row-wise state needs {plan.total_rows} entries (one per row id)")
+    if err_flag is not None and (err_flag.dtype != torch.int32 or err_flag.numel() < 1):
+        raise ValueError("err_flag must be an int32 tensor with at least one element")
+    opt = L.OptimParams(int(optimizer), int(weight_decay_mode), float(learning_rate), float(eps), float(beta1),
+                        float(beta2), float(weight_decay), 0, int(step))
+    status = L.lib().pdm_tbe_backward_fused(
+        plan.handle, weights.data_ptr(), momentum1.data_ptr(), _ptr(momentum2),
+        indices.data_ptr() if indices.numel() else None, 32 if indices.dtype == torch.int32 else 64,
+        indices.numel(), offsets.data_ptr(), batch_size, padding_idx, grad_out.data_ptr(), grad_out.stride(0),
+        ctypes.byref(opt), workspace.data_ptr(), workspace.numel(), _ptr(err_flag), L.stream_ptr(dev))
+    L.check(status, "pdm_tbe_backward_fused")
+
+
+def tbe_backward_sparse_grad_raw(plan: TbePlan, indices: torch.Tensor, offsets: torch.Tensor, batch_size: int,
+                                 grad_out: torch.Tensor, padding_idx: int = -1,
+                                 workspace: Optional[torch.Tensor] = None,
+                                 err_flag: Optional[torch.Tensor] = None):
+    """Launches pdm_tbe_backward_sparse_grad; returns (row_ids [N] int64, grad_rows [N, D] float32,
+    num_unique int64 scalar tensor): the first num_unique entries are the distinct row ids (ascending)
+    and their gradients."""
+    dev = _require_cuda(indices, offsets, grad_out, workspace, err_flag)
+    workspace = _check_bwd_inputs(plan, indices, offsets, batch_size, grad_out, workspace)
+    n = max(indices.numel(), 1)
+    if len(set(plan.dims)) != 1:
+        raise ValueError("the sparse gradient needs one dim across the plan")
+    D = plan.dims[0]
+    row_ids = torch.empty(n, dtype=torch.int64, device=dev)
+    grad_rows = torch.empty((n, D), dtype=torch.float32, device=dev)
+    num_unique = torch.empty((), dtype=torch.int64, device=dev)
+    status = L.lib().pdm_tbe_backward_sparse_grad(
+        plan.handle, indices.data_ptr() if indices.numel() else None, 32 if indices.dtype == torch.int32 else 64,
+        indices.numel(), offsets.data_ptr(), batch_size, padding_idx, grad_out.data_ptr(), grad_out.stride(0),
+        row_ids.data_ptr(), grad_rows.data_ptr(), num_unique.data_ptr(), workspace.data_ptr(), workspace.numel(),
+        _ptr(err_flag), L.stream_ptr(dev))
+    L.check(status, "pdm_tbe_backward_sparse_grad")
+    return row_ids, grad_rows, num_unique
 
 
 _DTYPE_CODES = {0: torch.float32, 1: torch.float16, 2: torch.bfloat16}

@@ -33,6 +33,7 @@ def test_struct_layouts_match_header(pdm):
     assert ctypes.sizeof(L.BlockWeights) == 72
     assert L.SeqDesc.max_len.offset == 32
     assert ctypes.sizeof(L.SeqDesc) == 32 + 4 * 8 + 4 * 8 + 8 * 8 + 8 * 8
+    assert ctypes.sizeof(L.OptimParams) == 40 and L.OptimParams.step.offset == 32
 
 
 def test_argument_errors_are_reported_not_raised(pdm):
@@ -57,6 +58,21 @@ def test_argument_errors_are_reported_not_raised(pdm):
     two = (ctypes.c_int64 * 2)(1, 1)
     assert lib.pdm_cross_hash_fwd(None, two, 2, 4, 0, 0, None, None) == L.PDM_ERR_INVALID
     assert "table_size" in L.last_error()
+    assert lib.pdm_tbe_backward_workspace_size(None, 10) == -1
+    assert lib.pdm_tbe_plan_total_rows(None) == -1 and lib.pdm_tbe_plan_row_offset(None, 0) == -1
+    assert lib.pdm_tbe_backward_fused(None, None, None, None, None, 64, 0, None, 1, -1, None, 8, None, None, 0,
+                                      None, None) == L.PDM_ERR_INVALID
+    assert "optimizer" in L.last_error()
+    opt = L.OptimParams(L.PDM_OPT_ADAM, 0, 0.01, 1e-8, 0.9, 0.999, 0.0, 0, 1)
+    assert lib.pdm_tbe_backward_fused(None, None, None, None, None, 64, 0, None, 1, -1, None, 8, ctypes.byref(opt),
+                                      None, 0, None, None) == L.PDM_ERR_INVALID
+    assert "null plan" in L.last_error()
+    opt.optimizer = 7
+    assert lib.pdm_tbe_backward_fused(None, None, None, None, None, 64, 0, None, 1, -1, None, 8, ctypes.byref(opt),
+                                      None, 0, None, None) == L.PDM_ERR_INVALID
+    assert lib.pdm_tbe_backward_sparse_grad(None, None, 64, 0, None, 1, -1, None, 8, None, None, None, None, 0, None,
+                                            None) == L.PDM_ERR_INVALID
+    assert "null plan" in L.last_error()
 
 
 def test_ops_refuse_cpu_tensors(pdm):
