@@ -10,6 +10,9 @@ fp32 out).  ``--workload`` selects another:
   seq_gather  3 behaviour pools, item 10M x 256 + artist 1M x 64 + album 2M x 64 bf16, B=1024
   onetrans    4-layer OneTrans block stack, B=1024, 384 S + 16 NS tokens, d 256, schedule 384/256/128/64
   cross_hash  cross-feature ids: xxHash64 of (uid, artist_id) int64 pairs % 100,000,000, 16,777,216 rows
+  train_adam  pooled backward + fused Adam (lr 1e-2, eps 1e-8, wd 1e-5): 8 tables x 10,000,000 x 64 fp32,
+              sum, Poisson(10) bags in [0, 50], uniform ids, B=65,536 (about 5.2 M lookups)
+  train_rowwise_adagrad  the same with fused row-wise Adagrad (L2 weight decay 1e-5)
   copy_1gib   calibration only: a 1 GiB device-to-device copy (the HBM counters' reference kernel)
 
 A step is one forward of the path over one batch already resident in HBM.
@@ -170,6 +173,90 @@ def cpu_pooled(orc, w, threads: int, row_cap: int, weight_std: float):
 
 
 # ----------------------------------------------------------------------------------------------
+# pooled backward + fused optimizer
+# ----------------------------------------------------------------------------------------------
+
+def setup_train(pdm, torch, dev, w, optimizer: str):
+    """fp32 tables of ``w`` with zeroed optimizer state; a step is one fused backward + update over the
+    batch with a fixed output gradient.  Returns (step, algorithmic bytes, distinct rows, keepalive)."""
+    L = pdm._lib
+    D = w.dim
+    offs, off = [], 0
+    for r in w.rows:
+        off = (off + 255) // 256 * 256
+        offs.append(off)
+        off += r * D * 4
+    log(f"allocating {off / 1e9:.2f} GB of fp32 tables (+ optimizer state)")
+    flat = torch.empty(off // 4, dtype=torch.float32, device=dev)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(1007)
+    for r0 in range(0, flat.numel(), 1 << 26):
+        flat[r0:r0 + (1 << 26)].uniform_(-0.01, 0.01, generator=gen)
+    slots, col = [], 0
+    for t, r in enumerate(w.rows):
+        slots.append(dict(rows=r, weights_offset=offs[t], dim=D, dtype=L.PDM_F32, pooling=L.PDM_POOL_SUM,
+                          row_bytes=4 * D, out_offset=col))
+        col += D
+    plan = pdm.ops.TbePlan(slots, dev)
+    adam = optimizer == "adam"
+    m1 = torch.zeros_like(flat) if adam else torch.zeros(plan.total_rows, dtype=torch.float32, device=dev)
+    m2 = torch.zeros_like(flat) if adam else None
+    indices = torch.from_numpy(w.indices).to(dev)
+    offsets = torch.from_numpy(w.offsets).to(dev)
+    grad = torch.randn(w.batch, col, device=dev, generator=gen)
+    ws = pdm.ops.tbe_backward_workspace(plan, indices.numel(), w.batch, dev)
+    counter = [0]
+    opt = L.PDM_OPT_ADAM if adam else L.PDM_OPT_ROWWISE_ADAGRAD
+
+    def step():
+        counter[0] += 1
+        pdm.ops.tbe_backward_fused_raw(plan, flat, m1, m2, indices, offsets, w.batch, grad, optimizer=opt,
+                                       learning_rate=0.01, eps=1e-8, weight_decay=1e-5,
+                                       weight_decay_mode=L.PDM_WD_L2, step=counter[0], workspace=ws)
+
+    distinct = 0
+    for t in range(len(w.rows)):
+        seg = w.indices[w.offsets[t * w.batch]:w.offsets[(t + 1) * w.batch]]
+        distinct += int(np.unique(seg).size)
+    n = w.num_lookups
+    per_row = 6 * D * 4 if adam else 2 * D * 4 + 8  # weights (+ state) read and written once per distinct row
+    alg_bytes = n * 8 + w.offsets.size * 8 + w.batch * col * 4 + distinct * per_row
+    return step, alg_bytes, distinct, (flat, m1, m2, plan, indices, offsets, grad, ws)
+
+
+def cpu_train(orc, w, optimizer: str, batch: int, row_cap: int):
+    """The oracle's backward + update over the first ``batch`` bags of every table, on tables capped at
+    ``row_cap`` rows (ids taken modulo)."""
+    D, T = w.dim, len(w.rows)
+    rows = [min(r, row_cap) for r in w.rows]
+    g = np.random.default_rng(8)
+    slots, off = [], 0
+    for t, r in enumerate(rows):
+        slots.append(dict(rows=r, weights_offset=off * 4, dim=D, dtype="fp32", pooling="sum", row_bytes=0,
+                          out_offset=t * D))
+        off += r * D
+    lens = np.diff(w.offsets).reshape(T, w.batch)[:, :batch]
+    idx = np.concatenate([w.indices[w.offsets[t * w.batch]:w.offsets[t * w.batch] + int(lens[t].sum())] % rows[t]
+                          for t in range(T)])
+    offsets = orc.offsets_np(lens.reshape(-1))
+    grad = g.standard_normal((batch, T * D), dtype=np.float32)
+    flat = (g.random(off, dtype=np.float32) - np.float32(0.5)) * np.float32(0.02)
+    adam = optimizer == "adam"
+    m1 = np.zeros(off if adam else sum(rows), dtype=np.float32)
+    m2 = np.zeros(off if adam else 1, dtype=np.float32)
+    step = [0]
+
+    def run():
+        step[0] += 1
+        orc.tbe_backward(slots, idx, offsets, batch, grad, optimizer=orc.ADAM if adam else orc.ROWWISE_ADAGRAD,
+                         weights=flat, m1=m1, m2=m2, lr=0.01, eps=1e-8, weight_decay=1e-5, wd_mode=orc.WD_L2,
+                         step=step[0])
+
+    sec = time_cpu(run)
+    return idx.size, sec
+
+
+# ----------------------------------------------------------------------------------------------
 # S-token gather
 # ----------------------------------------------------------------------------------------------
 
@@ -269,7 +356,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="single_hot",
                     choices=["single_hot", "ebc_fp32", "int8_mean", "seq_gather", "onetrans", "cross_hash",
-                             "copy_1gib"])
+                             "train_adam", "train_rowwise_adagrad", "copy_1gib"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
 
@@ -343,6 +430,23 @@ def main() -> int:
             sec = time_cpu(lambda: orc.cross_hash([uid, artist], table_size, 0))
             return {"value": round(n_rows / sec, 1), "unit": unit, "cores": threads, "kind": "port",
                     "sample": f"C oracle (XXH64 per row, OpenMP), all {n_rows} rows, median of 5 reps = {sec:.3f} s"}
+    elif args.workload in ("train_adam", "train_rowwise_adagrad"):
+        optimizer = "adam" if args.workload == "train_adam" else "rowwise_adagrad"
+        w = syn.ebc_fp32(scale_rows=100.0, batch=65_536)
+        step, alg, distinct, keep = setup_train(pdm, torch, dev, w, optimizer)
+        units, unit, bound, dtype = w.num_lookups, "lookups/s", "hbm", "f32"
+        cfg = {"workload": f"{w.name}_{optimizer}", "tables": w.num_tables, "rows_total": int(sum(w.rows)),
+               "dim": w.dim, "batch": w.batch, "lookups_per_batch": w.num_lookups, "distinct_rows": distinct,
+               "pooling": "sum", "weights": "fp32", "optimizer": optimizer, "lr": 0.01, "eps": 1e-8,
+               "weight_decay": 1e-5, "timed": "whole fused backward (linearise, 3 radix passes, accumulate)"}
+        cpu_b, cpu_cap = 16_384, 250_000
+
+        def cpu_fn():
+            n, sec = cpu_train(orc, w, optimizer, cpu_b, cpu_cap)
+            return {"value": round(n / sec, 1), "unit": unit, "cores": 1, "kind": "port",
+                    "sample": f"C oracle (one thread): backward + {optimizer} over the first {cpu_b} bags of each "
+                              f"table ({n} lookups) on tables capped at {cpu_cap} rows (ids modulo), "
+                              f"median of 5 reps = {sec:.3f} s"}
     elif args.workload == "copy_1gib":
         # calibration: a plain device copy of 1 GiB (reads 1 GiB, writes 1 GiB) for the HBM counters
         src = torch.ones(1 << 28, dtype=torch.float32, device=dev)

@@ -159,8 +159,10 @@ typedef struct {
 int64_t pdm_tbe_plan_total_rows(pdm_tbe_plan plan);
 int64_t pdm_tbe_plan_row_offset(pdm_tbe_plan plan, int32_t slot);
 
-/* Device workspace bytes the backward needs for num_indices lookups. */
-int64_t pdm_tbe_backward_workspace_size(pdm_tbe_plan plan, int64_t num_indices);
+/* Device workspace bytes the backward needs for num_indices lookups over
+ * batch_size bags per slot. */
+int64_t pdm_tbe_backward_workspace_size(pdm_tbe_plan plan, int64_t num_indices,
+                                        int64_t batch_size);
 
 /* Fused backward + optimizer update, in place.
  * weights:   device fp32 base (every slot PDM_F32, row_bytes == 4 * dim,

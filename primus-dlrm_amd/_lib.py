@@ -161,7 +161,7 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.pdm_tbe_plan_row_offset.restype = i64
     lib.pdm_tbe_plan_row_offset.argtypes = [vp, i32]
     lib.pdm_tbe_backward_workspace_size.restype = i64
-    lib.pdm_tbe_backward_workspace_size.argtypes = [vp, i64]
+    lib.pdm_tbe_backward_workspace_size.argtypes = [vp, i64, i64]
     lib.pdm_tbe_backward_fused.restype = ctypes.c_int
     lib.pdm_tbe_backward_fused.argtypes = [vp, vp, vp, vp, vp, i32, i64, vp, i64, i64, vp, i64,
                                            ctypes.POINTER(OptimParams), vp, i64, vp, vp]

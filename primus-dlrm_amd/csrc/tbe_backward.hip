@@ -81,53 +81,94 @@ struct LinArgs {
   const void* indices;
   const int64_t* offsets;
   const BwdSlot* slots;
-  uint32_t* keys;  // [n_pad], pre-filled with the sentinel
-  uint2* info;     // [num_indices] {gradient float4 index, scale bits}
+  uint32_t* keys;    // [n_pad], pre-filled with the sentinel
+  uint32_t* bags;    // [n_pad] bag id (t * B + b) of each lookup
+  float* bag_scale;  // [num_bags] 1 / pooled ids of the bag (written when a slot pools by mean)
   int32_t* err;
   int64_t num_indices;
-  int64_t B;
   int64_t num_bags;
   int64_t padding_idx;
-  int64_t grad_stride;
+  uint32_t B;
+  int32_t has_mean;
 };
 
-// One thread per bag: counts the bag's pooled ids (mean scale), then writes a
-// key and a record for each of them.  A bag whose offsets are malformed is
-// skipped and flagged; an id outside [0, rows) is skipped and flagged.
+constexpr int kLinBags = 256;
+
+// A block owns 256 consecutive bags and the lookups between their offsets:
+// lanes walk those positions with coalesced index reads and key / bag writes,
+// finding each position's bag by binary search over the block's offsets in
+// LDS, and count the pooled ids per bag for the mean scale.  A block whose
+// offsets are malformed (decreasing, negative or past num_indices) flags the
+// error and handles its well-formed bags one per thread.  Out-of-range ids
+// are skipped and flagged; padding ids are skipped.
 template <typename IdxT>
 __global__ __launch_bounds__(256) void bwd_linearize_kernel(LinArgs a) {
-  const int64_t bag = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (bag >= a.num_bags) return;
-  const int64_t t = bag / a.B;
-  const int64_t b = bag - t * a.B;
-  const BwdSlot s = a.slots[t];
-  const int64_t lo = a.offsets[bag], hi = a.offsets[bag + 1];
-  if (lo < 0 || hi < lo || hi > a.num_indices) {
-    if (a.err) *a.err = 1;
+  __shared__ int64_t s_off[kLinBags + 1];
+  __shared__ uint32_t s_cnt[kLinBags];
+  __shared__ int s_bad;
+  const int tid = threadIdx.x;
+  const int64_t bag0 = (int64_t)blockIdx.x * kLinBags;
+  const int nb = (int)(a.num_bags - bag0 < kLinBags ? a.num_bags - bag0 : kLinBags);
+  for (int i = tid; i <= nb; i += 256) s_off[i] = a.offsets[bag0 + i];
+  s_cnt[tid] = 0;
+  if (tid == 0) s_bad = 0;
+  __syncthreads();
+  if (tid < nb) {
+    const int64_t lo = s_off[tid], hi = s_off[tid + 1];
+    if (lo < 0 || hi < lo || hi > a.num_indices) s_bad = 1;
+  }
+  __syncthreads();
+  const IdxT* idx = reinterpret_cast<const IdxT*>(a.indices);
+  const bool has_pad = a.padding_idx >= 0;
+  if (s_bad) {
+    if (tid == 0 && a.err) *a.err = 1;
+    if (tid >= nb) return;
+    const int64_t lo = s_off[tid], hi = s_off[tid + 1];
+    if (lo < 0 || hi < lo || hi > a.num_indices) return;
+    const uint32_t bag = (uint32_t)(bag0 + tid);
+    const BwdSlot sl = a.slots[bag / a.B];
+    uint32_t cnt = 0;
+    bool bad = false;
+    for (int64_t p = lo; p < hi; ++p) {
+      const int64_t v = (int64_t)idx[p];
+      if (has_pad && v == a.padding_idx) continue;
+      if (v < 0 || v >= sl.rows) {
+        bad = true;
+        continue;
+      }
+      a.keys[p] = (uint32_t)(sl.row_off + v);
+      a.bags[p] = bag;
+      ++cnt;
+    }
+    if (bad && a.err) *a.err = 1;
+    if (a.has_mean) a.bag_scale[bag] = cnt > 0 ? 1.0f / (float)cnt : 0.0f;
     return;
   }
-  const IdxT* idx = reinterpret_cast<const IdxT*>(a.indices);
-  int64_t cnt = 0;
+  const int64_t p0 = s_off[0], p1 = s_off[nb];
   bool bad = false;
-  const bool has_pad = a.padding_idx >= 0;
-  for (int64_t p = lo; p < hi; ++p) {
+  for (int64_t p = p0 + tid; p < p1; p += 256) {
+    int lo = 0, hi = nb - 1;  // the bag holding p: last j with s_off[j] <= p
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (s_off[mid] <= p) lo = mid;
+      else hi = mid - 1;
+    }
+    const uint32_t bag = (uint32_t)(bag0 + lo);
+    const BwdSlot sl = a.slots[bag / a.B];
     const int64_t v = (int64_t)idx[p];
     if (has_pad && v == a.padding_idx) continue;
-    if (v < 0 || v >= s.rows) {
+    if (v < 0 || v >= sl.rows) {
       bad = true;
       continue;
     }
-    ++cnt;
+    a.keys[p] = (uint32_t)(sl.row_off + v);
+    a.bags[p] = bag;
+    if (a.has_mean) atomicAdd(&s_cnt[lo], 1u);
   }
   if (bad && a.err) *a.err = 1;
-  if (cnt == 0) return;
-  const float scale = s.pooling == PDM_POOL_MEAN ? 1.0f / (float)cnt : 1.0f;
-  const uint2 rec = make_uint2((uint32_t)((b * a.grad_stride + s.out_col) >> 2), __float_as_uint(scale));
-  for (int64_t p = lo; p < hi; ++p) {
-    const int64_t v = (int64_t)idx[p];
-    if ((has_pad && v == a.padding_idx) || v < 0 || v >= s.rows) continue;
-    a.keys[p] = (uint32_t)(s.row_off + v);
-    a.info[p] = rec;
+  if (a.has_mean) {
+    __syncthreads();
+    if (tid < nb) a.bag_scale[bag0 + tid] = s_cnt[tid] > 0 ? 1.0f / (float)s_cnt[tid] : 0.0f;
   }
 }
 
@@ -187,9 +228,7 @@ __global__ __launch_bounds__(256) void scan_rows_kernel(uint32_t* __restrict__ r
 // with equal digits are found with one ballot per digit bit, and a per-wave
 // LDS counter per digit carries ranks across rounds.  Keys (and values) are
 // then placed in LDS in tile-sorted order and written out in that order, so
-// the global writes of a digit are contiguous.  FIRST: the values are the
-// key positions.
-template <bool FIRST>
+// the global writes of a digit are contiguous.
 __global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
     const uint32_t* __restrict__ keys_in, const uint32_t* __restrict__ vals_in, uint32_t* __restrict__ keys_out,
     uint32_t* __restrict__ vals_out, const uint32_t* __restrict__ hist, const uint32_t* __restrict__ totals,
@@ -215,7 +254,7 @@ __global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
 #pragma unroll
   for (int j = 0; j < kSortItems; ++j) {
     key[j] = keys_in[p0 + j * 64 + lane];
-    val[j] = FIRST ? (uint32_t)(p0 + j * 64 + lane) : vals_in[p0 + j * 64 + lane];
+    val[j] = vals_in[p0 + j * 64 + lane];
   }
   __syncthreads();  // cnt zeroed, tmp free
   const uint64_t lt = lanemask_lt(lane);
@@ -273,8 +312,9 @@ __global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
 
 struct AccArgs {
   const uint32_t* keys;  // sorted keys [n_pad]
-  const uint32_t* vals;  // lookup positions, in key order
-  const uint2* info;     // per lookup position
+  const uint32_t* vals;  // bag ids of the lookups, in key order
+  const BwdSlot* slots;
+  const float* bag_scale;
   const float* grad;
   float* w;
   float* m1;
@@ -282,13 +322,16 @@ struct AccArgs {
   float* part_first;  // [num_chunks, D]: sum of a chunk's first run when it began in an earlier chunk
   float* part_last;   // [num_chunks, D]: sum of a chunk's last run when it began there and continues
   const BwdTable* tabs;
+  int64_t w_delta;  // element index of row `key` = key * D + w_delta for every table, or kNoDelta
   int32_t ntab;
   int32_t D;
   uint32_t key_lo;
   uint32_t key_hi;
   int64_t n_pad;
   int64_t num_chunks;
-  int64_t num_indices;
+  int64_t num_bags;
+  int64_t grad_stride;
+  uint32_t B;
   // optimizer
   int32_t wd_mode;
   float lr, eps, b1, b2, omb1, omb2, bc1, bc2, wd;
@@ -302,11 +345,89 @@ struct AccArgs {
 
 enum { MODE_ADAM = 0, MODE_ADAGRAD = 1, MODE_GRAD = 2 };
 
-// Applies the update of row `key` from its summed gradient g (lane gl of a
-// group of G lanes holds float4 columns gl, gl + G, ...).
+#ifndef PDM_BWD_NT_STORE
+#define PDM_BWD_NT_STORE 1
+#endif
+
+constexpr int64_t kNoDelta = INT64_MIN;
+
+// Weights / optimizer state of one row held in registers across the update
+// (lane gl of a group of G lanes holds float4 columns gl, gl + G, ...).
+template <int VEC>
+struct RowState {
+  f32x4_t w[VEC];
+  f32x4_t m[VEC];
+  f32x4_t v[VEC];
+  float s;
+  int64_t e0;  // fp32 element index of the row in the weights buffer
+};
+
+template <typename T>
+__device__ __forceinline__ void store_row(T* p, const T& v) {
+#if PDM_BWD_NT_STORE
+  // rows are written once per step and not read again by this step
+  __builtin_nontemporal_store(v, p);
+#else
+  *p = v;
+#endif
+}
+
+#ifndef PDM_BWD_NT_LOAD
+#define PDM_BWD_NT_LOAD 1
+#endif
+
+__device__ __forceinline__ f32x4_t load_row(const f32x4_t* p) {
+#if PDM_BWD_NT_LOAD
+  return __builtin_nontemporal_load(p);
+#else
+  return *p;
+#endif
+}
+
+// Element index of row `key`: one multiply when the group's tables sit in the
+// weights buffer at a common offset from their row ids (tables packed without
+// gaps), else a binary search for the last table whose first row id <= key.
+__device__ __forceinline__ int64_t row_elem(const AccArgs& a, uint32_t key) {
+  if (a.w_delta != kNoDelta) return (int64_t)key * a.D + a.w_delta;
+  int lo = 0, hi = a.ntab - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (a.tabs[mid].row_off <= (int64_t)key) lo = mid;
+    else hi = mid - 1;
+  }
+  const BwdTable tb = a.tabs[lo];
+  return tb.w_elem + ((int64_t)key - tb.row_off) * a.D;
+}
+
+// Issues the loads of the row's weights and state (independent of the
+// gradient, so they overlap the gradient sum).
 template <int G, int VEC, int MODE>
-__device__ __forceinline__ void apply_row(const AccArgs& a, uint32_t key, const f32x4_t (&g)[VEC], int gl,
-                                          int64_t slot) {
+__device__ __forceinline__ void load_state(const AccArgs& a, uint32_t key, int gl, RowState<VEC>& st) {
+  if constexpr (MODE != MODE_GRAD) {
+    const int D4 = a.D >> 2;
+    st.e0 = row_elem(a, key);
+    const f32x4_t* W = reinterpret_cast<const f32x4_t*>(a.w + st.e0);
+    const f32x4_t* M = reinterpret_cast<const f32x4_t*>(a.m1 + st.e0);
+    const f32x4_t* V = reinterpret_cast<const f32x4_t*>(a.m2 + st.e0);
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) {
+      const int c = gl + v * G;
+      const f32x4_t z{0.0f, 0.0f, 0.0f, 0.0f};
+      st.w[v] = c < D4 ? load_row(W + c) : z;
+      if constexpr (MODE == MODE_ADAM) {
+        st.m[v] = c < D4 ? load_row(M + c) : z;
+        st.v[v] = c < D4 ? load_row(V + c) : z;
+      }
+    }
+    if constexpr (MODE == MODE_ADAGRAD) st.s = a.m1[key];
+  }
+}
+
+// Applies the update of row `key` from its summed gradient g and stores it
+// (MODE_GRAD: writes the id and the gradient to output slot `slot`).
+template <int G, int VEC, int MODE>
+__device__ __forceinline__ void update_row(const AccArgs& a, uint32_t key, const f32x4_t (&g)[VEC],
+                                           RowState<VEC>& st, int gl, int64_t slot) {
   const int D4 = a.D >> 2;
   if constexpr (MODE == MODE_GRAD) {
     if (gl == 0) a.out_ids[slot] = (int64_t)key;
@@ -314,58 +435,80 @@ __device__ __forceinline__ void apply_row(const AccArgs& a, uint32_t key, const 
 #pragma unroll
     for (int v = 0; v < VEC; ++v)
       if (gl + v * G < D4) o[gl + v * G] = g[v];
-    return;
-  } else {
-    int lo = 0, hi = a.ntab - 1;  // last table whose first row id <= key
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (a.tabs[mid].row_off <= (int64_t)key) lo = mid;
-      else hi = mid - 1;
+  } else if constexpr (MODE == MODE_ADAM) {
+    f32x4_t* W = reinterpret_cast<f32x4_t*>(a.w + st.e0);
+    f32x4_t* M = reinterpret_cast<f32x4_t*>(a.m1 + st.e0);
+    f32x4_t* V = reinterpret_cast<f32x4_t*>(a.m2 + st.e0);
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) {
+      const int c = gl + v * G;
+      if (c >= D4) continue;
+      f32x4_t w = st.w[v], m = st.m[v], s = st.v[v];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        m[e] = fmaf(g[v][e], a.omb1, m[e] * a.b1);
+        s[e] = fmaf(g[v][e] * g[v][e], a.omb2, s[e] * a.b2);
+        w[e] = w[e] - a.lr * ((m[e] / a.bc1) / (sqrtf(s[e] / a.bc2) + a.eps) + a.wd * w[e]);
+      }
+      store_row(W + c, w);
+      store_row(M + c, m);
+      store_row(V + c, s);
     }
-    const BwdTable tb = a.tabs[lo];
-    const int64_t e0 = tb.w_elem + ((int64_t)key - tb.row_off) * a.D;
-    f32x4_t* W = reinterpret_cast<f32x4_t*>(a.w + e0);
-    if constexpr (MODE == MODE_ADAM) {
-      f32x4_t* M = reinterpret_cast<f32x4_t*>(a.m1 + e0);
-      f32x4_t* V = reinterpret_cast<f32x4_t*>(a.m2 + e0);
+  } else {
+    float ss = 0.0f;
 #pragma unroll
-      for (int v = 0; v < VEC; ++v) {
-        const int c = gl + v * G;
-        if (c >= D4) continue;
-        f32x4_t w = W[c], m = M[c], s = V[c];
+    for (int v = 0; v < VEC; ++v) {
+      f32x4_t gg = g[v];
+      if (a.wd_mode == PDM_WD_L2) gg = gg + a.wd * st.w[v];
+      ss += gg[0] * gg[0] + gg[1] * gg[1] + gg[2] * gg[2] + gg[3] * gg[3];
+    }
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          m[e] = fmaf(g[v][e], a.omb1, m[e] * a.b1);
-          s[e] = fmaf(g[v][e] * g[v][e], a.omb2, s[e] * a.b2);
-          w[e] = w[e] - a.lr * ((m[e] / a.bc1) / (sqrtf(s[e] / a.bc2) + a.eps) + a.wd * w[e]);
-        }
-        W[c] = w;
-        M[c] = m;
-        V[c] = s;
-      }
-    } else {
-      f32x4_t w[VEC];
-      float ss = 0.0f;
+    for (int o = G / 2; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+    const float state = st.s + ss / (float)a.D;
+    const float mult = a.lr / (sqrtf(state) + a.eps);
+    const float corr = a.wd_mode == PDM_WD_L2 ? 1.0f - mult * a.wd : 1.0f;
+    f32x4_t* W = reinterpret_cast<f32x4_t*>(a.w + st.e0);
 #pragma unroll
-      for (int v = 0; v < VEC; ++v) {
-        const int c = gl + v * G;
-        w[v] = c < D4 ? W[c] : f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-        f32x4_t gg = g[v];
-        if (a.wd_mode == PDM_WD_L2) gg = gg + a.wd * w[v];
-        ss += gg[0] * gg[0] + gg[1] * gg[1] + gg[2] * gg[2] + gg[3] * gg[3];
-      }
+    for (int v = 0; v < VEC; ++v) {
+      const int c = gl + v * G;
+      if (c < D4) store_row(W + c, corr * st.w[v] - mult * g[v]);
+    }
+    if (gl == 0) a.m1[key] = state;
+  }
+}
+
+// acc += sc * grad row, over the entries [i, e] of a wave's chunk, in order
+// (4 gradient rows in flight).
+template <int G, int VEC>
+__device__ __forceinline__ void sum_entries(const uint32_t* s_off, const float* s_sc, int i, int e,
+                                            const f32x4_t* grad4, int gl, int D4, f32x4_t (&acc)[VEC]) {
+  for (; i + 3 <= e; i += 4) {
+    f32x4_t gv[4][VEC];
+    float sc[4];
 #pragma unroll
-      for (int o = G / 2; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
-      const float gavg = ss / (float)a.D;
-      const float state = a.m1[key] + gavg;
-      const float mult = a.lr / (sqrtf(state) + a.eps);
-      const float corr = a.wd_mode == PDM_WD_L2 ? 1.0f - mult * a.wd : 1.0f;
+    for (int u = 0; u < 4; ++u) {
+      const uint32_t off = s_off[i + u];
+      sc[u] = s_sc[i + u];
 #pragma unroll
-      for (int v = 0; v < VEC; ++v) {
-        const int c = gl + v * G;
-        if (c < D4) W[c] = corr * w[v] - mult * g[v];
-      }
-      if (gl == 0) a.m1[key] = state;
+      for (int v = 0; v < VEC; ++v)
+        gv[u][v] = gl + v * G < D4 ? grad4[off + gl + v * G] : f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int v = 0; v < VEC; ++v)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[v][c] = fmaf(sc[u], gv[u][v][c], acc[v][c]);
+  }
+  for (; i <= e; ++i) {
+    const uint32_t off = s_off[i];
+    const float sc = s_sc[i];
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) {
+      if (gl + v * G >= D4) continue;
+      const f32x4_t gv = grad4[off + gl + v * G];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) acc[v][c] = fmaf(sc, gv[c], acc[v][c]);
     }
   }
 }
@@ -386,8 +529,8 @@ __global__ __launch_bounds__(256) void bwd_accumulate_kernel(AccArgs a) {
   if (chunk >= a.num_chunks) return;
   const int64_t base = chunk * kChunk;
   const uint32_t k = a.keys[base + lane];
-  const uint32_t pos = a.vals[base + lane];
-  const bool mine = k >= a.key_lo && k < a.key_hi && pos < a.num_indices;
+  const uint32_t bag = a.vals[base + lane];
+  const bool mine = k >= a.key_lo && k < a.key_hi && bag < a.num_bags;
   if (__ballot(mine) == 0) return;
   uint32_t kp = __shfl_up(k, 1), kn = __shfl_down(k, 1);
   if (lane == 0) kp = base > 0 ? a.keys[base - 1] : ~k;
@@ -397,10 +540,17 @@ __global__ __launch_bounds__(256) void bwd_accumulate_kernel(AccArgs a) {
   const uint64_t starts = __ballot(pstart), ends = __ballot(pend);
   const bool cont_first = __ballot(lane == 0 && mine && k == kp) != 0;
   const bool cont_last = __ballot(lane == 63 && mine && k == kn) != 0;
-  uint2 rec = make_uint2(0u, 0u);
-  if (mine) rec = a.info[pos];
-  s_off[w][lane] = rec.x;
-  s_sc[w][lane] = __uint_as_float(rec.y);
+  // this lane's lookup: the bag's gradient row and scale
+  uint32_t goff = 0;
+  float gsc = 0.0f;
+  if (mine) {
+    const uint32_t t = bag / a.B, b = bag - t * a.B;
+    const BwdSlot sl = a.slots[t];
+    goff = (uint32_t)(((int64_t)b * a.grad_stride + sl.out_col) >> 2);
+    gsc = sl.pooling == PDM_POOL_MEAN ? a.bag_scale[bag] : 1.0f;
+  }
+  s_off[w][lane] = goff;
+  s_sc[w][lane] = gsc;
   const uint64_t lt = lanemask_lt(lane);
   if (pstart) {
     const int j = __popcll(starts & lt);
@@ -413,51 +563,58 @@ __global__ __launch_bounds__(256) void bwd_accumulate_kernel(AccArgs a) {
   const int gl = lane % G;
   const f32x4_t* grad4 = reinterpret_cast<const f32x4_t*>(a.grad);
   const int D4 = a.D >> 2;
-  for (int j = lane / G; j < nparts; j += NG) {
-    const int h = s_head[w][j], e = s_tail[w][j];
-    f32x4_t acc[VEC];
-#pragma unroll
-    for (int v = 0; v < VEC; ++v) acc[v] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-    int i = h;
-    for (; i + 3 <= e; i += 4) {
-      f32x4_t gv[4][VEC];
-      float sc[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const uint32_t off = s_off[w][i + u];
-        sc[u] = s_sc[w][i + u];
-#pragma unroll
-        for (int v = 0; v < VEC; ++v)
-          gv[u][v] = gl + v * G < D4 ? grad4[off + gl + v * G] : f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-      }
-#pragma unroll
-      for (int u = 0; u < 4; ++u)
-#pragma unroll
-        for (int v = 0; v < VEC; ++v)
-#pragma unroll
-          for (int c = 0; c < 4; ++c) acc[v][c] = fmaf(sc[u], gv[u][v][c], acc[v][c]);
-    }
-    for (; i <= e; ++i) {
-      const uint32_t off = s_off[w][i];
-      const float sc = s_sc[w][i];
+  // Runs j and j + NG together: two rows' state and gradient loads in flight.
+  for (int j0 = lane / G; j0 < nparts; j0 += 2 * NG) {
+    const int j1 = j0 + NG;
+    const bool two = j1 < nparts;
+    // a run continued from the previous chunk is part 0; one continuing into the next is the last part
+    const bool cross0 = (j0 == 0 && cont_first) || (j0 == nparts - 1 && cont_last);
+    const bool cross1 = two && j1 == nparts - 1 && cont_last;
+    const uint32_t k0 = s_key[w][j0], k1 = two ? s_key[w][j1] : k0;
+    RowState<VEC> st0, st1;
+    if (!cross0) load_state<G, VEC, MODE>(a, k0, gl, st0);
+    if (two && !cross1) load_state<G, VEC, MODE>(a, k1, gl, st1);
+    const int h0 = s_head[w][j0], e0 = s_tail[w][j0];
+    const int h1 = two ? s_head[w][j1] : 0, e1 = two ? s_tail[w][j1] : -1;
+    f32x4_t acc0[VEC], acc1[VEC];
+    {  // first entry of each run, both loads issued before either is used
+      const uint32_t o0 = s_off[w][h0], o1 = two ? s_off[w][h1] : o0;
+      const float c0 = s_sc[w][h0], c1 = two ? s_sc[w][h1] : 0.0f;
+      f32x4_t g0[VEC], g1[VEC];
 #pragma unroll
       for (int v = 0; v < VEC; ++v) {
-        if (gl + v * G >= D4) continue;
-        const f32x4_t gv = grad4[off + gl + v * G];
-#pragma unroll
-        for (int c = 0; c < 4; ++c) acc[v][c] = fmaf(sc, gv[c], acc[v][c]);
+        const bool in = gl + v * G < D4;
+        g0[v] = in ? grad4[o0 + gl + v * G] : f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        g1[v] = in && two ? grad4[o1 + gl + v * G] : f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
       }
-    }
-    const bool first_cont = j == 0 && cont_first;
-    const bool last_cont = j == nparts - 1 && cont_last;
-    if (first_cont || last_cont) {
-      f32x4_t* p = reinterpret_cast<f32x4_t*>((first_cont ? a.part_first : a.part_last) + chunk * a.D);
 #pragma unroll
       for (int v = 0; v < VEC; ++v)
-        if (gl + v * G < D4) p[gl + v * G] = acc[v];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          acc0[v][c] = fmaf(c0, g0[v][c], 0.0f);
+          acc1[v][c] = fmaf(c1, g1[v][c], 0.0f);
+        }
+    }
+    sum_entries<G, VEC>(s_off[w], s_sc[w], h0 + 1, e0, grad4, gl, D4, acc0);
+    if (two) sum_entries<G, VEC>(s_off[w], s_sc[w], h1 + 1, e1, grad4, gl, D4, acc1);
+    const int64_t slot_base = MODE == MODE_GRAD ? (int64_t)a.head_prefix[chunk] - (cont_first ? 1 : 0) : 0;
+    if (cross0) {
+      f32x4_t* p = reinterpret_cast<f32x4_t*>((j0 == 0 && cont_first ? a.part_first : a.part_last) + chunk * a.D);
+#pragma unroll
+      for (int v = 0; v < VEC; ++v)
+        if (gl + v * G < D4) p[gl + v * G] = acc0[v];
     } else {
-      const int64_t slot = MODE == MODE_GRAD ? (int64_t)a.head_prefix[chunk] + j - (cont_first ? 1 : 0) : 0;
-      apply_row<G, VEC, MODE>(a, s_key[w][j], acc, gl, slot);
+      update_row<G, VEC, MODE>(a, k0, acc0, st0, gl, slot_base + j0);
+    }
+    if (two) {
+      if (cross1) {
+        f32x4_t* p = reinterpret_cast<f32x4_t*>(a.part_last + chunk * a.D);
+#pragma unroll
+        for (int v = 0; v < VEC; ++v)
+          if (gl + v * G < D4) p[gl + v * G] = acc1[v];
+      } else {
+        update_row<G, VEC, MODE>(a, k1, acc1, st1, gl, slot_base + j1);
+      }
     }
   }
 }
@@ -489,7 +646,9 @@ __global__ __launch_bounds__(256) void bwd_fixup_kernel(AccArgs a) {
     if (ce >= a.n_pad || a.keys[ce] != key) break;
   }
   const int64_t slot = MODE == MODE_GRAD ? (int64_t)a.head_prefix[chunk + 1] - 1 : 0;
-  apply_row<G, VEC, MODE>(a, key, acc, gl, slot);
+  RowState<VEC> st;
+  load_state<G, VEC, MODE>(a, key, gl, st);
+  update_row<G, VEC, MODE>(a, key, acc, st, gl, slot);
 }
 
 // Distinct rows (of the key range) whose first entry lies in each chunk.
@@ -515,12 +674,13 @@ __global__ void write_i64_kernel(int64_t* p, int64_t v) {
 
 struct BwdLayout {
   int64_t n_pad, num_tiles, num_chunks, dmax;
-  int64_t keys_a, keys_b, vals_a, vals_b, info, hist, totals, part_first, part_last, total;
+  int64_t keys_a, keys_b, vals_a, vals_b, bag_scale, hist, totals, part_first, part_last, total;
 };
 
 int64_t align256(int64_t v) { return (v + 255) & ~int64_t(255); }
 
-BwdLayout bwd_layout(const pdm_tbe_plan_s* plan, int64_t n) {
+BwdLayout bwd_layout(const pdm_tbe_plan_s* plan, int64_t n, int64_t batch_size) {
+  const int64_t num_bags = (int64_t)plan->tables.size() * batch_size;
   BwdLayout L{};
   L.n_pad = (std::max<int64_t>(n, 1) + kTile - 1) / kTile * kTile;
   L.num_tiles = L.n_pad / kTile;
@@ -537,7 +697,7 @@ BwdLayout bwd_layout(const pdm_tbe_plan_s* plan, int64_t n) {
   L.keys_b = take(L.n_pad * 4);
   L.vals_a = take(L.n_pad * 4);
   L.vals_b = take(L.n_pad * 4);
-  L.info = take(std::max<int64_t>(n, 1) * 8);
+  L.bag_scale = take(std::max<int64_t>(num_bags, 1) * 4);
   L.hist = take(kBins * L.num_tiles * 4);
   L.totals = take(kBins * 4);
   L.part_first = take(L.num_chunks * L.dmax * 4);
@@ -547,6 +707,12 @@ BwdLayout bwd_layout(const pdm_tbe_plan_s* plan, int64_t n) {
 }
 
 using AccFn = void (*)(AccArgs);
+
+// float4 columns per lane of a row update: fewer lanes per row put more rows
+// of a wavefront in flight (the update is latency-bound on its loads).
+#ifndef PDM_BWD_VEC
+#define PDM_BWD_VEC 1
+#endif
 
 template <int MODE>
 bool pick_acc(int D, AccFn& acc, AccFn& fix, int& ng) {
@@ -558,15 +724,16 @@ bool pick_acc(int D, AccFn& acc, AccFn& fix, int& ng) {
     ng = 64 / G_;                                       \
     return true;                                        \
   }
-  if (d4 <= 1) PDM_ACC_CASE(1, 1)
-  if (d4 <= 2) PDM_ACC_CASE(2, 1)
-  if (d4 <= 4) PDM_ACC_CASE(4, 1)
-  if (d4 <= 8) PDM_ACC_CASE(8, 1)
-  if (d4 <= 16) PDM_ACC_CASE(16, 1)
-  if (d4 <= 32) PDM_ACC_CASE(32, 1)
-  if (d4 <= 64) PDM_ACC_CASE(64, 1)
-  if (d4 <= 128) PDM_ACC_CASE(64, 2)
-  if (d4 <= 256) PDM_ACC_CASE(64, 4)
+  constexpr int V = PDM_BWD_VEC;
+  if (d4 <= V) PDM_ACC_CASE(1, V)
+  if (d4 <= 2 * V) PDM_ACC_CASE(2, V)
+  if (d4 <= 4 * V) PDM_ACC_CASE(4, V)
+  if (d4 <= 8 * V) PDM_ACC_CASE(8, V)
+  if (d4 <= 16 * V) PDM_ACC_CASE(16, V)
+  if (d4 <= 32 * V) PDM_ACC_CASE(32, V)
+  if (d4 <= 64 * V) PDM_ACC_CASE(64, V)
+  if (V < 2 && d4 <= 128) PDM_ACC_CASE(64, 2)
+  if (V < 4 && d4 <= 256) PDM_ACC_CASE(64, 4)
 #undef PDM_ACC_CASE
   return false;
 }
@@ -609,6 +776,7 @@ int run_backward(const BwdCall& c) {
   PDM_CHECK_ARG(c.index_bits == 32 || c.index_bits == 64, "index_bits must be 32 or 64");
   PDM_CHECK_ARG(c.num_indices >= 0 && c.B >= 0, "negative size");
   PDM_CHECK_ARG(c.num_indices < (int64_t)kSentinel - kTile, "num_indices must be < 2^32 - 4097");
+  PDM_CHECK_ARG((int64_t)plan->tables.size() * c.B < (int64_t)kSentinel, "T * batch_size must be < 2^32 - 1");
   PDM_CHECK_ARG(plan->total_rows < (int64_t)kSentinel, "the plan's row space must hold < 2^32 - 1 rows");
   for (const auto& d : plan->tables) {
     PDM_CHECK_ARG(d.dtype == PDM_F32 && d.row_bytes == 4 * d.dim, "the backward needs dense fp32 tables");
@@ -637,7 +805,7 @@ int run_backward(const BwdCall& c) {
                     "weight_decay_mode must be PDM_WD_NONE or PDM_WD_L2");
     }
   }
-  const BwdLayout L = bwd_layout(plan, c.num_indices);
+  const BwdLayout L = bwd_layout(plan, c.num_indices, c.B);
   if (c.B == 0 || c.num_indices == 0) {
     if (c.mode == MODE_GRAD) {
       hipLaunchKernelGGL(write_i64_kernel, dim3(1), dim3(64), 0, c.stream, c.out_count, (int64_t)0);
@@ -658,7 +826,7 @@ int run_backward(const BwdCall& c) {
   uint32_t* keys_b = reinterpret_cast<uint32_t*>(ws + L.keys_b);
   uint32_t* vals_a = reinterpret_cast<uint32_t*>(ws + L.vals_a);
   uint32_t* vals_b = reinterpret_cast<uint32_t*>(ws + L.vals_b);
-  uint2* info = reinterpret_cast<uint2*>(ws + L.info);
+  float* bag_scale = reinterpret_cast<float*>(ws + L.bag_scale);
   uint32_t* hist = reinterpret_cast<uint32_t*>(ws + L.hist);
   uint32_t* totals = reinterpret_cast<uint32_t*>(ws + L.totals);
 
@@ -667,9 +835,11 @@ int run_backward(const BwdCall& c) {
   hipLaunchKernelGGL(fill_u32_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, c.stream, keys_a, n4,
                      kSentinel);
   PDM_CHECK_LAUNCH();
-  LinArgs la{c.indices, c.offsets, plan->d_bwd_slots, keys_a, info, c.err, c.num_indices, c.B, T * c.B,
-             c.padding_idx, c.grad_stride};
-  const int64_t lin_blocks = (T * c.B + 255) / 256;
+  bool has_mean = false;
+  for (const auto& d : plan->tables) has_mean = has_mean || d.pooling == PDM_POOL_MEAN;
+  LinArgs la{c.indices, c.offsets, plan->d_bwd_slots, keys_a, vals_a, bag_scale, c.err, c.num_indices, T * c.B,
+             c.padding_idx, (uint32_t)c.B, has_mean ? 1 : 0};
+  const int64_t lin_blocks = (T * c.B + kLinBags - 1) / kLinBags;
   PDM_CHECK_ARG(lin_blocks < (int64_t(1) << 31), "too many bags for one launch");
   if (c.index_bits == 32)
     hipLaunchKernelGGL(bwd_linearize_kernel<int32_t>, dim3((unsigned)lin_blocks), dim3(256), 0, c.stream, la);
@@ -691,13 +861,8 @@ int run_backward(const BwdCall& c) {
     PDM_CHECK_LAUNCH();
     hipLaunchKernelGGL(scan_rows_kernel, dim3(kBins), dim3(256), 0, c.stream, hist, totals, L.num_tiles);
     PDM_CHECK_LAUNCH();
-    if (p == 0)
-      hipLaunchKernelGGL(radix_scatter_kernel<true>, dim3((unsigned)L.num_tiles), dim3(kSortThreads), 0, c.stream,
-                         kin, (const uint32_t*)nullptr, kout, vout, hist, totals, shift, nb, L.num_tiles,
-                         (uint32_t)L.n_pad);
-    else
-      hipLaunchKernelGGL(radix_scatter_kernel<false>, dim3((unsigned)L.num_tiles), dim3(kSortThreads), 0, c.stream,
-                         kin, vin, kout, vout, hist, totals, shift, nb, L.num_tiles, (uint32_t)L.n_pad);
+    hipLaunchKernelGGL(radix_scatter_kernel, dim3((unsigned)L.num_tiles), dim3(kSortThreads), 0, c.stream, kin,
+                       vin, kout, vout, hist, totals, shift, nb, L.num_tiles, (uint32_t)L.n_pad);
     PDM_CHECK_LAUNCH();
     std::swap(kin, kout);
     std::swap(vin, vout);
@@ -708,7 +873,8 @@ int run_backward(const BwdCall& c) {
   AccArgs a{};
   a.keys = kin;
   a.vals = vin;
-  a.info = info;
+  a.slots = plan->d_bwd_slots;
+  a.bag_scale = bag_scale;
   a.grad = c.grad;
   a.w = c.weights;
   a.m1 = c.m1;
@@ -717,7 +883,9 @@ int run_backward(const BwdCall& c) {
   a.part_last = reinterpret_cast<float*>(ws + L.part_last);
   a.n_pad = L.n_pad;
   a.num_chunks = L.num_chunks;
-  a.num_indices = c.num_indices;
+  a.num_bags = T * c.B;
+  a.grad_stride = c.grad_stride;
+  a.B = (uint32_t)c.B;
   if (c.mode != MODE_GRAD) {
     const pdm_optim_params& o = *c.opt;
     a.wd_mode = o.weight_decay_mode;
@@ -753,6 +921,7 @@ int run_backward(const BwdCall& c) {
     }
     a.tabs = plan->d_bwd_tables + g.first_table;
     a.ntab = g.num_tables;
+    a.w_delta = g.w_delta;
     a.D = g.dim;
     a.key_lo = (uint32_t)g.row_lo;
     a.key_hi = (uint32_t)g.row_hi;
@@ -780,9 +949,9 @@ int run_backward(const BwdCall& c) {
 
 using namespace pdm;
 
-extern "C" int64_t pdm_tbe_backward_workspace_size(pdm_tbe_plan plan, int64_t num_indices) {
-  if (!plan || num_indices < 0) return -1;
-  return bwd_layout(plan, num_indices).total;
+extern "C" int64_t pdm_tbe_backward_workspace_size(pdm_tbe_plan plan, int64_t num_indices, int64_t batch_size) {
+  if (!plan || num_indices < 0 || batch_size < 0) return -1;
+  return bwd_layout(plan, num_indices, batch_size).total;
 }
 
 extern "C" int pdm_tbe_backward_fused(pdm_tbe_plan plan, float* weights, float* momentum1, float* momentum2,

@@ -56,6 +56,7 @@ struct BwdGroup {
   int32_t reserved;
   int64_t row_lo;
   int64_t row_hi;
+  int64_t w_delta;  // w_elem - row_off * dim, common to the group's tables; INT64_MIN if they differ
 };
 
 }  // namespace pdm

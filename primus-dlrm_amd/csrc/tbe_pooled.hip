@@ -653,7 +653,8 @@ extern "C" int pdm_tbe_plan_create(const pdm_table_desc* tables, int32_t num_tab
   std::vector<BwdSlot> bslots(num_tables);
   plan->slot_row_off.assign(num_tables, 0);
   for (const auto& g : plan->groups) {
-    BwdGroup bg{g.dim, g.dtype, (int32_t)btabs.size(), 0, 1, 0, plan->total_rows, 0};
+    BwdGroup bg{g.dim, g.dtype, (int32_t)btabs.size(), 0, 1, 0, plan->total_rows, 0, INT64_MIN};
+    bool delta_set = false, delta_same = true;
     for (int i = 0; i < g.count; ++i) {
       const int t = order[g.first + i];
       const auto& d = plan->tables[t];
@@ -671,6 +672,10 @@ extern "C" int pdm_tbe_plan_create(const pdm_table_desc* tables, int32_t num_tab
         if (d.rows > 0) {
           btabs.push_back(BwdTable{plan->total_rows, d.weights_offset / 4});
           ++bg.num_tables;
+          const int64_t delta = d.weights_offset / 4 - plan->total_rows * (int64_t)d.dim;
+          if (!delta_set) bg.w_delta = delta;
+          else if (delta != bg.w_delta) delta_same = false;
+          delta_set = true;
         }
         plan->total_rows += d.rows;
       }
@@ -678,6 +683,7 @@ extern "C" int pdm_tbe_plan_create(const pdm_table_desc* tables, int32_t num_tab
       bslots[t] = BwdSlot{d.rows, plan->slot_row_off[t], d.out_offset, d.pooling};
     }
     bg.row_hi = plan->total_rows;
+    if (!delta_same || bg.dense_rows == 0 || !delta_set) bg.w_delta = INT64_MIN;
     plan->bwd_groups.push_back(bg);
   }
   if (btabs.empty()) btabs.push_back(BwdTable{0, 0});

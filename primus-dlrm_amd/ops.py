@@ -133,9 +133,10 @@ def tbe_pooled_raw(plan: TbePlan, weights: torch.Tensor, indices: torch.Tensor, 
     return out
 
 
-def tbe_backward_workspace(plan: TbePlan, num_indices: int, device=None) -> torch.Tensor:
-    """Device workspace for pdm_tbe_backward_fused / _sparse_grad over ``num_indices`` lookups."""
-    n = int(L.lib().pdm_tbe_backward_workspace_size(plan.handle, int(num_indices)))
+def tbe_backward_workspace(plan: TbePlan, num_indices: int, batch_size: int, device=None) -> torch.Tensor:
+    """Device workspace for pdm_tbe_backward_fused / _sparse_grad over ``num_indices`` lookups in
+    ``batch_size`` bags per slot."""
+    n = int(L.lib().pdm_tbe_backward_workspace_size(plan.handle, int(num_indices), int(batch_size)))
     if n < 0:
         raise ValueError("bad plan or num_indices")
     return torch.empty(n, dtype=torch.uint8, device=device if device is not None else plan.device)
@@ -155,7 +156,7 @@ def _check_bwd_inputs(plan: TbePlan, indices, offsets, batch_size, grad_out, wor
             or (grad_out.numel() and grad_out.stride(1) != 1) or grad_out.shape[1] < plan.total_dim:
         raise ValueError("grad_out must be float32 [B, >= total_dim] with unit column stride")
     if workspace is None:
-        workspace = tbe_backward_workspace(plan, indices.numel(), grad_out.device)
+        workspace = tbe_backward_workspace(plan, indices.numel(), batch_size, grad_out.device)
     if workspace.dtype != torch.uint8 or not workspace.is_contiguous():
         raise ValueError("workspace must be a contiguous uint8 tensor")
     return workspace

@@ -83,7 +83,9 @@ def ebc_fp32(scale_rows: float = 1.0, batch: int = 2048) -> PooledWorkload:
         ln = poisson_lengths(g, batch, 10.0, 0, 50)
         lens.append(ln)
         idx.append(g.integers(0, rows, int(ln.sum()), dtype=np.int64))
-    return PooledWorkload("ebc_fp32_8x100k_d64_b2048", [rows] * T, 64, "fp32", "sum", "fp32", batch,
+    name = f"ebc_fp32_8x{rows // 1000}k_d64_b{batch}" if rows < 1_000_000 else \
+        f"ebc_fp32_8x{rows // 1_000_000}m_d64_b{batch}"
+    return PooledWorkload(name, [rows] * T, 64, "fp32", "sum", "fp32", batch,
                           np.concatenate(idx), offsets_from_lengths(np.concatenate(lens)), "uniform0.01")
 
 

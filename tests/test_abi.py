@@ -58,7 +58,7 @@ def test_argument_errors_are_reported_not_raised(pdm):
     two = (ctypes.c_int64 * 2)(1, 1)
     assert lib.pdm_cross_hash_fwd(None, two, 2, 4, 0, 0, None, None) == L.PDM_ERR_INVALID
     assert "table_size" in L.last_error()
-    assert lib.pdm_tbe_backward_workspace_size(None, 10) == -1
+    assert lib.pdm_tbe_backward_workspace_size(None, 10, 2) == -1
     assert lib.pdm_tbe_plan_total_rows(None) == -1 and lib.pdm_tbe_plan_row_offset(None, 0) == -1
     assert lib.pdm_tbe_backward_fused(None, None, None, None, None, 64, 0, None, 1, -1, None, 8, None, None, 0,
                                       None, None) == L.PDM_ERR_INVALID
