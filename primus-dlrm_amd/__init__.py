@@ -13,10 +13,12 @@ from .onetrans import (MixedAttention, MixedFFN, OneTransBlock, OneTransStack, R
                        pyramid_schedule)
 from . import ops
 from . import hashing
+from .optim import EmbOptimType, FusedEmbeddingOptimizer, RowWiseAdagrad, WeightDecayMode
 
 __all__ = [
     "DataType", "EmbeddingBagCollection", "EmbeddingBagConfig", "EmbeddingCollection", "EmbeddingConfig",
     "EmbeddingTableConfig", "PoolingType", "SequenceGather", "TorchRecEmbeddings", "JaggedTensor",
     "KeyedJaggedTensor", "KeyedTensor", "MixedAttention", "MixedFFN", "OneTransBlock", "OneTransStack",
-    "RMSNorm", "build_pyramid_mask", "pyramid_schedule", "ops", "hashing",
+    "RMSNorm", "build_pyramid_mask", "pyramid_schedule", "ops", "hashing", "EmbOptimType",
+    "FusedEmbeddingOptimizer", "RowWiseAdagrad", "WeightDecayMode",
 ]

@@ -29,6 +29,7 @@ import torch.nn as nn
 from . import _lib as L
 from . import ops
 from .kjt import JaggedTensor, KeyedJaggedTensor, KeyedTensor
+from .optim import FusedEmbeddingOptimizer, _optimizer_tag
 
 
 class PoolingType(enum.Enum):
@@ -100,10 +101,19 @@ def _default_init(w: torch.Tensor) -> None:
     w.uniform_(-bound, bound)
 
 
+_IN_BACKWARD_TAGS = ("_optimizer_classes", "_optimizer_kwargs", "_in_backward_optimizers")
+
+
 class _TableWeight(nn.Module):
-    def __init__(self, weight: torch.Tensor):
+    def __init__(self, weight: torch.Tensor, previous: Optional[torch.Tensor] = None):
         super().__init__()
-        self.weight = nn.Parameter(weight, requires_grad=False)
+        # float tables require grad like TorchRec's, so _apply_optimizer_in_backward can tag them; their
+        # gradient never materialises (the lookup's backward updates the rows in place)
+        self.weight = nn.Parameter(weight, requires_grad=weight.is_floating_point())
+        if previous is not None:  # keep in-backward optimizer tags across .to() / .cuda()
+            for k in _IN_BACKWARD_TAGS:
+                if hasattr(previous, k):
+                    setattr(self.weight, k, getattr(previous, k))
 
 
 class _FlatTables(nn.Module):
@@ -140,7 +150,8 @@ class _FlatTables(nn.Module):
     def _make_views(self) -> None:
         md = getattr(self, self._prefix)
         for i, cfg in enumerate(self._configs):
-            md[cfg.name] = _TableWeight(self._view(i))
+            prev = md[cfg.name].weight if cfg.name in md else None
+            md[cfg.name] = _TableWeight(self._view(i), prev)
 
     @torch.no_grad()
     def _initialise(self, chunk: int) -> None:
@@ -255,6 +266,8 @@ class EmbeddingBagCollection(nn.Module):
         self._total_dim = col
         self._plan: Optional[ops.TbePlan] = None
         self._plan_device: Optional[torch.device] = None
+        self._fused: Optional[FusedEmbeddingOptimizer] = None
+        self._fused_key = None
 
     # TorchRec-style accessors
     @property
@@ -296,13 +309,66 @@ class EmbeddingBagCollection(nn.Module):
         return ops.tbe_pooled_raw(self._get_plan(), self._store.flat, values, offsets, batch_size,
                                   self._output_dtype, padding_idx, err_flag=err_flag)
 
-    def forward(self, features) -> KeyedTensor:
-        values, offsets = _kjt_slot_offsets(features, self._feature_names)
+    @property
+    def fused_optimizer(self) -> Optional[FusedEmbeddingOptimizer]:
+        """The in-backward optimizer the table weights were tagged with by
+        ``torch.distributed.optim._apply_optimizer_in_backward`` (None when untagged); TorchRec's sharded
+        model exposes the same as ``model.fused_optimizer`` (dist_trainer.py:298)."""
+        tags = [_optimizer_tag(self._store.weight(t.name)) for t in self._tables]
+        if all(tg is None for tg in tags):
+            return None
+        if any(tg is None for tg in tags) or any(tg[0] is not tags[0][0] or tg[1] != tags[0][1] for tg in tags):
+            raise NotImplementedError("every table of the collection needs the same in-backward optimizer")
+        key = (tags[0][0], tuple(sorted((k, repr(v)) for k, v in tags[0][1].items())), self._store.flat.device)
+        if self._fused is None or self._fused_key != key:
+            plan = self._get_plan()
+            first_slot = {}
+            for i, t in enumerate(self._tables):
+                first_slot.setdefault(t.name, sum(len(u.feature_names) for u in self._tables[:i]))
+            self._fused = FusedEmbeddingOptimizer(
+                tags[0][0], tags[0][1], plan, self._store.total_bytes, self._store.flat.device,
+                [t.name for t in self._tables], {t.name: t.num_embeddings for t in self._tables},
+                {t.name: t.embedding_dim for t in self._tables},
+                {t.name: self._store.offsets[i] for i, t in enumerate(self._tables)},
+                {t.name: plan.row_offsets[first_slot[t.name]] if t.feature_names else 0 for t in self._tables})
+            self._fused.param_groups[0]["params"] = [self._store.weight(t.name) for t in self._tables]
+            self._fused_key = key
+        return self._fused
+
+    def _pooled_out(self, values: torch.Tensor, offsets: torch.Tensor) -> torch.Tensor:
         plan = self._get_plan()
         code = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}[self._output_dtype]
-        out = torch.ops.pdm.tbe_pooled_fwd(self._store.flat, values, offsets, plan.plan_id, plan.num_slots,
-                                           self._total_dim, code, -1)
+        return torch.ops.pdm.tbe_pooled_fwd(self._store.flat, values, offsets, plan.plan_id, plan.num_slots,
+                                            self._total_dim, code, -1)
+
+    def forward(self, features) -> KeyedTensor:
+        values, offsets = _kjt_slot_offsets(features, self._feature_names)
+        fused = self.fused_optimizer if torch.is_grad_enabled() else None
+        if fused is not None:
+            weights = [self._store.weight(t.name) for t in self._tables]
+            out = _FusedPooledLookup.apply(self, values.contiguous(), offsets.contiguous(), *weights)
+        else:
+            out = self._pooled_out(values, offsets)
         return KeyedTensor(self._feature_names, self._dims, out)
+
+
+class _FusedPooledLookup(torch.autograd.Function):
+    """Pooled lookup whose backward is the fused backward + optimizer update (pdm_tbe_backward_fused): the
+    table rows change in place and no weight gradient is produced, as with TorchRec's fused TBE."""
+
+    @staticmethod
+    def forward(ctx, ebc, values, offsets, *weights):
+        ctx.ebc = ebc
+        ctx.save_for_backward(values, offsets)
+        return ebc._pooled_out(values, offsets)
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        values, offsets = ctx.saved_tensors
+        ebc = ctx.ebc
+        batch = (offsets.numel() - 1) // max(len(ebc._feature_names), 1)
+        ebc.fused_optimizer.apply(ebc._store.flat, values, offsets, batch, grad_out.float().contiguous())
+        return (None, None, None) + (None,) * len(ebc._tables)
 
 
 class EmbeddingCollection(nn.Module):
