@@ -159,6 +159,14 @@ typedef struct {
 int64_t pdm_tbe_plan_total_rows(pdm_tbe_plan plan);
 int64_t pdm_tbe_plan_row_offset(pdm_tbe_plan plan, int32_t slot);
 
+/* Where each slot's table keeps its row-wise optimizer state: row r of slot
+ * t's table uses entry state_row_offsets[t] + r (host array, one per slot;
+ * -1 keeps the default, the row id).  Lets several plans over one set of
+ * tables (e.g. a collection's pooled features and its S-token gather) share
+ * one state buffer.  Slots of one table need equal offsets.  Synchronous. */
+int pdm_tbe_plan_set_state_offsets(pdm_tbe_plan plan,
+                                   const int64_t* state_row_offsets);
+
 /* Device workspace bytes the backward needs for num_indices lookups over
  * batch_size bags per slot. */
 int64_t pdm_tbe_backward_workspace_size(pdm_tbe_plan plan, int64_t num_indices,
@@ -251,6 +259,28 @@ int pdm_seq_gather_fwd(const pdm_seq_desc* desc, const void* const* tables,
                        const int64_t* const* ids,
                        const int64_t* const* offsets, void* out,
                        uint8_t* mask, int32_t* err_flag, pdm_stream_t stream);
+
+/* Backward of pdm_seq_gather_fwd with the embedding optimizer fused in: the
+ * S-token slot (b, s) of feature f is a one-id bag whose gradient is
+ * grad_out[b, s, col_f : col_f + dim_f], so every looked-up row (row 0 for a
+ * ROW0 padding slot, as the forward reads it) gets the sum of its slots'
+ * gradients and one update (replaces the EmbeddingCollection backward of the
+ * reference's sequence lookups, onetrans.py:480-520,553-558, under the fused
+ * optimizer of distributed/wrapper.py:151-174).
+ * plan:      one slot per feature, fp32 tables, sum pooling, slot f's
+ *            out_offset = col_f (sum of the earlier dims), rows/dim as desc
+ * desc, ids, offsets: as given to the forward (desc->dtype = PDM_F32)
+ * grad_out:  device fp32 [B, S, sum dim] (S = sum max_len)
+ * weights, momentum1, momentum2, opt, err_flag: as pdm_tbe_backward_fused
+ * workspace: >= pdm_tbe_backward_workspace_size(plan, F * B * S, B * S). */
+int pdm_seq_gather_backward_fused(pdm_tbe_plan plan, const pdm_seq_desc* desc,
+                                  float* weights, float* momentum1,
+                                  float* momentum2, const int64_t* const* ids,
+                                  const int64_t* const* offsets,
+                                  const float* grad_out,
+                                  const pdm_optim_params* opt, void* workspace,
+                                  int64_t workspace_bytes, int32_t* err_flag,
+                                  pdm_stream_t stream);
 
 /* ------------------------------------------------------------------------
  * OneTrans mixed-parameter interaction block forward (bf16 MFMA).

@@ -21,6 +21,9 @@ reference's lookup semantics on the CPU:
                       update per distinct row (fbgemm_gpu 2026.4.29, absent here; rules
                       restated at oracle_tbe_backward in pdm_oracle.c).  ``row_space``
                       numbers the distinct tables the way the library documents it.
+* ``seq_gather_backward`` the S-token gather's backward: ``seq_token_ids`` restates the forward's slot
+                      placement (dataset.py:604-626, onetrans.py:515-520,553-558) and every slot becomes
+                      a one-id bag of ``tbe_backward``.
 """
 from __future__ import annotations
 
@@ -337,3 +340,42 @@ def tbe_backward(slots: Sequence[dict], indices: np.ndarray, offsets: np.ndarray
                                   _p(weights) if weights is not None else None, _p(m1) if m1 is not None else None,
                                   _p(m2) if m2 is not None else None, _p(entries), ctypes.byref(bad))
     return ids[:u], rows[:u], int(bad.value)
+
+
+SEQ_PAD = 1 << 62  # slot marker the sequence backward skips (padding in ZERO mode)
+
+
+def seq_token_ids(ids: Sequence[Sequence[np.ndarray]], offsets: Sequence[np.ndarray], max_len: Sequence[int],
+                  pad_mode: str = "row0", align: str = "right") -> np.ndarray:
+    """Id of every S-token slot, [F, B, S]: pool p keeps the last min(len, L_p) events of each sample, right
+    aligned with left padding (data/dataset.py:604-626) or left aligned; a padding slot holds id 0 (row0, the
+    reference's pad id) or SEQ_PAD (zero: the slot looks nothing up)."""
+    P, F = len(offsets), len(ids[0])
+    B = offsets[0].size - 1
+    S = int(sum(max_len))
+    out = np.full((F, B, S), 0 if pad_mode == "row0" else SEQ_PAD, dtype=np.int64)
+    s0 = 0
+    for p in range(P):
+        L = int(max_len[p])
+        for b in range(B):
+            beg, end = int(offsets[p][b]), int(offsets[p][b + 1])
+            if beg < 0 or end < beg or end > len(ids[p][0]):
+                beg = end = 0  # malformed offsets: the forward treats the sample as empty
+            n = min(end - beg, L)
+            first = L - n if align == "right" else 0
+            for f in range(F):
+                out[f, b, s0 + first:s0 + first + n] = ids[p][f][end - n:end]
+        s0 += L
+    return out
+
+
+def seq_gather_backward(slots: Sequence[dict], ids, offsets, max_len, grad: np.ndarray, pad_mode: str = "row0",
+                        align: str = "right", **kw):
+    """Backward of the S-token gather + fused optimizer: every (feature, slot) is a one-id bag of slot f whose
+    gradient is token row (b, s), columns of feature f; ``slots`` are the features' fp32 tables (sum pooling,
+    out_offset = column).  Returns what ``tbe_backward`` returns."""
+    tok = seq_token_ids(ids, offsets, max_len, pad_mode, align)
+    F, B, S = tok.shape
+    g2 = np.ascontiguousarray(grad, dtype=np.float32).reshape(B * S, -1)
+    return tbe_backward(slots, tok.reshape(-1), np.arange(F * B * S + 1, dtype=np.int64), B * S, g2,
+                        padding_idx=SEQ_PAD, **kw)

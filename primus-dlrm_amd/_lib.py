@@ -43,6 +43,8 @@ EXPORTED_SYMBOLS = (
     "pdm_tbe_backward_workspace_size",
     "pdm_tbe_backward_fused",
     "pdm_tbe_backward_sparse_grad",
+    "pdm_tbe_plan_set_state_offsets",
+    "pdm_seq_gather_backward_fused",
     "pdm_seq_gather_fwd",
     "pdm_cross_hash_fwd",
     "pdm_onetrans_block_workspace_size",
@@ -168,6 +170,12 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.pdm_tbe_backward_sparse_grad.restype = ctypes.c_int
     lib.pdm_tbe_backward_sparse_grad.argtypes = [vp, vp, i32, i64, vp, i64, i64, vp, i64, vp, vp, vp, vp, i64,
                                                  vp, vp]
+    lib.pdm_tbe_plan_set_state_offsets.restype = ctypes.c_int
+    lib.pdm_tbe_plan_set_state_offsets.argtypes = [vp, ctypes.POINTER(i64)]
+    lib.pdm_seq_gather_backward_fused.restype = ctypes.c_int
+    lib.pdm_seq_gather_backward_fused.argtypes = [vp, ctypes.POINTER(SeqDesc), vp, vp, vp, ctypes.POINTER(vp),
+                                                  ctypes.POINTER(vp), vp, ctypes.POINTER(OptimParams), vp, i64, vp,
+                                                  vp]
     lib.pdm_cross_hash_fwd.restype = ctypes.c_int
     lib.pdm_cross_hash_fwd.argtypes = [ctypes.POINTER(vp), ctypes.POINTER(i64), i32, i64, ctypes.c_uint64,
                                        ctypes.c_uint64, vp, vp]

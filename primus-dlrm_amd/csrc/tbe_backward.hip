@@ -172,6 +172,62 @@ __global__ __launch_bounds__(256) void bwd_linearize_kernel(LinArgs a) {
   }
 }
 
+struct SeqLinArgs {
+  const int64_t* ids[PDM_SEQ_MAX_POOLS * PDM_SEQ_MAX_FEATURES];  // [pool][feature]
+  const int64_t* offsets[PDM_SEQ_MAX_POOLS];
+  int64_t num_ids[PDM_SEQ_MAX_POOLS];
+  int32_t lmax[PDM_SEQ_MAX_POOLS];
+  int32_t soff[PDM_SEQ_MAX_POOLS + 1];
+  const BwdSlot* slots;  // one per feature
+  uint32_t* keys;        // [n_pad], pre-filled with the sentinel
+  uint32_t* bags;        // [n_pad]
+  int32_t* err;
+  int64_t num_tokens;    // B * S
+  int32_t P, F, S, pad_zero, align_left;
+};
+
+// One thread per S-token slot (sample b, slot s): the slot's event (the last
+// min(len, L) events of its pool, right or left aligned, exactly as the
+// gather's forward places them) or padding, then per feature the looked-up
+// row: lookup q = f * B*S + token is a one-id bag of slot f whose gradient is
+// token row `token`, columns of feature f.  A padding slot looks up row 0
+// (pad mode ROW0) or nothing (ZERO); ids outside the table and malformed
+// offsets are skipped and flagged, as the forward does.
+__global__ __launch_bounds__(256) void seq_linearize_kernel(SeqLinArgs a) {
+  const int64_t tok = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (tok >= a.num_tokens) return;
+  const int64_t b = tok / a.S;
+  const int s = (int)(tok - b * a.S);
+  int p = 0;
+  while (p + 1 < a.P && s >= a.soff[p + 1]) ++p;
+  int64_t beg = a.offsets[p][b], end = a.offsets[p][b + 1];
+  bool bad = false;
+  if (beg < 0 || end < beg || end > a.num_ids[p]) {
+    bad = true;
+    beg = end = 0;
+  }
+  const int pos = s - a.soff[p], L = a.lmax[p];
+  const int n = (int)(end - beg < (int64_t)L ? end - beg : (int64_t)L);
+  const int64_t ev = a.align_left ? (pos < n ? end - n + pos : -1) : (pos >= L - n ? end - n + (pos - (L - n)) : -1);
+  for (int f = 0; f < a.F; ++f) {
+    int64_t id = 0;
+    if (ev < 0) {
+      if (a.pad_zero) continue;
+    } else {
+      id = a.ids[p * PDM_SEQ_MAX_FEATURES + f][ev];
+    }
+    const BwdSlot sl = a.slots[f];
+    if (id < 0 || id >= sl.rows) {
+      bad = true;
+      continue;
+    }
+    const int64_t q = (int64_t)f * a.num_tokens + tok;
+    a.keys[q] = (uint32_t)(sl.row_off + id);
+    a.bags[q] = (uint32_t)q;
+  }
+  if (bad && a.err) *a.err = 1;
+}
+
 // ---- 2. radix sort ---------------------------------------------------------------
 
 // Per-tile digit counts, stored digit-major: hist[d * num_tiles + tile].
@@ -323,6 +379,7 @@ struct AccArgs {
   float* part_last;   // [num_chunks, D]: sum of a chunk's last run when it began there and continues
   const BwdTable* tabs;
   int64_t w_delta;  // element index of row `key` = key * D + w_delta for every table, or kNoDelta
+  int64_t s_delta;  // row-wise state index of row `key` = key + s_delta for every table, or kNoDelta
   int32_t ntab;
   int32_t D;
   uint32_t key_lo;
@@ -360,6 +417,7 @@ struct RowState {
   f32x4_t v[VEC];
   float s;
   int64_t e0;  // fp32 element index of the row in the weights buffer
+  int64_t si;  // index of the row's row-wise state
 };
 
 template <typename T>
@@ -384,11 +442,16 @@ __device__ __forceinline__ f32x4_t load_row(const f32x4_t* p) {
 #endif
 }
 
-// Element index of row `key`: one multiply when the group's tables sit in the
-// weights buffer at a common offset from their row ids (tables packed without
-// gaps), else a binary search for the last table whose first row id <= key.
-__device__ __forceinline__ int64_t row_elem(const AccArgs& a, uint32_t key) {
-  if (a.w_delta != kNoDelta) return (int64_t)key * a.D + a.w_delta;
+// Weights element index and row-wise state index of row `key`: one multiply
+// / add when the group's tables sit at a common offset from their row ids
+// (tables packed without gaps), else a binary search for the last table whose
+// first row id <= key.
+__device__ __forceinline__ void row_loc(const AccArgs& a, uint32_t key, int64_t& e0, int64_t& si) {
+  if (a.w_delta != kNoDelta && a.s_delta != kNoDelta) {
+    e0 = (int64_t)key * a.D + a.w_delta;
+    si = (int64_t)key + a.s_delta;
+    return;
+  }
   int lo = 0, hi = a.ntab - 1;
   while (lo < hi) {
     const int mid = (lo + hi + 1) >> 1;
@@ -396,7 +459,8 @@ __device__ __forceinline__ int64_t row_elem(const AccArgs& a, uint32_t key) {
     else hi = mid - 1;
   }
   const BwdTable tb = a.tabs[lo];
-  return tb.w_elem + ((int64_t)key - tb.row_off) * a.D;
+  e0 = tb.w_elem + ((int64_t)key - tb.row_off) * a.D;
+  si = tb.s_off + ((int64_t)key - tb.row_off);
 }
 
 // Issues the loads of the row's weights and state (independent of the
@@ -405,7 +469,7 @@ template <int G, int VEC, int MODE>
 __device__ __forceinline__ void load_state(const AccArgs& a, uint32_t key, int gl, RowState<VEC>& st) {
   if constexpr (MODE != MODE_GRAD) {
     const int D4 = a.D >> 2;
-    st.e0 = row_elem(a, key);
+    row_loc(a, key, st.e0, st.si);
     const f32x4_t* W = reinterpret_cast<const f32x4_t*>(a.w + st.e0);
     const f32x4_t* M = reinterpret_cast<const f32x4_t*>(a.m1 + st.e0);
     const f32x4_t* V = reinterpret_cast<const f32x4_t*>(a.m2 + st.e0);
@@ -419,7 +483,7 @@ __device__ __forceinline__ void load_state(const AccArgs& a, uint32_t key, int g
         st.v[v] = c < D4 ? load_row(V + c) : z;
       }
     }
-    if constexpr (MODE == MODE_ADAGRAD) st.s = a.m1[key];
+    if constexpr (MODE == MODE_ADAGRAD) st.s = a.m1[st.si];
   }
 }
 
@@ -473,7 +537,7 @@ __device__ __forceinline__ void update_row(const AccArgs& a, uint32_t key, const
       const int c = gl + v * G;
       if (c < D4) store_row(W + c, corr * st.w[v] - mult * g[v]);
     }
-    if (gl == 0) a.m1[key] = state;
+    if (gl == 0) a.m1[st.si] = state;
   }
 }
 
@@ -768,6 +832,7 @@ struct BwdCall {
   int64_t ws_bytes;
   int32_t* err;
   hipStream_t stream;
+  const SeqLinArgs* seq;  // non-null: the lookups are the S-token slots of a sequence gather
 };
 
 int run_backward(const BwdCall& c) {
@@ -816,7 +881,7 @@ int run_backward(const BwdCall& c) {
   PDM_CHECK_ARG(c.grad_stride >= plan->total_dim && c.grad_stride % 4 == 0,
                 "grad_row_stride must be >= the plan's total dim and a multiple of 4");
   PDM_CHECK_ARG(c.B * c.grad_stride < (int64_t(1) << 34), "grad_out holds too many elements (>= 2^34)");
-  PDM_CHECK_ARG(c.indices && c.offsets && c.grad, "null device pointer");
+  PDM_CHECK_ARG((c.seq || (c.indices && c.offsets)) && c.grad, "null device pointer");
   PDM_CHECK_ARG(((uintptr_t)c.grad & 15) == 0, "grad_out must be 16-byte aligned");
   PDM_CHECK_ARG(c.ws != nullptr && c.ws_bytes >= L.total,
                 "workspace smaller than pdm_tbe_backward_workspace_size");
@@ -835,17 +900,29 @@ int run_backward(const BwdCall& c) {
   hipLaunchKernelGGL(fill_u32_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, c.stream, keys_a, n4,
                      kSentinel);
   PDM_CHECK_LAUNCH();
-  bool has_mean = false;
-  for (const auto& d : plan->tables) has_mean = has_mean || d.pooling == PDM_POOL_MEAN;
-  LinArgs la{c.indices, c.offsets, plan->d_bwd_slots, keys_a, vals_a, bag_scale, c.err, c.num_indices, T * c.B,
-             c.padding_idx, (uint32_t)c.B, has_mean ? 1 : 0};
-  const int64_t lin_blocks = (T * c.B + kLinBags - 1) / kLinBags;
-  PDM_CHECK_ARG(lin_blocks < (int64_t(1) << 31), "too many bags for one launch");
-  if (c.index_bits == 32)
-    hipLaunchKernelGGL(bwd_linearize_kernel<int32_t>, dim3((unsigned)lin_blocks), dim3(256), 0, c.stream, la);
-  else
-    hipLaunchKernelGGL(bwd_linearize_kernel<int64_t>, dim3((unsigned)lin_blocks), dim3(256), 0, c.stream, la);
-  PDM_CHECK_LAUNCH();
+  if (c.seq) {
+    SeqLinArgs sa = *c.seq;
+    sa.slots = plan->d_bwd_slots;
+    sa.keys = keys_a;
+    sa.bags = vals_a;
+    sa.err = c.err;
+    const int64_t blocks = (sa.num_tokens + 255) / 256;
+    PDM_CHECK_ARG(blocks < (int64_t(1) << 31), "too many tokens for one launch");
+    hipLaunchKernelGGL(seq_linearize_kernel, dim3((unsigned)blocks), dim3(256), 0, c.stream, sa);
+    PDM_CHECK_LAUNCH();
+  } else {
+    bool has_mean = false;
+    for (const auto& d : plan->tables) has_mean = has_mean || d.pooling == PDM_POOL_MEAN;
+    LinArgs la{c.indices, c.offsets, plan->d_bwd_slots, keys_a, vals_a, bag_scale, c.err, c.num_indices, T * c.B,
+               c.padding_idx, (uint32_t)c.B, has_mean ? 1 : 0};
+    const int64_t lin_blocks = (T * c.B + kLinBags - 1) / kLinBags;
+    PDM_CHECK_ARG(lin_blocks < (int64_t(1) << 31), "too many bags for one launch");
+    if (c.index_bits == 32)
+      hipLaunchKernelGGL(bwd_linearize_kernel<int32_t>, dim3((unsigned)lin_blocks), dim3(256), 0, c.stream, la);
+    else
+      hipLaunchKernelGGL(bwd_linearize_kernel<int64_t>, dim3((unsigned)lin_blocks), dim3(256), 0, c.stream, la);
+    PDM_CHECK_LAUNCH();
+  }
 
   // 2. sort (key, position) on the bits the row space needs
   int bits = 1;
@@ -922,6 +999,7 @@ int run_backward(const BwdCall& c) {
     a.tabs = plan->d_bwd_tables + g.first_table;
     a.ntab = g.num_tables;
     a.w_delta = g.w_delta;
+    a.s_delta = g.s_delta;
     a.D = g.dim;
     a.key_lo = (uint32_t)g.row_lo;
     a.key_hi = (uint32_t)g.row_hi;
@@ -967,7 +1045,7 @@ extern "C" int pdm_tbe_backward_fused(pdm_tbe_plan plan, float* weights, float* 
   BwdCall c{plan, opt->optimizer == PDM_OPT_ADAM ? MODE_ADAM : MODE_ADAGRAD, weights, momentum1, momentum2,
             indices, index_bits, num_indices, offsets, batch_size, padding_idx, grad_out, grad_row_stride, opt,
             nullptr, nullptr, nullptr, workspace, workspace_bytes, err_flag,
-            reinterpret_cast<hipStream_t>(stream)};
+            reinterpret_cast<hipStream_t>(stream), nullptr};
   return run_backward(c);
 }
 
@@ -980,6 +1058,62 @@ extern "C" int pdm_tbe_backward_sparse_grad(pdm_tbe_plan plan, const void* indic
   clear_error();
   BwdCall c{plan, MODE_GRAD, nullptr, nullptr, nullptr, indices, index_bits, num_indices, offsets, batch_size,
             padding_idx, grad_out, grad_row_stride, nullptr, row_ids, grad_rows, num_unique, workspace,
-            workspace_bytes, err_flag, reinterpret_cast<hipStream_t>(stream)};
+            workspace_bytes, err_flag, reinterpret_cast<hipStream_t>(stream), nullptr};
+  return run_backward(c);
+}
+
+extern "C" int pdm_seq_gather_backward_fused(pdm_tbe_plan plan, const pdm_seq_desc* desc, float* weights,
+                                             float* momentum1, float* momentum2, const int64_t* const* ids,
+                                             const int64_t* const* offsets, const float* grad_out,
+                                             const pdm_optim_params* opt, void* workspace, int64_t workspace_bytes,
+                                             int32_t* err_flag, pdm_stream_t stream) {
+  clear_error();
+  PDM_CHECK_ARG(plan != nullptr && desc != nullptr && opt != nullptr, "null plan, desc or optimizer parameters");
+  PDM_CHECK_ARG(opt->optimizer == PDM_OPT_ADAM || opt->optimizer == PDM_OPT_ROWWISE_ADAGRAD,
+                "optimizer must be PDM_OPT_ADAM or PDM_OPT_ROWWISE_ADAGRAD");
+  const pdm_seq_desc& d = *desc;
+  PDM_CHECK_ARG(d.num_pools >= 1 && d.num_pools <= PDM_SEQ_MAX_POOLS, "num_pools out of range");
+  PDM_CHECK_ARG(d.num_features >= 1 && d.num_features <= PDM_SEQ_MAX_FEATURES, "num_features out of range");
+  PDM_CHECK_ARG(d.dtype == PDM_F32, "the sequence backward needs fp32 tables (and an fp32 gradient)");
+  PDM_CHECK_ARG(d.pad_mode == PDM_PAD_ROW0 || d.pad_mode == PDM_PAD_ZERO, "bad pad_mode");
+  PDM_CHECK_ARG(d.align == PDM_ALIGN_RIGHT || d.align == PDM_ALIGN_LEFT, "bad align");
+  PDM_CHECK_ARG(d.batch_size >= 0, "batch_size < 0");
+  PDM_CHECK_ARG((int)plan->tables.size() == d.num_features, "the plan needs one slot per feature");
+  SeqLinArgs sa{};
+  int64_t col = 0;
+  for (int f = 0; f < d.num_features; ++f) {
+    const pdm_table_desc& t = plan->tables[f];
+    PDM_CHECK_ARG(t.dim == d.dim[f] && t.rows == d.rows[f] && t.out_offset == col,
+                  "plan slot " + std::to_string(f) + " must be feature f's table (rows, dim) at column sum of "
+                  "the earlier dims");
+    PDM_CHECK_ARG(t.pooling == PDM_POOL_SUM, "plan slots must pool by sum (one id per bag)");
+    col += t.dim;
+  }
+  int32_t S = 0;
+  PDM_CHECK_ARG(ids && offsets, "null pointer array");
+  for (int p = 0; p < d.num_pools; ++p) {
+    PDM_CHECK_ARG(d.max_len[p] >= 0 && d.num_ids[p] >= 0, "max_len and num_ids must be >= 0");
+    PDM_CHECK_ARG(offsets[p] != nullptr, "null offsets pointer");
+    sa.offsets[p] = offsets[p];
+    sa.num_ids[p] = d.num_ids[p];
+    sa.lmax[p] = d.max_len[p];
+    sa.soff[p] = S;
+    S += d.max_len[p];
+    for (int f = 0; f < d.num_features; ++f) {
+      PDM_CHECK_ARG(d.num_ids[p] == 0 || ids[p * d.num_features + f] != nullptr, "null ids pointer");
+      sa.ids[p * PDM_SEQ_MAX_FEATURES + f] = ids[p * d.num_features + f];
+    }
+  }
+  sa.soff[d.num_pools] = S;
+  sa.P = d.num_pools;
+  sa.F = d.num_features;
+  sa.S = S;
+  sa.num_tokens = (int64_t)S * d.batch_size;
+  sa.pad_zero = d.pad_mode == PDM_PAD_ZERO;
+  sa.align_left = d.align == PDM_ALIGN_LEFT;
+  BwdCall c{plan, opt->optimizer == PDM_OPT_ADAM ? MODE_ADAM : MODE_ADAGRAD, weights, momentum1, momentum2,
+            nullptr, 64, sa.num_tokens * d.num_features, nullptr, sa.num_tokens, -1, grad_out, col, opt,
+            nullptr, nullptr, nullptr, workspace, workspace_bytes, err_flag, reinterpret_cast<hipStream_t>(stream),
+            &sa};
   return run_backward(c);
 }

@@ -42,6 +42,7 @@ struct BwdSlot {
 struct BwdTable {
   int64_t row_off;  // row-space id of row 0
   int64_t w_elem;   // fp32 element index of row 0 in the weights buffer
+  int64_t s_off;    // index of row 0's entry in the row-wise optimizer state
 };
 
 // The distinct tables of one forward group occupy the contiguous row-space
@@ -57,7 +58,24 @@ struct BwdGroup {
   int64_t row_lo;
   int64_t row_hi;
   int64_t w_delta;  // w_elem - row_off * dim, common to the group's tables; INT64_MIN if they differ
+  int64_t s_delta;  // s_off - row_off, common to the group's tables; INT64_MIN if they differ
 };
+
+// Sets each group's s_delta from bwd_tables (after state offsets change).
+inline void refresh_state_deltas(std::vector<BwdGroup>& groups, const std::vector<BwdTable>& tabs) {
+  for (auto& g : groups) {
+    g.s_delta = INT64_MIN;
+    for (int i = 0; i < g.num_tables; ++i) {
+      const BwdTable& t = tabs[g.first_table + i];
+      const int64_t d = t.s_off - t.row_off;
+      if (i == 0) g.s_delta = d;
+      else if (d != g.s_delta) {
+        g.s_delta = INT64_MIN;
+        break;
+      }
+    }
+  }
+}
 
 }  // namespace pdm
 
@@ -70,6 +88,8 @@ struct pdm_tbe_plan_s {
   int64_t total_dim = 0;
   // row space of the distinct tables (backward and optimizer state layout)
   std::vector<int64_t> slot_row_off;
+  std::vector<int32_t> slot_table;  // index into bwd_tables of the slot's table (-1: no rows)
+  std::vector<pdm::BwdTable> bwd_tables;
   std::vector<pdm::BwdGroup> bwd_groups;
   int64_t total_rows = 0;
   pdm::BwdSlot* d_bwd_slots = nullptr;

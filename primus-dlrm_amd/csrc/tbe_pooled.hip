@@ -652,8 +652,9 @@ extern "C" int pdm_tbe_plan_create(const pdm_table_desc* tables, int32_t num_tab
   std::vector<BwdTable> btabs;
   std::vector<BwdSlot> bslots(num_tables);
   plan->slot_row_off.assign(num_tables, 0);
+  plan->slot_table.assign(num_tables, -1);
   for (const auto& g : plan->groups) {
-    BwdGroup bg{g.dim, g.dtype, (int32_t)btabs.size(), 0, 1, 0, plan->total_rows, 0, INT64_MIN};
+    BwdGroup bg{g.dim, g.dtype, (int32_t)btabs.size(), 0, 1, 0, plan->total_rows, 0, INT64_MIN, INT64_MIN};
     bool delta_set = false, delta_same = true;
     for (int i = 0; i < g.count; ++i) {
       const int t = order[g.first + i];
@@ -667,10 +668,12 @@ extern "C" int pdm_tbe_plan_create(const pdm_table_desc* tables, int32_t num_tab
       }
       if (same >= 0) {
         plan->slot_row_off[t] = plan->slot_row_off[same];
+        plan->slot_table[t] = plan->slot_table[same];
       } else {
         plan->slot_row_off[t] = plan->total_rows;
         if (d.rows > 0) {
-          btabs.push_back(BwdTable{plan->total_rows, d.weights_offset / 4});
+          plan->slot_table[t] = (int32_t)btabs.size();
+          btabs.push_back(BwdTable{plan->total_rows, d.weights_offset / 4, plan->total_rows});
           ++bg.num_tables;
           const int64_t delta = d.weights_offset / 4 - plan->total_rows * (int64_t)d.dim;
           if (!delta_set) bg.w_delta = delta;
@@ -686,7 +689,9 @@ extern "C" int pdm_tbe_plan_create(const pdm_table_desc* tables, int32_t num_tab
     if (!delta_same || bg.dense_rows == 0 || !delta_set) bg.w_delta = INT64_MIN;
     plan->bwd_groups.push_back(bg);
   }
-  if (btabs.empty()) btabs.push_back(BwdTable{0, 0});
+  refresh_state_deltas(plan->bwd_groups, btabs);
+  plan->bwd_tables = btabs;
+  if (btabs.empty()) btabs.push_back(BwdTable{0, 0, 0});
   PDM_CHECK_HIP(hipGetDevice(&plan->device));
   PDM_CHECK_HIP(hipMalloc(&plan->d_meta, sizeof(TbeMeta) * num_tables));
   PDM_CHECK_HIP(hipMalloc(&plan->d_group_tables, sizeof(int32_t) * num_tables));
@@ -714,6 +719,38 @@ pdm_tbe_plan_s::~pdm_tbe_plan_s() {
 }
 
 extern "C" int64_t pdm_tbe_plan_total_rows(pdm_tbe_plan plan) { return plan ? plan->total_rows : -1; }
+
+extern "C" int pdm_tbe_plan_set_state_offsets(pdm_tbe_plan plan, const int64_t* state_row_offsets) {
+  clear_error();
+  PDM_CHECK_ARG(plan != nullptr && state_row_offsets != nullptr, "null argument");
+  std::vector<BwdTable> tabs = plan->bwd_tables;
+  std::vector<int> set(tabs.size(), 0);
+  for (size_t t = 0; t < plan->tables.size(); ++t) {
+    const int64_t so = state_row_offsets[t];
+    PDM_CHECK_ARG(so >= -1, "slot " + std::to_string(t) + ": state offset must be >= 0 (or -1: default)");
+    const int32_t ti = plan->slot_table[t];
+    if (ti < 0 || so < 0) continue;
+    if (set[ti]) {
+      PDM_CHECK_ARG(tabs[ti].s_off == so, "slots of one table need the same state offset");
+    } else {
+      tabs[ti].s_off = so;
+      set[ti] = 1;
+    }
+  }
+  std::vector<BwdGroup> groups = plan->bwd_groups;
+  refresh_state_deltas(groups, tabs);
+  int cur = 0;
+  PDM_CHECK_HIP(hipGetDevice(&cur));
+  PDM_CHECK_HIP(hipSetDevice(plan->device));
+  const hipError_t e = tabs.empty() ? hipSuccess
+                                    : hipMemcpy(plan->d_bwd_tables, tabs.data(), sizeof(BwdTable) * tabs.size(),
+                                                hipMemcpyHostToDevice);
+  (void)hipSetDevice(cur);
+  PDM_CHECK_HIP(e);
+  plan->bwd_tables = tabs;
+  plan->bwd_groups = groups;
+  return PDM_OK;
+}
 
 extern "C" int64_t pdm_tbe_plan_row_offset(pdm_tbe_plan plan, int32_t slot) {
   if (!plan || slot < 0 || slot >= (int32_t)plan->slot_row_off.size()) return -1;

@@ -116,6 +116,28 @@ class _TableWeight(nn.Module):
                     setattr(self.weight, k, getattr(previous, k))
 
 
+def _collection_fused_optimizer(module) -> Optional[FusedEmbeddingOptimizer]:
+    """The in-backward optimizer the tables of ``module`` (a collection with ``_tables`` and ``_store``) were
+    tagged with by ``torch.distributed.optim._apply_optimizer_in_backward`` (None when untagged), created on
+    first use and rebuilt when the tags or the device change."""
+    tables, store = module._tables, module._store
+    tags = [_optimizer_tag(store.weight(t.name)) for t in tables]
+    if all(tg is None for tg in tags):
+        return None
+    if any(tg is None for tg in tags) or any(tg[0] is not tags[0][0] or tg[1] != tags[0][1] for tg in tags):
+        raise NotImplementedError("every table of the collection needs the same in-backward optimizer")
+    key = (tags[0][0], tuple(sorted((k, repr(v)) for k, v in tags[0][1].items())), store.flat.device)
+    if module._fused is None or module._fused_key != key:
+        fo = FusedEmbeddingOptimizer(
+            tags[0][0], tags[0][1], store.total_bytes, store.flat.device, [t.name for t in tables],
+            {t.name: t.num_embeddings for t in tables}, {t.name: t.embedding_dim for t in tables},
+            {t.name: store.offsets[i] for i, t in enumerate(tables)})
+        fo.param_groups[0]["params"] = [store.weight(t.name) for t in tables]
+        module._fused, module._fused_key = fo, key
+        module._fused_plans = {}
+    return module._fused
+
+
 class _FlatTables(nn.Module):
     """All tables of a collection in one uint8 device buffer, exposed as typed
     per-table ``weight`` views under ``<prefix>.<table>.weight``."""
@@ -268,6 +290,7 @@ class EmbeddingBagCollection(nn.Module):
         self._plan_device: Optional[torch.device] = None
         self._fused: Optional[FusedEmbeddingOptimizer] = None
         self._fused_key = None
+        self._fused_plans: Dict[str, ops.TbePlan] = {}
 
     # TorchRec-style accessors
     @property
@@ -314,26 +337,16 @@ class EmbeddingBagCollection(nn.Module):
         """The in-backward optimizer the table weights were tagged with by
         ``torch.distributed.optim._apply_optimizer_in_backward`` (None when untagged); TorchRec's sharded
         model exposes the same as ``model.fused_optimizer`` (dist_trainer.py:298)."""
-        tags = [_optimizer_tag(self._store.weight(t.name)) for t in self._tables]
-        if all(tg is None for tg in tags):
-            return None
-        if any(tg is None for tg in tags) or any(tg[0] is not tags[0][0] or tg[1] != tags[0][1] for tg in tags):
-            raise NotImplementedError("every table of the collection needs the same in-backward optimizer")
-        key = (tags[0][0], tuple(sorted((k, repr(v)) for k, v in tags[0][1].items())), self._store.flat.device)
-        if self._fused is None or self._fused_key != key:
-            plan = self._get_plan()
-            first_slot = {}
-            for i, t in enumerate(self._tables):
-                first_slot.setdefault(t.name, sum(len(u.feature_names) for u in self._tables[:i]))
-            self._fused = FusedEmbeddingOptimizer(
-                tags[0][0], tags[0][1], plan, self._store.total_bytes, self._store.flat.device,
-                [t.name for t in self._tables], {t.name: t.num_embeddings for t in self._tables},
-                {t.name: t.embedding_dim for t in self._tables},
-                {t.name: self._store.offsets[i] for i, t in enumerate(self._tables)},
-                {t.name: plan.row_offsets[first_slot[t.name]] if t.feature_names else 0 for t in self._tables})
-            self._fused.param_groups[0]["params"] = [self._store.weight(t.name) for t in self._tables]
-            self._fused_key = key
-        return self._fused
+        return _collection_fused_optimizer(self)
+
+    def _fused_plan(self) -> ops.TbePlan:
+        """The lookup plan with its row-wise state offsets pointed at the fused optimizer's state."""
+        plan = self._get_plan()
+        if self._fused_plans.get("ebc") is not plan:
+            fo = self._fused
+            plan.set_state_offsets([fo.state_offset[t.name] for t in self._tables for _ in t.feature_names])
+            self._fused_plans["ebc"] = plan
+        return plan
 
     def _pooled_out(self, values: torch.Tensor, offsets: torch.Tensor) -> torch.Tensor:
         plan = self._get_plan()
@@ -367,7 +380,8 @@ class _FusedPooledLookup(torch.autograd.Function):
         values, offsets = ctx.saved_tensors
         ebc = ctx.ebc
         batch = (offsets.numel() - 1) // max(len(ebc._feature_names), 1)
-        ebc.fused_optimizer.apply(ebc._store.flat, values, offsets, batch, grad_out.float().contiguous())
+        fo = ebc.fused_optimizer
+        fo.apply(ebc._fused_plan(), ebc._store.flat, values, offsets, batch, grad_out.float().contiguous())
         return (None, None, None) + (None,) * len(ebc._tables)
 
 
@@ -395,6 +409,15 @@ class EmbeddingCollection(nn.Module):
                 self._feature_names.append(f)
                 self._feature_table[f] = i
         self._plans: Dict[Tuple[int, str], ops.TbePlan] = {}
+        self._fused: Optional[FusedEmbeddingOptimizer] = None
+        self._fused_key = None
+        self._fused_plans: Dict[str, ops.TbePlan] = {}
+
+    @property
+    def fused_optimizer(self) -> Optional[FusedEmbeddingOptimizer]:
+        """The in-backward optimizer of the collection's tables (see EmbeddingBagCollection.fused_optimizer);
+        the S-token gather over these tables updates them through it."""
+        return _collection_fused_optimizer(self)
 
     @property
     def embeddings(self) -> nn.ModuleDict:
@@ -446,23 +469,77 @@ class EmbeddingCollection(nn.Module):
         offsets = torch.arange(n + 1, dtype=torch.int64, device=ids.device)
         return ops.tbe_pooled_raw(self._plan_for(ti), self._store.flat, ids, offsets, n, _DT_TORCH[t.data_type])
 
+    def _fused_plan(self, names: Tuple[str, ...]) -> ops.TbePlan:
+        """One slot per feature of ``names`` (sum, column of the feature) with the optimizer's state offsets."""
+        key = f"ec:{names}:{self._store.flat.device}"
+        if key not in self._fused_plans:
+            slots, col = [], 0
+            for n in names:
+                ti = self._feature_table[n]
+                t = self._tables[ti]
+                slots.append(dict(rows=t.num_embeddings, weights_offset=self._store.offsets[ti], dim=t.embedding_dim,
+                                  dtype=_DT_PDM[t.data_type], pooling=L.PDM_POOL_SUM, row_bytes=_row_bytes(t),
+                                  out_offset=col))
+                col += t.embedding_dim
+            plan = ops.TbePlan(slots, self._store.flat.device)
+            plan.set_state_offsets([self._fused.state_offset[self._tables[self._feature_table[n]].name]
+                                    for n in names])
+            self._fused_plans[key] = plan
+        return self._fused_plans[key]
+
     def forward(self, features) -> Dict[str, JaggedTensor]:
         keys = list(features.keys())
         B = features.stride()
         offsets = features.offsets().to(torch.int64)
         bounds = offsets.view(-1)[:: B] if B > 0 else offsets[:1]
         starts = bounds.tolist()  # per-key value ranges: one host sync, as TorchRec's length_per_key()
-        out: Dict[str, JaggedTensor] = {}
         values = features.values()
+        names, segs, seg_offs = [], [], []
         for k, name in enumerate(keys):
             if name not in self._feature_table:
                 continue
             lo, hi = starts[k], starts[k + 1]
-            seg = values[lo:hi]
-            rows = self.gather(name, seg)
-            seg_off = offsets[k * B:(k + 1) * B + 1] - lo
-            out[name] = JaggedTensor(rows, offsets=seg_off)
-        return out
+            names.append(name)
+            segs.append(values[lo:hi].reshape(-1).contiguous())
+            seg_offs.append(offsets[k * B:(k + 1) * B + 1] - lo)
+        fused = self.fused_optimizer if torch.is_grad_enabled() and names else None
+        if fused is not None:
+            rows = _FusedECLookup.apply(self, tuple(names), segs,
+                                        *[self._store.weight(t.name) for t in self._tables])
+        else:
+            rows = [self.gather(n, seg) for n, seg in zip(names, segs)]
+        return {n: JaggedTensor(r, offsets=o) for n, r, o in zip(names, rows, seg_offs)}
+
+
+class _FusedECLookup(torch.autograd.Function):
+    """Unpooled lookups whose backward is the fused update: every id of feature f is a one-id bag of slot f;
+    the features' bag counts are padded to the largest with empty bags, and the output gradients are laid side
+    by side in one [max n_f, sum D] buffer (pdm_tbe_backward_fused)."""
+
+    @staticmethod
+    def forward(ctx, ec, names, segs, *tables):
+        ctx.ec, ctx.names, ctx.segs = ec, names, segs
+        return tuple(ec.gather(n, seg) for n, seg in zip(names, segs))
+
+    @staticmethod
+    def backward(ctx, *grads):
+        ec, names, segs = ctx.ec, ctx.names, ctx.segs
+        dev = ec._store.flat.device
+        ns = [int(seg.numel()) for seg in segs]
+        dims = [ec._tables[ec._feature_table[n]].embedding_dim for n in names]
+        bags = max(ns)
+        g_all = torch.zeros((bags, sum(dims)), dtype=torch.float32, device=dev)
+        col = 0
+        for gr, n, d in zip(grads, ns, dims):
+            if gr is not None:
+                g_all[:n, col:col + d] = gr
+            col += d
+        ar = torch.arange(bags, device=dev)
+        lengths = torch.cat([(ar < n).to(torch.int64) for n in ns])
+        offsets = torch.zeros(lengths.numel() + 1, dtype=torch.int64, device=dev)
+        torch.cumsum(lengths, 0, out=offsets[1:])
+        ec.fused_optimizer.apply(ec._fused_plan(names), ec._store.flat, torch.cat(segs), offsets, bags, g_all)
+        return (None, None, None) + (None,) * len(ec._tables)
 
 
 class SequenceGather(nn.Module):
@@ -522,8 +599,54 @@ class SequenceGather(nn.Module):
             ids.append([batch[f].reshape(-1).to(torch.int64).contiguous() for f in fs])
             max_len.append(self.max_len[g])
         flat_ids = [t for row in ids for t in row]
-        out, mask = torch.ops.pdm.seq_gather_fwd(tables, flat_ids, offsets, max_len, self.pad_mode, self.align)
+        fused = self.ec.fused_optimizer if torch.is_grad_enabled() else None
+        if fused is not None:
+            out, mask = _FusedSeqGather.apply(self, ids, offsets, max_len, *tables)
+        else:
+            out, mask = torch.ops.pdm.seq_gather_fwd(tables, flat_ids, offsets, max_len, self.pad_mode, self.align)
         return out, mask.view(torch.bool)
+
+    def _fused_plan(self) -> ops.TbePlan:
+        """One slot per feature (fp32 table, sum, column of the feature) with the EC optimizer's state offsets."""
+        ec = self.ec
+        fo = ec._fused
+        key = f"seq:{id(self)}:{ec._store.flat.device}"
+        if key not in ec._fused_plans:
+            slots, col = [], 0
+            for ti in self._feature_tables:
+                t = ec._tables[ti]
+                slots.append(dict(rows=t.num_embeddings, weights_offset=ec._store.offsets[ti], dim=t.embedding_dim,
+                                  dtype=_DT_PDM[t.data_type], pooling=L.PDM_POOL_SUM, row_bytes=_row_bytes(t),
+                                  out_offset=col))
+                col += t.embedding_dim
+            plan = ops.TbePlan(slots, ec._store.flat.device)
+            plan.set_state_offsets([fo.state_offset[ec._tables[ti].name] for ti in self._feature_tables])
+            ec._fused_plans[key] = plan
+        return ec._fused_plans[key]
+
+
+class _FusedSeqGather(torch.autograd.Function):
+    """S-token gather whose backward is the fused backward + optimizer update of the EC's tables
+    (pdm_seq_gather_backward_fused): rows change in place, no weight gradient is produced."""
+
+    @staticmethod
+    def forward(ctx, sg, ids, offsets, max_len, *tables):
+        ctx.sg, ctx.ids, ctx.offsets, ctx.max_len = sg, ids, offsets, max_len
+        flat_ids = [t for row in ids for t in row]
+        out, mask = torch.ops.pdm.seq_gather_fwd(list(tables), flat_ids, offsets, max_len, sg.pad_mode, sg.align)
+        ctx.mark_non_differentiable(mask)
+        return out, mask
+
+    @staticmethod
+    def backward(ctx, grad_out, grad_mask):
+        sg = ctx.sg
+        ec = sg.ec
+        fo = ec.fused_optimizer
+        tabs = [ec._tables[ti] for ti in sg._feature_tables]
+        fo.apply_seq(sg._fused_plan(), ec._store.flat, [t.num_embeddings for t in tabs],
+                     [t.embedding_dim for t in tabs], ctx.ids, ctx.offsets, ctx.max_len,
+                     grad_out.float().contiguous(), sg.pad_mode, sg.align)
+        return (None, None, None, None) + (None,) * len(tabs)
 
 
 class TorchRecEmbeddings(nn.Module):

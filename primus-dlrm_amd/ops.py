@@ -79,6 +79,14 @@ class TbePlan:
             self.plan_id = next(TbePlan._ids)
             TbePlan._registry[self.plan_id] = self
 
+    def set_state_offsets(self, offsets: Sequence[int]) -> None:
+        """Row-wise optimizer state index of row 0 of each slot's table (pdm_tbe_plan_set_state_offsets)."""
+        if len(offsets) != self.num_slots:
+            raise ValueError("one state offset per slot")
+        arr = (ctypes.c_int64 * self.num_slots)(*[int(v) for v in offsets])
+        with torch.cuda.device(self.device):
+            L.check(L.lib().pdm_tbe_plan_set_state_offsets(self.handle, arr), "pdm_tbe_plan_set_state_offsets")
+
     def release(self) -> None:
         if self.handle is not None and self.handle.value:
             with TbePlan._lock:
@@ -311,6 +319,66 @@ def seq_gather_raw(tables: Sequence[torch.Tensor], ids: Sequence[Sequence[torch.
                                         _ptr(mask), _ptr(err_flag), L.stream_ptr(dev))
     L.check(status, "pdm_seq_gather_fwd")
     return out, mask
+
+
+def seq_gather_backward_fused_raw(plan: TbePlan, weights: torch.Tensor, momentum1: torch.Tensor,
+                                  momentum2: Optional[torch.Tensor], table_rows: Sequence[int],
+                                  table_dims: Sequence[int], ids: Sequence[Sequence[torch.Tensor]],
+                                  offsets: Sequence[torch.Tensor], max_len: Sequence[int], grad_out: torch.Tensor,
+                                  pad_mode: int = L.PDM_PAD_ROW0, align: int = L.PDM_ALIGN_RIGHT,
+                                  optimizer: int = L.PDM_OPT_ADAM, learning_rate: float = 0.01, eps: float = 1e-8,
+                                  beta1: float = 0.9, beta2: float = 0.999, weight_decay: float = 0.0,
+                                  weight_decay_mode: int = L.PDM_WD_NONE, step: int = 1,
+                                  workspace: Optional[torch.Tensor] = None,
+                                  err_flag: Optional[torch.Tensor] = None) -> None:
+    """Launches pdm_seq_gather_backward_fused: the S-token gather's backward with the fused update of the
+    feature tables (``plan``: one fp32 slot per feature, sum pooling, out_offset = column of the feature).
+    ``grad_out``: fp32 [B, sum(max_len), sum(dims)] gradient of the gathered tokens."""
+    P, F = len(offsets), len(table_dims)
+    flat_ids = [t for row in ids for t in row]
+    dev = _require_cuda(weights, momentum1, momentum2, grad_out, *flat_ids, *offsets, workspace, err_flag)
+    if not (1 <= P <= L.PDM_SEQ_MAX_POOLS and 1 <= F <= L.PDM_SEQ_MAX_FEATURES) or len(ids) != P \
+            or any(len(r) != F for r in ids) or len(max_len) != P:
+        raise ValueError("ids must be [pools][features] and max_len one per pool")
+    B = offsets[0].numel() - 1
+    S = sum(int(m) for m in max_len)
+    Dtot = sum(int(d) for d in table_dims)
+    if grad_out.dtype != torch.float32 or tuple(grad_out.shape) != (B, S, Dtot) or not grad_out.is_contiguous():
+        raise ValueError(f"grad_out must be contiguous float32 [{B}, {S}, {Dtot}]")
+    desc = L.SeqDesc()
+    desc.num_pools, desc.num_features = P, F
+    desc.dtype, desc.pad_mode, desc.align = L.PDM_F32, pad_mode, align
+    desc.batch_size = B
+    for f in range(F):
+        desc.dim[f] = int(table_dims[f])
+        desc.rows[f] = int(table_rows[f])
+    for p in range(P):
+        o = offsets[p]
+        if o.dtype != torch.int64 or o.numel() != B + 1 or not o.is_contiguous():
+            raise ValueError("offsets must be contiguous int64 [B+1], the same B for every pool")
+        n = ids[p][0].numel()
+        for t in ids[p]:
+            if t.dtype != torch.int64 or not t.is_contiguous() or t.numel() != n:
+                raise ValueError("ids of one pool must be contiguous int64 vectors of equal length")
+        desc.num_ids[p] = n
+        desc.max_len[p] = int(max_len[p])
+    ntok = B * S
+    if workspace is None:
+        workspace = tbe_backward_workspace(plan, F * ntok, ntok, dev)
+    for name, t in (("weights", weights), ("momentum1", momentum1), ("momentum2", momentum2)):
+        if t is not None and not t.is_contiguous():
+            raise ValueError(f"{name} must be contiguous")
+    if weights.numel() * weights.element_size() < plan.fp32_extent:
+        raise ValueError("weights is smaller than the plan's fp32 tables")
+    opt = L.OptimParams(int(optimizer), int(weight_decay_mode), float(learning_rate), float(eps), float(beta1),
+                        float(beta2), float(weight_decay), 0, int(step))
+    ids_arr = (ctypes.c_void_p * (P * F))(*[t.data_ptr() if t.numel() else None for t in flat_ids])
+    off_arr = (ctypes.c_void_p * P)(*[o.data_ptr() for o in offsets])
+    status = L.lib().pdm_seq_gather_backward_fused(
+        plan.handle, ctypes.byref(desc), weights.data_ptr(), momentum1.data_ptr(), _ptr(momentum2), ids_arr, off_arr,
+        grad_out.data_ptr(), ctypes.byref(opt), workspace.data_ptr(), workspace.numel(), _ptr(err_flag),
+        L.stream_ptr(dev))
+    L.check(status, "pdm_seq_gather_backward_fused")
 
 
 @torch.library.custom_op("pdm::seq_gather_fwd", mutates_args=())

@@ -6,9 +6,10 @@ The reference tags every embedding weight with ``_apply_optimizer_in_backward(op
 fused backward (ADAM / EXACT_ROWWISE_ADAGRAD) and exposes ``model.fused_optimizer``, whose ``param_groups`` lr
 the trainer's sparse warm-up drives (primus_dlrm/training/dist_trainer.py:298,316-325).
 
-Here :class:`FusedEmbeddingOptimizer` is that object for one :class:`~primus_dlrm_amd.embedding.
-EmbeddingBagCollection`: it reads the tags, owns the optimizer state (laid out for the C ABI's
-``pdm_tbe_backward_fused``) and launches the fused backward with the current ``param_groups[0]["lr"]``.
+Here :class:`FusedEmbeddingOptimizer` is that object for one collection of this package
+(``EmbeddingBagCollection``, or ``EmbeddingCollection`` whose tables the S-token gather reads): it reads the
+tags, owns the optimizer state (laid out for the C ABI's ``pdm_tbe_backward_fused`` /
+``pdm_seq_gather_backward_fused``) and launches the fused backward with the current ``param_groups[0]["lr"]``.
 
 * ``torch.optim.Adam`` -> FBGEMM ADAM: ``m = b1 m + (1-b1) g``, ``v = b2 v + (1-b2) g^2``,
   ``w -= lr ((m / (1-b1^t)) / (sqrt(v / (1-b2^t)) + eps) + wd w)`` (weight decay applied decoupled, inside
@@ -89,11 +90,12 @@ class FusedEmbeddingOptimizer:
     """The fused optimizer of one collection: hyper-parameters, state and step count.
 
     ``momentum1`` / ``momentum2`` are fp32 device tensors laid out as the C ABI expects (Adam: like the fp32
-    weights buffer; row-wise Adagrad: one entry per row id of the plan's row space)."""
+    weights buffer; row-wise Adagrad: one entry per row of the collection, tables in collection order, so every
+    plan over these tables addresses the same state through ``state_offset``)."""
 
-    def __init__(self, optimizer_class, kwargs: Dict[str, Any], plan, weights_bytes: int, device: torch.device,
+    def __init__(self, optimizer_class, kwargs: Dict[str, Any], weights_bytes: int, device: torch.device,
                  table_names: List[str], table_rows: Dict[str, int], table_dims: Dict[str, int],
-                 table_offsets: Dict[str, int], table_row_ids: Dict[str, int]):
+                 table_offsets: Dict[str, int]):
         name = getattr(optimizer_class, "__name__", str(optimizer_class))
         if optimizer_class is torch.optim.Adam or name == "Adam":
             self.optim_type = EmbOptimType.ADAM
@@ -117,11 +119,15 @@ class FusedEmbeddingOptimizer:
         self.weight_decay = float(kwargs.get("weight_decay", 0.0))
         self.param_groups = [{"lr": float(kwargs.get("lr", 1e-2)), "params": []}]
         self.iter = 0
-        self._plan = plan
         self._names = list(table_names)
-        self._rows, self._dims, self._offsets, self._row_ids = table_rows, table_dims, table_offsets, table_row_ids
+        self._rows, self._dims, self._offsets = table_rows, table_dims, table_offsets
+        self.state_offset: Dict[str, int] = {}
+        r = 0
+        for n in self._names:
+            self.state_offset[n] = r
+            r += table_rows[n]
         adam = self.optim_type == EmbOptimType.ADAM
-        n1 = (weights_bytes + 3) // 4 if adam else max(plan.total_rows, 1)
+        n1 = (weights_bytes + 3) // 4 if adam else max(r, 1)
         self.momentum1 = torch.zeros(n1, dtype=torch.float32, device=device)
         self.momentum2 = torch.zeros(n1, dtype=torch.float32, device=device) if adam else None
         self._workspace: Optional[torch.Tensor] = None
@@ -139,7 +145,7 @@ class FusedEmbeddingOptimizer:
             e0 = self._offsets[name] // 4
             return {"momentum1": self.momentum1[e0:e0 + rows * dim].view(rows, dim),
                     "momentum2": self.momentum2[e0:e0 + rows * dim].view(rows, dim)}
-        r0 = self._row_ids[name]
+        r0 = self.state_offset[name]
         return {"sum": self.momentum1[r0:r0 + rows]}
 
     def state_dict(self) -> Dict[str, Any]:
@@ -155,21 +161,40 @@ class FusedEmbeddingOptimizer:
         self.param_groups[0]["lr"] = float(sd["param_groups"][0]["lr"])
         self.iter = int(sd.get("iter", self.iter))
 
-    def apply(self, weights_flat: torch.Tensor, values: torch.Tensor, offsets: torch.Tensor, batch_size: int,
+    def _hyper(self) -> Dict[str, Any]:
+        adam = self.optim_type == EmbOptimType.ADAM
+        return dict(optimizer=L.PDM_OPT_ADAM if adam else L.PDM_OPT_ROWWISE_ADAGRAD,
+                    learning_rate=self.param_groups[0]["lr"], eps=self.eps, beta1=self.beta1, beta2=self.beta2,
+                    weight_decay=self.weight_decay,
+                    weight_decay_mode=L.PDM_WD_L2 if self.weight_decay_mode == WeightDecayMode.L2 else L.PDM_WD_NONE,
+                    step=self.iter)
+
+    def _ws(self, plan, num_lookups: int, num_bags: int, device) -> torch.Tensor:
+        need = int(L.lib().pdm_tbe_backward_workspace_size(plan.handle, num_lookups, num_bags))
+        if self._workspace is None or self._workspace.numel() < need:
+            self._workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=device)
+        return self._workspace
+
+    def apply(self, plan, weights_flat: torch.Tensor, values: torch.Tensor, offsets: torch.Tensor, batch_size: int,
               grad_out: torch.Tensor) -> None:
-        """Runs the fused backward + update of one batch (called from the autograd backward)."""
+        """The fused backward + update of one pooled batch (called from the autograd backward); ``plan``'s
+        state offsets must be this optimizer's (``state_offset``)."""
         from . import ops
 
         self.iter += 1
-        n = values.numel()
-        need = int(L.lib().pdm_tbe_backward_workspace_size(self._plan.handle, n, batch_size))
-        if self._workspace is None or self._workspace.numel() < need:
-            self._workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=weights_flat.device)
-        adam = self.optim_type == EmbOptimType.ADAM
-        ops.tbe_backward_fused_raw(
-            self._plan, weights_flat, self.momentum1, self.momentum2, values, offsets, batch_size, grad_out,
-            optimizer=L.PDM_OPT_ADAM if adam else L.PDM_OPT_ROWWISE_ADAGRAD,
-            learning_rate=self.param_groups[0]["lr"], eps=self.eps, beta1=self.beta1, beta2=self.beta2,
-            weight_decay=self.weight_decay,
-            weight_decay_mode=L.PDM_WD_L2 if self.weight_decay_mode == WeightDecayMode.L2 else L.PDM_WD_NONE,
-            step=self.iter, workspace=self._workspace)
+        ops.tbe_backward_fused_raw(plan, weights_flat, self.momentum1, self.momentum2, values, offsets, batch_size,
+                                   grad_out, workspace=self._ws(plan, values.numel(), batch_size, weights_flat.device),
+                                   **self._hyper())
+
+    def apply_seq(self, plan, weights_flat: torch.Tensor, table_rows, table_dims, ids, offsets, max_len,
+                  grad_out: torch.Tensor, pad_mode: int, align: int) -> None:
+        """The fused backward + update of one S-token gather (called from the autograd backward)."""
+        from . import ops
+
+        self.iter += 1
+        B = offsets[0].numel() - 1
+        ntok = B * sum(int(m) for m in max_len)
+        ops.seq_gather_backward_fused_raw(
+            plan, weights_flat, self.momentum1, self.momentum2, table_rows, table_dims, ids, offsets, max_len,
+            grad_out, pad_mode=pad_mode, align=align,
+            workspace=self._ws(plan, ntok * len(table_dims), ntok, weights_flat.device), **self._hyper())

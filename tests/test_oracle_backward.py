@@ -232,3 +232,66 @@ def test_adam_first_step_closed_form():
         want = before[k * 4:(k + 1) * 4] - 0.01 * gr / (np.abs(gr) + 1e-8)
         np.testing.assert_allclose(flat[k * 4:(k + 1) * 4], want, rtol=1e-6, atol=1e-9)
     assert math.isfinite(float(flat.sum()))
+
+
+# ---- S-token gather backward ------------------------------------------------------------
+
+def _seq_problem(g, B=7, pools=((6, 5.0), (4, 2.0)), tables=((40, 8), (25, 4))):
+    ids, offs = [], []
+    for L, mean in pools:
+        ln = np.minimum(g.poisson(mean, B), 2 * L)
+        n = int(ln.sum())
+        ids.append([g.integers(0, r, n) for r, _ in tables])
+        offs.append(o.offsets_np(ln))
+    max_len = [L for L, _ in pools]
+    slots, off, col = [], 0, 0
+    for r, d in tables:
+        slots.append(dict(rows=r, weights_offset=off, dim=d, dtype="fp32", pooling="sum", row_bytes=0, out_offset=col))
+        off += r * d * 4
+        col += d
+    return ids, offs, max_len, slots
+
+
+@pytest.mark.parametrize("pad_mode,align", [("row0", "right"), ("zero", "right"), ("row0", "left")])
+def test_seq_token_ids_match_the_forward_oracle(pad_mode, align):
+    g = np.random.default_rng(40)
+    ids, offs, max_len, slots = _seq_problem(g)
+    tabs = [g.integers(1, 1 << 15, (s["rows"], s["dim"]), dtype=np.uint16) for s in slots]
+    want, mask = o.seq_gather(tabs, ids, offs, max_len, pad_mode={"row0": 0, "zero": 1}[pad_mode],
+                              align={"right": 0, "left": 1}[align])
+    tok = o.seq_token_ids(ids, offs, max_len, pad_mode, align)
+    got = np.concatenate([np.where((tok[f] == o.SEQ_PAD)[..., None], 0, tabs[f][np.where(tok[f] == o.SEQ_PAD, 0, tok[f])])
+                          for f in range(len(tabs))], axis=-1)
+    assert np.array_equal(got, want)
+
+
+def test_seq_gather_backward_matches_embedding_autograd():
+    # the reference's path: ids left padded with 0 to L (dataset.py:604-626), EC lookup, per-pool concat of
+    # the features (onetrans.py:515-520) and concat of the pools (:553-558)
+    g = np.random.default_rng(41)
+    ids, offs, max_len, slots = _seq_problem(g)
+    B, S, Dt = 7, sum(max_len), sum(s["dim"] for s in slots)
+    W = [torch.tensor(g.uniform(-1, 1, (s["rows"], s["dim"])), requires_grad=True) for s in slots]
+    pools = []
+    for p, L in enumerate(max_len):
+        feats = []
+        for f in range(len(slots)):
+            padded = torch.zeros(B, L, dtype=torch.long)
+            for b in range(B):
+                seq = ids[p][f][offs[p][b]:offs[p][b + 1]][-L:]
+                if len(seq):
+                    padded[b, L - len(seq):] = torch.from_numpy(seq)
+            feats.append(F.embedding(padded, W[f]))
+        pools.append(torch.cat(feats, dim=-1))
+    out = torch.cat(pools, dim=1)
+    G = g.normal(0, 1, (B, S, Dt)).astype(np.float32)
+    (out * torch.from_numpy(G).double()).sum().backward()
+    rids, rows, bad = o.seq_gather_backward(slots, ids, offs, max_len, G)
+    assert bad == 0
+    row_off, _ = o.row_space(slots)
+    for f, s in enumerate(slots):
+        dense = np.zeros((s["rows"], s["dim"]))
+        for k, r in zip(rids, rows):
+            if row_off[f] <= k < row_off[f] + s["rows"]:
+                dense[k - row_off[f]] = r[:s["dim"]]
+        np.testing.assert_allclose(dense, W[f].grad.numpy(), rtol=1e-5, atol=1e-5)
