@@ -42,6 +42,7 @@ constexpr int kTile = kSortThreads * kSortItems;  // keys per sort tile
 constexpr int kBins = 256;                         // 8-bit digits
 constexpr int kChunk = 64;                         // sorted entries per accumulating wavefront
 constexpr uint32_t kSentinel = 0xFFFFFFFFu;
+constexpr int kMaxLevels = 6;  // chunk partial sums folded 64 at a time: 64^5 chunks cover any 32-bit key count
 
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
@@ -377,6 +378,10 @@ struct AccArgs {
   float* m2;
   float* part_first;  // [num_chunks, D]: sum of a chunk's first run when it began in an earlier chunk
   float* part_last;   // [num_chunks, D]: sum of a chunk's last run when it began there and continues
+  // part_lv[0] = part_first; part_lv[L][u]: the run's sum over the chunks of level-L unit u (64^L chunks) from
+  // its first chunk to where the run ends, for units whose first chunk continues a run
+  const float* part_lv[kMaxLevels];
+  int32_t num_levels;
   const BwdTable* tabs;
   int64_t w_delta;  // element index of row `key` = key * D + w_delta for every table, or kNoDelta
   int64_t s_delta;  // row-wise state index of row `key` = key + s_delta for every table, or kNoDelta
@@ -683,13 +688,85 @@ __global__ __launch_bounds__(256) void bwd_accumulate_kernel(AccArgs a) {
   }
 }
 
-// Finishes the runs that cross chunk boundaries: the chunk holding a run's
-// first entry adds the partial sums of the following chunks in order.
+// acc += rows u0 .. u0 + n - 1 of a [*, D] partial-sum array, in order.
+template <int G, int VEC>
+__device__ __forceinline__ void add_rows(f32x4_t (&acc)[VEC], const float* src, int64_t u0, int n, int D, int gl) {
+  const int D4 = D >> 2;
+  int j = 0;
+  for (; j + 4 <= n; j += 4) {
+    f32x4_t r[4][VEC];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int v = 0; v < VEC; ++v)
+        r[u][v] = gl + v * G < D4 ? reinterpret_cast<const f32x4_t*>(src + (u0 + j + u) * D)[gl + v * G]
+                                  : f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) acc[v] = acc[v] + r[u][v];
+  }
+  for (; j < n; ++j)
+#pragma unroll
+    for (int v = 0; v < VEC; ++v)
+      if (gl + v * G < D4) acc[v] = acc[v] + reinterpret_cast<const f32x4_t*>(src + (u0 + j) * D)[gl + v * G];
+}
+
+// The first unit of level L that a run starting at `key` covers, and how many
+// of the next `span` units it continues into (it does when a unit's first
+// entry still holds the key; keys are sorted, so those units form a prefix).
+__device__ __forceinline__ int run_units(const uint32_t* keys, int64_t n_pad, uint32_t key, int64_t u0,
+                                         int64_t unit_chunks, int span, int lane) {
+  const int64_t e = (u0 + lane) * unit_chunks * kChunk;
+  const bool cont = lane < span && e < n_pad && keys[e] == key;
+  const uint64_t m = __ballot(cont);
+  return ~m == 0 ? 64 : __builtin_ctzll(~m);
+}
+
+struct FoldArgs {
+  const uint32_t* keys;
+  const float* src;  // level L - 1 partials
+  float* dst;        // level L partials
+  int64_t n_pad;
+  int64_t unit_chunks;  // chunks per unit of level L - 1
+  int64_t num_blocks;   // units of level L
+  int32_t D;
+  uint32_t key_lo, key_hi;
+};
+
+// Level-L partial of each block of 64 level-(L-1) units whose first chunk
+// continues a run: the run's partials over the leading units it covers, added
+// in order.  One wavefront per block.
+template <int G, int VEC>
+__global__ __launch_bounds__(256) void bwd_fold_kernel(FoldArgs f) {
+  const int lane = threadIdx.x & 63, gl = lane % G;
+  const int64_t s = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (s >= f.num_blocks) return;
+  const int64_t e0 = s * 64 * f.unit_chunks * kChunk;
+  if (e0 == 0 || e0 >= f.n_pad) return;
+  const uint32_t key = f.keys[e0];
+  if (key < f.key_lo || key >= f.key_hi || f.keys[e0 - 1] != key) return;
+  const int n = run_units(f.keys, f.n_pad, key, s * 64, f.unit_chunks, 64, lane);
+  if (lane >= G) return;
+  f32x4_t acc[VEC];
+#pragma unroll
+  for (int v = 0; v < VEC; ++v) acc[v] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  add_rows<G, VEC>(acc, f.src, s * 64, n, f.D, gl);
+  f32x4_t* d = reinterpret_cast<f32x4_t*>(f.dst + s * f.D);
+#pragma unroll
+  for (int v = 0; v < VEC; ++v)
+    if (gl + v * G < (f.D >> 2)) d[gl + v * G] = acc[v];
+}
+
+// Finishes the runs that cross chunk boundaries: the wavefront of the chunk
+// holding a run's first entry adds the partial sums of the chunks the run
+// covers, climbing the levels (up to 63 units per level, probed at once with a
+// ballot), so a run over k chunks costs O(log k) steps; the order of the
+// additions is fixed, so every run gives the same bits.
 template <int G, int VEC, int MODE>
 __global__ __launch_bounds__(256) void bwd_fixup_kernel(AccArgs a) {
-  constexpr int NG = 64 / G;
   const int lane = threadIdx.x & 63, gl = lane % G;
-  const int64_t chunk = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * NG + lane / G;
+  const int64_t chunk = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (chunk >= a.num_chunks) return;
   const int64_t base = chunk * kChunk, end = base + kChunk;
   if (end >= a.n_pad) return;
@@ -700,15 +777,24 @@ __global__ __launch_bounds__(256) void bwd_fixup_kernel(AccArgs a) {
   f32x4_t acc[VEC];
   const f32x4_t* pl = reinterpret_cast<const f32x4_t*>(a.part_last + chunk * a.D);
 #pragma unroll
-  for (int v = 0; v < VEC; ++v) acc[v] = gl + v * G < D4 ? pl[gl + v * G] : f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-  for (int64_t c = chunk + 1;; ++c) {
-    const f32x4_t* pf = reinterpret_cast<const f32x4_t*>(a.part_first + c * a.D);
-#pragma unroll
-    for (int v = 0; v < VEC; ++v)
-      if (gl + v * G < D4) acc[v] = acc[v] + pf[gl + v * G];
-    const int64_t ce = (c + 1) * kChunk;
-    if (ce >= a.n_pad || a.keys[ce] != key) break;
+  for (int v = 0; v < VEC; ++v)
+    acc[v] = lane < G && gl + v * G < D4 ? pl[gl + v * G] : f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  int64_t pos = chunk + 1;  // first chunk not yet added, at a unit boundary of level L
+  int L = 0;
+  int64_t unit = 1;
+  for (;;) {
+    const int64_t u0 = pos / unit;
+    const int span = 64 - (int)(u0 & 63);
+    const int n = run_units(a.keys, a.n_pad, key, u0, unit, span, lane);
+    if (lane < G) add_rows<G, VEC>(acc, a.part_lv[L], u0, n, a.D, gl);
+    if (n < span) break;
+    pos = (u0 + n) * unit;
+    if (L + 1 < a.num_levels) {
+      ++L;
+      unit *= 64;
+    }
   }
+  if (lane >= G) return;
   const int64_t slot = MODE == MODE_GRAD ? (int64_t)a.head_prefix[chunk + 1] - 1 : 0;
   RowState<VEC> st;
   load_state<G, VEC, MODE>(a, key, gl, st);
@@ -739,6 +825,8 @@ __global__ void write_i64_kernel(int64_t* p, int64_t v) {
 struct BwdLayout {
   int64_t n_pad, num_tiles, num_chunks, dmax;
   int64_t keys_a, keys_b, vals_a, vals_b, bag_scale, hist, totals, part_first, part_last, total;
+  int32_t num_levels;
+  int64_t level[kMaxLevels];  // byte offset of each level >= 1
 };
 
 int64_t align256(int64_t v) { return (v + 255) & ~int64_t(255); }
@@ -766,11 +854,19 @@ BwdLayout bwd_layout(const pdm_tbe_plan_s* plan, int64_t n, int64_t batch_size) 
   L.totals = take(kBins * 4);
   L.part_first = take(L.num_chunks * L.dmax * 4);
   L.part_last = take(L.num_chunks * L.dmax * 4);
+  L.num_levels = 1;
+  int64_t span = 64;
+  while (L.num_levels < kMaxLevels && span < L.num_chunks) {
+    L.level[L.num_levels] = take((L.num_chunks + span - 1) / span * L.dmax * 4);
+    ++L.num_levels;
+    span *= 64;
+  }
   L.total = off;
   return L;
 }
 
 using AccFn = void (*)(AccArgs);
+using FoldFn = void (*)(FoldArgs);
 
 // float4 columns per lane of a row update: fewer lanes per row put more rows
 // of a wavefront in flight (the update is latency-bound on its loads).
@@ -779,13 +875,13 @@ using AccFn = void (*)(AccArgs);
 #endif
 
 template <int MODE>
-bool pick_acc(int D, AccFn& acc, AccFn& fix, int& ng) {
+bool pick_acc(int D, AccFn& acc, AccFn& fix, FoldFn& fold) {
   const int d4 = D / 4;
 #define PDM_ACC_CASE(G_, V_)                            \
   {                                                     \
     acc = bwd_accumulate_kernel<G_, V_, MODE>;          \
     fix = bwd_fixup_kernel<G_, V_, MODE>;               \
-    ng = 64 / G_;                                       \
+    fold = bwd_fold_kernel<G_, V_>;                     \
     return true;                                        \
   }
   constexpr int V = PDM_BWD_VEC;
@@ -802,11 +898,11 @@ bool pick_acc(int D, AccFn& acc, AccFn& fix, int& ng) {
   return false;
 }
 
-bool pick_acc_mode(int mode, int D, AccFn& acc, AccFn& fix, int& ng) {
+bool pick_acc_mode(int mode, int D, AccFn& acc, AccFn& fix, FoldFn& fold) {
   switch (mode) {
-    case MODE_ADAM: return pick_acc<MODE_ADAM>(D, acc, fix, ng);
-    case MODE_ADAGRAD: return pick_acc<MODE_ADAGRAD>(D, acc, fix, ng);
-    default: return pick_acc<MODE_GRAD>(D, acc, fix, ng);
+    case MODE_ADAM: return pick_acc<MODE_ADAM>(D, acc, fix, fold);
+    case MODE_ADAGRAD: return pick_acc<MODE_ADAGRAD>(D, acc, fix, fold);
+    default: return pick_acc<MODE_GRAD>(D, acc, fix, fold);
   }
 }
 
@@ -958,6 +1054,9 @@ int run_backward(const BwdCall& c) {
   a.m2 = c.m2;
   a.part_first = reinterpret_cast<float*>(ws + L.part_first);
   a.part_last = reinterpret_cast<float*>(ws + L.part_last);
+  a.num_levels = L.num_levels;
+  a.part_lv[0] = a.part_first;
+  for (int l = 1; l < L.num_levels; ++l) a.part_lv[l] = reinterpret_cast<float*>(ws + L.level[l]);
   a.n_pad = L.n_pad;
   a.num_chunks = L.num_chunks;
   a.num_bags = T * c.B;
@@ -991,8 +1090,8 @@ int run_backward(const BwdCall& c) {
       continue;
     }
     AccFn acc = nullptr, fix = nullptr;
-    int ng = 1;
-    if (!pick_acc_mode(c.mode, g.dim, acc, fix, ng)) {
+    FoldFn fold = nullptr;
+    if (!pick_acc_mode(c.mode, g.dim, acc, fix, fold)) {
       set_error("pdm_tbe_backward: unsupported dim " + std::to_string(g.dim));
       return PDM_ERR_UNSUPPORTED;
     }
@@ -1014,8 +1113,16 @@ int run_backward(const BwdCall& c) {
     }
     hipLaunchKernelGGL(acc, dim3((unsigned)acc_blocks), dim3(256), 0, c.stream, a);
     PDM_CHECK_LAUNCH();
-    const int64_t fix_blocks = (L.num_chunks + 4 * ng - 1) / (4 * ng);
-    hipLaunchKernelGGL(fix, dim3((unsigned)fix_blocks), dim3(256), 0, c.stream, a);
+    int64_t unit = 1;
+    for (int l = 1; l < L.num_levels; ++l) {
+      FoldArgs fa{kin, a.part_lv[l - 1], const_cast<float*>(a.part_lv[l]), L.n_pad, unit, 0, g.dim, a.key_lo,
+                  a.key_hi};
+      unit *= 64;
+      fa.num_blocks = (L.num_chunks + unit - 1) / unit;
+      hipLaunchKernelGGL(fold, dim3((unsigned)((fa.num_blocks + 3) / 4)), dim3(256), 0, c.stream, fa);
+      PDM_CHECK_LAUNCH();
+    }
+    hipLaunchKernelGGL(fix, dim3((unsigned)acc_blocks), dim3(256), 0, c.stream, a);
     PDM_CHECK_LAUNCH();
   }
   return PDM_OK;

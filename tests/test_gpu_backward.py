@@ -69,11 +69,33 @@ def _sparse(pdm, dev, slots, indices, offsets, B, grad, padding_idx=-1, index_dt
     return out
 
 
+def _exact_rows(slots, indices, offsets, B, grad, padding_idx, ids):
+    """Row gradients summed in float64 (numpy), at the given row ids."""
+    row_off, total = o.row_space(slots)
+    D = max(s["dim"] for s in slots)
+    acc = np.zeros((total, D), np.float64)
+    for t, s in enumerate(slots):
+        lo, hi = offsets[t * B], offsets[(t + 1) * B]
+        idx = indices[lo:hi].astype(np.int64)
+        bag = np.repeat(np.arange(B), np.diff(offsets[t * B:(t + 1) * B + 1]))
+        keep = (idx >= 0) & (idx < s["rows"])
+        if padding_idx >= 0:
+            keep &= idx != padding_idx
+        cnt = np.bincount(bag[keep], minlength=B)
+        sc = 1.0 / np.maximum(cnt[bag[keep]], 1) if s["pooling"] == "mean" else np.ones(int(keep.sum()))
+        cols = grad[:, s["out_offset"]:s["out_offset"] + s["dim"]].astype(np.float64)
+        np.add.at(acc, row_off[t] + idx[keep], np.pad(cols[bag[keep]] * sc[:, None], ((0, 0), (0, D - s["dim"]))))
+    return acc[ids]
+
+
 def _check_sparse(slots, indices, offsets, B, grad, got_ids, got_rows, padding_idx=-1):
+    """Row ids exactly as the oracle's; row gradients within 1e-6 of the sum of |terms| of the exact (float64)
+    sums (the kernel adds a run in lookup order within 64-entry chunks, then the chunk sums in order)."""
     want_ids, want_rows, bad = o.tbe_backward(slots, indices, offsets, B, grad, padding_idx=padding_idx)
     np.testing.assert_array_equal(got_ids, want_ids)
     _, absum, _ = o.tbe_backward(slots, indices, offsets, B, np.abs(grad), padding_idx=padding_idx)
-    err = np.abs(got_rows.astype(np.float64) - want_rows)
+    exact = _exact_rows(slots, indices, offsets, B, grad, padding_idx, got_ids)[:, :got_rows.shape[1]]
+    err = np.abs(got_rows.astype(np.float64) - exact)
     assert np.all(err <= 1e-6 * absum + 1e-30), f"max err {err.max()} at {np.unravel_index(err.argmax(), err.shape)}"
     return bad
 
@@ -120,6 +142,34 @@ def test_sparse_grad_single_row(pdm, dev):
     ids, rows, _ = _sparse(pdm, dev, slots, idx, offsets, 2000, grad)
     assert ids.tolist() == [7]
     _check_sparse(slots, idx, offsets, 2000, grad, ids, rows)
+
+
+@pytest.mark.parametrize("optimizer", [None, o.ADAM])
+def test_very_long_run(pdm, dev, optimizer):
+    # ~540k lookups of one row: the run covers ~8,400 chunks, folded over two levels of 64
+    g = np.random.default_rng(12)
+    B = 60_000
+    slots, flat, idx, offsets, grad = _tables(g, [(5000, 32)], [(0, "sum")], B, lengths=10)
+    idx[g.random(idx.size) < 0.9] = 7
+    if optimizer is None:
+        ids, rows, _ = _sparse(pdm, dev, slots, idx, offsets, B, grad)
+        _check_sparse(slots, idx, offsets, B, grad, ids, rows)
+        return
+    plan = _plan(pdm, dev, slots)
+    w = torch.from_numpy(flat).to(dev)
+    m1, m2 = torch.zeros_like(w), torch.zeros_like(w)
+    pdm.ops.tbe_backward_fused_raw(plan, w, m1, m2, torch.from_numpy(idx).to(dev), torch.from_numpy(offsets).to(dev),
+                                   B, torch.from_numpy(grad).to(dev))
+    wm1, wm2 = np.zeros_like(flat), np.zeros_like(flat)
+    o.tbe_backward(slots, idx, offsets, B, grad, optimizer=o.ADAM, weights=flat, m1=wm1, m2=wm2)
+    _, absum, _ = o.tbe_backward(slots, idx, offsets, B, np.abs(grad))
+    ids, _, _ = o.tbe_backward(slots, idx, offsets, B, grad)
+    gmag = np.zeros_like(flat)
+    for k, a_ in zip(ids, absum):
+        gmag[k * 32:(k + 1) * 32] = a_
+    _close(w.cpu().numpy(), flat, "weights")
+    _close(m1.cpu().numpy(), wm1, "m", gmag)
+    plan.release()
 
 
 def test_sparse_grad_padding_invalid_empty(pdm, dev):
