@@ -13,6 +13,8 @@ fp32 out).  ``--workload`` selects another:
   train_adam  pooled backward + fused Adam (lr 1e-2, eps 1e-8, wd 1e-5): 8 tables x 10,000,000 x 64 fp32,
               sum, Poisson(10) bags in [0, 50], uniform ids, B=65,536 (about 5.2 M lookups)
   train_rowwise_adagrad  the same with fused row-wise Adagrad (L2 weight decay 1e-5)
+  train_seq_adam  S-token gather backward + fused Adam over the seq_gather workload's tables in fp32
+              (item 10M x 256, artist 1M x 64, album 2M x 64; B=1024, 768 slots, row-0 padding)
   copy_1gib   calibration only: a 1 GiB device-to-device copy (the HBM counters' reference kernel)
 
 A step is one forward of the path over one batch already resident in HBM.
@@ -256,6 +258,87 @@ def cpu_train(orc, w, optimizer: str, batch: int, row_cap: int):
     return idx.size, sec
 
 
+def setup_train_seq(pdm, torch, dev, w):
+    """fp32 feature tables of the S-token workload with zeroed Adam state; a step is one gather backward +
+    fused update with a fixed token gradient.  Returns (step, algorithmic bytes, distinct rows, keepalive)."""
+    L = pdm._lib
+    offs, off = [], 0
+    for r, d in zip(w.table_rows, w.table_dims):
+        off = (off + 255) // 256 * 256
+        offs.append(off)
+        off += r * d * 4
+    log(f"allocating {off / 1e9:.2f} GB of fp32 tables (+ Adam state)")
+    flat = torch.empty(off // 4, dtype=torch.float32, device=dev)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(1008)
+    for r0 in range(0, flat.numel(), 1 << 26):
+        flat[r0:r0 + (1 << 26)].uniform_(-0.01, 0.01, generator=gen)
+    slots, col = [], 0
+    for f, (r, d) in enumerate(zip(w.table_rows, w.table_dims)):
+        slots.append(dict(rows=r, weights_offset=offs[f], dim=d, dtype=L.PDM_F32, pooling=L.PDM_POOL_SUM,
+                          row_bytes=4 * d, out_offset=col))
+        col += d
+    plan = pdm.ops.TbePlan(slots, dev)
+    m1, m2 = torch.zeros_like(flat), torch.zeros_like(flat)
+    ids = [[torch.from_numpy(a).to(dev) for a in row] for row in w.ids]
+    offsets = [torch.from_numpy(o).to(dev) for o in w.offsets]
+    S = sum(w.max_len)
+    grad = torch.randn(w.batch, S, col, device=dev, generator=gen)
+    ws = pdm.ops.tbe_backward_workspace(plan, len(slots) * w.batch * S, w.batch * S, dev)
+    counter = [0]
+
+    def step():
+        counter[0] += 1
+        pdm.ops.seq_gather_backward_fused_raw(plan, flat, m1, m2, w.table_rows, w.table_dims, ids, offsets,
+                                              w.max_len, grad, learning_rate=0.01, eps=1e-8, weight_decay=1e-5,
+                                              step=counter[0], workspace=ws)
+
+    # distinct rows: the kept events' ids per table, plus row 0 when some slot is padding; each distinct row's
+    # weights and both Adam moments are read and written once
+    distinct, kept, upd = 0, 0, 0
+    for f, d in enumerate(w.table_dims):
+        seen, pad = [], False
+        for p, (o, m) in enumerate(zip(w.offsets, w.max_len)):
+            k = np.minimum(np.diff(o), m)
+            pad = pad or bool((k < m).any())
+            sel = np.concatenate([np.arange(a, a + n) for a, n in zip(o[1:] - k, k)])
+            seen.append(w.ids[p][f][sel])
+            if f == 0:
+                kept += int(k.sum())
+        u = np.unique(np.concatenate(seen + ([np.zeros(1, np.int64)] if pad else [])))
+        distinct += int(u.size)
+        upd += int(u.size) * 6 * 4 * d
+    alg_bytes = kept * 3 * 8 + sum(o.size * 8 for o in w.offsets) + w.batch * S * col * 4 + upd
+    return step, alg_bytes, distinct, kept, (flat, m1, m2, plan, ids, offsets, grad, ws)
+
+
+def cpu_train_seq(orc, w, batch: int, row_cap: int):
+    """The oracle's gather backward + Adam over the first ``batch`` samples, tables capped at ``row_cap`` rows."""
+    g = np.random.default_rng(9)
+    rows = [min(r, row_cap) for r in w.table_rows]
+    slots, off, col = [], 0, 0
+    for r, d in zip(rows, w.table_dims):
+        slots.append(dict(rows=r, weights_offset=off * 4, dim=d, dtype="fp32", pooling="sum", row_bytes=0,
+                          out_offset=col))
+        off += r * d
+        col += d
+    ids = [[a[:o[batch]] % r for a, r in zip(row, rows)] for row, o in zip(w.ids, w.offsets)]
+    offsets = [o[:batch + 1] for o in w.offsets]
+    S = sum(w.max_len)
+    grad = g.standard_normal((batch, S, col), dtype=np.float32)
+    flat = (g.random(off, dtype=np.float32) - np.float32(0.5)) * np.float32(0.02)
+    m1, m2 = np.zeros(off, np.float32), np.zeros(off, np.float32)
+    step = [0]
+
+    def run():
+        step[0] += 1
+        orc.seq_gather_backward(slots, ids, offsets, w.max_len, grad, optimizer=orc.ADAM, weights=flat, m1=m1,
+                                m2=m2, lr=0.01, eps=1e-8, weight_decay=1e-5, step=step[0])
+
+    sec = time_cpu(run)
+    return batch * S, sec
+
+
 # ----------------------------------------------------------------------------------------------
 # S-token gather
 # ----------------------------------------------------------------------------------------------
@@ -356,7 +439,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="single_hot",
                     choices=["single_hot", "ebc_fp32", "int8_mean", "seq_gather", "onetrans", "cross_hash",
-                             "train_adam", "train_rowwise_adagrad", "copy_1gib"])
+                             "train_adam", "train_rowwise_adagrad", "train_seq_adam", "copy_1gib"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
 
@@ -447,6 +530,24 @@ def main() -> int:
                     "sample": f"C oracle (one thread): backward + {optimizer} over the first {cpu_b} bags of each "
                               f"table ({n} lookups) on tables capped at {cpu_cap} rows (ids modulo), "
                               f"median of 5 reps = {sec:.3f} s"}
+    elif args.workload == "train_seq_adam":
+        w = syn.seq_gather()
+        step, alg, distinct, kept, keep = setup_train_seq(pdm, torch, dev, w)
+        S = sum(w.max_len)
+        units, unit, bound, dtype = w.batch * S, "slots/s", "hbm", "f32"
+        cfg = {"workload": "seq_gather_3pools_b1024_fp32_adam", "batch": w.batch, "slots": S,
+               "tables": {"rows": w.table_rows, "dims": w.table_dims}, "events_kept": kept,
+               "distinct_rows": distinct, "pad": "row0 (pad slots update row 0, as the reference's pad id 0)",
+               "optimizer": "adam", "lr": 0.01, "eps": 1e-8, "weight_decay": 1e-5,
+               "timed": "whole fused gather backward"}
+        cpu_b, cpu_cap = 256, 250_000
+
+        def cpu_fn():
+            n, sec = cpu_train_seq(orc, w, cpu_b, cpu_cap)
+            return {"value": round(n / sec, 1), "unit": unit, "cores": 1, "kind": "port",
+                    "sample": f"C oracle (one thread, slot placement in numpy): gather backward + Adam over the "
+                              f"first {cpu_b} samples ({n} slots x 3 features) on tables capped at {cpu_cap} rows "
+                              f"(ids modulo), median of 5 reps = {sec:.3f} s"}
     elif args.workload == "copy_1gib":
         # calibration: a plain device copy of 1 GiB (reads 1 GiB, writes 1 GiB) for the HBM counters
         src = torch.ones(1 << 28, dtype=torch.float32, device=dev)

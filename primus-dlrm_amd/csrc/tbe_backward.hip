@@ -546,16 +546,22 @@ __device__ __forceinline__ void update_row(const AccArgs& a, uint32_t key, const
   }
 }
 
+// Gradient rows in flight per lane group while a run is summed.
+#ifndef PDM_BWD_UNROLL
+#define PDM_BWD_UNROLL 4
+#endif
+
 // acc += sc * grad row, over the entries [i, e] of a wave's chunk, in order
-// (4 gradient rows in flight).
+// (U gradient rows in flight).
 template <int G, int VEC>
 __device__ __forceinline__ void sum_entries(const uint32_t* s_off, const float* s_sc, int i, int e,
                                             const f32x4_t* grad4, int gl, int D4, f32x4_t (&acc)[VEC]) {
-  for (; i + 3 <= e; i += 4) {
-    f32x4_t gv[4][VEC];
-    float sc[4];
+  constexpr int U = VEC == 1 ? PDM_BWD_UNROLL : 4;
+  for (; i + U - 1 <= e; i += U) {
+    f32x4_t gv[U][VEC];
+    float sc[U];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < U; ++u) {
       const uint32_t off = s_off[i + u];
       sc[u] = s_sc[i + u];
 #pragma unroll
@@ -563,7 +569,7 @@ __device__ __forceinline__ void sum_entries(const uint32_t* s_off, const float* 
         gv[u][v] = gl + v * G < D4 ? grad4[off + gl + v * G] : f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
     }
 #pragma unroll
-    for (int u = 0; u < 4; ++u)
+    for (int u = 0; u < U; ++u)
 #pragma unroll
       for (int v = 0; v < VEC; ++v)
 #pragma unroll
