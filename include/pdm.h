@@ -326,6 +326,46 @@ int pdm_onetrans_block_fwd(const pdm_block_desc* desc, const float* x,
                            pdm_stream_t stream);
 
 /* ------------------------------------------------------------------------
+ * KeyedJaggedTensor construction on the device (no host synchronisation).
+ *
+ * Replaces _build_pooled_kjt (primus_dlrm/models/embedding.py:177-204): per
+ * feature, mask = ids != padding_idx over a dense [B, L] id matrix, lengths =
+ * mask.sum(1), values = ids[mask] (row-major), features concatenated in
+ * order; and the key permutation of build_kjt / KJT.permute
+ * (primus_dlrm/data/pipeline_batch.py:70-100).  The reference sizes `values`
+ * with a host sync; here values are written into a buffer of the known
+ * capacity and the exact count is offsets[rows] on the device.
+ * ------------------------------------------------------------------------ */
+
+#define PDM_KJT_MAX_FEATURES 64
+
+/* Workspace bytes for num_rows (= keys * batch) lengths. */
+int64_t pdm_kjt_workspace_size(int64_t num_rows);
+
+/* ids[f]:    device [B, row_len[f]] int32 / int64 (index_bits), row-major
+ * row_len:   host [num_features]
+ * values:    device, capacity sum_f B * row_len[f] ids of the same type;
+ *            the first offsets[F*B] hold the kept ids, feature-major
+ * lengths:   device int32 [F * B]; offsets: device int64 [F * B + 1]
+ * padding_idx < 0 keeps every id. */
+int pdm_kjt_from_dense(const void* const* ids, const int32_t* row_len,
+                       int32_t num_features, int64_t batch_size,
+                       int32_t index_bits, int64_t padding_idx, void* values,
+                       int32_t* lengths, int64_t* offsets, void* workspace,
+                       int64_t workspace_bytes, pdm_stream_t stream);
+
+/* Reorders the keys of a KJT (values, offsets [num_keys * B + 1]): output key
+ * k is input key perm[k] (host array, num_out <= PDM_KJT_MAX_FEATURES; keys
+ * may repeat or be dropped).  out_values: capacity of the input's values;
+ * out_lengths int32 [num_out * B]; out_offsets int64 [num_out * B + 1]. */
+int pdm_kjt_permute(const void* values, int32_t index_bits,
+                    const int64_t* offsets, int32_t num_keys,
+                    int64_t batch_size, const int32_t* perm, int32_t num_out,
+                    void* out_values, int32_t* out_lengths,
+                    int64_t* out_offsets, void* workspace,
+                    int64_t workspace_bytes, pdm_stream_t stream);
+
+/* ------------------------------------------------------------------------
  * Cross-feature ids: xxHash64 of the little-endian concatenation of n int64
  * keys, seeded with salt, modulo table_size (an unsigned 64-bit remainder).
  *

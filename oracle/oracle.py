@@ -21,6 +21,8 @@ reference's lookup semantics on the CPU:
                       update per distinct row (fbgemm_gpu 2026.4.29, absent here; rules
                       restated at oracle_tbe_backward in pdm_oracle.c).  ``row_space``
                       numbers the distinct tables the way the library documents it.
+* ``kjt_from_dense`` / ``kjt_permute``  KJT construction: _build_pooled_kjt (embedding.py:177-204, padding
+                      filter per row, lengths, key-major concat) and key permutation (pipeline_batch.py:70-100).
 * ``seq_gather_backward`` the S-token gather's backward: ``seq_token_ids`` restates the forward's slot
                       placement (dataset.py:604-626, onetrans.py:515-520,553-558) and every slot becomes
                       a one-id bag of ``tbe_backward``.
@@ -379,3 +381,31 @@ def seq_gather_backward(slots: Sequence[dict], ids, offsets, max_len, grad: np.n
     g2 = np.ascontiguousarray(grad, dtype=np.float32).reshape(B * S, -1)
     return tbe_backward(slots, tok.reshape(-1), np.arange(F * B * S + 1, dtype=np.int64), B * S, g2,
                         padding_idx=SEQ_PAD, **kw)
+
+
+# ---- KeyedJaggedTensor construction ----------------------------------------------------------
+
+def kjt_from_dense(mats: Sequence[np.ndarray], padding_idx: int = -1):
+    """Per feature, per row of the dense [B, L] ids, the ids != padding_idx in row order, features concatenated;
+    returns (values, lengths int32 [F*B], offsets int64 [F*B+1])."""
+    vals, lens = [], []
+    for m in mats:
+        m = np.asarray(m)
+        keep = np.ones(m.shape, bool) if padding_idx < 0 else m != padding_idx
+        vals.append(m[keep])
+        lens.append(keep.sum(axis=1).astype(np.int32))
+    lengths = np.concatenate(lens) if lens else np.zeros(0, np.int32)
+    values = np.concatenate(vals) if vals else np.zeros(0, np.int64)
+    return values, lengths, offsets_np(lengths)
+
+
+def kjt_permute(values: np.ndarray, offsets: np.ndarray, num_keys: int, batch: int, perm: Sequence[int]):
+    """Output key k = input key perm[k]: its B bags copied in order."""
+    segs, lens = [], []
+    for k in perm:
+        for b in range(batch):
+            lo, hi = int(offsets[k * batch + b]), int(offsets[k * batch + b + 1])
+            segs.append(values[lo:hi])
+            lens.append(hi - lo)
+    lengths = np.asarray(lens, np.int32)
+    return (np.concatenate(segs) if segs else values[:0]), lengths, offsets_np(lengths)

@@ -28,6 +28,7 @@ PDM_SEQ_MAX_POOLS = 8
 PDM_SEQ_MAX_FEATURES = 8
 PDM_OPT_ADAM, PDM_OPT_ROWWISE_ADAGRAD, PDM_OPT_NONE = 0, 1, 2
 PDM_WD_NONE, PDM_WD_L2 = 0, 1
+PDM_KJT_MAX_FEATURES = 64
 
 # Every symbol include/pdm.h declares (checked by the ABI test).
 EXPORTED_SYMBOLS = (
@@ -45,6 +46,9 @@ EXPORTED_SYMBOLS = (
     "pdm_tbe_backward_sparse_grad",
     "pdm_tbe_plan_set_state_offsets",
     "pdm_seq_gather_backward_fused",
+    "pdm_kjt_workspace_size",
+    "pdm_kjt_from_dense",
+    "pdm_kjt_permute",
     "pdm_seq_gather_fwd",
     "pdm_cross_hash_fwd",
     "pdm_onetrans_block_workspace_size",
@@ -176,6 +180,13 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.pdm_seq_gather_backward_fused.argtypes = [vp, ctypes.POINTER(SeqDesc), vp, vp, vp, ctypes.POINTER(vp),
                                                   ctypes.POINTER(vp), vp, ctypes.POINTER(OptimParams), vp, i64, vp,
                                                   vp]
+    lib.pdm_kjt_workspace_size.restype = i64
+    lib.pdm_kjt_workspace_size.argtypes = [i64]
+    lib.pdm_kjt_from_dense.restype = ctypes.c_int
+    lib.pdm_kjt_from_dense.argtypes = [ctypes.POINTER(vp), ctypes.POINTER(i32), i32, i64, i32, i64, vp, vp, vp, vp,
+                                       i64, vp]
+    lib.pdm_kjt_permute.restype = ctypes.c_int
+    lib.pdm_kjt_permute.argtypes = [vp, i32, vp, i32, i64, ctypes.POINTER(i32), i32, vp, vp, vp, vp, i64, vp]
     lib.pdm_cross_hash_fwd.restype = ctypes.c_int
     lib.pdm_cross_hash_fwd.argtypes = [ctypes.POINTER(vp), ctypes.POINTER(i64), i32, i64, ctypes.c_uint64,
                                        ctypes.c_uint64, vp, vp]

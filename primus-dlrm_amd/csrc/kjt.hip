@@ -1,0 +1,352 @@
+// KeyedJaggedTensor construction on the device, without host synchronisation.
+//
+// Reference: _build_pooled_kjt (primus_dlrm/models/embedding.py:177-204): per
+// feature in feature order, mask = ids != padding_idx over a dense [B, L]
+// id matrix, lengths = mask.sum(1) (int32), values = ids[mask] (row-major
+// order), concatenated over the features; build_kjt / _build_unpooled_kjt
+// (primus_dlrm/data/pipeline_batch.py:70-100, embedding.py:207-232) and
+// TorchRec's KJT.permute reorder keys.  The reference's boolean indexing
+// synchronises the host to size `values`; here every output is written into
+// a buffer of the known capacity (the total id count of the inputs) and the
+// exact size lives on the device, in offsets[F * B].
+//
+// Kernels (all HBM-bound integer work):
+//  * count: a group of G lanes per (feature, row) reads the row's ids with
+//    coalesced loads and counts the non-padding ids with a ballot;
+//  * scan:  lengths -> int64 offsets in three launches (per-block sums, one
+//    block scanning the block sums, per-block exclusive scan + carry);
+//  * compact: the same groups re-read the row and write each kept id at
+//    offsets[row] + (kept ids before it in the row), found with the ballot's
+//    lane mask, so the output keeps row-major order;
+//  * permute: one wavefront per output row copies its segment.
+#include <algorithm>
+#include <vector>
+
+#include "pdm_common.h"
+
+namespace pdm {
+
+namespace {
+
+constexpr int kScanBlock = 1024;  // lengths per scan block (256 threads x 4)
+
+struct KjtDenseArgs {
+  const void* ids[PDM_KJT_MAX_FEATURES];
+  int64_t row0[PDM_KJT_MAX_FEATURES + 1];  // first (feature, row) index of each feature (f * B)
+  int32_t len[PDM_KJT_MAX_FEATURES];       // ids per row of each feature
+  int32_t F;
+  int32_t index_bits;
+  int64_t B;
+  int64_t rows;  // F * B
+  int64_t padding_idx;
+  int32_t* lengths;
+  const int64_t* offsets;
+  void* values;
+};
+
+__device__ __forceinline__ int64_t load_id(const void* p, int64_t i, int bits) {
+  return bits == 32 ? (int64_t) reinterpret_cast<const int32_t*>(p)[i] : reinterpret_cast<const int64_t*>(p)[i];
+}
+
+// Groups of G lanes per (feature, row); COMPACT = false counts, true writes.
+template <int G, bool COMPACT>
+__global__ __launch_bounds__(256) void kjt_dense_kernel(KjtDenseArgs a) {
+  constexpr int RPW = 64 / G;  // rows per wavefront
+  const int lane = threadIdx.x & 63, gl = lane & (G - 1), grp = lane / G;
+  const int64_t row = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW + grp;
+  const bool live = row < a.rows;
+  int f = 0;
+  if (live)
+    while (f + 1 < a.F && row >= a.row0[f + 1]) ++f;
+  const int64_t b = live ? row - a.row0[f] : 0;
+  const int L = live ? a.len[f] : 0;
+  const bool has_pad = a.padding_idx >= 0;
+  const uint64_t gmask = G == 64 ? ~uint64_t(0) : ((uint64_t(1) << G) - 1) << (grp * G);
+  const uint64_t lt = (uint64_t(1) << lane) - 1;
+  int64_t out = 0;
+  if constexpr (COMPACT) {
+    if (live) out = a.offsets[row];
+  }
+  int count = 0;
+  // every lane runs the same number of rounds (the longest row of the wavefront is not known, so rounds
+  // cover the longest feature); lanes past their row's end hold no id
+  int Lmax = 0;
+  for (int i = 0; i < a.F; ++i) Lmax = max(Lmax, a.len[i]);
+  for (int c = 0; c < Lmax; c += G) {
+    const int k = c + gl;
+    bool keep = false;
+    int64_t v = 0;
+    if (live && k < L) {
+      v = load_id(a.ids[f], b * L + k, a.index_bits);
+      keep = !(has_pad && v == a.padding_idx);
+    }
+    const uint64_t m = __ballot(keep) & gmask;
+    if constexpr (COMPACT) {
+      if (keep) {
+        const int64_t at = out + count + __popcll(m & lt);
+        if (a.index_bits == 32) reinterpret_cast<int32_t*>(a.values)[at] = (int32_t)v;
+        else reinterpret_cast<int64_t*>(a.values)[at] = v;
+      }
+    }
+    count += __popcll(m);
+  }
+  if constexpr (!COMPACT) {
+    if (live && gl == 0) a.lengths[row] = count;
+  }
+}
+
+// Per-block sums of lengths (1024 per block).
+__global__ __launch_bounds__(256) void kjt_block_sums_kernel(const int32_t* __restrict__ lengths, int64_t n,
+                                                             int64_t* __restrict__ sums) {
+  __shared__ int64_t w[4];
+  const int64_t i0 = (int64_t)blockIdx.x * kScanBlock + threadIdx.x * 4;
+  int64_t s = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) s += i0 + j < n ? (int64_t)lengths[i0 + j] : 0;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o);
+  if ((threadIdx.x & 63) == 0) w[threadIdx.x >> 6] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) sums[blockIdx.x] = w[0] + w[1] + w[2] + w[3];
+}
+
+__device__ __forceinline__ int64_t wave_incl_scan64(int64_t v, int lane) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int64_t t = __shfl_up(v, o);
+    if (lane >= o) v += t;
+  }
+  return v;
+}
+
+// Exclusive scan of 4 values per thread over a 256-thread block, plus carry; returns the block total.
+__device__ __forceinline__ int64_t block_scan4(int64_t (&v)[4], int64_t carry, int64_t* tmp) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t t = v[0] + v[1] + v[2] + v[3];
+  const int64_t incl = wave_incl_scan64(t, lane);
+  if (lane == 63) tmp[w] = incl;
+  __syncthreads();
+  int64_t pre = carry;
+  for (int i = 0; i < w; ++i) pre += tmp[i];
+  const int64_t total = tmp[0] + tmp[1] + tmp[2] + tmp[3];
+  int64_t run = pre + incl - t;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int64_t x = v[j];
+    v[j] = run;
+    run += x;
+  }
+  __syncthreads();
+  return total;
+}
+
+// One block: exclusive scan of the block sums in place.
+__global__ __launch_bounds__(256) void kjt_scan_sums_kernel(int64_t* __restrict__ sums, int64_t nblocks) {
+  __shared__ int64_t tmp[4];
+  int64_t carry = 0;
+  for (int64_t base = 0; base < nblocks; base += kScanBlock) {
+    const int64_t i0 = base + threadIdx.x * 4;
+    int64_t v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = i0 + j < nblocks ? sums[i0 + j] : 0;
+    const int64_t total = block_scan4(v, carry, tmp);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (i0 + j < nblocks) sums[i0 + j] = v[j];
+    carry += total;
+  }
+}
+
+// offsets[i] = sums[block] + exclusive scan inside the block; offsets[n] = the total.
+__global__ __launch_bounds__(256) void kjt_offsets_kernel(const int32_t* __restrict__ lengths, int64_t n,
+                                                          const int64_t* __restrict__ sums,
+                                                          int64_t* __restrict__ offsets) {
+  __shared__ int64_t tmp[4];
+  const int64_t i0 = (int64_t)blockIdx.x * kScanBlock + threadIdx.x * 4;
+  int64_t v[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) v[j] = i0 + j < n ? (int64_t)lengths[i0 + j] : 0;
+  const int64_t carry = sums[blockIdx.x];
+  const int64_t total = block_scan4(v, carry, tmp);
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    if (i0 + j < n) offsets[i0 + j] = v[j];
+  if (blockIdx.x == gridDim.x - 1 && threadIdx.x == 0) offsets[n] = carry + total;
+}
+
+struct PermArgs {
+  const void* values;
+  const int64_t* offsets;  // input, [K * B + 1]
+  int32_t* lengths;        // output, [K' * B]
+  const int64_t* out_offsets;
+  void* out_values;
+  int32_t perm[PDM_KJT_MAX_FEATURES];
+  int32_t num_out;
+  int32_t index_bits;
+  int64_t B;
+  int64_t rows;  // K' * B
+};
+
+// lengths' of every output row.
+__global__ __launch_bounds__(256) void kjt_perm_lengths_kernel(PermArgs a) {
+  const int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (r >= a.rows) return;
+  const int64_t k = r / a.B, b = r - k * a.B;
+  const int64_t src = (int64_t)a.perm[k] * a.B + b;
+  a.lengths[r] = (int32_t)(a.offsets[src + 1] - a.offsets[src]);
+}
+
+// One wavefront per output row copies the row's segment (coalesced).
+__global__ __launch_bounds__(256) void kjt_perm_copy_kernel(PermArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= a.rows) return;
+  const int64_t k = r / a.B, b = r - k * a.B;
+  const int64_t src = (int64_t)a.perm[k] * a.B + b;
+  const int64_t s0 = a.offsets[src], n = a.offsets[src + 1] - s0, d0 = a.out_offsets[r];
+  if (a.index_bits == 32) {
+    const int32_t* in = reinterpret_cast<const int32_t*>(a.values) + s0;
+    int32_t* out = reinterpret_cast<int32_t*>(a.out_values) + d0;
+    for (int64_t i = lane; i < n; i += 64) out[i] = in[i];
+  } else {
+    const int64_t* in = reinterpret_cast<const int64_t*>(a.values) + s0;
+    int64_t* out = reinterpret_cast<int64_t*>(a.out_values) + d0;
+    for (int64_t i = lane; i < n; i += 64) out[i] = in[i];
+  }
+}
+
+int64_t scan_blocks(int64_t n) { return (n + kScanBlock - 1) / kScanBlock; }
+
+// lengths [n] -> offsets [n + 1] on the stream; sums: scan_blocks(n) int64 of workspace.
+int launch_scan(const int32_t* lengths, int64_t n, int64_t* sums, int64_t* offsets, hipStream_t s) {
+  const int64_t nb = scan_blocks(n);
+  PDM_CHECK_ARG(nb < (int64_t(1) << 31), "too many rows");
+  hipLaunchKernelGGL(kjt_block_sums_kernel, dim3((unsigned)nb), dim3(256), 0, s, lengths, n, sums);
+  PDM_CHECK_LAUNCH();
+  hipLaunchKernelGGL(kjt_scan_sums_kernel, dim3(1), dim3(256), 0, s, sums, nb);
+  PDM_CHECK_LAUNCH();
+  hipLaunchKernelGGL(kjt_offsets_kernel, dim3((unsigned)nb), dim3(256), 0, s, lengths, n, sums, offsets);
+  PDM_CHECK_LAUNCH();
+  return PDM_OK;
+}
+
+__global__ void kjt_zero_kernel(int64_t* p) {
+  if (threadIdx.x == 0) *p = 0;
+}
+
+}  // namespace
+
+}  // namespace pdm
+
+using namespace pdm;
+
+extern "C" int64_t pdm_kjt_workspace_size(int64_t num_rows) {
+  if (num_rows < 0) return -1;
+  return std::max<int64_t>(scan_blocks(num_rows), 1) * 8;
+}
+
+extern "C" int pdm_kjt_from_dense(const void* const* ids, const int32_t* row_len, int32_t num_features,
+                                  int64_t batch_size, int32_t index_bits, int64_t padding_idx, void* values,
+                                  int32_t* lengths, int64_t* offsets, void* workspace, int64_t workspace_bytes,
+                                  pdm_stream_t stream) {
+  clear_error();
+  PDM_CHECK_ARG(num_features >= 0 && num_features <= PDM_KJT_MAX_FEATURES, "num_features out of range");
+  PDM_CHECK_ARG(index_bits == 32 || index_bits == 64, "index_bits must be 32 or 64");
+  PDM_CHECK_ARG(batch_size >= 0, "batch_size < 0");
+  PDM_CHECK_ARG(offsets != nullptr, "null offsets");
+  auto s = reinterpret_cast<hipStream_t>(stream);
+  const int64_t rows = (int64_t)num_features * batch_size;
+  if (rows == 0) {
+    hipLaunchKernelGGL(kjt_zero_kernel, dim3(1), dim3(64), 0, s, offsets);
+    PDM_CHECK_LAUNCH();
+    return PDM_OK;
+  }
+  PDM_CHECK_ARG(ids && row_len && lengths && values, "null argument");
+  PDM_CHECK_ARG(workspace != nullptr && workspace_bytes >= pdm_kjt_workspace_size(rows), "workspace too small");
+  KjtDenseArgs a{};
+  int32_t Lmax = 0;
+  for (int f = 0; f < num_features; ++f) {
+    PDM_CHECK_ARG(row_len[f] >= 0, "row length < 0");
+    PDM_CHECK_ARG(row_len[f] == 0 || ids[f] != nullptr, "null ids pointer");
+    a.ids[f] = ids[f];
+    a.len[f] = row_len[f];
+    a.row0[f] = (int64_t)f * batch_size;
+    Lmax = std::max(Lmax, row_len[f]);
+  }
+  a.row0[num_features] = rows;
+  a.F = num_features;
+  a.index_bits = index_bits;
+  a.B = batch_size;
+  a.rows = rows;
+  a.padding_idx = padding_idx;
+  a.lengths = lengths;
+  a.offsets = offsets;
+  a.values = values;
+  int G = 1;
+  while (G < Lmax && G < 64) G <<= 1;
+  const int64_t rpb = 4 * (64 / G);
+  const int64_t blocks = (rows + rpb - 1) / rpb;
+  PDM_CHECK_ARG(blocks < (int64_t(1) << 31), "too many rows");
+#define PDM_KJT_LAUNCH(G_, C_) hipLaunchKernelGGL((kjt_dense_kernel<G_, C_>), dim3((unsigned)blocks), dim3(256), 0, s, a)
+#define PDM_KJT_BY_G(C_)                 \
+  switch (G) {                           \
+    case 1: PDM_KJT_LAUNCH(1, C_); break;   \
+    case 2: PDM_KJT_LAUNCH(2, C_); break;   \
+    case 4: PDM_KJT_LAUNCH(4, C_); break;   \
+    case 8: PDM_KJT_LAUNCH(8, C_); break;   \
+    case 16: PDM_KJT_LAUNCH(16, C_); break; \
+    case 32: PDM_KJT_LAUNCH(32, C_); break; \
+    default: PDM_KJT_LAUNCH(64, C_); break; \
+  }
+  PDM_KJT_BY_G(false)
+  PDM_CHECK_LAUNCH();
+  const int rc = launch_scan(lengths, rows, reinterpret_cast<int64_t*>(workspace), offsets, s);
+  if (rc != PDM_OK) return rc;
+  PDM_KJT_BY_G(true)
+  PDM_CHECK_LAUNCH();
+#undef PDM_KJT_BY_G
+#undef PDM_KJT_LAUNCH
+  return PDM_OK;
+}
+
+extern "C" int pdm_kjt_permute(const void* values, int32_t index_bits, const int64_t* offsets, int32_t num_keys,
+                               int64_t batch_size, const int32_t* perm, int32_t num_out, void* out_values,
+                               int32_t* out_lengths, int64_t* out_offsets, void* workspace, int64_t workspace_bytes,
+                               pdm_stream_t stream) {
+  clear_error();
+  PDM_CHECK_ARG(index_bits == 32 || index_bits == 64, "index_bits must be 32 or 64");
+  PDM_CHECK_ARG(num_keys >= 0 && num_out >= 0 && num_out <= PDM_KJT_MAX_FEATURES, "key counts out of range");
+  PDM_CHECK_ARG(batch_size >= 0, "batch_size < 0");
+  PDM_CHECK_ARG(out_offsets != nullptr, "null out_offsets");
+  auto s = reinterpret_cast<hipStream_t>(stream);
+  const int64_t rows = (int64_t)num_out * batch_size;
+  if (rows == 0) {
+    hipLaunchKernelGGL(kjt_zero_kernel, dim3(1), dim3(64), 0, s, out_offsets);
+    PDM_CHECK_LAUNCH();
+    return PDM_OK;
+  }
+  PDM_CHECK_ARG(perm && offsets && out_lengths && out_values, "null argument");
+  PDM_CHECK_ARG(workspace != nullptr && workspace_bytes >= pdm_kjt_workspace_size(rows), "workspace too small");
+  PermArgs a{};
+  for (int k = 0; k < num_out; ++k) {
+    PDM_CHECK_ARG(perm[k] >= 0 && perm[k] < num_keys, "perm entry out of range");
+    a.perm[k] = perm[k];
+  }
+  a.values = values;
+  a.offsets = offsets;
+  a.lengths = out_lengths;
+  a.out_offsets = out_offsets;
+  a.out_values = out_values;
+  a.num_out = num_out;
+  a.index_bits = index_bits;
+  a.B = batch_size;
+  a.rows = rows;
+  PDM_CHECK_ARG((rows + 255) / 256 < (int64_t(1) << 31), "too many rows");
+  hipLaunchKernelGGL(kjt_perm_lengths_kernel, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, s, a);
+  PDM_CHECK_LAUNCH();
+  const int rc = launch_scan(out_lengths, rows, reinterpret_cast<int64_t*>(workspace), out_offsets, s);
+  if (rc != PDM_OK) return rc;
+  hipLaunchKernelGGL(kjt_perm_copy_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, a);
+  PDM_CHECK_LAUNCH();
+  return PDM_OK;
+}

@@ -219,9 +219,8 @@ class _FlatTables(nn.Module):
 def _kjt_slot_offsets(kjt, order: List[str]) -> Tuple[torch.Tensor, torch.Tensor]:
     """Returns (values, offsets) with bags laid out key-major in ``order``.
 
-    Zero copy when the KJT already holds exactly ``order``; otherwise values
-    are gathered on the device into the requested key order (TorchRec permutes
-    the KJT the same way before its lookup)."""
+    Zero copy when the KJT already holds exactly ``order``; otherwise the keys are permuted on the device
+    (pdm_kjt_permute, no host sync; TorchRec permutes the KJT the same way before its lookup)."""
     keys = list(kjt.keys())
     values = kjt.values()
     B = kjt.stride()
@@ -232,21 +231,8 @@ def _kjt_slot_offsets(kjt, order: List[str]) -> Tuple[torch.Tensor, torch.Tensor
     missing = [k for k in order if k not in pos]
     if missing:
         raise KeyError(f"KeyedJaggedTensor lacks features {missing}")
-    dev = values.device
-    lengths = kjt.lengths().to(torch.int64).view(len(keys), B)
-    perm = torch.tensor([pos[k] for k in order], device=dev)
-    new_lengths = lengths.index_select(0, perm).reshape(-1)
-    new_offsets = torch.zeros(new_lengths.numel() + 1, dtype=torch.int64, device=dev)
-    torch.cumsum(new_lengths, 0, out=new_offsets[1:])
-    if sorted(order) == sorted(keys):
-        total = values.numel()
-    else:
-        total = int(new_offsets[-1].item())  # a subset of keys: the output size needs one sync
-    i = torch.arange(total, device=dev)
-    seg = torch.searchsorted(new_offsets, i, right=True) - 1
-    old_starts = offsets[:-1].view(len(keys), B).index_select(0, perm).reshape(-1)
-    src = old_starts[seg] + (i - new_offsets[seg])
-    return values[src], new_offsets
+    v, _, o = ops.kjt_permute_raw(values, offsets.contiguous(), len(keys), B, [pos[k] for k in order])
+    return v, o
 
 
 class EmbeddingBagCollection(nn.Module):

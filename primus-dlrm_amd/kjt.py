@@ -8,6 +8,11 @@ TorchRec's: ``values`` holds the ids of every (key, sample) bag key-major,
 ``lengths`` is ``[len(keys) * stride]``.  Offsets are computed on the device
 with a cumulative sum, so building one never synchronises the host.
 
+``build_pooled_kjt`` / ``build_unpooled_kjt`` / ``build_kjt`` mirror the reference's builders
+(embedding.py:177-232, data/pipeline_batch.py:70-100) and ``KeyedJaggedTensor.permute`` TorchRec's; on the GPU
+the padding filter and the permutation run in the library's kernels without a host sync, so ``values()`` of
+such a KJT is a buffer of the known capacity whose first ``offsets()[-1]`` entries are the ids.
+
 ``KeyedTensor`` (pooled output, ``kt[key] -> [B, D]``, embedding.py:154) and
 ``JaggedTensor`` (unpooled output, ``jt.values() -> [sum len, D]``,
 embedding.py:161-172) are the matching result types.  Objects from a real
@@ -86,6 +91,17 @@ class KeyedJaggedTensor:
     def device(self) -> torch.device:
         return self._values.device
 
+    def permute(self, indices: List[int]) -> "KeyedJaggedTensor":
+        """Output key k is key ``indices[k]`` (TorchRec's KJT.permute); keys may repeat or be dropped.
+        On the GPU one kernel pass, no host sync."""
+        if self._values.device.type != "cuda":
+            raise RuntimeError("KeyedJaggedTensor.permute runs on the GPU only")
+        from . import ops
+        v, lengths, offsets = ops.kjt_permute_raw(self._values, self.offsets().to(torch.int64), len(self._keys),
+                                                  self._stride, list(indices))
+        return KeyedJaggedTensor([self._keys[i] for i in indices], v, lengths=lengths, offsets=offsets,
+                                 stride=self._stride)
+
     def __repr__(self) -> str:
         return f"KeyedJaggedTensor(keys={self._keys}, stride={self._stride}, values={tuple(self._values.shape)})"
 
@@ -152,3 +168,64 @@ class JaggedTensor:
         if self._offsets is None:
             self._offsets = _offsets_from_lengths(self._lengths)
         return self._offsets
+
+
+def build_pooled_kjt(features: Dict[str, torch.Tensor], feature_order: List[str],
+                     padding_idx: int) -> KeyedJaggedTensor:
+    """``_build_pooled_kjt`` (primus_dlrm/models/embedding.py:177-204): per feature present in
+    ``feature_order``, the ids of each row of ``features[name]`` ([B, L]) that differ from ``padding_idx``,
+    in row order; lengths int32.  On the GPU: ``pdm_kjt_from_dense``, no host sync."""
+    names = [n for n in feature_order if n in features]
+    if not names:
+        return KeyedJaggedTensor([], torch.empty(0, dtype=torch.long), lengths=torch.empty(0, dtype=torch.int32))
+    mats = [features[n] if features[n].dim() == 2 else features[n].reshape(features[n].shape[0], -1) for n in names]
+    if mats[0].device.type != "cuda":
+        raise RuntimeError("build_pooled_kjt runs on the GPU only")
+    from . import ops
+    dt = torch.int64 if any(m.dtype == torch.int64 for m in mats) else mats[0].dtype
+    values, lengths, offsets = ops.kjt_from_dense_raw([m.to(dt) for m in mats], padding_idx)
+    return KeyedJaggedTensor(names, values, lengths=lengths, offsets=offsets, stride=mats[0].shape[0])
+
+
+def build_unpooled_kjt(features: Dict[str, torch.Tensor], feature_order: List[str]) -> KeyedJaggedTensor:
+    """``_build_unpooled_kjt`` (embedding.py:207-232): every id of ``features[name]`` ([B] or [B, L]), each row
+    a bag of L ids (no filter; the sizes are known, so nothing synchronises)."""
+    names, vals, lens = [], [], []
+    for n in feature_order:
+        if n not in features:
+            continue
+        ids = features[n]
+        B = ids.shape[0]
+        flat = ids.reshape(-1)
+        names.append(n)
+        vals.append(flat.to(torch.int64))
+        lens.append(torch.full((B,), flat.shape[0] // max(B, 1), dtype=torch.int32, device=ids.device))
+    if not names:
+        return KeyedJaggedTensor([], torch.empty(0, dtype=torch.long), lengths=torch.empty(0, dtype=torch.int32))
+    return KeyedJaggedTensor(names, torch.cat(vals), lengths=torch.cat(lens))
+
+
+def build_kjt(tensors: Dict[str, torch.Tensor], feature_order: List[str],
+              feature_to_batch_key: Optional[Dict[str, str]] = None) -> KeyedJaggedTensor:
+    """``build_kjt`` (primus_dlrm/data/pipeline_batch.py:70-100): a feature with ``<key>__lengths`` in the
+    batch is jagged (its flat ids and lengths are taken as they are), any other is a dense [B, L] matrix of
+    bags of L ids."""
+    fk = feature_to_batch_key or {}
+    names, vals, lens = [], [], []
+    for feat in feature_order:
+        key = fk.get(feat, feat)
+        if key not in tensors:
+            continue
+        ids = tensors[key]
+        names.append(feat)
+        if key + "__lengths" in tensors:
+            vals.append(ids.reshape(-1).to(torch.int64))
+            lens.append(tensors[key + "__lengths"].to(torch.int32))
+        else:
+            B = ids.shape[0]
+            flat = ids.reshape(-1)
+            vals.append(flat.to(torch.int64))
+            lens.append(torch.full((B,), flat.shape[0] // max(B, 1), dtype=torch.int32, device=ids.device))
+    if not names:
+        return KeyedJaggedTensor([], torch.empty(0, dtype=torch.long), lengths=torch.empty(0, dtype=torch.int32))
+    return KeyedJaggedTensor(names, torch.cat(vals), lengths=torch.cat(lens))

@@ -234,6 +234,67 @@ def tbe_backward_sparse_grad_raw(plan: TbePlan, indices: torch.Tensor, offsets: 
     return row_ids, grad_rows, num_unique
 
 
+# ---------------------------------------------------------------------------
+# KeyedJaggedTensor construction
+# ---------------------------------------------------------------------------
+
+def kjt_from_dense_raw(features: Sequence[torch.Tensor], padding_idx: int = -1):
+    """Dense [B, L_f] id matrices (one dtype, int32 or int64) -> (values, lengths int32 [F*B], offsets int64
+    [F*B+1]) with every id equal to ``padding_idx`` removed (pdm_kjt_from_dense).  ``values`` has the inputs'
+    total id count as capacity; its first ``offsets[-1]`` entries are the kept ids."""
+    if not features:
+        raise ValueError("need at least one feature")
+    if len(features) > L.PDM_KJT_MAX_FEATURES:
+        raise ValueError(f"at most {L.PDM_KJT_MAX_FEATURES} features")
+    dev = _require_cuda(*features)
+    dt = features[0].dtype
+    if dt not in (torch.int32, torch.int64):
+        raise TypeError("ids must be int32 or int64")
+    B = features[0].shape[0]
+    feats = []
+    for t in features:
+        if t.dtype != dt or t.dim() != 2 or t.shape[0] != B:
+            raise ValueError("features must be [B, L_f] tensors of one dtype and one B")
+        feats.append(t.contiguous())
+    F = len(feats)
+    cap = sum(t.numel() for t in feats)
+    values = torch.empty(max(cap, 1), dtype=dt, device=dev)
+    lengths = torch.empty(F * B, dtype=torch.int32, device=dev)
+    offsets = torch.empty(F * B + 1, dtype=torch.int64, device=dev)
+    ws = torch.empty(int(L.lib().pdm_kjt_workspace_size(F * B)), dtype=torch.uint8, device=dev)
+    ids_arr = (ctypes.c_void_p * F)(*[t.data_ptr() if t.numel() else None for t in feats])
+    len_arr = (ctypes.c_int32 * F)(*[t.shape[1] for t in feats])
+    L.check(L.lib().pdm_kjt_from_dense(ids_arr, len_arr, F, B, 32 if dt == torch.int32 else 64, int(padding_idx),
+                                       values.data_ptr(), lengths.data_ptr(), offsets.data_ptr(), ws.data_ptr(),
+                                       ws.numel(), L.stream_ptr(dev)), "pdm_kjt_from_dense")
+    return values[:cap], lengths, offsets
+
+
+def kjt_permute_raw(values: torch.Tensor, offsets: torch.Tensor, num_keys: int, batch_size: int,
+                    perm: Sequence[int]):
+    """Key permutation of a KJT on the device (pdm_kjt_permute): output key k is input key perm[k].
+    Returns (values with the input's capacity, lengths int32, offsets int64)."""
+    dev = _require_cuda(values, offsets)
+    if values.dtype not in (torch.int32, torch.int64):
+        raise TypeError("values must be int32 or int64")
+    if offsets.dtype != torch.int64 or offsets.numel() != num_keys * batch_size + 1 or not offsets.is_contiguous():
+        raise ValueError("offsets must be contiguous int64 [num_keys * B + 1]")
+    if len(perm) > L.PDM_KJT_MAX_FEATURES:
+        raise ValueError(f"at most {L.PDM_KJT_MAX_FEATURES} output keys")
+    values = values.contiguous()
+    K = len(perm)
+    out_v = torch.empty(max(values.numel(), 1), dtype=values.dtype, device=dev)
+    out_l = torch.empty(K * batch_size, dtype=torch.int32, device=dev)
+    out_o = torch.empty(K * batch_size + 1, dtype=torch.int64, device=dev)
+    ws = torch.empty(int(L.lib().pdm_kjt_workspace_size(K * batch_size)), dtype=torch.uint8, device=dev)
+    perm_arr = (ctypes.c_int32 * max(K, 1))(*[int(p) for p in perm])
+    L.check(L.lib().pdm_kjt_permute(values.data_ptr() if values.numel() else None,
+                                    32 if values.dtype == torch.int32 else 64, offsets.data_ptr(), num_keys,
+                                    batch_size, perm_arr, K, out_v.data_ptr(), out_l.data_ptr(), out_o.data_ptr(),
+                                    ws.data_ptr(), ws.numel(), L.stream_ptr(dev)), "pdm_kjt_permute")
+    return out_v[:values.numel()], out_l, out_o
+
+
 _DTYPE_CODES = {0: torch.float32, 1: torch.float16, 2: torch.bfloat16}
 
 
