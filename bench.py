@@ -15,6 +15,8 @@ fp32 out).  ``--workload`` selects another:
   train_rowwise_adagrad  the same with fused row-wise Adagrad (L2 weight decay 1e-5)
   train_seq_adam  S-token gather backward + fused Adam over the seq_gather workload's tables in fp32
               (item 10M x 256, artist 1M x 64, album 2M x 64; B=1024, 768 slots, row-0 padding)
+  kjt_build   device KJT build: 26 features x 65,536 rows x 20 int64 ids, 30 % padding id 0 filtered
+              (lengths, offsets, compacted values; no host sync)
   copy_1gib   calibration only: a 1 GiB device-to-device copy (the HBM counters' reference kernel)
 
 A step is one forward of the path over one batch already resident in HBM.
@@ -439,7 +441,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="single_hot",
                     choices=["single_hot", "ebc_fp32", "int8_mean", "seq_gather", "onetrans", "cross_hash",
-                             "train_adam", "train_rowwise_adagrad", "train_seq_adam", "copy_1gib"])
+                             "train_adam", "train_rowwise_adagrad", "train_seq_adam", "kjt_build", "copy_1gib"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
 
@@ -548,6 +550,33 @@ def main() -> int:
                     "sample": f"C oracle (one thread, slot placement in numpy): gather backward + Adam over the "
                               f"first {cpu_b} samples ({n} slots x 3 features) on tables capped at {cpu_cap} rows "
                               f"(ids modulo), median of 5 reps = {sec:.3f} s"}
+    elif args.workload == "kjt_build":
+        # the pooled-history KJT of _build_pooled_kjt (embedding.py:177-204) at the single-hot batch
+        F_, B_, L_ = 26, 65_536, 20
+        rng = np.random.default_rng(1009)
+        mats = []
+        for _ in range(F_):
+            m = rng.integers(1, 1 << 40, (B_, L_), dtype=np.int64)
+            m[rng.random((B_, L_)) < 0.3] = 0
+            mats.append(m)
+        feats = [torch.from_numpy(m).to(dev) for m in mats]
+        kept = int(sum(int((m != 0).sum()) for m in mats))
+        keep = feats
+
+        def step():
+            pdm.ops.kjt_from_dense_raw(feats, 0)
+
+        rows = F_ * B_
+        alg = F_ * B_ * L_ * 8 + kept * 8 + rows * 4 + (rows + 1) * 8
+        units, unit, bound, dtype = F_ * B_ * L_, "ids/s", "hbm", "int64"
+        cfg = {"workload": "kjt_build_26x65536x20_pad30", "features": F_, "batch": B_, "ids_per_row": L_,
+               "kept": kept, "padding_idx": 0}
+
+        def cpu_fn():
+            sec = time_cpu(lambda: orc.kjt_from_dense(mats, 0))
+            return {"value": round(units / sec, 1), "unit": unit, "cores": 1, "kind": "port",
+                    "sample": f"numpy oracle (boolean mask per feature, one thread), all {units} ids, median of 5 "
+                              f"reps = {sec:.3f} s"}
     elif args.workload == "copy_1gib":
         # calibration: a plain device copy of 1 GiB (reads 1 GiB, writes 1 GiB) for the HBM counters
         src = torch.ones(1 << 28, dtype=torch.float32, device=dev)

@@ -36,6 +36,7 @@ struct KjtDenseArgs {
   int32_t len[PDM_KJT_MAX_FEATURES];       // ids per row of each feature
   int32_t F;
   int32_t index_bits;
+  int32_t Lmax;  // longest row of any feature
   int64_t B;
   int64_t rows;  // F * B
   int64_t padding_idx;
@@ -48,50 +49,107 @@ __device__ __forceinline__ int64_t load_id(const void* p, int64_t i, int bits) {
   return bits == 32 ? (int64_t) reinterpret_cast<const int32_t*>(p)[i] : reinterpret_cast<const int64_t*>(p)[i];
 }
 
+// Kept ids staged per wavefront before the contiguous write (int64 slots).
+constexpr int kStageIds = 1024;
+
 // Groups of G lanes per (feature, row); COMPACT = false counts, true writes.
-template <int G, bool COMPACT>
+// The rows of a wavefront are consecutive, so their kept ids form one
+// contiguous output range: with STAGE the ids are placed in LDS first and the
+// range is written with coalesced stores.
+// V ids per lane per round (V = 2: one 16-byte int64 / 8-byte int32 load; every row length even).
+template <int G, bool COMPACT, bool STAGE, int V>
 __global__ __launch_bounds__(256) void kjt_dense_kernel(KjtDenseArgs a) {
   constexpr int RPW = 64 / G;  // rows per wavefront
+  __shared__ int64_t stage[STAGE ? 4 * kStageIds : 1];
   const int lane = threadIdx.x & 63, gl = lane & (G - 1), grp = lane / G;
   const int64_t row = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW + grp;
   const bool live = row < a.rows;
-  int f = 0;
-  if (live)
-    while (f + 1 < a.F && row >= a.row0[f + 1]) ++f;
-  const int64_t b = live ? row - a.row0[f] : 0;
+  const int f = live ? (int)(row / a.B) : 0;  // rows are feature-major: row = f * B + b
+  const int64_t b = live ? row - (int64_t)f * a.B : 0;
   const int L = live ? a.len[f] : 0;
   const bool has_pad = a.padding_idx >= 0;
   const uint64_t gmask = G == 64 ? ~uint64_t(0) : ((uint64_t(1) << G) - 1) << (grp * G);
   const uint64_t lt = (uint64_t(1) << lane) - 1;
   int64_t out = 0;
+  int64_t wbase = 0;  // output position of the wavefront's first row
   if constexpr (COMPACT) {
     if (live) out = a.offsets[row];
+    if constexpr (STAGE) wbase = __shfl(out, 0);
   }
+  int64_t* wst = STAGE ? stage + (threadIdx.x >> 6) * kStageIds : nullptr;
   int count = 0;
-  // every lane runs the same number of rounds (the longest row of the wavefront is not known, so rounds
-  // cover the longest feature); lanes past their row's end hold no id
-  int Lmax = 0;
-  for (int i = 0; i < a.F; ++i) Lmax = max(Lmax, a.len[i]);
-  for (int c = 0; c < Lmax; c += G) {
-    const int k = c + gl;
-    bool keep = false;
-    int64_t v = 0;
-    if (live && k < L) {
-      v = load_id(a.ids[f], b * L + k, a.index_bits);
-      keep = !(has_pad && v == a.padding_idx);
+  // every lane runs the same number of rounds (covering the longest feature), so the ballots see the whole
+  // wavefront; lanes past their row's end hold no id
+  for (int c = 0; c < a.Lmax; c += G * V) {
+    const int k = c + gl * V;  // this lane's first id of the round (V consecutive ids)
+    bool keep[V];
+    int64_t v[V];
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+      keep[j] = false;
+      v[j] = 0;
     }
-    const uint64_t m = __ballot(keep) & gmask;
+    if (live && k < L) {  // L is a multiple of V, so all V ids of the lane are in the row
+      if constexpr (V == 2) {
+        if (a.index_bits == 32) {
+          const int2 p = reinterpret_cast<const int2*>(a.ids[f])[(b * L + k) >> 1];
+          v[0] = p.x;
+          v[1] = p.y;
+        } else {
+          const longlong2 p = reinterpret_cast<const longlong2*>(a.ids[f])[(b * L + k) >> 1];
+          v[0] = p.x;
+          v[1] = p.y;
+        }
+      } else {
+        v[0] = load_id(a.ids[f], b * L + k, a.index_bits);
+      }
+#pragma unroll
+      for (int j = 0; j < V; ++j) keep[j] = !(has_pad && v[j] == a.padding_idx);
+    }
+    uint64_t m[V];
+    int before = 0;  // kept ids of this round in earlier lanes of the row
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+      m[j] = __ballot(keep[j]) & gmask;
+      before += __popcll(m[j] & lt);
+    }
     if constexpr (COMPACT) {
-      if (keep) {
-        const int64_t at = out + count + __popcll(m & lt);
-        if (a.index_bits == 32) reinterpret_cast<int32_t*>(a.values)[at] = (int32_t)v;
-        else reinterpret_cast<int64_t*>(a.values)[at] = v;
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        if (keep[j]) {
+          const int64_t at = out + count + before;
+          if constexpr (STAGE) {
+            wst[at - wbase] = v[j];
+          } else {
+            if (a.index_bits == 32) reinterpret_cast<int32_t*>(a.values)[at] = (int32_t)v[j];
+            else reinterpret_cast<int64_t*>(a.values)[at] = v[j];
+          }
+          ++before;
+        }
       }
     }
-    count += __popcll(m);
+#pragma unroll
+    for (int j = 0; j < V; ++j) count += __popcll(m[j]);
   }
   if constexpr (!COMPACT) {
     if (live && gl == 0) a.lengths[row] = count;
+  }
+  if constexpr (COMPACT && STAGE) {
+    const int64_t r0 = row - grp;  // the wavefront's first row
+    if (r0 < a.rows) {             // uniform across the wavefront
+      // the range ends where the wavefront's last live row ends
+      const int g_last = (int)min<int64_t>(RPW - 1, a.rows - 1 - r0);
+      const int64_t wend = __shfl(out + count, g_last * G);
+      __builtin_amdgcn_wave_barrier();
+      const int64_t n = wend - wbase;
+      if (a.index_bits == 32) {
+        int32_t* dst = reinterpret_cast<int32_t*>(a.values) + wbase;
+        for (int64_t i = lane; i < n; i += 64) dst[i] = (int32_t)wst[i];
+      } else {
+        int64_t* dst = reinterpret_cast<int64_t*>(a.values) + wbase;
+        for (int64_t i = lane; i < n; i += 64) dst[i] = wst[i];
+      }
+    }
   }
 }
 
@@ -276,18 +334,53 @@ extern "C" int pdm_kjt_from_dense(const void* const* ids, const int32_t* row_len
   a.row0[num_features] = rows;
   a.F = num_features;
   a.index_bits = index_bits;
+  a.Lmax = Lmax;
   a.B = batch_size;
   a.rows = rows;
   a.padding_idx = padding_idx;
   a.lengths = lengths;
   a.offsets = offsets;
   a.values = values;
+  // two ids per lane (one wide load) when every row length is even and the id arrays are aligned for it
+  bool even = true;
+  for (int f = 0; f < num_features; ++f)
+    even = even && row_len[f] % 2 == 0 && ((uintptr_t)ids[f] % (index_bits / 4)) == 0;
+  const int V = even && Lmax >= 2 ? 2 : 1;
+  const int Lv = (Lmax + V - 1) / V;  // lane slots per row
+  // lanes per row: the power of two that wastes the fewest lanes over ceil(Lv / G) rounds (ties: fewer rounds)
   int G = 1;
-  while (G < Lmax && G < 64) G <<= 1;
+  while (G < Lv && G < 4) G <<= 1;
+  if (Lv > 4) {
+    double best = -1.0;
+    for (int g = 4; g <= 64; g <<= 1) {
+      const int rounds = (Lv + g - 1) / g;
+      const double use = (double)Lv / (double)(rounds * g);
+      if (use > best + 1e-9) {
+        best = use;
+        G = g;
+      } else if (use > best - 1e-9) {
+        G = g;
+      }
+    }
+  }
   const int64_t rpb = 4 * (64 / G);
   const int64_t blocks = (rows + rpb - 1) / rpb;
   PDM_CHECK_ARG(blocks < (int64_t(1) << 31), "too many rows");
-#define PDM_KJT_LAUNCH(G_, C_) hipLaunchKernelGGL((kjt_dense_kernel<G_, C_>), dim3((unsigned)blocks), dim3(256), 0, s, a)
+  const bool stage = (int64_t)(64 / G) * Lmax <= kStageIds;
+#define PDM_KJT_LAUNCH(G_, C_)                                                                                  \
+  do {                                                                                                          \
+    if (V == 2) {                                                                                               \
+      if (C_ && stage)                                                                                          \
+        hipLaunchKernelGGL((kjt_dense_kernel<G_, C_, true, 2>), dim3((unsigned)blocks), dim3(256), 0, s, a);  \
+      else                                                                                                      \
+        hipLaunchKernelGGL((kjt_dense_kernel<G_, C_, false, 2>), dim3((unsigned)blocks), dim3(256), 0, s, a); \
+    } else {                                                                                                    \
+      if (C_ && stage)                                                                                          \
+        hipLaunchKernelGGL((kjt_dense_kernel<G_, C_, true, 1>), dim3((unsigned)blocks), dim3(256), 0, s, a);  \
+      else                                                                                                      \
+        hipLaunchKernelGGL((kjt_dense_kernel<G_, C_, false, 1>), dim3((unsigned)blocks), dim3(256), 0, s, a); \
+    }                                                                                                           \
+  } while (0)
 #define PDM_KJT_BY_G(C_)                 \
   switch (G) {                           \
     case 1: PDM_KJT_LAUNCH(1, C_); break;   \

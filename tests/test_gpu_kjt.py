@@ -11,7 +11,7 @@ pytestmark = pytest.mark.gpu
 
 @pytest.mark.parametrize("dtype", [np.int32, np.int64])
 @pytest.mark.parametrize("pad", [0, -1, 3])
-@pytest.mark.parametrize("lens", [(1,), (5, 20, 1), (64,), (100, 7, 300), (0, 4)])
+@pytest.mark.parametrize("lens", [(1,), (5, 20, 1), (64,), (100, 7, 300), (0, 4), (20, 2, 40), (2,)])
 def test_kjt_from_dense(pdm, dev, dtype, pad, lens):
     g = np.random.default_rng(sum(lens) + pad)
     B = 257
