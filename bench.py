@@ -8,6 +8,8 @@ fp32 out).  ``--workload`` selects another:
   single_hot  (default, above)
   int8_mean   64 tables x 5,000,000 x 128 int8 rowwise, mean, Poisson(20) bags, B=16,384, fp16 out
   seq_gather  3 behaviour pools, item 10M x 256 + artist 1M x 64 + album 2M x 64 bf16, B=1024
+  seq_tokenize  the seq_gather workload fused with one SequentialTokenizer per pool (Linear 384 -> 256,
+              GELU, Linear 256 -> 256, + pos_emb of 2048 x 256 fp32), fp32 S-tokens [1024, 768, 256]
   onetrans    4-layer OneTrans block stack, B=1024, 384 S + 16 NS tokens, d 256, schedule 384/256/128/64
   cross_hash  cross-feature ids: xxHash64 of (uid, artist_id) int64 pairs % 100,000,000, 16,777,216 rows
   train_adam  pooled backward + fused Adam (lr 1e-2, eps 1e-8, wd 1e-5): 8 tables x 10,000,000 x 64 fp32,
@@ -382,6 +384,56 @@ def cpu_seq(orc, w, row_cap: int):
 
 
 # ----------------------------------------------------------------------------------------------
+# S-token gather fused with the sequential tokenizers
+# ----------------------------------------------------------------------------------------------
+
+TOK_D, TOK_POS_ROWS = 256, 2048
+
+
+def setup_tokenize(pdm, torch, dev, w):
+    _, _, kept, (tables, ids, offs) = setup_seq(pdm, torch, dev, w)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(1010)
+    K, d = sum(w.table_dims), TOK_D
+    bf = lambda *shape: (torch.randn(*shape, device=dev, generator=gen) * 0.05).to(torch.bfloat16)  # noqa: E731
+    weights = [dict(w1=bf(d, K), b1=bf(d), w2=bf(d, d), b2=bf(d),
+                    pos=torch.randn(TOK_POS_ROWS, d, device=dev, generator=gen)) for _ in w.max_len]
+    S = sum(w.max_len)
+    out = torch.empty(w.batch, S, d, device=dev)
+    work = pdm.ops.seq_tokenize_workspace(tables, ids, offs, w.max_len, d)
+
+    def step():
+        pdm.ops.seq_tokenize_raw(tables, ids, offs, w.max_len, weights, out=out, workspace=work)
+
+    # HBM bytes a perfect kernel moves: kept events' rows and ids, offsets, the fp32 S-tokens and mask written,
+    # the tokenizer weights and the used position rows read once
+    row_bytes = K * 2
+    alg_bytes = kept * row_bytes + kept * 3 * 8 + sum(o.size * 8 for o in w.offsets) + \
+        w.batch * S * (d * 4 + 1) + len(w.max_len) * ((K * d + d * d + 2 * d) * 2 + max(w.max_len) * d * 4)
+    # MFMA work: the MLP of every kept event plus one padding row per pool
+    flops = 2.0 * (K * d + d * d) * (kept + len(w.max_len))
+    return step, alg_bytes, flops, kept, (tables, ids, offs, weights, out, work)
+
+
+def cpu_tokenize(w, threads: int, batch: int, row_cap: int):
+    """The oracle (C gather + PyTorch-CPU tokenizer in autocast emulation) on the first ``batch`` samples."""
+    import torch
+    from oracle import onetrans as ot
+
+    torch.set_num_threads(threads)
+    g = np.random.default_rng(6)
+    # random bf16 bits with bit 14 clear: finite values of magnitude below 2
+    tabs = [g.integers(0, 1 << 16, (min(r, row_cap), dm), dtype=np.uint16) & 0xBFFF
+            for r, dm in zip(w.table_rows, w.table_dims)]
+    offs = [o[:batch + 1] for o in w.offsets]
+    ids = [[a[:int(o[batch])] % min(r, row_cap) for a, r in zip(row, w.table_rows)] for row, o in zip(w.ids, offs)]
+    K = sum(w.table_dims)
+    ws = [ot.random_tokenizer_weights(K, TOK_D, max(w.max_len), seed=p) for p in range(len(w.max_len))]
+    sec = time_cpu(lambda: ot.seq_tokenize(tabs, ids, offs, w.max_len, ws), reps=3)
+    return sec
+
+
+# ----------------------------------------------------------------------------------------------
 # OneTrans block stack
 # ----------------------------------------------------------------------------------------------
 
@@ -440,7 +492,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="single_hot",
-                    choices=["single_hot", "ebc_fp32", "int8_mean", "seq_gather", "onetrans", "cross_hash",
+                    choices=["single_hot", "ebc_fp32", "int8_mean", "seq_gather", "seq_tokenize", "onetrans",
+                             "cross_hash",
                              "train_adam", "train_rowwise_adagrad", "train_seq_adam", "kjt_build", "copy_1gib"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
@@ -494,6 +547,24 @@ def main() -> int:
             return {"value": round(kept / sec, 1), "unit": unit, "cores": 1, "kind": "port",
                     "sample": f"C oracle (one thread), full batch of {kept} kept events, item table capped at "
                               f"1,000,000 rows (ids taken modulo), median of 5 reps = {sec:.3f} s"}
+    elif args.workload == "seq_tokenize":
+        w = syn.seq_gather()
+        step, alg, flops, kept, keep = setup_tokenize(pdm, torch, dev, w)
+        S = sum(w.max_len)
+        units, unit, bound, dtype = w.batch * S, "slots/s", "hbm", "bf16->f32"
+        cfg = {"workload": w.name + "_tokenize", "batch": w.batch, "pools": len(w.max_len), "max_len": w.max_len,
+               "tables": {"rows": w.table_rows, "dims": w.table_dims}, "events_kept": kept,
+               "tokenizer": {"raw_dim": sum(w.table_dims), "d_model": TOK_D, "pos_rows": TOK_POS_ROWS},
+               "out": [w.batch, S, TOK_D], "mlp_gflop_per_step": round(flops / 1e9, 2),
+               "timed": "whole fused call (list build, MLP over kept events, padding fill)"}
+        cpu_b, cpu_cap = 256, 250_000
+
+        def cpu_fn():
+            sec = cpu_tokenize(w, threads, cpu_b, cpu_cap)
+            return {"value": round(cpu_b * S / sec, 1), "unit": unit, "cores": threads, "kind": "port",
+                    "sample": f"oracle (C gather + PyTorch-CPU tokenizers, autocast emulation) on the first {cpu_b} "
+                              f"samples ({cpu_b * S} slots), tables capped at {cpu_cap} rows (ids modulo), "
+                              f"median of 3 reps = {sec:.3f} s"}
     elif args.workload == "cross_hash":
         # user_x_artist cross ids (config.py:151): one (uid, artist_id) pair per row, 100M buckets, salt 0
         n_rows, table_size = 1 << 24, 100_000_000

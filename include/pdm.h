@@ -282,6 +282,52 @@ int pdm_seq_gather_backward_fused(pdm_tbe_plan plan, const pdm_seq_desc* desc,
                                   int64_t workspace_bytes, int32_t* err_flag,
                                   pdm_stream_t stream);
 
+/* S-token gather fused with the per-pool SequentialTokenizer
+ * (primus_dlrm/models/onetrans.py:238-257, one per sequence group at
+ * :326-332,553-558) under autocast(bf16): for slot l of pool p of sample b,
+ *   raw = concat_f table_f[id_f]         (the gather's placement and padding,
+ *                                         as pdm_seq_gather_fwd; bf16, fp32
+ *                                         tables rounded to bf16 on load)
+ *   h   = bf16(gelu(bf16(raw . W1_p^T + b1_p)))          (exact-erf GELU)
+ *   out[b, s0_p + l, :] = float(bf16(h . W2_p^T + b2_p)) + pos_p[l]   (fp32)
+ * so the [B, S, sum dim] raw rows never reach memory.  The padding slots of a
+ * pool share one raw row, whose MLP runs once.
+ * desc:    the gather (dtype PDM_BF16 or PDM_F32; every dim a multiple of 8,
+ *          sum of dims = raw_dim in {128, 192, 256, 384}; ROW0 padding needs
+ *          rows >= 1)
+ * weights: [P]; w1 [d_model, raw_dim], w2 [d_model, d_model], b1, b2
+ *          [d_model] bf16 (autocast's casts of the fp32 parameters); pos fp32
+ *          [pos_rows >= max_len[p], d_model] or NULL (use_pos_embed = False);
+ *          16-byte aligned.  Unused (may be NULL) for pools with max_len 0.
+ * out:     fp32, 16-byte aligned; token (b, s) at
+ *          out + b * out_sample_stride + s * d_model (e.g. the first S rows of
+ *          the block's [B, S + n_ns, d_model] input)
+ * d_model: 128 or 256.  mask / err_flag as pdm_seq_gather_fwd (mask
+ *          optional).  B * S < 2^31.
+ * workspace: 256-byte aligned, >= pdm_seq_tokenize_workspace_size(desc,
+ *          d_model) bytes; no initialisation needed; calls sharing one
+ *          workspace must not overlap. */
+typedef struct {
+  const uint16_t* w1;
+  const uint16_t* b1;
+  const uint16_t* w2;
+  const uint16_t* b2;
+  const float* pos;
+  int64_t pos_rows;
+} pdm_tokenizer_weights;
+
+int64_t pdm_seq_tokenize_workspace_size(const pdm_seq_desc* desc,
+                                        int32_t d_model);
+
+int pdm_seq_tokenize_fwd(const pdm_seq_desc* desc, const void* const* tables,
+                         const int64_t* const* ids,
+                         const int64_t* const* offsets,
+                         const pdm_tokenizer_weights* weights,
+                         int32_t d_model, float* out,
+                         int64_t out_sample_stride, uint8_t* mask,
+                         void* workspace, int64_t workspace_bytes,
+                         int32_t* err_flag, pdm_stream_t stream);
+
 /* ------------------------------------------------------------------------
  * OneTrans mixed-parameter interaction block forward (bf16 MFMA).
  *

@@ -9,6 +9,11 @@ Restates primus_dlrm/models/onetrans.py in PyTorch on the CPU:
 * ``rmsnorm``            onetrans.py:74-82  (fp32, eps 1e-6, ``(x * rms) * w``)
 * ``block_forward``      OneTransBlock.forward onetrans.py:220-231 with
                          MixedAttention.forward :124-169 and MixedFFN.forward :195-204
+* ``sequential_tokenizer`` SequentialTokenizer.forward onetrans.py:250-257 (Linear, exact GELU,
+                         Linear, + pos_emb(arange(L)))
+* ``seq_tokenize``       the S-token construction of OneTransModel._backbone onetrans.py:553-558:
+                         per-pool gather (onetrans.py:515-520, the sequence gather of oracle.py),
+                         tokenizer, concatenation along the sequence
 
 ``mode="autocast"`` reproduces the rounding points the reference has under
 ``torch.autocast(bf16)`` (primus_dlrm/training/dist_trainer.py:471) with an
@@ -17,7 +22,10 @@ accumulates in fp32 and rounds its output to bf16; attention takes bf16
 q/k/v, runs the softmax in fp32 and rounds its output to bf16; GELU (exact
 erf) runs in fp32 on the bf16 GEMM output and rounds to bf16; RMSNorm and the
 residual additions stay fp32.  ``mode="fp64"`` runs the same graph in float64
-without any rounding (ground truth).
+without any rounding (ground truth).  A Linear with a bias rounds once, after
+the bias: bf16(x . W^T + b) with the bias taken as bf16 (the fused GEMM
+epilogue of autocast's ``addmm``).  The tokenizer's sum ``tokens + pos_emb``
+adds the bf16 tokens to the fp32 position table in fp32 (type promotion).
 
 Weights use the reference's parameter names (onetrans.py:111-113,180-184,214-218):
 norm1, s_qkv [3D, D], ns_qkv [NS, 3D, D], out [D, D], norm2, s_w1 [F, D],
@@ -164,3 +172,54 @@ def block_flops(B: int, kv: int, q_len: int, D: int, F: int, n_ns: int) -> float
     f += 2 * q_len * D * D
     f += 4 * q_len * D * F
     return float(f) * B
+
+
+def _lin_bias(x: torch.Tensor, w: torch.Tensor, b: torch.Tensor, num: _Num) -> torch.Tensor:
+    """autocast ``F.linear(x, w, b)``: bf16 operands, fp32 accumulation, one rounding after the bias."""
+    acc = torch.matmul(num.round(x), num.round(w.to(num.dt)).transpose(-1, -2)) + num.round(b.to(num.dt))
+    return num.round(acc)
+
+
+def sequential_tokenizer(raw: torch.Tensor, w: Dict[str, torch.Tensor], mode: str = "autocast") -> torch.Tensor:
+    """SequentialTokenizer.forward (onetrans.py:250-257) for raw [B, L, K]:
+    proj = Linear(K, d) -> GELU (exact erf) -> Linear(d, d) (:243-247), then
+    ``+ pos_emb(arange(L))`` when ``w["pos"]`` is not None (:254-256).  Weights
+    use the module's parameter names: ``w1`` / ``b1`` = proj.0, ``w2`` / ``b2`` =
+    proj.2, ``pos`` = pos_emb.weight [max_len, d] (fp32)."""
+    num = _Num(mode)
+    u = _lin_bias(raw.to(num.dt), w["w1"], w["b1"], num)
+    h = num.round(torch.nn.functional.gelu(u))
+    y = _lin_bias(h, w["w2"], w["b2"], num)
+    if w.get("pos") is not None:
+        L = raw.shape[1]
+        y = y + w["pos"][:L].to(num.dt)
+    return y
+
+
+def seq_tokenize(tables, ids, offsets, max_len: List[int], weights: List[Dict[str, torch.Tensor]],
+                 pad_mode: int = 0, align: int = 0, mode: str = "autocast"):
+    """S-tokens of OneTransModel._backbone (onetrans.py:553-558): the padded
+    per-pool gather (``oracle.seq_gather``: tables as uint16 bf16 bits or
+    float32), one SequentialTokenizer per pool, pools concatenated along the
+    sequence.  Returns (tokens [B, S, d] float32 (float64 in fp64 mode), mask)."""
+    from . import oracle as orc
+    import numpy as np
+
+    raw, mask = orc.seq_gather(tables, ids, offsets, max_len, pad_mode=pad_mode, align=align)
+    if raw.dtype == np.uint16:
+        raw = (raw.astype(np.uint32) << 16).view(np.float32)
+    raw = torch.from_numpy(np.ascontiguousarray(raw))
+    parts, s0 = [], 0
+    for p, L in enumerate(max_len):
+        parts.append(sequential_tokenizer(raw[:, s0:s0 + L], weights[p], mode))
+        s0 += L
+    return torch.cat(parts, dim=1), mask
+
+
+def random_tokenizer_weights(K: int, d: int, max_len: int, std: float = 0.05, seed: int = 0,
+                             pos: bool = True) -> Dict[str, torch.Tensor]:
+    """bf16-representable N(0, std) Linear weights and biases (fp32 storage), N(0, 1) fp32 positions."""
+    g = torch.Generator().manual_seed(seed)
+    r = lambda *shape: _bf16(torch.randn(*shape, generator=g) * std)  # noqa: E731
+    return {"w1": r(d, K), "b1": r(d), "w2": r(d, d), "b2": r(d),
+            "pos": torch.randn(max_len, d, generator=g) if pos else None}

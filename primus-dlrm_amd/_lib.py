@@ -50,6 +50,8 @@ EXPORTED_SYMBOLS = (
     "pdm_kjt_from_dense",
     "pdm_kjt_permute",
     "pdm_seq_gather_fwd",
+    "pdm_seq_tokenize_workspace_size",
+    "pdm_seq_tokenize_fwd",
     "pdm_cross_hash_fwd",
     "pdm_onetrans_block_workspace_size",
     "pdm_onetrans_block_fwd",
@@ -107,6 +109,18 @@ class SeqDesc(ctypes.Structure):
     ]
 
 
+class TokenizerWeights(ctypes.Structure):
+    """pdm_tokenizer_weights: one pool's SequentialTokenizer (bf16 Linear weights / biases, fp32 positions)."""
+    _fields_ = [
+        ("w1", ctypes.c_void_p),
+        ("b1", ctypes.c_void_p),
+        ("w2", ctypes.c_void_p),
+        ("b2", ctypes.c_void_p),
+        ("pos", ctypes.c_void_p),
+        ("pos_rows", ctypes.c_int64),
+    ]
+
+
 class BlockDesc(ctypes.Structure):
     _fields_ = [
         ("batch", ctypes.c_int32),
@@ -157,6 +171,12 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.pdm_seq_gather_fwd.restype = ctypes.c_int
     lib.pdm_seq_gather_fwd.argtypes = [ctypes.POINTER(SeqDesc), ctypes.POINTER(vp), ctypes.POINTER(vp),
                                        ctypes.POINTER(vp), vp, vp, vp, vp]
+    lib.pdm_seq_tokenize_workspace_size.restype = i64
+    lib.pdm_seq_tokenize_workspace_size.argtypes = [ctypes.POINTER(SeqDesc), i32]
+    lib.pdm_seq_tokenize_fwd.restype = ctypes.c_int
+    lib.pdm_seq_tokenize_fwd.argtypes = [ctypes.POINTER(SeqDesc), ctypes.POINTER(vp), ctypes.POINTER(vp),
+                                         ctypes.POINTER(vp), ctypes.POINTER(TokenizerWeights), i32, vp, i64, vp, vp,
+                                         i64, vp, vp]
     lib.pdm_onetrans_block_workspace_size.restype = i64
     lib.pdm_onetrans_block_workspace_size.argtypes = [ctypes.POINTER(BlockDesc)]
     lib.pdm_onetrans_block_fwd.restype = ctypes.c_int

@@ -34,46 +34,9 @@
 #include <mutex>
 
 #include "pdm_common.h"
+#include "mfma_common.h"
 
 namespace pdm {
-
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef float f32x16_t __attribute__((ext_vector_type(16)));
-typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
-typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
-typedef float f32x4_t __attribute__((ext_vector_type(4)));
-typedef float f32x2_t __attribute__((ext_vector_type(2)));
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-
-__device__ __forceinline__ f32x16_t mfma32x32x16(u32x4_t a, u32x4_t b, f32x16_t c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
-                                                 c, 0, 0, 0);
-}
-
-// Pins the instruction order of a fully unrolled loop of N MFMAs, each fed by
-// one LDS read: the first LEAD reads are issued up front, then one MFMA and
-// the next read alternate, so every read has LEAD MFMAs of latency slack.
-template <int N, int LEAD>
-__device__ __forceinline__ void sched_mfma_ds_pipeline() {
-  __builtin_amdgcn_sched_group_barrier(0x100, LEAD, 0);  // DS reads
-#pragma unroll
-  for (int i = 0; i < N - LEAD; ++i) {
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
-  }
-  __builtin_amdgcn_sched_group_barrier(0x008, LEAD, 0);
-}
-
-// bf16 rounding of the block kernels: the hardware conversion (v_cvt_pk_bf16_f32,
-// round to nearest even), branch free.
-__device__ __forceinline__ uint32_t bf16_bits(float v) { return __builtin_bit_cast(uint16_t, (__bf16)v); }
-
-__device__ __forceinline__ float bf16_round(float v) { return (float)(__bf16)v; }
-
-// two values in one conversion: lo in bits 0..15, hi in bits 16..31
-__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, bf16x2_t));
-}
 
 // ---------------------------------------------------------------------------
 // RMSNorm -> bf16 rows.  One wave per row, D = 64 * VPL.
@@ -127,25 +90,6 @@ __global__ __launch_bounds__(256) void rmsnorm_bf16_kernel(const float* __restri
 // Grouped GEMM  C = A . W^T  over (sample, token) rows.
 // ---------------------------------------------------------------------------
 enum { EPI_BF16 = 0, EPI_QKV = 1, EPI_RESID = 2, EPI_GELU = 3 };
-
-// GELU with the error function, 0.5 x (1 + erf(x / sqrt 2)) (the reference's
-// exact-erf F.gelu), branch free.  erfc(a) for a = |x| / sqrt 2 follows
-// Abramowitz & Stegun, Handbook of Mathematical Functions, formula 7.1.26
-// (|error| <= 1.5e-7): erfc(a) = t (a1 + t (a2 + t (a3 + t (a4 + t a5)))) exp(-a^2),
-// t = 1 / (1 + p a).  With e = erfc(a) / 2, GELU(x) = x - x e for x >= 0 and
-// x e = -|x| e for x < 0, i.e. max(x, 0) - |x| e in both cases, so the
-// negative tail carries no cancellation.  After the bf16 rounding of the result
-// it agrees with the exact-erf GELU except in the far negative tail (x < -3.5,
-// |GELU| < 1e-3), where the two can differ by one bf16 step.
-__device__ __forceinline__ float gelu_erf(float v) {
-  const float ax = fabsf(v);
-  // p / sqrt 2 with p = 0.3275911; coefficients a_i / 2
-  const float t = __builtin_amdgcn_rcpf(__builtin_fmaf(ax, 0.23164189619f, 1.0f));
-  const float poly = t * (0.127414796f + t * (-0.142248368f + t * (0.7107068705f + t * (-0.7265760135f + t * 0.5307027145f))));
-  // exp(-x^2 / 2) = 2^(-x^2 log2(e) / 2)
-  const float e = poly * __builtin_amdgcn_exp2f((v * v) * -0.72134752044448170f);
-  return __builtin_fmaf(-ax, e, fmaxf(v, 0.0f));
-}
 
 constexpr int GBM = 128, GBN = 128, GBK = 64, GPAD = 8;
 
@@ -408,14 +352,6 @@ __device__ __forceinline__ void load_row_fragments(const GemmArgs& a, const int*
 // 2*D + 16, so rows r and r + 1 start 16 bytes apart in the banks: the lanes
 // reading one 16-byte piece of 16 consecutive rows hit distinct banks, and a
 // lane's piece offsets are immediates.
-template <int D>
-constexpr int w_stride() { return 2 * D + 16; }
-
-template <int D>
-__device__ __forceinline__ u32x4_t read_w_frag(const char* lds, int r, int piece) {
-  return *reinterpret_cast<const u32x4_t*>(lds + r * w_stride<D>() + (piece << 4));
-}
-
 template <int D, int RB, int EPI, bool NORM>
 __global__ __launch_bounds__(256, 2) void rowgemm_kernel(GemmArgs a) {
   constexpr int KS = D / 16;

@@ -331,12 +331,9 @@ def int8_rowwise_quantize(src: torch.Tensor, row_bytes: int = 0) -> torch.Tensor
 # Jagged -> padded S-token gather
 # ---------------------------------------------------------------------------
 
-def seq_gather_raw(tables: Sequence[torch.Tensor], ids: Sequence[Sequence[torch.Tensor]],
-                   offsets: Sequence[torch.Tensor], max_len: Sequence[int], pad_mode: int = L.PDM_PAD_ROW0,
-                   align: int = L.PDM_ALIGN_RIGHT, want_mask: bool = True,
-                   err_flag: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
-    """tables[f]: [rows_f, dim_f]; ids[p][f]: int64 [n_p]; offsets[p]: int64 [B+1].
-    Returns out [B, sum(max_len), sum(dim)] and mask uint8 [B, sum(max_len)]."""
+def _seq_desc(tables: Sequence[torch.Tensor], ids: Sequence[Sequence[torch.Tensor]], offsets: Sequence[torch.Tensor],
+              max_len: Sequence[int], pad_mode: int, align: int, err_flag: Optional[torch.Tensor]):
+    """Validates a sequence gather's inputs; returns (desc, device, B, S, table / id / offset pointer arrays)."""
     P, F = len(offsets), len(tables)
     if not (1 <= P <= L.PDM_SEQ_MAX_POOLS and 1 <= F <= L.PDM_SEQ_MAX_FEATURES):
         raise ValueError(f"need 1..{L.PDM_SEQ_MAX_POOLS} pools and 1..{L.PDM_SEQ_MAX_FEATURES} features")
@@ -370,15 +367,90 @@ def seq_gather_raw(tables: Sequence[torch.Tensor], ids: Sequence[Sequence[torch.
             raise ValueError("max_len must be >= 0")
         desc.max_len[p] = int(max_len[p])
     S = sum(int(m) for m in max_len)
-    Dtot = sum(t.shape[1] for t in tables)
-    out = torch.empty((B, S, Dtot), dtype=dtype, device=dev)
-    mask = torch.empty((B, S), dtype=torch.uint8, device=dev) if want_mask else None
     tab_arr = (ctypes.c_void_p * F)(*[t.data_ptr() for t in tables])
     ids_arr = (ctypes.c_void_p * (P * F))(*[t.data_ptr() if t.numel() else None for t in flat_ids])
     off_arr = (ctypes.c_void_p * P)(*[o.data_ptr() for o in offsets])
+    return desc, dev, B, S, tab_arr, ids_arr, off_arr
+
+
+def seq_gather_raw(tables: Sequence[torch.Tensor], ids: Sequence[Sequence[torch.Tensor]],
+                   offsets: Sequence[torch.Tensor], max_len: Sequence[int], pad_mode: int = L.PDM_PAD_ROW0,
+                   align: int = L.PDM_ALIGN_RIGHT, want_mask: bool = True,
+                   err_flag: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
+    """tables[f]: [rows_f, dim_f]; ids[p][f]: int64 [n_p]; offsets[p]: int64 [B+1].
+    Returns out [B, sum(max_len), sum(dim)] and mask uint8 [B, sum(max_len)]."""
+    desc, dev, B, S, tab_arr, ids_arr, off_arr = _seq_desc(tables, ids, offsets, max_len, pad_mode, align, err_flag)
+    Dtot = sum(t.shape[1] for t in tables)
+    out = torch.empty((B, S, Dtot), dtype=tables[0].dtype, device=dev)
+    mask = torch.empty((B, S), dtype=torch.uint8, device=dev) if want_mask else None
     status = L.lib().pdm_seq_gather_fwd(ctypes.byref(desc), tab_arr, ids_arr, off_arr, out.data_ptr(),
                                         _ptr(mask), _ptr(err_flag), L.stream_ptr(dev))
     L.check(status, "pdm_seq_gather_fwd")
+    return out, mask
+
+
+def seq_tokenize_workspace(tables: Sequence[torch.Tensor], ids: Sequence[Sequence[torch.Tensor]],
+                           offsets: Sequence[torch.Tensor], max_len: Sequence[int], d_model: int) -> torch.Tensor:
+    """A workspace for :func:`seq_tokenize_raw` on inputs of these shapes."""
+    desc, dev = _seq_desc(tables, ids, offsets, max_len, L.PDM_PAD_ROW0, L.PDM_ALIGN_RIGHT, None)[:2]
+    need = int(L.lib().pdm_seq_tokenize_workspace_size(ctypes.byref(desc), d_model))
+    if need < 0:
+        raise L.PdmError(L.PDM_ERR_INVALID, "pdm_seq_tokenize_workspace_size", L.last_error())
+    return torch.empty(max(need, 1), dtype=torch.uint8, device=dev)
+
+
+def seq_tokenize_raw(tables: Sequence[torch.Tensor], ids: Sequence[Sequence[torch.Tensor]],
+                     offsets: Sequence[torch.Tensor], max_len: Sequence[int], weights: Sequence[dict],
+                     pad_mode: int = L.PDM_PAD_ROW0, align: int = L.PDM_ALIGN_RIGHT, want_mask: bool = True,
+                     out: Optional[torch.Tensor] = None, workspace: Optional[torch.Tensor] = None,
+                     err_flag: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
+    """The S-token gather fused with one SequentialTokenizer per pool (C ABI ``pdm_seq_tokenize_fwd``).
+
+    tables / ids / offsets / max_len as :func:`seq_gather_raw` (bf16 or fp32 tables).  ``weights[p]`` holds
+    ``w1`` [d, K] / ``b1`` [d] / ``w2`` [d, d] / ``b2`` [d] (bf16) and ``pos`` (fp32 [>= max_len[p], d] or
+    None).  ``out`` may be a float32 view [B, >= S, d] whose rows are contiguous (e.g. the leading S-token
+    rows of the block input); by default a new [B, S, d] tensor.  Returns (out, mask)."""
+    desc, dev, B, S, tab_arr, ids_arr, off_arr = _seq_desc(tables, ids, offsets, max_len, pad_mode, align, err_flag)
+    P = len(offsets)
+    if len(weights) != P:
+        raise ValueError("one tokenizer weight dict per pool")
+    d = None
+    warr = (L.TokenizerWeights * P)()
+    keep = []
+    for p, w in enumerate(weights):
+        if int(max_len[p]) == 0:
+            continue
+        w1, b1, w2, b2, pos = w["w1"], w["b1"], w["w2"], w["b2"], w.get("pos")
+        d = w1.shape[0] if d is None else d
+        for t, shape in ((w1, (d, None)), (b1, (d,)), (w2, (d, d)), (b2, (d,))):
+            if t.dtype != torch.bfloat16 or not t.is_contiguous() or t.device != dev or t.dim() != len(shape) or \
+                    any(e is not None and e != g for e, g in zip(shape, t.shape)):
+                raise ValueError("tokenizer weights must be contiguous bf16 w1 [d, K], b1 [d], w2 [d, d], b2 [d] "
+                                 "on the tables' device")
+        if pos is not None and (pos.dtype != torch.float32 or not pos.is_contiguous() or pos.device != dev or
+                                pos.dim() != 2 or pos.shape[1] != d):
+            raise ValueError("pos must be a contiguous float32 [rows, d] tensor on the tables' device")
+        warr[p] = L.TokenizerWeights(w1.data_ptr(), b1.data_ptr(), w2.data_ptr(), b2.data_ptr(),
+                                     None if pos is None else pos.data_ptr(), 0 if pos is None else pos.shape[0])
+        keep.append(w)
+    if d is None:
+        d = int(out.shape[-1]) if out is not None else 256
+    if out is None:
+        out = torch.empty((B, S, d), dtype=torch.float32, device=dev)
+    elif (out.dtype != torch.float32 or out.device != dev or out.dim() != 3 or out.shape[0] != B or
+          out.shape[1] < S or out.shape[2] != d or out.stride(2) != 1 or out.stride(1) != d):
+        raise ValueError("out must be float32 [B, >= S, d] with contiguous rows on the tables' device")
+    mask = torch.empty((B, S), dtype=torch.uint8, device=dev) if want_mask else None
+    lib = L.lib()
+    need = int(lib.pdm_seq_tokenize_workspace_size(ctypes.byref(desc), d))
+    if need < 0:
+        raise L.PdmError(L.PDM_ERR_INVALID, "pdm_seq_tokenize_workspace_size", L.last_error())
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=dev)
+    status = lib.pdm_seq_tokenize_fwd(ctypes.byref(desc), tab_arr, ids_arr, off_arr, warr, d, out.data_ptr(),
+                                      out.stride(0) if B > 0 else S * d, _ptr(mask), workspace.data_ptr(),
+                                      workspace.numel(), _ptr(err_flag), L.stream_ptr(dev))
+    L.check(status, "pdm_seq_tokenize_fwd")
     return out, mask
 
 

@@ -1,0 +1,198 @@
+"""GPU parity of the fused S-token gather + SequentialTokenizer (pdm_seq_tokenize_fwd) against the oracle
+(``onetrans.seq_tokenize``: the pinned sequence gather, then the autocast tokenizer of
+primus_dlrm/models/onetrans.py:238-257 per pool).
+
+Tolerance (bf16 autocast): the kernel and the oracle sum in different orders, so a value can land on the
+other side of a bf16 rounding boundary, in the output or in a hidden unit (which moves an output by at most
+one ulp of that unit times |w2|).  Every element must satisfy |got - want| <= 2^-7 (|y| + |h| . |w2|^T)
+(y: the token before pos, h: the hidden row), fewer than 2% of them may differ at all, and the relative
+error norm must stay below 2e-2.  The mask is bit-exact, and padding slots at one position are bitwise
+equal across samples (their MLP row is computed once per pool)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import onetrans as ot
+from oracle import oracle as o
+
+pytestmark = pytest.mark.gpu
+
+
+def _inputs(g, B, pools, specs, dtype, bad_id=False):
+    tabs = []
+    for r, d in specs:
+        w = g.normal(0, 0.5, (r, d)).astype(np.float32)
+        tabs.append(o.f32_to_bf16_bits(w).reshape(r, d) if dtype == "bf16" else w)
+    ids, offs = [], []
+    for L, mean in pools:
+        ln = g.poisson(mean, B) if B else np.zeros(0, np.int64)
+        n = int(ln.sum())
+        items = g.integers(0, specs[0][0], n)
+        ids.append([items] + [items % r for r, _ in specs[1:]])
+        offs.append(o.offsets_np(ln))
+    if bad_id:
+        ids[0][-1][len(ids[0][-1]) - 1] = specs[-1][0] + 3
+    return tabs, ids, offs
+
+
+def _dev_tables(tabs, dev):
+    out = []
+    for t in tabs:
+        if t.dtype == np.uint16:
+            out.append(torch.from_numpy(t.view(np.int16)).view(torch.bfloat16).to(dev))
+        else:
+            out.append(torch.from_numpy(t).to(dev))
+    return out
+
+
+def _check(got, tabs, ids, offs, max_len, ws, pad_mode, align, mask=None):
+    want, wmask = ot.seq_tokenize(tabs, ids, offs, max_len, ws, pad_mode=pad_mode, align=align)
+    raw, _ = o.seq_gather(tabs, ids, offs, max_len, pad_mode=pad_mode, align=align)
+    if raw.dtype == np.uint16:
+        raw = (raw.astype(np.uint32) << 16).view(np.float32)
+    raw = torch.from_numpy(np.ascontiguousarray(raw))
+    if mask is not None:
+        assert np.array_equal(mask.cpu().numpy(), wmask)
+    num = ot._Num("autocast")
+    s0 = 0
+    for p, L in enumerate(max_len):
+        if L == 0:
+            continue
+        w = ws[p]
+        h = num.round(torch.nn.functional.gelu(ot._lin_bias(raw[:, s0:s0 + L], w["w1"], w["b1"], num)))
+        y = ot._lin_bias(h, w["w2"], w["b2"], num)
+        mag = y.abs() + h.abs() @ w["w2"].abs().T
+        g_p, w_p = got[:, s0:s0 + L], want[:, s0:s0 + L]
+        diff = (g_p - w_p).abs()
+        assert bool((diff <= 2.0 ** -7 * mag + 1e-6).all()), f"pool {p}: max excess {(diff - 2.0 ** -7 * mag).max()}"
+        assert (diff > 0).float().mean().item() < 0.02
+        rel = ((g_p - w_p).norm() / w_p.norm().clamp_min(1e-30)).item()
+        assert rel < 2e-2, rel
+        # padding slots: one MLP row per pool, so equal bits at equal positions
+        pm = wmask[:, s0:s0 + L] == 0
+        for l in range(L):
+            bs = np.nonzero(pm[:, l])[0]
+            if len(bs) > 1:
+                assert torch.equal(g_p[bs, l], g_p[bs[:1], l].expand(len(bs), -1))
+        s0 += L
+
+
+CASES = [
+    # name, specs [(rows, dim)], pools [(max_len, mean)], d, dtype, pad, align, pos
+    ("k384_d256_bf16", [(3000, 256), (300, 64), (500, 64)], [(48, 30), (16, 12), (32, 20)], 256, "bf16", 0, 0, True),
+    ("k128_d128_fp32", [(400, 64), (90, 64)], [(20, 8), (9, 12)], 128, "fp32", 0, 0, True),
+    ("k192_d256_zero_left", [(700, 128), (60, 64)], [(24, 10), (40, 30)], 256, "bf16", 1, 1, True),
+    ("k256_d128_nopos", [(512, 256)], [(33, 20)], 128, "bf16", 0, 0, False),
+    ("k384_d128_fp32_zero", [(800, 128), (300, 128), (200, 128)], [(12, 6), (20, 25)], 128, "fp32", 1, 0, True),
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
+def test_tokenize_matches_oracle(pdm, dev, case):
+    name, specs, pools, d, dtype, pad_mode, align, use_pos = case
+    g = np.random.default_rng(len(name))
+    B = 37
+    K = sum(dm for _, dm in specs)
+    tabs, ids, offs = _inputs(g, B, pools, specs, dtype)
+    max_len = [L for L, _ in pools]
+    ws = [ot.random_tokenizer_weights(K, d, L + 3, seed=i, pos=use_pos) for i, (L, _) in enumerate(pools)]
+    wd = [{k: (v.to(torch.bfloat16) if k != "pos" else v).contiguous().to(dev) if v is not None else None
+           for k, v in w.items()} for w in ws]
+    err = torch.zeros(1, dtype=torch.int32, device=dev)
+    out, mask = pdm.ops.seq_tokenize_raw(_dev_tables(tabs, dev), [[torch.from_numpy(a).to(dev) for a in r] for r in ids],
+                                         [torch.from_numpy(x).to(dev) for x in offs], max_len, wd,
+                                         pad_mode=pad_mode, align=align, err_flag=err)
+    torch.cuda.synchronize()
+    assert err.item() == 0
+    _check(out.cpu(), tabs, ids, offs, max_len, ws, pad_mode, align, mask)
+
+
+def test_many_passes_and_long_pools(pdm, dev):
+    """~45k real tokens: hundreds of passes over the persistent workgroups, pools longer than a pass."""
+    g = np.random.default_rng(5)
+    specs, pools, d = [(20000, 256), (2000, 64), (3000, 64)], [(200, 150), (64, 40), (128, 80)], 256
+    B = 160
+    tabs, ids, offs = _inputs(g, B, pools, specs, "bf16")
+    max_len = [L for L, _ in pools]
+    ws = [ot.random_tokenizer_weights(384, d, 256, seed=10 + i) for i in range(3)]
+    wd = [{k: (v.to(torch.bfloat16) if k != "pos" else v).contiguous().to(dev) for k, v in w.items()} for w in ws]
+    out, mask = pdm.ops.seq_tokenize_raw(_dev_tables(tabs, dev), [[torch.from_numpy(a).to(dev) for a in r] for r in ids],
+                                         [torch.from_numpy(x).to(dev) for x in offs], max_len, wd)
+    torch.cuda.synchronize()
+    _check(out.cpu(), tabs, ids, offs, max_len, ws, 0, 0, mask)
+
+
+def test_writes_into_block_input_rows(pdm, dev):
+    """out = the leading S rows of a [B, S + n_ns, d] buffer: NS rows untouched; a second call reuses the
+    workspace (no initialisation needed)."""
+    g = np.random.default_rng(9)
+    specs, pools, d, n_ns = [(300, 64), (40, 64)], [(10, 5), (6, 4)], 128, 3
+    B = 11
+    tabs, ids, offs = _inputs(g, B, pools, specs, "bf16")
+    max_len = [10, 6]
+    ws = [ot.random_tokenizer_weights(128, d, 16, seed=i) for i in range(2)]
+    wd = [{k: (v.to(torch.bfloat16) if k != "pos" else v).contiguous().to(dev) for k, v in w.items()} for w in ws]
+    buf = torch.full((B, 16 + n_ns, d), 7.0, device=dev)
+    work = torch.empty(1 << 20, dtype=torch.uint8, device=dev)
+    args = (_dev_tables(tabs, dev), [[torch.from_numpy(a).to(dev) for a in r] for r in ids],
+            [torch.from_numpy(x).to(dev) for x in offs], max_len, wd)
+    out, mask = pdm.ops.seq_tokenize_raw(*args, out=buf, workspace=work)
+    first = buf.clone()
+    pdm.ops.seq_tokenize_raw(*args, out=buf, workspace=work)
+    torch.cuda.synchronize()
+    assert torch.equal(first, buf)
+    assert bool((buf[:, 16:] == 7.0).all())
+    _check(buf[:, :16].cpu(), tabs, ids, offs, max_len, ws, 0, 0, mask)
+
+
+def test_bad_ids_and_offsets_raise_the_flag(pdm, dev):
+    g = np.random.default_rng(4)
+    specs, pools, d = [(100, 64), (30, 64)], [(8, 5)], 128
+    B = 6
+    tabs, ids, offs = _inputs(g, B, pools, specs, "bf16", bad_id=True)
+    ws = [ot.random_tokenizer_weights(128, d, 8, seed=1)]
+    wd = [{k: (v.to(torch.bfloat16) if k != "pos" else v).contiguous().to(dev) for k, v in w.items()} for w in ws]
+    err = torch.zeros(1, dtype=torch.int32, device=dev)
+    out, mask = pdm.ops.seq_tokenize_raw(_dev_tables(tabs, dev), [[torch.from_numpy(a).to(dev) for a in r] for r in ids],
+                                         [torch.from_numpy(x).to(dev) for x in offs], [8], wd, err_flag=err)
+    torch.cuda.synchronize()
+    assert err.item() == 1
+    # the bad id's feature reads zeros, as in the gather
+    _check(out.cpu(), tabs, ids, offs, [8], ws, 0, 0, mask)
+    # offsets past the ids: the sample counts as empty and the flag is raised
+    bad_offs = [offs[0].copy()]
+    bad_offs[0][-1] = len(ids[0][0]) + 4
+    err.zero_()
+    out2, mask2 = pdm.ops.seq_tokenize_raw(_dev_tables(tabs, dev),
+                                           [[torch.from_numpy(a).to(dev) for a in r] for r in ids],
+                                           [torch.from_numpy(x).to(dev) for x in bad_offs], [8], wd, err_flag=err)
+    torch.cuda.synchronize()
+    assert err.item() == 1
+    assert int(mask2[-1].sum().item()) == 0
+
+
+def test_empty_batch_and_empty_pool(pdm, dev):
+    g = np.random.default_rng(3)
+    specs, d = [(50, 64), (20, 64)], 128
+    ws = [ot.random_tokenizer_weights(128, d, 8, seed=i) for i in range(2)]
+    wd = [{k: (v.to(torch.bfloat16) if k != "pos" else v).contiguous().to(dev) for k, v in w.items()} for w in ws]
+    tabs, ids, offs = _inputs(g, 0, [(8, 3), (0, 2)], specs, "bf16")
+    out, mask = pdm.ops.seq_tokenize_raw(_dev_tables(tabs, dev), [[torch.from_numpy(a).to(dev) for a in r] for r in ids],
+                                         [torch.from_numpy(x).to(dev) for x in offs], [8, 0], wd)
+    assert out.shape == (0, 8, d)
+    tabs, ids, offs = _inputs(g, 5, [(8, 3), (0, 2)], specs, "bf16")
+    wd[1] = {k: None for k in wd[1]}
+    out, mask = pdm.ops.seq_tokenize_raw(_dev_tables(tabs, dev), [[torch.from_numpy(a).to(dev) for a in r] for r in ids],
+                                         [torch.from_numpy(x).to(dev) for x in offs], [8, 0], [wd[0], wd[1]])
+    torch.cuda.synchronize()
+    _check(out.cpu(), tabs, ids, offs, [8, 0], ws, 0, 0, mask)
+
+
+def test_unsupported_width_is_an_error(pdm, dev):
+    tabs = [torch.zeros(10, 72, dtype=torch.bfloat16, device=dev)]
+    ids = [[torch.zeros(3, dtype=torch.int64, device=dev)]]
+    offs = [torch.tensor([0, 3], dtype=torch.int64, device=dev)]
+    w = ot.random_tokenizer_weights(72, 128, 4)
+    wd = [{k: (v.to(torch.bfloat16) if k != "pos" else v).contiguous().to(dev) for k, v in w.items()}]
+    with pytest.raises(pdm._lib.PdmError):
+        pdm.ops.seq_tokenize_raw(tabs, ids, offs, [4], wd)
