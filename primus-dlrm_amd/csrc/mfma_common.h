@@ -20,6 +20,13 @@ __device__ __forceinline__ f32x16_t mfma32x32x16(u32x4_t a, u32x4_t b, f32x16_t 
                                                  c, 0, 0, 0);
 }
 
+// 16x16x32 bf16: lane l supplies row (A) / column (B) l % 16, k = 8 (l / 16) .. +8;
+// accumulator element i of lane l is row 4 (l / 16) + i, column l % 16.
+__device__ __forceinline__ f32x4_t mfma16x16x32(u32x4_t a, u32x4_t b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
+                                                 c, 0, 0, 0);
+}
+
 // Pins the instruction order of a fully unrolled loop of N MFMAs, each fed by
 // one LDS read: the first LEAD reads are issued up front, then one MFMA and
 // the next read alternate, so every read has LEAD MFMAs of latency slack.

@@ -16,7 +16,7 @@
 //   2. tok_list_kernel   a wave per (pool, sample): the pool's list of real
 //                        tokens in sample order (output slot and the validated
 //                        row id of every feature).
-//   3. tok_mlp_kernel    persistent workgroups of 4 waves take passes of 128
+//   3. tok_mlp_kernel    persistent workgroups of 8 waves take passes of 128
 //                        list entries (entry 0 of a pool is its padding
 //                        token) from an atomic counter; Linear -> GELU ->
 //                        Linear on bf16 MFMAs; token rows written (the padding
@@ -31,13 +31,14 @@
 
 namespace pdm {
 
-constexpr int kTokNW = 4;               // waves per MLP workgroup (one per SIMD)
-constexpr int kTokRows = kTokNW * 32;   // list entries per pass
+constexpr int kTokNW = 8;               // waves per MLP workgroup (two per SIMD)
+constexpr int kTokRows = kTokNW * 16;   // list entries per pass
 constexpr int kTokNST = 4;              // LDS ring stages
 constexpr int kTokPF = kTokNST - 1;     // ring chunks read ahead
 constexpr int kScanThreads = 1024;
 constexpr int kTokMaxPieces = 64;       // 16-byte raw pieces (8 columns) per token row, K <= 512
 constexpr int kTokZeroBytes = 2048;     // zero row read for padding in ZERO mode and ids outside a table
+constexpr int kTokMaxFeatures = 4;      // tables per event
 
 struct TokArgs {
   const int64_t* ids[PDM_SEQ_MAX_POOLS * PDM_SEQ_MAX_FEATURES];
@@ -66,7 +67,7 @@ struct TokArgs {
   uint32_t* counter;  // next pass of the MLP kernel
   int32_t* cnt;       // [P][B + 1] exclusive scan of n_b
   int32_t* tok_slot;  // pool p's list at B * soff[p]: b * L + l
-  int64_t* tok_id;    // [F][B * S]: row id of feature f of each entry, -1 for an id outside the table
+  int32_t* tok_id;    // [F][B * S]: row of feature f of each entry, -1 for an id outside the table
   float* y_pad;       // [P][d] padding token's row (before pos)
   char* zero_row;     // kTokZeroBytes of zeros
 };
@@ -143,81 +144,84 @@ __global__ __launch_bounds__(256) void tok_list_kernel(TokArgs a) {
     const int l = a.align_left ? j : L - n + j;
     a.tok_slot[base + j] = (int32_t)(b * L + l);
 #pragma unroll
-    for (int f = 0; f < PDM_SEQ_MAX_FEATURES; ++f) {
+    for (int f = 0; f < kTokMaxFeatures; ++f) {
       if (f >= a.F) break;
-      int64_t id = a.ids[p * PDM_SEQ_MAX_FEATURES + f][e];
-      if (id < 0 || id >= a.rows[f]) {
-        bad = true;
-        id = -1;
-      }
-      a.tok_id[f * fstride + base + j] = id;
+      const int64_t id = a.ids[p * PDM_SEQ_MAX_FEATURES + f][e];
+      const bool ok = id >= 0 && id < a.rows[f];
+      bad |= !ok;
+      a.tok_id[f * fstride + base + j] = ok ? (int32_t)id : -1;
     }
   }
   if (bad && a.err) a.err[0] = 1;
 }
 
-// bf16(u + b1) -> exact-erf GELU -> bf16, two values per packed word.  u[e] is
-// hidden unit (e/8)*16 + (l/32)*8 + e%8 of the chunk; bl / bh hold the biases
-// of units (l/32)*8 + 0..7 and 16 + (l/32)*8 + 0..7 as bf16 pairs.
-__device__ __forceinline__ void bias_gelu_pack(const f32x16_t& u, u32x4_t bl, u32x4_t bh, uint32_t (&g)[8]) {
-  const uint32_t bw[8] = {bl.x, bl.y, bl.z, bl.w, bh.x, bh.y, bh.z, bh.w};
+// bf16(u + b1) -> exact-erf GELU -> bf16 for 8 hidden units held as two 16x16
+// accumulator quarters (u0: units 0..3, u1: units 4..7), packed two per word;
+// bb holds their biases as bf16 pairs.
+__device__ __forceinline__ u32x4_t bias_gelu_pack8(const f32x4_t& u0, const f32x4_t& u1, u32x4_t bb) {
+  const float v[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+  const uint32_t bw[4] = {bb.x, bb.y, bb.z, bb.w};
+  uint32_t g[4];
 #pragma unroll
-  for (int e = 0; e < 16; e += 2) {
-    const uint32_t bb = bw[e >> 1];
-    const float x0 = bf16_round(u[e] + __uint_as_float(bb << 16));
-    const float x1 = bf16_round(u[e + 1] + __uint_as_float(bb & 0xffff0000u));
+  for (int e = 0; e < 8; e += 2) {
+    const uint32_t w = bw[e >> 1];
+    const float x0 = bf16_round(v[e] + __uint_as_float(w << 16));
+    const float x1 = bf16_round(v[e + 1] + __uint_as_float(w & 0xffff0000u));
     g[e >> 1] = pack_bf16x2(gelu_erf(x0), gelu_erf(x1));
   }
+  return u32x4_t{g[0], g[1], g[2], g[3]};
 }
 
 // One pass's list entries as seen by a thread of the first kTokRows.
 struct TokEntry {
-  int64_t o;  // output element offset; -1: no entry, -2: the pool's padding token
-  int l;      // sequence position
-  int64_t id[PDM_SEQ_MAX_FEATURES];  // row per feature, -1: zeros
+  int sl;  // slot b * L + l; -1: no entry, -2: the pool's padding token
+  int id[kTokMaxFeatures];  // row per feature, -1: zeros
 };
 
 // ---------------------------------------------------------------------------
 // 3. The MLP over passes of 128 list entries.
 //
-// Wave w of a pass owns entries w*32 .. w*32+31; lane l holds entry l%32 and
-// k-slots (l/32)*8 .. +8 of every 16-wide k step of its raw row (the MFMA
-// operand layout), loaded straight from the tables (16-byte pieces; features
-// are multiples of 8 columns, so no piece straddles two tables).
+// Eight waves of 16 entries each, two waves per SIMD: one wave's GELU and
+// memory waits overlap the other's MFMAs (a wave's own MFMA and VALU work do
+// not overlap).  On 16x16x32 MFMAs lane l holds entry l%16 and k-slots
+// 8(l/16) .. +8 of every 32-wide k step of its raw row, loaded straight from
+// the tables (16-byte pieces; features are multiples of 8 columns, so no piece
+// straddles two tables).
 //
-// Linear 1, U^T = W1_c . raw^T per chunk c of 32 hidden units (hidden units on
-// the accumulator rows, tokens on the columns), then bf16(U + b1), GELU, bf16
-// packed into registers: after the chunks each lane holds its token's d hidden
-// values as the B operand of Linear 2, y^T += W2[rows, c] . G_c^T, computed in
-// two halves of d/2 outputs.  LDS row r of a W1 chunk holds hidden unit
-// swap23(r) (bits 2 and 3 swapped) so that accumulator element e of lane l is
-// hidden unit (e/8)*16 + (l/32)*8 + e%8 and the packed values are k-step
-// halves of Linear 2 without any shuffle.
+// Linear 1 walks the hidden units in chunks of 32 as two 16-row tiles: U^T =
+// W1_c . raw^T (hidden units on the accumulator rows, entries on the
+// columns).  LDS row 16t + 4g + i of a W1 chunk holds hidden unit 8g + 4t + i,
+// so lane l (g = l/16) ends with the contiguous units 8g .. 8g+7 of the chunk:
+// after bias, GELU and bf16 packing they are exactly its B operand of Linear 2's
+// 32-wide k step, y^T += W2[rows, step] . G^T, computed for two halves of d/2
+// outputs in 16-row accumulator tiles.
 //
 // Weights stream through one NST-stage LDS ring as a continuous sequence of
 // chunks: per pass NC W1 chunks (32 x K, padded rows), then 2 x NC2 W2 chunks
-// (d/2 rows x 64 hidden units); chunk cc + PF is read to registers during chunk
-// cc and stored to the stage chunk cc - 1 used.  The last PF chunks of a pass
-// read the next pass's first W1 chunks.
+// (d/2 rows x 64 hidden units, pieces XOR-swizzled by row).  Chunk cc + PF is
+// read to registers during chunk cc and stored at the start of chunk cc + 1
+// (after its barrier) to the stage chunk cc - 1 used, so its loads have a whole
+// chunk of MFMA work to arrive in.  The last PF chunks of a pass read the next
+// pass's first W1 chunks.
 //
 // Vector memory completions are counted in issue order (stores included), so a
 // wait for any load also waits for every older access.  The schedule keeps
 // long-latency accesses out of the way of the ring's per-chunk wait: the next
 // pass is taken from the counter at Linear 1 chunk 0, its entries and biases
 // are read after chunk 1's ring loads and stored to the other LDS buffer at
-// chunk 2; biases are read from LDS; an epilogue issues all its position
+// chunk 2; biases are read from LDS; an epilogue half issues all its position
 // loads before its first store; the next pass's raw rows are gathered after
 // the last store of the pass.
 // ---------------------------------------------------------------------------
 template <int K, int D, bool F32>
-__global__ __launch_bounds__(kTokNW * 64) void tok_mlp_kernel(TokArgs a) {
+__global__ __launch_bounds__(kTokNW * 64, 1) void tok_mlp_kernel(TokArgs a) {
   constexpr int NT = kTokNW * 64;
   constexpr int ROWS = kTokRows;
-  constexpr int KS = K / 16;         // k steps of Linear 1
-  constexpr int NC = D / 32;         // Linear 1 chunks (32 hidden units)
-  constexpr int NC2 = D / 64;        // Linear 2 chunks per output half (64 hidden units)
-  constexpr int HD = D / 2;          // outputs per half
-  constexpr int DBH = HD / 32;       // 32-row output blocks per half
+  constexpr int KS = K / 32;    // k steps of Linear 1
+  constexpr int NC = D / 32;    // Linear 1 chunks of 32 hidden units (= Linear 2 k steps)
+  constexpr int NC2 = D / 64;   // Linear 2 chunks per output half (64 hidden units)
+  constexpr int HD = D / 2;     // outputs per half
+  constexpr int MTH = HD / 16;  // 16-row output tiles per half
   constexpr int NCH = NC + 2 * NC2;  // ring chunks per pass
   constexpr int NST = kTokNST, PF = kTokPF;
   constexpr int W1_BYTES = 32 * w_stride<K>();
@@ -225,16 +229,16 @@ __global__ __launch_bounds__(kTokNW * 64) void tok_mlp_kernel(TokArgs a) {
   constexpr int SLOT = W1_BYTES > W2_BYTES ? W1_BYTES : W2_BYTES;
   constexpr int SEG = 32;             // outputs per epilogue step
   constexpr int SROW = SEG * 4 + 16;  // staging row stride (bytes), padded against bank conflicts
-  constexpr int NSQ = HD / SEG;       // epilogue steps per half
-  constexpr int PPL = 32 * (SEG / 4) / 64;  // 16-byte output pieces per lane and step
+  constexpr int NSQ = D / SEG;        // epilogue steps (both halves)
+  constexpr int PPL = 16 * (SEG / 4) / 64;  // 16-byte output pieces per lane and step
   constexpr int CPR = K / 8;                    // 16-byte pieces per W1 row
   constexpr int L1 = (32 * CPR + NT - 1) / NT;  // W1 chunk pieces per thread
-  constexpr int L2 = HD * 8 / NT;               // W2 chunk pieces per thread
-  static_assert(K % 16 == 0 && D % 64 == 0 && (HD * 8) % NT == 0 && HD % SEG == 0, "unsupported tokenizer shape");
+  constexpr int L2 = (HD * 8 + NT - 1) / NT;    // W2 chunk pieces per thread
+  static_assert(K % 32 == 0 && D % 64 == 0 && HD % SEG == 0 && NSQ % 2 == 0, "unsupported tokenizer shape");
   static_assert(NCH % NST == 0 && PF <= NC && NC >= 4 && NT - ROWS >= D / 4, "schedule needs these");
   __shared__ __attribute__((aligned(16))) char sRing[NST * SLOT];
   __shared__ __attribute__((aligned(16))) char sStage[ROWS * SROW];  // per-wave epilogue staging
-  __shared__ const char* s_rp[2][PDM_SEQ_MAX_FEATURES][ROWS];       // row of each feature
+  __shared__ const char* s_rp[2][kTokMaxFeatures][ROWS];            // row of each feature
   __shared__ int64_t s_out[2][ROWS];
   __shared__ int s_l[2][ROWS];
   __shared__ __attribute__((aligned(16))) uint16_t s_b1[2][D];
@@ -246,7 +250,7 @@ __global__ __launch_bounds__(kTokNW * 64) void tok_mlp_kernel(TokArgs a) {
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
-  const int fr = lane & 31, hf = lane >> 5;
+  const int r16 = lane & 15, g4 = lane >> 4;
   static_assert(CPR <= kTokMaxPieces && K * (F32 ? 4 : 2) <= kTokZeroBytes, "raw row too wide");
   for (int j = tid; j < CPR; j += NT) s_piece[j] = a.piece[j];
   if (tid == 0) {
@@ -261,14 +265,16 @@ __global__ __launch_bounds__(kTokNW * 64) void tok_mlp_kernel(TokArgs a) {
     s_q[0] = (int)atomicAdd(a.counter, 1u);
   }
   __syncthreads();
-  const int total = s_np[a.P];
-  int q = s_q[0];
+  const int total = __builtin_amdgcn_readfirstlane(s_np[a.P]);
+  int q = __builtin_amdgcn_readfirstlane(s_q[0]);
   if (q >= total) return;  // uniform
 
+  // pass and pool indices are wave-uniform: readfirstlane keeps them in scalar registers, so the per-pool
+  // kernel arguments are indexed with scalar loads
   auto pool_of = [&](int qq) {
     int p = 0;
     while (p + 1 < a.P && qq >= s_np[p + 1]) ++p;
-    return p;
+    return __builtin_amdgcn_readfirstlane(p);
   };
   const int64_t fstride = a.B * a.S;
   // threads 0 .. ROWS-1: one entry each; threads ROWS .. ROWS + D/4 - 1: one 16-byte piece of b1 or b2
@@ -281,45 +287,48 @@ __global__ __launch_bounds__(kTokNW * 64) void tok_mlp_kernel(TokArgs a) {
       return;
     }
     const int i = (qq - s_np[p]) * ROWS + tid;
-    en.o = -1;
-    en.l = 0;
-    if (i == 0) {
-      en.o = -2;
+    en.sl = -1;
 #pragma unroll
-      for (int f = 0; f < PDM_SEQ_MAX_FEATURES; ++f) en.id[f] = a.pad_zero ? -1 : 0;
+    for (int f = 0; f < kTokMaxFeatures; ++f) en.id[f] = -1;
+    if (i == 0) {
+      en.sl = -2;
+#pragma unroll
+      for (int f = 0; f < kTokMaxFeatures; ++f) en.id[f] = a.pad_zero ? -1 : 0;
     } else if (i - 1 < s_tot[p]) {
       const int64_t base = a.B * a.soff[p] + (i - 1);
-      const int sl = a.tok_slot[base];
+      en.sl = a.tok_slot[base];
 #pragma unroll
-      for (int f = 0; f < PDM_SEQ_MAX_FEATURES; ++f) en.id[f] = f < a.F ? a.tok_id[f * fstride + base] : -1;
-      const int L = a.lmax[p];
-      const int b = sl / L;
-      en.l = sl - b * L;
-      en.o = (int64_t)b * a.out_bstride + (int64_t)(a.soff[p] + en.l) * D;
-    } else {
-#pragma unroll
-      for (int f = 0; f < PDM_SEQ_MAX_FEATURES; ++f) en.id[f] = -1;
+      for (int f = 0; f < kTokMaxFeatures; ++f)
+        if (f < a.F) en.id[f] = a.tok_id[f * fstride + base];
     }
   };
-  auto store_entry = [&](int buf, const TokEntry& en) {
+  auto store_entry = [&](int buf, int p, const TokEntry& en) {
     if (tid >= ROWS) {
       const int t = tid - ROWS;
       if (t < D / 8) *reinterpret_cast<u32x4_t*>(&s_b1[buf][t * 8]) = bias_piece;
       else if (t < D / 4) *reinterpret_cast<u32x4_t*>(&s_b2[buf][(t - D / 8) * 8]) = bias_piece;
       return;
     }
-    s_out[buf][tid] = en.o;
-    s_l[buf][tid] = en.l;
+    int64_t o = en.sl == -2 ? -2 : -1;
+    int l = 0;
+    if (en.sl >= 0) {
+      const int L = a.lmax[p];
+      const int b = en.sl / L;
+      l = en.sl - b * L;
+      o = (int64_t)b * a.out_bstride + (int64_t)(a.soff[p] + l) * D;
+    }
+    s_out[buf][tid] = o;
+    s_l[buf][tid] = l;
 #pragma unroll
-    for (int f = 0; f < PDM_SEQ_MAX_FEATURES; ++f)
-      if (f < a.F) s_rp[buf][f][tid] = en.id[f] >= 0 ? a.tables[f] + en.id[f] * a.row_bytes[f] : a.zero_row;
+    for (int f = 0; f < kTokMaxFeatures; ++f)
+      if (f < a.F) s_rp[buf][f][tid] = en.id[f] >= 0 ? a.tables[f] + (int64_t)en.id[f] * a.row_bytes[f] : a.zero_row;
   };
-  const int row = wave * 32 + fr;
+  const int row = wave * 16 + r16;  // the lane's entry
   // every piece is one load, without branches (rows outside a table and ZERO padding read the zero row)
   auto gather = [&](int buf, u32x4_t (&af)[KS]) {
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
-      const int pi = s_piece[2 * s + hf];
+      const int pi = s_piece[4 * s + g4];
       const char* rp = s_rp[buf][pi >> 16][row] + (pi & 0xffff);
       if constexpr (F32) {
         const f32x4_t x0 = *reinterpret_cast<const f32x4_t*>(rp);
@@ -332,9 +341,10 @@ __global__ __launch_bounds__(kTokNW * 64) void tok_mlp_kernel(TokArgs a) {
     }
   };
 
-  // Ring chunk c < NC: W1 rows c*32 + swap23(r), all K columns.  Chunk NC + h*NC2 + c: W2 rows
-  // h*HD .. h*HD + HD, hidden units c*64 .. c*64 + 64, as 128-byte LDS rows with piece v of row d at
-  // v ^ sw(d), sw(d) = ((d >> 1) & 7) ^ ((d & 1) << 2): 8 consecutive rows, and also 16, cover all banks.
+  // Ring chunk c < NC: W1 rows c*32 + perm(r), perm(16t + 4g + i) = 8g + 4t + i, all K columns.  Chunk
+  // NC + h*NC2 + c: W2 rows h*HD .. h*HD + HD, hidden units c*64 .. c*64 + 64, as 128-byte LDS rows with piece
+  // v of row e at v ^ sw(e), sw(e) = ((e >> 1) & 7) ^ ((e & 1) << 2): 8 consecutive rows, and also 16, cover
+  // all banks.
   u32x4_t r1[L1], r2[L2];
   auto gload = [&](int cc, const uint16_t* W1p, const uint16_t* W2p) {
     if (cc < NC) {
@@ -342,7 +352,7 @@ __global__ __launch_bounds__(kTokNW * 64) void tok_mlp_kernel(TokArgs a) {
       for (int i = 0; i < L1; ++i) {
         const int pc = i * NT + tid;
         const int r = pc / CPR, j = pc - (pc / CPR) * CPR;
-        const int hid = cc * 32 + ((r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1));
+        const int hid = cc * 32 + ((r >> 2) & 3) * 8 + (r >> 4) * 4 + (r & 3);
         if (pc < 32 * CPR) r1[i] = *reinterpret_cast<const u32x4_t*>(W1p + (int64_t)hid * K + j * 8);
       }
     } else {
@@ -350,9 +360,9 @@ __global__ __launch_bounds__(kTokNW * 64) void tok_mlp_kernel(TokArgs a) {
 #pragma unroll
       for (int i = 0; i < L2; ++i) {
         const int pc = i * NT + tid;
-        const int d = pc >> 3;
-        const int v = (pc & 7) ^ (((d >> 1) & 7) ^ ((d & 1) << 2));
-        r2[i] = *reinterpret_cast<const u32x4_t*>(W2p + (int64_t)(h * HD + d) * D + c * 64 + v * 8);
+        const int e = pc >> 3, v = (pc & 7) ^ (((e >> 1) & 7) ^ ((e & 1) << 2));
+        if (pc < HD * 8)
+          r2[i] = *reinterpret_cast<const u32x4_t*>(W2p + (int64_t)(h * HD + e) * D + c * 64 + v * 8);
       }
     }
   };
@@ -367,17 +377,21 @@ __global__ __launch_bounds__(kTokNW * 64) void tok_mlp_kernel(TokArgs a) {
       }
     } else {
 #pragma unroll
-      for (int i = 0; i < L2; ++i) *reinterpret_cast<u32x4_t*>(st + (i * NT + tid) * 16) = r2[i];
+      for (int i = 0; i < L2; ++i) {
+        const int pc = i * NT + tid;
+        if (pc < HD * 8) *reinterpret_cast<u32x4_t*>(st + pc * 16) = r2[i];
+      }
     }
   };
 
   int p = pool_of(q);
   int buf = 0;
+  bool pend = false;  // r1 / r2 hold chunk cc - 1 + PF, to be stored at the start of chunk cc
   u32x4_t af[KS];
   {
     TokEntry en;
     load_entry(q, p, en);
-    store_entry(0, en);
+    store_entry(0, p, en);
 #pragma unroll
     for (int cc = 0; cc < PF; ++cc) {
       gload(cc, a.w1[p], a.w2[p]);
@@ -393,116 +407,116 @@ __global__ __launch_bounds__(kTokNW * 64) void tok_mlp_kernel(TokArgs a) {
     int qn = total, pn = 0;
     TokEntry en;
 
-    // Linear 1 + GELU: gp[c][0..3] = hidden c*32 + hf*8 + 0..7, gp[c][4..7] = c*32 + 16 + hf*8 + 0..7
-    uint32_t gp[NC][8];
+    // Linear 1 + GELU: gp[c] = bf16 GELU values of hidden units c*32 + 8*g4 .. +8 of the lane's entry
+    u32x4_t gp[NC];
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-      __syncthreads();  // chunks c .. c+PF-1 are in LDS; chunk c-1's stage is free
+      __syncthreads();  // chunks c .. c+PF-2 are in LDS; chunks c-2 and c-1 are done with
       if (c == 0 && tid == 0) s_q[1] = (int)atomicAdd(a.counter, 1u);
+      // the chunk read during the previous chunk goes to LDS now (a whole chunk after its loads were issued;
+      // its stage, chunk c-2's, is free), then chunk c + PF is read
+      if (pend) sstore(c - 1 + PF + (c == 0 ? NCH : 0));
       gload(c + PF, W1, W2);
+      pend = true;
       if (c == 1) {
         // the next pass: its entries and biases, read after this chunk's ring loads
-        qn = s_q[1];
+        qn = __builtin_amdgcn_readfirstlane(s_q[1]);
         if (qn < total) {
           pn = pool_of(qn);
           load_entry(qn, pn, en);
         }
       }
-      if (c == 2 && qn < total) store_entry(buf ^ 1, en);
+      if (c == 2 && qn < total) store_entry(buf ^ 1, pn, en);
       const char* w1 = sRing + (c % NST) * SLOT;
-      f32x16_t u;
+      f32x4_t u0 = {0.0f, 0.0f, 0.0f, 0.0f}, u1 = {0.0f, 0.0f, 0.0f, 0.0f};
+      u32x4_t wf[2 * KS];
 #pragma unroll
-      for (int e = 0; e < 16; ++e) u[e] = 0.0f;
-      u32x4_t wf[KS];
+      for (int s = 0; s < KS; ++s) {
+        wf[2 * s] = read_w_frag<K>(w1, r16, 4 * s + g4);
+        wf[2 * s + 1] = read_w_frag<K>(w1, 16 + r16, 4 * s + g4);
+      }
 #pragma unroll
-      for (int s = 0; s < KS; ++s) wf[s] = read_w_frag<K>(w1, fr, 2 * s + hf);
-#pragma unroll
-      for (int s = 0; s < KS; ++s) u = mfma32x32x16(wf[s], af[s], u);
-      sched_mfma_ds_pipeline<KS, 4>();
-      sstore(c + PF);
-      const u32x4_t bl = *reinterpret_cast<const u32x4_t*>(&s_b1[buf][c * 32 + hf * 8]);
-      const u32x4_t bh = *reinterpret_cast<const u32x4_t*>(&s_b1[buf][c * 32 + 16 + hf * 8]);
-      bias_gelu_pack(u, bl, bh, gp[c]);
+      for (int s = 0; s < KS; ++s) {
+        u0 = mfma16x16x32(wf[2 * s], af[s], u0);
+        u1 = mfma16x16x32(wf[2 * s + 1], af[s], u1);
+      }
+      sched_mfma_ds_pipeline<2 * KS, 4>();
+      const u32x4_t bb = *reinterpret_cast<const u32x4_t*>(&s_b1[buf][c * 32 + 8 * g4]);
+      gp[c] = bias_gelu_pack8(u0, u1, bb);
     }
 
     const float* pos = a.pos[p];
     float* ypad = a.y_pad + (int64_t)p * D;
-    char* stage = sStage + wave * (32 * SROW);
+    char* stage = sStage + wave * (16 * SROW);
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      // Linear 2 on outputs h*HD .. h*HD + HD: y^T[db] += W2[rows, chunk] . G^T over 4 k steps per chunk;
-      // k step t of chunk c is hidden c*64 + 16t + hf*8 + 0..7 = gp[2c + t/2][4*(t%2) ..], piece 2t + hf
-      f32x16_t y[DBH];
+      // Linear 2 on outputs h*HD .. h*HD + HD: y[m] = outputs h*HD + 16m + 4*g4 + 0..3 of the lane's entry;
+      // k step t of chunk c is hidden units (2c + t)*32 + 8*g4 .. +8 = gp[2c + t], piece 4t + g4 of the row
+      f32x4_t y[MTH];
 #pragma unroll
-      for (int db = 0; db < DBH; ++db)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) y[db][e] = 0.0f;
+      for (int m = 0; m < MTH; ++m) y[m] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int c = 0; c < NC2; ++c) {
         const int cc = NC + h * NC2 + c;
         __syncthreads();
+        if (pend) sstore(cc - 1 + PF);
         const bool next = cc + PF >= NCH;
+        pend = !next || qn < total;
         if (!next) gload(cc + PF, W1, W2);
         else if (qn < total) gload(cc + PF - NCH, a.w1[pn], nullptr);
         const char* w2 = sRing + (cc % NST) * SLOT;
-        u32x4_t wf[DBH * 4];
+        u32x4_t wf[2 * MTH];
 #pragma unroll
-        for (int t = 0; t < 4; ++t)
+        for (int t = 0; t < 2; ++t)
 #pragma unroll
-          for (int db = 0; db < DBH; ++db) {
-            const int d = db * 32 + fr;
-            const int sw = ((d >> 1) & 7) ^ ((d & 1) << 2);
-            wf[t * DBH + db] = *reinterpret_cast<const u32x4_t*>(w2 + d * 128 + (((2 * t + hf) ^ sw) << 4));
+          for (int m = 0; m < MTH; ++m) {
+            const int e = m * 16 + r16;
+            const int sw = ((e >> 1) & 7) ^ ((e & 1) << 2);
+            wf[t * MTH + m] = *reinterpret_cast<const u32x4_t*>(w2 + e * 128 + (((4 * t + g4) ^ sw) << 4));
           }
 #pragma unroll
-        for (int t = 0; t < 4; ++t)
+        for (int t = 0; t < 2; ++t)
 #pragma unroll
-          for (int db = 0; db < DBH; ++db) {
-            const uint32_t* g = &gp[2 * c + (t >> 1)][4 * (t & 1)];
-            const u32x4_t gb = {g[0], g[1], g[2], g[3]};
-            y[db] = mfma32x32x16(wf[t * DBH + db], gb, y[db]);
-          }
-        sched_mfma_ds_pipeline<DBH * 4, 4>();
-        if (!next || qn < total) sstore(cc + PF);
+          for (int m = 0; m < MTH; ++m) y[m] = mfma16x16x32(wf[t * MTH + m], gp[2 * c + t], y[m]);
+        sched_mfma_ds_pipeline<2 * MTH, 4>();
       }
 
-      // Epilogue of the half: bf16(y + b2) (+ pos[l]) through the wave's own staging rows, SEG outputs at
-      // a time, written as row segments.  y[db][e] is output h*HD + db*32 + (e/4)*8 + hf*4 + e%4 of the
-      // lane's entry.  Every position load of the half is issued before its first store.
-      f32x4_t pe[NSQ][PPL];
+      // Epilogue of the half: bf16(y + b2) (+ pos[l]) through the wave's own staging rows, SEG outputs at a
+      // time, written as row segments; every position load of the half is issued before its first store.
+      f32x4_t pe[NSQ / 2][PPL];
 #pragma unroll
-      for (int sq = 0; sq < NSQ; ++sq)
+      for (int sq = 0; sq < NSQ / 2; ++sq)
 #pragma unroll
         for (int it = 0; it < PPL; ++it) {
           const int piece = it * 64 + lane;
           const int r = piece / (SEG / 4), c4 = piece - (piece / (SEG / 4)) * (SEG / 4);
-          const int ent = wave * 32 + r;
+          const int ent = wave * 16 + r;
           pe[sq][it] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
           if (pos && s_out[buf][ent] >= 0)
             pe[sq][it] = *reinterpret_cast<const f32x4_t*>(pos + (int64_t)s_l[buf][ent] * D + h * HD + sq * SEG +
                                                            c4 * 4);
         }
 #pragma unroll
-      for (int sq = 0; sq < NSQ; ++sq) {
-        const int db = sq * (SEG / 32);
-        const int d0 = h * HD + db * 32;
+      for (int sq = 0; sq < NSQ / 2; ++sq) {
+        const int col0 = h * HD + sq * SEG;
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const u32x2_t bb = *reinterpret_cast<const u32x2_t*>(&s_b2[buf][d0 + g * 8 + hf * 4]);
-          *reinterpret_cast<f32x4_t*>(stage + fr * SROW + (g * 8 + hf * 4) * 4) =
-              f32x4_t{bf16_round(y[db][4 * g] + __uint_as_float(bb.x << 16)),
-                      bf16_round(y[db][4 * g + 1] + __uint_as_float(bb.x & 0xffff0000u)),
-                      bf16_round(y[db][4 * g + 2] + __uint_as_float(bb.y << 16)),
-                      bf16_round(y[db][4 * g + 3] + __uint_as_float(bb.y & 0xffff0000u))};
+        for (int mm = 0; mm < SEG / 16; ++mm) {
+          const int m = sq * (SEG / 16) + mm;
+          const u32x2_t bb = *reinterpret_cast<const u32x2_t*>(&s_b2[buf][h * HD + m * 16 + 4 * g4]);
+          *reinterpret_cast<f32x4_t*>(stage + r16 * SROW + (mm * 16 + 4 * g4) * 4) =
+              f32x4_t{bf16_round(y[m].x + __uint_as_float(bb.x << 16)),
+                      bf16_round(y[m].y + __uint_as_float(bb.x & 0xffff0000u)),
+                      bf16_round(y[m].z + __uint_as_float(bb.y << 16)),
+                      bf16_round(y[m].w + __uint_as_float(bb.y & 0xffff0000u))};
         }
         // a wave reads back only its own rows; its LDS accesses execute in order
 #pragma unroll
         for (int it = 0; it < PPL; ++it) {
           const int piece = it * 64 + lane;
           const int r = piece / (SEG / 4), c4 = piece - (piece / (SEG / 4)) * (SEG / 4);
-          const int64_t o = s_out[buf][wave * 32 + r];
+          const int64_t o = s_out[buf][wave * 16 + r];
           if (o == -1) continue;
-          const int col = h * HD + sq * SEG + c4 * 4;
+          const int col = col0 + c4 * 4;
           const f32x4_t v = *reinterpret_cast<const f32x4_t*>(stage + r * SROW + c4 * 16);
           if (o == -2) {
             *reinterpret_cast<f32x4_t*>(ypad + col) = v;
@@ -578,7 +592,7 @@ TokLayout tok_layout(int64_t P, int64_t F, int64_t B, int64_t S, int64_t D) {
   l.cnt = l.zero + kTokZeroBytes;
   l.slot = l.cnt + align256(P * (B + 1) * 4);
   l.id = l.slot + align256(B * S * 4);
-  l.ypad = l.id + align256(F * B * S * 8);
+  l.ypad = l.id + align256(F * B * S * 4);
   l.total = l.ypad + align256(P * D * 4);
   return l;
 }
@@ -632,6 +646,7 @@ extern "C" int pdm_seq_tokenize_fwd(const pdm_seq_desc* desc, const void* const*
   PDM_CHECK_ARG(d.batch_size >= 0, "batch_size < 0");
   PDM_CHECK_ARG(d_model == 128 || d_model == 256, "d_model must be 128 or 256");
   PDM_CHECK_ARG(tables && ids && offsets && weights, "null pointer array");
+  PDM_CHECK_ARG(d.num_features <= kTokMaxFeatures, "the tokenizer takes at most 4 tables per event");
   const bool f32 = d.dtype == PDM_F32;
   const int es = f32 ? 4 : 2;
   TokArgs a{};
@@ -640,7 +655,7 @@ extern "C" int pdm_seq_tokenize_fwd(const pdm_seq_desc* desc, const void* const*
   int32_t col = 0;
   for (int f = 0; f < a.F; ++f) {
     PDM_CHECK_ARG(d.dim[f] > 0 && d.dim[f] % 8 == 0, "every dim must be a positive multiple of 8");
-    PDM_CHECK_ARG(d.rows[f] >= 0, "rows < 0");
+    PDM_CHECK_ARG(d.rows[f] >= 0 && d.rows[f] < (int64_t(1) << 31), "rows must be in [0, 2^31)");
     PDM_CHECK_ARG(d.rows[f] == 0 || tables[f] != nullptr, "null table pointer");
     PDM_CHECK_ARG(((uintptr_t)tables[f] & 15) == 0, "table pointers must be 16-byte aligned");
     PDM_CHECK_ARG(d.pad_mode == PDM_PAD_ZERO || d.rows[f] > 0, "ROW0 padding needs a row 0 in every table");
@@ -707,7 +722,7 @@ extern "C" int pdm_seq_tokenize_fwd(const pdm_seq_desc* desc, const void* const*
   a.zero_row = ws + lay.zero;
   a.cnt = reinterpret_cast<int32_t*>(ws + lay.cnt);
   a.tok_slot = reinterpret_cast<int32_t*>(ws + lay.slot);
-  a.tok_id = reinterpret_cast<int64_t*>(ws + lay.id);
+  a.tok_id = reinterpret_cast<int32_t*>(ws + lay.id);
   a.y_pad = reinterpret_cast<float*>(ws + lay.ypad);
   a.out = out;
   a.out_bstride = out_sample_stride;
