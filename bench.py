@@ -415,6 +415,37 @@ def setup_tokenize(pdm, torch, dev, w):
     return step, alg_bytes, flops, kept, (tables, ids, offs, weights, out, work)
 
 
+def unfused_tokenize_ms(pdm, torch, keep, w, reps: int = 20) -> float:
+    """The same S-tokens the reference's way on this GPU: the S-token gather to [B, S, 384] bf16, then per pool
+    torch bf16 Linear (+bias), exact GELU, Linear (+bias) and + pos_emb in fp32, concatenated (reported beside
+    the fused call, not the bench value)."""
+    import torch.nn.functional as Fn
+
+    tables, ids, offs, weights, _, _ = keep
+    S = sum(w.max_len)
+
+    def run():
+        raw, _ = pdm.ops.seq_gather_raw(tables, ids, offs, w.max_len)
+        parts, s0 = [], 0
+        for p, L in enumerate(w.max_len):
+            wt = weights[p]
+            hdn = Fn.gelu(Fn.linear(raw[:, s0:s0 + L], wt["w1"], wt["b1"]))
+            parts.append(Fn.linear(hdn, wt["w2"], wt["b2"]).float() + wt["pos"][:L])
+            s0 += L
+        return torch.cat(parts, dim=1)
+
+    for _ in range(3):
+        run()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        run()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / reps
+
+
 def cpu_tokenize(w, threads: int, batch: int, row_cap: int):
     """The oracle (C gather + PyTorch-CPU tokenizer in autocast emulation) on the first ``batch`` samples."""
     import torch
@@ -557,6 +588,7 @@ def main() -> int:
                "tokenizer": {"raw_dim": sum(w.table_dims), "d_model": TOK_D, "pos_rows": TOK_POS_ROWS},
                "out": [w.batch, S, TOK_D], "mlp_gflop_per_step": round(flops / 1e9, 2),
                "timed": "whole fused call (list build, MLP over kept events, padding fill)"}
+        cfg["unfused_same_gpu_ms"] = round(unfused_tokenize_ms(pdm, torch, keep, w), 4)
         cpu_b, cpu_cap = 256, 250_000
 
         def cpu_fn():

@@ -9,8 +9,8 @@ from . import _lib
 from .embedding import (DataType, EmbeddingBagCollection, EmbeddingBagConfig, EmbeddingCollection,
                         EmbeddingConfig, EmbeddingTableConfig, PoolingType, SequenceGather, TorchRecEmbeddings)
 from .kjt import JaggedTensor, KeyedJaggedTensor, KeyedTensor
-from .onetrans import (MixedAttention, MixedFFN, OneTransBlock, OneTransStack, RMSNorm, build_pyramid_mask,
-                       pyramid_schedule)
+from .onetrans import (FusedSequenceTokenizer, MixedAttention, MixedFFN, OneTransBlock, OneTransStack, RMSNorm,
+                       SequentialTokenizer, build_pyramid_mask, pyramid_schedule)
 from . import ops
 from . import hashing
 from .optim import EmbOptimType, FusedEmbeddingOptimizer, RowWiseAdagrad, WeightDecayMode
@@ -19,6 +19,7 @@ __all__ = [
     "DataType", "EmbeddingBagCollection", "EmbeddingBagConfig", "EmbeddingCollection", "EmbeddingConfig",
     "EmbeddingTableConfig", "PoolingType", "SequenceGather", "TorchRecEmbeddings", "JaggedTensor",
     "KeyedJaggedTensor", "KeyedTensor", "MixedAttention", "MixedFFN", "OneTransBlock", "OneTransStack",
+    "SequentialTokenizer", "FusedSequenceTokenizer",
     "RMSNorm", "build_pyramid_mask", "pyramid_schedule", "ops", "hashing", "EmbOptimType",
     "FusedEmbeddingOptimizer", "RowWiseAdagrad", "WeightDecayMode",
 ]

@@ -12,14 +12,21 @@ kernels in the numerics the reference gets under ``autocast(bf16)``
 accumulation, fp32 RMSNorm, exact-erf GELU, fp32 residual stream.
 
 ``pyramid_schedule`` and ``build_pyramid_mask`` restate onetrans.py:50-67.
+
+``SequentialTokenizer(raw_dim, d_model, max_len, use_pos_embed)`` follows
+onetrans.py:238-257 (``proj.0`` / ``proj.2`` Linear layers, ``pos_emb``); its
+forward and ``FusedSequenceTokenizer`` (the S-token construction of
+onetrans.py:553-558 straight from the sequence ids) run the fused gather +
+tokenizer kernel with the same autocast numerics.
 """
 from __future__ import annotations
 
-from typing import List, Optional, Sequence
+from typing import Dict, List, Optional, Sequence, Tuple
 
 import torch
 import torch.nn as nn
 
+from . import _lib as L
 from . import ops
 
 
@@ -158,3 +165,90 @@ class OneTransStack(nn.Module):
             mask = build_pyramid_mask(q_len, kv_len, x.device)
             x = block(x, mask=mask, q_len=q_len, n_s_tokens=kv_len - self.n_ns)
         return x
+
+
+class SequentialTokenizer(nn.Module):
+    """Per-position history embeddings -> S-tokens (onetrans.py:238-257): ``proj`` = Linear(raw_dim, d_model),
+    GELU, Linear(d_model, d_model), plus ``pos_emb(arange(L))`` when ``use_pos_embed``.
+
+    ``forward(raw)`` takes raw ``[B, L, raw_dim]`` (fp32 or bf16) and returns fp32 ``[B, L, d_model]``: the
+    reference's result under ``autocast(bf16)``.  The rows of ``raw`` are fed to the fused kernel as a table
+    read in order.  Forward only; raw_dim in {128, 192, 256, 384}, d_model in {128, 256}."""
+
+    def __init__(self, raw_dim: int, d_model: int, max_len: int = 1024, use_pos_embed: bool = True):
+        super().__init__()
+        self.proj = nn.Sequential(nn.Linear(raw_dim, d_model), nn.GELU(), nn.Linear(d_model, d_model))
+        self.pos_emb = nn.Embedding(max_len, d_model) if use_pos_embed else None
+        self._cache: Optional[tuple] = None
+
+    def kernel_weights(self) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, Optional[torch.Tensor]]:
+        """(w1, b1, w2, b2) as bf16 (autocast's casts, made once per parameter version) and the fp32 positions."""
+        lin1, lin2 = self.proj[0], self.proj[2]
+        params = (lin1.weight, lin1.bias, lin2.weight, lin2.bias)
+        key = tuple((t.data_ptr(), t._version, t.device) for t in params)
+        if self._cache is None or self._cache[0] != key:
+            self._cache = (key, tuple(t.detach().to(torch.bfloat16).contiguous() for t in params))
+        pos = None if self.pos_emb is None else self.pos_emb.weight.detach().float().contiguous()
+        return (*self._cache[1], pos)
+
+    def forward(self, raw: torch.Tensor) -> torch.Tensor:
+        if raw.dim() != 3:
+            raise ValueError("raw must be [B, L, raw_dim]")
+        B, Lq, K = raw.shape
+        if raw.dtype not in (torch.float32, torch.bfloat16):
+            raise TypeError("raw must be fp32 or bf16")
+        table = raw.reshape(B * Lq, K).contiguous()
+        ids = torch.arange(B * Lq, dtype=torch.int64, device=raw.device)
+        offsets = torch.arange(0, B * Lq + 1, max(Lq, 1), dtype=torch.int64, device=raw.device)[:B + 1]
+        if Lq == 0:
+            offsets = torch.zeros(B + 1, dtype=torch.int64, device=raw.device)
+        w1, b1, w2, b2, pos = self.kernel_weights()
+        out, _ = torch.ops.pdm.seq_tokenize_fwd([table], [ids], [offsets], [Lq], [w1], [b1], [w2], [b2], [pos],
+                                                L.PDM_PAD_ROW0, L.PDM_ALIGN_RIGHT)
+        return out
+
+
+class FusedSequenceTokenizer(nn.Module):
+    """The S-tokens of OneTransModel._backbone (onetrans.py:553-558) from the sequence ids: the padded gather of
+    ``gather`` (a SequenceGather) and ``tokenizers[pool]`` (SequentialTokenizer modules, e.g. the reference's
+    ``seq_tokenizers`` ModuleDict) fused, so the ``[B, S, sum D]`` raw rows never reach memory.
+
+    ``forward(batch)`` takes the SequenceGather batch convention and returns (tokens fp32 ``[B, S, d_model]``,
+    mask bool ``[B, S]``); the pools' tokens are concatenated along the sequence in the gather's pool order.
+    With ``out`` given (fp32 ``[B, >= S, d_model]`` with contiguous rows, e.g. the leading rows of the block
+    input) the tokens are written there.  Forward only."""
+
+    def __init__(self, gather, tokenizers: Dict[str, SequentialTokenizer]):
+        super().__init__()
+        self.gather = gather
+        self.tokenizers = tokenizers if isinstance(tokenizers, nn.ModuleDict) else nn.ModuleDict(tokenizers)
+        missing = [g for g in gather.groups if g not in self.tokenizers]
+        if missing:
+            raise ValueError(f"no tokenizer for pools {missing}")
+
+    def forward(self, batch: Dict[str, torch.Tensor], out: Optional[torch.Tensor] = None
+                ) -> Tuple[torch.Tensor, torch.Tensor]:
+        g = self.gather
+        ec = g.ec
+        tables = [ec._store.weight(ec._tables[ti].name) for ti in g._feature_tables]
+        ids, offsets, max_len = [], [], []
+        w = {k: [] for k in ("w1", "b1", "w2", "b2", "pos")}
+        for name, fs in g.groups.items():
+            lengths = batch[fs[0] + "__lengths"]
+            off = torch.zeros(lengths.numel() + 1, dtype=torch.int64, device=lengths.device)
+            torch.cumsum(lengths.to(torch.int64), 0, out=off[1:])
+            offsets.append(off)
+            ids.extend(batch[f].reshape(-1).to(torch.int64).contiguous() for f in fs)
+            max_len.append(g.max_len[name])
+            for k, t in zip(("w1", "b1", "w2", "b2", "pos"), self.tokenizers[name].kernel_weights()):
+                w[k].append(t)
+        if out is None:
+            tokens, mask = torch.ops.pdm.seq_tokenize_fwd(tables, ids, offsets, max_len, w["w1"], w["b1"], w["w2"],
+                                                          w["b2"], w["pos"], g.pad_mode, g.align)
+            return tokens, mask.view(torch.bool)
+        F = len(tables)
+        grid = [ids[p * F:(p + 1) * F] for p in range(len(offsets))]
+        weights = [dict(w1=w["w1"][p], b1=w["b1"][p], w2=w["w2"][p], b2=w["b2"][p], pos=w["pos"][p])
+                   for p in range(len(offsets))]
+        tokens, mask = ops.seq_tokenize_raw(tables, grid, offsets, max_len, weights, g.pad_mode, g.align, out=out)
+        return tokens, mask.view(torch.bool)

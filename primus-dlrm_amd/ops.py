@@ -531,6 +531,27 @@ def _(tables, ids, offsets, max_len, pad_mode, align):
     return (tables[0].new_empty((B, S, D)), tables[0].new_empty((B, S), dtype=torch.uint8))
 
 
+@torch.library.custom_op("pdm::seq_tokenize_fwd", mutates_args=())
+def seq_tokenize_fwd(tables: List[torch.Tensor], ids: List[torch.Tensor], offsets: List[torch.Tensor],
+                     max_len: List[int], w1: List[torch.Tensor], b1: List[torch.Tensor], w2: List[torch.Tensor],
+                     b2: List[torch.Tensor], pos: List[Optional[torch.Tensor]], pad_mode: int,
+                     align: int) -> Tuple[torch.Tensor, torch.Tensor]:
+    """S-token gather fused with one SequentialTokenizer per pool (bf16 weights, fp32 positions or None);
+    ``ids`` is pool-major as for ``seq_gather_fwd``.  Returns (fp32 tokens [B, S, d], mask uint8 [B, S])."""
+    F = len(tables)
+    grid = [ids[p * F:(p + 1) * F] for p in range(len(offsets))]
+    weights = [dict(w1=w1[p], b1=b1[p], w2=w2[p], b2=b2[p], pos=pos[p]) for p in range(len(offsets))]
+    return seq_tokenize_raw(tables, grid, offsets, max_len, weights, pad_mode, align, want_mask=True)
+
+
+@seq_tokenize_fwd.register_fake
+def _(tables, ids, offsets, max_len, w1, b1, w2, b2, pos, pad_mode, align):
+    B = offsets[0].shape[0] - 1
+    S = sum(max_len)
+    d = w1[0].shape[0]
+    return (tables[0].new_empty((B, S, d), dtype=torch.float32), tables[0].new_empty((B, S), dtype=torch.uint8))
+
+
 # ---------------------------------------------------------------------------
 # OneTrans block
 # ---------------------------------------------------------------------------

@@ -196,3 +196,66 @@ def test_unsupported_width_is_an_error(pdm, dev):
     wd = [{k: (v.to(torch.bfloat16) if k != "pos" else v).contiguous().to(dev) for k, v in w.items()}]
     with pytest.raises(pdm._lib.PdmError):
         pdm.ops.seq_tokenize_raw(tabs, ids, offs, [4], wd)
+
+
+def _module_weights(tok):
+    """The oracle's weight dict from a SequentialTokenizer module (fp32 parameters; the oracle rounds to bf16)."""
+    return {"w1": tok.proj[0].weight.detach().cpu(), "b1": tok.proj[0].bias.detach().cpu(),
+            "w2": tok.proj[2].weight.detach().cpu(), "b2": tok.proj[2].bias.detach().cpu(),
+            "pos": None if tok.pos_emb is None else tok.pos_emb.weight.detach().cpu()}
+
+
+@pytest.mark.parametrize("raw_dtype", [torch.float32, torch.bfloat16])
+def test_sequential_tokenizer_module(pdm, dev, raw_dtype):
+    """SequentialTokenizer.forward(raw) (onetrans.py:250-257) against the oracle on the module's parameters."""
+    torch.manual_seed(3)
+    tok = pdm.SequentialTokenizer(384, 256, max_len=64).to(dev)
+    raw = torch.randn(5, 37, 384, device=dev).to(raw_dtype)
+    got = tok(raw)
+    assert got.dtype == torch.float32 and got.shape == (5, 37, 256)
+    w = _module_weights(tok)
+    num = ot._Num("autocast")
+    rawc = raw.float().cpu()
+    want = ot.sequential_tokenizer(rawc, w)
+    h = num.round(torch.nn.functional.gelu(ot._lin_bias(rawc, w["w1"], w["b1"], num)))
+    y = ot._lin_bias(h, w["w2"], w["b2"], num)
+    mag = y.abs() + h.abs() @ num.round(w["w2"]).abs().T
+    diff = (got.cpu() - want).abs()
+    assert bool((diff <= 2.0 ** -7 * mag + 1e-6).all())
+    assert (diff > 0).float().mean().item() < 0.02
+
+
+def test_fused_sequence_tokenizer_module(pdm, dev):
+    """FusedSequenceTokenizer (gather + per-pool tokenizers fused) equals SequenceGather followed by the
+    SequentialTokenizer modules bit for bit (the same kernel arithmetic per token), and the oracle within
+    the bf16 tolerance."""
+    g = np.random.default_rng(21)
+    tables = [pdm.EmbeddingConfig(1000, 128, "item", pdm.DataType.BF16, ["lp_item", "like_item"]),
+              pdm.EmbeddingConfig(100, 64, "artist", pdm.DataType.BF16, ["lp_artist", "like_artist"])]
+    ec = pdm.EmbeddingCollection(tables, device=dev)
+    B = 23
+    lens_lp, lens_like = g.integers(0, 30, B), g.integers(0, 9, B)
+    lp_items, like_items = g.integers(0, 1000, lens_lp.sum()), g.integers(0, 1000, lens_like.sum())
+    batch = {"lp_item": lp_items, "lp_artist": lp_items % 100, "like_item": like_items,
+             "like_artist": like_items % 100, "lp_item__lengths": lens_lp, "like_item__lengths": lens_like}
+    batch = {k: torch.from_numpy(np.asarray(v)).to(dev) for k, v in batch.items()}
+    sg = pdm.SequenceGather(ec, {"lp": ["lp_item", "lp_artist"], "like": ["like_item", "like_artist"]},
+                            {"lp": 24, "like": 8})
+    torch.manual_seed(5)
+    toks = torch.nn.ModuleDict({"lp": pdm.SequentialTokenizer(192, 128, max_len=32),
+                                "like": pdm.SequentialTokenizer(192, 128, max_len=32, use_pos_embed=False)}).to(dev)
+    fused = pdm.FusedSequenceTokenizer(sg, toks)
+    with torch.no_grad():
+        tokens, mask = fused(batch)
+        raw, mask2 = sg(batch)
+        want = torch.cat([toks["lp"](raw[:, :24]), toks["like"](raw[:, 24:])], dim=1)
+    torch.cuda.synchronize()
+    assert torch.equal(mask, mask2)
+    assert torch.equal(tokens, want)
+    # and the oracle, through the C gather and the torch restatement
+    tabs = [o.table_bytes(ec.embeddings[n].weight.detach().cpu()).view(np.uint16).reshape(r, d)
+            for n, r, d in (("item", 1000, 128), ("artist", 100, 64))]
+    ids = [[lp_items, lp_items % 100], [like_items, like_items % 100]]
+    offs = [o.offsets_np(lens_lp), o.offsets_np(lens_like)]
+    _check(tokens.cpu(), tabs, ids, offs, [24, 8], [_module_weights(toks["lp"]), _module_weights(toks["like"])],
+           0, 0, mask.to(torch.uint8))
