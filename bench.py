@@ -10,6 +10,8 @@ fp32 out).  ``--workload`` selects another:
   seq_gather  3 behaviour pools, item 10M x 256 + artist 1M x 64 + album 2M x 64 bf16, B=1024
   seq_tokenize  the seq_gather workload fused with one SequentialTokenizer per pool (Linear 384 -> 256,
               GELU, Linear 256 -> 256, + pos_emb of 2048 x 256 fp32), fp32 S-tokens [1024, 768, 256]
+  ns_tokenize NS tokens: uid/item/artist/album rows (1M/9.4M/1.3M/3.4M x 64 bf16) + dense parts 64/6/6/64 -> 396
+              wide NS input -> AutoSplitTokenizer Linear(396, 4096) + GELU + Linear(4096, 4096), B=1024
   onetrans    4-layer OneTrans block stack, B=1024, 384 S + 16 NS tokens, d 256, schedule 384/256/128/64
   cross_hash  cross-feature ids: xxHash64 of (uid, artist_id) int64 pairs % 100,000,000, 16,777,216 rows
   train_adam  pooled backward + fused Adam (lr 1e-2, eps 1e-8, wd 1e-5): 8 tables x 10,000,000 x 64 fp32,
@@ -465,6 +467,79 @@ def cpu_tokenize(w, threads: int, batch: int, row_cap: int):
 
 
 # ----------------------------------------------------------------------------------------------
+# NS tokens (scalar-feature rows + dense parts through the AutoSplitTokenizer)
+# ----------------------------------------------------------------------------------------------
+
+NS_TABLES = [("uid", 1_000_001), ("item", 9_390_624), ("artist", 1_293_395), ("album", 3_367_692)]
+NS_DIM, NS_DENSE, NS_D, NS_N = 64, [64, 6, 6, 64], 256, 16
+
+
+def setup_ns(pdm, torch, dev, batch: int):
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(1011)
+    tables = []
+    for _, rows in NS_TABLES:
+        t = torch.empty((rows, NS_DIM), dtype=torch.bfloat16, device=dev)
+        for r0 in range(0, rows, 1 << 21):
+            n = min(1 << 21, rows - r0)
+            t[r0:r0 + n].copy_(torch.empty((n, NS_DIM), device=dev).uniform_(-0.05, 0.05, generator=gen))
+        tables.append(t)
+    rng = np.random.default_rng(1012)
+    ids = [torch.from_numpy(rng.integers(0, rows, batch)).to(dev) for _, rows in NS_TABLES]
+    dense = [torch.randn(batch, d, device=dev, generator=gen) for d in NS_DENSE]
+    K, N = NS_DIM * len(NS_TABLES) + sum(NS_DENSE), NS_D * NS_N
+    bf = lambda *shape: (torch.randn(*shape, device=dev, generator=gen) * 0.02).to(torch.bfloat16)  # noqa: E731
+    w1, b1, w2, b2 = bf(N, K), bf(N), bf(N, N), bf(N)
+    out = torch.empty(batch, NS_N, NS_D, device=dev)
+    ws = torch.empty(64 << 20, dtype=torch.uint8, device=dev)
+
+    def step():
+        pdm.ops.ns_tokenize_raw(tables, ids, dense, w1, b1, w2, b2, NS_N, out=out, workspace=ws)
+
+    flops = 2.0 * batch * (K * N + N * N)
+    return step, flops, K, N, (tables, ids, dense, w1, b1, w2, b2, out, ws)
+
+
+def unfused_ns_ms(pdm, torch, keep, reps: int = 20) -> float:
+    """The same NS tokens the reference's way on this GPU: row lookups + cat to [B, 396] bf16, then torch bf16
+    F.linear + bias, F.gelu, F.linear + bias, viewed [B, n_ns, d] and converted to fp32 (reported beside the
+    fused call)."""
+    import torch.nn.functional as Fn
+
+    tables, ids, dense, w1, b1, w2, b2, _, _ = keep
+
+    def run():
+        raw = torch.cat([t[i] for t, i in zip(tables, ids)] + [x.to(torch.bfloat16) for x in dense], dim=1)
+        hdn = Fn.gelu(Fn.linear(raw, w1, b1))
+        return Fn.linear(hdn, w2, b2).view(raw.shape[0], NS_N, NS_D).float()
+
+    for _ in range(3):
+        run()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        run()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / reps
+
+
+def cpu_ns(threads: int, batch: int):
+    import torch
+    from oracle import onetrans as ot
+
+    torch.set_num_threads(threads)
+    g = np.random.default_rng(7)
+    K, N = NS_DIM * len(NS_TABLES) + sum(NS_DENSE), NS_D * NS_N
+    tabs = [g.normal(0, 0.05, (100_000, NS_DIM)).astype(np.float32) for _ in NS_TABLES]
+    ids = [g.integers(0, 100_000, batch) for _ in NS_TABLES]
+    dense = [g.normal(0, 1, (batch, d)).astype(np.float32) for d in NS_DENSE]
+    w = ot.random_autosplit_weights(K, N, std=0.02, seed=3)
+    return time_cpu(lambda: ot.ns_tokenize(tabs, ids, dense, w, NS_N), reps=3)
+
+
+# ----------------------------------------------------------------------------------------------
 # OneTrans block stack
 # ----------------------------------------------------------------------------------------------
 
@@ -523,7 +598,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="single_hot",
-                    choices=["single_hot", "ebc_fp32", "int8_mean", "seq_gather", "seq_tokenize", "onetrans",
+                    choices=["single_hot", "ebc_fp32", "int8_mean", "seq_gather", "seq_tokenize", "ns_tokenize",
+                             "onetrans",
                              "cross_hash",
                              "train_adam", "train_rowwise_adagrad", "train_seq_adam", "kjt_build", "copy_1gib"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -597,6 +673,22 @@ def main() -> int:
                     "sample": f"oracle (C gather + PyTorch-CPU tokenizers, autocast emulation) on the first {cpu_b} "
                               f"samples ({cpu_b * S} slots), tables capped at {cpu_cap} rows (ids modulo), "
                               f"median of 3 reps = {sec:.3f} s"}
+    elif args.workload == "ns_tokenize":
+        B_ = 1024
+        step, alg, K_, N_, keep = setup_ns(pdm, torch, dev, B_)
+        units, unit, bound, dtype = B_, "samples/s", "mfma", "bf16"
+        cfg = {"workload": "ns_tokens_b1024_k396_n4096", "batch": B_,
+               "scalar_tables": {n: r for n, r in NS_TABLES}, "scalar_dim": NS_DIM, "dense_dims": NS_DENSE,
+               "ns_input": K_, "d_model": NS_D, "n_ns": NS_N, "gflop_per_step": round(alg / 1e9, 2),
+               "timed": "whole call (NS rows gather, W1 padding copy, Linear 1 + bias + GELU, Linear 2 + bias)"}
+        cfg["unfused_same_gpu_ms"] = round(unfused_ns_ms(pdm, torch, keep), 4)
+        cpu_b = 1024
+
+        def cpu_fn():
+            sec = cpu_ns(threads, cpu_b)
+            return {"value": round(cpu_b / sec, 1), "unit": unit, "cores": threads, "kind": "port",
+                    "sample": f"oracle (numpy row gather + PyTorch-CPU AutoSplitTokenizer, autocast emulation) at "
+                              f"batch {cpu_b}, tables of 100,000 rows, median of 3 reps = {sec:.3f} s"}
     elif args.workload == "cross_hash":
         # user_x_artist cross ids (config.py:151): one (uid, artist_id) pair per row, 100M buckets, salt 0
         n_rows, table_size = 1 << 24, 100_000_000

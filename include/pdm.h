@@ -371,6 +371,50 @@ int pdm_onetrans_block_fwd(const pdm_block_desc* desc, const float* x,
                            void* workspace, int64_t workspace_bytes,
                            pdm_stream_t stream);
 
+/* NS-token construction: OneTransModel._build_ns_raw
+ * (primus_dlrm/models/onetrans.py:522-532) + AutoSplitTokenizer
+ * (onetrans.py:260-276), used at onetrans.py:561-563, under autocast(bf16):
+ *   raw[b] = concat(table_f[ids_f[b]] for the scalar features,
+ *                   dense_j[b] for the dense parts)            (bf16)
+ *   h[b]   = bf16(gelu(bf16(raw[b] . W1^T + b1)))             (N = d * n_ns)
+ *   out[b] = float(bf16(h[b] . W2^T + b2)), viewed as [n_ns, d] rows
+ * The dense parts are given as computed (the reference's projections
+ * dense_projs[name](batch[name]) run before, or the raw feature).
+ * ------------------------------------------------------------------------ */
+
+#define PDM_NS_MAX_PARTS 8
+
+typedef struct {
+  int32_t num_scalar;   /* scalar feature tables (0..8) */
+  int32_t num_dense;    /* dense parts (0..8) */
+  int32_t table_dtype;  /* PDM_F32 | PDM_BF16 (all scalar tables) */
+  int32_t n_out;        /* N = d_model * n_ns, a multiple of 64 */
+  int64_t batch_size;
+  int32_t scalar_dim[PDM_NS_MAX_PARTS]; /* >= 1 */
+  int64_t scalar_rows[PDM_NS_MAX_PARTS];
+  int32_t dense_dim[PDM_NS_MAX_PARTS];  /* any >= 1 */
+} pdm_ns_desc;
+
+/* Bytes of device workspace pdm_ns_tokenize_fwd needs. */
+int64_t pdm_ns_tokenize_workspace_size(const pdm_ns_desc* desc);
+
+/* tables / ids: [num_scalar] device pointers, ids int64 [B] each (one id per
+ * sample; an id outside the table reads zeros and sets err_flag);
+ * dense: [num_dense] device pointers to fp32 [B, dense_dim] rows (row stride
+ * dense_stride[j] floats); w1 bf16 [N, K] (K = sum of the dims, in the order
+ * above), b1 bf16 [N], w2 bf16 [N, N], b2 bf16 [N]; out fp32, sample b's N
+ * values at out + b * out_sample_stride (e.g. the n_ns NS rows of the block
+ * input).  workspace: 256-byte aligned, pdm_ns_tokenize_workspace_size bytes,
+ * no initialisation needed. */
+int pdm_ns_tokenize_fwd(const pdm_ns_desc* desc, const void* const* tables,
+                        const int64_t* const* ids, const float* const* dense,
+                        const int64_t* dense_stride, const uint16_t* w1,
+                        const uint16_t* b1, const uint16_t* w2,
+                        const uint16_t* b2, float* out,
+                        int64_t out_sample_stride, void* workspace,
+                        int64_t workspace_bytes, int32_t* err_flag,
+                        pdm_stream_t stream);
+
 /* ------------------------------------------------------------------------
  * KeyedJaggedTensor construction on the device (no host synchronisation).
  *

@@ -11,6 +11,10 @@ Restates primus_dlrm/models/onetrans.py in PyTorch on the CPU:
                          MixedAttention.forward :124-169 and MixedFFN.forward :195-204
 * ``sequential_tokenizer`` SequentialTokenizer.forward onetrans.py:250-257 (Linear, exact GELU,
                          Linear, + pos_emb(arange(L)))
+* ``autosplit_tokenizer`` AutoSplitTokenizer.forward onetrans.py:260-276 (Linear, exact GELU, Linear,
+                         view [B, n_ns, d])
+* ``ns_tokenize``        OneTransModel._build_ns_raw onetrans.py:522-532 (scalar rows, then dense parts)
+                         followed by the AutoSplitTokenizer (onetrans.py:561-563)
 * ``seq_tokenize``       the S-token construction of OneTransModel._backbone onetrans.py:553-558:
                          per-pool gather (onetrans.py:515-520, the sequence gather of oracle.py),
                          tokenizer, concatenation along the sequence
@@ -223,3 +227,40 @@ def random_tokenizer_weights(K: int, d: int, max_len: int, std: float = 0.05, se
     r = lambda *shape: _bf16(torch.randn(*shape, generator=g) * std)  # noqa: E731
     return {"w1": r(d, K), "b1": r(d), "w2": r(d, d), "b2": r(d),
             "pos": torch.randn(max_len, d, generator=g) if pos else None}
+
+
+def autosplit_tokenizer(ns_raw: torch.Tensor, w: Dict[str, torch.Tensor], n_ns: int,
+                        mode: str = "autocast") -> torch.Tensor:
+    """AutoSplitTokenizer.forward (onetrans.py:260-276) for ns_raw [B, K]: proj = Linear(K, d*n_ns), GELU,
+    Linear(d*n_ns, d*n_ns), viewed as [B, n_ns, d] (bf16 values as float32 in autocast mode)."""
+    num = _Num(mode)
+    h = num.round(torch.nn.functional.gelu(_lin_bias(ns_raw.to(num.dt), w["w1"], w["b1"], num)))
+    y = _lin_bias(h, w["w2"], w["b2"], num)
+    return y.view(y.shape[0], n_ns, -1)
+
+
+def ns_tokenize(tables, ids, dense, w: Dict[str, torch.Tensor], n_ns: int, mode: str = "autocast"):
+    """NS tokens from the scalar-feature rows ``tables[j][ids[j]]`` (numpy uint16 bf16 bits or float32; an id
+    outside the table gives a zero row) and the float32 ``dense`` parts [B, dim], concatenated in that order
+    (onetrans.py:522-532), through the AutoSplitTokenizer."""
+    import numpy as np
+
+    parts = []
+    for t, i in zip(tables, ids):
+        t = np.ascontiguousarray(t)
+        if t.dtype == np.uint16:
+            t = (t.astype(np.uint32) << 16).view(np.float32)
+        i = np.asarray(i, dtype=np.int64)
+        ok = (i >= 0) & (i < t.shape[0])
+        rows = t[np.where(ok, i, 0)].copy()
+        rows[~ok] = 0
+        parts.append(torch.from_numpy(rows))
+    parts += [torch.as_tensor(np.asarray(x, dtype=np.float32)) for x in dense]
+    return autosplit_tokenizer(torch.cat(parts, dim=1), w, n_ns, mode)
+
+
+def random_autosplit_weights(K: int, N: int, std: float = 0.05, seed: int = 0) -> Dict[str, torch.Tensor]:
+    """bf16-representable N(0, std) AutoSplitTokenizer weights and biases (fp32 storage)."""
+    g = torch.Generator().manual_seed(seed)
+    r = lambda *shape: _bf16(torch.randn(*shape, generator=g) * std)  # noqa: E731
+    return {"w1": r(N, K), "b1": r(N), "w2": r(N, N), "b2": r(N)}

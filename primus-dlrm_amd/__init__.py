@@ -9,7 +9,7 @@ from . import _lib
 from .embedding import (DataType, EmbeddingBagCollection, EmbeddingBagConfig, EmbeddingCollection,
                         EmbeddingConfig, EmbeddingTableConfig, PoolingType, SequenceGather, TorchRecEmbeddings)
 from .kjt import JaggedTensor, KeyedJaggedTensor, KeyedTensor
-from .onetrans import (FusedSequenceTokenizer, MixedAttention, MixedFFN, OneTransBlock, OneTransStack, RMSNorm,
+from .onetrans import (AutoSplitTokenizer, FusedNSTokenizer, FusedSequenceTokenizer, MixedAttention, MixedFFN, OneTransBlock, OneTransStack, RMSNorm,
                        SequentialTokenizer, build_pyramid_mask, pyramid_schedule)
 from . import ops
 from . import hashing
@@ -19,7 +19,7 @@ __all__ = [
     "DataType", "EmbeddingBagCollection", "EmbeddingBagConfig", "EmbeddingCollection", "EmbeddingConfig",
     "EmbeddingTableConfig", "PoolingType", "SequenceGather", "TorchRecEmbeddings", "JaggedTensor",
     "KeyedJaggedTensor", "KeyedTensor", "MixedAttention", "MixedFFN", "OneTransBlock", "OneTransStack",
-    "SequentialTokenizer", "FusedSequenceTokenizer",
+    "SequentialTokenizer", "FusedSequenceTokenizer", "AutoSplitTokenizer", "FusedNSTokenizer",
     "RMSNorm", "build_pyramid_mask", "pyramid_schedule", "ops", "hashing", "EmbOptimType",
     "FusedEmbeddingOptimizer", "RowWiseAdagrad", "WeightDecayMode",
 ]

@@ -53,6 +53,8 @@ EXPORTED_SYMBOLS = (
     "pdm_seq_tokenize_workspace_size",
     "pdm_seq_tokenize_fwd",
     "pdm_cross_hash_fwd",
+    "pdm_ns_tokenize_workspace_size",
+    "pdm_ns_tokenize_fwd",
     "pdm_onetrans_block_workspace_size",
     "pdm_onetrans_block_fwd",
 )
@@ -106,6 +108,23 @@ class SeqDesc(ctypes.Structure):
         ("dim", ctypes.c_int32 * PDM_SEQ_MAX_FEATURES),
         ("rows", ctypes.c_int64 * PDM_SEQ_MAX_FEATURES),
         ("num_ids", ctypes.c_int64 * PDM_SEQ_MAX_POOLS),
+    ]
+
+
+PDM_NS_MAX_PARTS = 8
+
+
+class NsDesc(ctypes.Structure):
+    """pdm_ns_desc: the NS input parts (scalar-feature tables, dense parts) and the tokenizer width."""
+    _fields_ = [
+        ("num_scalar", ctypes.c_int32),
+        ("num_dense", ctypes.c_int32),
+        ("table_dtype", ctypes.c_int32),
+        ("n_out", ctypes.c_int32),
+        ("batch_size", ctypes.c_int64),
+        ("scalar_dim", ctypes.c_int32 * PDM_NS_MAX_PARTS),
+        ("scalar_rows", ctypes.c_int64 * PDM_NS_MAX_PARTS),
+        ("dense_dim", ctypes.c_int32 * PDM_NS_MAX_PARTS),
     ]
 
 
@@ -177,6 +196,12 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.pdm_seq_tokenize_fwd.argtypes = [ctypes.POINTER(SeqDesc), ctypes.POINTER(vp), ctypes.POINTER(vp),
                                          ctypes.POINTER(vp), ctypes.POINTER(TokenizerWeights), i32, vp, i64, vp, vp,
                                          i64, vp, vp]
+    lib.pdm_ns_tokenize_workspace_size.restype = i64
+    lib.pdm_ns_tokenize_workspace_size.argtypes = [ctypes.POINTER(NsDesc)]
+    lib.pdm_ns_tokenize_fwd.restype = ctypes.c_int
+    lib.pdm_ns_tokenize_fwd.argtypes = [ctypes.POINTER(NsDesc), ctypes.POINTER(vp), ctypes.POINTER(vp),
+                                        ctypes.POINTER(vp), ctypes.POINTER(i64), vp, vp, vp, vp, vp, i64, vp, i64,
+                                        vp, vp]
     lib.pdm_onetrans_block_workspace_size.restype = i64
     lib.pdm_onetrans_block_workspace_size.argtypes = [ctypes.POINTER(BlockDesc)]
     lib.pdm_onetrans_block_fwd.restype = ctypes.c_int

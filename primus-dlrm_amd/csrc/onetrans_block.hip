@@ -89,7 +89,7 @@ __global__ __launch_bounds__(256) void rmsnorm_bf16_kernel(const float* __restri
 // ---------------------------------------------------------------------------
 // Grouped GEMM  C = A . W^T  over (sample, token) rows.
 // ---------------------------------------------------------------------------
-enum { EPI_BF16 = 0, EPI_QKV = 1, EPI_RESID = 2, EPI_GELU = 3 };
+enum { EPI_BF16 = 0, EPI_QKV = 1, EPI_RESID = 2, EPI_GELU = 3, EPI_BIAS_GELU = 4, EPI_BIAS_F32 = 5 };
 
 constexpr int GBM = 128, GBN = 128, GBK = 64, GPAD = 8;
 
@@ -122,6 +122,7 @@ struct GemmArgs {
   const float* norm_w;
   const uint16_t* W2;     // FFN-down [D, F] shared
   const uint16_t* W2_ns;  // [n_ns, D, F]
+  const uint16_t* bias;   // EPI_BIAS_*: bf16 [N]
 };
 
 // Stores one GEMM output element (b, t, n) with the epilogue EPI.
@@ -133,6 +134,15 @@ __device__ __forceinline__ void epilogue_store(const GemmArgs& a, int b, int t, 
   } else if constexpr (EPI == EPI_GELU) {
     reinterpret_cast<uint16_t*>(a.out)[(int64_t)b * a.out_bstride + (int64_t)t * a.N + n] =
         (uint16_t)bf16_bits(gelu_erf(bf16_round(v)));
+  } else if constexpr (EPI == EPI_BIAS_GELU) {
+    // autocast Linear with bias (one rounding after the bias), then GELU on the bf16 value, rounded to bf16
+    const float x = bf16_round(v + bf16_bits_to_f32(a.bias[n]));
+    reinterpret_cast<uint16_t*>(a.out)[(int64_t)b * a.out_bstride + (int64_t)t * a.N + n] =
+        (uint16_t)bf16_bits(gelu_erf(x));
+  } else if constexpr (EPI == EPI_BIAS_F32) {
+    // autocast Linear with bias, its bf16 result stored as fp32 (the promotion of the token concat)
+    reinterpret_cast<float*>(a.out)[(int64_t)b * a.out_bstride + (int64_t)t * a.N + n] =
+        bf16_round(v + bf16_bits_to_f32(a.bias[n]));
   } else if constexpr (EPI == EPI_RESID) {
     const float r = a.res[(int64_t)b * a.res_bstride + (int64_t)(t + a.res_toff) * a.N + n];
     reinterpret_cast<float*>(a.out)[(int64_t)b * a.out_bstride + (int64_t)t * a.N + n] = bf16_round(v) + r;
@@ -1387,4 +1397,321 @@ extern "C" int pdm_onetrans_block_fwd(const pdm_block_desc* desc, const float* x
     if ((st = launch_gemm<EPI_RESID>(g3, s)) != PDM_OK) return st;
   }
   return PDM_OK;
+}
+
+// ---------------------------------------------------------------------------
+// NS tokens: the NS input rows (scalar-feature rows and dense parts, bf16,
+// zero-padded to a multiple of 64 columns), then AutoSplitTokenizer's two
+// Linear layers on the tiled GEMM with bias epilogues.
+// ---------------------------------------------------------------------------
+namespace pdm {
+
+struct NsArgs {
+  const char* tables[PDM_NS_MAX_PARTS];
+  const int64_t* ids[PDM_NS_MAX_PARTS];
+  int64_t rows[PDM_NS_MAX_PARTS];
+  const float* dense[PDM_NS_MAX_PARTS];
+  int64_t dense_stride[PDM_NS_MAX_PARTS];
+  int32_t col[2 * PDM_NS_MAX_PARTS + 1];  // first column of part j (scalar parts, then dense parts)
+  int32_t n_scalar, n_parts, f32_tables, K, K64;
+  int64_t B;
+  uint16_t* raw;  // [B, K64] bf16
+  int32_t* err;
+};
+
+// one wave per sample: part by part, lanes over the part's columns, bf16 (round to nearest even) out
+__global__ __launch_bounds__(256) void ns_raw_kernel(NsArgs a) {
+  const int64_t b = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (b >= a.B) return;
+  uint16_t* dst = a.raw + b * a.K64;
+  bool bad = false;
+  for (int j = 0; j < a.n_parts; ++j) {
+    const int c0 = a.col[j], w = a.col[j + 1] - c0;
+    if (j < a.n_scalar) {
+      const int64_t id = a.ids[j][b];
+      const bool ok = id >= 0 && id < a.rows[j];
+      bad |= !ok;
+      if (a.f32_tables) {
+        const float* row = reinterpret_cast<const float*>(a.tables[j]) + (ok ? id : 0) * w;
+        for (int c = lane; c < w; c += 64) dst[c0 + c] = ok ? (uint16_t)f32_to_bf16_bits(row[c]) : 0;
+      } else {
+        const uint16_t* row = reinterpret_cast<const uint16_t*>(a.tables[j]) + (ok ? id : 0) * w;
+        for (int c = lane; c < w; c += 64) dst[c0 + c] = ok ? row[c] : 0;
+      }
+    } else {
+      const int d = j - a.n_scalar;
+      const float* row = a.dense[d] + b * a.dense_stride[d];
+      for (int c = lane; c < w; c += 64) dst[c0 + c] = (uint16_t)f32_to_bf16_bits(row[c]);
+    }
+  }
+  for (int c = a.K + lane; c < a.K64; c += 64) dst[c] = 0;
+  if (bad && a.err) a.err[0] = 1;
+}
+
+// W1 [N, K] -> [N, K64] with zero columns K .. K64
+__global__ __launch_bounds__(256) void ns_pad_w1_kernel(const uint16_t* __restrict__ w1, uint16_t* __restrict__ w1p,
+                                                        int N, int K, int K64) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (int64_t)N * K64) return;
+  const int n = (int)(i / K64), k = (int)(i - (int64_t)n * K64);
+  w1p[i] = k < K ? w1[(int64_t)n * K + k] : 0;
+}
+
+// Tiled GEMM for the NS tokenizer's Linear layers, C = A . W^T (+ bias epilogue), A [M, K] rows with stride
+// a_bstride, W [N, K], K a multiple of 64.  128 x 128 tiles on 4 waves (one per SIMD, 512 registers each):
+// every k step's A and W tiles are read PD steps ahead into registers (the weight tiles come from the
+// Infinity Cache or HBM, about 2 k cycles away, while a k step is about 600 cycles of MFMA work), stored
+// to one of two LDS buffers at the start of the step before their use and read back as 32x32x16 fragments.
+template <int EPI, int PD>
+__global__ __launch_bounds__(256, 1) void ns_gemm_kernel(GemmArgs a) {
+  __shared__ __attribute__((aligned(16))) uint16_t sA[2][GBM][GBK + GPAD];
+  __shared__ __attribute__((aligned(16))) uint16_t sB[2][GBN][GBK + GPAD];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  // Block ids are dealt to the 8 XCDs round robin.  With N tiles in multiples of 8, XCD x computes N tiles
+  // [x n/8, (x+1) n/8) for every M tile: its L2 holds an eighth of W and all of A, instead of all of W (which
+  // an M-tile-per-XCD order streams through every XCD).
+  const int64_t bid = blockIdx.x;
+  int mt, nt;
+  if (a.n_tiles % 8 == 0) {
+    const int per = a.n_tiles / 8;
+    const int64_t x = bid & 7, j = bid >> 3;  // j-th block of XCD x
+    mt = (int)(j % a.tiles_s);
+    nt = (int)(x * per + j / a.tiles_s);
+  } else {
+    mt = (int)(bid / a.n_tiles);
+    nt = (int)(bid - (int64_t)mt * a.n_tiles);
+  }
+  const int m0 = mt * GBM;
+  const int n0 = nt * GBN;
+  const int M = a.B;
+
+  const int lr = tid >> 3, lc = (tid & 7) * 8;
+  const uint16_t* arow[4];
+  const uint16_t* wrow[4];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const int m = m0 + p * 32 + lr, n = n0 + p * 32 + lr;
+    arow[p] = m < M ? a.A + (int64_t)m * a.a_bstride + lc : nullptr;
+    wrow[p] = n < a.N ? a.W + (int64_t)n * a.K + lc : nullptr;
+  }
+  u32x4_t ra[PD][4], rb[PD][4];
+  auto gload = [&](int st, int k0) {
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      ra[st][p] = arow[p] ? *reinterpret_cast<const u32x4_t*>(arow[p] + k0) : u32x4_t{0, 0, 0, 0};
+      rb[st][p] = wrow[p] ? *reinterpret_cast<const u32x4_t*>(wrow[p] + k0) : u32x4_t{0, 0, 0, 0};
+    }
+  };
+  auto sstore = [&](int st, int buf) {
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      *reinterpret_cast<u32x4_t*>(&sA[buf][p * 32 + lr][lc]) = ra[st][p];
+      *reinterpret_cast<u32x4_t*>(&sB[buf][p * 32 + lr][lc]) = rb[st][p];
+    }
+  };
+
+  f32x16_t acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+  const int nk = a.K / GBK;
+  // k step j lives in register stage j % PD until it is stored to LDS buffer j & 1 at the start of step j - 1
+#pragma unroll
+  for (int j = 0; j < PD; ++j)
+    if (j < nk) gload(j, j * GBK);
+  sstore(0, 0);
+  if (PD < nk) gload(0, PD * GBK);
+  const int fr = lane & 31, fk = (lane >> 5) * 8;
+  for (int k0 = 0; k0 < nk; k0 += PD) {
+#pragma unroll
+    for (int s = 0; s < PD; ++s) {
+      const int kt = k0 + s;
+      if (kt < nk) {
+        // every wave is done with step kt - 1, whose buffer receives step kt + 1
+        __syncthreads();
+        if (kt + 1 < nk) {
+          sstore((s + 1) % PD, (kt + 1) & 1);
+          if (kt + 1 + PD < nk) gload((s + 1) % PD, (kt + 1 + PD) * GBK);
+        }
+        const int buf = kt & 1;
+#pragma unroll
+        for (int ks = 0; ks < GBK / 16; ++ks) {
+          u32x4_t af[2], bf[2];
+#pragma unroll
+          for (int i = 0; i < 2; ++i)
+            af[i] = *reinterpret_cast<const u32x4_t*>(&sA[buf][wm * 64 + i * 32 + fr][ks * 16 + fk]);
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+            bf[j] = *reinterpret_cast<const u32x4_t*>(&sB[buf][wn * 64 + j * 32 + fr][ks * 16 + fk]);
+#pragma unroll
+          for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) acc[i][j] = mfma32x32x16(af[i], bf[j], acc[i][j]);
+        }
+      }
+    }
+  }
+
+  // epilogue: acc[i][j][e] is row wm*64 + i*32 + (e/4)*8 + (lane/32)*4 + e%4, column n0 + wn*64 + j*32 + lane%32
+  const int hf = lane >> 5;
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int m = m0 + wm * 64 + i * 32 + (e >> 2) * 8 + hf * 4 + (e & 3);
+      if (m >= M) continue;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int n = n0 + wn * 64 + j * 32 + fr;
+        if (n < a.N) epilogue_store<EPI>(a, m, 0, n, acc[i][j][e]);
+      }
+    }
+}
+
+template <int EPI>
+static int launch_ns_gemm(GemmArgs& g, hipStream_t s) {
+  gemm_tiles(g);
+  if (g.total_blocks == 0) return PDM_OK;
+  PDM_CHECK_ARG(g.total_blocks < (int64_t(1) << 31), "GEMM grid too large");
+  hipLaunchKernelGGL((ns_gemm_kernel<EPI, 5>), dim3((unsigned)g.total_blocks), dim3(256), 0, s, g);
+  PDM_CHECK_LAUNCH();
+  return PDM_OK;
+}
+
+struct NsLayout {
+  int64_t raw, h, w1p, total;
+};
+
+static NsLayout ns_layout(int64_t B, int64_t K64, int64_t N) {
+  NsLayout l{};
+  l.raw = 0;
+  l.h = align256(B * K64 * 2);
+  l.w1p = l.h + align256(B * N * 2);
+  l.total = l.w1p + align256(N * K64 * 2);
+  return l;
+}
+
+static const char* check_ns_desc(const pdm_ns_desc* d, int& K) {
+  if (!d) return "null desc";
+  if (d->num_scalar < 0 || d->num_scalar > PDM_NS_MAX_PARTS || d->num_dense < 0 || d->num_dense > PDM_NS_MAX_PARTS)
+    return "num_scalar and num_dense must be in [0, 8]";
+  if (d->num_scalar + d->num_dense == 0) return "no NS input parts";
+  if (d->table_dtype != PDM_F32 && d->table_dtype != PDM_BF16) return "table_dtype must be F32 or BF16";
+  if (d->n_out < 8 || d->n_out % 8 != 0) return "n_out must be a positive multiple of 8";
+  if (d->batch_size < 0) return "batch_size < 0";
+  K = 0;
+  for (int j = 0; j < d->num_scalar; ++j) {
+    if (d->scalar_dim[j] <= 0 || d->scalar_rows[j] < 0) return "bad scalar table shape";
+    K += d->scalar_dim[j];
+  }
+  for (int j = 0; j < d->num_dense; ++j) {
+    if (d->dense_dim[j] <= 0) return "bad dense part width";
+    K += d->dense_dim[j];
+  }
+  return nullptr;
+}
+
+}  // namespace pdm
+
+extern "C" int64_t pdm_ns_tokenize_workspace_size(const pdm_ns_desc* desc) {
+  clear_error();
+  int K = 0;
+  if (const char* e = check_ns_desc(desc, K)) {
+    set_error(std::string("pdm_ns_tokenize_workspace_size: ") + e);
+    return -1;
+  }
+  return ns_layout(desc->batch_size, (K + GBK - 1) / GBK * GBK, desc->n_out).total;
+}
+
+extern "C" int pdm_ns_tokenize_fwd(const pdm_ns_desc* desc, const void* const* tables, const int64_t* const* ids,
+                                   const float* const* dense, const int64_t* dense_stride, const uint16_t* w1,
+                                   const uint16_t* b1, const uint16_t* w2, const uint16_t* b2, float* out,
+                                   int64_t out_sample_stride, void* workspace, int64_t workspace_bytes,
+                                   int32_t* err_flag, pdm_stream_t stream) {
+  clear_error();
+  int K = 0;
+  if (const char* e = check_ns_desc(desc, K)) {
+    set_error(std::string("pdm_ns_tokenize_fwd: ") + e);
+    return PDM_ERR_INVALID;
+  }
+  const pdm_ns_desc& d = *desc;
+  const int N = d.n_out;
+  const int K64 = (K + GBK - 1) / GBK * GBK;
+  if (d.batch_size == 0) return PDM_OK;
+  PDM_CHECK_ARG(d.batch_size < (int64_t(1) << 31), "batch_size too large");
+  PDM_CHECK_ARG(w1 && b1 && w2 && b2 && out, "null weight or output pointer");
+  PDM_CHECK_ARG(((uintptr_t)w2 & 15) == 0 && ((uintptr_t)w1 & 1) == 0, "w2 must be 16-byte aligned");
+  PDM_CHECK_ARG(out_sample_stride >= N, "out_sample_stride must be >= n_out");
+  PDM_CHECK_ARG(N % GBK == 0, "n_out must be a multiple of 64");
+  NsArgs a{};
+  a.n_scalar = d.num_scalar;
+  a.n_parts = d.num_scalar + d.num_dense;
+  a.f32_tables = d.table_dtype == PDM_F32;
+  int col = 0;
+  for (int j = 0; j < d.num_scalar; ++j) {
+    PDM_CHECK_ARG(tables && ids && tables[j] && ids[j], "null scalar table or ids pointer");
+    a.tables[j] = reinterpret_cast<const char*>(tables[j]);
+    a.ids[j] = ids[j];
+    a.rows[j] = d.scalar_rows[j];
+    a.col[j] = col;
+    col += d.scalar_dim[j];
+  }
+  for (int j = 0; j < d.num_dense; ++j) {
+    PDM_CHECK_ARG(dense && dense_stride && dense[j], "null dense pointer");
+    PDM_CHECK_ARG(dense_stride[j] >= d.dense_dim[j], "dense_stride must be >= dense_dim");
+    a.dense[j] = dense[j];
+    a.dense_stride[j] = dense_stride[j];
+    a.col[d.num_scalar + j] = col;
+    col += d.dense_dim[j];
+  }
+  a.col[a.n_parts] = col;
+  a.K = K;
+  a.K64 = K64;
+  a.B = d.batch_size;
+  a.err = err_flag;
+  const NsLayout lay = ns_layout(d.batch_size, K64, N);
+  PDM_CHECK_ARG(workspace != nullptr && ((uintptr_t)workspace & 255) == 0, "workspace must be 256-byte aligned");
+  PDM_CHECK_ARG(workspace_bytes >= lay.total, "workspace too small");
+  char* ws = reinterpret_cast<char*>(workspace);
+  a.raw = reinterpret_cast<uint16_t*>(ws + lay.raw);
+  uint16_t* h = reinterpret_cast<uint16_t*>(ws + lay.h);
+  uint16_t* w1p = reinterpret_cast<uint16_t*>(ws + lay.w1p);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+
+  hipLaunchKernelGGL(ns_raw_kernel, dim3((unsigned)((d.batch_size + 3) / 4)), dim3(256), 0, s, a);
+  PDM_CHECK_LAUNCH();
+  const int64_t wn = (int64_t)N * K64;
+  hipLaunchKernelGGL(ns_pad_w1_kernel, dim3((unsigned)((wn + 255) / 256)), dim3(256), 0, s, w1, w1p, N, K, K64);
+  PDM_CHECK_LAUNCH();
+  GemmArgs g{};
+  g.B = (int)d.batch_size;
+  g.n_s = 1;
+  g.n_ns = 0;
+  // Linear 1: h = bf16(gelu(bf16(raw . W1^T + b1)))
+  g.A = a.raw;
+  g.a_bstride = K64;
+  g.W = w1p;
+  g.N = N;
+  g.K = K64;
+  g.bias = b1;
+  g.out = h;
+  g.out_bstride = N;
+  if (int st = launch_ns_gemm<EPI_BIAS_GELU>(g, s)) return st;
+  // Linear 2: out = float(bf16(h . W2^T + b2))
+  g.A = h;
+  g.a_bstride = N;
+  g.W = w2;
+  g.K = N;
+  g.bias = b2;
+  g.out = out;
+  g.out_bstride = out_sample_stride;
+  return launch_ns_gemm<EPI_BIAS_F32>(g, s);
 }

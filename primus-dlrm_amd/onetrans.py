@@ -17,7 +17,10 @@ accumulation, fp32 RMSNorm, exact-erf GELU, fp32 residual stream.
 onetrans.py:238-257 (``proj.0`` / ``proj.2`` Linear layers, ``pos_emb``); its
 forward and ``FusedSequenceTokenizer`` (the S-token construction of
 onetrans.py:553-558 straight from the sequence ids) run the fused gather +
-tokenizer kernel with the same autocast numerics.
+tokenizer kernel with the same autocast numerics.  ``AutoSplitTokenizer(ns_input_dim,
+d_model, n_ns_tokens)`` follows onetrans.py:260-276; ``FusedNSTokenizer`` builds the
+NS input of onetrans.py:522-532 (scalar-feature rows, then dense parts) on the
+device and runs it.
 """
 from __future__ import annotations
 
@@ -252,3 +255,59 @@ class FusedSequenceTokenizer(nn.Module):
                    for p in range(len(offsets))]
         tokens, mask = ops.seq_tokenize_raw(tables, grid, offsets, max_len, weights, g.pad_mode, g.align, out=out)
         return tokens, mask.view(torch.bool)
+
+
+class AutoSplitTokenizer(nn.Module):
+    """NS features -> n_ns tokens (onetrans.py:260-276): ``proj`` = Linear(ns_input_dim, d*n_ns), GELU,
+    Linear(d*n_ns, d*n_ns), viewed as [B, n_ns, d].  ``forward(ns_features)`` takes fp32 [B, ns_input_dim] and
+    returns fp32 [B, n_ns, d] (the bf16 result of the reference under autocast).  Forward only; d*n_ns a
+    multiple of 64."""
+
+    def __init__(self, ns_input_dim: int, d_model: int, n_ns_tokens: int):
+        super().__init__()
+        out_dim = d_model * n_ns_tokens
+        self.proj = nn.Sequential(nn.Linear(ns_input_dim, out_dim), nn.GELU(), nn.Linear(out_dim, out_dim))
+        self.n_ns_tokens = n_ns_tokens
+        self.d_model = d_model
+        self._cache: Optional[tuple] = None
+        self._ws: Optional[torch.Tensor] = None
+
+    def kernel_weights(self) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+        """(w1, b1, w2, b2) as bf16 (autocast's casts, made once per parameter version)."""
+        lin1, lin2 = self.proj[0], self.proj[2]
+        params = (lin1.weight, lin1.bias, lin2.weight, lin2.bias)
+        key = tuple((t.data_ptr(), t._version, t.device) for t in params)
+        if self._cache is None or self._cache[0] != key:
+            self._cache = (key, tuple(t.detach().to(torch.bfloat16).contiguous() for t in params))
+        return self._cache[1]
+
+    def run(self, tables, ids, dense, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        w1, b1, w2, b2 = self.kernel_weights()
+        return ops.ns_tokenize_raw(tables, ids, dense, w1, b1, w2, b2, self.n_ns_tokens, out=out)
+
+    def forward(self, ns_features: torch.Tensor) -> torch.Tensor:
+        x = ns_features if ns_features.dtype == torch.float32 else ns_features.float()
+        return self.run([], [], [x])
+
+
+class FusedNSTokenizer(nn.Module):
+    """The NS tokens of OneTransModel._backbone (onetrans.py:522-532,561-563) with the scalar-feature lookups
+    fused: ``forward(batch, dense_parts)`` reads one id per sample of every scalar feature from ``batch`` (the
+    EmbeddingCollection ``ec``'s tables, in ``scalar_features`` order), appends the fp32 dense parts (the
+    reference's ``dense_projs[name](batch[name])`` or raw features, in config order) and runs ``tokenizer`` (an
+    AutoSplitTokenizer).  Returns fp32 [B, n_ns, d]; ``out`` may be the block input's NS rows.  Forward only."""
+
+    def __init__(self, ec, scalar_features: Sequence[str], tokenizer: AutoSplitTokenizer):
+        super().__init__()
+        self.ec = ec
+        self.scalar_features = list(scalar_features)
+        self.tokenizer = tokenizer
+        self._tables = [ec._feature_table[f] for f in self.scalar_features]
+
+    def forward(self, batch: Dict[str, torch.Tensor], dense_parts: Sequence[torch.Tensor] = (),
+                out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        ec = self.ec
+        tables = [ec._store.weight(ec._tables[ti].name) for ti in self._tables]
+        ids = [batch[f].reshape(-1).to(torch.int64).contiguous() for f in self.scalar_features]
+        dense = [x if x.dtype == torch.float32 else x.float() for x in dense_parts]
+        return self.tokenizer.run(tables, ids, dense, out=out)

@@ -552,6 +552,69 @@ def _(tables, ids, offsets, max_len, w1, b1, w2, b2, pos, pad_mode, align):
     return (tables[0].new_empty((B, S, d), dtype=torch.float32), tables[0].new_empty((B, S), dtype=torch.uint8))
 
 
+def ns_tokenize_raw(tables: Sequence[torch.Tensor], ids: Sequence[torch.Tensor], dense: Sequence[torch.Tensor],
+                    w1: torch.Tensor, b1: torch.Tensor, w2: torch.Tensor, b2: torch.Tensor, n_ns: int,
+                    out: Optional[torch.Tensor] = None, workspace: Optional[torch.Tensor] = None,
+                    err_flag: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """NS tokens (C ABI ``pdm_ns_tokenize_fwd``): the NS input rows (``tables[j][ids[j]]`` for the scalar features,
+    then the fp32 ``dense`` parts [B, dim], in that order) through AutoSplitTokenizer's Linear + bias, GELU,
+    Linear + bias (``w1`` [N, K], ``b1`` [N], ``w2`` [N, N], ``b2`` [N] bf16; N = n_ns * d).  Returns fp32
+    [B, n_ns, d]; ``out`` may be a float32 view [B, n_ns, d] with contiguous rows (e.g. the block input's NS
+    rows)."""
+    if len(tables) != len(ids) or len(tables) > L.PDM_NS_MAX_PARTS or len(dense) > L.PDM_NS_MAX_PARTS:
+        raise ValueError("one ids vector per scalar table, at most 8 scalar tables and 8 dense parts")
+    dev = _require_cuda(*tables, *ids, *dense, w1, b1, w2, b2, err_flag)
+    N, K = int(w1.shape[0]), int(w1.shape[1]) if w1.dim() == 2 else -1
+    if N % n_ns:
+        raise ValueError("w1 rows must be n_ns * d_model")
+    d = N // n_ns
+    for t, shape in ((w1, (N, K)), (b1, (N,)), (w2, (N, N)), (b2, (N,))):
+        if t.dtype != torch.bfloat16 or not t.is_contiguous() or tuple(t.shape) != shape:
+            raise ValueError("w1 [N, K], b1 [N], w2 [N, N], b2 [N] must be contiguous bf16")
+    B = ids[0].numel() if ids else dense[0].shape[0]
+    desc = L.NsDesc()
+    desc.num_scalar, desc.num_dense, desc.n_out, desc.batch_size = len(tables), len(dense), N, B
+    desc.table_dtype = TORCH_TO_PDM[tables[0].dtype] if tables else L.PDM_F32
+    ksum = 0
+    for j, (t, i) in enumerate(zip(tables, ids)):
+        if t.dim() != 2 or not t.is_contiguous() or t.dtype != tables[0].dtype or t.dtype not in (torch.float32,
+                                                                                                 torch.bfloat16):
+            raise ValueError("scalar tables must be contiguous 2-D fp32 or bf16 tensors of one dtype")
+        if i.dtype != torch.int64 or i.numel() != B or not i.is_contiguous():
+            raise ValueError("ids must be contiguous int64 vectors of one length (one id per sample)")
+        desc.scalar_dim[j], desc.scalar_rows[j] = t.shape[1], t.shape[0]
+        ksum += t.shape[1]
+    strides = (ctypes.c_int64 * max(len(dense), 1))()
+    for j, x in enumerate(dense):
+        if x.dtype != torch.float32 or x.dim() != 2 or x.shape[0] != B or x.stride(1) != 1:
+            raise ValueError("dense parts must be fp32 [B, dim] with contiguous rows")
+        desc.dense_dim[j] = x.shape[1]
+        strides[j] = x.stride(0)
+        ksum += x.shape[1]
+    if ksum != K:
+        raise ValueError(f"w1 has {K} columns but the NS parts are {ksum} wide")
+    if out is None:
+        out = torch.empty((B, n_ns, d), dtype=torch.float32, device=dev)
+    elif (out.dtype != torch.float32 or out.device != dev or tuple(out.shape) != (B, n_ns, d) or
+          out.stride(2) != 1 or out.stride(1) != d):
+        raise ValueError("out must be float32 [B, n_ns, d] with contiguous sample rows")
+    lib = L.lib()
+    need = int(lib.pdm_ns_tokenize_workspace_size(ctypes.byref(desc)))
+    if need < 0:
+        raise L.PdmError(L.PDM_ERR_INVALID, "pdm_ns_tokenize_workspace_size", L.last_error())
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=dev)
+    tab_arr = (ctypes.c_void_p * max(len(tables), 1))(*[t.data_ptr() for t in tables])
+    ids_arr = (ctypes.c_void_p * max(len(ids), 1))(*[i.data_ptr() for i in ids])
+    den_arr = (ctypes.c_void_p * max(len(dense), 1))(*[x.data_ptr() for x in dense])
+    status = lib.pdm_ns_tokenize_fwd(ctypes.byref(desc), tab_arr, ids_arr, den_arr, strides, w1.data_ptr(),
+                                     b1.data_ptr(), w2.data_ptr(), b2.data_ptr(), out.data_ptr(),
+                                     out.stride(0) if B > 0 else N, workspace.data_ptr(), workspace.numel(),
+                                     _ptr(err_flag), L.stream_ptr(dev))
+    L.check(status, "pdm_ns_tokenize_fwd")
+    return out
+
+
 # ---------------------------------------------------------------------------
 # OneTrans block
 # ---------------------------------------------------------------------------

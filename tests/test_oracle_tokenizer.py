@@ -103,3 +103,47 @@ def test_seq_tokenize_composes_gather_and_tokenizer(pad_mode, align):
         rows = {tuple(nopos[b, l].tolist()) for b, l in pads}
         assert len(pads) > 0 and len(rows) == 1
         s0 += L
+
+
+def test_autosplit_rounding_points_match_torch_autocast():
+    """AutoSplitTokenizer (onetrans.py:260-276) under torch's CPU autocast vs the oracle's rounding points."""
+    K, d, n_ns = 130, 64, 4
+    N = d * n_ns
+    w = ot.random_autosplit_weights(K, N, seed=4)
+    x = torch.randn(9, K, generator=torch.Generator().manual_seed(2))
+    m = torch.nn.Sequential(torch.nn.Linear(K, N), torch.nn.GELU(), torch.nn.Linear(N, N))
+    with torch.no_grad():
+        m[0].weight.copy_(w["w1"])
+        m[0].bias.copy_(w["b1"])
+        m[2].weight.copy_(w["w2"])
+        m[2].bias.copy_(w["b2"])
+    with torch.no_grad(), torch.autocast("cpu", dtype=torch.bfloat16):
+        ref = m(x).view(-1, n_ns, d)
+    assert ref.dtype == torch.bfloat16
+    got = ot.autosplit_tokenizer(x, w, n_ns)
+    num = ot._Num("autocast")
+    h = num.round(torch.nn.functional.gelu(ot._lin_bias(x, w["w1"], w["b1"], num)))
+    mag = (got.reshape(9, N).abs() + h.abs() @ w["w2"].abs().T).view(9, n_ns, d)
+    diff = (got - ref.float()).abs()
+    assert (diff > 0).float().mean().item() < 0.01
+    assert bool((diff <= 2.0 ** -7 * mag).all())
+    # fp64 mode = the float64 layers
+    m64 = m.double()
+    with torch.no_grad():
+        r64 = m64(x.double()).view(-1, n_ns, d)
+    assert torch.allclose(ot.autosplit_tokenizer(x.double(), w, n_ns, mode="fp64"), r64, rtol=0, atol=1e-12)
+
+
+def test_ns_tokenize_concatenates_scalar_rows_then_dense():
+    """_build_ns_raw order (onetrans.py:522-532): scalar rows in feature order, then dense parts; an id outside
+    a table gives a zero row."""
+    g = np.random.default_rng(1)
+    t0 = g.normal(0, 1, (10, 8)).astype(np.float32)
+    t1 = g.normal(0, 1, (5, 16)).astype(np.float32)
+    ids = [np.array([3, 9, 0]), np.array([4, 7, 1])]  # 7 is outside t1
+    dense = [g.normal(0, 1, (3, 6)).astype(np.float32)]
+    w = ot.random_autosplit_weights(30, 64, seed=2)
+    got = ot.ns_tokenize([t0, t1], ids, dense, w, 2, mode="fp64")
+    raw = np.concatenate([t0[[3, 9, 0]], np.stack([t1[4], np.zeros(16, np.float32), t1[1]]), dense[0]], axis=1)
+    want = ot.autosplit_tokenizer(torch.from_numpy(raw).double(), w, 2, mode="fp64")
+    assert torch.equal(got, want)
