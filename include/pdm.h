@@ -302,7 +302,7 @@ int pdm_seq_gather_backward_fused(pdm_tbe_plan plan, const pdm_seq_desc* desc,
  * out:     fp32, 16-byte aligned; token (b, s) at
  *          out + b * out_sample_stride + s * d_model (e.g. the first S rows of
  *          the block's [B, S + n_ns, d_model] input)
- * d_model: 128 or 256.  mask / err_flag as pdm_seq_gather_fwd (mask
+ * d_model: 128, 256 or 384.  mask / err_flag as pdm_seq_gather_fwd (mask
  *          optional).  B * S < 2^31.
  * workspace: 256-byte aligned, >= pdm_seq_tokenize_workspace_size(desc,
  *          d_model) bytes; no initialisation needed; calls sharing one

@@ -33,8 +33,7 @@ namespace pdm {
 
 constexpr int kTokNW = 8;               // waves per MLP workgroup (two per SIMD)
 constexpr int kTokRows = kTokNW * 16;   // list entries per pass
-constexpr int kTokNST = 4;              // LDS ring stages
-constexpr int kTokPF = kTokNST - 1;     // ring chunks read ahead
+constexpr int kTokNST = 4;              // LDS ring stages (3 where 4 does not divide the chunks of a pass)
 constexpr int kScanThreads = 1024;
 constexpr int kTokMaxPieces = 64;       // 16-byte raw pieces (8 columns) per token row, K <= 512
 constexpr int kTokZeroBytes = 2048;     // zero row read for padding in ZERO mode and ids outside a table
@@ -193,12 +192,12 @@ struct TokEntry {
 // columns).  LDS row 16t + 4g + i of a W1 chunk holds hidden unit 8g + 4t + i,
 // so lane l (g = l/16) ends with the contiguous units 8g .. 8g+7 of the chunk:
 // after bias, GELU and bf16 packing they are exactly its B operand of Linear 2's
-// 32-wide k step, y^T += W2[rows, step] . G^T, computed for two halves of d/2
-// outputs in 16-row accumulator tiles.
+// 32-wide k step, y^T += W2[rows, step] . G^T, computed for output parts of at
+// most 128 outputs in 16-row accumulator tiles.
 //
 // Weights stream through one NST-stage LDS ring as a continuous sequence of
-// chunks: per pass NC W1 chunks (32 x K, padded rows), then 2 x NC2 W2 chunks
-// (d/2 rows x 64 hidden units, pieces XOR-swizzled by row).  Chunk cc + PF is
+// chunks: per pass NC W1 chunks (32 x K, padded rows), then NC2 W2 chunks per
+// output part (part rows x 64 hidden units, pieces XOR-swizzled by row).  Chunk cc + PF is
 // read to registers during chunk cc and stored at the start of chunk cc + 1
 // (after its barrier) to the stage chunk cc - 1 used, so its loads have a whole
 // chunk of MFMA work to arrive in.  The last PF chunks of a pass read the next
@@ -219,22 +218,25 @@ __global__ __launch_bounds__(kTokNW * 64, 1) void tok_mlp_kernel(TokArgs a) {
   constexpr int ROWS = kTokRows;
   constexpr int KS = K / 32;    // k steps of Linear 1
   constexpr int NC = D / 32;    // Linear 1 chunks of 32 hidden units (= Linear 2 k steps)
-  constexpr int NC2 = D / 64;   // Linear 2 chunks per output half (64 hidden units)
-  constexpr int HD = D / 2;     // outputs per half
-  constexpr int MTH = HD / 16;  // 16-row output tiles per half
-  constexpr int NCH = NC + 2 * NC2;  // ring chunks per pass
-  constexpr int NST = kTokNST, PF = kTokPF;
+  constexpr int NC2 = D / 64;   // Linear 2 chunks per output part (64 hidden units)
+  constexpr int HD = D <= 128 ? D / 2 : 128;  // outputs per part
+  constexpr int NH = D / HD;                  // output parts
+  constexpr int MTH = HD / 16;  // 16-row output tiles per part
+  constexpr int NCH = NC + NH * NC2;  // ring chunks per pass
+  // ring stages: a divisor of the chunks per pass, so that a chunk's stage is the same in every pass
+  constexpr int NST = NCH % kTokNST == 0 ? kTokNST : 3;
+  constexpr int PF = NST - 1;
   constexpr int W1_BYTES = 32 * w_stride<K>();
   constexpr int W2_BYTES = HD * 128;
   constexpr int SLOT = W1_BYTES > W2_BYTES ? W1_BYTES : W2_BYTES;
   constexpr int SEG = 32;             // outputs per epilogue step
   constexpr int SROW = SEG * 4 + 16;  // staging row stride (bytes), padded against bank conflicts
-  constexpr int NSQ = D / SEG;        // epilogue steps (both halves)
+  constexpr int NSQ = HD / SEG;       // epilogue steps per output part
   constexpr int PPL = 16 * (SEG / 4) / 64;  // 16-byte output pieces per lane and step
   constexpr int CPR = K / 8;                    // 16-byte pieces per W1 row
   constexpr int L1 = (32 * CPR + NT - 1) / NT;  // W1 chunk pieces per thread
   constexpr int L2 = (HD * 8 + NT - 1) / NT;    // W2 chunk pieces per thread
-  static_assert(K % 32 == 0 && D % 64 == 0 && HD % SEG == 0 && NSQ % 2 == 0, "unsupported tokenizer shape");
+  static_assert(K % 32 == 0 && D % 64 == 0 && D % HD == 0 && HD % SEG == 0, "unsupported tokenizer shape");
   static_assert(NCH % NST == 0 && PF <= NC && NC >= 4 && NT - ROWS >= D / 4, "schedule needs these");
   __shared__ __attribute__((aligned(16))) char sRing[NST * SLOT];
   __shared__ __attribute__((aligned(16))) char sStage[ROWS * SROW];  // per-wave epilogue staging
@@ -342,7 +344,7 @@ __global__ __launch_bounds__(kTokNW * 64, 1) void tok_mlp_kernel(TokArgs a) {
   };
 
   // Ring chunk c < NC: W1 rows c*32 + perm(r), perm(16t + 4g + i) = 8g + 4t + i, all K columns.  Chunk
-  // NC + h*NC2 + c: W2 rows h*HD .. h*HD + HD, hidden units c*64 .. c*64 + 64, as 128-byte LDS rows with piece
+  // NC + h*NC2 + c: W2 rows h*HD .. h*HD + HD (output part h), hidden units c*64 .. c*64 + 64, as 128-byte LDS rows with piece
   // v of row e at v ^ sw(e), sw(e) = ((e >> 1) & 7) ^ ((e & 1) << 2): 8 consecutive rows, and also 16, cover
   // all banks.
   u32x4_t r1[L1], r2[L2];
@@ -449,7 +451,7 @@ __global__ __launch_bounds__(kTokNW * 64, 1) void tok_mlp_kernel(TokArgs a) {
     float* ypad = a.y_pad + (int64_t)p * D;
     char* stage = sStage + wave * (16 * SROW);
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
+    for (int h = 0; h < NH; ++h) {
       // Linear 2 on outputs h*HD .. h*HD + HD: y[m] = outputs h*HD + 16m + 4*g4 + 0..3 of the lane's entry;
       // k step t of chunk c is hidden units (2c + t)*32 + 8*g4 .. +8 = gp[2c + t], piece 4t + g4 of the row
       f32x4_t y[MTH];
@@ -481,11 +483,11 @@ __global__ __launch_bounds__(kTokNW * 64, 1) void tok_mlp_kernel(TokArgs a) {
         sched_mfma_ds_pipeline<2 * MTH, 4>();
       }
 
-      // Epilogue of the half: bf16(y + b2) (+ pos[l]) through the wave's own staging rows, SEG outputs at a
-      // time, written as row segments; every position load of the half is issued before its first store.
-      f32x4_t pe[NSQ / 2][PPL];
+      // Epilogue of the part: bf16(y + b2) (+ pos[l]) through the wave's own staging rows, SEG outputs at a
+      // time, written as row segments; every position load of the part is issued before its first store.
+      f32x4_t pe[NSQ][PPL];
 #pragma unroll
-      for (int sq = 0; sq < NSQ / 2; ++sq)
+      for (int sq = 0; sq < NSQ; ++sq)
 #pragma unroll
         for (int it = 0; it < PPL; ++it) {
           const int piece = it * 64 + lane;
@@ -497,7 +499,7 @@ __global__ __launch_bounds__(kTokNW * 64, 1) void tok_mlp_kernel(TokArgs a) {
                                                            c4 * 4);
         }
 #pragma unroll
-      for (int sq = 0; sq < NSQ / 2; ++sq) {
+      for (int sq = 0; sq < NSQ; ++sq) {
         const int col0 = h * HD + sq * SEG;
 #pragma unroll
         for (int mm = 0; mm < SEG / 16; ++mm) {
@@ -611,6 +613,7 @@ MlpFn pick_mlp_k(int K) {
 }
 
 MlpFn pick_mlp(int K, int D, bool f32) {
+  if (D == 384) return f32 ? pick_mlp_k<384, true>(K) : pick_mlp_k<384, false>(K);
   if (D == 256) return f32 ? pick_mlp_k<256, true>(K) : pick_mlp_k<256, false>(K);
   if (D == 128) return f32 ? pick_mlp_k<128, true>(K) : pick_mlp_k<128, false>(K);
   return nullptr;
@@ -644,7 +647,7 @@ extern "C" int pdm_seq_tokenize_fwd(const pdm_seq_desc* desc, const void* const*
   PDM_CHECK_ARG(d.pad_mode == PDM_PAD_ROW0 || d.pad_mode == PDM_PAD_ZERO, "bad pad_mode");
   PDM_CHECK_ARG(d.align == PDM_ALIGN_RIGHT || d.align == PDM_ALIGN_LEFT, "bad align");
   PDM_CHECK_ARG(d.batch_size >= 0, "batch_size < 0");
-  PDM_CHECK_ARG(d_model == 128 || d_model == 256, "d_model must be 128 or 256");
+  PDM_CHECK_ARG(d_model == 128 || d_model == 256 || d_model == 384, "d_model must be 128, 256 or 384");
   PDM_CHECK_ARG(tables && ids && offsets && weights, "null pointer array");
   PDM_CHECK_ARG(d.num_features <= kTokMaxFeatures, "the tokenizer takes at most 4 tables per event");
   const bool f32 = d.dtype == PDM_F32;
@@ -751,7 +754,8 @@ extern "C" int pdm_seq_tokenize_fwd(const pdm_seq_desc* desc, const void* const*
   const int64_t grid = std::max<int64_t>(1, std::min<int64_t>(passes_max, std::max(ncu[dev], 1)));
   hipLaunchKernelGGL(mlp, dim3((unsigned)grid), dim3(kTokNW * 64), 0, s, a);
   PDM_CHECK_LAUNCH();
-  if (d_model == 256) hipLaunchKernelGGL(tok_fill_kernel<256>, dim3((unsigned)pairs), dim3(256), 0, s, a);
+  if (d_model == 384) hipLaunchKernelGGL(tok_fill_kernel<384>, dim3((unsigned)pairs), dim3(256), 0, s, a);
+  else if (d_model == 256) hipLaunchKernelGGL(tok_fill_kernel<256>, dim3((unsigned)pairs), dim3(256), 0, s, a);
   else hipLaunchKernelGGL(tok_fill_kernel<128>, dim3((unsigned)pairs), dim3(256), 0, s, a);
   PDM_CHECK_LAUNCH();
   return PDM_OK;

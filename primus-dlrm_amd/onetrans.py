@@ -176,7 +176,7 @@ class SequentialTokenizer(nn.Module):
 
     ``forward(raw)`` takes raw ``[B, L, raw_dim]`` (fp32 or bf16) and returns fp32 ``[B, L, d_model]``: the
     reference's result under ``autocast(bf16)``.  The rows of ``raw`` are fed to the fused kernel as a table
-    read in order.  Forward only; raw_dim in {128, 192, 256, 384}, d_model in {128, 256}."""
+    read in order.  Forward only; raw_dim in {128, 192, 256, 384}, d_model in {128, 256, 384}."""
 
     def __init__(self, raw_dim: int, d_model: int, max_len: int = 1024, use_pos_embed: bool = True):
         super().__init__()

@@ -58,7 +58,9 @@ def _check(got, tabs, ids, dense, w, n_ns):
     ([(700, 32), (90, 64)], [2, 32], 128, 4, "fp32", 200),
     ([], [130], 64, 2, "bf16", 5),
     ([(100, 128)], [], 64, 4, "bf16", 129),
-], ids=["reference_shape_k396_n4096", "fp32_k130_n512", "dense_only", "scalar_only_b129"])
+    ([(5000, 64), (3000, 64), (800, 64), (1200, 64)], [64, 6, 6, 64], 384, 16, "bf16", 21),
+], ids=["reference_shape_k396_n4096", "fp32_k130_n512", "dense_only", "scalar_only_b129",
+        "reference_large_k396_n6144"])
 def test_ns_tokenize_matches_oracle(pdm, dev, case):
     scalar, dense_dims, d, n_ns, dtype, B = case
     g = np.random.default_rng(B)

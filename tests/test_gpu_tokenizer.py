@@ -84,6 +84,9 @@ CASES = [
     ("k192_d256_zero_left", [(700, 128), (60, 64)], [(24, 10), (40, 30)], 256, "bf16", 1, 1, True),
     ("k256_d128_nopos", [(512, 256)], [(33, 20)], 128, "bf16", 0, 0, False),
     ("k384_d128_fp32_zero", [(800, 128), (300, 128), (200, 128)], [(12, 6), (20, 25)], 128, "fp32", 1, 0, True),
+    # the reference's large OneTrans config: item / artist / album of dim 64 per event, d_model 384
+    ("k192_d384_reference_large", [(2000, 64), (300, 64), (500, 64)], [(40, 25), (24, 10), (32, 16)], 384, "bf16",
+     0, 0, True),
 ]
 
 
