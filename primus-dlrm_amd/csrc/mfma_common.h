@@ -61,14 +61,62 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 // negative tail carries no cancellation.  After the bf16 rounding of the result
 // it agrees with the exact-erf GELU except in the far negative tail (x < -3.5,
 // |GELU| < 1e-3), where the two can differ by one bf16 step.
-__device__ __forceinline__ float gelu_erf(float v) {
-  const float ax = fabsf(v);
+__device__ __forceinline__ float gelu_tail(float ax) {  // e = erfc(ax / sqrt 2) / 2, ax >= 0
   // p / sqrt 2 with p = 0.3275911; coefficients a_i / 2
   const float t = __builtin_amdgcn_rcpf(__builtin_fmaf(ax, 0.23164189619f, 1.0f));
   const float poly = t * (0.127414796f + t * (-0.142248368f + t * (0.7107068705f + t * (-0.7265760135f + t * 0.5307027145f))));
   // exp(-x^2 / 2) = 2^(-x^2 log2(e) / 2)
-  const float e = poly * __builtin_amdgcn_exp2f((v * v) * -0.72134752044448170f);
-  return __builtin_fmaf(-ax, e, fmaxf(v, 0.0f));
+  return poly * __builtin_amdgcn_exp2f((ax * ax) * -0.72134752044448170f);
+}
+
+__device__ __forceinline__ float gelu_erf(float v) {
+  const float ax = fabsf(v);
+  return __builtin_fmaf(-ax, gelu_tail(ax), fmaxf(v, 0.0f));
+}
+
+// GELU of a bf16 value through a table of e(|x|) = gelu_tail(|x|) over the bf16
+// values 2^-16 <= |x| <= 8 (bit patterns 0x3780 .. 0x4100, 2433 floats, 9.5 KB
+// of LDS).  Inside that range the result is gelu_erf(x) bit for bit (same e,
+// same final FMA).  Outside it |x| is clamped to the range ends: for
+// |x| < 2^-16 both e values are 1/2 to within 2^-17, so both results round to
+// the bf16 value x/2; for x > 8 both round to x; for x < -8 both are below
+// 1e-14 in magnitude (the exact-erf GELU's fp32 value there is -0).  The
+// table replaces two transcendental and ten other VALU operations per
+// element with a clamp, a shift and one LDS read.
+constexpr uint32_t GELU_T_LO = 0x3780u, GELU_T_HI = 0x4100u;
+constexpr int GELU_T_N = int(GELU_T_HI - GELU_T_LO) + 1;
+
+__device__ __forceinline__ void gelu_table_fill(float* t, int tid, int nthreads) {
+  for (int i = tid; i < GELU_T_N; i += nthreads)
+    t[i] = gelu_tail(__builtin_bit_cast(float, (GELU_T_LO + (uint32_t)i) << 16));
+}
+
+__device__ __forceinline__ float gelu_lut(const float* t, float x) {  // x: a bf16 value held as fp32
+  const float ax = fabsf(x);
+  const float c = __builtin_amdgcn_fmed3f(ax, 0x1p-16f, 8.0f);
+  const float e = t[(__builtin_bit_cast(uint32_t, c) >> 16) - GELU_T_LO];
+  return __builtin_fmaf(-ax, e, fmaxf(x, 0.0f));
+}
+
+// G[i] = bf16(GELU(bf16(u[2i]))) | bf16(GELU(bf16(u[2i+1]))) << 16 for N values: all N table reads are
+// issued before the first is used, so the LDS latency is paid once.
+template <int N>
+__device__ __forceinline__ void gelu_lut_pack(const float* t, const float* u, uint32_t* g) {
+  float x[N], e[N];
+#pragma unroll
+  for (int i = 0; i < N; i += 2) {
+    const uint32_t p = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{u[i], u[i + 1]}, bf16x2_t));
+    x[i] = __builtin_bit_cast(float, p << 16);
+    x[i + 1] = __builtin_bit_cast(float, p & 0xffff0000u);
+  }
+#pragma unroll
+  for (int i = 0; i < N; ++i)
+    e[i] = t[(__builtin_bit_cast(uint32_t, __builtin_amdgcn_fmed3f(fabsf(x[i]), 0x1p-16f, 8.0f)) >> 16) - GELU_T_LO];
+#pragma unroll
+  for (int i = 0; i < N; i += 2)
+    g[i >> 1] = __builtin_bit_cast(uint32_t, __builtin_convertvector(
+        f32x2_t{__builtin_fmaf(-fabsf(x[i]), e[i], fmaxf(x[i], 0.0f)),
+                __builtin_fmaf(-fabsf(x[i + 1]), e[i + 1], fmaxf(x[i + 1], 0.0f))}, bf16x2_t));
 }
 
 template <int D>

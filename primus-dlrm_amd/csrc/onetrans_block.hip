@@ -93,6 +93,18 @@ enum { EPI_BF16 = 0, EPI_QKV = 1, EPI_RESID = 2, EPI_GELU = 3, EPI_BIAS_GELU = 4
 
 constexpr int GBM = 128, GBN = 128, GBK = 64, GPAD = 8;
 
+// 16 bytes per lane from global memory (uniform base + per-lane 32-bit byte offset) into LDS at the
+// wave-uniform address lds + 16 * lane (global_load_lds_dwordx4; M0 holds the LDS address, one wait state
+// between its write and the load).  Completion is counted by vmcnt.
+// s_waitcnt vmcnt(0) (gfx9 encoding: vmcnt bits 3:0 and 15:14 zero, expcnt 7, lgkmcnt 15), issued through
+// the builtin so that the compiler's own wait tracking knows every vector memory access is complete
+constexpr unsigned kWaitVmcnt0 = 0x0F70;
+
+__device__ __forceinline__ void lds_dma16(uint64_t base, uint32_t off, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :: "v"(off), "s"(base), "s"(lds) : "memory", "m0");
+}
+
 struct GemmArgs {
   const uint16_t* A;  // bf16 rows: row (b, t) at A + b * a_bstride + t * K
   int64_t a_bstride;  // elements between samples
@@ -557,7 +569,7 @@ __global__ __launch_bounds__(NW * 64, WPS) void ffn_kernel(GemmArgs a) {
   constexpr int KS = D / 16;
   constexpr int DB = D / 32;                 // 32-row blocks of the output (d)
   constexpr int TROWS = NW * RB * 32;
-  constexpr int W1_BYTES = 32 * w_stride<D>();  // 32 hidden units x D (padded rows)
+  constexpr int W1_BYTES = 32 * 2 * D;       // 32 hidden units x D
   constexpr int W2_BYTES = D * 64;           // D outputs x 32 hidden units
   // one LDS block: the weight ring, reused by the epilogue's staging tile
   constexpr int RING_BYTES = NST * (W1_BYTES + W2_BYTES);
@@ -566,61 +578,61 @@ __global__ __launch_bounds__(NW * 64, WPS) void ffn_kernel(GemmArgs a) {
   char (*sW2)[W2_BYTES] = reinterpret_cast<char (*)[W2_BYTES]>(sRing + NST * W1_BYTES);
   __shared__ int s_rb[TROWS];
   __shared__ int s_rt[TROWS];
+  __shared__ float sGelu[GELU_T_N];
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
+  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int fr = lane & 31, hf = lane >> 5;
   const int mt = blockIdx.x;
   for (int i = tid; i < TROWS; i += NT) tile_row(a, mt, TROWS, i, s_rb[i], s_rt[i]);
+  gelu_table_fill(sGelu, tid, NT);
   const int F = a.N;
   const int64_t gsel = mt < a.tiles_s ? -1 : (mt - a.tiles_s) / a.tiles_b;
   const uint16_t* W1 = gsel < 0 ? a.W : a.W_ns + gsel * (int64_t)F * D;
   const uint16_t* W2 = gsel < 0 ? a.W2 : a.W2_ns + gsel * (int64_t)D * F;
-  __syncthreads();
 
-  // Weight chunk c: W1 rows c*32 + swap23(r) (all D columns) as 32 padded LDS
-  // rows; W2[d, c*32 .. c*32+32) as D LDS rows of 64 bytes with piece v of row
-  // d at v ^ ((d >> 2) & 3).
-  constexpr int CPR = D / 8;
-  constexpr int L1 = 32 * CPR / NT;   // 16-byte pieces per thread of a W1 chunk
-  constexpr int L2 = D * 4 / NT;      // and of a W2 chunk
-  u32x4_t r1[L1], r2[L2];
-  constexpr int RPP = NT / CPR;       // W1 chunk rows covered by one piece round
-  const int w1r0 = tid / CPR, w1p0 = tid - (tid / CPR) * CPR;
-  auto gload1 = [&](int c) {
+  // Weight chunk c goes from global memory straight into LDS (global_load_lds_dwordx4: lane l of a wave
+  // writes the 16 bytes at the wave's LDS base + 16 l), so LDS piece o of a stage is loaded by thread
+  // o mod NT, round o / NT, and the source address is what decides the layout.
+  // W1 stage: row r = hidden unit c*32 + swap23(r) (bits 2 and 3 swapped), D columns in 2D bytes,
+  // 16-byte piece v of the row at slot v ^ (r & 15), so the 32 rows of one fragment read hit distinct
+  // bank groups.  W2 stage: W2[d, c*32 .. c*32+32) as D rows of 64 bytes, piece v at v ^ ((d >> 2) & 3).
+  constexpr int L1 = W1_BYTES / 16 / NT;     // pieces per thread of a W1 chunk
+  constexpr int L2 = W2_BYTES / 16 / NT;     // and of a W2 chunk
+  static_assert(L1 * NT * 16 == W1_BYTES && L2 * NT * 16 == W2_BYTES, "chunk pieces must cover the threads");
+  // per-thread byte offsets of its pieces within chunk 0 (the chunk adds a uniform offset)
+  uint32_t off1[L1], off2[L2];
 #pragma unroll
-    for (int p = 0; p < L1; ++p) {
-      const int r = p * RPP + w1r0;
-      const int hid = c * 32 + ((r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1));
-      r1[p] = *reinterpret_cast<const u32x4_t*>(W1 + (int64_t)hid * D + w1p0 * 8);
-    }
-  };
-  auto gload2 = [&](int c) {
+  for (int p = 0; p < L1; ++p) {
+    const int o = p * NT + tid;              // piece index in the stage
+    const int r = o / (D / 8), slot = o % (D / 8);  // a row is D / 8 pieces
+    off1[p] = (uint32_t)((((r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1)) * D + ((slot ^ (r & 15)) << 3)) * 2);
+  }
 #pragma unroll
-    for (int p = 0; p < L2; ++p) {
-      const int q = p * NT + tid;
-      const int d = q >> 2, v = (q & 3) ^ ((d >> 2) & 3);
-      r2[p] = *reinterpret_cast<const u32x4_t*>(W2 + (int64_t)d * F + c * 32 + v * 8);
-    }
-  };
-  auto sstore1 = [&](int buf) {
+  for (int p = 0; p < L2; ++p) {
+    const int q = p * NT + tid;
+    const int d = q >> 2, v = (q & 3) ^ ((d >> 2) & 3);
+    off2[p] = (uint32_t)((d * F + v * 8) * 2);
+  }
+  // The DMA is issued from inline assembly: the compiler's own tracking of LDS DMA makes every later LDS
+  // read wait for it.  Its completion is awaited explicitly (s_waitcnt vmcnt(0) before the barrier that
+  // publishes a chunk and before the epilogue reuses the ring); the compiler's own vmcnt waits stay
+  // correct with these loads outstanding, since vector memory loads complete in issue order.
+  auto dma = [&](int c, int stg) {
+    const uint64_t b1 = (uint64_t)(uintptr_t)W1 + (uint64_t)c * 32 * D * 2;
+    const uint64_t b2 = (uint64_t)(uintptr_t)W2 + (uint64_t)c * 32 * 2;
 #pragma unroll
     for (int p = 0; p < L1; ++p)
-      *reinterpret_cast<u32x4_t*>(sW1[buf] + (p * RPP + w1r0) * w_stride<D>() + w1p0 * 16) = r1[p];
-  };
-  auto sstore2 = [&](int buf) {
+      lds_dma16(b1, off1[p], (uint32_t)(uintptr_t)(sW1[stg] + (p * NT + wave * 64) * 16));
 #pragma unroll
-    for (int p = 0; p < L2; ++p) *reinterpret_cast<u32x4_t*>(sW2[buf] + (p * NT + tid) * 16) = r2[p];
+    for (int p = 0; p < L2; ++p)
+      lds_dma16(b2, off2[p], (uint32_t)(uintptr_t)(sW2[stg] + (p * NT + wave * 64) * 16));
   };
   const int nchunks = F / 32;
-  gload1(0); gload2(0);
-  sstore1(0); sstore2(0);
+  __syncthreads();
 #pragma unroll
-  for (int c = 1; c < PF; ++c)
-    if (c < nchunks) {
-      gload1(c); gload2(c);
-      sstore1(c); sstore2(c);
-    }
+  for (int c = 0; c < PF; ++c)
+    if (c < nchunks) dma(c, c);
 
   u32x4_t hfr[RB][KS];
   load_row_fragments<D, RB, true>(a, s_rb, s_rt, wave, fr, hf, hfr);
@@ -633,69 +645,82 @@ __global__ __launch_bounds__(NW * 64, WPS) void ffn_kernel(GemmArgs a) {
 #pragma unroll
       for (int e = 0; e < 16; ++e) y[rb][db][e] = 0.0f;
 
-  for (int c = 0; c < nchunks; ++c) {
-    // chunks c .. c + PF - 1 are in LDS, and every wave is done with chunk c - 1, whose stage receives chunk c + PF
-    __syncthreads();
-    const bool more = c + PF < nchunks;
-    const int st = c % NST, st2 = (c + PF) % NST;
-    if (more) gload1(c + PF);
-    // FFN-up: U^T[rb] = W1_c . h[rb]^T, each W1 fragment feeding RB MFMAs
-    const char* w1 = sW1[st];
-    f32x16_t u[RB];
+  // The chunk loop is unrolled by the ring depth so that every stage index is a constant: the LDS reads of
+  // stage k and the LDS DMA into stage (k + PF) % NST are then distinct objects to the compiler.
+  for (int c0 = 0; c0 < nchunks; c0 += NST) {
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb)
+    for (int k = 0; k < NST; ++k) {
+      const int c = c0 + k;
+      if (c >= nchunks) break;
+      // chunks c .. c + PF - 1 are in LDS once every wave's DMA has landed (the wait) and every wave has
+      // passed the barrier, which also means every wave is done with chunk c - 1, whose stage receives
+      // chunk c + PF
+      __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+      __syncthreads();
+      // issued unconditionally (a branch around it costs the compiler its stage tracking): past the last chunk
+      // it reloads the last chunk into the stage just freed, which no later chunk reads
+      dma(min(c + PF, nchunks - 1), (k + PF) % NST);
+      // FFN-up: U^T[rb] = W1_c . h[rb]^T, each W1 fragment feeding RB MFMAs
+      const char* w1 = sW1[k];
+      f32x16_t u[RB];
 #pragma unroll
-      for (int e = 0; e < 16; ++e) u[rb][e] = 0.0f;
-    {
-      u32x4_t wf[KS];
+      for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-      for (int s = 0; s < KS; ++s) wf[s] = read_w_frag<D>(w1, fr, 2 * s + hf);
+        for (int e = 0; e < 16; ++e) u[rb][e] = 0.0f;
+      {
+        u32x4_t wf[KS];
 #pragma unroll
-      for (int s = 0; s < KS; ++s)
+        for (int s = 0; s < KS; ++s)
+          wf[s] = *reinterpret_cast<const u32x4_t*>(w1 + fr * (2 * D) + (((2 * s + hf) ^ (fr & 15)) << 4));
 #pragma unroll
-        for (int rb = 0; rb < RB; ++rb) u[rb] = mfma32x32x16(wf[s], hfr[rb][s], u[rb]);
-      if constexpr (RB == 1) sched_mfma_ds_pipeline<KS, 4>();
+        for (int s = 0; s < KS; ++s)
+#pragma unroll
+          for (int rb = 0; rb < RB; ++rb) u[rb] = mfma32x32x16(wf[s], hfr[rb][s], u[rb]);
+        if constexpr (RB == 1) sched_mfma_ds_pipeline<KS, 4>();
+      }
+      // G = bf16(gelu(bf16(U))): u[rb][e] is hidden unit (e/4)*8 + hf*4 + e%4 (LDS row order) of token fr;
+      // two halves of 8 values bound the registers the table reads hold in flight
+      uint32_t gp[RB][8];
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int h2 = 0; h2 < 2; ++h2) {
+          float uv[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) uv[e] = u[rb][8 * h2 + e];
+          gelu_lut_pack<8>(sGelu, uv, gp[rb] + 4 * h2);
+        }
+      // FFN-down: y^T[rb][db] += W2[db rows, chunk c] . G[rb]^T; chunk c2 of G^T holds hidden units
+      // 16*c2 + hf*8 + 0..7, piece 2*c2 + hf of W2 row d, stored at (2*c2 + hf) ^ ((d >> 2) & 3)
+      const char* w2 = sW2[k];
+      {
+        // (d >> 2) & 3 = (fr >> 2) & 3 for d = db*32 + fr
+        u32x4_t wf[DB * 2];
+#pragma unroll
+        for (int c2 = 0; c2 < 2; ++c2)
+#pragma unroll
+          for (int db = 0; db < DB; ++db)
+            wf[c2 * DB + db] =
+                *reinterpret_cast<const u32x4_t*>(w2 + (db * 32 + fr) * 64 + (((2 * c2 + hf) ^ ((fr >> 2) & 3)) << 4));
+#pragma unroll
+        for (int c2 = 0; c2 < 2; ++c2)
+#pragma unroll
+          for (int db = 0; db < DB; ++db)
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb) {
+              const u32x4_t gb = {gp[rb][4 * c2], gp[rb][4 * c2 + 1], gp[rb][4 * c2 + 2], gp[rb][4 * c2 + 3]};
+              y[rb][db] = mfma32x32x16(wf[c2 * DB + db], gb, y[rb][db]);
+            }
+        if constexpr (RB == 1) sched_mfma_ds_pipeline<DB * 2, 4>();
+      }
     }
-    if (more) {
-      sstore1(st2);
-      gload2(c + PF);
-    }
-    // G = bf16(gelu(bf16(U))): u[rb][e] is hidden unit (e/4)*8 + hf*4 + e%4 (LDS row order) of token fr
-    uint32_t gp[RB][8];
-#pragma unroll
-    for (int rb = 0; rb < RB; ++rb)
-#pragma unroll
-      for (int e = 0; e < 16; e += 2)
-        gp[rb][e >> 1] = pack_bf16x2(gelu_erf(bf16_round(u[rb][e])), gelu_erf(bf16_round(u[rb][e + 1])));
-    // FFN-down: y^T[rb][db] += W2[db rows, chunk c] . G[rb]^T; chunk c2 of G^T holds hidden units
-    // 16*c2 + hf*8 + 0..7, piece 2*c2 + hf of W2 row d, stored at (2*c2 + hf) ^ ((d >> 2) & 3)
-    const char* w2 = sW2[st];
-    {
-      // (d >> 2) & 3 = (fr >> 2) & 3 for d = db*32 + fr
-      u32x4_t wf[DB * 2];
-#pragma unroll
-      for (int c2 = 0; c2 < 2; ++c2)
-#pragma unroll
-        for (int db = 0; db < DB; ++db)
-          wf[c2 * DB + db] = *reinterpret_cast<const u32x4_t*>(w2 + (db * 32 + fr) * 64 + (((2 * c2 + hf) ^ ((fr >> 2) & 3)) << 4));
-#pragma unroll
-      for (int c2 = 0; c2 < 2; ++c2)
-#pragma unroll
-        for (int db = 0; db < DB; ++db)
-#pragma unroll
-          for (int rb = 0; rb < RB; ++rb) {
-            const u32x4_t gb = {gp[rb][4 * c2], gp[rb][4 * c2 + 1], gp[rb][4 * c2 + 2], gp[rb][4 * c2 + 3]};
-            y[rb][db] = mfma32x32x16(wf[c2 * DB + db], gb, y[rb][db]);
-          }
-      if constexpr (RB == 1) sched_mfma_ds_pipeline<DB * 2, 4>();
-    }
-    if (more) sstore2(st2);
   }
 
   // Epilogue y = z + bf16(FFN).  y[rb][db][e] is output d = db*32 + (e/4)*8 + hf*4 + e%4 of row
   // wave*RB*32 + rb*32 + fr.  The values go through LDS (the weight ring is free now) SEG outputs at a
   // time, so that z is read and y written as whole row segments of SEG outputs, with
   // non-temporal stores (y is streamed to memory; the next kernel reads it from there).
+  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);  // the last DMA must land before the ring is reused
   __syncthreads();
   constexpr int SEG = NW * RB * 32 * (64 * 4 + 16) <= RING_BYTES ? 64 : 32;  // outputs per pass
   constexpr int SROW = SEG * 4 + 16;       // LDS row stride (bytes), padded against bank conflicts
