@@ -370,21 +370,28 @@ __device__ __forceinline__ void load_row_fragments(const GemmArgs& a, const int*
   }
 }
 
-// Weight chunks live in LDS as rows of 2*D bytes padded to a stride of
-// 2*D + 16, so rows r and r + 1 start 16 bytes apart in the banks: the lanes
-// reading one 16-byte piece of 16 consecutive rows hit distinct banks, and a
-// lane's piece offsets are immediates.
+// Weight chunks of 32 output columns x D.  Register path (the residual
+// epilogue, whose per-chunk residual loads must not wait for weight loads):
+// a double buffer of rows padded to a stride of 2*D + 16, loaded into
+// registers at the top of a chunk and written to LDS after its MFMAs.  DMA
+// path (the Q/K/V epilogue, whose chunks only store): a 4-stage ring filled by
+// LDS DMA three chunks ahead, rows of 2*D bytes with 16-byte piece v of row r
+// at slot v ^ (r & 15), the chunk loop unrolled by the ring depth.  Either way
+// the 32 rows of one fragment read hit distinct bank groups.
 template <int D, int RB, int EPI, bool NORM>
 __global__ __launch_bounds__(256, 2) void rowgemm_kernel(GemmArgs a) {
   constexpr int KS = D / 16;
   constexpr int TROWS = 4 * RB * 32;
-  constexpr int CHUNK_BYTES = 32 * w_stride<D>();
-  __shared__ __attribute__((aligned(16))) char sW[2][CHUNK_BYTES];
+  constexpr bool DMA = EPI == EPI_QKV;
+  constexpr int NST = DMA ? 4 : 2;
+  constexpr int PF = NST - 1;
+  constexpr int CHUNK_BYTES = DMA ? 32 * 2 * D : 32 * w_stride<D>();
+  __shared__ __attribute__((aligned(16))) char sW[NST][CHUNK_BYTES];
   __shared__ int s_rb[TROWS];
   __shared__ int s_rt[TROWS];
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
+  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int fr = lane & 31, hf = lane >> 5;
   const int mt = blockIdx.x;
   for (int i = tid; i < TROWS; i += 256) tile_row(a, mt, TROWS, i, s_rb[i], s_rt[i]);
@@ -399,13 +406,12 @@ __global__ __launch_bounds__(256, 2) void rowgemm_kernel(GemmArgs a) {
     if (!__syncthreads_or(need)) c0 = D / 32;
   }
   const int nchunks = a.N / 32;
-  // weight chunk c: 32 rows x D as 32 LDS rows, 16-byte piece v of row r at v ^ (r & 15);
-  // loaded into registers at the top of an iteration, written to LDS at its bottom
-  constexpr int CPR = D / 8;
-  constexpr int WL = 32 * CPR / 256;  // 16-byte pieces per thread
+  constexpr int CPR = D / 8;          // 16-byte pieces per weight row
+  constexpr int WL = 32 * CPR / 256;  // 16-byte pieces per thread of a chunk
+  // register path
   constexpr int RPP = 256 / CPR;      // chunk rows covered by one piece round
   const int wr0 = tid / CPR, wp0 = tid - (tid / CPR) * CPR;
-  u32x4_t wr[WL];
+  u32x4_t wr[DMA ? 1 : WL];
   auto gload = [&](int c) {
 #pragma unroll
     for (int p = 0; p < WL; ++p)
@@ -416,8 +422,32 @@ __global__ __launch_bounds__(256, 2) void rowgemm_kernel(GemmArgs a) {
     for (int p = 0; p < WL; ++p)
       *reinterpret_cast<u32x4_t*>(sW[buf] + (p * RPP + wr0) * w_stride<D>() + wp0 * 16) = wr[p];
   };
-  gload(c0);
-  sstore(0);
+  // DMA path: LDS piece o of a stage is loaded by thread o mod 256 (round o / 256) from row o / CPR,
+  // logical piece (o mod CPR) ^ (row & 15)
+  uint32_t woff[WL];
+#pragma unroll
+  for (int p = 0; p < WL; ++p) {
+    const int o = p * 256 + tid, r = o / CPR;
+    woff[p] = (uint32_t)((r * D + (((o % CPR) ^ (r & 15)) << 3)) * 2);
+  }
+  auto dma = [&](int c, int stg) {
+    const uint64_t base = (uint64_t)(uintptr_t)W + (uint64_t)c * 32 * D * 2;
+#pragma unroll
+    for (int p = 0; p < WL; ++p) lds_dma16(base, woff[p], (uint32_t)(uintptr_t)(sW[stg] + (p * 256 + wave * 64) * 16));
+  };
+  auto wfrag = [&](const char* wb, int s) -> u32x4_t {
+    if constexpr (DMA)
+      return *reinterpret_cast<const u32x4_t*>(wb + fr * (2 * D) + (((2 * s + hf) ^ (fr & 15)) << 4));
+    else
+      return read_w_frag<D>(wb, fr, 2 * s + hf);
+  };
+  if constexpr (DMA) {
+#pragma unroll
+    for (int j = 0; j < PF; ++j) dma(min(c0 + j, nchunks - 1), j);
+  } else {
+    gload(c0);
+    sstore(0);
+  }
 
   u32x4_t af[RB][KS];
   load_row_fragments<D, RB, NORM>(a, s_rb, s_rt, wave, fr, hf, af);
@@ -445,11 +475,8 @@ __global__ __launch_bounds__(256, 2) void rowgemm_kernel(GemmArgs a) {
   }
   const int my_row = wave * RB * 32 + fr;  // + rb * 32: this lane's row in the rows-on-lanes layout
 
-  for (int c = c0; c < nchunks; ++c) {
-    const int buf = (c - c0) & 1;
-    __syncthreads();  // chunk c is in LDS; every wave is done with chunk c - 1
-    const bool more = c + 1 < nchunks;
-    if (more) gload(c + 1);
+  // chunk c with its weights at wb (the MFMAs, then after_mfma(), then the stores)
+  auto chunk = [&](int c, const char* wb, auto&& after_mfma) {
     const bool cols_on_lanes = EPI == EPI_QKV && c * 32 >= 2 * a.D;
     f32x4_t res[RB][4];
     if constexpr (EPI == EPI_RESID) {
@@ -472,10 +499,13 @@ __global__ __launch_bounds__(256, 2) void rowgemm_kernel(GemmArgs a) {
     if (cols_on_lanes) {
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
-        const u32x4_t wf = read_w_frag<D>(sW[buf], fr, 2 * s + hf);
+        const u32x4_t wf = wfrag(wb, s);
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) acc[rb] = mfma32x32x16(af[rb][s], wf, acc[rb]);
       }
+      // (register path) the next chunk goes to LDS before this chunk's stores: its wait on the loads would
+      // otherwise also wait for the stores (vector memory completes in issue order)
+      after_mfma();
       // V^T[b, h, d, token]: column cv = c*32 + fr - 2D of V is head cv / 64, d = cv % 64
       const int cv = c * 32 + fr - 2 * a.D;
       uint16_t* vrow = a.vt + ((int64_t)(cv >> 6) * 64 + (cv & 63)) * a.kv_pad;
@@ -500,10 +530,11 @@ __global__ __launch_bounds__(256, 2) void rowgemm_kernel(GemmArgs a) {
     } else {
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
-        const u32x4_t wf = read_w_frag<D>(sW[buf], fr, 2 * s + hf);
+        const u32x4_t wf = wfrag(wb, s);
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) acc[rb] = mfma32x32x16(wf, af[rb][s], acc[rb]);
       }
+      after_mfma();
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb) {
         const int b = s_rb[my_row + rb * 32];
@@ -537,7 +568,33 @@ __global__ __launch_bounds__(256, 2) void rowgemm_kernel(GemmArgs a) {
         }
       }
     }
-    if (more) sstore(buf ^ 1);
+  };
+  if constexpr (DMA) {
+    // before the barrier of chunk c: every DMA but the 2 * WL pieces issued for chunks c + 1 and c + 2 has
+    // landed, whatever number of stores came between (vector memory completes in issue order)
+    constexpr unsigned kWait = 0x0F70u | (2u * WL);
+    static_assert(2 * WL < 16, "vmcnt immediate");
+    for (int cb = c0; cb < nchunks; cb += NST) {
+#pragma unroll
+      for (int k = 0; k < NST; ++k) {
+        const int c = cb + k;
+        if (c >= nchunks) break;
+        __builtin_amdgcn_s_waitcnt(kWait);
+        __syncthreads();  // chunk c is in LDS; every wave is done with chunk c - 1, whose stage is refilled
+        // unconditional (past the end it reloads the last chunk into the freed stage, read by no later chunk)
+        dma(min(c + PF, nchunks - 1), (k + PF) % NST);
+        chunk(c, sW[k], [] {});
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);  // no DMA may land in LDS after the workgroup ends
+  } else {
+    for (int c = c0; c < nchunks; ++c) {
+      const int buf = (c - c0) & 1;
+      __syncthreads();  // chunk c is in LDS; every wave is done with chunk c - 1
+      const bool more = c + 1 < nchunks;
+      if (more) gload(c + 1);
+      chunk(c, sW[buf], [&] { if (more) sstore(buf ^ 1); });
+    }
   }
 }
 
