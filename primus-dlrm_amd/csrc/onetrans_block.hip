@@ -686,6 +686,8 @@ __global__ __launch_bounds__(NW * 64, WPS) void ffn_kernel(GemmArgs a) {
       lds_dma16(b2, off2[p], (uint32_t)(uintptr_t)(sW2[stg] + (p * NT + wave * 64) * 16));
   };
   const int nchunks = F / 32;
+  constexpr unsigned kWaitDma = 0x0F70u | (unsigned)((PF - 1) * (L1 + L2));
+  static_assert((PF - 1) * (L1 + L2) < 16, "vmcnt immediate");
   __syncthreads();
 #pragma unroll
   for (int c = 0; c < PF; ++c)
@@ -709,10 +711,11 @@ __global__ __launch_bounds__(NW * 64, WPS) void ffn_kernel(GemmArgs a) {
     for (int k = 0; k < NST; ++k) {
       const int c = c0 + k;
       if (c >= nchunks) break;
-      // chunks c .. c + PF - 1 are in LDS once every wave's DMA has landed (the wait) and every wave has
-      // passed the barrier, which also means every wave is done with chunk c - 1, whose stage receives
-      // chunk c + PF
-      __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+      // chunks c .. c + PF - 1 are in LDS once every wave's DMA but the (PF - 1) (L1 + L2) pieces issued for
+      // chunks c + 1 .. c + PF - 1 has landed (the wait; no other vector memory access is issued in the
+      // loop, and they complete in issue order) and every wave has passed the barrier, which also means
+      // every wave is done with chunk c - 1, whose stage receives chunk c + PF
+      __builtin_amdgcn_s_waitcnt(kWaitDma);
       __syncthreads();
       // issued unconditionally (a branch around it costs the compiler its stage tracking): past the last chunk
       // it reloads the last chunk into the stage just freed, which no later chunk reads
@@ -1266,19 +1269,22 @@ static int launch_rowgemm(GemmArgs& g, int D, hipStream_t s) {
 }
 
 // FFN launch shape: RB * 32 rows per wave, NW waves per workgroup, an NST-stage
-// weight ring, WPS workgroups per CU.  Eight waves of 32 rows (two per SIMD:
-// one wave's GELU runs beside the other's MFMAs) measured fastest at d_model 256.
+// weight ring, WPS workgroups per CU.  Two workgroups of four 32-row waves per
+// CU (two waves per SIMD, 2-stage ring, 75 KB of LDS each) measured fastest at
+// d_model 256: the workgroups' barriers are independent, so one's GELU,
+// prologue and epilogue run beside the other's MFMAs (one workgroup of eight
+// waves keeps every wave of a SIMD in the same phase).
 #ifndef PDM_FFN_RB
 #define PDM_FFN_RB 1
 #endif
 #ifndef PDM_FFN_NW
-#define PDM_FFN_NW 8
+#define PDM_FFN_NW 4
 #endif
 #ifndef PDM_FFN_NST
-#define PDM_FFN_NST 3
+#define PDM_FFN_NST 2
 #endif
 #ifndef PDM_FFN_WPS
-#define PDM_FFN_WPS 1
+#define PDM_FFN_WPS 2
 #endif
 static int launch_ffn(GemmArgs& g, int D, hipStream_t s) {
   constexpr int RB = PDM_FFN_RB, NW = PDM_FFN_NW, NST = PDM_FFN_NST, WPS = PDM_FFN_WPS;
