@@ -378,12 +378,19 @@ __device__ __forceinline__ void load_row_fragments(const GemmArgs& a, const int*
 // LDS DMA three chunks ahead, rows of 2*D bytes with 16-byte piece v of row r
 // at slot v ^ (r & 15), the chunk loop unrolled by the ring depth.  Either way
 // the 32 rows of one fragment read hit distinct bank groups.
+// Q/K/V GEMM: weight ring depth and workgroups per CU
+#ifndef PDM_QKV_NST
+#define PDM_QKV_NST 4
+#endif
+#ifndef PDM_QKV_WPS
+#define PDM_QKV_WPS 2
+#endif
 template <int D, int RB, int EPI, bool NORM>
-__global__ __launch_bounds__(256, 2) void rowgemm_kernel(GemmArgs a) {
+__global__ __launch_bounds__(256, EPI == EPI_QKV ? PDM_QKV_WPS : 2) void rowgemm_kernel(GemmArgs a) {
   constexpr int KS = D / 16;
   constexpr int TROWS = 4 * RB * 32;
   constexpr bool DMA = EPI == EPI_QKV;
-  constexpr int NST = DMA ? 4 : 2;
+  constexpr int NST = DMA ? PDM_QKV_NST : 2;
   constexpr int PF = NST - 1;
   constexpr int CHUNK_BYTES = DMA ? 32 * 2 * D : 32 * w_stride<D>();
   __shared__ __attribute__((aligned(16))) char sW[NST][CHUNK_BYTES];
@@ -570,10 +577,10 @@ __global__ __launch_bounds__(256, 2) void rowgemm_kernel(GemmArgs a) {
     }
   };
   if constexpr (DMA) {
-    // before the barrier of chunk c: every DMA but the 2 * WL pieces issued for chunks c + 1 and c + 2 has
-    // landed, whatever number of stores came between (vector memory completes in issue order)
-    constexpr unsigned kWait = 0x0F70u | (2u * WL);
-    static_assert(2 * WL < 16, "vmcnt immediate");
+    // before the barrier of chunk c: every DMA but the (PF - 1) * WL pieces issued for chunks c + 1 ..
+    // c + PF - 1 has landed, whatever number of stores came between (vector memory completes in issue order)
+    constexpr unsigned kWait = 0x0F70u | (unsigned)((PF - 1) * WL);
+    static_assert((PF - 1) * WL < 16, "vmcnt immediate");
     for (int cb = c0; cb < nchunks; cb += NST) {
 #pragma unroll
       for (int k = 0; k < NST; ++k) {
