@@ -153,7 +153,7 @@ def test_autocast_mode_close_to_fp64_and_rounds_like_bf16():
         assert torch.equal(t, t.to(torch.bfloat16).float()), name
     assert y16.dtype == torch.float32
 
-
+    # the 4-layer benchmark stack: B=1024, L_S=384, 16 NS, d 256, FFN 1024, schedule 384/256/128/64
 def test_block_flops_reference_convention():
     # BASELINE workload: B=1024, L_S=384, 16 NS, d 256, FFN 1024, schedule 384/256/128/64
     tot, kv = 0.0, 400
