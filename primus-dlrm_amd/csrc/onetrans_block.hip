@@ -1685,11 +1685,15 @@ struct NsLayout {
   int64_t raw, h, w1p, total;
 };
 
+// Row stride (elements) of the hidden activations h: N plus one 128-byte line, so that the rows an XCD's
+// tiles read at one k step do not all fall into the same few L2 sets (N is a multiple of 64).
+static int64_t ns_h_stride(int64_t N) { return N + 64; }
+
 static NsLayout ns_layout(int64_t B, int64_t K64, int64_t N) {
   NsLayout l{};
   l.raw = 0;
   l.h = align256(B * K64 * 2);
-  l.w1p = l.h + align256(B * N * 2);
+  l.w1p = l.h + align256(B * ns_h_stride(N) * 2);
   l.total = l.w1p + align256(N * K64 * 2);
   return l;
 }
@@ -1798,11 +1802,11 @@ extern "C" int pdm_ns_tokenize_fwd(const pdm_ns_desc* desc, const void* const* t
   g.K = K64;
   g.bias = b1;
   g.out = h;
-  g.out_bstride = N;
+  g.out_bstride = ns_h_stride(N);
   if (int st = launch_ns_gemm<EPI_BIAS_GELU>(g, s)) return st;
   // Linear 2: out = float(bf16(h . W2^T + b2))
   g.A = h;
-  g.a_bstride = N;
+  g.a_bstride = ns_h_stride(N);
   g.W = w2;
   g.K = N;
   g.bias = b2;
