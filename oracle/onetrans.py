@@ -103,18 +103,20 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, num: _Num) -> t
     return num.round(o.transpose(1, 2))  # [B, Lq, H, dh]
 
 
-def block_forward(x: torch.Tensor, w: Dict[str, torch.Tensor], q_len: int, n_heads: int,
-                  mode: str = "autocast", return_parts: bool = False):
-    """OneTransBlock.forward (onetrans.py:220-231) for x [B, kv, D]; the last
-    ``w['ns_qkv'].shape[0]`` tokens of x are the NS-tokens.  With
-    ``return_parts`` also returns the intermediates (h1, q, k, v, o, z, h2, g)."""
-    num = _Num(mode)
+def _num(mode) -> _Num:
+    return mode if isinstance(mode, _Num) else _Num(mode)
+
+
+def attention_inputs(x: torch.Tensor, w: Dict[str, torch.Tensor], q_len: int, n_heads: int, mode="autocast"):
+    """MixedAttention's projections (onetrans.py:124-146) on RMSNorm1(x) (OneTransBlock.forward :224-225):
+    shared S-token QKV Linear on the first kv - n_ns tokens, one QKV matrix per NS-token (the einsum
+    "btn,tmn->btm"), Q cut to its last ``q_len`` rows.  Returns (h1, q [B, q_len, H, dh], k, v [B, kv, H, dh])."""
+    num = _num(mode)
     x = x.to(num.dt)
     B, kv, D = x.shape
     n_ns = w["ns_qkv"].shape[0]
     n_s = kv - n_ns
     dh = D // n_heads
-    # MixedAttention (:124-169)
     h = rmsnorm(x, w["norm1"])
     s_qkv = num.lin(h[:, :n_s], w["s_qkv"]).reshape(B, n_s, 3, n_heads, dh)
     ns_qkv = torch.stack([num.lin(h[:, n_s + t], w["ns_qkv"][t]) for t in range(n_ns)], dim=1) if n_ns else \
@@ -123,28 +125,54 @@ def block_forward(x: torch.Tensor, w: Dict[str, torch.Tensor], q_len: int, n_hea
     q = torch.cat([s_qkv[:, :, 0], ns_qkv[:, :, 0]], dim=1)
     k = torch.cat([s_qkv[:, :, 1], ns_qkv[:, :, 1]], dim=1)
     v = torch.cat([s_qkv[:, :, 2], ns_qkv[:, :, 2]], dim=1)
-    q = q[:, kv - q_len:]
-    o = attention(q, k, v, num).reshape(B, q_len, D)
-    z = num.lin(o, w["out"]) + x[:, kv - q_len:]
-    # MixedFFN (:195-204) on the pre-normed stream, n_s = q_len - n_ns
+    return h, q[:, kv - q_len:], k, v
+
+
+def out_residual(o: torch.Tensor, x_tail: torch.Tensor, w: Dict[str, torch.Tensor], mode="autocast"):
+    """z = out_proj(o) + x[:, kv - q_len:] (onetrans.py:169, :226-227) for o [B, q_len, D]."""
+    num = _num(mode)
+    return num.lin(o.to(num.dt), w["out"]) + x_tail.to(num.dt)
+
+
+def ffn_residual(z: torch.Tensor, w: Dict[str, torch.Tensor], mode="autocast"):
+    """y = z + MixedFFN(RMSNorm2(z), n_s = q_len - n_ns) (onetrans.py:195-204, :229-231): shared
+    Linear -> exact GELU -> Linear on the S rows, per-token matrices on the last n_ns rows.
+    Returns (y, h2, g) with g the GELU activations [B, q_len, F]."""
+    num = _num(mode)
+    z = z.to(num.dt)
+    n_ns = w["ns_w1"].shape[0]
     h2 = rmsnorm(z, w["norm2"])
-    n_s_out = q_len - n_ns
+    n_s_out = z.shape[1] - n_ns
     gelu = lambda t: num.round(torch.nn.functional.gelu(t))  # noqa: E731  exact erf
     g_s = gelu(num.lin(h2[:, :n_s_out], w["s_w1"]))
     g_ns = [gelu(num.lin(h2[:, n_s_out + t], w["ns_w1"][t])) for t in range(n_ns)]
     s_out = num.lin(g_s, w["s_w2"])
     ns_out = [num.lin(g_ns[t], w["ns_w2"][t]) for t in range(n_ns)]
-    ffn = torch.cat([s_out] + [t.unsqueeze(1) for t in ns_out], dim=1)
-    y = z + ffn
+    y = z + torch.cat([s_out] + [t.unsqueeze(1) for t in ns_out], dim=1)
+    g = torch.cat([g_s] + [t.unsqueeze(1) for t in g_ns], dim=1)
+    return y, h2, g
+
+
+def block_forward(x: torch.Tensor, w: Dict[str, torch.Tensor], q_len: int, n_heads: int,
+                  mode="autocast", return_parts: bool = False):
+    """OneTransBlock.forward (onetrans.py:220-231) for x [B, kv, D]; the last
+    ``w['ns_qkv'].shape[0]`` tokens of x are the NS-tokens.  With
+    ``return_parts`` also returns the intermediates (h1, q, k, v, o, z, h2, g)."""
+    num = _num(mode)
+    x = x.to(num.dt)
+    B, kv, D = x.shape
+    h, q, k, v = attention_inputs(x, w, q_len, n_heads, num)
+    o = attention(q, k, v, num).reshape(B, q_len, D)
+    z = out_residual(o, x[:, kv - q_len:], w, num)
+    y, h2, g = ffn_residual(z, w, num)
     if return_parts:
-        g = torch.cat([g_s] + [t.unsqueeze(1) for t in g_ns], dim=1)
         return y, dict(h1=h, q=q.reshape(B, q_len, D), k=k.reshape(B, kv, D), v=v.reshape(B, kv, D), o=o, z=z,
                        h2=h2, g=g)
     return y
 
 
 def stack_forward(x: torch.Tensor, layers: List[Dict[str, torch.Tensor]], schedule: List[int], n_heads: int,
-                  mode: str = "autocast") -> torch.Tensor:
+                  mode="autocast") -> torch.Tensor:
     """The block loop of OneTransModel._backbone (onetrans.py:568-582)."""
     n_ns = layers[0]["ns_qkv"].shape[0]
     for w, q_s in zip(layers, schedule):
@@ -264,3 +292,44 @@ def random_autosplit_weights(K: int, N: int, std: float = 0.05, seed: int = 0) -
     g = torch.Generator().manual_seed(seed)
     r = lambda *shape: _bf16(torch.randn(*shape, generator=g) * std)  # noqa: E731
     return {"w1": r(N, K), "b1": r(N), "w2": r(N, N), "b2": r(N)}
+
+
+def term_magnitudes(x: torch.Tensor, w: Dict[str, torch.Tensor], q_len: int, n_heads: int,
+                    parts: Dict[str, torch.Tensor]) -> Dict[str, torch.Tensor]:
+    """Sum of the absolute terms behind each block intermediate (float64), the scale against which a
+    rounding difference is measured: a dot product's result may move by about one bf16 ulp of its
+    largest terms when an input moves across a rounding boundary or the summation order changes.
+
+    k, v: |h1| . |W_qkv|^T (shared or per-token rows); o: P . |V| with the softmax probabilities P of the
+    bf16 q, k; y (and the update y - x_tail): |o| . |W_out|^T + |g| . |W_2|^T (shared or per-token);
+    h2 (when ``parts`` holds z): the out-projection's terms scaled by RMSNorm2's factor and weight;
+    g (when ``parts`` holds h2): |h2| . |W_1|^T, the FFN-up terms (GELU's slope is at most 1.13)."""
+    B, kv, D = x.shape
+    n_ns = w["ns_qkv"].shape[0]
+    n_s = kv - n_ns
+    dh = D // n_heads
+    f = lambda t: t.double().abs()  # noqa: E731
+    h1 = f(_bf16(parts["h1"].float()))
+    qkv = torch.cat([h1[:, :n_s] @ f(w["s_qkv"]).T] +
+                    [(h1[:, n_s + t] @ f(w["ns_qkv"][t]).T).unsqueeze(1) for t in range(n_ns)], dim=1)
+    q = parts["q"].double().reshape(B, q_len, n_heads, dh).transpose(1, 2)
+    k = parts["k"].double().reshape(B, kv, n_heads, dh).transpose(1, 2)
+    v = f(parts["v"]).reshape(B, kv, n_heads, dh).transpose(1, 2)
+    s = (q @ k.transpose(-1, -2)) / math.sqrt(dh)
+    p = torch.softmax(s.masked_fill(~pyramid_mask(q_len, kv), float("-inf")), dim=-1)
+    o = (p @ v).transpose(1, 2).reshape(B, q_len, D)
+    n_s_out = q_len - n_ns
+    g = f(parts["g"])
+    ffn = torch.cat([g[:, :n_s_out] @ f(w["s_w2"]).T] +
+                    [(g[:, n_s_out + t] @ f(w["ns_w2"][t]).T).unsqueeze(1) for t in range(n_ns)], dim=1)
+    z_terms = f(parts["o"]) @ f(w["out"]).T
+    upd = z_terms + ffn
+    out = dict(k=qkv[..., D:2 * D], v=qkv[..., 2 * D:], q=qkv[:, kv - q_len:, :D], o=o, y=upd)
+    if "z" in parts:
+        z = parts["z"].double()
+        out["h2"] = z_terms * z.pow(2).mean(-1, keepdim=True).add(1e-6).rsqrt() * f(w["norm2"])
+    if "h2" in parts:
+        h2 = f(_bf16(parts["h2"].float()))
+        out["g"] = torch.cat([h2[:, :n_s_out] @ f(w["s_w1"]).T] +
+                             [(h2[:, n_s_out + t] @ f(w["ns_w1"][t]).T).unsqueeze(1) for t in range(n_ns)], dim=1)
+    return out

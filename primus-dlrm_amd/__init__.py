@@ -13,6 +13,7 @@ from .onetrans import (AutoSplitTokenizer, FusedNSTokenizer, FusedSequenceTokeni
                        SequentialTokenizer, build_pyramid_mask, pyramid_schedule)
 from . import ops
 from . import hashing
+from . import synthetic
 from .optim import EmbOptimType, FusedEmbeddingOptimizer, RowWiseAdagrad, WeightDecayMode
 
 __all__ = [

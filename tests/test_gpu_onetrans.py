@@ -1,11 +1,17 @@
 """GPU parity of the OneTrans block kernels against the CPU oracle
-(oracle/onetrans.py, autocast emulation) on the same seeded inputs.
+(oracle/onetrans.py, autocast mode, whose rounding points are pinned against
+torch's CPU autocast) on the same seeded inputs.
 
-Tolerance (bf16 path): every bf16 intermediate (Q, K, V, attention output,
-GELU activations) and the block's update y - x_tail must satisfy
-|got - want| <= 2e-2 * max|want| elementwise and ||got - want||_2 <= 1e-2 * ||want||_2.
-GEMM and softmax summation orders differ from the oracle's, so bf16
-intermediates may round to a neighbouring bf16 value; nothing larger."""
+Tolerance (bf16 path), per element: every bf16 intermediate (Q, K, V,
+attention output, GELU activations) and the block's update y - x_tail
+satisfy |got - want| <= 2e-2 * (|want| + terms), where ``terms`` is the sum
+of the absolute terms of the dot products that produce the value
+(``oracle.onetrans.term_magnitudes``: |h| . |W|^T for a GEMM output, P . |V|
+for attention).  That is the bf16 relative tolerance of 2e-2, measured
+against the magnitude a rounding difference scales with.  Beyond it, fewer
+than 1 % of the elements may differ by more than 2^-7 of that scale (one
+bf16 ulp): GEMM and softmax summation orders differ from the oracle's, so a
+bf16 value may round to its neighbour, and nothing larger."""
 import pytest
 import torch
 
@@ -13,20 +19,21 @@ from oracle import onetrans as ot
 
 pytestmark = pytest.mark.gpu
 
-MAX_TOL = 2e-2
-L2_TOL = 1e-2
+ELEM_TOL = 2e-2
+ULP = 2.0 ** -7
 
 
-def _close(name, got, want):
+def _close(name, got, want, terms=None, tight_frac=0.01):
     got, want = got.double().cpu(), want.double().cpu()
     assert got.shape == want.shape, (name, got.shape, want.shape)
     assert torch.isfinite(got).all(), f"{name}: non-finite values"
-    scale = want.abs().max().item()
+    scale = want.abs() if terms is None else want.abs() + terms.double().reshape(want.shape)
     err = (got - want).abs()
-    assert err.max().item() <= MAX_TOL * scale, f"{name}: max err {err.max().item():.3e} vs scale {scale:.3e}"
-    l2 = ((got - want).norm() / want.norm()).item()
-    assert l2 <= L2_TOL, f"{name}: rel l2 {l2:.3e}"
-    return l2
+    worst = (err / scale.clamp_min(1e-30)).max().item()
+    beyond = (err > ULP * scale).double().mean().item()
+    print(f"{name}: worst err / (|want| + terms) {worst:.2e}, beyond one ulp {beyond:.2e}", flush=True)
+    assert bool((err <= ELEM_TOL * scale).all()), f"{name}: worst err / (|want| + terms) {worst:.3e}"
+    assert beyond < tight_frac, f"{name}: {beyond:.3%} of the elements beyond one bf16 ulp"
 
 
 def _gpu_weights(w, dev):
@@ -44,33 +51,42 @@ def _ws_view(ws, layout, name, shape, dtype=torch.bfloat16):
     return ws[off:off + size].view(dtype)[:n].view(*shape)
 
 
-def _run_case(pdm, dev, B, kv, q_len, n_ns, D=256, F=1024, seed=0, x_std=1.0, w_std=0.02, norm_std=0.0):
+def _check_layer(pdm, dev, x, w, q_len, label=""):
+    """Runs one block on the GPU and checks its intermediates and output against the oracle on the same x."""
+    B, kv, D = x.shape
     H = D // 64
-    w = ot.random_weights(D, F, n_ns, std=w_std, seed=seed, norm_std=norm_std)
-    x = torch.randn(B, kv, D, generator=torch.Generator().manual_seed(seed + 1)) * x_std
+    F = w["s_w1"].shape[0]
+    print(f"block {label} B={B} kv={kv} q_len={q_len} D={D} n_ns={w['ns_qkv'].shape[0]}", flush=True)
     want, parts = ot.block_forward(x, w, q_len, H, mode="autocast", return_parts=True)
+    terms = ot.term_magnitudes(x, w, q_len, H, parts)
     layout = pdm.ops.onetrans_workspace_layout(B, kv, q_len, D, F)
     ws = torch.empty(layout["total"][0], dtype=torch.uint8, device=dev)
     got = pdm.ops.onetrans_block_raw(x.to(dev), _gpu_weights(w, dev), H, q_len, workspace=ws)
     torch.cuda.synchronize()
-    # intermediates still held by the workspace: K, V^T, GELU activations, RMSNorm2 rows
+    # intermediates still held by the workspace: K, V^T, the attention output, GELU activations
     k = _ws_view(ws, layout, "k", (B, kv, D))
     kv_pad = (kv + 31) // 32 * 32
     vt = _ws_view(ws, layout, "vt", (B, H, 64, kv_pad))[..., :kv]
     v = vt.permute(0, 3, 1, 2).reshape(B, kv, D)
     o = _ws_view(ws, layout, "q", (B, q_len, D))
-    _close("k", k, parts["k"])
-    _close("v", v, parts["v"])
-    _close("attention out", o, parts["o"])
-    if "g" in layout:  # the unfused path keeps RMSNorm2 rows and GELU activations in the workspace
+    _close("k", k, parts["k"], terms["k"])
+    _close("v", v, parts["v"], terms["v"])
+    _close("attention out", o, parts["o"], terms["o"])
+    if "g" in layout:  # the tiled path keeps RMSNorm2 rows and GELU activations in the workspace
         g = _ws_view(ws, layout, "g", (B, q_len, F))
         h2 = _ws_view(ws, layout, "h", (B, q_len, D))
-        _close("rmsnorm2", h2, parts["h2"].to(torch.bfloat16))
-        _close("gelu(ffn up)", g, parts["g"])
+        _close("rmsnorm2", h2, parts["h2"].to(torch.bfloat16), terms["h2"])
+        _close("gelu(ffn up)", g, parts["g"], terms["g"])
     x_tail = x[:, kv - q_len:]
-    _close("block update y - x_tail", got.cpu() - x_tail, want - x_tail)
-    _close("block output y", got.cpu(), want)
+    got = got.cpu()
+    _close("block update y - x_tail", got - x_tail, want - x_tail, terms["y"])
     return got
+
+
+def _run_case(pdm, dev, B, kv, q_len, n_ns, D=256, F=1024, seed=0, x_std=1.0, w_std=0.02, norm_std=0.0):
+    w = ot.random_weights(D, F, n_ns, std=w_std, seed=seed, norm_std=norm_std)
+    x = torch.randn(B, kv, D, generator=torch.Generator().manual_seed(seed + 1)) * x_std
+    return _check_layer(pdm, dev, x, w, q_len)
 
 
 @pytest.mark.parametrize("B,kv,q_len,n_ns", [
@@ -93,36 +109,77 @@ def test_block_d384_tiled_path(pdm, dev):
     _run_case(pdm, dev, 5, 45, 21, 3, D=384, F=1536, seed=8, norm_std=0.2)
 
 
+def test_block_d512_tiled_path(pdm, dev):
+    """d_model 512 (8 heads) on the tiled GEMM path."""
+    _run_case(pdm, dev, 3, 40, 20, 3, D=512, F=2048, seed=9, norm_std=0.2)
+
+
 def test_block_baseline_shape_reduced_batch(pdm, dev):
-    """The benchmark's first layer (400 tokens, 16 NS, d 256, FFN 1024) at batch 8."""
+    """The 4-layer benchmark's first layer (400 tokens, 16 NS, d 256, FFN 1024) at batch 8."""
     _run_case(pdm, dev, 8, 400, 400, 16, seed=11)
 
 
-def test_stack_pyramid_matches_oracle(pdm, dev):
-    """OneTransStack with an explicit schedule against the oracle's block loop."""
-    D, F, n_ns, H, B = 256, 1024, 16, 4, 4
-    schedule = [96, 64, 32, 0]
+def test_block_batch1024_short_sequence(pdm, dev):
+    """Batch 1024 (the benchmark's batch: 48 k rows, hundreds of GEMM row tiles and 4096 attention
+    (sample, head) pairs over the persistent grids) at a short sequence of 48 tokens keeping 32."""
+    _run_case(pdm, dev, 1024, 48, 32, 16, seed=12, norm_std=0.1)
+
+
+@pytest.mark.parametrize("B,kv,q_len", [
+    (2, 720, 300),       # above the LDS-resident attention's 608 keys: the streaming attention kernel
+    (1, 1516, 1516),     # the reference OneTransL's first layer (L_S = 1500 + 16 NS, full causal)
+])
+def test_block_long_sequence_streaming_attention(pdm, dev, B, kv, q_len):
+    _run_case(pdm, dev, B, kv, q_len, 16, seed=kv, norm_std=0.1)
+
+
+def _load_block(blk, w):
+    with torch.no_grad():
+        blk.norm1.weight.copy_(w["norm1"])
+        blk.attn.s_qkv.weight.copy_(w["s_qkv"])
+        blk.attn.ns_qkv_weight.copy_(w["ns_qkv"])
+        blk.attn.out_proj.weight.copy_(w["out"])
+        blk.norm2.weight.copy_(w["norm2"])
+        blk.ffn.s_w1.weight.copy_(w["s_w1"])
+        blk.ffn.s_w2.weight.copy_(w["s_w2"])
+        blk.ffn.ns_w1.copy_(w["ns_w1"])
+        blk.ffn.ns_w2.copy_(w["ns_w2"])
+
+
+@pytest.mark.parametrize("B,L_S,schedule", [
+    (16, 384, [384, 256, 128, 64]),   # the benchmark's 4-layer pyramid: (kv, q) = (400,400),(400,272),(272,144),(144,80)
+    (4, 96, [96, 64, 32, 0]),         # down to the NS tokens only
+])
+def test_stack_pyramid_matches_oracle(pdm, dev, B, L_S, schedule):
+    """OneTransStack (the block loop of onetrans.py:568-582) with an explicit schedule.  Each layer is
+    checked element-wise against the oracle on the GPU's own input to that layer; the stack's output
+    equals the chained layers bit for bit, and stays within 1e-2 (relative L2) of the oracle's stack."""
+    D, F, n_ns, H = 256, 1024, 16, 4
     stack = pdm.OneTransStack(D, H, n_ns, len(schedule), schedule=schedule).to(dev).eval()
     layers = []
-    with torch.no_grad():
-        for i, blk in enumerate(stack.blocks):
-            w = ot.random_weights(D, F, n_ns, std=0.02, seed=100 + i, norm_std=0.1)
-            blk.norm1.weight.copy_(w["norm1"])
-            blk.attn.s_qkv.weight.copy_(w["s_qkv"])
-            blk.attn.ns_qkv_weight.copy_(w["ns_qkv"])
-            blk.attn.out_proj.weight.copy_(w["out"])
-            blk.norm2.weight.copy_(w["norm2"])
-            blk.ffn.s_w1.weight.copy_(w["s_w1"])
-            blk.ffn.s_w2.weight.copy_(w["s_w2"])
-            blk.ffn.ns_w1.copy_(w["ns_w1"])
-            blk.ffn.ns_w2.copy_(w["ns_w2"])
-            layers.append(w)
-    x = torch.randn(B, 96 + n_ns, D, generator=torch.Generator().manual_seed(5))
-    got = stack(x.to(dev))
+    for i, blk in enumerate(stack.blocks):
+        w = ot.random_weights(D, F, n_ns, std=0.02, seed=100 + i, norm_std=0.1)
+        _load_block(blk, w)
+        layers.append(w)
+    x = torch.randn(B, L_S + n_ns, D, generator=torch.Generator().manual_seed(5))
+    got = stack(x.to(dev)).cpu()
+    assert got.shape == (B, schedule[-1] + n_ns, D)
+    h = x
+    for i, (w, q_s) in enumerate(zip(layers, schedule)):
+        h = _check_layer(pdm, dev, h, w, q_s + n_ns, label=f"layer {i}")
+    assert torch.equal(got, h)
     want = ot.stack_forward(x, layers, schedule, H)
-    assert got.shape == (B, n_ns, D)
-    _close("stack output", got.cpu(), want)
-    _close("stack update", got.cpu() - x[:, -n_ns:], want - x[:, -n_ns:])
+    drift = ((got.double() - want.double()).norm() / (want.double() - x[:, -got.shape[1]:].double()).norm()).item()
+    print(f"stack drift (relative L2 of the update) {drift:.2e}", flush=True)
+    assert drift <= 1e-2
+
+
+def test_stack_default_schedule_is_reference_pyramid(pdm, dev):
+    """Without an explicit schedule the stack keeps pyramid_schedule(L_S, n_ns, n_layers) queries."""
+    D, n_ns, H = 128, 4, 2
+    stack = pdm.OneTransStack(D, H, n_ns, 3).to(dev).eval()
+    x = torch.randn(2, 40 + n_ns, D, device=dev)
+    assert stack(x).shape == (2, pdm.pyramid_schedule(40, n_ns, 3)[-1] + n_ns, D)
 
 
 def test_block_rejects_bad_shapes(pdm, dev):
