@@ -334,41 +334,57 @@ class EmbeddingBagCollection(nn.Module):
             self._fused_plans["ebc"] = plan
         return plan
 
-    def _pooled_out(self, values: torch.Tensor, offsets: torch.Tensor) -> torch.Tensor:
+    def _pooled_out(self, values: torch.Tensor, offsets: torch.Tensor, padding_idx: int = -1) -> torch.Tensor:
         plan = self._get_plan()
         code = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}[self._output_dtype]
         return torch.ops.pdm.tbe_pooled_fwd(self._store.flat, values, offsets, plan.plan_id, plan.num_slots,
-                                            self._total_dim, code, -1)
+                                            self._total_dim, code, int(padding_idx))
+
+    def pooled_lookup(self, values: torch.Tensor, offsets: torch.Tensor, padding_idx: int = -1) -> torch.Tensor:
+        """Table-batched pooled lookup ``[B, sum D]`` over this collection's feature order (``offsets`` is
+        ``[T*B+1]``), with autograd: when gradients are enabled and the tables require them, the backward
+        is the fused backward + optimizer update of the tables' in-backward optimizer."""
+        weights = [self._store.weight(t.name) for t in self._tables]
+        if torch.is_grad_enabled() and any(w.requires_grad for w in weights):
+            return _FusedPooledLookup.apply(self, values.contiguous(), offsets.contiguous(), int(padding_idx),
+                                            *weights)
+        return self._pooled_out(values, offsets, padding_idx)
 
     def forward(self, features) -> KeyedTensor:
         values, offsets = _kjt_slot_offsets(features, self._feature_names)
-        fused = self.fused_optimizer if torch.is_grad_enabled() else None
-        if fused is not None:
-            weights = [self._store.weight(t.name) for t in self._tables]
-            out = _FusedPooledLookup.apply(self, values.contiguous(), offsets.contiguous(), *weights)
-        else:
-            out = self._pooled_out(values, offsets)
-        return KeyedTensor(self._feature_names, self._dims, out)
+        return KeyedTensor(self._feature_names, self._dims, self.pooled_lookup(values, offsets))
+
+
+_NO_OPTIMIZER = ("the embedding tables have no in-backward optimizer: tag their weights with "
+                 "torch.distributed.optim._apply_optimizer_in_backward(torch.optim.Adam or RowWiseAdagrad, ...) "
+                 "as the reference's wrapper does (primus_dlrm/distributed/wrapper.py:151-174), or set "
+                 "requires_grad=False on them; the lookup's backward is the fused update and produces no "
+                 "weight gradient")
 
 
 class _FusedPooledLookup(torch.autograd.Function):
     """Pooled lookup whose backward is the fused backward + optimizer update (pdm_tbe_backward_fused): the
-    table rows change in place and no weight gradient is produced, as with TorchRec's fused TBE."""
+    table rows change in place and no weight gradient is produced, as with TorchRec's fused TBE.  Ids equal
+    to ``padding_idx`` contribute nothing forward and receive no update."""
 
     @staticmethod
-    def forward(ctx, ebc, values, offsets, *weights):
+    def forward(ctx, ebc, values, offsets, padding_idx, *weights):
         ctx.ebc = ebc
+        ctx.padding_idx = padding_idx
         ctx.save_for_backward(values, offsets)
-        return ebc._pooled_out(values, offsets)
+        return ebc._pooled_out(values, offsets, padding_idx)
 
     @staticmethod
     def backward(ctx, grad_out):
         values, offsets = ctx.saved_tensors
         ebc = ctx.ebc
-        batch = (offsets.numel() - 1) // max(len(ebc._feature_names), 1)
         fo = ebc.fused_optimizer
-        fo.apply(ebc._fused_plan(), ebc._store.flat, values, offsets, batch, grad_out.float().contiguous())
-        return (None, None, None) + (None,) * len(ebc._tables)
+        if fo is None:
+            raise NotImplementedError(_NO_OPTIMIZER)
+        batch = (offsets.numel() - 1) // max(len(ebc._feature_names), 1)
+        fo.apply(ebc._fused_plan(), ebc._store.flat, values, offsets, batch, grad_out.float().contiguous(),
+                 padding_idx=ctx.padding_idx)
+        return (None, None, None, None) + (None,) * len(ebc._tables)
 
 
 class EmbeddingCollection(nn.Module):
@@ -473,6 +489,16 @@ class EmbeddingCollection(nn.Module):
             self._fused_plans[key] = plan
         return self._fused_plans[key]
 
+    def lookup(self, names: Sequence[str], ids: Sequence[torch.Tensor]) -> List[torch.Tensor]:
+        """``weight[ids]`` ``[n_f, D_f]`` per feature, with autograd: when gradients are enabled and the tables
+        require them, the backward is the fused update of the tables' in-backward optimizer."""
+        names = tuple(names)
+        segs = [i.reshape(-1).contiguous() for i in ids]
+        tables = [self._store.weight(t.name) for t in self._tables]
+        if names and torch.is_grad_enabled() and any(w.requires_grad for w in tables):
+            return list(_FusedECLookup.apply(self, names, segs, *tables))
+        return [self.gather(n, seg) for n, seg in zip(names, segs)]
+
     def forward(self, features) -> Dict[str, JaggedTensor]:
         keys = list(features.keys())
         B = features.stride()
@@ -486,14 +512,9 @@ class EmbeddingCollection(nn.Module):
                 continue
             lo, hi = starts[k], starts[k + 1]
             names.append(name)
-            segs.append(values[lo:hi].reshape(-1).contiguous())
+            segs.append(values[lo:hi])
             seg_offs.append(offsets[k * B:(k + 1) * B + 1] - lo)
-        fused = self.fused_optimizer if torch.is_grad_enabled() and names else None
-        if fused is not None:
-            rows = _FusedECLookup.apply(self, tuple(names), segs,
-                                        *[self._store.weight(t.name) for t in self._tables])
-        else:
-            rows = [self.gather(n, seg) for n, seg in zip(names, segs)]
+        rows = self.lookup(names, segs)
         return {n: JaggedTensor(r, offsets=o) for n, r, o in zip(names, rows, seg_offs)}
 
 
@@ -510,6 +531,8 @@ class _FusedECLookup(torch.autograd.Function):
     @staticmethod
     def backward(ctx, *grads):
         ec, names, segs = ctx.ec, ctx.names, ctx.segs
+        if ec.fused_optimizer is None:
+            raise NotImplementedError(_NO_OPTIMIZER)
         dev = ec._store.flat.device
         ns = [int(seg.numel()) for seg in segs]
         dims = [ec._tables[ec._feature_table[n]].embedding_dim for n in names]
@@ -585,8 +608,7 @@ class SequenceGather(nn.Module):
             ids.append([batch[f].reshape(-1).to(torch.int64).contiguous() for f in fs])
             max_len.append(self.max_len[g])
         flat_ids = [t for row in ids for t in row]
-        fused = self.ec.fused_optimizer if torch.is_grad_enabled() else None
-        if fused is not None:
+        if torch.is_grad_enabled() and any(t.requires_grad for t in tables):
             out, mask = _FusedSeqGather.apply(self, ids, offsets, max_len, *tables)
         else:
             out, mask = torch.ops.pdm.seq_gather_fwd(tables, flat_ids, offsets, max_len, self.pad_mode, self.align)
@@ -628,6 +650,8 @@ class _FusedSeqGather(torch.autograd.Function):
         sg = ctx.sg
         ec = sg.ec
         fo = ec.fused_optimizer
+        if fo is None:
+            raise NotImplementedError(_NO_OPTIMIZER)
         tabs = [ec._tables[ti] for ti in sg._feature_tables]
         fo.apply_seq(sg._fused_plan(), ec._store.flat, [t.num_embeddings for t in tabs],
                      [t.embedding_dim for t in tabs], ctx.ids, ctx.offsets, ctx.max_len,
@@ -702,19 +726,16 @@ class TorchRecEmbeddings(nn.Module):
                 values = torch.cat(vals) if len(vals) > 1 else vals[0].contiguous()
                 if values.dtype not in (torch.int32, torch.int64):
                     values = values.to(torch.int64)
-                out = self.ebc.pooled(values, torch.cat(offs), B, padding_idx)
+                out = self.ebc.pooled_lookup(values, torch.cat(offs), padding_idx)
                 col = 0
                 for f in self._pooled_features:
                     D = self._feature_dims[f]
                     results[f] = out[:, col:col + D]
                     col += D
         if self.ec is not None:
-            for f in self._unpooled_features:
-                if f not in features:
-                    continue
-                ids = features[f]
+            present = [f for f in self._unpooled_features if f in features]
+            for f, rows in zip(present, self.ec.lookup(present, [features[f] for f in present])):
                 D = self._feature_dims[f]
-                rows = self.ec.gather(f, ids)
-                B = ids.shape[0]
+                B = features[f].shape[0]
                 results[f] = rows.view(B, D) if f in self._scalar_features else rows.view(B, -1, D)
         return results

@@ -176,14 +176,15 @@ class FusedEmbeddingOptimizer:
         return self._workspace
 
     def apply(self, plan, weights_flat: torch.Tensor, values: torch.Tensor, offsets: torch.Tensor, batch_size: int,
-              grad_out: torch.Tensor) -> None:
+              grad_out: torch.Tensor, padding_idx: int = -1) -> None:
         """The fused backward + update of one pooled batch (called from the autograd backward); ``plan``'s
         state offsets must be this optimizer's (``state_offset``)."""
         from . import ops
 
         self.iter += 1
         ops.tbe_backward_fused_raw(plan, weights_flat, self.momentum1, self.momentum2, values, offsets, batch_size,
-                                   grad_out, workspace=self._ws(plan, values.numel(), batch_size, weights_flat.device),
+                                   grad_out, padding_idx=padding_idx,
+                                   workspace=self._ws(plan, values.numel(), batch_size, weights_flat.device),
                                    **self._hyper())
 
     def apply_seq(self, plan, weights_flat: torch.Tensor, table_rows, table_dims, ids, offsets, max_len,

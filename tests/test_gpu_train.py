@@ -103,6 +103,64 @@ def test_no_grad_forward_does_not_update(pdm, dev):
         out = ebc(kjt).values()
     assert not out.requires_grad
     assert torch.equal(before, ebc._store.flat)
-    # an untagged collection keeps the plain lookup (no graph to the tables)
+    # an untagged collection whose tables require gradients fails loudly at the backward instead of
+    # silently training nothing; with frozen tables it is the plain lookup
     plain = _build(pdm, dev)
-    assert plain.fused_optimizer is None and not plain(kjt).values().requires_grad
+    out = plain(kjt).values()
+    assert plain.fused_optimizer is None and out.requires_grad
+    with pytest.raises(NotImplementedError, match="in-backward optimizer"):
+        out.sum().backward()
+    for p in plain.parameters():
+        p.requires_grad_(False)
+    assert not plain(kjt).values().requires_grad
+
+
+def test_torchrec_embeddings_trains_through_fused_optimizer(pdm, dev):
+    """TorchRecEmbeddings (embedding.py:72-174 of the reference) tagged like the reference's wrapper: the pooled
+    features (padding id 0 filtered) and the unpooled ones update their tables in loss.backward(), matching the
+    oracle's fused Adam on the same bags."""
+    g = np.random.default_rng(12)
+    specs = [pdm.EmbeddingTableConfig("hist", ["h1", "h2"], 400, 32, "mean"),
+             pdm.EmbeddingTableConfig("item", ["item", "seq"], 300, 16, "none")]
+    emb = pdm.TorchRecEmbeddings(specs, device=dev, scalar_feature_names={"item"})
+    kw = {"lr": 0.02, "eps": 1e-8, "weight_decay": 0.0}
+    for p in emb.parameters():
+        _apply_optimizer_in_backward(torch.optim.Adam, [p], kw)
+    B, L = 24, 6
+    h1, h2 = g.integers(0, 400, (B, L)), g.integers(0, 400, (B, L))
+    h1[g.random((B, L)) < 0.4] = 0
+    h1[3] = 0
+    item, seq = g.integers(0, 300, B), g.integers(0, 300, (B, 5))
+    feats = {k: torch.from_numpy(v).to(dev) for k, v in dict(h1=h1, h2=h2, item=item, seq=seq).items()}
+    hist0 = emb.ebc._store.flat.cpu().numpy().view(np.float32).copy()
+    row0 = hist0[:32].copy()
+    item0 = emb.ec._store.flat.cpu().numpy().view(np.float32).copy()
+    G = {k: g.normal(0, 1, s).astype(np.float32) for k, s in
+         (("h1", (B, 32)), ("h2", (B, 32)), ("item", (B, 16)), ("seq", (B, 5, 16)))}
+    out = emb(feats, padding_idx=0)
+    loss = sum((out[k] * torch.from_numpy(v).to(dev)).sum() for k, v in G.items())
+    loss.backward()
+    torch.cuda.synchronize()
+    hp = dict(optimizer=o.ADAM, lr=0.02, eps=1e-8, beta1=0.9, beta2=0.999, weight_decay=0.0, step=1)
+    # pooled: two slots (h1, h2) over the one hist table, mean pooling, padding id 0 filtered
+    slots = [dict(rows=400, weights_offset=0, dim=32, dtype="fp32", pooling="mean", row_bytes=0, out_offset=0),
+             dict(rows=400, weights_offset=0, dim=32, dtype="fp32", pooling="mean", row_bytes=0, out_offset=32)]
+    vals = np.concatenate([h1.reshape(-1), h2.reshape(-1)])
+    offs = o.offsets_np(np.full(2 * B, L))
+    m1, m2 = np.zeros_like(hist0), np.zeros_like(hist0)
+    o.tbe_backward(slots, vals, offs, B, np.concatenate([G["h1"], G["h2"]], 1), padding_idx=0, weights=hist0,
+                   m1=m1, m2=m2, **hp)
+    _close(emb.ebc._store.flat.cpu().numpy().view(np.float32), hist0, "pooled table")
+    assert np.array_equal(emb.ebc._store.flat.cpu().numpy().view(np.float32)[:32], row0)  # padding row 0 untouched
+    # unpooled: one-id bags of item (B) and seq (B * 5) on the item table, as side-by-side slots
+    n = B * 5
+    slots = [dict(rows=300, weights_offset=0, dim=16, dtype="fp32", pooling="sum", row_bytes=0, out_offset=c)
+             for c in (0, 16)]
+    vals = np.concatenate([item, seq.reshape(-1)])
+    lens = np.concatenate([(np.arange(n) < B), np.ones(n, bool)]).astype(np.int64)
+    grad = np.zeros((n, 32), np.float32)
+    grad[:B, :16] = G["item"]
+    grad[:, 16:] = G["seq"].reshape(n, 16)
+    m1, m2 = np.zeros_like(item0), np.zeros_like(item0)
+    o.tbe_backward(slots, vals, o.offsets_np(lens), n, grad, weights=item0, m1=m1, m2=m2, **hp)
+    _close(emb.ec._store.flat.cpu().numpy().view(np.float32), item0, "unpooled table")
