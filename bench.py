@@ -1,12 +1,16 @@
 """Benchmark of the lookup / interaction forward path on one MI355X.
 
-Default workload: the single-hot pooled lookup (26 tables, rows log-uniform
-in [1e3, 4e7], dim 128 bf16, one Zipf(1.05) id per bag, batch 65,536, sum,
-fp32 out).  ``--workload`` selects another:
+Default workload: the quantized-inference TBE, the largest single-GPU lookup
+(64 tables x 5,000,000 rows x dim 128 int8 rowwise with fp16 scale and bias,
+mean pooling over Poisson(20) bags in [1, 100] of Zipf(1.2) ids, batch
+16,384, fp16 out: 42.2 GB of tables, about 21 M lookups per batch).
+``--workload`` selects another:
 
-  ebc_fp32    8 tables x 100,000 x 64 fp32, sum, Poisson(10) bags, B=2048
-  single_hot  (default, above)
-  int8_mean   64 tables x 5,000,000 x 128 int8 rowwise, mean, Poisson(20) bags, B=16,384, fp16 out
+  int8_mean   (default, above)
+  ebc_fp32    8 tables x 100,000 x 64 fp32, sum, Poisson(10) bags, B=2048; also timed as 64 back-to-back
+              batches in one HIP graph (steady state, launch overhead amortised)
+  single_hot  26 tables, rows log-uniform in [1e3, 4e7], dim 128 bf16, one Zipf(1.05) id per bag, B=65,536,
+              sum, fp32 out
   seq_gather  3 behaviour pools, item 10M x 256 + artist 1M x 64 + album 2M x 64 bf16, B=1024
   seq_tokenize  the seq_gather workload fused with one SequentialTokenizer per pool (Linear 384 -> 256,
               GELU, Linear 256 -> 256, + pos_emb of 2048 x 256 fp32), fp32 S-tokens [1024, 768, 256]
@@ -26,8 +30,10 @@ fp32 out).  ``--workload`` selects another:
 A step is one forward of the path over one batch already resident in HBM.
 Prints ONE JSON line with the throughput, the roofline of the dominant kernel
 (algorithmic bytes or FLOPs per launch over its HIP-event-timed average
-duration on the launch stream) and a CPU baseline (the oracle on the host
-cores, bounded sample).
+duration on the launch stream) and a CPU baseline: the reference's own CPU
+path (the PyTorch CPU operators that the unsharded TorchRec modules and the
+OneTrans model reduce to) on the host cores, on the same seeded inputs or a
+bounded sample of them.
 """
 from __future__ import annotations
 
@@ -69,22 +75,131 @@ def traffic_from_profiles(workload: str):
     return None
 
 
-def cpu_threads() -> int:
+def cpu_env():
+    """(threads used, cores in this process's affinity, CPU model).  Every affinity core is used, except
+    that a set OMP_NUM_THREADS (the host's CPU share for this process) caps the count."""
     try:
-        n = len(os.sched_getaffinity(0))
+        aff = len(os.sched_getaffinity(0))
     except AttributeError:
-        n = os.cpu_count() or 1
-    return max(1, min(16, n))
+        aff = os.cpu_count() or 1
+    cap = os.environ.get("OMP_NUM_THREADS", "")
+    used = min(aff, int(cap)) if cap.isdigit() and int(cap) > 0 else aff
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return max(1, used), aff, model
 
 
-def time_cpu(fn, reps: int = 5) -> float:
+def host_mem_available() -> int:
+    try:
+        with open("/proc/meminfo") as f:
+            for line in f:
+                if line.startswith("MemAvailable:"):
+                    return int(line.split()[1]) * 1024
+    except OSError:
+        pass
+    return 0
+
+
+def time_cpu(fn, reps: int = 5, slow_s: float = 4.0) -> tuple:
+    """Median wall time of ``reps`` calls after one warmup call (3 reps when one call takes over ``slow_s``).
+    Returns (seconds, reps)."""
+    t0 = time.perf_counter()
     fn()
+    if time.perf_counter() - t0 > slow_s:
+        reps = min(reps, 3)
     ts = []
     for _ in range(reps):
         t0 = time.perf_counter()
         fn()
         ts.append(time.perf_counter() - t0)
-    return statistics.median(ts)
+    return statistics.median(ts), reps
+
+
+def fill_tiled(torch, dst, block):
+    """Fills the rows of ``dst`` [rows, C] with repeated copies of ``block`` [b, C] (host tables for the CPU
+    baseline: the values do not change the timing, and tiling fills tens of GB in seconds)."""
+    b, rows = block.shape[0], dst.shape[0]
+    full = rows // b
+    if full:
+        dst[:full * b].view(full, b, -1).copy_(block.unsqueeze(0).expand(full, -1, -1))
+    if rows % b:
+        dst[full * b:].copy_(block[:rows % b])
+
+
+def cpu_result(value, unit, threads, path, sample, sec, reps, **extra):
+    used, aff, model = cpu_env()
+    out = {"value": round(value, 1), "unit": unit, "cores": threads, "kind": "port", "path": path,
+           "sample": f"{sample}, median of {reps} reps = {sec:.4g} s", "cpu_model": model, "affinity_cores": aff}
+    out.update(extra)
+    return out
+
+
+GRAPH_BATCHES = 64
+
+
+def graph_steady_state(torch, dev, step, n: int, reps: int = 20) -> float:
+    """Milliseconds per batch of ``n`` back-to-back launches of ``step`` captured in one HIP graph and replayed
+    ``reps`` times (launch overhead amortised: the steady-state rate of a stream of batches)."""
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream(dev).wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(n):
+            step()
+    graph.replay()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        graph.replay()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / (reps * n)
+
+
+def cpu_cross_hash(a, b, table_size: int):
+    """The reference's cross ids on the CPU: ``cross_hash_batch`` is a Python loop of ``xxhash.xxh64`` over
+    ``struct.pack("<qq", a, b)`` modulo the table size (primus_dlrm/data/hashing.py:86-112)."""
+    import struct
+    import xxhash
+
+    pack = struct.Struct("<2q").pack
+    al, bl = a.tolist(), b.tolist()
+
+    def run():
+        return [xxhash.xxh64(pack(x, y), seed=0).intdigest() % table_size for x, y in zip(al, bl)]
+
+    sec, reps = time_cpu(run, reps=3)
+    return sec, reps, "python loop of xxhash.xxh64 over struct-packed int64 pairs (hashing.py cross_hash_batch)"
+
+
+def cpu_kjt(torch, mats, padding_idx: int, threads: int):
+    """``_build_pooled_kjt`` (primus_dlrm/models/embedding.py:179-204) on the CPU: per feature ``mask = ids != pad``,
+    ``lengths = mask.sum(1)``, ``values = ids[mask]``, concatenated, offsets by a cumulative sum."""
+    torch.set_num_threads(threads)
+    feats = [torch.from_numpy(m) for m in mats]
+
+    def run():
+        vals, lens = [], []
+        for ids in feats:
+            mask = ids != padding_idx
+            lens.append(mask.sum(1).to(torch.int32))
+            vals.append(ids[mask])
+        lengths = torch.cat(lens)
+        return torch.cat(vals), lengths, torch.cumsum(lengths.to(torch.int64), 0)
+
+    return time_cpu(run)
 
 
 # ----------------------------------------------------------------------------------------------
@@ -142,42 +257,67 @@ def setup_pooled(pdm, torch, dev, w, weight_std: float):
     return step, alg_bytes, (flat, plan, indices, offsets, out)
 
 
-def cpu_pooled(orc, w, threads: int, row_cap: int, weight_std: float):
-    """The oracle over the same bags on tables capped at ``row_cap`` rows (ids of a
-    capped table are redrawn over the capped rows with the same distribution)."""
+def cpu_pooled(torch, w, threads: int, weight_std: float):
+    """The unsharded TorchRec EmbeddingBagCollection's CPU path: one ``F.embedding_bag(include_last_offset=True)``
+    per table (int8 tables: torch's ``quantized::embedding_bag_byte_rowwise_offsets`` on rows repacked with an
+    fp32 scale and bias after the codes), outputs concatenated in table order (the KeyedTensor values), on the
+    full batch.  Tables are full size when host memory holds them, else every table is row-subsampled to fit
+    and the ids of a subsampled table redrawn over its rows from the same distribution."""
+    import torch.nn.functional as Fn
     import primus_dlrm_amd.synthetic as syn
 
-    g = np.random.default_rng(5)
-    rows = [min(r, row_cap) for r in w.rows]
-    row_bytes = {"fp32": 4 * w.dim, "bf16": 2 * w.dim, "int8": (4 + w.dim + 3) & ~3}[w.dtype]
-    chunks, slots, off, col = [], [], 0, 0
-    for t, r in enumerate(rows):
-        # random finite values: the timing does not depend on them
+    torch.set_num_threads(threads)
+    T, B = len(w.rows), w.batch
+    bpr = {"fp32": 4 * w.dim, "bf16": 2 * w.dim, "int8": w.dim + 8}[w.dtype]
+    budget = int(0.6 * host_mem_available())
+    cap = max(w.rows)
+    if sum(w.rows) * bpr > budget:
+        cap = max(1, budget // (T * bpr))
+    rows = [min(r, cap) for r in w.rows]
+    g = torch.Generator().manual_seed(5)
+    tables = []
+    for r in rows:
+        nb = min(r, 1 << 16)
         if w.dtype == "int8":
-            b = g.integers(0, 256, (r, row_bytes), dtype=np.uint8)
-            b[:, 0:4] = np.frombuffer(np.array([weight_std / 64, -weight_std], np.float16).tobytes(), np.uint8)
-        elif w.dtype == "bf16":
-            b = (g.integers(0, 1 << 16, (r, w.dim), dtype=np.uint16) & 0x807F) | 0x3C00
+            t = torch.empty((r, w.dim + 8), dtype=torch.uint8)
+            block = torch.randint(0, 256, (nb, w.dim + 8), dtype=torch.uint8, generator=g)
+            block[:, w.dim:] = torch.tensor([weight_std / 64, -2 * weight_std], dtype=torch.float32).view(torch.uint8)
         else:
-            b = g.random((r, w.dim), dtype=np.float32) * np.float32(0.02) - np.float32(0.01)
-        b = b.view(np.uint8).reshape(-1)
-        slots.append(dict(rows=r, weights_offset=off, dim=w.dim, dtype=w.dtype, pooling=w.pooling,
-                          row_bytes=row_bytes if w.dtype == "int8" else 0, out_offset=col))
-        chunks.append(b)
-        off += b.size
-        col += w.dim
-    flat = np.concatenate(chunks)
-    idx = w.indices.copy()
-    alpha = {"bf16": 1.05, "int8": 1.2}.get(w.dtype, None)
-    for t, r in enumerate(w.rows):
-        if r > row_cap:
-            seg = slice(w.offsets[t * w.batch], w.offsets[(t + 1) * w.batch])
-            n = int(w.offsets[(t + 1) * w.batch] - w.offsets[t * w.batch])
-            idx[seg] = syn.zipf_rows(syn.rng(99, t), n, row_cap, alpha) if alpha else \
-                syn.rng(99, t).integers(0, row_cap, n)
-    od = "fp32" if w.out_dtype == "fp32" else "fp16"
-    sec = time_cpu(lambda: orc.tbe_pooled(flat, slots, idx, w.offsets, w.batch, -1, od, threads=threads))
-    return w.num_lookups / sec, sec
+            dt = torch.float32 if w.dtype == "fp32" else torch.bfloat16
+            t = torch.empty((r, w.dim), dtype=dt)
+            block = (torch.randn(nb, w.dim, generator=g) * weight_std).to(dt)
+        fill_tiled(torch, t, block)
+        tables.append(t)
+    idx, offs = [], []
+    alpha = {"bf16": 1.05, "int8": 1.2}.get(w.dtype)
+    for t in range(T):
+        lo, hi = int(w.offsets[t * B]), int(w.offsets[(t + 1) * B])
+        ids = w.indices[lo:hi]
+        if rows[t] < w.rows[t]:
+            ids = syn.zipf_rows(syn.rng(99, t), hi - lo, rows[t], alpha) if alpha else \
+                syn.rng(99, t).integers(0, rows[t], hi - lo)
+        idx.append(torch.from_numpy(np.ascontiguousarray(ids)))
+        offs.append(torch.from_numpy(w.offsets[t * B:(t + 1) * B + 1] - lo))
+    out_dt = torch.float32 if w.out_dtype == "fp32" else torch.float16
+    mode = 0 if w.pooling == "sum" else 1
+
+    def run():
+        outs = []
+        for t in range(T):
+            if w.dtype == "int8":
+                outs.append(torch.ops.quantized.embedding_bag_byte_rowwise_offsets(
+                    tables[t], idx[t], offs[t], False, mode, False, None, None, True))
+            else:
+                outs.append(Fn.embedding_bag(idx[t], tables[t], offs[t], mode=w.pooling, include_last_offset=True))
+        return torch.cat(outs, 1).to(out_dt)
+
+    sec, reps = time_cpu(run)
+    size = "full-size tables" if cap >= max(w.rows) else \
+        f"tables row-subsampled to {cap} rows to fit host memory (ids redrawn, same distribution)"
+    op = "quantized::embedding_bag_byte_rowwise_offsets (fp32 scale/bias repack)" if w.dtype == "int8" else \
+        "F.embedding_bag"
+    return w.num_lookups / sec, sec, reps, op, f"full batch of {w.num_lookups} lookups on {size}, " \
+        f"{sum(r * bpr for r in rows) / 1e9:.1f} GB of host tables"
 
 
 # ----------------------------------------------------------------------------------------------
@@ -232,36 +372,39 @@ def setup_train(pdm, torch, dev, w, optimizer: str):
     return step, alg_bytes, distinct, (flat, m1, m2, plan, indices, offsets, grad, ws)
 
 
-def cpu_train(orc, w, optimizer: str, batch: int, row_cap: int):
-    """The oracle's backward + update over the first ``batch`` bags of every table, on tables capped at
-    ``row_cap`` rows (ids taken modulo)."""
+def cpu_train(torch, w, optimizer: str, batch: int, row_cap: int, threads: int):
+    """The PyTorch CPU form of an embedding backward + row-sparse update: per table ``F.embedding_bag`` with a
+    sparse gradient, ``backward`` of the fixed output gradient, then ``torch.optim.SparseAdam`` (Adam; no weight
+    decay there) or ``torch.optim.Adagrad`` (element-wise: torch has no row-wise Adagrad) over the first
+    ``batch`` bags of every table, tables capped at ``row_cap`` rows (ids taken modulo)."""
+    import torch.nn.functional as Fn
+
+    torch.set_num_threads(threads)
     D, T = w.dim, len(w.rows)
     rows = [min(r, row_cap) for r in w.rows]
-    g = np.random.default_rng(8)
-    slots, off = [], 0
+    g = torch.Generator().manual_seed(8)
+    params, idx, offs = [], [], []
     for t, r in enumerate(rows):
-        slots.append(dict(rows=r, weights_offset=off * 4, dim=D, dtype="fp32", pooling="sum", row_bytes=0,
-                          out_offset=t * D))
-        off += r * D
-    lens = np.diff(w.offsets).reshape(T, w.batch)[:, :batch]
-    idx = np.concatenate([w.indices[w.offsets[t * w.batch]:w.offsets[t * w.batch] + int(lens[t].sum())] % rows[t]
-                          for t in range(T)])
-    offsets = orc.offsets_np(lens.reshape(-1))
-    grad = g.standard_normal((batch, T * D), dtype=np.float32)
-    flat = (g.random(off, dtype=np.float32) - np.float32(0.5)) * np.float32(0.02)
-    adam = optimizer == "adam"
-    m1 = np.zeros(off if adam else sum(rows), dtype=np.float32)
-    m2 = np.zeros(off if adam else 1, dtype=np.float32)
-    step = [0]
+        p = torch.empty(r, D)
+        fill_tiled(torch, p, torch.rand(min(r, 1 << 16), D, generator=g) * 0.02 - 0.01)
+        params.append(p.requires_grad_())
+        lo = int(w.offsets[t * w.batch])
+        o = w.offsets[t * w.batch:t * w.batch + batch + 1] - lo
+        idx.append(torch.from_numpy(w.indices[lo:lo + int(o[-1])] % r))
+        offs.append(torch.from_numpy(o))
+    grad = torch.randn(batch, D, generator=g)
+    opt = torch.optim.SparseAdam(params, lr=0.01, eps=1e-8) if optimizer == "adam" else \
+        torch.optim.Adagrad(params, lr=0.01, eps=1e-8)
 
     def run():
-        step[0] += 1
-        orc.tbe_backward(slots, idx, offsets, batch, grad, optimizer=orc.ADAM if adam else orc.ROWWISE_ADAGRAD,
-                         weights=flat, m1=m1, m2=m2, lr=0.01, eps=1e-8, weight_decay=1e-5, wd_mode=orc.WD_L2,
-                         step=step[0])
+        for t in range(T):
+            out = Fn.embedding_bag(idx[t], params[t], offs[t], mode="sum", sparse=True, include_last_offset=True)
+            out.backward(grad)
+        opt.step()
+        opt.zero_grad(set_to_none=True)
 
-    sec = time_cpu(run)
-    return idx.size, sec
+    sec, reps = time_cpu(run)
+    return int(sum(i.numel() for i in idx)), sec, reps
 
 
 def setup_train_seq(pdm, torch, dev, w):
@@ -318,31 +461,34 @@ def setup_train_seq(pdm, torch, dev, w):
     return step, alg_bytes, distinct, kept, (flat, m1, m2, plan, ids, offsets, grad, ws)
 
 
-def cpu_train_seq(orc, w, batch: int, row_cap: int):
-    """The oracle's gather backward + Adam over the first ``batch`` samples, tables capped at ``row_cap`` rows."""
-    g = np.random.default_rng(9)
+def cpu_train_seq(torch, w, batch: int, row_cap: int, threads: int):
+    """The PyTorch CPU form of the S-token gather backward + Adam: the padded lookups of ``cpu_seq`` with sparse
+    gradients on fp32 tables, ``backward`` of the fixed token gradient, ``torch.optim.SparseAdam``, over the
+    first ``batch`` samples, tables capped at ``row_cap`` rows (ids taken modulo)."""
+    import torch.nn.functional as Fn
+
+    torch.set_num_threads(threads)
+    g = torch.Generator().manual_seed(9)
     rows = [min(r, row_cap) for r in w.table_rows]
-    slots, off, col = [], 0, 0
+    params = []
     for r, d in zip(rows, w.table_dims):
-        slots.append(dict(rows=r, weights_offset=off * 4, dim=d, dtype="fp32", pooling="sum", row_bytes=0,
-                          out_offset=col))
-        off += r * d
-        col += d
-    ids = [[a[:o[batch]] % r for a, r in zip(row, rows)] for row, o in zip(w.ids, w.offsets)]
-    offsets = [o[:batch + 1] for o in w.offsets]
+        p = torch.empty(r, d)
+        fill_tiled(torch, p, torch.rand(min(r, 1 << 16), d, generator=g) * 0.02 - 0.01)
+        params.append(p.requires_grad_())
+    padded = _padded_ids(torch, [[a % r for a, r in zip(row, rows)] for row in w.ids], w.offsets, w.max_len, batch)
     S = sum(w.max_len)
-    grad = g.standard_normal((batch, S, col), dtype=np.float32)
-    flat = (g.random(off, dtype=np.float32) - np.float32(0.5)) * np.float32(0.02)
-    m1, m2 = np.zeros(off, np.float32), np.zeros(off, np.float32)
-    step = [0]
+    grad = torch.randn(batch, S, sum(w.table_dims), generator=g)
+    opt = torch.optim.SparseAdam(params, lr=0.01, eps=1e-8)
 
     def run():
-        step[0] += 1
-        orc.seq_gather_backward(slots, ids, offsets, w.max_len, grad, optimizer=orc.ADAM, weights=flat, m1=m1,
-                                m2=m2, lr=0.01, eps=1e-8, weight_decay=1e-5, step=step[0])
+        parts = [torch.cat([Fn.embedding(pid, params[f], sparse=True) for f, pid in enumerate(pool)], -1)
+                 for pool, _ in padded]
+        torch.cat(parts, 1).backward(grad)
+        opt.step()
+        opt.zero_grad(set_to_none=True)
 
-    sec = time_cpu(run)
-    return batch * S, sec
+    sec, reps = time_cpu(run)
+    return batch * S, sec, reps
 
 
 # ----------------------------------------------------------------------------------------------
@@ -376,13 +522,47 @@ def setup_seq(pdm, torch, dev, w):
     return step, alg_bytes, kept, (tables, ids, offs)
 
 
-def cpu_seq(orc, w, row_cap: int):
-    g = np.random.default_rng(6)
-    tabs = [g.integers(0, 1 << 16, (min(r, row_cap), d), dtype=np.uint16) for r, d in zip(w.table_rows,
-                                                                                          w.table_dims)]
-    ids = [[a % min(r, row_cap) for a, r in zip(row, w.table_rows)] for row in w.ids]
-    sec = time_cpu(lambda: orc.seq_gather(tabs, ids, w.offsets, w.max_len))
-    return sec
+def _padded_ids(torch, ids, offsets, max_len, batch=None):
+    """The dataset's jagged -> padded step (primus_dlrm/data/dataset.py:604-626) on the CPU: per pool the last
+    ``L`` events of each sample, right aligned, left padded with id 0; returns [(per-feature [B, L] ids, mask)]."""
+    out = []
+    for p, L in enumerate(max_len):
+        off = torch.from_numpy(offsets[p] if batch is None else offsets[p][:batch + 1])
+        n = (off[1:] - off[:-1]).clamp(max=L)
+        k = torch.arange(L).unsqueeze(0) - (L - n).unsqueeze(1)
+        valid = k >= 0
+        src = (off[1:] - n).unsqueeze(1) + k.clamp(min=0)
+        feats = []
+        for a in ids[p]:
+            t = torch.from_numpy(a)
+            feats.append(torch.where(valid, t[src.clamp(max=max(t.numel() - 1, 0))], 0) if t.numel() else
+                         torch.zeros_like(src))
+        out.append((feats, valid))
+    return out
+
+
+def cpu_seq(torch, w, threads: int):
+    """The reference's S-token input on the CPU: the jagged -> padded ids (dataset.py:604-626), ``W[ids]`` per
+    feature (EmbeddingCollection rows, ``values().view(B, L, D)``), ``cat`` of item | artist | album per pool
+    (onetrans.py:515-520) and of the pools along the sequence (:553-558), with the padding mask, on the full
+    batch over full-size bf16 tables."""
+    torch.set_num_threads(threads)
+    g = torch.Generator().manual_seed(6)
+    tables = []
+    for r, d in zip(w.table_rows, w.table_dims):
+        t = torch.empty((r, d), dtype=torch.bfloat16)
+        fill_tiled(torch, t, (torch.randn(min(r, 1 << 16), d, generator=g) * 0.02).to(torch.bfloat16))
+        tables.append(t)
+
+    def run():
+        parts, masks = [], []
+        for feats, valid in _padded_ids(torch, w.ids, w.offsets, w.max_len):
+            parts.append(torch.cat([tables[f][pid] for f, pid in enumerate(feats)], -1))
+            masks.append(valid)
+        return torch.cat(parts, 1), torch.cat(masks, 1)
+
+    sec, reps = time_cpu(run)
+    return sec, reps, sum(r * d * 2 for r, d in zip(w.table_rows, w.table_dims))
 
 
 # ----------------------------------------------------------------------------------------------
@@ -448,22 +628,34 @@ def unfused_tokenize_ms(pdm, torch, keep, w, reps: int = 20) -> float:
     return a.elapsed_time(b) / reps
 
 
-def cpu_tokenize(w, threads: int, batch: int, row_cap: int):
-    """The oracle (C gather + PyTorch-CPU tokenizer in autocast emulation) on the first ``batch`` samples."""
-    import torch
-    from oracle import onetrans as ot
+def cpu_tokenize(torch, w, threads: int, batch: int):
+    """The reference's S-tokens on the CPU in fp32: the padded lookups and concat of ``cpu_seq`` (full-size
+    tables) for the first ``batch`` samples, then per pool ``SequentialTokenizer`` (Linear(384, 256), exact GELU,
+    Linear(256, 256), + pos_emb(arange(L)); onetrans.py:238-257) and the concat along the sequence."""
+    import torch.nn.functional as Fn
 
     torch.set_num_threads(threads)
-    g = np.random.default_rng(6)
-    # random bf16 bits with bit 14 clear: finite values of magnitude below 2
-    tabs = [g.integers(0, 1 << 16, (min(r, row_cap), dm), dtype=np.uint16) & 0xBFFF
-            for r, dm in zip(w.table_rows, w.table_dims)]
-    offs = [o[:batch + 1] for o in w.offsets]
-    ids = [[a[:int(o[batch])] % min(r, row_cap) for a, r in zip(row, w.table_rows)] for row, o in zip(w.ids, offs)]
+    g = torch.Generator().manual_seed(6)
+    tables = []
+    for r, d in zip(w.table_rows, w.table_dims):
+        t = torch.empty((r, d))
+        fill_tiled(torch, t, torch.randn(min(r, 1 << 16), d, generator=g) * 0.02)
+        tables.append(t)
     K = sum(w.table_dims)
-    ws = [ot.random_tokenizer_weights(K, TOK_D, max(w.max_len), seed=p) for p in range(len(w.max_len))]
-    sec = time_cpu(lambda: ot.seq_tokenize(tabs, ids, offs, w.max_len, ws), reps=3)
-    return sec
+    ws = [dict(w1=torch.randn(TOK_D, K, generator=g) * 0.05, b1=torch.randn(TOK_D, generator=g) * 0.05,
+               w2=torch.randn(TOK_D, TOK_D, generator=g) * 0.05, b2=torch.randn(TOK_D, generator=g) * 0.05,
+               pos=torch.randn(TOK_POS_ROWS, TOK_D, generator=g)) for _ in w.max_len]
+
+    def run():
+        parts = []
+        for p, (feats, _) in enumerate(_padded_ids(torch, w.ids, w.offsets, w.max_len, batch)):
+            raw = torch.cat([tables[f][pid] for f, pid in enumerate(feats)], -1)
+            wt = ws[p]
+            h = Fn.gelu(Fn.linear(raw, wt["w1"], wt["b1"]))
+            parts.append(Fn.linear(h, wt["w2"], wt["b2"]) + wt["pos"][:raw.shape[1]])
+        return torch.cat(parts, 1)
+
+    return time_cpu(run, reps=3)
 
 
 # ----------------------------------------------------------------------------------------------
@@ -525,18 +717,30 @@ def unfused_ns_ms(pdm, torch, keep, reps: int = 20) -> float:
     return a.elapsed_time(b) / reps
 
 
-def cpu_ns(threads: int, batch: int):
-    import torch
-    from oracle import onetrans as ot
+def cpu_ns(torch, threads: int, batch: int):
+    """The reference's NS tokens on the CPU in fp32: one row per scalar feature from full-size tables, the dense
+    parts, ``cat`` (_build_ns_raw, onetrans.py:522-532), then AutoSplitTokenizer's Linear(396, 4096), exact GELU,
+    Linear(4096, 4096), viewed [B, 16, 256] (onetrans.py:260-276)."""
+    import torch.nn.functional as Fn
 
     torch.set_num_threads(threads)
-    g = np.random.default_rng(7)
+    g = torch.Generator().manual_seed(7)
+    tabs = []
+    for _, rows in NS_TABLES:
+        t = torch.empty(rows, NS_DIM)
+        fill_tiled(torch, t, torch.rand(min(rows, 1 << 16), NS_DIM, generator=g) * 0.1 - 0.05)
+        tabs.append(t)
+    ids = [torch.randint(0, rows, (batch,), generator=g) for _, rows in NS_TABLES]
+    dense = [torch.randn(batch, d, generator=g) for d in NS_DENSE]
     K, N = NS_DIM * len(NS_TABLES) + sum(NS_DENSE), NS_D * NS_N
-    tabs = [g.normal(0, 0.05, (100_000, NS_DIM)).astype(np.float32) for _ in NS_TABLES]
-    ids = [g.integers(0, 100_000, batch) for _ in NS_TABLES]
-    dense = [g.normal(0, 1, (batch, d)).astype(np.float32) for d in NS_DENSE]
-    w = ot.random_autosplit_weights(K, N, std=0.02, seed=3)
-    return time_cpu(lambda: ot.ns_tokenize(tabs, ids, dense, w, NS_N), reps=3)
+    w1, b1 = torch.randn(N, K, generator=g) * 0.02, torch.randn(N, generator=g) * 0.02
+    w2, b2 = torch.randn(N, N, generator=g) * 0.02, torch.randn(N, generator=g) * 0.02
+
+    def run():
+        raw = torch.cat([t[i] for t, i in zip(tabs, ids)] + dense, dim=1)
+        return Fn.linear(Fn.gelu(Fn.linear(raw, w1, b1)), w2, b2).view(batch, NS_N, NS_D)
+
+    return time_cpu(run, reps=3)
 
 
 # ----------------------------------------------------------------------------------------------
@@ -544,7 +748,7 @@ def cpu_ns(threads: int, batch: int):
 # ----------------------------------------------------------------------------------------------
 
 def setup_onetrans(pdm, torch, dev, w):
-    from oracle import onetrans as ot  # noqa: F401  (flop convention lives with the oracle)
+    import primus_dlrm_amd.synthetic as syn
 
     D, F, n_ns = w.d_model, w.d_model * w.ffn_mult, w.n_ns
     gen = torch.Generator(device=dev)
@@ -560,7 +764,6 @@ def setup_onetrans(pdm, torch, dev, w):
     ws_size = pdm.ops.onetrans_workspace_layout(w.batch, kv0, kv0, D, F)["total"][0]
     ws = torch.empty(ws_size, dtype=torch.uint8, device=dev)
     outs = []
-    kv = kv0
     for q_s in w.schedule:
         outs.append(torch.empty(w.batch, q_s + n_ns, D, device=dev))
     H = D // 64
@@ -571,23 +774,60 @@ def setup_onetrans(pdm, torch, dev, w):
             pdm.ops.onetrans_block_raw(cur, layers[layer], H, q_s + n_ns, out=outs[layer], workspace=ws)
             cur = outs[layer]
 
-    flops = 0.0
-    for q_s in w.schedule:
-        flops += ot.block_flops(w.batch, kv, q_s + n_ns, D, F, n_ns)
-        kv = q_s + n_ns
-    return step, flops, (x, layers, ws, outs)
+    return step, syn.block_flops(w), syn.block_flops_causal(w), (x, layers, ws, outs)
 
 
-def cpu_onetrans(w, threads: int, batch: int):
-    import torch
-    from oracle import onetrans as ot
+def _torch_block(torch, x, w, q_len: int, n_heads: int):
+    """OneTransBlock.forward as the reference writes it (onetrans.py:74-231) with torch functional ops in fp32:
+    RMSNorm, shared Linear QKV + per-token einsum, SDPA with the bool pyramid mask, out-projection, RMSNorm,
+    shared FFN + per-token einsum FFN, residuals."""
+    import torch.nn.functional as Fn
 
+    B, kv, D = x.shape
+    n_ns = w["ns_qkv"].shape[0]
+    n_s, dh = kv - n_ns, D // n_heads
+
+    def rms(t, wt):
+        return (t * t.pow(2).mean(-1, keepdim=True).add(1e-6).rsqrt()) * wt
+
+    h = rms(x, w["norm1"])
+    sq = Fn.linear(h[:, :n_s], w["s_qkv"]).reshape(B, n_s, 3, n_heads, dh)
+    nq = torch.einsum("btn,tmn->btm", h[:, n_s:], w["ns_qkv"]).reshape(B, n_ns, 3, n_heads, dh)
+    q = torch.cat([sq[:, :, 0], nq[:, :, 0]], 1)[:, kv - q_len:]
+    k = torch.cat([sq[:, :, 1], nq[:, :, 1]], 1)
+    v = torch.cat([sq[:, :, 2], nq[:, :, 2]], 1)
+    mask = torch.arange(kv).unsqueeze(0) <= torch.arange(q_len).unsqueeze(1) + (kv - q_len)
+    o = Fn.scaled_dot_product_attention(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2),
+                                        attn_mask=mask[None, None]).transpose(1, 2).reshape(B, q_len, D)
+    z = Fn.linear(o, w["out"]) + x[:, kv - q_len:]
+    h2 = rms(z, w["norm2"])
+    n_s_out = q_len - n_ns
+    s_out = Fn.linear(Fn.gelu(Fn.linear(h2[:, :n_s_out], w["s_w1"])), w["s_w2"])
+    ns_h = Fn.gelu(torch.einsum("btn,tmn->btm", h2[:, n_s_out:], w["ns_w1"]))
+    ns_out = torch.einsum("btm,tnm->btn", ns_h, w["ns_w2"])
+    return z + torch.cat([s_out, ns_out], 1)
+
+
+def cpu_onetrans(torch, w, threads: int, batch: int):
+    """The reference's 4-layer block stack (the block loop of onetrans.py:568-582) in fp32 torch on the CPU at
+    ``batch`` samples, N(0, 0.02) weights and inputs."""
     torch.set_num_threads(threads)
-    D, F = w.d_model, w.d_model * w.ffn_mult
-    layers = [ot.random_weights(D, F, w.n_ns, seed=i) for i in range(len(w.schedule))]
-    x = torch.randn(batch, w.l_s + w.n_ns, D) * 0.02
-    sec = time_cpu(lambda: ot.stack_forward(x, layers, w.schedule, D // 64), reps=3)
-    return sec
+    g = torch.Generator().manual_seed(1005)
+    D, F, n_ns = w.d_model, w.d_model * w.ffn_mult, w.n_ns
+    r = lambda *shape: torch.randn(*shape, generator=g) * 0.02  # noqa: E731
+    layers = [dict(norm1=torch.ones(D), s_qkv=r(3 * D, D), ns_qkv=r(n_ns, 3 * D, D), out=r(D, D),
+                   norm2=torch.ones(D), s_w1=r(F, D), s_w2=r(D, F), ns_w1=r(n_ns, F, D), ns_w2=r(n_ns, D, F))
+              for _ in w.schedule]
+    x0 = r(batch, w.l_s + n_ns, D)
+
+    def run():
+        with torch.no_grad():
+            x = x0
+            for lw, q_s in zip(layers, w.schedule):
+                x = _torch_block(torch, x, lw, q_s + n_ns, D // 64)
+        return x
+
+    return time_cpu(run, reps=3)
 
 
 # ----------------------------------------------------------------------------------------------
@@ -597,7 +837,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="single_hot",
+    ap.add_argument("--workload", default="int8_mean",
                     choices=["single_hot", "ebc_fp32", "int8_mean", "seq_gather", "seq_tokenize", "ns_tokenize",
                              "onetrans",
                              "cross_hash",
@@ -615,32 +855,33 @@ def main() -> int:
 
     pdm = ge.pdm_import()
     import primus_dlrm_amd.synthetic as syn
-    from oracle import oracle as orc
-
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    threads = cpu_threads()
+    threads, _, cpu_model = cpu_env()
     cpu_fn = None
+    graph_fn = None
 
     if args.workload in ("single_hot", "ebc_fp32", "int8_mean"):
         if args.workload == "single_hot":
-            w, std, cap = syn.single_hot_bf16(), 0.02, 500_000
+            w, std = syn.single_hot_bf16(), 0.02
         elif args.workload == "ebc_fp32":
-            w, std, cap = syn.ebc_fp32(), 0.01, 100_000
+            w, std = syn.ebc_fp32(), 0.01
         else:
-            w, std, cap = syn.int8_mean(), 0.05, 200_000
+            w, std = syn.int8_mean(), 0.05
         step, alg, keep = setup_pooled(pdm, torch, dev, w, std)
         units, unit, bound = w.num_lookups, "lookups/s", "hbm"
         dtype = {"bf16": "bf16->f32", "fp32": "f32", "int8": "u8->f32"}[w.dtype]
         cfg = {"workload": w.name, "tables": w.num_tables, "rows_total": int(sum(w.rows)), "dim": w.dim,
                "batch": w.batch, "lookups_per_batch": w.num_lookups, "pooling": w.pooling,
                "weights": w.dtype, "out": w.out_dtype}
+        if args.workload == "ebc_fp32":
+            def graph_fn():
+                return graph_steady_state(torch, dev, step, GRAPH_BATCHES)
 
         def cpu_fn():
-            val, sec = cpu_pooled(orc, w, threads, cap, std)
-            return {"value": round(val, 1), "unit": unit, "cores": threads, "kind": "port",
-                    "sample": f"C oracle, full batch of {w.num_lookups} lookups on tables capped at {cap} rows "
-                              f"(ids redrawn over the capped rows), median of 5 reps = {sec:.3f} s"}
+            val, sec, reps, op, sample = cpu_pooled(torch, w, threads, std)
+            return cpu_result(val, unit, threads, f"torch {op} per table + cat (unsharded TorchRec EBC)",
+                              sample, sec, reps)
     elif args.workload == "seq_gather":
         w = syn.seq_gather()
         step, alg, kept, keep = setup_seq(pdm, torch, dev, w)
@@ -650,10 +891,10 @@ def main() -> int:
                "out": [w.batch, sum(w.max_len), sum(w.table_dims)]}
 
         def cpu_fn():
-            sec = cpu_seq(orc, w, 1_000_000)
-            return {"value": round(kept / sec, 1), "unit": unit, "cores": 1, "kind": "port",
-                    "sample": f"C oracle (one thread), full batch of {kept} kept events, item table capped at "
-                              f"1,000,000 rows (ids taken modulo), median of 5 reps = {sec:.3f} s"}
+            sec, reps, tb = cpu_seq(torch, w, threads)
+            return cpu_result(kept / sec, unit, threads, "torch jagged->padded ids + W[ids] + cat (EC rows, "
+                              "_build_pool_raw, pool concat)", f"full batch of {kept} kept events on full-size "
+                              f"bf16 tables ({tb / 1e9:.1f} GB)", sec, reps)
     elif args.workload == "seq_tokenize":
         w = syn.seq_gather()
         step, alg, flops, kept, keep = setup_tokenize(pdm, torch, dev, w)
@@ -665,14 +906,13 @@ def main() -> int:
                "out": [w.batch, S, TOK_D], "mlp_gflop_per_step": round(flops / 1e9, 2),
                "timed": "whole fused call (list build, MLP over kept events, padding fill)"}
         cfg["unfused_same_gpu_ms"] = round(unfused_tokenize_ms(pdm, torch, keep, w), 4)
-        cpu_b, cpu_cap = 256, 250_000
+        cpu_b = 256
 
         def cpu_fn():
-            sec = cpu_tokenize(w, threads, cpu_b, cpu_cap)
-            return {"value": round(cpu_b * S / sec, 1), "unit": unit, "cores": threads, "kind": "port",
-                    "sample": f"oracle (C gather + PyTorch-CPU tokenizers, autocast emulation) on the first {cpu_b} "
-                              f"samples ({cpu_b * S} slots), tables capped at {cpu_cap} rows (ids modulo), "
-                              f"median of 3 reps = {sec:.3f} s"}
+            sec, reps = cpu_tokenize(torch, w, threads, cpu_b)
+            return cpu_result(cpu_b * S / sec, unit, threads, "torch fp32: padded lookups + cat, per pool "
+                              "Linear / GELU / Linear + pos_emb (SequentialTokenizer), cat",
+                              f"the first {cpu_b} samples ({cpu_b * S} slots) on full-size fp32 tables", sec, reps)
     elif args.workload == "ns_tokenize":
         B_ = 1024
         step, alg, K_, N_, keep = setup_ns(pdm, torch, dev, B_)
@@ -682,13 +922,12 @@ def main() -> int:
                "ns_input": K_, "d_model": NS_D, "n_ns": NS_N, "gflop_per_step": round(alg / 1e9, 2),
                "timed": "whole call (NS rows gather, W1 padding copy, Linear 1 + bias + GELU, Linear 2 + bias)"}
         cfg["unfused_same_gpu_ms"] = round(unfused_ns_ms(pdm, torch, keep), 4)
-        cpu_b = 1024
 
         def cpu_fn():
-            sec = cpu_ns(threads, cpu_b)
-            return {"value": round(cpu_b / sec, 1), "unit": unit, "cores": threads, "kind": "port",
-                    "sample": f"oracle (numpy row gather + PyTorch-CPU AutoSplitTokenizer, autocast emulation) at "
-                              f"batch {cpu_b}, tables of 100,000 rows, median of 3 reps = {sec:.3f} s"}
+            sec, reps = cpu_ns(torch, threads, B_)
+            return cpu_result(B_ / sec, unit, threads, "torch fp32: scalar rows + dense cat (_build_ns_raw), "
+                              "Linear / GELU / Linear (AutoSplitTokenizer)", f"full batch of {B_} samples on "
+                              "full-size fp32 tables", sec, reps)
     elif args.workload == "cross_hash":
         # user_x_artist cross ids (config.py:151): one (uid, artist_id) pair per row, 100M buckets, salt 0
         n_rows, table_size = 1 << 24, 100_000_000
@@ -705,11 +944,11 @@ def main() -> int:
         alg, units, unit, bound, dtype = n_rows * 24, n_rows, "hashes/s", "hbm", "int64"
         cfg = {"workload": "cross_hash_uid_x_artist_16m", "rows": n_rows, "keys": 2, "table_size": table_size,
                "salt": 0}
+        cpu_rows = 200_000
 
         def cpu_fn():
-            sec = time_cpu(lambda: orc.cross_hash([uid, artist], table_size, 0))
-            return {"value": round(n_rows / sec, 1), "unit": unit, "cores": threads, "kind": "port",
-                    "sample": f"C oracle (XXH64 per row, OpenMP), all {n_rows} rows, median of 5 reps = {sec:.3f} s"}
+            sec, reps, path = cpu_cross_hash(uid[:cpu_rows], artist[:cpu_rows], table_size)
+            return cpu_result(cpu_rows / sec, unit, 1, path, f"the first {cpu_rows} rows", sec, reps)
     elif args.workload in ("train_adam", "train_rowwise_adagrad"):
         optimizer = "adam" if args.workload == "train_adam" else "rowwise_adagrad"
         w = syn.ebc_fp32(scale_rows=100.0, batch=65_536)
@@ -719,14 +958,14 @@ def main() -> int:
                "dim": w.dim, "batch": w.batch, "lookups_per_batch": w.num_lookups, "distinct_rows": distinct,
                "pooling": "sum", "weights": "fp32", "optimizer": optimizer, "lr": 0.01, "eps": 1e-8,
                "weight_decay": 1e-5, "timed": "whole fused backward (linearise, 3 radix passes, accumulate)"}
-        cpu_b, cpu_cap = 16_384, 250_000
+        cpu_b, cpu_cap = 16_384, 1_000_000
 
         def cpu_fn():
-            n, sec = cpu_train(orc, w, optimizer, cpu_b, cpu_cap)
-            return {"value": round(n / sec, 1), "unit": unit, "cores": 1, "kind": "port",
-                    "sample": f"C oracle (one thread): backward + {optimizer} over the first {cpu_b} bags of each "
-                              f"table ({n} lookups) on tables capped at {cpu_cap} rows (ids modulo), "
-                              f"median of 5 reps = {sec:.3f} s"}
+            n, sec, reps = cpu_train(torch, w, optimizer, cpu_b, cpu_cap, threads)
+            opt = "SparseAdam" if optimizer == "adam" else "Adagrad (element-wise)"
+            return cpu_result(n / sec, unit, threads, f"torch F.embedding_bag(sparse=True) backward + {opt}",
+                              f"the first {cpu_b} bags of each table ({n} lookups), tables capped at {cpu_cap} "
+                              "rows (ids modulo)", sec, reps)
     elif args.workload == "train_seq_adam":
         w = syn.seq_gather()
         step, alg, distinct, kept, keep = setup_train_seq(pdm, torch, dev, w)
@@ -737,14 +976,13 @@ def main() -> int:
                "distinct_rows": distinct, "pad": "row0 (pad slots update row 0, as the reference's pad id 0)",
                "optimizer": "adam", "lr": 0.01, "eps": 1e-8, "weight_decay": 1e-5,
                "timed": "whole fused gather backward"}
-        cpu_b, cpu_cap = 256, 250_000
+        cpu_b, cpu_cap = 256, 1_000_000
 
         def cpu_fn():
-            n, sec = cpu_train_seq(orc, w, cpu_b, cpu_cap)
-            return {"value": round(n / sec, 1), "unit": unit, "cores": 1, "kind": "port",
-                    "sample": f"C oracle (one thread, slot placement in numpy): gather backward + Adam over the "
-                              f"first {cpu_b} samples ({n} slots x 3 features) on tables capped at {cpu_cap} rows "
-                              f"(ids modulo), median of 5 reps = {sec:.3f} s"}
+            n, sec, reps = cpu_train_seq(torch, w, cpu_b, cpu_cap, threads)
+            return cpu_result(n / sec, unit, threads, "torch padded F.embedding(sparse=True) + cat, backward, "
+                              "SparseAdam", f"the first {cpu_b} samples ({n} slots x 3 features), tables capped "
+                              f"at {cpu_cap} rows (ids modulo)", sec, reps)
     elif args.workload == "kjt_build":
         # the pooled-history KJT of _build_pooled_kjt (embedding.py:177-204) at the single-hot batch
         F_, B_, L_ = 26, 65_536, 20
@@ -768,10 +1006,9 @@ def main() -> int:
                "kept": kept, "padding_idx": 0}
 
         def cpu_fn():
-            sec = time_cpu(lambda: orc.kjt_from_dense(mats, 0))
-            return {"value": round(units / sec, 1), "unit": unit, "cores": 1, "kind": "port",
-                    "sample": f"numpy oracle (boolean mask per feature, one thread), all {units} ids, median of 5 "
-                              f"reps = {sec:.3f} s"}
+            sec, reps = cpu_kjt(torch, mats, 0, threads)
+            return cpu_result(units / sec, unit, threads, "torch _build_pooled_kjt expression (mask, sum, ids[mask], "
+                              "cat, offsets cumsum)", f"all {units} ids", sec, reps)
     elif args.workload == "copy_1gib":
         # calibration: a plain device copy of 1 GiB (reads 1 GiB, writes 1 GiB) for the HBM counters
         src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
@@ -785,18 +1022,18 @@ def main() -> int:
         cfg = {"workload": "device_copy_1gib"}
     else:
         w = syn.onetrans_block()
-        step, alg, keep = setup_onetrans(pdm, torch, dev, w)
+        step, alg, causal, keep = setup_onetrans(pdm, torch, dev, w)
         units, unit, bound, dtype = w.batch, "samples/s", "mfma", "bf16"
         cfg = {"workload": w.name, "batch": w.batch, "l_s": w.l_s, "n_ns": w.n_ns, "d_model": w.d_model,
                "n_heads": w.n_heads, "ffn": w.d_model * w.ffn_mult, "schedule": w.schedule,
-               "gflop_per_step": round(alg / 1e9, 1)}
-        cpu_batch = 8
+               "gflop_per_step": round(alg / 1e9, 1), "causal_gflop_per_step": round(causal / 1e9, 1)}
+        cpu_batch = 16
 
         def cpu_fn():
-            sec = cpu_onetrans(w, threads, cpu_batch)
-            return {"value": round(cpu_batch / sec, 2), "unit": unit, "cores": threads, "kind": "port",
-                    "sample": f"PyTorch-CPU oracle (autocast emulation, fp32) of the 4-layer stack at batch "
-                              f"{cpu_batch}, median of 3 reps = {sec:.3f} s"}
+            sec, reps = cpu_onetrans(torch, w, threads, cpu_batch)
+            return cpu_result(cpu_batch / sec, unit, threads, "torch fp32 OneTransBlock x4 (Linear, einsum, SDPA "
+                              "with the bool pyramid mask, RMSNorm, GELU)", f"the 4-layer stack at batch {cpu_batch}",
+                              sec, reps)
 
     stream = torch.cuda.current_stream(dev)
     log(f"warmup {args.warmup} steps")
@@ -825,11 +1062,25 @@ def main() -> int:
         roofline = {"bound": "mfma", "achieved": round(achieved, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                     "frac": round(achieved / BF16_PEAK_TFLOPS, 4), "traffic": traffic_from_profiles(args.workload),
                     "algorithmic_flops": alg, "kernel_ms": round(kernel_ms, 5)}
+        if args.workload == "onetrans":
+            # the same step against the FLOPs the causal pyramid needs (no masked keys, no dropped Q rows)
+            ach_c = causal / (kernel_ms * 1e-3) / 1e12
+            roofline.update(causal_flops=causal, achieved_causal=round(ach_c, 1),
+                            frac_causal=round(ach_c / BF16_PEAK_TFLOPS, 4))
     log(f"{value:.4g} {unit}, step {kernel_ms:.4f} ms, {achieved:.1f} {roofline['unit']}")
+    if graph_fn is not None:
+        g_ms = graph_fn()
+        g_ach = alg / (g_ms * 1e-3) / 1e9
+        roofline["graph_steady_state"] = {
+            "batches_per_graph": GRAPH_BATCHES, "ms_per_batch": round(g_ms, 5), "achieved": round(g_ach, 1),
+            "frac": round(g_ach / HBM_PEAK_GBS, 4),
+            "note": "the same launch replayed back to back from one HIP graph; the eager figure above is one "
+                    "batch's launch latency"}
+        log(f"graph steady state: {g_ms:.4f} ms per batch, {g_ach:.1f} GB/s")
 
     cpu = None
     if not args.no_cpu_baseline and cpu_fn is not None:
-        log(f"cpu baseline on {threads} threads")
+        log(f"cpu baseline on {threads} threads ({cpu_model})")
         cpu = cpu_fn()
 
     line = {"metric": METRIC, "value": round(value, 1), "unit": unit, "n_gpus": 1, "steps": args.steps,

@@ -188,3 +188,20 @@ def block_flops(w: BlockWorkload) -> float:
         total += 2 * (q - w.n_ns) * D * F * 2 + 2 * w.n_ns * D * F * 2
         kv = q
     return total * w.batch
+
+
+def block_flops_causal(w: BlockWorkload) -> float:
+    """Forward FLOPs of the work the causal pyramid needs: K and V of every kv token, Q only of the kept
+    queries, attention over the keys each query sees (query i of a layer keeping q of kv tokens sees
+    kv - q + i + 1 keys), the out-projection and FFN of the kept queries."""
+    D, F = w.d_model, w.d_model * w.ffn_mult
+    kv = w.l_s + w.n_ns
+    total = 0.0
+    for q_s in w.schedule:
+        q = q_s + w.n_ns
+        total += 2 * kv * D * 2 * D + 2 * q * D * D           # K, V of all tokens; Q of the kept ones
+        visible = q * (kv - q) + q * (q + 1) // 2              # keys summed over the kept queries
+        total += 4 * D * visible                              # S = Q K^T and O = P V
+        total += 2 * q * D * D + 4 * q * D * F                # out-projection, FFN up and down
+        kv = q
+    return total * w.batch
