@@ -444,6 +444,22 @@ int pdm_kjt_from_dense(const void* const* ids, const int32_t* row_len,
                        int32_t* lengths, int64_t* offsets, void* workspace,
                        int64_t workspace_bytes, pdm_stream_t stream);
 
+/* pdm_kjt_from_dense without a workspace argument and without any device
+ * allocation.  No counterpart in the reference: it is for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  The scan's block sums live in a
+ * library-owned static device array (512 KiB per device, held until the
+ * process ends), so F * B must not exceed PDM_KJT_NOALLOC_MAX_ROWS (larger
+ * inputs return PDM_ERR_INVALID), and calls that overlap on one GPU (on
+ * different streams) race on that array.  Arguments and results are those of
+ * pdm_kjt_from_dense. */
+#define PDM_KJT_NOALLOC_MAX_ROWS 67108864
+int pdm_kjt_from_dense_noalloc(const void* const* ids, const int32_t* row_len,
+                               int32_t num_features, int64_t batch_size,
+                               int32_t index_bits, int64_t padding_idx,
+                               void* values, int32_t* lengths,
+                               int64_t* offsets, pdm_stream_t stream);
+
 /* Reorders the keys of a KJT (values, offsets [num_keys * B + 1]): output key
  * k is input key perm[k] (host array, num_out <= PDM_KJT_MAX_FEATURES; keys
  * may repeat or be dropped).  out_values: capacity of the input's values;

@@ -29,6 +29,7 @@ PDM_SEQ_MAX_FEATURES = 8
 PDM_OPT_ADAM, PDM_OPT_ROWWISE_ADAGRAD, PDM_OPT_NONE = 0, 1, 2
 PDM_WD_NONE, PDM_WD_L2 = 0, 1
 PDM_KJT_MAX_FEATURES = 64
+PDM_KJT_NOALLOC_MAX_ROWS = 67108864
 
 # Every symbol include/pdm.h declares (checked by the ABI test).
 EXPORTED_SYMBOLS = (
@@ -48,6 +49,7 @@ EXPORTED_SYMBOLS = (
     "pdm_seq_gather_backward_fused",
     "pdm_kjt_workspace_size",
     "pdm_kjt_from_dense",
+    "pdm_kjt_from_dense_noalloc",
     "pdm_kjt_permute",
     "pdm_seq_gather_fwd",
     "pdm_seq_tokenize_workspace_size",
@@ -230,6 +232,9 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.pdm_kjt_from_dense.restype = ctypes.c_int
     lib.pdm_kjt_from_dense.argtypes = [ctypes.POINTER(vp), ctypes.POINTER(i32), i32, i64, i32, i64, vp, vp, vp, vp,
                                        i64, vp]
+    lib.pdm_kjt_from_dense_noalloc.restype = ctypes.c_int
+    lib.pdm_kjt_from_dense_noalloc.argtypes = [ctypes.POINTER(vp), ctypes.POINTER(i32), i32, i64, i32, i64, vp, vp,
+                                               vp, vp]
     lib.pdm_kjt_permute.restype = ctypes.c_int
     lib.pdm_kjt_permute.argtypes = [vp, i32, vp, i32, i64, ctypes.POINTER(i32), i32, vp, vp, vp, vp, i64, vp]
     lib.pdm_cross_hash_fwd.restype = ctypes.c_int

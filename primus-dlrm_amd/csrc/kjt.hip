@@ -20,9 +20,16 @@
 //    lane mask, so the output keeps row-major order;
 //  * permute: one wavefront per output row copies its segment.
 #include <algorithm>
+#include <mutex>
 #include <vector>
 
 #include "pdm_common.h"
+
+// Scratch of pdm_kjt_from_dense_noalloc: the scan's block sums, one int64 per 1024 rows, enough for
+// 65,536 x 1024 = 67,108,864 rows (512 KiB, held by every device the library runs on until the process
+// ends).  Host code never passes this name to a kernel: it is a host-side stand-in for the device
+// array, whose per-device address comes from hipGetSymbolAddress (kjt_scratch_ptr below).
+static __device__ __align__(256) int64_t scratch[65536];
 
 namespace pdm {
 
@@ -303,11 +310,11 @@ extern "C" int64_t pdm_kjt_workspace_size(int64_t num_rows) {
   return std::max<int64_t>(scan_blocks(num_rows), 1) * 8;
 }
 
-extern "C" int pdm_kjt_from_dense(const void* const* ids, const int32_t* row_len, int32_t num_features,
-                                  int64_t batch_size, int32_t index_bits, int64_t padding_idx, void* values,
-                                  int32_t* lengths, int64_t* offsets, void* workspace, int64_t workspace_bytes,
-                                  pdm_stream_t stream) {
-  clear_error();
+namespace {
+
+int kjt_from_dense_impl(const void* const* ids, const int32_t* row_len, int32_t num_features, int64_t batch_size,
+                        int32_t index_bits, int64_t padding_idx, void* values, int32_t* lengths, int64_t* offsets,
+                        void* workspace, int64_t workspace_bytes, pdm_stream_t stream) {
   PDM_CHECK_ARG(num_features >= 0 && num_features <= PDM_KJT_MAX_FEATURES, "num_features out of range");
   PDM_CHECK_ARG(index_bits == 32 || index_bits == 64, "index_bits must be 32 or 64");
   PDM_CHECK_ARG(batch_size >= 0, "batch_size < 0");
@@ -400,6 +407,55 @@ extern "C" int pdm_kjt_from_dense(const void* const* ids, const int32_t* row_len
 #undef PDM_KJT_BY_G
 #undef PDM_KJT_LAUNCH
   return PDM_OK;
+}
+
+// Device address of `scratch` on the current device, looked up once per device with that device current.
+int kjt_scratch_ptr(int64_t** out) {
+  static std::mutex mu;
+  static std::vector<int64_t*> ptrs;
+  int dev = 0;
+  PDM_CHECK_HIP(hipGetDevice(&dev));
+  std::lock_guard<std::mutex> lock(mu);
+  if (dev >= (int)ptrs.size()) ptrs.resize(dev + 1, nullptr);
+  if (ptrs[dev] == nullptr) {
+    void* p = nullptr;
+    PDM_CHECK_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    ptrs[dev] = reinterpret_cast<int64_t*>(p);
+  }
+  *out = ptrs[dev];
+  return PDM_OK;
+}
+
+}  // namespace
+
+extern "C" int pdm_kjt_from_dense(const void* const* ids, const int32_t* row_len, int32_t num_features,
+                                  int64_t batch_size, int32_t index_bits, int64_t padding_idx, void* values,
+                                  int32_t* lengths, int64_t* offsets, void* workspace, int64_t workspace_bytes,
+                                  pdm_stream_t stream) {
+  clear_error();
+  return kjt_from_dense_impl(ids, row_len, num_features, batch_size, index_bits, padding_idx, values, lengths,
+                             offsets, workspace, workspace_bytes, stream);
+}
+
+static_assert((int64_t)(sizeof(scratch) / sizeof(int64_t)) * kScanBlock == PDM_KJT_NOALLOC_MAX_ROWS,
+              "the scratch array holds one block sum per 1024 rows of the largest input");
+
+extern "C" int pdm_kjt_from_dense_noalloc(const void* const* ids, const int32_t* row_len, int32_t num_features,
+                                          int64_t batch_size, int32_t index_bits, int64_t padding_idx,
+                                          void* values, int32_t* lengths, int64_t* offsets, pdm_stream_t stream) {
+  clear_error();
+  PDM_CHECK_ARG(num_features >= 0 && batch_size >= 0, "negative size");
+  const int64_t rows = (int64_t)num_features * batch_size;
+  if (rows > PDM_KJT_NOALLOC_MAX_ROWS) {
+    set_error("pdm_kjt_from_dense_noalloc: " + std::to_string(rows) + " rows exceed the no-allocation limit of " +
+              std::to_string((int64_t)PDM_KJT_NOALLOC_MAX_ROWS) + " rows (use pdm_kjt_from_dense with a workspace)");
+    return PDM_ERR_INVALID;
+  }
+  int64_t* sums = nullptr;
+  if (const int rc = kjt_scratch_ptr(&sums)) return rc;
+  // every block sum the scan reads is written by the same call first: nothing needs clearing
+  return kjt_from_dense_impl(ids, row_len, num_features, batch_size, index_bits, padding_idx, values, lengths,
+                             offsets, sums, (int64_t)sizeof(scratch), stream);
 }
 
 extern "C" int pdm_kjt_permute(const void* values, int32_t index_bits, const int64_t* offsets, int32_t num_keys,
