@@ -36,7 +36,8 @@ from typing import List, Optional, Sequence
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-_LIB_PATH = os.path.join(_HERE, "_build", "liboracle.so")
+# PDM_ORACLE_LIB selects another build of the same source (the sanitizer build of ``make -C oracle sanitize``)
+_LIB_PATH = os.environ.get("PDM_ORACLE_LIB") or os.path.join(_HERE, "_build", "liboracle.so")
 _lib = None
 
 F32, F16, BF16, I8 = 0, 1, 2, 3

@@ -11,7 +11,8 @@ import os
 import threading
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libpdm.so")
+# PDM_LIB selects another build of the same sources (e.g. the host-sanitizer build of the csrc Makefile)
+LIB_PATH = os.environ.get("PDM_LIB") or os.path.join(_HERE, "libpdm.so")
 PDM_CROSS_MAX_KEYS = 8
 
 PDM_OK = 0

@@ -969,6 +969,135 @@ __device__ __forceinline__ int swap23(int m) { return (m & ~12) | ((m & 4) << 1)
 // Largest key count held in LDS (K 128 B + V^T 128 B per key).
 constexpr int kAttnLdsMaxKeys = 608;
 
+// One 32-query tile (queries 32 qt .. 32 qt + 31 of the kept tail) of causal bottom-right attention over
+// one head's keys resident in LDS: K rows at sK (LDS row m holds key (m & ~15) | swap23(m & 15), 16-byte
+// piece p at position p ^ ((m >> 1) & 7)) and V^T rows at sV (row d, piece pv of keys 8 pv .. at position
+// pv ^ ((d >> 2) & 3)).  S^T = K Q^T per 32-key tile, online softmax in fp32, O^T += V^T P^T with P^T in
+// registers; qf holds the tile's Q fragments; writes the tile's O rows (bf16) at o + qi * D.
+struct AttnTile {
+  const char* sK;
+  const char* sV;
+  uint16_t* o;  // O row 0 of this (sample, head): o + qi * D for query qi
+  int kvp, q_len, kv, D;
+  float scale_log2;
+};
+
+__device__ __forceinline__ void attn_query_tile(const AttnTile& t, const int qt, const u32x4_t (&qf)[4], int fr,
+                                                int hf) {
+  const int qi0 = qt * 32;
+  const int qi = qi0 + fr;
+  const int off = t.kv - t.q_len;
+  const int p_last = qi + off;  // last key this query sees
+  const int q_last = min(qi0 + 31, t.q_len - 1);
+  const int kv_end = min(t.kv, q_last + off + 1);
+
+  f32x16_t o[2];
+#pragma unroll
+  for (int e = 0; e < 16; ++e) { o[0][e] = 0.0f; o[1][e] = 0.0f; }
+  // m: the shift of the exponentials (log2 units), shared by the two lanes of a query; l: this lane's
+  // share of the softmax denominator.  m is raised only when a score exceeds it by more than 8, so
+  // every exponential stays <= 2^8 and the rescale of O is skipped for most key tiles; the
+  // normalised output does not depend on the shift.
+  float m = -INFINITY, l = 0.0f;
+  // key j0 + 16*(e/8) + hf*8 + e%8 of element e is visible iff 16*(e/8) + e%8 <= lim - j0
+  const int lim = min(p_last, t.kv - 1) - hf * 8;
+  const char* kp = t.sK + fr * 128;
+  const char* vp0 = t.sV + fr * (2 * t.kvp);
+  const char* vp1 = t.sV + (32 + fr) * (2 * t.kvp);
+  int kofs[4], vofs[2];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) kofs[c] = ((2 * c + hf) ^ ((fr >> 1) & 7)) << 4;
+#pragma unroll
+  for (int c2 = 0; c2 < 2; ++c2) vofs[c2] = ((2 * c2 + hf) ^ ((fr >> 2) & 3)) << 4;  // (d >> 2) & 3, d = fr or 32 + fr
+
+  // K and V^T fragments of a key tile are read one tile ahead of their MFMAs
+  u32x4_t kf[4], vf[4];
+  auto kread = [&](int j0, u32x4_t (&f)[4]) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) f[c] = *reinterpret_cast<const u32x4_t*>(kp + j0 * 128 + kofs[c]);
+  };
+  // O^T[d][q] += V^T . P^T; chunk c2 of P^T holds keys j0 + 16*c2 + hf*8 + 0..7, which sit in
+  // piece j0/8 + 2*c2 + hf of V^T row d, at position (j0/8) + ((2*c2 + hf) ^ ((d >> 2) & 3))
+  auto vread = [&](int j0, u32x4_t (&f)[4]) {
+#pragma unroll
+    for (int c2 = 0; c2 < 2; ++c2) {
+      f[2 * c2] = *reinterpret_cast<const u32x4_t*>(vp0 + j0 * 2 + vofs[c2]);
+      f[2 * c2 + 1] = *reinterpret_cast<const u32x4_t*>(vp1 + j0 * 2 + vofs[c2]);
+    }
+  };
+  kread(0, kf);
+  vread(0, vf);
+  for (int j0 = 0; j0 < kv_end; j0 += 32) {
+    const int jn = j0 + 32 < kv_end ? j0 + 32 : j0;  // the last tile re-reads itself
+    // S^T[key][q] = K . Q^T over the 32 LDS rows j0 .. j0+31 (row j0 + fr: piece p at p ^ ((fr >> 1) & 7))
+    f32x16_t s;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) s[e] = 0.0f;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) s = mfma32x32x16(kf[c], qf[c], s);
+    kread(jn, kf);
+    // s[e] is LDS row j0 + (e/4)*8 + hf*4 + e%4, i.e. key j0 + 16*(e/8) + hf*8 + e%8
+    if (j0 + 31 > qi0 + off || j0 + 32 > t.kv) {  // some key of the tile is masked for some query
+      const int r = lim - j0;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) s[e] = (16 * (e >> 3) + (e & 7) <= r) ? s[e] : -INFINITY;
+    }
+    float mx = fmaxf(fmaxf(s[0], s[1]), s[2]);
+#pragma unroll
+    for (int e = 3; e < 15; e += 2) mx = fmaxf(fmaxf(mx, s[e]), s[e + 1]);
+    mx = fmaxf(mx, s[15]);
+    {  // max with the other half of the wave (lane l ^ 32 holds the same query)
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+      mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+    }
+    const float mt = mx * t.scale_log2;  // tile max in log2 units (scale_log2 > 0)
+    if (__builtin_amdgcn_ballot_w64(mt > m + 8.0f)) {
+      const float m_new = fmaxf(m, mt);
+      const float alpha = __builtin_amdgcn_exp2f(m - m_new);  // 0 on the first tile (m = -inf)
+      m = m_new;
+      l *= alpha;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) { o[0][e] *= alpha; o[1][e] *= alpha; }
+    }
+    float ps = 0.0f;
+    uint32_t pk[8];
+#pragma unroll
+    for (int e = 0; e < 16; e += 2) {
+      const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[e], t.scale_log2, -m));
+      const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[e + 1], t.scale_log2, -m));
+      ps += p0 + p1;
+      pk[e >> 1] = pack_bf16x2(p0, p1);
+    }
+    l += ps;
+#pragma unroll
+    for (int c2 = 0; c2 < 2; ++c2) {
+      const u32x4_t pb = {pk[4 * c2], pk[4 * c2 + 1], pk[4 * c2 + 2], pk[4 * c2 + 3]};
+      o[0] = mfma32x32x16(vf[2 * c2], pb, o[0]);
+      o[1] = mfma32x32x16(vf[2 * c2 + 1], pb, o[1]);
+    }
+    vread(jn, vf);
+  }
+  {
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(l), __float_as_uint(l), false, false);
+    l = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+  }
+  if (qi < t.q_len) {
+    // O may be written over Q: the calling wave has read every Q row of this tile, and no other wave reads them
+    const float inv = 1.0f / l;
+    uint16_t* orow = t.o + (int64_t)qi * t.D;
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d = db * 32 + g * 8 + hf * 4;
+        u32x2_t w;
+        w[0] = pack_bf16x2(o[db][4 * g] * inv, o[db][4 * g + 1] * inv);
+        w[1] = pack_bf16x2(o[db][4 * g + 2] * inv, o[db][4 * g + 3] * inv);
+        *reinterpret_cast<u32x2_t*>(orow + d) = w;
+      }
+  }
+}
+
 // NP: 16-byte pieces per thread of K (and of V^T), kv_pad * 8 <= NP * 512.
 template <int NP>
 __global__ __launch_bounds__(512) void attn_lds_kernel(AttnArgs a) {
@@ -980,7 +1109,6 @@ __global__ __launch_bounds__(512) void attn_lds_kernel(AttnArgs a) {
   const int lane = tid & 63, wave = tid >> 6;
   const int fr = lane & 31, hf = lane >> 5;
   const int D = a.H * 64;
-  const int off = a.kv - a.q_len;
   const int BH = a.B * a.H;
 
   // Copy of one head, NP rounds of 512 16-byte pieces for K and for V^T:
@@ -1051,120 +1179,8 @@ __global__ __launch_bounds__(512) void attn_lds_kernel(AttnArgs a) {
 #pragma unroll
       for (int c = 0; c < 4; ++c) f[c] = *reinterpret_cast<const u32x4_t*>(qbase + (int64_t)qi * D + c * 16);
     };
-    // One 32-query tile: S^T, online softmax and O^T over the key tiles up to its causal limit.
-    auto process_tile = [&](const int qt, const u32x4_t (&qf)[4]) {
-      const int qi0 = qt * 32;
-      const int qi = qi0 + fr;
-      const int p_last = qi + off;  // last key this query sees
-      const int q_last = min(qi0 + 31, a.q_len - 1);
-      const int kv_end = min(a.kv, q_last + off + 1);
-
-      f32x16_t o[2];
-#pragma unroll
-      for (int e = 0; e < 16; ++e) { o[0][e] = 0.0f; o[1][e] = 0.0f; }
-      // m: the shift of the exponentials (log2 units), shared by the two lanes of a query; l: this lane's
-      // share of the softmax denominator.  m is raised only when a score exceeds it by more than 8, so
-      // every exponential stays <= 2^8 and the rescale of O is skipped for most key tiles; the
-      // normalised output does not depend on the shift.
-      float m = -INFINITY, l = 0.0f;
-      // key j0 + 16*(e/8) + hf*8 + e%8 of element e is visible iff 16*(e/8) + e%8 <= lim - j0
-      const int lim = min(p_last, a.kv - 1) - hf * 8;
-      const char* kp = sK + fr * 128;
-      const char* vp0 = sV + fr * (2 * kvp);
-      const char* vp1 = sV + (32 + fr) * (2 * kvp);
-      int kofs[4], vofs[2];
-#pragma unroll
-      for (int c = 0; c < 4; ++c) kofs[c] = ((2 * c + hf) ^ ((fr >> 1) & 7)) << 4;
-#pragma unroll
-      for (int c2 = 0; c2 < 2; ++c2) vofs[c2] = ((2 * c2 + hf) ^ ((fr >> 2) & 3)) << 4;  // (d >> 2) & 3, d = fr or 32 + fr
-
-      // K and V^T fragments of a key tile are read one tile ahead of their MFMAs
-      u32x4_t kf[4], vf[4];
-      auto kread = [&](int j0, u32x4_t (&f)[4]) {
-#pragma unroll
-        for (int c = 0; c < 4; ++c) f[c] = *reinterpret_cast<const u32x4_t*>(kp + j0 * 128 + kofs[c]);
-      };
-      // O^T[d][q] += V^T . P^T; chunk c2 of P^T holds keys j0 + 16*c2 + hf*8 + 0..7, which sit in
-      // piece j0/8 + 2*c2 + hf of V^T row d, at position (j0/8) + ((2*c2 + hf) ^ ((d >> 2) & 3))
-      auto vread = [&](int j0, u32x4_t (&f)[4]) {
-#pragma unroll
-        for (int c2 = 0; c2 < 2; ++c2) {
-          f[2 * c2] = *reinterpret_cast<const u32x4_t*>(vp0 + j0 * 2 + vofs[c2]);
-          f[2 * c2 + 1] = *reinterpret_cast<const u32x4_t*>(vp1 + j0 * 2 + vofs[c2]);
-        }
-      };
-      kread(0, kf);
-      vread(0, vf);
-      for (int j0 = 0; j0 < kv_end; j0 += 32) {
-        const int jn = j0 + 32 < kv_end ? j0 + 32 : j0;  // the last tile re-reads itself
-        // S^T[key][q] = K . Q^T over the 32 LDS rows j0 .. j0+31 (row j0 + fr: piece p at p ^ ((fr >> 1) & 7))
-        f32x16_t s;
-#pragma unroll
-        for (int e = 0; e < 16; ++e) s[e] = 0.0f;
-#pragma unroll
-        for (int c = 0; c < 4; ++c) s = mfma32x32x16(kf[c], qf[c], s);
-        kread(jn, kf);
-        // s[e] is LDS row j0 + (e/4)*8 + hf*4 + e%4, i.e. key j0 + 16*(e/8) + hf*8 + e%8
-        if (j0 + 31 > qi0 + off || j0 + 32 > a.kv) {  // some key of the tile is masked for some query
-          const int r = lim - j0;
-#pragma unroll
-          for (int e = 0; e < 16; ++e) s[e] = (16 * (e >> 3) + (e & 7) <= r) ? s[e] : -INFINITY;
-        }
-        float mx = fmaxf(fmaxf(s[0], s[1]), s[2]);
-#pragma unroll
-        for (int e = 3; e < 15; e += 2) mx = fmaxf(fmaxf(mx, s[e]), s[e + 1]);
-        mx = fmaxf(mx, s[15]);
-        {  // max with the other half of the wave (lane l ^ 32 holds the same query)
-          const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
-          mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
-        }
-        const float mt = mx * a.scale_log2;  // tile max in log2 units (scale_log2 > 0)
-        if (__builtin_amdgcn_ballot_w64(mt > m + 8.0f)) {
-          const float m_new = fmaxf(m, mt);
-          const float alpha = __builtin_amdgcn_exp2f(m - m_new);  // 0 on the first tile (m = -inf)
-          m = m_new;
-          l *= alpha;
-#pragma unroll
-          for (int e = 0; e < 16; ++e) { o[0][e] *= alpha; o[1][e] *= alpha; }
-        }
-        float ps = 0.0f;
-        uint32_t pk[8];
-#pragma unroll
-        for (int e = 0; e < 16; e += 2) {
-          const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[e], a.scale_log2, -m));
-          const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[e + 1], a.scale_log2, -m));
-          ps += p0 + p1;
-          pk[e >> 1] = pack_bf16x2(p0, p1);
-        }
-        l += ps;
-#pragma unroll
-        for (int c2 = 0; c2 < 2; ++c2) {
-          const u32x4_t pb = {pk[4 * c2], pk[4 * c2 + 1], pk[4 * c2 + 2], pk[4 * c2 + 3]};
-          o[0] = mfma32x32x16(vf[2 * c2], pb, o[0]);
-          o[1] = mfma32x32x16(vf[2 * c2 + 1], pb, o[1]);
-        }
-        vread(jn, vf);
-      }
-      {
-        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(l), __float_as_uint(l), false, false);
-        l = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
-      }
-      if (qi < a.q_len) {
-        // O is written over Q: this wave has read every Q row of this tile, and no other wave reads them
-        const float inv = 1.0f / l;
-        uint16_t* orow = a.o + ((int64_t)b * a.q_len + qi) * D + h * 64;
-#pragma unroll
-        for (int db = 0; db < 2; ++db)
-#pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            const int d = db * 32 + g * 8 + hf * 4;
-            u32x2_t w;
-            w[0] = pack_bf16x2(o[db][4 * g] * inv, o[db][4 * g + 1] * inv);
-            w[1] = pack_bf16x2(o[db][4 * g + 2] * inv, o[db][4 * g + 3] * inv);
-            *reinterpret_cast<u32x2_t*>(orow + d) = w;
-          }
-      }
-    };
+    const AttnTile at{sK, sV, a.o + (int64_t)b * a.q_len * D + h * 64, kvp, a.q_len, a.kv, D, a.scale_log2};
+    auto process_tile = [&](const int qt, const u32x4_t (&qf)[4]) { attn_query_tile(at, qt, qf, fr, hf); };
     // A wave's first two tiles (all of them while q_len <= 512) have their Q requested before the next
     // head's copy, which then overlaps the whole head: memory reads complete in issue order for the
     // wait counter, so waiting for Q does not wait for the copy.  The code is straight-line up to the

@@ -195,6 +195,30 @@ def test_int8_quantizer_closed_forms():
     assert np.all(err <= scale[:, None] * 0.5 + np.abs(x.min(1) - bias)[:, None] + 1e-6)
     assert q[1, 4:].max() == 255 or q[1, 4:].max() == 254
     assert np.all(q[2:, 4:].max(1) >= 254)  # max element lands at the top code
-    r = 3
-    want_q = np.clip(np.rint((x[r] - bias[r]) * np.float32(1.0 / scale[r])), 0, 255)
-    assert np.array_equal(q[r, 4:], want_q.astype(np.uint8))
+    # every code is the nearest grid point: no neighbouring code decodes closer to x
+    codes = q[:, 4:].astype(np.int64)
+    for dq in (-1, 1):
+        nb = np.clip(codes + dq, 0, 255)
+        dec_nb = nb.astype(np.float32) * scale[:, None] + bias[:, None]
+        assert np.all(np.abs(dec - x) <= np.abs(dec_nb - x) + 1e-7 * np.abs(x))
+    # codes are monotone in x within a row
+    for r in range(2, 40):
+        order = np.argsort(x[r], kind="stable")
+        assert np.all(np.diff(codes[r, order]) >= 0)
+
+
+def test_int8_quantizer_rounds_half_to_even_on_exact_ties():
+    """A row whose grid is exact (bias 0, scale 2^-8: min 0, max 255/256) puts x = (k + 1/2) / 256 exactly halfway
+    between two codes: the quantizer keeps the even one (round half to even), whatever the parity of k."""
+    D = 64
+    k = np.arange(D, dtype=np.float32) * 3 + 1  # codes 1, 4, 7, ... both parities
+    x = ((k + 0.5) / 256.0).astype(np.float32)
+    x[0], x[-1] = 0.0, 255.0 / 256.0  # pin min and max
+    q = o.int8_quantize(x[None, :])
+    sb = q[:, :4].copy().view(np.float16)
+    assert float(sb[0, 0]) == 2.0 ** -8 and float(sb[0, 1]) == 0.0
+    codes = q[0, 4:].astype(np.int64)
+    tie = (k[1:-1] + 0.5).astype(np.float64)
+    want = np.where(np.floor(tie) % 2 == 0, np.floor(tie), np.ceil(tie))
+    assert np.array_equal(codes[1:-1], want.astype(np.int64))
+    assert codes[0] == 0 and codes[-1] == 255
