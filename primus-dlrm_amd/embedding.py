@@ -19,7 +19,9 @@ per-table offsets describe all tables to the kernels.
 from __future__ import annotations
 
 import enum
+import itertools
 import math
+import weakref
 from dataclasses import dataclass, field
 from typing import Callable, Dict, List, Optional, Sequence, Tuple
 
@@ -28,7 +30,7 @@ import torch.nn as nn
 
 from . import _lib as L
 from . import ops
-from .kjt import JaggedTensor, KeyedJaggedTensor, KeyedTensor
+from .kjt import JaggedTensor, KeyedJaggedTensor, KeyedTensor, mask_as_bool
 from .optim import FusedEmbeddingOptimizer, _optimizer_tag
 
 
@@ -138,6 +140,67 @@ def _collection_fused_optimizer(module) -> Optional[FusedEmbeddingOptimizer]:
     return module._fused
 
 
+_OWNERS: Dict[int, "weakref.ReferenceType"] = {}
+_OWNER_IDS = itertools.count(1)
+
+
+def _register_owner(module: nn.Module) -> int:
+    """A process-wide id for ``module``.  The lookup ops carry it (an op's arguments are tensors and scalars)
+    so their backward finds the module's fused optimizer and plans."""
+    oid = next(_OWNER_IDS)
+    _OWNERS[oid] = weakref.ref(module)
+    weakref.finalize(module, _OWNERS.pop, oid, None)
+    return oid
+
+
+def _owner(oid: int):
+    ref = _OWNERS.get(oid)
+    module = ref() if ref is not None else None
+    if module is None:
+        raise RuntimeError(f"the embedding module of this lookup (owner {oid}) no longer exists")
+    return module
+
+
+class _LookupModule(nn.Module):
+    """What the collections and the S-token gather share: an owner id, re-issued for copies, and lookup
+    plans built eagerly whenever the tables move to a GPU, so a compiled forward only reads them."""
+
+    _PLAN_ATTRS: Dict[str, Callable] = {}
+
+    def _build_plans(self) -> None:
+        pass
+
+    def _refresh_plans(self) -> None:
+        for name, empty in self._PLAN_ATTRS.items():
+            old = getattr(self, name, None)
+            for plan in (old.values() if isinstance(old, dict) else [old]):
+                if plan is not None:
+                    plan.release()
+            setattr(self, name, empty())
+        if self._tables_device().type == "cuda":
+            self._build_plans()
+
+    def _tables_device(self) -> torch.device:
+        return self._store.flat.device
+
+    def _apply(self, fn, recurse=True):
+        super()._apply(fn, recurse)
+        self._refresh_plans()
+        return self
+
+    def __getstate__(self):
+        # plans hold device handles: a copy builds its own
+        state = self.__dict__.copy()
+        for name, empty in self._PLAN_ATTRS.items():
+            state[name] = empty()
+        return state
+
+    def __setstate__(self, state):
+        super().__setstate__(state)
+        self._owner_id = _register_owner(self)
+        self._refresh_plans()
+
+
 class _FlatTables(nn.Module):
     """All tables of a collection in one uint8 device buffer, exposed as typed
     per-table ``weight`` views under ``<prefix>.<table>.weight``."""
@@ -231,14 +294,16 @@ def _kjt_slot_offsets(kjt, order: List[str]) -> Tuple[torch.Tensor, torch.Tensor
     missing = [k for k in order if k not in pos]
     if missing:
         raise KeyError(f"KeyedJaggedTensor lacks features {missing}")
-    v, _, o = ops.kjt_permute_raw(values, offsets.contiguous(), len(keys), B, [pos[k] for k in order])
+    v, _, o = torch.ops.pdm.kjt_permute(values, offsets.contiguous(), len(keys), B, [pos[k] for k in order])
     return v, o
 
 
-class EmbeddingBagCollection(nn.Module):
+class EmbeddingBagCollection(_LookupModule):
     """Pooled lookups of several tables in one table-batched launch per
     (dtype, dim) group.  Output ``KeyedTensor`` columns follow table order,
     then feature order inside a table (TorchRec's order)."""
+
+    _PLAN_ATTRS = {"_plan": lambda: None, "_fused_plans": dict}
 
     def __init__(self, tables: List[EmbeddingBagConfig], device: Optional[torch.device] = None,
                  output_dtype: torch.dtype = torch.float32, is_weighted: bool = False):
@@ -273,10 +338,11 @@ class EmbeddingBagCollection(nn.Module):
                 col += t.embedding_dim
         self._total_dim = col
         self._plan: Optional[ops.TbePlan] = None
-        self._plan_device: Optional[torch.device] = None
         self._fused: Optional[FusedEmbeddingOptimizer] = None
         self._fused_key = None
         self._fused_plans: Dict[str, ops.TbePlan] = {}
+        self._owner_id = _register_owner(self)
+        self._refresh_plans()
 
     # TorchRec-style accessors
     @property
@@ -304,11 +370,12 @@ class EmbeddingBagCollection(nn.Module):
                     raise KeyError(f"missing key {key}")
         return None
 
+    def _build_plans(self) -> None:
+        self._plan = ops.TbePlan(self._slots, self._tables_device())
+
     def _get_plan(self) -> ops.TbePlan:
-        dev = self._store.flat.device
-        if self._plan is None or self._plan_device != dev:
-            self._plan = ops.TbePlan(self._slots, dev)
-            self._plan_device = dev
+        if self._plan is None:
+            raise RuntimeError("the collection's tables are not on a GPU")
         return self._plan
 
     def pooled(self, values: torch.Tensor, offsets: torch.Tensor, batch_size: int,
@@ -334,21 +401,15 @@ class EmbeddingBagCollection(nn.Module):
             self._fused_plans["ebc"] = plan
         return plan
 
-    def _pooled_out(self, values: torch.Tensor, offsets: torch.Tensor, padding_idx: int = -1) -> torch.Tensor:
-        plan = self._get_plan()
-        code = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}[self._output_dtype]
-        return torch.ops.pdm.tbe_pooled_fwd(self._store.flat, values, offsets, plan.plan_id, plan.num_slots,
-                                            self._total_dim, code, int(padding_idx))
-
     def pooled_lookup(self, values: torch.Tensor, offsets: torch.Tensor, padding_idx: int = -1) -> torch.Tensor:
         """Table-batched pooled lookup ``[B, sum D]`` over this collection's feature order (``offsets`` is
         ``[T*B+1]``), with autograd: when gradients are enabled and the tables require them, the backward
-        is the fused backward + optimizer update of the tables' in-backward optimizer."""
-        weights = [self._store.weight(t.name) for t in self._tables]
-        if torch.is_grad_enabled() and any(w.requires_grad for w in weights):
-            return _FusedPooledLookup.apply(self, values.contiguous(), offsets.contiguous(), int(padding_idx),
-                                            *weights)
-        return self._pooled_out(values, offsets, padding_idx)
+        is the fused backward + optimizer update of the tables' in-backward optimizer (pdm::tbe_fused_update)."""
+        plan = self._get_plan()
+        code = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}[self._output_dtype]
+        tables = [self._store.weight(t.name) for t in self._tables]
+        return torch.ops.pdm.tbe_pooled_fwd(self._store.flat, tables, values, offsets, plan.plan_id, plan.num_slots,
+                                            self._total_dim, code, int(padding_idx), self._owner_id)
 
     def forward(self, features) -> KeyedTensor:
         values, offsets = _kjt_slot_offsets(features, self._feature_names)
@@ -362,35 +423,59 @@ _NO_OPTIMIZER = ("the embedding tables have no in-backward optimizer: tag their 
                  "weight gradient")
 
 
-class _FusedPooledLookup(torch.autograd.Function):
-    """Pooled lookup whose backward is the fused backward + optimizer update (pdm_tbe_backward_fused): the
-    table rows change in place and no weight gradient is produced, as with TorchRec's fused TBE.  Ids equal
-    to ``padding_idx`` contribute nothing forward and receive no update."""
-
-    @staticmethod
-    def forward(ctx, ebc, values, offsets, padding_idx, *weights):
-        ctx.ebc = ebc
-        ctx.padding_idx = padding_idx
-        ctx.save_for_backward(values, offsets)
-        return ebc._pooled_out(values, offsets, padding_idx)
-
-    @staticmethod
-    def backward(ctx, grad_out):
-        values, offsets = ctx.saved_tensors
-        ebc = ctx.ebc
-        fo = ebc.fused_optimizer
-        if fo is None:
-            raise NotImplementedError(_NO_OPTIMIZER)
-        batch = (offsets.numel() - 1) // max(len(ebc._feature_names), 1)
-        fo.apply(ebc._fused_plan(), ebc._store.flat, values, offsets, batch, grad_out.float().contiguous(),
-                 padding_idx=ctx.padding_idx)
-        return (None, None, None, None) + (None,) * len(ebc._tables)
+def _fused_optimizer_of(module) -> FusedEmbeddingOptimizer:
+    fo = module.fused_optimizer
+    if fo is None:
+        raise NotImplementedError(_NO_OPTIMIZER)
+    return fo
 
 
-class EmbeddingCollection(nn.Module):
+# The lookups' backward is the owner's fused backward + optimizer update: the table rows change in place and
+# no weight gradient is produced, as with TorchRec's fused TBE.  Each update is an op that declares the
+# collection buffer mutated, so a compiled backward keeps it and orders it.  The buffer is kept on the
+# autograd context as an attribute, not a saved tensor: several lookups of one collection in one graph each
+# update it, which a saved tensor's version check would reject.
+
+@torch.library.custom_op("pdm::tbe_fused_update", mutates_args=("flat",))
+def tbe_fused_update(flat: torch.Tensor, indices: torch.Tensor, offsets: torch.Tensor, grad_out: torch.Tensor,
+                     num_slots: int, padding_idx: int, owner_id: int) -> None:
+    """Fused backward + update of an EmbeddingBagCollection's pooled lookup (pdm_tbe_backward_fused); ids equal
+    to ``padding_idx`` receive no update."""
+    ebc = _owner(owner_id)
+    fo = _fused_optimizer_of(ebc)
+    batch = (offsets.numel() - 1) // num_slots
+    fo.apply(ebc._fused_plan(), flat, indices.contiguous(), offsets.contiguous(), batch,
+             grad_out.float().contiguous(), padding_idx=padding_idx)
+
+
+@tbe_fused_update.register_fake
+def _(flat, indices, offsets, grad_out, num_slots, padding_idx, owner_id):
+    return None
+
+
+def _pooled_setup(ctx, inputs, output):
+    flat, tables, indices, offsets, _plan_id, num_slots, _total_dim, _code, padding_idx, owner_id = inputs
+    ctx.flat = flat
+    ctx.save_for_backward(indices, offsets)
+    ctx.n_tables, ctx.num_slots, ctx.padding_idx, ctx.owner_id = len(tables), num_slots, padding_idx, owner_id
+
+
+def _pooled_backward(ctx, grad_out):
+    indices, offsets = ctx.saved_tensors
+    torch.ops.pdm.tbe_fused_update(ctx.flat, indices, offsets, grad_out, ctx.num_slots, ctx.padding_idx,
+                                   ctx.owner_id)
+    return (None, [None] * ctx.n_tables) + (None,) * 8
+
+
+ops.tbe_pooled_fwd.register_autograd(_pooled_backward, setup_context=_pooled_setup)
+
+
+class EmbeddingCollection(_LookupModule):
     """Unpooled lookups: every id of feature f becomes row ``weight[id]`` of
     f's table, bit-exact (a one-id bag summed in fp32 and written in the
     table's dtype is the stored value)."""
+
+    _PLAN_ATTRS = {"_plans": dict, "_fused_plans": dict}
 
     def __init__(self, tables: List[EmbeddingConfig], device: Optional[torch.device] = None):
         super().__init__()
@@ -410,10 +495,12 @@ class EmbeddingCollection(nn.Module):
             for f in t.feature_names:
                 self._feature_names.append(f)
                 self._feature_table[f] = i
-        self._plans: Dict[Tuple[int, str], ops.TbePlan] = {}
+        self._plans: Dict[int, ops.TbePlan] = {}
         self._fused: Optional[FusedEmbeddingOptimizer] = None
         self._fused_key = None
         self._fused_plans: Dict[str, ops.TbePlan] = {}
+        self._owner_id = _register_owner(self)
+        self._refresh_plans()
 
     @property
     def fused_optimizer(self) -> Optional[FusedEmbeddingOptimizer]:
@@ -449,55 +536,53 @@ class EmbeddingCollection(nn.Module):
                     raise KeyError(f"missing key {key}")
         return None
 
-    def _plan_for(self, ti: int) -> ops.TbePlan:
-        dev = self._store.flat.device
-        key = (ti, str(dev))
-        if key not in self._plans:
-            t = self._tables[ti]
-            self._plans[key] = ops.TbePlan([dict(rows=t.num_embeddings, weights_offset=self._store.offsets[ti],
-                                                 dim=t.embedding_dim, dtype=_DT_PDM[t.data_type],
-                                                 pooling=L.PDM_POOL_SUM, row_bytes=_row_bytes(t),
-                                                 out_offset=0)], dev)
-        return self._plans[key]
+    def _build_plans(self) -> None:
+        for ti, t in enumerate(self._tables):
+            self._plans[ti] = ops.TbePlan([dict(rows=t.num_embeddings, weights_offset=self._store.offsets[ti],
+                                                dim=t.embedding_dim, dtype=_DT_PDM[t.data_type],
+                                                pooling=L.PDM_POOL_SUM, row_bytes=_row_bytes(t),
+                                                out_offset=0)], self._tables_device())
+
+    def _gather_table(self, ti: int, ids: torch.Tensor) -> torch.Tensor:
+        """``weight[ids]`` of table ``ti`` for a flat id vector: ``[n, D]`` (one-id bags)."""
+        if ti not in self._plans:
+            raise RuntimeError("the collection's tables are not on a GPU")
+        ids = ids.reshape(-1).contiguous()
+        n = ids.numel()
+        offsets = torch.arange(n + 1, dtype=torch.int64, device=ids.device)
+        return ops.tbe_pooled_raw(self._plans[ti], self._store.flat, ids, offsets, n,
+                                  _DT_TORCH[self._tables[ti].data_type])
 
     def gather(self, feature: str, ids: torch.Tensor) -> torch.Tensor:
         """``weight[ids]`` for a flat id vector of ``feature``: ``[n, D]``."""
-        ti = self._feature_table[feature]
-        t = self._tables[ti]
-        ids = ids.reshape(-1)
-        if not ids.is_contiguous():
-            ids = ids.contiguous()
-        n = ids.numel()
-        offsets = torch.arange(n + 1, dtype=torch.int64, device=ids.device)
-        return ops.tbe_pooled_raw(self._plan_for(ti), self._store.flat, ids, offsets, n, _DT_TORCH[t.data_type])
+        return self._gather_table(self._feature_table[feature], ids)
 
-    def _fused_plan(self, names: Tuple[str, ...]) -> ops.TbePlan:
-        """One slot per feature of ``names`` (sum, column of the feature) with the optimizer's state offsets."""
-        key = f"ec:{names}:{self._store.flat.device}"
+    def _fused_plan(self, table_index: Sequence[int]) -> ops.TbePlan:
+        """One slot per looked-up feature (its table ``table_index[k]``, sum, the feature's column) with the
+        optimizer's state offsets."""
+        key = f"ec:{tuple(table_index)}"
         if key not in self._fused_plans:
             slots, col = [], 0
-            for n in names:
-                ti = self._feature_table[n]
+            for ti in table_index:
                 t = self._tables[ti]
                 slots.append(dict(rows=t.num_embeddings, weights_offset=self._store.offsets[ti], dim=t.embedding_dim,
                                   dtype=_DT_PDM[t.data_type], pooling=L.PDM_POOL_SUM, row_bytes=_row_bytes(t),
                                   out_offset=col))
                 col += t.embedding_dim
             plan = ops.TbePlan(slots, self._store.flat.device)
-            plan.set_state_offsets([self._fused.state_offset[self._tables[self._feature_table[n]].name]
-                                    for n in names])
+            plan.set_state_offsets([self._fused.state_offset[self._tables[ti].name] for ti in table_index])
             self._fused_plans[key] = plan
         return self._fused_plans[key]
 
     def lookup(self, names: Sequence[str], ids: Sequence[torch.Tensor]) -> List[torch.Tensor]:
         """``weight[ids]`` ``[n_f, D_f]`` per feature, with autograd: when gradients are enabled and the tables
         require them, the backward is the fused update of the tables' in-backward optimizer."""
-        names = tuple(names)
-        segs = [i.reshape(-1).contiguous() for i in ids]
+        if not names:
+            return []
+        segs = [i.reshape(-1) for i in ids]
         tables = [self._store.weight(t.name) for t in self._tables]
-        if names and torch.is_grad_enabled() and any(w.requires_grad for w in tables):
-            return list(_FusedECLookup.apply(self, names, segs, *tables))
-        return [self.gather(n, seg) for n, seg in zip(names, segs)]
+        return list(torch.ops.pdm.ec_lookup(self._store.flat, tables, segs,
+                                            [self._feature_table[n] for n in names], self._owner_id))
 
     def forward(self, features) -> Dict[str, JaggedTensor]:
         keys = list(features.keys())
@@ -518,40 +603,64 @@ class EmbeddingCollection(nn.Module):
         return {n: JaggedTensor(r, offsets=o) for n, r, o in zip(names, rows, seg_offs)}
 
 
-class _FusedECLookup(torch.autograd.Function):
-    """Unpooled lookups whose backward is the fused update: every id of feature f is a one-id bag of slot f;
-    the features' bag counts are padded to the largest with empty bags, and the output gradients are laid side
-    by side in one [max n_f, sum D] buffer (pdm_tbe_backward_fused)."""
-
-    @staticmethod
-    def forward(ctx, ec, names, segs, *tables):
-        ctx.ec, ctx.names, ctx.segs = ec, names, segs
-        return tuple(ec.gather(n, seg) for n, seg in zip(names, segs))
-
-    @staticmethod
-    def backward(ctx, *grads):
-        ec, names, segs = ctx.ec, ctx.names, ctx.segs
-        if ec.fused_optimizer is None:
-            raise NotImplementedError(_NO_OPTIMIZER)
-        dev = ec._store.flat.device
-        ns = [int(seg.numel()) for seg in segs]
-        dims = [ec._tables[ec._feature_table[n]].embedding_dim for n in names]
-        bags = max(ns)
-        g_all = torch.zeros((bags, sum(dims)), dtype=torch.float32, device=dev)
-        col = 0
-        for gr, n, d in zip(grads, ns, dims):
-            if gr is not None:
-                g_all[:n, col:col + d] = gr
-            col += d
-        ar = torch.arange(bags, device=dev)
-        lengths = torch.cat([(ar < n).to(torch.int64) for n in ns])
-        offsets = torch.zeros(lengths.numel() + 1, dtype=torch.int64, device=dev)
-        torch.cumsum(lengths, 0, out=offsets[1:])
-        ec.fused_optimizer.apply(ec._fused_plan(names), ec._store.flat, torch.cat(segs), offsets, bags, g_all)
-        return (None, None, None) + (None,) * len(ec._tables)
+@torch.library.custom_op("pdm::ec_lookup", mutates_args=())
+def ec_lookup(flat: torch.Tensor, tables: List[torch.Tensor], ids: List[torch.Tensor], table_index: List[int],
+              owner_id: int) -> List[torch.Tensor]:
+    """``tables[table_index[k]][ids[k]]`` per looked-up feature k, read from the collection buffer ``flat``."""
+    ec = _owner(owner_id)
+    return [ec._gather_table(ti, seg) for ti, seg in zip(table_index, ids)]
 
 
-class SequenceGather(nn.Module):
+@ec_lookup.register_fake
+def _(flat, tables, ids, table_index, owner_id):
+    return [tables[ti].new_empty((seg.shape[0], tables[ti].shape[1])) for ti, seg in zip(table_index, ids)]
+
+
+@torch.library.custom_op("pdm::ec_fused_update", mutates_args=("flat",))
+def ec_fused_update(flat: torch.Tensor, ids: List[torch.Tensor], grads: List[torch.Tensor], table_index: List[int],
+                    owner_id: int) -> None:
+    """Fused backward + update of an EmbeddingCollection's unpooled lookups (pdm_tbe_backward_fused): every id
+    of feature k is a one-id bag of slot k; the features' bag counts are padded to the largest with empty
+    bags, and the output gradients are laid side by side in one [max n_k, sum D] buffer."""
+    ec = _owner(owner_id)
+    fo = _fused_optimizer_of(ec)
+    dev = flat.device
+    ns = [int(seg.numel()) for seg in ids]
+    dims = [ec._tables[ti].embedding_dim for ti in table_index]
+    bags = max(ns)
+    g_all = torch.zeros((bags, sum(dims)), dtype=torch.float32, device=dev)
+    col = 0
+    for gr, n, d in zip(grads, ns, dims):
+        g_all[:n, col:col + d] = gr
+        col += d
+    ar = torch.arange(bags, device=dev)
+    lengths = torch.cat([(ar < n).to(torch.int64) for n in ns])
+    offsets = torch.nn.functional.pad(lengths.cumsum(0), (1, 0))
+    fo.apply(ec._fused_plan(table_index), flat, torch.cat([seg.contiguous() for seg in ids]), offsets, bags, g_all)
+
+
+@ec_fused_update.register_fake
+def _(flat, ids, grads, table_index, owner_id):
+    return None
+
+
+def _ec_setup(ctx, inputs, output):
+    flat, tables, ids, table_index, owner_id = inputs
+    ctx.flat = flat
+    ctx.save_for_backward(*ids)
+    ctx.n_tables, ctx.table_index, ctx.owner_id = len(tables), list(table_index), owner_id
+
+
+def _ec_backward(ctx, grads):
+    ids = list(ctx.saved_tensors)
+    torch.ops.pdm.ec_fused_update(ctx.flat, ids, [g.contiguous() for g in grads], ctx.table_index, ctx.owner_id)
+    return None, [None] * ctx.n_tables, [None] * len(ids), None, None
+
+
+ec_lookup.register_autograd(_ec_backward, setup_context=_ec_setup)
+
+
+class SequenceGather(_LookupModule):
     """Jagged behaviour-pool ids -> padded S-token rows on the device.
 
     ``sequence_groups`` maps a pool name to its features (concat order per
@@ -584,6 +693,10 @@ class SequenceGather(nn.Module):
                 if self.ec._feature_table[a] != self.ec._feature_table[b]:
                     raise ValueError("the k-th feature of every pool must share one table")
         self._feature_tables = [ec._feature_table[f] for f in first]
+        self._owner_id = _register_owner(self)
+
+    def _tables_device(self) -> torch.device:
+        return self.ec._store.flat.device
 
     def slot_ranges(self) -> Dict[str, Tuple[int, int]]:
         out, s = {}, 0
@@ -602,17 +715,12 @@ class SequenceGather(nn.Module):
         ids, offsets, max_len = [], [], []
         for g, fs in self.groups.items():
             lengths = batch[fs[0] + "__lengths"]
-            off = torch.zeros(lengths.numel() + 1, dtype=torch.int64, device=lengths.device)
-            torch.cumsum(lengths.to(torch.int64), 0, out=off[1:])
-            offsets.append(off)
-            ids.append([batch[f].reshape(-1).to(torch.int64).contiguous() for f in fs])
+            offsets.append(torch.nn.functional.pad(lengths.reshape(-1).to(torch.int64).cumsum(0), (1, 0)))
+            ids.extend(batch[f].reshape(-1).to(torch.int64).contiguous() for f in fs)
             max_len.append(self.max_len[g])
-        flat_ids = [t for row in ids for t in row]
-        if torch.is_grad_enabled() and any(t.requires_grad for t in tables):
-            out, mask = _FusedSeqGather.apply(self, ids, offsets, max_len, *tables)
-        else:
-            out, mask = torch.ops.pdm.seq_gather_fwd(tables, flat_ids, offsets, max_len, self.pad_mode, self.align)
-        return out, mask.view(torch.bool)
+        out, mask = torch.ops.pdm.seq_gather_fwd(self.ec._store.flat, tables, ids, offsets, max_len, self.pad_mode,
+                                                 self.align, self._owner_id)
+        return out, mask_as_bool(mask)
 
     def _fused_plan(self) -> ops.TbePlan:
         """One slot per feature (fp32 table, sum, column of the feature) with the EC optimizer's state offsets."""
@@ -633,30 +741,43 @@ class SequenceGather(nn.Module):
         return ec._fused_plans[key]
 
 
-class _FusedSeqGather(torch.autograd.Function):
-    """S-token gather whose backward is the fused backward + optimizer update of the EC's tables
-    (pdm_seq_gather_backward_fused): rows change in place, no weight gradient is produced."""
+@torch.library.custom_op("pdm::seq_fused_update", mutates_args=("flat",))
+def seq_fused_update(flat: torch.Tensor, ids: List[torch.Tensor], offsets: List[torch.Tensor], max_len: List[int],
+                     grad_out: torch.Tensor, owner_id: int) -> None:
+    """Fused backward + update of a SequenceGather's tables (pdm_seq_gather_backward_fused); ``ids`` is
+    pool-major as for pdm::seq_gather_fwd."""
+    sg = _owner(owner_id)
+    ec = sg.ec
+    fo = _fused_optimizer_of(ec)
+    tabs = [ec._tables[ti] for ti in sg._feature_tables]
+    F = len(tabs)
+    grid = [ids[p * F:(p + 1) * F] for p in range(len(offsets))]
+    fo.apply_seq(sg._fused_plan(), flat, [t.num_embeddings for t in tabs], [t.embedding_dim for t in tabs], grid,
+                 offsets, max_len, grad_out.float().contiguous(), sg.pad_mode, sg.align)
 
-    @staticmethod
-    def forward(ctx, sg, ids, offsets, max_len, *tables):
-        ctx.sg, ctx.ids, ctx.offsets, ctx.max_len = sg, ids, offsets, max_len
-        flat_ids = [t for row in ids for t in row]
-        out, mask = torch.ops.pdm.seq_gather_fwd(list(tables), flat_ids, offsets, max_len, sg.pad_mode, sg.align)
-        ctx.mark_non_differentiable(mask)
-        return out, mask
 
-    @staticmethod
-    def backward(ctx, grad_out, grad_mask):
-        sg = ctx.sg
-        ec = sg.ec
-        fo = ec.fused_optimizer
-        if fo is None:
-            raise NotImplementedError(_NO_OPTIMIZER)
-        tabs = [ec._tables[ti] for ti in sg._feature_tables]
-        fo.apply_seq(sg._fused_plan(), ec._store.flat, [t.num_embeddings for t in tabs],
-                     [t.embedding_dim for t in tabs], ctx.ids, ctx.offsets, ctx.max_len,
-                     grad_out.float().contiguous(), sg.pad_mode, sg.align)
-        return (None, None, None, None) + (None,) * len(tabs)
+@seq_fused_update.register_fake
+def _(flat, ids, offsets, max_len, grad_out, owner_id):
+    return None
+
+
+def _seq_setup(ctx, inputs, output):
+    flat, tables, ids, offsets, max_len, _pad_mode, _align, owner_id = inputs
+    ctx.flat = flat
+    ctx.save_for_backward(*ids, *offsets)
+    ctx.n_tables, ctx.n_ids, ctx.max_len, ctx.owner_id = len(tables), len(ids), list(max_len), owner_id
+    ctx.set_materialize_grads(False)
+
+
+def _seq_backward(ctx, grad_out, _grad_mask):
+    saved = ctx.saved_tensors
+    ids, offsets = list(saved[:ctx.n_ids]), list(saved[ctx.n_ids:])
+    if grad_out is not None:
+        torch.ops.pdm.seq_fused_update(ctx.flat, ids, offsets, ctx.max_len, grad_out, ctx.owner_id)
+    return None, [None] * ctx.n_tables, [None] * len(ids), [None] * len(offsets), None, None, None, None
+
+
+ops.seq_gather_fwd.register_autograd(_seq_backward, setup_context=_seq_setup)
 
 
 class TorchRecEmbeddings(nn.Module):

@@ -26,11 +26,14 @@ from typing import Dict, List, Optional
 import torch
 
 
+def mask_as_bool(mask: torch.Tensor) -> torch.Tensor:
+    """The kernels' uint8 0/1 mask as bool: a free reinterpretation eagerly; a conversion inside a compiled graph
+    (Inductor does not lower a uint8 -> bool view)."""
+    return mask.bool() if torch.compiler.is_compiling() else mask.view(torch.bool)
+
+
 def _offsets_from_lengths(lengths: torch.Tensor) -> torch.Tensor:
-    out = torch.zeros(lengths.numel() + 1, dtype=torch.int64, device=lengths.device)
-    if lengths.numel():
-        torch.cumsum(lengths.reshape(-1).to(torch.int64), 0, out=out[1:])
-    return out
+    return torch.nn.functional.pad(lengths.reshape(-1).to(torch.int64).cumsum(0), (1, 0))
 
 
 class KeyedJaggedTensor:
@@ -96,9 +99,9 @@ class KeyedJaggedTensor:
         On the GPU one kernel pass, no host sync."""
         if self._values.device.type != "cuda":
             raise RuntimeError("KeyedJaggedTensor.permute runs on the GPU only")
-        from . import ops
-        v, lengths, offsets = ops.kjt_permute_raw(self._values, self.offsets().to(torch.int64), len(self._keys),
-                                                  self._stride, list(indices))
+        from . import ops  # noqa: F401  (registers pdm::kjt_permute)
+        v, lengths, offsets = torch.ops.pdm.kjt_permute(self._values, self.offsets().to(torch.int64).contiguous(),
+                                                        len(self._keys), self._stride, list(indices))
         return KeyedJaggedTensor([self._keys[i] for i in indices], v, lengths=lengths, offsets=offsets,
                                  stride=self._stride)
 

@@ -31,6 +31,7 @@ import torch.nn as nn
 
 from . import _lib as L
 from . import ops
+from .kjt import mask_as_bool
 
 
 def pyramid_schedule(l_s: int, l_ns: int, n_layers: int) -> List[int]:
@@ -43,6 +44,29 @@ def pyramid_schedule(l_s: int, l_ns: int, n_layers: int) -> List[int]:
         q = l_s - layer * (l_s - l_ns) / (n_layers - 1)
         out.append(max(int(round(q)), l_ns))
     return out
+
+
+# symbolic tracing records calls to the schedule as one node (its Python loop needs concrete ints), as the
+# reference's @torch.fx.wrap does (onetrans.py:49)
+torch.fx.wrap("pyramid_schedule")
+
+
+def _in_graph(*tensors) -> bool:
+    """True inside torch.compile tracing or torch.fx symbolic tracing (where tensors are proxies)."""
+    return torch.compiler.is_compiling() or any(isinstance(t, torch.fx.Proxy) for t in tensors)
+
+
+def _bf16_copies(module: nn.Module, params: Sequence[torch.Tensor]) -> tuple:
+    """bf16 copies of ``params``: autocast's casts of fp32 weights for every matmul.  Eagerly they are made once
+    per parameter version and kept on ``module``; inside a traced or compiled graph they are graph ops."""
+    if _in_graph(*params):
+        return tuple(p.detach().to(torch.bfloat16).contiguous() for p in params)
+    key = tuple((p.data_ptr(), p._version, p.device) for p in params)
+    cache = module.__dict__.get("_bf16_cache")
+    if cache is None or cache[0] != key:
+        cache = (key, tuple(p.detach().to(torch.bfloat16).contiguous() for p in params))
+        module.__dict__["_bf16_cache"] = cache
+    return cache[1]
 
 
 def build_pyramid_mask(q_len: int, kv_len: int, device: torch.device) -> torch.Tensor:
@@ -117,34 +141,33 @@ class OneTransBlock(nn.Module):
         self.attn = MixedAttention(d_model, n_heads, n_ns_tokens, dropout, attention_impl)
         self.norm2 = RMSNorm(d_model)
         self.ffn = MixedFFN(d_model, d_model * ffn_mult, n_ns_tokens, dropout)
-        self._bf16_cache: Optional[tuple] = None
-
-    def _bf16_weights(self):
-        params = (self.attn.s_qkv.weight, self.attn.ns_qkv_weight, self.attn.out_proj.weight,
-                  self.ffn.s_w1.weight, self.ffn.s_w2.weight, self.ffn.ns_w1, self.ffn.ns_w2)
-        key = tuple((p.data_ptr(), p._version, p.device) for p in params)
-        if self._bf16_cache is None or self._bf16_cache[0] != key:
-            # autocast casts fp32 weights to bf16 for every matmul; cast once per weight version
-            conv = tuple(p.detach().to(torch.bfloat16).contiguous() for p in params)
-            self._bf16_cache = (key, conv)
-        return self._bf16_cache[1]
 
     def forward(self, x: torch.Tensor, mask: torch.Tensor, q_len: int, n_s_tokens: int) -> torch.Tensor:
         if self.training and (self.attn.attn_drop > 0 or self.ffn.dropout.p > 0):
             raise RuntimeError("OneTransBlock forward kernels do not implement dropout; call .eval()")
-        kv_len = x.shape[1]
-        if n_s_tokens != kv_len - self.attn.n_ns:
-            raise ValueError(f"n_s_tokens ({n_s_tokens}) must equal kv_len - n_ns ({kv_len - self.attn.n_ns})")
-        if mask is not None and tuple(mask.shape) != (q_len, kv_len):
-            raise ValueError(f"mask must be [q_len, kv_len] = [{q_len}, {kv_len}]")
-        if x.dtype != torch.float32:
-            raise TypeError("the residual stream x must be fp32 (the reference's stream with positional "
-                            "embeddings under autocast)")
-        s_qkv, ns_qkv, out_w, s_w1, s_w2, ns_w1, ns_w2 = self._bf16_weights()
+        # under torch.fx symbolic tracing the arguments are proxies: the checks run when the traced graph runs
+        # the op (its host-side validation), not here
+        fx_tracing = isinstance(x, torch.fx.Proxy)
+        if not fx_tracing:
+            kv_len = x.shape[1]
+            if n_s_tokens != kv_len - self.attn.n_ns:
+                raise ValueError(f"n_s_tokens ({n_s_tokens}) must equal kv_len - n_ns ({kv_len - self.attn.n_ns})")
+            # (not while compiling: the mask is no graph input, and equating q_len with its size would leave
+            # q_len bound to a symbol the compiled graph does not receive)
+            if mask is not None and not torch.compiler.is_compiling() and tuple(mask.shape) != (q_len, kv_len):
+                raise ValueError(f"mask must be [q_len, kv_len] = [{q_len}, {kv_len}]")
+            if x.dtype != torch.float32:
+                raise TypeError("the residual stream x must be fp32: the reference's stream under autocast when "
+                                "the S-tokens carry positional embeddings (use_pos_embed=True); a bf16 stream "
+                                "(use_pos_embed=False) rounds the RMSNorm outputs and residual sums to bf16, "
+                                "rounding points these kernels do not implement")
+        s_qkv, ns_qkv, out_w, s_w1, s_w2, ns_w1, ns_w2 = _bf16_copies(self, (
+            self.attn.s_qkv.weight, self.attn.ns_qkv_weight, self.attn.out_proj.weight,
+            self.ffn.s_w1.weight, self.ffn.s_w2.weight, self.ffn.ns_w1, self.ffn.ns_w2))
         return torch.ops.pdm.onetrans_block_fwd(
             x.contiguous(), self.norm1.weight.detach().float().contiguous(), s_qkv, ns_qkv, out_w,
             self.norm2.weight.detach().float().contiguous(), s_w1, s_w2, ns_w1, ns_w2,
-            self.attn.n_heads, int(q_len))
+            self.attn.n_heads, q_len)
 
 
 class OneTransStack(nn.Module):
@@ -182,17 +205,12 @@ class SequentialTokenizer(nn.Module):
         super().__init__()
         self.proj = nn.Sequential(nn.Linear(raw_dim, d_model), nn.GELU(), nn.Linear(d_model, d_model))
         self.pos_emb = nn.Embedding(max_len, d_model) if use_pos_embed else None
-        self._cache: Optional[tuple] = None
 
     def kernel_weights(self) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, Optional[torch.Tensor]]:
         """(w1, b1, w2, b2) as bf16 (autocast's casts, made once per parameter version) and the fp32 positions."""
         lin1, lin2 = self.proj[0], self.proj[2]
-        params = (lin1.weight, lin1.bias, lin2.weight, lin2.bias)
-        key = tuple((t.data_ptr(), t._version, t.device) for t in params)
-        if self._cache is None or self._cache[0] != key:
-            self._cache = (key, tuple(t.detach().to(torch.bfloat16).contiguous() for t in params))
         pos = None if self.pos_emb is None else self.pos_emb.weight.detach().float().contiguous()
-        return (*self._cache[1], pos)
+        return (*_bf16_copies(self, (lin1.weight, lin1.bias, lin2.weight, lin2.bias)), pos)
 
     def forward(self, raw: torch.Tensor) -> torch.Tensor:
         if raw.dim() != 3:
@@ -238,9 +256,7 @@ class FusedSequenceTokenizer(nn.Module):
         w = {k: [] for k in ("w1", "b1", "w2", "b2", "pos")}
         for name, fs in g.groups.items():
             lengths = batch[fs[0] + "__lengths"]
-            off = torch.zeros(lengths.numel() + 1, dtype=torch.int64, device=lengths.device)
-            torch.cumsum(lengths.to(torch.int64), 0, out=off[1:])
-            offsets.append(off)
+            offsets.append(torch.nn.functional.pad(lengths.reshape(-1).to(torch.int64).cumsum(0), (1, 0)))
             ids.extend(batch[f].reshape(-1).to(torch.int64).contiguous() for f in fs)
             max_len.append(g.max_len[name])
             for k, t in zip(("w1", "b1", "w2", "b2", "pos"), self.tokenizers[name].kernel_weights()):
@@ -248,13 +264,13 @@ class FusedSequenceTokenizer(nn.Module):
         if out is None:
             tokens, mask = torch.ops.pdm.seq_tokenize_fwd(tables, ids, offsets, max_len, w["w1"], w["b1"], w["w2"],
                                                           w["b2"], w["pos"], g.pad_mode, g.align)
-            return tokens, mask.view(torch.bool)
+            return tokens, mask_as_bool(mask)
         F = len(tables)
         grid = [ids[p * F:(p + 1) * F] for p in range(len(offsets))]
         weights = [dict(w1=w["w1"][p], b1=w["b1"][p], w2=w["w2"][p], b2=w["b2"][p], pos=w["pos"][p])
                    for p in range(len(offsets))]
         tokens, mask = ops.seq_tokenize_raw(tables, grid, offsets, max_len, weights, g.pad_mode, g.align, out=out)
-        return tokens, mask.view(torch.bool)
+        return tokens, mask_as_bool(mask)
 
 
 class AutoSplitTokenizer(nn.Module):
@@ -269,17 +285,12 @@ class AutoSplitTokenizer(nn.Module):
         self.proj = nn.Sequential(nn.Linear(ns_input_dim, out_dim), nn.GELU(), nn.Linear(out_dim, out_dim))
         self.n_ns_tokens = n_ns_tokens
         self.d_model = d_model
-        self._cache: Optional[tuple] = None
         self._ws: Optional[torch.Tensor] = None
 
     def kernel_weights(self) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
         """(w1, b1, w2, b2) as bf16 (autocast's casts, made once per parameter version)."""
         lin1, lin2 = self.proj[0], self.proj[2]
-        params = (lin1.weight, lin1.bias, lin2.weight, lin2.bias)
-        key = tuple((t.data_ptr(), t._version, t.device) for t in params)
-        if self._cache is None or self._cache[0] != key:
-            self._cache = (key, tuple(t.detach().to(torch.bfloat16).contiguous() for t in params))
-        return self._cache[1]
+        return _bf16_copies(self, (lin1.weight, lin1.bias, lin2.weight, lin2.bias))
 
     def run(self, tables, ids, dense, out: Optional[torch.Tensor] = None) -> torch.Tensor:
         w1, b1, w2, b2 = self.kernel_weights()

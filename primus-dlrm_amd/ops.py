@@ -3,8 +3,12 @@
 Each op validates shapes, dtypes and devices on the host, then enqueues the
 HIP kernels of libpdm.so on torch's current stream.  Ops are registered with
 ``torch.library.custom_op`` and carry fake (meta) kernels, so FX tracing and
-``torch.compile(dynamic=True)`` see them as single opaque nodes (the
-reference compiles its blocks that way: primus_dlrm/models/onetrans.py:382-390).
+``torch.compile(dynamic=True, fullgraph=True)`` see them as single opaque nodes
+(the reference compiles its blocks that way: primus_dlrm/models/onetrans.py:382-390).
+The lookup ops also take the per-table weight views and the id of the module
+that owns them: the views make autograd record the lookup when the tables
+require gradients, and the backward registered for the op (in embedding.py)
+runs the owner's fused optimizer update as an op that mutates the tables.
 
 There is no CPU implementation: called with CPU tensors these ops raise.
 """
@@ -292,22 +296,40 @@ def kjt_permute_raw(values: torch.Tensor, offsets: torch.Tensor, num_keys: int, 
                                     32 if values.dtype == torch.int32 else 64, offsets.data_ptr(), num_keys,
                                     batch_size, perm_arr, K, out_v.data_ptr(), out_l.data_ptr(), out_o.data_ptr(),
                                     ws.data_ptr(), ws.numel(), L.stream_ptr(dev)), "pdm_kjt_permute")
-    return out_v[:values.numel()], out_l, out_o
+    return (out_v if values.numel() else out_v[:0]), out_l, out_o
+
+
+@torch.library.custom_op("pdm::kjt_permute", mutates_args=())
+def kjt_permute(values: torch.Tensor, offsets: torch.Tensor, num_keys: int, batch_size: int,
+                perm: List[int]) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    v, lengths, offs = kjt_permute_raw(values, offsets, num_keys, batch_size, perm)
+    return (v if v._base is None else v.clone()), lengths, offs
+
+
+@kjt_permute.register_fake
+def _(values, offsets, num_keys, batch_size, perm):
+    K = len(perm)
+    return (values.new_empty(values.shape), offsets.new_empty(K * batch_size, dtype=torch.int32),
+            offsets.new_empty(K * batch_size + 1, dtype=torch.int64))
 
 
 _DTYPE_CODES = {0: torch.float32, 1: torch.float16, 2: torch.bfloat16}
 
 
 @torch.library.custom_op("pdm::tbe_pooled_fwd", mutates_args=())
-def tbe_pooled_fwd(weights: torch.Tensor, indices: torch.Tensor, offsets: torch.Tensor, plan_id: int,
-                   num_slots: int, total_dim: int, out_dtype_code: int, padding_idx: int) -> torch.Tensor:
+def tbe_pooled_fwd(weights: torch.Tensor, tables: List[torch.Tensor], indices: torch.Tensor, offsets: torch.Tensor,
+                   plan_id: int, num_slots: int, total_dim: int, out_dtype_code: int, padding_idx: int,
+                   owner_id: int) -> torch.Tensor:
+    """Pooled lookup over the collection buffer ``weights`` (``tables``: its per-table views, not read here;
+    ``owner_id``: the collection, used by the backward)."""
     plan = TbePlan.get(plan_id)
     batch = (offsets.numel() - 1) // num_slots
-    return tbe_pooled_raw(plan, weights, indices, offsets, batch, _DTYPE_CODES[out_dtype_code], padding_idx)
+    return tbe_pooled_raw(plan, weights, indices.contiguous(), offsets.contiguous(), batch,
+                          _DTYPE_CODES[out_dtype_code], padding_idx)
 
 
 @tbe_pooled_fwd.register_fake
-def _(weights, indices, offsets, plan_id, num_slots, total_dim, out_dtype_code, padding_idx):
+def _(weights, tables, indices, offsets, plan_id, num_slots, total_dim, out_dtype_code, padding_idx, owner_id):
     batch = (offsets.shape[0] - 1) // num_slots
     return weights.new_empty((batch, total_dim), dtype=_DTYPE_CODES[out_dtype_code])
 
@@ -515,8 +537,11 @@ def seq_gather_backward_fused_raw(plan: TbePlan, weights: torch.Tensor, momentum
 
 
 @torch.library.custom_op("pdm::seq_gather_fwd", mutates_args=())
-def seq_gather_fwd(tables: List[torch.Tensor], ids: List[torch.Tensor], offsets: List[torch.Tensor],
-                   max_len: List[int], pad_mode: int, align: int) -> Tuple[torch.Tensor, torch.Tensor]:
+def seq_gather_fwd(flat: torch.Tensor, tables: List[torch.Tensor], ids: List[torch.Tensor],
+                   offsets: List[torch.Tensor], max_len: List[int], pad_mode: int, align: int,
+                   owner_id: int) -> Tuple[torch.Tensor, torch.Tensor]:
+    """S-token gather from ``tables`` (views of the collection buffer ``flat``, which the backward updates);
+    ``ids`` is pool-major, ``len(tables)`` features per pool."""
     F = len(tables)
     grid = [ids[p * F:(p + 1) * F] for p in range(len(offsets))]
     out, mask = seq_gather_raw(tables, grid, offsets, max_len, pad_mode, align, want_mask=True)
@@ -524,7 +549,7 @@ def seq_gather_fwd(tables: List[torch.Tensor], ids: List[torch.Tensor], offsets:
 
 
 @seq_gather_fwd.register_fake
-def _(tables, ids, offsets, max_len, pad_mode, align):
+def _(flat, tables, ids, offsets, max_len, pad_mode, align, owner_id):
     B = offsets[0].shape[0] - 1
     S = sum(max_len)
     D = sum(t.shape[1] for t in tables)
