@@ -761,20 +761,16 @@ def setup_onetrans(pdm, torch, dev, w):
                            ns_w1=r(n_ns, F, D), ns_w2=r(n_ns, D, F)))
     kv0 = w.l_s + n_ns
     x = torch.randn(w.batch, kv0, D, device=dev, generator=gen) * 0.02
-    ws_size = pdm.ops.onetrans_workspace_layout(w.batch, kv0, kv0, D, F)["total"][0]
-    ws = torch.empty(ws_size, dtype=torch.uint8, device=dev)
-    outs = []
-    for q_s in w.schedule:
-        outs.append(torch.empty(w.batch, q_s + n_ns, D, device=dev))
     H = D // 64
+    ws = torch.empty(pdm.ops.onetrans_stack_workspace_bytes(w.batch, kv0, D, F, n_ns, H, w.schedule),
+                     dtype=torch.uint8, device=dev)
+    out = torch.empty(w.batch, w.schedule[-1] + n_ns, D, device=dev)
 
     def step():
-        cur = x
-        for layer, q_s in enumerate(w.schedule):
-            pdm.ops.onetrans_block_raw(cur, layers[layer], H, q_s + n_ns, out=outs[layer], workspace=ws)
-            cur = outs[layer]
+        # the whole 4-layer loop in one call (pdm_onetrans_stack_fwd)
+        pdm.ops.onetrans_stack_raw(x, layers, H, w.schedule, out=out, workspace=ws)
 
-    return step, syn.block_flops(w), syn.block_flops_causal(w), (x, layers, ws, outs)
+    return step, syn.block_flops(w), syn.block_flops_causal(w), (x, layers, ws, out)
 
 
 def _torch_block(torch, x, w, q_len: int, n_heads: int):

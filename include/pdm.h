@@ -371,6 +371,31 @@ int pdm_onetrans_block_fwd(const pdm_block_desc* desc, const float* x,
                            void* workspace, int64_t workspace_bytes,
                            pdm_stream_t stream);
 
+/* ------------------------------------------------------------------------
+ * OneTrans block stack: the layer loop of OneTransModel._backbone
+ * (primus_dlrm/models/onetrans.py:568-582).  Layer l runs OneTransBlock l on
+ * the previous layer's output (layer 0 on x, kv_len = desc->kv_len; layer l
+ * > 0 with kv_len = the previous layer's q_len) with the pyramid mask and
+ * q_len = q_s[l] + n_ns, n_s_tokens = kv_len - n_ns (:574-582); q_s is the
+ * schedule of pyramid_schedule (:50-59) or [L_S] * n_layers.  desc gives B,
+ * D, H, n_ns, ffn_dim and layer 0's kv_len (its q_len is not read).
+ * weights: n_layers layers.  x: device fp32 [B, kv_len, D]; y: device fp32
+ * [B, q_s[n_layers-1] + n_ns, D].  One workspace serves every layer (the
+ * inner layers' outputs live in it); the intermediate tensors never reach
+ * the caller and no per-layer call crosses the ABI.
+ * ------------------------------------------------------------------------ */
+#define PDM_STACK_MAX_LAYERS 64
+
+/* Bytes of device workspace pdm_onetrans_stack_fwd needs. */
+int64_t pdm_onetrans_stack_workspace_size(const pdm_block_desc* desc,
+                                          const int32_t* q_s, int32_t n_layers);
+
+int pdm_onetrans_stack_fwd(const pdm_block_desc* desc, const int32_t* q_s,
+                           int32_t n_layers, const float* x,
+                           const pdm_block_weights* weights, float* y,
+                           void* workspace, int64_t workspace_bytes,
+                           pdm_stream_t stream);
+
 /* NS-token construction: OneTransModel._build_ns_raw
  * (primus_dlrm/models/onetrans.py:522-532) + AutoSplitTokenizer
  * (onetrans.py:260-276), used at onetrans.py:561-563, under autocast(bf16):

@@ -31,6 +31,7 @@ PDM_OPT_ADAM, PDM_OPT_ROWWISE_ADAGRAD, PDM_OPT_NONE = 0, 1, 2
 PDM_WD_NONE, PDM_WD_L2 = 0, 1
 PDM_KJT_MAX_FEATURES = 64
 PDM_KJT_NOALLOC_MAX_ROWS = 67108864
+PDM_STACK_MAX_LAYERS = 64
 
 # Every symbol include/pdm.h declares (checked by the ABI test).
 EXPORTED_SYMBOLS = (
@@ -60,6 +61,8 @@ EXPORTED_SYMBOLS = (
     "pdm_ns_tokenize_fwd",
     "pdm_onetrans_block_workspace_size",
     "pdm_onetrans_block_fwd",
+    "pdm_onetrans_stack_workspace_size",
+    "pdm_onetrans_stack_fwd",
 )
 
 
@@ -210,6 +213,11 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.pdm_onetrans_block_fwd.restype = ctypes.c_int
     lib.pdm_onetrans_block_fwd.argtypes = [ctypes.POINTER(BlockDesc), vp, ctypes.POINTER(BlockWeights), vp,
                                            vp, i64, vp]
+    lib.pdm_onetrans_stack_workspace_size.restype = i64
+    lib.pdm_onetrans_stack_workspace_size.argtypes = [ctypes.POINTER(BlockDesc), ctypes.POINTER(i32), i32]
+    lib.pdm_onetrans_stack_fwd.restype = ctypes.c_int
+    lib.pdm_onetrans_stack_fwd.argtypes = [ctypes.POINTER(BlockDesc), ctypes.POINTER(i32), i32, vp,
+                                           ctypes.POINTER(BlockWeights), vp, vp, i64, vp]
     lib.pdm_tbe_plan_total_rows.restype = i64
     lib.pdm_tbe_plan_total_rows.argtypes = [vp]
     lib.pdm_tbe_plan_row_offset.restype = i64

@@ -1382,30 +1382,12 @@ extern "C" int64_t pdm_onetrans_block_workspace_size(const pdm_block_desc* desc)
   return block_layout(*desc).total;
 }
 
-extern "C" int pdm_onetrans_block_fwd(const pdm_block_desc* desc, const float* x, const pdm_block_weights* w,
-                                      float* y, void* workspace, int64_t workspace_bytes, pdm_stream_t stream) {
-  clear_error();
-  if (const char* e = check_desc(desc)) {
-    set_error(std::string("pdm_onetrans_block_fwd: ") + e);
-    return PDM_ERR_INVALID;
-  }
-  const pdm_block_desc& d = *desc;
-  PDM_CHECK_ARG(x && w && y && workspace, "null pointer");
-  PDM_CHECK_ARG(w->norm1_w && w->s_qkv_w && w->out_w && w->norm2_w && w->s_w1 && w->s_w2, "null weight pointer");
-  PDM_CHECK_ARG(d.n_ns == 0 || (w->ns_qkv_w && w->ns_w1 && w->ns_w2), "null per-token weight pointer");
-  const BlockLayout L = block_layout(d);
-  if (workspace_bytes < L.total) {
-    set_error("pdm_onetrans_block_fwd: workspace of " + std::to_string(workspace_bytes) + " bytes, need " +
-              std::to_string(L.total));
-    return PDM_ERR_WORKSPACE;
-  }
-  const void* ptrs[] = {x, y, workspace, w->s_qkv_w, w->out_w, w->s_w1, w->s_w2,
-                        d.n_ns ? w->ns_qkv_w : w->s_qkv_w, d.n_ns ? w->ns_w1 : w->s_w1,
-                        d.n_ns ? w->ns_w2 : w->s_w2, w->norm1_w, w->norm2_w};
-  for (const void* p : ptrs) PDM_CHECK_ARG(aligned16(p), "every tensor must be 16-byte aligned");
-  PDM_CHECK_ARG((const void*)y != (const void*)x, "y must not alias x");
+namespace pdm {
 
-  auto s = reinterpret_cast<hipStream_t>(stream);
+// One block on stream s; the descriptor is checked, the pointers are not.
+static int block_fwd(const pdm_block_desc& d, const float* x, const pdm_block_weights* w, float* y, void* workspace,
+                     hipStream_t s) {
+  const BlockLayout L = block_layout(d);
   char* ws = reinterpret_cast<char*>(workspace);
   uint16_t* h = reinterpret_cast<uint16_t*>(ws + L.h);
   uint16_t* q = reinterpret_cast<uint16_t*>(ws + L.q);
@@ -1506,6 +1488,124 @@ extern "C" int pdm_onetrans_block_fwd(const pdm_block_desc* desc, const float* x
     g3.out = y; g3.out_bstride = (int64_t)ql * D;
     g3.res = y; g3.res_bstride = (int64_t)ql * D; g3.res_toff = 0;
     if ((st = launch_gemm<EPI_RESID>(g3, s)) != PDM_OK) return st;
+  }
+  return PDM_OK;
+}
+
+// Checks the weight pointers of one layer (alignment of every tensor the kernels read with 16-byte loads).
+static int check_block_weights(const pdm_block_desc& d, const pdm_block_weights* w) {
+  PDM_CHECK_ARG(w, "null weights");
+  PDM_CHECK_ARG(w->norm1_w && w->s_qkv_w && w->out_w && w->norm2_w && w->s_w1 && w->s_w2, "null weight pointer");
+  PDM_CHECK_ARG(d.n_ns == 0 || (w->ns_qkv_w && w->ns_w1 && w->ns_w2), "null per-token weight pointer");
+  const void* ptrs[] = {w->s_qkv_w, w->out_w, w->s_w1, w->s_w2, d.n_ns ? w->ns_qkv_w : w->s_qkv_w,
+                        d.n_ns ? w->ns_w1 : w->s_w1, d.n_ns ? w->ns_w2 : w->s_w2, w->norm1_w, w->norm2_w};
+  for (const void* p : ptrs) PDM_CHECK_ARG(aligned16(p), "every tensor must be 16-byte aligned");
+  return PDM_OK;
+}
+
+}  // namespace pdm
+
+extern "C" int pdm_onetrans_block_fwd(const pdm_block_desc* desc, const float* x, const pdm_block_weights* w,
+                                      float* y, void* workspace, int64_t workspace_bytes, pdm_stream_t stream) {
+  clear_error();
+  if (const char* e = check_desc(desc)) {
+    set_error(std::string("pdm_onetrans_block_fwd: ") + e);
+    return PDM_ERR_INVALID;
+  }
+  const pdm_block_desc& d = *desc;
+  PDM_CHECK_ARG(x && w && y && workspace, "null pointer");
+  int st;
+  if ((st = check_block_weights(d, w)) != PDM_OK) return st;
+  const BlockLayout L = block_layout(d);
+  if (workspace_bytes < L.total) {
+    set_error("pdm_onetrans_block_fwd: workspace of " + std::to_string(workspace_bytes) + " bytes, need " +
+              std::to_string(L.total));
+    return PDM_ERR_WORKSPACE;
+  }
+  PDM_CHECK_ARG(aligned16(x) && aligned16(y) && aligned16(workspace), "every tensor must be 16-byte aligned");
+  PDM_CHECK_ARG((const void*)y != (const void*)x, "y must not alias x");
+  return block_fwd(d, x, w, y, workspace, reinterpret_cast<hipStream_t>(stream));
+}
+
+// ---------------------------------------------------------------------------
+// Block stack: the layer loop of OneTransModel._backbone.  Layer l runs on the
+// previous layer's output (kv_len = its q_len) and keeps q_s[l] + n_ns tokens.
+// Workspace: one block workspace sized for the largest layer, reused by every
+// layer, then the fp32 outputs of the inner layers in two alternating buffers
+// of the largest inner layer's size.
+// ---------------------------------------------------------------------------
+namespace pdm {
+
+struct StackLayout {
+  int64_t block;    // bytes of the shared block workspace
+  int64_t buf[2];   // offsets of the two inner-layer output buffers
+  int64_t total;
+};
+
+static const char* stack_layout(const pdm_block_desc* desc, const int32_t* q_s, int32_t n_layers, StackLayout& S) {
+  if (!desc) return "null desc";
+  if (!q_s) return "null q_s";
+  if (n_layers < 1 || n_layers > PDM_STACK_MAX_LAYERS) return "n_layers must be in [1, PDM_STACK_MAX_LAYERS]";
+  pdm_block_desc d = *desc;
+  int64_t block = 0, inner = 0;
+  for (int l = 0; l < n_layers; ++l) {
+    if (q_s[l] < 0) return "q_s must be >= 0";
+    d.q_len = q_s[l] + desc->n_ns;
+    if (const char* e = check_desc(&d)) return e;
+    block = std::max(block, block_layout(d).total);
+    if (l + 1 < n_layers) inner = std::max(inner, align256((int64_t)d.batch * d.q_len * d.d_model * 4));
+    d.kv_len = d.q_len;
+  }
+  S.block = align256(block);
+  S.buf[0] = S.block;
+  S.buf[1] = S.block + (n_layers > 1 ? inner : 0);
+  S.total = S.buf[1] + (n_layers > 2 ? inner : 0);
+  return nullptr;
+}
+
+}  // namespace pdm
+
+extern "C" int64_t pdm_onetrans_stack_workspace_size(const pdm_block_desc* desc, const int32_t* q_s,
+                                                     int32_t n_layers) {
+  clear_error();
+  StackLayout S;
+  if (const char* e = stack_layout(desc, q_s, n_layers, S)) {
+    set_error(std::string("pdm_onetrans_stack_workspace_size: ") + e);
+    return PDM_ERR_INVALID;
+  }
+  return S.total;
+}
+
+extern "C" int pdm_onetrans_stack_fwd(const pdm_block_desc* desc, const int32_t* q_s, int32_t n_layers,
+                                      const float* x, const pdm_block_weights* weights, float* y, void* workspace,
+                                      int64_t workspace_bytes, pdm_stream_t stream) {
+  clear_error();
+  StackLayout S;
+  if (const char* e = stack_layout(desc, q_s, n_layers, S)) {
+    set_error(std::string("pdm_onetrans_stack_fwd: ") + e);
+    return PDM_ERR_INVALID;
+  }
+  PDM_CHECK_ARG(x && weights && y && workspace, "null pointer");
+  if (workspace_bytes < S.total) {
+    set_error("pdm_onetrans_stack_fwd: workspace of " + std::to_string(workspace_bytes) + " bytes, need " +
+              std::to_string(S.total));
+    return PDM_ERR_WORKSPACE;
+  }
+  PDM_CHECK_ARG(aligned16(x) && aligned16(y) && aligned16(workspace), "every tensor must be 16-byte aligned");
+  PDM_CHECK_ARG((const void*)y != (const void*)x, "y must not alias x");
+  pdm_block_desc d = *desc;
+  int st;
+  for (int l = 0; l < n_layers; ++l)
+    if ((st = check_block_weights(d, &weights[l])) != PDM_OK) return st;
+  auto s = reinterpret_cast<hipStream_t>(stream);
+  char* ws = reinterpret_cast<char*>(workspace);
+  const float* in = x;
+  for (int l = 0; l < n_layers; ++l) {
+    d.q_len = q_s[l] + desc->n_ns;
+    float* out = l + 1 == n_layers ? y : reinterpret_cast<float*>(ws + S.buf[l & 1]);
+    if ((st = block_fwd(d, in, &weights[l], out, ws, s)) != PDM_OK) return st;
+    in = out;
+    d.kv_len = d.q_len;
   }
   return PDM_OK;
 }

@@ -69,6 +69,14 @@ def _bf16_copies(module: nn.Module, params: Sequence[torch.Tensor]) -> tuple:
     return cache[1]
 
 
+def _check_stream(x: torch.Tensor) -> None:
+    if x.dtype != torch.float32:
+        raise TypeError("the residual stream x must be fp32: the reference's stream under autocast when the "
+                        "S-tokens carry positional embeddings (use_pos_embed=True); a bf16 stream "
+                        "(use_pos_embed=False) rounds the RMSNorm outputs and residual sums to bf16, rounding "
+                        "points these kernels do not implement")
+
+
 def build_pyramid_mask(q_len: int, kv_len: int, device: torch.device) -> torch.Tensor:
     """Bottom-right causal mask ``[q_len, kv_len]``: query i sees keys
     j <= i + (kv_len - q_len) (onetrans.py:62-67)."""
@@ -143,8 +151,7 @@ class OneTransBlock(nn.Module):
         self.ffn = MixedFFN(d_model, d_model * ffn_mult, n_ns_tokens, dropout)
 
     def forward(self, x: torch.Tensor, mask: torch.Tensor, q_len: int, n_s_tokens: int) -> torch.Tensor:
-        if self.training and (self.attn.attn_drop > 0 or self.ffn.dropout.p > 0):
-            raise RuntimeError("OneTransBlock forward kernels do not implement dropout; call .eval()")
+        self._check_eval()
         # under torch.fx symbolic tracing the arguments are proxies: the checks run when the traced graph runs
         # the op (its host-side validation), not here
         fx_tracing = isinstance(x, torch.fx.Proxy)
@@ -156,23 +163,28 @@ class OneTransBlock(nn.Module):
             # q_len bound to a symbol the compiled graph does not receive)
             if mask is not None and not torch.compiler.is_compiling() and tuple(mask.shape) != (q_len, kv_len):
                 raise ValueError(f"mask must be [q_len, kv_len] = [{q_len}, {kv_len}]")
-            if x.dtype != torch.float32:
-                raise TypeError("the residual stream x must be fp32: the reference's stream under autocast when "
-                                "the S-tokens carry positional embeddings (use_pos_embed=True); a bf16 stream "
-                                "(use_pos_embed=False) rounds the RMSNorm outputs and residual sums to bf16, "
-                                "rounding points these kernels do not implement")
+            _check_stream(x)
+        return torch.ops.pdm.onetrans_block_fwd(x.contiguous(), *self.kernel_weights(), self.attn.n_heads, q_len)
+
+    def kernel_weights(self) -> Tuple[torch.Tensor, ...]:
+        """The nine tensors the kernels take, in pdm_block_weights order: the RMSNorm weights as fp32 and the
+        projection weights as autocast's bf16 casts (made once per parameter version)."""
         s_qkv, ns_qkv, out_w, s_w1, s_w2, ns_w1, ns_w2 = _bf16_copies(self, (
             self.attn.s_qkv.weight, self.attn.ns_qkv_weight, self.attn.out_proj.weight,
             self.ffn.s_w1.weight, self.ffn.s_w2.weight, self.ffn.ns_w1, self.ffn.ns_w2))
-        return torch.ops.pdm.onetrans_block_fwd(
-            x.contiguous(), self.norm1.weight.detach().float().contiguous(), s_qkv, ns_qkv, out_w,
-            self.norm2.weight.detach().float().contiguous(), s_w1, s_w2, ns_w1, ns_w2,
-            self.attn.n_heads, q_len)
+        return (self.norm1.weight.detach().float().contiguous(), s_qkv, ns_qkv, out_w,
+                self.norm2.weight.detach().float().contiguous(), s_w1, s_w2, ns_w1, ns_w2)
+
+    def _check_eval(self) -> None:
+        if self.training and (self.attn.attn_drop > 0 or self.ffn.dropout.p > 0):
+            raise RuntimeError("OneTransBlock forward kernels do not implement dropout; call .eval()")
 
 
 class OneTransStack(nn.Module):
     """The block loop of OneTransModel._backbone (onetrans.py:568-582): layer
-    l keeps ``schedule[l] + n_ns`` query tokens of the previous output."""
+    l keeps ``schedule[l] + n_ns`` query tokens of the previous output.  The
+    whole loop is one call (pdm_onetrans_stack_fwd): the layers share one
+    workspace and the inner layers' outputs never leave it."""
 
     def __init__(self, d_model: int, n_heads: int, n_ns_tokens: int, n_layers: int, ffn_mult: int = 4,
                  schedule: Optional[Sequence[int]] = None):
@@ -185,12 +197,13 @@ class OneTransStack(nn.Module):
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         L_S = x.shape[1] - self.n_ns
         schedule = self.schedule or pyramid_schedule(L_S, self.n_ns, len(self.blocks))
-        for layer, block in enumerate(self.blocks):
-            q_len = schedule[layer] + self.n_ns
-            kv_len = x.shape[1]
-            mask = build_pyramid_mask(q_len, kv_len, x.device)
-            x = block(x, mask=mask, q_len=q_len, n_s_tokens=kv_len - self.n_ns)
-        return x
+        if not isinstance(x, torch.fx.Proxy):
+            _check_stream(x)
+        weights = []
+        for block in self.blocks:
+            block._check_eval()
+            weights.extend(block.kernel_weights())
+        return torch.ops.pdm.onetrans_stack_fwd(x.contiguous(), weights, self.blocks[0].attn.n_heads, schedule)
 
 
 class SequentialTokenizer(nn.Module):

@@ -719,6 +719,77 @@ def _(x, norm1_w, s_qkv_w, ns_qkv_w, out_w, norm2_w, s_w1, s_w2, ns_w1, ns_w2, n
     return x.new_empty((x.shape[0], q_len, x.shape[2]))
 
 
+_BLOCK_WEIGHT_NAMES = ("norm1_w", "s_qkv_w", "ns_qkv_w", "out_w", "norm2_w", "s_w1", "s_w2", "ns_w1", "ns_w2")
+
+
+def onetrans_stack_workspace_bytes(B: int, kv: int, D: int, F: int, n_ns: int, n_heads: int,
+                                   q_s: Sequence[int]) -> int:
+    """pdm_onetrans_stack_workspace_size for a stack whose layer 0 sees ``kv`` tokens."""
+    desc = L.BlockDesc(B, D, n_heads, n_ns, F, kv, int(q_s[0]) + n_ns if len(q_s) else n_ns, 0)
+    qs = (ctypes.c_int32 * max(len(q_s), 1))(*[int(q) for q in q_s])
+    n = int(L.lib().pdm_onetrans_stack_workspace_size(ctypes.byref(desc), qs, len(q_s)))
+    if n < 0:
+        raise L.PdmError(n, "pdm_onetrans_stack_workspace_size", L.last_error())
+    return n
+
+
+def onetrans_stack_raw(x: torch.Tensor, layers: Sequence[Dict[str, torch.Tensor]], n_heads: int,
+                       q_s: Sequence[int], out: Optional[torch.Tensor] = None,
+                       workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """The block loop in one call (pdm_onetrans_stack_fwd): layer l keeps ``q_s[l] + n_ns`` tokens of the
+    previous layer's output.  ``layers[l]`` holds the weights of block l as for ``onetrans_block_raw``.
+    Returns fp32 [B, q_s[-1] + n_ns, D]."""
+    n = len(layers)
+    if n != len(q_s) or not 1 <= n <= L.PDM_STACK_MAX_LAYERS:
+        raise ValueError(f"need one schedule entry per layer and 1..{L.PDM_STACK_MAX_LAYERS} layers")
+    dev = _require_cuda(x, *[w[k] for w in layers for k in _BLOCK_WEIGHT_NAMES])
+    if x.dtype != torch.float32 or x.dim() != 3 or not x.is_contiguous():
+        raise ValueError("x must be a contiguous fp32 [B, kv_len, D] tensor")
+    B, kv, D = x.shape
+    n_ns = layers[0]["ns_qkv_w"].shape[0]
+    Fd = layers[0]["s_w1"].shape[0]
+    shapes = {"norm1_w": (D,), "s_qkv_w": (3 * D, D), "ns_qkv_w": (n_ns, 3 * D, D), "out_w": (D, D),
+              "norm2_w": (D,), "s_w1": (Fd, D), "s_w2": (D, Fd), "ns_w1": (n_ns, Fd, D), "ns_w2": (n_ns, D, Fd)}
+    for w in layers:
+        for k in _BLOCK_WEIGHT_NAMES:
+            t = w[k]
+            want = torch.float32 if k.startswith("norm") else torch.bfloat16
+            if tuple(t.shape) != shapes[k] or t.dtype != want or not t.is_contiguous():
+                raise ValueError(f"{k}: expected contiguous {want} {shapes[k]}, got {t.dtype} {tuple(t.shape)}")
+    kv_l = kv
+    for q in q_s:
+        if q < 0 or q + n_ns > kv_l:
+            raise ValueError(f"schedule {list(q_s)}: each layer keeps n_ns <= q + n_ns <= its kv_len")
+        kv_l = q + n_ns
+    desc = L.BlockDesc(B, D, n_heads, n_ns, Fd, kv, int(q_s[0]) + n_ns, 0)
+    qs = (ctypes.c_int32 * n)(*[int(q) for q in q_s])
+    ws_bytes = onetrans_stack_workspace_bytes(B, kv, D, Fd, n_ns, n_heads, q_s)
+    if workspace is None:
+        workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    elif workspace.dtype != torch.uint8 or workspace.numel() < ws_bytes or workspace.device != dev:
+        raise ValueError(f"workspace must be a uint8 tensor of >= {ws_bytes} bytes on {dev}")
+    if out is None:
+        out = torch.empty((B, int(q_s[-1]) + n_ns, D), dtype=torch.float32, device=dev)
+    bw = (L.BlockWeights * n)(*[L.BlockWeights(*[w[k].data_ptr() for k in _BLOCK_WEIGHT_NAMES]) for w in layers])
+    status = L.lib().pdm_onetrans_stack_fwd(ctypes.byref(desc), qs, n, x.data_ptr(), bw, out.data_ptr(),
+                                            workspace.data_ptr(), ws_bytes, L.stream_ptr(dev))
+    L.check(status, "pdm_onetrans_stack_fwd")
+    return out
+
+
+@torch.library.custom_op("pdm::onetrans_stack_fwd", mutates_args=())
+def onetrans_stack_fwd(x: torch.Tensor, weights: List[torch.Tensor], n_heads: int, q_s: List[int]) -> torch.Tensor:
+    """``weights``: the nine block weights of every layer in turn (the order of pdm_block_weights)."""
+    k = len(_BLOCK_WEIGHT_NAMES)
+    layers = [dict(zip(_BLOCK_WEIGHT_NAMES, weights[i * k:(i + 1) * k])) for i in range(len(weights) // k)]
+    return onetrans_stack_raw(x, layers, n_heads, q_s)
+
+
+@onetrans_stack_fwd.register_fake
+def _(x, weights, n_heads, q_s):
+    return x.new_empty((x.shape[0], q_s[-1] + weights[2].shape[0], x.shape[2]))
+
+
 # ---------------------------------------------------------------------------
 # Cross-feature ids (xxHash64)
 # ---------------------------------------------------------------------------

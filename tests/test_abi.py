@@ -88,7 +88,8 @@ def test_ops_refuse_cpu_tensors(pdm):
 def test_custom_ops_registered(pdm):
     import torch
 
-    for name in ("tbe_pooled_fwd", "seq_gather_fwd", "onetrans_block_fwd"):
+    for name in ("tbe_pooled_fwd", "seq_gather_fwd", "onetrans_block_fwd", "onetrans_stack_fwd", "ec_lookup",
+                 "tbe_fused_update", "ec_fused_update", "seq_fused_update", "kjt_permute", "cross_hash_fwd"):
         assert hasattr(torch.ops.pdm, name)
 
 
@@ -103,3 +104,31 @@ def test_block_workspace_size_matches_python_layout(pdm):
     assert "head dim" in L.last_error()
     bad = L.BlockDesc(4, 256, 4, 6, 1024, 10, 5, 0)  # q_len < n_ns
     assert L.lib().pdm_onetrans_block_workspace_size(ctypes.byref(bad)) == L.PDM_ERR_INVALID
+
+
+def test_stack_workspace_size(pdm):
+    """One block workspace for the largest layer (layer 0) plus two fp32 buffers of the largest inner layer's
+    output; one buffer for two layers, none for one; schedules that grow or go negative are refused."""
+    L = pdm._lib
+    a = lambda v: (v + 255) // 256 * 256  # noqa: E731
+
+    def size(B, kv, D, Fd, ns, q_s):
+        d = L.BlockDesc(B, D, D // 64, ns, Fd, kv, 0, 0)
+        arr = (ctypes.c_int32 * len(q_s))(*q_s)
+        return L.lib().pdm_onetrans_stack_workspace_size(ctypes.byref(d), arr, len(q_s))
+
+    B, kv, D, Fd, ns = 1024, 400, 256, 1024, 16
+    block0 = pdm.ops.onetrans_workspace_layout(B, kv, 384 + ns, D, Fd)["total"][0]
+    inner = a(B * (384 + ns) * D * 4)
+    assert size(B, kv, D, Fd, ns, [384, 256, 128, 64]) == a(block0) + 2 * inner
+    assert size(B, kv, D, Fd, ns, [384, 256]) == a(block0) + inner
+    assert size(B, kv, D, Fd, ns, [384]) == a(block0)
+    # the tiled path (d_model 384) holds h and g too: still layer 0's block workspace
+    blk384 = pdm.ops.onetrans_workspace_layout(4, 60, 40 + 3, 384, 1536)["total"][0]
+    assert size(4, 60, 384, 1536, 3, [40, 20]) == a(blk384) + a(4 * 43 * 384 * 4)
+    assert size(B, kv, D, Fd, ns, [384, 390]) == L.PDM_ERR_INVALID  # layer 1 keeps more than its kv
+    assert "q_len" in L.last_error()
+    assert size(B, kv, D, Fd, ns, [384, -1]) == L.PDM_ERR_INVALID
+    assert size(B, kv, D, Fd, ns, []) == L.PDM_ERR_INVALID
+    d = L.BlockDesc(B, D, D // 64, ns, Fd, kv, 0, 0)
+    assert L.lib().pdm_onetrans_stack_workspace_size(ctypes.byref(d), None, 2) == L.PDM_ERR_INVALID

@@ -155,6 +155,10 @@ def test_opcheck_block_and_tokenizer_ops(pdm, dev):
              (x, blk.norm1.weight.detach().float(), bf(blk.attn.s_qkv.weight), bf(blk.attn.ns_qkv_weight),
               bf(blk.attn.out_proj.weight), blk.norm2.weight.detach().float(), bf(blk.ffn.s_w1.weight),
               bf(blk.ffn.s_w2.weight), bf(blk.ffn.ns_w1), bf(blk.ffn.ns_w2), 2, q_len))
+    stack = pdm.OneTransStack(128, 2, 4, 3, schedule=[20, 12, 4]).to(dev).eval()
+    x = torch.randn(2, 24, 128, device=dev)
+    _opcheck(torch.ops.pdm.onetrans_stack_fwd.default,
+             (x, [t for blk in stack.blocks for t in blk.kernel_weights()], 2, [20, 12, 4]))
     tables = [pdm.EmbeddingConfig(500, 128, "item", pdm.DataType.BF16, ["lp_item"]),
               pdm.EmbeddingConfig(60, 64, "artist", pdm.DataType.BF16, ["lp_artist"])]
     ec = pdm.EmbeddingCollection(tables, device=dev)
@@ -191,20 +195,24 @@ def test_block_compiles_fullgraph_dynamic(pdm, dev):
 
 
 def test_block_compiled_like_the_reference(pdm, dev):
-    """Each block compiled as OneTransModel.apply_compile does (fullgraph=False, dynamic=True) inside the
-    pyramid stack: same output as the eager stack."""
+    """The reference's backbone loop (onetrans.py:568-582) over blocks compiled as OneTransModel.apply_compile
+    does (fullgraph=False, dynamic=True): the same output as OneTransStack's one-call stack."""
     D, n_ns = 128, 4
-    stack = pdm.OneTransStack(D, 2, n_ns, 3, schedule=[36, 20, 8]).to(dev).eval()
+    schedule = [36, 20, 8]
+    stack = pdm.OneTransStack(D, 2, n_ns, 3, schedule=schedule).to(dev).eval()
     for i, blk in enumerate(stack.blocks):
-        stack.blocks[i].load_state_dict(_block(pdm, dev, seed=20 + i).state_dict())
-    x = torch.randn(3, 36 + n_ns, D, device=dev)
+        blk.load_state_dict(_block(pdm, dev, seed=20 + i).state_dict())
+    compiled = [torch.compile(blk, fullgraph=False, dynamic=True) for blk in stack.blocks]
     with torch.no_grad():
-        want = stack(x)
-        for i, blk in enumerate(stack.blocks):
-            stack.blocks[i] = torch.compile(blk, fullgraph=False, dynamic=True)
-        got = stack(x)
-    torch.cuda.synchronize()
-    assert torch.equal(got, want)
+        for B in (3, 6):
+            x = torch.randn(B, 36 + n_ns, D, device=dev)
+            want = stack(x)
+            h = x
+            for blk, q_s in zip(compiled, schedule):
+                q_len, kv_len = q_s + n_ns, h.shape[1]
+                h = blk(h, mask=pdm.build_pyramid_mask(q_len, kv_len, dev), q_len=q_len, n_s_tokens=kv_len - n_ns)
+            torch.cuda.synchronize()
+            assert torch.equal(h, want)
 
 
 def test_stack_compiles_fullgraph(pdm, dev):
@@ -354,9 +362,10 @@ def test_untagged_tables_raise_at_compiled_backward(pdm, dev):
 # ---------------------------------------------------------------------------
 
 def test_fx_trace_model_forward_with_leaf_lookups(pdm, dev):
-    """A model in the reference's shape: forward(batch) -> tokens from the S-token gather and a pooled
-    lookup, then the pyramid blocks.  Traced by an FX tracer that keeps the embedding modules as leaves; the
-    GraphModule calls the block op directly and reproduces the eager output."""
+    """A model in the reference's shape: forward(batch) -> tokens from the S-token gather, then the pyramid
+    stack with the default schedule (pyramid_schedule is wrapped, as the reference wraps it).  Traced by an FX
+    tracer that keeps the embedding modules as leaves; the GraphModule calls the stack op directly and
+    reproduces the eager output."""
     D, n_ns = 128, 4
     _, ec, sg = _collections(pdm, dev)
 
@@ -387,7 +396,7 @@ def test_fx_trace_model_forward_with_leaf_lookups(pdm, dev):
     gm = torch.fx.GraphModule(model, graph)
     targets = [str(n.target) for n in graph.nodes if n.op in ("call_function", "call_module")]
     print(targets, flush=True)
-    assert "sg" in targets and sum("onetrans_block_fwd" in t for t in targets) == 3
+    assert "sg" in targets and sum("onetrans_stack_fwd" in t for t in targets) == 1
     with torch.no_grad():
         for seed in (30, 31):
             batch = _seq_batch(dev, 6, seed)
