@@ -1670,58 +1670,63 @@ __global__ __launch_bounds__(256) void ns_pad_w1_kernel(const uint16_t* __restri
 }
 
 // Tiled GEMM for the NS tokenizer's Linear layers, C = A . W^T (+ bias epilogue), A [M, K] rows with stride
-// a_bstride, W [N, K], K a multiple of 64.  128 x 128 tiles on 4 waves (one per SIMD, 512 registers each):
-// every k step's A and W tiles are read PD steps ahead into registers (the weight tiles come from the
-// Infinity Cache or HBM, about 2 k cycles away, while a k step is about 600 cycles of MFMA work), stored
-// to one of two LDS buffers at the start of the step before their use and read back as 32x32x16 fragments.
-template <int EPI, int PD>
-__global__ __launch_bounds__(256, 1) void ns_gemm_kernel(GemmArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t sA[2][GBM][GBK + GPAD];
-  __shared__ __attribute__((aligned(16))) uint16_t sB[2][GBN][GBK + GPAD];
+// a_bstride, W [N, K], K a multiple of 64.  A 128 x 128 tile per workgroup of 8 waves, two per SIMD: waves w
+// and w + 4 compute the same 64 x 64 quarter of the tile over the two halves of every 64-wide k step.  The
+// LDS reads per MFMA are those of one wave per quarter (each 32x32x16 fragment feeds two MFMAs of the
+// wave's 2 x 2 tiles), but every SIMD has a second wave to issue while one waits; the two halves are added
+// through LDS at the end.  A and W tiles go global -> LDS by LDS DMA (global_load_lds_dwordx4, no staging registers) into an
+// NST-stage ring filled NST - 1 steps ahead; a tile row of 128 bytes holds 16-byte piece v of row r at
+// slot v ^ ((r >> 1) & 7), so the rows of one fragment read spread over all banks.  Rows past M or N read
+// the last row (their outputs are not stored).
+constexpr int kNsStages = 4;
+constexpr int kNsTileBytes = GBM * GBK * 2;  // one 128 x 64 bf16 tile
+
+__device__ __forceinline__ uint32_t ns_slot(int r, int v) { return (uint32_t)((v ^ ((r >> 1) & 7)) << 4); }
+
+template <int EPI, int NST>
+__global__ __launch_bounds__(512, 1) void ns_gemm_kernel(GemmArgs a) {
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  char* sA = smem;                          // [NST][kNsTileBytes]
+  char* sB = smem + NST * kNsTileBytes;     // [NST][kNsTileBytes]
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-  // Block ids are dealt to the 8 XCDs round robin.  With N tiles in multiples of 8, XCD x computes N tiles
-  // [x n/8, (x+1) n/8) for every M tile: its L2 holds an eighth of W and all of A, instead of all of W (which
-  // an M-tile-per-XCD order streams through every XCD).
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int q = wave & 3, kh = wave >> 2;
+  const int wm = q >> 1, wn = q & 1;
   const int64_t bid = blockIdx.x;
   int mt, nt;
   if (a.n_tiles % 8 == 0) {
     const int per = a.n_tiles / 8;
-    const int64_t x = bid & 7, j = bid >> 3;  // j-th block of XCD x
+    const int64_t x = bid & 7, j = bid >> 3;  // j-th block of XCD x: an eighth of the N tiles, every M tile
     mt = (int)(j % a.tiles_s);
     nt = (int)(x * per + j / a.tiles_s);
   } else {
     mt = (int)(bid / a.n_tiles);
     nt = (int)(bid - (int64_t)mt * a.n_tiles);
   }
-  const int m0 = mt * GBM;
-  const int n0 = nt * GBN;
+  const int m0 = mt * GBM, n0 = nt * GBN;
   const int M = a.B;
 
-  const int lr = tid >> 3, lc = (tid & 7) * 8;
-  const uint16_t* arow[4];
-  const uint16_t* wrow[4];
+  // DMA: wave w loads chunks 2w, 2w + 1 (8 rows each) of the A tile and of the W tile; lane l of chunk c
+  // fills LDS slot l % 8 of tile row 8c + l / 8 with the piece that slot holds
+  uint32_t offa[2], offb[2];
 #pragma unroll
-  for (int p = 0; p < 4; ++p) {
-    const int m = m0 + p * 32 + lr, n = n0 + p * 32 + lr;
-    arow[p] = m < M ? a.A + (int64_t)m * a.a_bstride + lc : nullptr;
-    wrow[p] = n < a.N ? a.W + (int64_t)n * a.K + lc : nullptr;
+  for (int h = 0; h < 2; ++h) {
+    const int r = (2 * wave + h) * 8 + (lane >> 3), slot = lane & 7;
+    const int v = slot ^ ((r >> 1) & 7);
+    const int ra = min(m0 + r, M - 1) - m0, rb = min(n0 + r, a.N - 1) - n0;
+    offa[h] = (uint32_t)(((int64_t)ra * a.a_bstride + v * 8) * 2);
+    offb[h] = (uint32_t)(((int64_t)rb * a.K + v * 8) * 2);
   }
-  u32x4_t ra[PD][4], rb[PD][4];
-  auto gload = [&](int st, int k0) {
+  const uint64_t abase = (uint64_t)(uintptr_t)(a.A + (int64_t)m0 * a.a_bstride);
+  const uint64_t wbase = (uint64_t)(uintptr_t)(a.W + (int64_t)n0 * a.K);
+  const int nk = a.K / GBK;
+  auto dma = [&](int kt, int stg) {
+    const uint64_t k2 = (uint64_t)kt * GBK * 2;
 #pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      ra[st][p] = arow[p] ? *reinterpret_cast<const u32x4_t*>(arow[p] + k0) : u32x4_t{0, 0, 0, 0};
-      rb[st][p] = wrow[p] ? *reinterpret_cast<const u32x4_t*>(wrow[p] + k0) : u32x4_t{0, 0, 0, 0};
-    }
-  };
-  auto sstore = [&](int st, int buf) {
-#pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      *reinterpret_cast<u32x4_t*>(&sA[buf][p * 32 + lr][lc]) = ra[st][p];
-      *reinterpret_cast<u32x4_t*>(&sB[buf][p * 32 + lr][lc]) = rb[st][p];
+    for (int h = 0; h < 2; ++h) {
+      lds_dma16(abase + k2, offa[h], (uint32_t)(uintptr_t)(sA + stg * kNsTileBytes + (2 * wave + h) * 1024));
+      lds_dma16(wbase + k2, offb[h], (uint32_t)(uintptr_t)(sB + stg * kNsTileBytes + (2 * wave + h) * 1024));
     }
   };
 
@@ -1733,46 +1738,67 @@ __global__ __launch_bounds__(256, 1) void ns_gemm_kernel(GemmArgs a) {
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-  const int nk = a.K / GBK;
-  // k step j lives in register stage j % PD until it is stored to LDS buffer j & 1 at the start of step j - 1
+  const int fr = lane & 31, hf = lane >> 5;
+  auto compute = [&](int stg) {
+    const char* ta = sA + stg * kNsTileBytes;
+    const char* tb = sB + stg * kNsTileBytes;
 #pragma unroll
-  for (int j = 0; j < PD; ++j)
-    if (j < nk) gload(j, j * GBK);
-  sstore(0, 0);
-  if (PD < nk) gload(0, PD * GBK);
-  const int fr = lane & 31, fk = (lane >> 5) * 8;
-  for (int k0 = 0; k0 < nk; k0 += PD) {
+    for (int s2 = 0; s2 < 2; ++s2) {
+      const int v = (kh * 2 + s2) * 2 + hf;  // 16-byte piece of k = (kh*2 + s2)*16 + hf*8
+      u32x4_t af[2], bf[2];
 #pragma unroll
-    for (int s = 0; s < PD; ++s) {
-      const int kt = k0 + s;
-      if (kt < nk) {
-        // every wave is done with step kt - 1, whose buffer receives step kt + 1
-        __syncthreads();
-        if (kt + 1 < nk) {
-          sstore((s + 1) % PD, (kt + 1) & 1);
-          if (kt + 1 + PD < nk) gload((s + 1) % PD, (kt + 1 + PD) * GBK);
-        }
-        const int buf = kt & 1;
-#pragma unroll
-        for (int ks = 0; ks < GBK / 16; ++ks) {
-          u32x4_t af[2], bf[2];
-#pragma unroll
-          for (int i = 0; i < 2; ++i)
-            af[i] = *reinterpret_cast<const u32x4_t*>(&sA[buf][wm * 64 + i * 32 + fr][ks * 16 + fk]);
-#pragma unroll
-          for (int j = 0; j < 2; ++j)
-            bf[j] = *reinterpret_cast<const u32x4_t*>(&sB[buf][wn * 64 + j * 32 + fr][ks * 16 + fk]);
-#pragma unroll
-          for (int i = 0; i < 2; ++i)
-#pragma unroll
-            for (int j = 0; j < 2; ++j) acc[i][j] = mfma32x32x16(af[i], bf[j], acc[i][j]);
-        }
+      for (int i = 0; i < 2; ++i) {
+        const int r = wm * 64 + i * 32 + fr;
+        af[i] = *reinterpret_cast<const u32x4_t*>(ta + r * 128 + ns_slot(r, v));
       }
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int r = wn * 64 + j * 32 + fr;
+        bf[j] = *reinterpret_cast<const u32x4_t*>(tb + r * 128 + ns_slot(r, v));
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = mfma32x32x16(af[i], bf[j], acc[i][j]);
     }
+  };
+  constexpr int PF = NST - 1;
+#pragma unroll
+  for (int j = 0; j < PF; ++j) dma(min(j, nk - 1), j);
+  // before the barrier of step kt every DMA but the 4 * (PF - 1) issued for steps kt + 1 .. kt + PF - 1 has
+  // landed (vector memory completes in issue order)
+  constexpr unsigned kWait = 0x0F70u | (unsigned)(4 * (PF - 1));
+  static_assert(4 * (PF - 1) < 16, "vmcnt immediate");
+  for (int kt = 0; kt < nk; ++kt) {
+    __builtin_amdgcn_s_waitcnt(kWait);
+    __syncthreads();  // step kt is in LDS; every wave is done with step kt - 1, whose stage is refilled
+    // unconditional (past the end it reloads the last step into the freed stage, read by no later step)
+    dma(min(kt + PF, nk - 1), (kt + PF) % NST);
+    compute(kt % NST);
   }
+  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);  // no DMA may land in LDS after this point
+  __syncthreads();
+  // the second k half adds its quarter into the first through LDS: element e of acc[i][j] of lane l at
+  // float ((q * 64 + (i * 2 + j) * 16 + e) * 64 + l)
+  float* red = reinterpret_cast<float*>(smem);
+  if (kh == 1) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) red[(q * 64 + (i * 2 + j) * 16 + e) * 64 + lane] = acc[i][j][e];
+  }
+  __syncthreads();
+  if (kh == 1) return;
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] += red[(q * 64 + (i * 2 + j) * 16 + e) * 64 + lane];
 
-  // epilogue: acc[i][j][e] is row wm*64 + i*32 + (e/4)*8 + (lane/32)*4 + e%4, column n0 + wn*64 + j*32 + lane%32
-  const int hf = lane >> 5;
+  // epilogue: acc[i][j][e] is row wm*64 + i*32 + (e/4)*8 + hf*4 + e%4, column n0 + wn*64 + j*32 + lane%32
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -1792,7 +1818,20 @@ static int launch_ns_gemm(GemmArgs& g, hipStream_t s) {
   gemm_tiles(g);
   if (g.total_blocks == 0) return PDM_OK;
   PDM_CHECK_ARG(g.total_blocks < (int64_t(1) << 31), "GEMM grid too large");
-  hipLaunchKernelGGL((ns_gemm_kernel<EPI, 5>), dim3((unsigned)g.total_blocks), dim3(256), 0, s, g);
+  // 32-bit per-lane DMA offsets within a tile's rows
+  PDM_CHECK_ARG((int64_t)GBM * std::max<int64_t>(g.a_bstride, g.K) * 2 < (int64_t(1) << 31), "rows too long");
+  constexpr int lds = 2 * kNsStages * kNsTileBytes;
+  static std::once_flag once[64];
+  static hipError_t err[64];
+  int dev = 0;
+  PDM_CHECK_HIP(hipGetDevice(&dev));
+  PDM_CHECK_ARG(dev >= 0 && dev < 64, "device index out of range");
+  std::call_once(once[dev], [&] {
+    err[dev] = hipFuncSetAttribute(reinterpret_cast<const void*>(ns_gemm_kernel<EPI, kNsStages>),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+  });
+  PDM_CHECK_HIP(err[dev]);
+  hipLaunchKernelGGL((ns_gemm_kernel<EPI, kNsStages>), dim3((unsigned)g.total_blocks), dim3(512), lds, s, g);
   PDM_CHECK_LAUNCH();
   return PDM_OK;
 }
