@@ -396,6 +396,14 @@ __global__ __launch_bounds__(256, EPI == EPI_QKV ? PDM_QKV_WPS : 2) void rowgemm
   __shared__ __attribute__((aligned(16))) char sW[NST][CHUNK_BYTES];
   __shared__ int s_rb[TROWS];
   __shared__ int s_rt[TROWS];
+  // Q/K/V^T epilogue: each wave's 32 x 32 bf16 output tile goes through LDS (rows of 64 bytes at a stride of
+  // 80, so that the lanes' 8-byte writes of one row group hit distinct banks) and leaves as 16-byte pieces,
+  // four lanes per 64-byte row segment, instead of 8-byte pieces of 32 rows
+  constexpr int SST = 80;
+  // residual epilogue: fp32 tiles through LDS (rows of 128 bytes at a stride of 144), leaving as full
+  // 128-byte row segments, eight lanes per row; the residual is read in the same layout
+  constexpr int RST = 144;
+  __shared__ __attribute__((aligned(16))) char sStage[EPI == EPI_QKV ? 4 * 32 * SST : (EPI == EPI_RESID ? 4 * 32 * RST : 16)];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -482,11 +490,60 @@ __global__ __launch_bounds__(256, EPI == EPI_QKV ? PDM_QKV_WPS : 2) void rowgemm
   }
   const int my_row = wave * RB * 32 + fr;  // + rb * 32: this lane's row in the rows-on-lanes layout
 
+  // Staged stores (RB == 1): lane l writes 16-byte piece (l & 3) of tile rows (l >> 2) and 16 + (l >> 2).
+  // Q and K rows of those tile rows (null: no row, or a Q row outside the kept tail); for V^T, vcontig says
+  // the wave's 32 rows are the consecutive tokens t0 .. t0 + 31 of one sample b0 with t0 a multiple of 8, so
+  // a tile row of V^T (one feature, 32 tokens) is one aligned 64-byte segment.
+  constexpr bool STAGE = EPI == EPI_QKV && RB == 1;
+  constexpr bool RSTAGE = EPI == EPI_RESID && RB == 1;
+  // residual staging: lane l handles piece (l & 7) (4 outputs) of tile rows (l >> 3) + 8i, i < 4
+  float* zrow[4] = {nullptr, nullptr, nullptr, nullptr};
+  const float* rrow[4] = {nullptr, nullptr, nullptr, nullptr};
+  if constexpr (RSTAGE) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = wave * 32 + i * 8 + (lane >> 3);
+      const int b = s_rb[r], t = s_rt[r];
+      if (b >= 0) {
+        zrow[i] = reinterpret_cast<float*>(a.out) + (int64_t)b * a.out_bstride + (int64_t)t * a.N + (lane & 7) * 4;
+        rrow[i] = a.res + (int64_t)b * a.res_bstride + (int64_t)(t + a.res_toff) * a.N + (lane & 7) * 4;
+      }
+    }
+  }
+  const int spiece = lane & 3;
+  uint16_t* qrow[2] = {nullptr, nullptr};
+  uint16_t* krow[2] = {nullptr, nullptr};
+  bool vcontig = false;
+  int vb0 = 0, vt0 = 0;
+  char* stage = sStage + (STAGE ? wave * 32 * SST : 0);
+  if constexpr (STAGE) {
+#pragma unroll
+    for (int i2 = 0; i2 < 2; ++i2) {
+      const int r = wave * 32 + i2 * 16 + (lane >> 2);
+      const int b = s_rb[r], t = s_rt[r];
+      if (b >= 0) {
+        krow[i2] = a.k + ((int64_t)b * a.kv + t) * a.D;
+        const int tq = t - (a.kv - a.q_len);
+        if (tq >= 0) qrow[i2] = a.q + ((int64_t)b * a.q_len + tq) * a.D;
+      }
+    }
+    vb0 = s_rb[wave * 32];
+    vt0 = s_rt[wave * 32];
+    // uniform over the wave: every group of 4 rows is contiguous (vgrp) and the groups continue each other
+    bool ok = vb0 >= 0 && (vt0 & 7) == 0 && s_rb[wave * 32 + 31] == vb0 && s_rt[wave * 32 + 31] == vt0 + 31;
+    vcontig = __builtin_amdgcn_readfirstlane(__all(ok && vgrp == 0xf) ? 1 : 0) != 0;
+  }
+
   // chunk c with its weights at wb (the MFMAs, then after_mfma(), then the stores)
   auto chunk = [&](int c, const char* wb, auto&& after_mfma) {
     const bool cols_on_lanes = EPI == EPI_QKV && c * 32 >= 2 * a.D;
     f32x4_t res[RB][4];
-    if constexpr (EPI == EPI_RESID) {
+    if constexpr (RSTAGE) {
+      // issue the residual loads before the MFMAs (in the staged layout)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        res[0][i] = rrow[i] ? *reinterpret_cast<const f32x4_t*>(rrow[i] + c * 32) : f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    } else if constexpr (EPI == EPI_RESID) {
       // issue the residual loads before the MFMAs
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb) {
@@ -513,6 +570,23 @@ __global__ __launch_bounds__(256, EPI == EPI_QKV ? PDM_QKV_WPS : 2) void rowgemm
       // (register path) the next chunk goes to LDS before this chunk's stores: its wait on the loads would
       // otherwise also wait for the stores (vector memory completes in issue order)
       after_mfma();
+      if (STAGE && vcontig) {
+        // tile row fr = feature c*32 + fr - 2D of V, columns = the wave's 32 tokens
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          *reinterpret_cast<u32x2_t*>(stage + fr * SST + (g * 8 + hf * 4) * 2) =
+              u32x2_t{pack_bf16x2(acc[0][4 * g], acc[0][4 * g + 1]), pack_bf16x2(acc[0][4 * g + 2], acc[0][4 * g + 3])};
+        const int64_t vbs = (int64_t)(a.D >> 6) * 64 * a.kv_pad;
+#pragma unroll
+        for (int i2 = 0; i2 < 2; ++i2) {
+          const int tr = i2 * 16 + (lane >> 2);
+          const int cv = c * 32 + tr - 2 * a.D;
+          const u32x4_t v = *reinterpret_cast<const u32x4_t*>(stage + tr * SST + spiece * 16);
+          *reinterpret_cast<u32x4_t*>(a.vt + vb0 * vbs + ((int64_t)(cv >> 6) * 64 + (cv & 63)) * a.kv_pad + vt0 +
+                                      spiece * 8) = v;
+        }
+        return;
+      }
       // V^T[b, h, d, token]: column cv = c*32 + fr - 2D of V is head cv / 64, d = cv % 64
       const int cv = c * 32 + fr - 2 * a.D;
       uint16_t* vrow = a.vt + ((int64_t)(cv >> 6) * 64 + (cv & 63)) * a.kv_pad;
@@ -542,6 +616,41 @@ __global__ __launch_bounds__(256, EPI == EPI_QKV ? PDM_QKV_WPS : 2) void rowgemm
         for (int rb = 0; rb < RB; ++rb) acc[rb] = mfma32x32x16(wf, af[rb][s], acc[rb]);
       }
       after_mfma();
+      if constexpr (RSTAGE) {
+        // tile row fr = the lane's row: bf16-rounded outputs c*32 .. c*32 + 31 as fp32, then each lane adds the
+        // residual to its pieces and stores them
+        char* st = sStage + wave * 32 * RST;
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          *reinterpret_cast<f32x4_t*>(st + fr * RST + (g * 8 + hf * 4) * 4) =
+              f32x4_t{bf16_round(acc[0][4 * g]), bf16_round(acc[0][4 * g + 1]), bf16_round(acc[0][4 * g + 2]),
+                      bf16_round(acc[0][4 * g + 3])};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const f32x4_t v = *reinterpret_cast<const f32x4_t*>(st + (i * 8 + (lane >> 3)) * RST + (lane & 7) * 16);
+          if (zrow[i])
+            *reinterpret_cast<f32x4_t*>(zrow[i] + c * 32) =
+                f32x4_t{v.x + res[0][i].x, v.y + res[0][i].y, v.z + res[0][i].z, v.w + res[0][i].w};
+        }
+        return;
+      }
+      if constexpr (STAGE) {
+        // every lane writes its row of the tile (rows without a token too: their pieces are not stored), then
+        // stores the pieces of its two tile rows: columns c*32 .. c*32 + 31 of Q or K
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          *reinterpret_cast<u32x2_t*>(stage + fr * SST + (g * 8 + hf * 4) * 2) =
+              u32x2_t{pack_bf16x2(acc[0][4 * g], acc[0][4 * g + 1]), pack_bf16x2(acc[0][4 * g + 2], acc[0][4 * g + 3])};
+        const bool isq = c * 32 < a.D;
+        const int col = (isq ? c * 32 : c * 32 - a.D) + spiece * 8;
+#pragma unroll
+        for (int i2 = 0; i2 < 2; ++i2) {
+          uint16_t* o = isq ? qrow[i2] : krow[i2];
+          const u32x4_t v = *reinterpret_cast<const u32x4_t*>(stage + (i2 * 16 + (lane >> 2)) * SST + spiece * 16);
+          if (o) *reinterpret_cast<u32x4_t*>(o + col) = v;
+        }
+        return;
+      }
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb) {
         const int b = s_rb[my_row + rb * 32];
