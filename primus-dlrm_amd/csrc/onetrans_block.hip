@@ -135,6 +135,7 @@ struct GemmArgs {
   const uint16_t* W2;     // FFN-down [D, F] shared
   const uint16_t* W2_ns;  // [n_ns, D, F]
   const uint16_t* bias;   // EPI_BIAS_*: bf16 [N]
+  const uint16_t* Wo;     // FFN with the out-projection in front: Wout [D, D], shared by every token
 };
 
 // Stores one GEMM output element (b, t, n) with the epilogue EPI.
@@ -734,8 +735,18 @@ __global__ __launch_bounds__(256, EPI == EPI_QKV ? PDM_QKV_WPS : 2) void rowgemm
 // read into registers in two halves (W1 during the FFN-up MFMAs, W2 during
 // GELU and FFN-down) and written to the stage chunk c - 1 used.  The
 // epilogue adds z (fp32) to the bf16-rounded FFN output.
+//
+// OPROJ: the out-projection runs in front, z = bf16(O . Wout^T) + x, so z is
+// produced on chip instead of being read back from memory.  z^T = Wout . O^T
+// accumulates straight into the y registers (the same layout: lane l holds
+// row l%32), the O fragments stream from memory one 64-column chunk ahead and
+// the Wout chunks (D rows x 64 columns, exactly one ring stage) go through the
+// same ring in front of the FFN chunks.  z is added to the residual x, written
+// to the output rows (the epilogue reads it back there), and normalised in
+// registers; the RMSNorm2 values reach the B-operand layout of the FFN-up
+// with one exchange of two words per 16-column step between the half-waves.
 // ---------------------------------------------------------------------------
-template <int D, int RB, int NW, int NST, int WPS>
+template <int D, int RB, int NW, int NST, int WPS, bool OPROJ>
 __global__ __launch_bounds__(NW * 64, WPS) void ffn_kernel(GemmArgs a) {
   constexpr int NT = NW * 64;                // threads
   constexpr int PF = NST - 1;                // chunks read ahead
@@ -805,14 +816,137 @@ __global__ __launch_bounds__(NW * 64, WPS) void ffn_kernel(GemmArgs a) {
   constexpr unsigned kWaitDma = 0x0F70u | (unsigned)((PF - 1) * (L1 + L2));
   static_assert((PF - 1) * (L1 + L2) < 16, "vmcnt immediate");
   __syncthreads();
-#pragma unroll
-  for (int c = 0; c < PF; ++c)
-    if (c < nchunks) dma(c, c);
-
   u32x4_t hfr[RB][KS];
-  load_row_fragments<D, RB, true>(a, s_rb, s_rt, wave, fr, hf, hfr);
-
   f32x16_t y[RB][DB];
+  if constexpr (OPROJ) {
+    static_assert(RB == 1 && NST == 2, "the out-projection prologue assumes one row block and a 2-stage ring");
+    constexpr int DW = D / 64;  // Wout chunks of 64 columns, each D rows x 128 bytes = one ring stage
+    static_assert(DW % NST == 0, "FFN chunk c must keep stage c % NST");
+    // Wout chunk kc: LDS row r (output feature) = Wout[r, kc*64 .. +64), rows 0 .. D/2 - 1 in the W1 part of
+    // the stage, the rest in its W2 part; 16-byte piece v of a row at slot v ^ (r & 7)
+    uint32_t offw[L1 + L2];
+#pragma unroll
+    for (int p = 0; p < L1 + L2; ++p) {
+      const int o = p * NT + tid, r = o >> 3;
+      offw[p] = (uint32_t)((r * D + (((o & 7) ^ (r & 7)) << 3)) * 2);
+    }
+    auto dma_wo = [&](int kc, int stg) {
+      const uint64_t b = (uint64_t)(uintptr_t)a.Wo + (uint64_t)kc * 128;
+#pragma unroll
+      for (int p = 0; p < L1; ++p)
+        lds_dma16(b, offw[p], (uint32_t)(uintptr_t)(sW1[stg] + (p * NT + wave * 64) * 16));
+#pragma unroll
+      for (int p = L1; p < L1 + L2; ++p)
+        lds_dma16(b, offw[p], (uint32_t)(uintptr_t)(sW2[stg] + ((p - L1) * NT + wave * 64) * 16));
+    };
+    const int row = wave * 32 + fr;
+    const int b = s_rb[row], t = s_rt[row];
+    const bool valid = b >= 0;
+    // O row of this lane (columns hf*8 .. of each 16-column step); rows past the end read row 0 unused
+    const uint16_t* orow = a.A + (valid ? (int64_t)b * a.a_bstride + (int64_t)t * D : 0) + hf * 8;
+    // every O fragment of the row (4 per Wout chunk) is requested up front, after the DMA of the first two
+    // Wout chunks (both ring stages are free), so one memory latency covers the whole out-projection
+    u32x4_t ofr[DW][4];
+    dma_wo(0, 0);
+    dma_wo(1, 1);
+#pragma unroll
+    for (int kc = 0; kc < DW; ++kc)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) ofr[kc][s] = *reinterpret_cast<const u32x4_t*>(orow + kc * 64 + s * 16);
+    const float* xrow = a.res + (valid ? (int64_t)b * a.res_bstride + (int64_t)(t + a.res_toff) * D : 0) + hf * 4;
+    f32x4_t xv[DB][4];
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) y[0][db][e] = 0.0f;
+#pragma unroll
+    for (int kc = 0; kc < DW; ++kc) {
+      const int stg = kc % NST;
+      // chunk kc's Wout rows have landed and every wave is done with the stage the next DMA fills.  Only DMA
+      // pieces are counted (the compiler may issue the O loads later; it waits for those itself): at chunk 0
+      // the L1 + L2 pieces of Wout chunk 1 may still be in flight, later chunks wait for everything.
+      if (kc == 0) __builtin_amdgcn_s_waitcnt(0x0F70u | (unsigned)(L1 + L2));
+      else __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+      __syncthreads();
+      if (kc >= 1) {
+        if (kc + 1 < DW) dma_wo(kc + 1, (kc + 1) % NST);
+        else dma(0, (kc + 1) % NST);  // FFN chunk 0
+      }
+      if (kc == DW - 1) {
+        // the residual of the first half of the outputs, before the last chunk's MFMAs
+#pragma unroll
+        for (int db = 0; db < DB / 2; ++db)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) xv[db][g] = *reinterpret_cast<const f32x4_t*>(xrow + db * 32 + g * 8);
+      }
+      // z^T[db] += Wout[db rows, kc*64 + s*16 ..] . O^T: logical piece 2s + hf of row db*32 + fr
+      u32x4_t wf[4 * DB];
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+          const char* base = db < DB / 2 ? sW1[stg] + (db * 32 + fr) * 128 : sW2[stg] + ((db - DB / 2) * 32 + fr) * 128;
+          wf[s * DB + db] = *reinterpret_cast<const u32x4_t*>(base + (((2 * s + hf) ^ (fr & 7)) << 4));
+        }
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int db = 0; db < DB; ++db) y[0][db] = mfma32x32x16(wf[s * DB + db], ofr[kc][s], y[0][db]);
+      sched_mfma_ds_pipeline<4 * DB, 4>();
+    }
+    // z = bf16(O . Wout^T) + x[:, t + res_toff] in y (lane: row fr, outputs db*32 + g*8 + hf*4 + 0..3), written
+    // to the output rows, where the epilogue reads it back
+    float* zrow = reinterpret_cast<float*>(a.out) + (valid ? (int64_t)b * a.out_bstride + (int64_t)t * D : 0) + hf * 4;
+    float ss = 0.0f;
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+      // the residual stays DB / 2 blocks ahead of its use
+      if (db + DB / 2 < DB) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          xv[db + DB / 2][g] = *reinterpret_cast<const f32x4_t*>(xrow + (db + DB / 2) * 32 + g * 8);
+      }
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float z = bf16_round(y[0][db][4 * g + j]) + xv[db][g][j];
+          y[0][db][4 * g + j] = z;
+          ss += z * z;
+        }
+        if (valid)
+          *reinterpret_cast<f32x4_t*>(zrow + db * 32 + g * 8) =
+              f32x4_t{y[0][db][4 * g], y[0][db][4 * g + 1], y[0][db][4 * g + 2], y[0][db][4 * g + 3]};
+      }
+    }
+    ss += __shfl_xor(ss, 32, 64);
+    const float rms = 1.0f / sqrtf(ss / (float)D + 1e-6f);
+    // RMSNorm2 -> the FFN-up B operand: 16-column step s (block db = s / 2, groups g0 = 2 (s % 2) and g0 + 1)
+    // needs columns 16s + hf*8 + 0..7 in lane (fr, hf); the lane holds g0*8 + hf*4 + 0..3 and (g0+1)*8 + hf*4
+    // + 0..3, so the half-waves swap one 4-column group
+    const float* nw = a.norm_w + hf * 4;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const int db = s >> 1, g0 = 2 * (s & 1);
+      const f32x4_t w0 = *reinterpret_cast<const f32x4_t*>(nw + db * 32 + g0 * 8);
+      const f32x4_t w1 = *reinterpret_cast<const f32x4_t*>(nw + db * 32 + g0 * 8 + 8);
+      const f32x16_t& zb = y[0][db];
+      const int e0 = 4 * g0;
+      const uint32_t a0 = pack_bf16x2((zb[e0] * rms) * w0.x, (zb[e0 + 1] * rms) * w0.y);
+      const uint32_t a1 = pack_bf16x2((zb[e0 + 2] * rms) * w0.z, (zb[e0 + 3] * rms) * w0.w);
+      const uint32_t b0 = pack_bf16x2((zb[e0 + 4] * rms) * w1.x, (zb[e0 + 5] * rms) * w1.y);
+      const uint32_t b1 = pack_bf16x2((zb[e0 + 6] * rms) * w1.z, (zb[e0 + 7] * rms) * w1.w);
+      const uint32_t r0 = (uint32_t)__shfl_xor((int)(hf ? a0 : b0), 32, 64);
+      const uint32_t r1 = (uint32_t)__shfl_xor((int)(hf ? a1 : b1), 32, 64);
+      hfr[0][s] = hf ? u32x4_t{r0, r1, b0, b1} : u32x4_t{a0, a1, r0, r1};
+    }
+  } else {
+#pragma unroll
+    for (int c = 0; c < PF; ++c)
+      if (c < nchunks) dma(c, c);
+    load_row_fragments<D, RB, true>(a, s_rb, s_rt, wave, fr, hf, hfr);
+  }
+
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
@@ -895,15 +1029,37 @@ __global__ __launch_bounds__(NW * 64, WPS) void ffn_kernel(GemmArgs a) {
   // Epilogue y = z + bf16(FFN).  y[rb][db][e] is output d = db*32 + (e/4)*8 + hf*4 + e%4 of row
   // wave*RB*32 + rb*32 + fr.  The values go through LDS (the weight ring is free now) SEG outputs at a
   // time, so that z is read and y written as whole row segments of SEG outputs, with
-  // non-temporal stores (y is streamed to memory; the next kernel reads it from there).
-  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);  // the last DMA must land before the ring is reused
-  __syncthreads();
+  // non-temporal stores (y is streamed to memory; the next kernel reads it from there).  The z segments
+  // of the first two passes are requested before the last DMA is awaited, each later pass's when the
+  // pass two before it is done, so the passes do not wait for memory one after another.
   constexpr int SEG = NW * RB * 32 * (64 * 4 + 16) <= RING_BYTES ? 64 : 32;  // outputs per pass
   constexpr int SROW = SEG * 4 + 16;       // LDS row stride (bytes), padded against bank conflicts
+  constexpr int NQ = D / SEG;              // passes
+  constexpr int EK = RB * 32 * (SEG / 4) / 64;  // 16-byte pieces per lane and pass
   static_assert(NW * RB * 32 * SROW <= RING_BYTES, "epilogue staging must fit the weight ring");
+  const float* zsrc = OPROJ ? reinterpret_cast<const float*>(a.out) : a.res;
+  int64_t eoff[EK];  // piece k of this lane: its row's output offset + its 4 columns (pass 0), or -1
+#pragma unroll
+  for (int k = 0; k < EK; ++k) {
+    const int piece = k * 64 + lane;     // 16-byte piece of the wave's RB*32 x SEG tile
+    const int r = piece / (SEG / 4), c4 = piece - (piece / (SEG / 4)) * (SEG / 4);
+    const int row = wave * RB * 32 + r;
+    const int b = s_rb[row];
+    eoff[k] = b < 0 ? -1 : (int64_t)b * a.out_bstride + (int64_t)s_rt[row] * D + c4 * 4;
+  }
+  f32x4_t zv[2][EK];
+  auto zload = [&](int q) {
+#pragma unroll
+    for (int k = 0; k < EK; ++k)
+      zv[q & 1][k] = *reinterpret_cast<const f32x4_t*>(zsrc + (eoff[k] < 0 ? 0 : eoff[k] + q * SEG));
+  };
+  zload(0);
+  if (NQ > 1) zload(1);
+  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);  // the last DMA must land before the ring is reused
+  __syncthreads();
   char* stage = sRing + wave * (RB * 32 * SROW);
 #pragma unroll
-  for (int q = 0; q < D / SEG; ++q) {
+  for (int q = 0; q < NQ; ++q) {
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
@@ -917,18 +1073,16 @@ __global__ __launch_bounds__(NW * 64, WPS) void ffn_kernel(GemmArgs a) {
       }
     // each wave reads back only its own tile; a wave's LDS accesses execute in order, so no barrier
 #pragma unroll
-    for (int k = 0; k < RB * 32 * (SEG / 4) / 64; ++k) {
-      const int piece = k * 64 + lane;     // 16-byte piece of the wave's RB*32 x SEG tile
+    for (int k = 0; k < EK; ++k) {
+      const int piece = k * 64 + lane;
       const int r = piece / (SEG / 4), c4 = piece - (piece / (SEG / 4)) * (SEG / 4);
-      const int row = wave * RB * 32 + r;
-      const int b = s_rb[row];
-      if (b < 0) continue;
-      const int64_t off = (int64_t)b * a.out_bstride + (int64_t)s_rt[row] * D + q * SEG + c4 * 4;
-      const f32x4_t z = *reinterpret_cast<const f32x4_t*>(a.res + off);
       const f32x4_t v = *reinterpret_cast<const f32x4_t*>(stage + r * SROW + c4 * 16);
-      __builtin_nontemporal_store(f32x4_t{z.x + v.x, z.y + v.y, z.z + v.z, z.w + v.w},
-                                  reinterpret_cast<f32x4_t*>(reinterpret_cast<float*>(a.out) + off));
+      const f32x4_t z = zv[q & 1][k];
+      if (eoff[k] >= 0)
+        __builtin_nontemporal_store(f32x4_t{z.x + v.x, z.y + v.y, z.z + v.z, z.w + v.w},
+                                    reinterpret_cast<f32x4_t*>(reinterpret_cast<float*>(a.out) + eoff[k] + q * SEG));
     }
+    if (q + 2 < NQ) zload(q + 2);
   }
 }
 
@@ -1418,13 +1572,18 @@ static int launch_rowgemm(GemmArgs& g, int D, hipStream_t s) {
 #ifndef PDM_FFN_WPS
 #define PDM_FFN_WPS 2
 #endif
+// the out-projection runs in the FFN kernel (1) or as its own GEMM in front of it (0)
+#ifndef PDM_FFN_OPROJ
+#define PDM_FFN_OPROJ 1
+#endif
+template <bool OPROJ>
 static int launch_ffn(GemmArgs& g, int D, hipStream_t s) {
   constexpr int RB = PDM_FFN_RB, NW = PDM_FFN_NW, NST = PDM_FFN_NST, WPS = PDM_FFN_WPS;
   const int64_t tiles = row_tiles(g, NW * RB * 32);
   if (tiles == 0) return PDM_OK;
   PDM_CHECK_ARG(tiles < (int64_t(1) << 31), "FFN grid too large");
-  if (D == 256) hipLaunchKernelGGL((ffn_kernel<256, RB, NW, NST, WPS>), dim3((unsigned)tiles), dim3(NW * 64), 0, s, g);
-  else hipLaunchKernelGGL((ffn_kernel<128, RB, NW, NST, WPS>), dim3((unsigned)tiles), dim3(NW * 64), 0, s, g);
+  if (D == 256) hipLaunchKernelGGL((ffn_kernel<256, RB, NW, NST, WPS, OPROJ>), dim3((unsigned)tiles), dim3(NW * 64), 0, s, g);
+  else hipLaunchKernelGGL((ffn_kernel<128, RB, NW, NST, WPS, OPROJ>), dim3((unsigned)tiles), dim3(NW * 64), 0, s, g);
   PDM_CHECK_LAUNCH();
   return PDM_OK;
 }
@@ -1549,6 +1708,24 @@ static int block_fwd(const pdm_block_desc& d, const float* x, const pdm_block_we
     }
     PDM_CHECK_LAUNCH();
   }
+#if PDM_FFN_OPROJ
+  if (fused_path(d)) {
+    // 4. z = bf16(O . Wout^T) + x[:, kv - q_len:] (written to y), y = z + bf16(W2 . gelu(W1 . RMSNorm2(z))):
+    // out-projection, norm, both FFN GEMMs and GELU in one kernel
+    GemmArgs g2{};
+    g2.A = q; g2.a_bstride = (int64_t)ql * D;
+    g2.Wo = reinterpret_cast<const uint16_t*>(w->out_w);
+    g2.res = x; g2.res_bstride = (int64_t)kv * D; g2.res_toff = kv - ql;
+    g2.norm_w = w->norm2_w;
+    g2.W = reinterpret_cast<const uint16_t*>(w->s_w1);
+    g2.W_ns = reinterpret_cast<const uint16_t*>(w->ns_w1);
+    g2.W2 = reinterpret_cast<const uint16_t*>(w->s_w2);
+    g2.W2_ns = reinterpret_cast<const uint16_t*>(w->ns_w2);
+    g2.B = B; g2.n_s = ql - nns; g2.n_ns = nns; g2.N = F; g2.K = D;
+    g2.out = y; g2.out_bstride = (int64_t)ql * D;
+    return launch_ffn<true>(g2, D, s);
+  }
+#endif
   // 4. z = bf16(O . Wout^T) + x[:, kv - q_len:]  -> y
   {
     GemmArgs g1{};
@@ -1573,7 +1750,7 @@ static int block_fwd(const pdm_block_desc& d, const float* x, const pdm_block_we
     g2.W2_ns = reinterpret_cast<const uint16_t*>(w->ns_w2);
     g2.B = B; g2.n_s = ql - nns; g2.n_ns = nns; g2.N = F; g2.K = D;
     g2.out = y; g2.out_bstride = (int64_t)ql * D; g2.res = y;
-    return launch_ffn(g2, D, s);
+    return launch_ffn<false>(g2, D, s);
   }
   // 5. h2 = RMSNorm2(z)  [B, q_len, D]
   if ((st = launch_rmsnorm(y, (int64_t)ql * D, ql, B, D, w->norm2_w, h, s)) != PDM_OK) return st;
