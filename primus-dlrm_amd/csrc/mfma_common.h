@@ -119,6 +119,19 @@ __device__ __forceinline__ void gelu_lut_pack(const float* t, const float* u, ui
                 __builtin_fmaf(-fabsf(x[i + 1]), e[i + 1], fmaxf(x[i + 1], 0.0f))}, bf16x2_t));
 }
 
+// 16 bytes per lane from global memory (uniform base + per-lane 32-bit byte offset) into LDS at the
+// wave-uniform address lds + 16 * lane (global_load_lds_dwordx4; M0 holds the LDS address, one wait state
+// between its write and the load).  Completion is counted by vmcnt.
+__device__ __forceinline__ void lds_dma16(uint64_t base, uint32_t off, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :: "v"(off), "s"(base), "s"(lds) : "memory", "m0");
+}
+
+// s_waitcnt immediates (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt bits 6:4 left at 7, lgkmcnt bits
+// 11:8 left at 15), issued through the builtin so that the compiler's own wait tracking sees them.
+constexpr unsigned waitcnt_vm(unsigned n) { return 0x0F70u | (n & 15u) | ((n >> 4) << 14); }
+constexpr unsigned kWaitVmcnt0 = waitcnt_vm(0);
+
 template <int D>
 constexpr int w_stride() { return 2 * D + 16; }
 

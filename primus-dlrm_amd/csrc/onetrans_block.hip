@@ -35,6 +35,12 @@
 
 #include "pdm_common.h"
 #include "mfma_common.h"
+#include "block_kernels.h"
+
+// d_model 256 runs the Q/K/V projection weight-stationary (1) or as the row GEMM (0)
+#ifndef PDM_QKV_STATIONARY
+#define PDM_QKV_STATIONARY 1
+#endif
 
 namespace pdm {
 
@@ -92,18 +98,6 @@ __global__ __launch_bounds__(256) void rmsnorm_bf16_kernel(const float* __restri
 enum { EPI_BF16 = 0, EPI_QKV = 1, EPI_RESID = 2, EPI_GELU = 3, EPI_BIAS_GELU = 4, EPI_BIAS_F32 = 5 };
 
 constexpr int GBM = 128, GBN = 128, GBK = 64, GPAD = 8;
-
-// 16 bytes per lane from global memory (uniform base + per-lane 32-bit byte offset) into LDS at the
-// wave-uniform address lds + 16 * lane (global_load_lds_dwordx4; M0 holds the LDS address, one wait state
-// between its write and the load).  Completion is counted by vmcnt.
-// s_waitcnt vmcnt(0) (gfx9 encoding: vmcnt bits 3:0 and 15:14 zero, expcnt 7, lgkmcnt 15), issued through
-// the builtin so that the compiler's own wait tracking knows every vector memory access is complete
-constexpr unsigned kWaitVmcnt0 = 0x0F70;
-
-__device__ __forceinline__ void lds_dma16(uint64_t base, uint32_t off, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
-               :: "v"(off), "s"(base), "s"(lds) : "memory", "m0");
-}
 
 struct GemmArgs {
   const uint16_t* A;  // bf16 rows: row (b, t) at A + b * a_bstride + t * K
@@ -1666,7 +1660,16 @@ static int block_fwd(const pdm_block_desc& d, const float* x, const pdm_block_we
   const int kv = d.kv_len, ql = d.q_len, nns = d.n_ns;
   int st;
 
-  if (fused_path(d)) {
+  if (fused_path(d) && D == 256 && PDM_QKV_STATIONARY) {
+    // 1. Q (tail rows), K, V^T = RMSNorm1(x) . Wqkv^T  (weight-stationary, norm fused)
+    QkvArgs qa{};
+    qa.x = x; qa.x_bstride = (int64_t)kv * D; qa.norm_w = w->norm1_w;
+    qa.W = reinterpret_cast<const uint16_t*>(w->s_qkv_w);
+    qa.W_ns = reinterpret_cast<const uint16_t*>(w->ns_qkv_w);
+    qa.q = q; qa.k = k; qa.vt = vt;
+    qa.B = B; qa.kv = kv; qa.q_len = ql; qa.n_ns = nns; qa.kv_pad = L.kv_pad;
+    if ((st = launch_qkv_stationary(qa, D, s)) != PDM_OK) return st;
+  } else if (fused_path(d)) {
     // 1. Q (tail rows), K, V^T = RMSNorm1(x) . Wqkv^T  (norm fused into the GEMM)
     GemmArgs g0{};
     g0.A32 = x; g0.a_bstride = (int64_t)kv * D; g0.norm_w = w->norm1_w;
