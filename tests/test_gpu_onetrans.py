@@ -125,6 +125,14 @@ def test_block_batch1024_short_sequence(pdm, dev):
     _run_case(pdm, dev, 1024, 48, 32, 16, seed=12, norm_std=0.1)
 
 
+def test_block_ns_tiles_cross_tokens(pdm, dev):
+    """Batch 1100 with 16 NS tokens: 35 row tiles of 32 samples per NS token (the last partial), 560 NS
+    tiles over the Q/K/V projection's persistent grid, so workgroups' shares start and end inside a token's
+    tiles and cross from one NS token's weight to the next; 33 S tokens (one full and one single-row tile per
+    sample) with the kept tail starting inside the first tile."""
+    _run_case(pdm, dev, 1100, 49, 20, 16, seed=13, norm_std=0.1)
+
+
 @pytest.mark.parametrize("B,kv,q_len", [
     (2, 720, 300),       # above the LDS-resident attention's 608 keys: the streaming attention kernel
     (1, 1516, 1516),     # the reference OneTransL's first layer (L_S = 1500 + 16 NS, full causal)
