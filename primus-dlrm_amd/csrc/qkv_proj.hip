@@ -14,20 +14,16 @@
 // persistent grid gives every workgroup an even share of the S tiles and then of the NS tiles (token-major,
 // so a share mostly needs one NS weight), walked by a cursor without divisions; the weight registers are
 // loaded at the start of each run of tiles that share a weight.  Per tile:
-//  - the fp32 rows arrive by LDS DMA (global_load_lds_dwordx4, one instruction per 1 KB row) into a
-//    3-stage ring, three tiles ahead; each wave loads and normalises its own 8 rows (8 lanes per row,
-//    the sum of squares reduced with DPP moves), so the ring needs no barrier, and writes the bf16 rows
-//    into a double-buffered tile in the MFMA operand layout (rows 528 bytes apart);
+//  - each wave loads its own 8 fp32 rows into registers one tile ahead (lane l: row l / 8, 32 columns) and
+//    normalises them (8 lanes per row, the sum of squares reduced with DPP moves) into a double-buffered
+//    bf16 tile in the MFMA operand layout (rows 528 bytes apart);
 //  - one barrier; each wave then runs its three block pairs (Q, K, V), each as one asm statement of 32
 //    MFMAs whose weight operands are named registers (the compiler otherwise copies AGPR-held operands
 //    into VGPRs before every MFMA) and whose tile operands are read four k steps ahead.  Q and K come out
 //    token-per-lane (acc = W . h^T) and leave through a per-wave LDS staging tile as 128-byte row segments;
 //    V comes out column-per-lane (acc = h . W^T) and leaves as 64-byte V^T segments of 32 tokens.
-// The DMA completions are waited with vmcnt, which also counts the stores issued after the DMA: a
-// regular tile (32 S tokens, Q for all or none) issues at least kMinStores stores per wave, any other
-// tile ends with a full wait, so the wait of a tile can leave the newer DMAs and stores in flight.
 // Measured on one MI355X (B=1024, 400 tokens, d_model 256): 286 us against 315 us for the row GEMM
-// (A-stationary, weights streamed through LDS) it replaces; the shader clock runs at about 1.7 GHz.
+// (A-stationary, weights streamed through LDS) it replaces.
 #include "block_kernels.h"
 #include "mfma_common.h"
 
@@ -39,12 +35,8 @@ namespace {
 
 constexpr int kD = 256;                // d_model
 constexpr int kKS = kD / 16;           // k steps
-constexpr int kRow32 = kD * 4;         // bytes of an fp32 row
 constexpr int kRow16 = kD * 2;         // bytes of a bf16 row
 constexpr int kNormStride = kRow16 + 16;  // normalised tile row stride (rows 4 banks apart)
-constexpr int kNst = 3;                // raw tile ring depth = DMA distance in tiles
-constexpr int kDmaPerTile = 8;         // DMA instructions per wave per tile (its 8 rows)
-constexpr int kMinStores = 8;          // stores per wave of a regular tile without Q (K 4, V^T 4)
 constexpr int kQkStride = 144;         // Q/K staging: 32 token rows of 64 bf16 (+16 B)
 constexpr int kVStride = 80;           // V staging: 64 feature rows of 32 bf16 (+16 B)
 constexpr int kStageBytes = 64 * kVStride;
@@ -58,17 +50,6 @@ struct QkvTile {
   bool regular;  // S tile of 32 tokens whose rows all or none need Q
 };
 
-// vmcnt wait for the DMA of the tile k = min(it, kNst) iterations into the range: every later tile's
-// DMA (kNst - 1 of them) and at least kMinStores stores of each of the k tiles before came after it.
-__device__ __forceinline__ void wait_tile_dma(int k) {
-  switch (k) {
-    case 0: __builtin_amdgcn_s_waitcnt(waitcnt_vm((kNst - 1) * kDmaPerTile)); break;
-    case 1: __builtin_amdgcn_s_waitcnt(waitcnt_vm((kNst - 1) * kDmaPerTile + kMinStores)); break;
-    case 2: __builtin_amdgcn_s_waitcnt(waitcnt_vm((kNst - 1) * kDmaPerTile + 2 * kMinStores)); break;
-    default: __builtin_amdgcn_s_waitcnt(waitcnt_vm((kNst - 1) * kDmaPerTile + 3 * kMinStores)); break;
-  }
-}
-static_assert(kNst == 3 && (kNst - 1) * kDmaPerTile + 3 * kMinStores < 64, "vmcnt range");
 
 // The 32 MFMAs of one block pair over the 16 k steps, as one asm statement: the weight operands are named
 // register operands (the Q/K weights in AGPRs, the V weights in VGPRs), so no copies are made before each
@@ -133,7 +114,7 @@ __device__ __forceinline__ void chain_h_by_w(f32x16_t& acc0, f32x16_t& acc1, con
 }  // namespace
 
 __global__ __launch_bounds__(256, 1) void qkv_stationary_kernel(QkvArgs a) {
-  __shared__ __attribute__((aligned(16))) char sRaw[kNst][32 * kRow32];
+  __shared__ __attribute__((aligned(16))) float sNw[kD];
   __shared__ __attribute__((aligned(16))) char sNorm[2][32 * kNormStride];
   __shared__ __attribute__((aligned(16))) char sStage[4][kStageBytes];
 
@@ -148,13 +129,7 @@ __global__ __launch_bounds__(256, 1) void qkv_stationary_kernel(QkvArgs a) {
   const int n_s_own = se - sb, count = n_s_own + ne - nb;
   if (count == 0) return;
   const int qlo = a.kv - a.q_len;
-  // RMSNorm1 weights of the lane's columns 64 j + 8 (lane % 8) .. +7 (the normalisation layout below)
-  f32x4_t nw[8];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    nw[2 * j] = *reinterpret_cast<const f32x4_t*>(a.norm_w + 64 * j + 8 * (lane & 7));
-    nw[2 * j + 1] = *reinterpret_cast<const f32x4_t*>(a.norm_w + 64 * j + 8 * (lane & 7) + 4);
-  }
+  sNw[tid] = a.norm_w[tid];  // RMSNorm1 weight (256 threads, 256 columns)
 
   // tile at position p as (b, t): S tile: sample b, first token t; NS tile: first sample b, token t.  The
   // loop advances positions without divisions; seek() divides, at the start and at the first NS tile.
@@ -219,26 +194,25 @@ __global__ __launch_bounds__(256, 1) void qkv_stationary_kernel(QkvArgs a) {
     }
   };
 
-  // DMA of tile t's rows 8 wave .. 8 wave + 7 (past the tile's end: its last row again) into stage stg
-  auto dma_tile = [&](const QkvTile& T, int stg) {
+  // The next tile's rows are loaded into registers while the current tile is computed: lane l holds
+  // row 8 wave + l / 8 of the tile (past the tile's end: its last row), columns 64 j + 8 (l % 8) .. +7
+  f32x4_t xv[8];
+  auto load_rows = [&](const QkvTile& T) {
+    const int r = min(8 * wave + (lane >> 3), T.nrows - 1);
+    const float* src = (T.ns ? a.x + (int64_t)(T.b + r) * a.x_bstride + (int64_t)T.t0 * kD
+                             : a.x + (int64_t)T.b * a.x_bstride + (int64_t)(T.t0 + r) * kD) + 8 * (lane & 7);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int r = min(8 * wave + i, T.nrows - 1);
-      const float* src = T.ns ? a.x + (int64_t)(T.b + r) * a.x_bstride + (int64_t)T.t0 * kD
-                              : a.x + (int64_t)T.b * a.x_bstride + (int64_t)(T.t0 + r) * kD;
-      lds_dma16((uint64_t)(uintptr_t)src, (uint32_t)lane * 16,
-                (uint32_t)(uintptr_t)(sRaw[stg] + (8 * wave + i) * kRow32));
+    for (int j = 0; j < 4; ++j) {
+      xv[2 * j] = *reinterpret_cast<const f32x4_t*>(src + 64 * j);
+      xv[2 * j + 1] = *reinterpret_cast<const f32x4_t*>(src + 64 * j + 4);
     }
   };
-
-  // DMA cursor: kNst tiles ahead of the compute cursor, held at the last tile
+  // load cursor: one tile ahead of the compute cursor
   int ap = 0, ab = 0, at = 0;
   seek(0, ab, at);
-#pragma unroll
-  for (int j = 0; j < kNst; ++j) {
-    dma_tile(tile_from(ap, ab, at), j);
-    if (ap < count - 1) advance(ap, ab, at);
-  }
+  load_rows(tile_from(ap, ab, at));
+  if (ap < count - 1) advance(ap, ab, at);
+  __syncthreads();  // sNw
 
   char* stage = sStage[wave];
   int it = 0, cb = 0, ct = 0;
@@ -250,20 +224,14 @@ __global__ __launch_bounds__(256, 1) void qkv_stationary_kernel(QkvArgs a) {
     load_weights(ws);
     __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);  // the weights are read by asm statements
   for (; it < seg_end; advance(it, cb, ct)) {
-    const int stg = it % kNst;
     const QkvTile T = tile_from(it, cb, ct);
-    wait_tile_dma(min(it, kNst));
 
     // RMSNorm1 of this wave's rows: lane holds row 8 wave + lane / 8, columns 64 j + 8 (lane % 8) .. +7
     {
       const int r = 8 * wave + (lane >> 3), sub = lane & 7;
-      const char* src = sRaw[stg] + r * kRow32 + sub * 32;
       f32x4_t v[8];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        v[2 * j] = *reinterpret_cast<const f32x4_t*>(src + j * 256);
-        v[2 * j + 1] = *reinterpret_cast<const f32x4_t*>(src + j * 256 + 16);
-      }
+      for (int i = 0; i < 8; ++i) v[i] = xv[i];
       float ss = 0.0f;
 #pragma unroll
       for (int i = 0; i < 8; ++i) ss += v[i].x * v[i].x + v[i].y * v[i].y + v[i].z * v[i].z + v[i].w * v[i].w;
@@ -275,7 +243,8 @@ __global__ __launch_bounds__(256, 1) void qkv_stationary_kernel(QkvArgs a) {
       char* dst = sNorm[it & 1] + r * kNormStride;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const f32x4_t w0 = nw[2 * j], w1 = nw[2 * j + 1];
+        const f32x4_t w0 = *reinterpret_cast<const f32x4_t*>(sNw + 64 * j + 8 * sub);
+        const f32x4_t w1 = *reinterpret_cast<const f32x4_t*>(sNw + 64 * j + 8 * sub + 4);
         const f32x4_t a0 = v[2 * j], a1 = v[2 * j + 1];
         *reinterpret_cast<u32x4_t*>(dst + (8 * j + sub) * 16) =
             u32x4_t{pack_bf16x2((a0.x * rms) * w0.x, (a0.y * rms) * w0.y),
@@ -284,9 +253,11 @@ __global__ __launch_bounds__(256, 1) void qkv_stationary_kernel(QkvArgs a) {
                     pack_bf16x2((a1.z * rms) * w1.z, (a1.w * rms) * w1.w)};
       }
     }
-    // this wave's rows of the stage are read: refill it three tiles ahead (past the end: the last tile)
-    dma_tile(tile_from(ap, ab, at), stg);
-    if (ap < count - 1) advance(ap, ab, at);
+    // the rows are consumed: request the next tile's
+    if (it + 1 < count) {
+      load_rows(tile_from(ap, ab, at));
+      if (ap < count - 1) advance(ap, ab, at);
+    }
     __syncthreads();  // the normalised tile is complete; every wave is done with the tile two back
 
     // lane-dependent offsets are recomputed per tile from an opaque copy of the lane index, so that the
@@ -353,10 +324,8 @@ __global__ __launch_bounds__(256, 1) void qkv_stationary_kernel(QkvArgs a) {
         }
       }
     }
-    if (!T.regular) __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
   }
   }
-  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);  // no DMA may land in LDS after the workgroup ends
 }
 
 int launch_qkv_stationary(const QkvArgs& a0, int D, hipStream_t s) {
