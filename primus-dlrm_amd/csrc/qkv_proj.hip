@@ -269,7 +269,7 @@ __global__ __launch_bounds__(256, 1) void qkv_stationary_kernel(QkvArgs a) {
     // output row r of the tile is Q/K row base + r * rstride (S: consecutive tokens; NS: one token per sample)
     const int64_t krow0 = (int64_t)T.b * a.kv + T.t0, qrow0 = (int64_t)T.b * a.q_len + (T.t0 - qlo);
     const int kstride = T.ns ? a.kv : 1, qstride = T.ns ? a.q_len : 1;
-    const int qfirst = T.ns ? 0 : qlo - T.t0;  // first tile row that is a kept query
+    const int qfirst = T.ns ? 0 : max(qlo - T.t0, 0);  // first tile row that is a kept query (if need_q)
 #pragma unroll
     for (int m = 0; m < 3; ++m) {
       if (m == 0 && !T.need_q) continue;
@@ -286,14 +286,16 @@ __global__ __launch_bounds__(256, 1) void qkv_stationary_kernel(QkvArgs a) {
             *reinterpret_cast<u32x2_t*>(stage + lfr * kQkStride + (bb * 32 + 8 * g + 4 * lhf) * 2) =
                 u32x2_t{pack_bf16x2(acc[bb][4 * g], acc[bb][4 * g + 1]),
                         pack_bf16x2(acc[bb][4 * g + 2], acc[bb][4 * g + 3])};
-        uint16_t* base = m == 0 ? a.q + qrow0 * kD : a.k + krow0 * kD;
+        // row r0 of the pointer: the first stored row (the first kept query for Q)
+        const int r0 = m == 0 ? qfirst : 0;
+        uint16_t* base = m == 0 ? a.q + (qrow0 + (int64_t)qfirst * qstride) * kD : a.k + krow0 * kD;
         base += wave * 64 + (ln & 7) * 8;
         const int rstride = (m == 0 ? qstride : kstride) * kD;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int r = (ln >> 3) + 8 * i;
           const u32x4_t v = *reinterpret_cast<const u32x4_t*>(stage + r * kQkStride + (ln & 7) * 16);
-          if (r < T.nrows && (m != 0 || r >= qfirst)) *reinterpret_cast<u32x4_t*>(base + r * rstride) = v;
+          if (r < T.nrows && r >= r0) *reinterpret_cast<u32x4_t*>(base + (r - r0) * rstride) = v;
         }
       } else {
         // feature bb*32 + lfr of head `wave`, tokens 8g + 4lhf .. +3: staged as 64 feature rows of the tile's
