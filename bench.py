@@ -990,10 +990,15 @@ def main() -> int:
             mats.append(m)
         feats = [torch.from_numpy(m).to(dev) for m in mats]
         kept = int(sum(int((m != 0).sum()) for m in mats))
-        keep = feats
+        # two batches of the same size (the second: the same matrices in a rolled feature order, in their own
+        # memory) alternate, so no build starts on ids the previous build left in the caches
+        batches = (feats, [t.clone() for t in feats[1:] + feats[:1]])
+        keep = batches
+        nstep = [0]
 
         def step():
-            pdm.ops.kjt_from_dense_raw(feats, 0)
+            pdm.ops.kjt_from_dense_raw(batches[nstep[0] & 1], 0)
+            nstep[0] += 1
 
         rows = F_ * B_
         alg = F_ * B_ * L_ * 8 + kept * 8 + rows * 4 + (rows + 1) * 8
