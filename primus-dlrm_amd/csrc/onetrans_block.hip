@@ -1208,7 +1208,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
 
 // ---------------------------------------------------------------------------
 // Persistent attention with the keys and values of a head resident in LDS.
-// Each workgroup of 8 waves walks the (sample, head) pairs blockIdx.x,
+// Each workgroup of NW waves walks the (sample, head) pairs blockIdx.x,
 // blockIdx.x + gridDim.x, ...  K rows and V^T rows of a head are read from
 // memory into registers while the previous head is computed, and written to
 // LDS between two barriers, so the copy hides behind the attention math.
@@ -1355,9 +1355,14 @@ __device__ __forceinline__ void attn_query_tile(const AttnTile& t, const int qt,
   }
 }
 
-// NP: 16-byte pieces per thread of K (and of V^T), kv_pad * 8 <= NP * 512.
-template <int NP>
-__global__ __launch_bounds__(512) void attn_lds_kernel(AttnArgs a) {
+// NP: 16-byte pieces per thread of K (and of V^T), kv_pad * 8 <= NP * 64 * NW.  NW = 8, one workgroup per
+// CU; NW = 4 (two workgroups per CU, each on its own head) for heads of at most 4 query tiles, which would
+// leave most of 8 waves idle.
+template <int NP, int NW>
+__global__ __launch_bounds__(NW * 64, 8 / NW) void attn_lds_kernel(AttnArgs a) {
+  constexpr int NT = NW * 64;                // threads
+  constexpr int RPR = NT / 8;                // K rows (and V^T rows) per copy round
+  constexpr int VRS = 64 / RPR;              // rounds per set of the 64 V^T rows
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const int kvp = a.kv_pad;                  // keys held (multiple of 32, <= kAttnLdsMaxKeys)
   char* sK = smem;                           // kvp rows x 128 bytes
@@ -1368,12 +1373,12 @@ __global__ __launch_bounds__(512) void attn_lds_kernel(AttnArgs a) {
   const int D = a.H * 64;
   const int BH = a.B * a.H;
 
-  // Copy of one head, NP rounds of 512 16-byte pieces for K and for V^T:
-  //  K: thread t holds LDS row m = 64 i + t / 8 (key (m & ~15) | swap23(m & 15)) and piece t % 8 of it,
+  // Copy of one head, NP rounds of NT 16-byte pieces for K and for V^T:
+  //  K: thread t holds LDS row m = RPR i + t / 8 (key (m & ~15) | swap23(m & 15)) and piece t % 8 of it,
   //     stored at piece position (t % 8) ^ ((m >> 1) & 7);
-  //  V^T: thread t holds row d = t / 8 and piece 8 i + t % 8 of it (keys 64 i + 8 (t % 8) ..), stored at
-  //     piece position (8 i + t % 8) ^ ((d >> 2) & 3).
-  // Every per-round address is a fixed stride from round 0's.
+  //  V^T: thread t holds row d = t / 8 + RPR (i % VRS) and piece 8 (i / VRS) + t % 8 of it (keys
+  //     64 (i / VRS) + 8 (t % 8) ..), stored at piece position (8 (i / VRS) + t % 8) ^ ((d >> 2) & 3).
+  // Every per-round address is a fixed stride from round 0's (RPR is a multiple of 16).
   const int m0 = tid >> 3, p0 = tid & 7;
   const int key0 = (m0 & ~15) | swap23(m0 & 15);
   const int ppr = kvp >> 3;                  // pieces per V^T row
@@ -1388,16 +1393,16 @@ __global__ __launch_bounds__(512) void attn_lds_kernel(AttnArgs a) {
     const uint16_t* vsrc = a.vt + ((int64_t)bh * 64 + m0) * kvp;
 #pragma unroll
     for (int i = 0; i < NP; ++i) {
-      kr[i] = *reinterpret_cast<const u32x4_t*>(ksrc + (int64_t)min(64 * i + key0, a.kv - 1) * D);
-      vr[i] = *reinterpret_cast<const u32x4_t*>(vsrc + min(8 * i + p0, ppr - 1) * 8);
+      kr[i] = *reinterpret_cast<const u32x4_t*>(ksrc + (int64_t)min(RPR * i + key0, a.kv - 1) * D);
+      vr[i] = *reinterpret_cast<const u32x4_t*>(vsrc + (int64_t)RPR * (i % VRS) * kvp + min(8 * (i / VRS) + p0, ppr - 1) * 8);
     }
   };
   auto sstore = [&]() {
 #pragma unroll
     for (int i = 0; i < NP; ++i) {
-      if (64 * i + m0 < kvp)
-        *reinterpret_cast<u32x4_t*>(sk0 + 64 * i * 128) = 64 * i + key0 < a.kv ? kr[i] : u32x4_t{0, 0, 0, 0};
-      const int pv = 8 * i + p0;
+      if (RPR * i + m0 < kvp)
+        *reinterpret_cast<u32x4_t*>(sk0 + RPR * i * 128) = RPR * i + key0 < a.kv ? kr[i] : u32x4_t{0, 0, 0, 0};
+      const int pv = 8 * (i / VRS) + p0;
       if (pv < ppr) {
         u32x4_t v = vr[i];
         if (pv * 8 + 8 > a.kv) {  // V^T beyond key kv - 1 is padding the QKV GEMM never wrote
@@ -1408,7 +1413,7 @@ __global__ __launch_bounds__(512) void attn_lds_kernel(AttnArgs a) {
             else if (k0 + 1 >= a.kv) v[w] &= 0xffffu;
           }
         }
-        *reinterpret_cast<u32x4_t*>(sv0 + 128 * i) = v;
+        *reinterpret_cast<u32x4_t*>(sv0 + (int64_t)RPR * (i % VRS) * (2 * kvp) + 128 * (i / VRS)) = v;
       }
     }
   };
@@ -1416,11 +1421,25 @@ __global__ __launch_bounds__(512) void attn_lds_kernel(AttnArgs a) {
   const int ntiles = (a.q_len + 31) >> 5;
   // k-th tile of this wave in snake order (index into tiles sorted by decreasing cost), or -1
   auto tile_of = [&](int k) {
-    const int idx = 8 * k + ((k & 1) ? 7 - wave : wave);
+    const int idx = NW * k + ((k & 1) ? NW - 1 - wave : wave);
     return idx < ntiles ? ntiles - 1 - idx : -1;
   };
 
+  // Q fragments of query tile qt of (sample, head) pair p; rows past q_len read row q_len - 1 (their outputs
+  // are never stored)
+  auto qload = [&](int p, int qt, u32x4_t (&f)[4]) {
+    const int b = p / a.H, h = p - (p / a.H) * a.H;
+    const uint16_t* qbase = a.q + (int64_t)b * a.q_len * D + h * 64 + hf * 8;
+    const int qi = min(qt * 32 + fr, a.q_len - 1);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) f[c] = *reinterpret_cast<const u32x4_t*>(qbase + (int64_t)qi * D + c * 16);
+  };
+  // With 4 waves (heads of at most 4 query tiles: one tile per wave) the wave's tile of the next head has its
+  // Q requested during this head, like the next head's K and V^T.
+  constexpr bool kQNext = NW == 4;
   int bh = blockIdx.x;
+  u32x4_t qf[4], qn[4];
+  if constexpr (kQNext) qload(bh, max(tile_of(0), 0), qf);
   gload(bh);
   for (;;) {
     __syncthreads();  // every wave is done with the previous head's LDS
@@ -1428,37 +1447,48 @@ __global__ __launch_bounds__(512) void attn_lds_kernel(AttnArgs a) {
     __syncthreads();
     const int b = bh / a.H, h = bh - (bh / a.H) * a.H;
     const int next = bh + (int)gridDim.x;
-    const uint16_t* qbase = a.q + (int64_t)b * a.q_len * D + h * 64 + hf * 8;
-    u32x4_t qf[4];
-    // rows past q_len read row q_len - 1 (their outputs are never stored)
-    auto qload = [&](int qt, u32x4_t (&f)[4]) {
-      const int qi = min(qt * 32 + fr, a.q_len - 1);
-#pragma unroll
-      for (int c = 0; c < 4; ++c) f[c] = *reinterpret_cast<const u32x4_t*>(qbase + (int64_t)qi * D + c * 16);
-    };
     const AttnTile at{sK, sV, a.o + (int64_t)b * a.q_len * D + h * 64, kvp, a.q_len, a.kv, D, a.scale_log2};
     auto process_tile = [&](const int qt, const u32x4_t (&qf)[4]) { attn_query_tile(at, qt, qf, fr, hf); };
-    // A wave's first two tiles (all of them while q_len <= 512) have their Q requested before the next
-    // head's copy, which then overlaps the whole head: memory reads complete in issue order for the
-    // wait counter, so waiting for Q does not wait for the copy.  The code is straight-line up to the
-    // second tile so that the compiler's waits count exactly; scheduling barriers keep the issue order.
     const int qt0 = tile_of(0), qt1 = tile_of(1);
-    u32x4_t qn[4];
-    qload(max(qt0, 0), qf);
-    qload(qt1 >= 0 ? qt1 : max(qt0, 0), qn);
-    __builtin_amdgcn_sched_barrier(0);
-    gload(next < BH ? next : bh);  // in flight while this head is computed (the last head re-reads itself)
-    __builtin_amdgcn_sched_barrier(0);
-    if (qt0 >= 0) process_tile(qt0, qf);
-    if (qt1 >= 0) process_tile(qt1, qn);
-    // tiles past the second (q_len > 512): Q read at the start of the tile
-    for (int kt = 2;; ++kt) {
-      const int qt = tile_of(kt);
-      if (qt < 0) break;
-      qload(qt, qf);
-      process_tile(qt, qf);
+    if constexpr (kQNext) {
+      // this head's first tile was requested during the previous head; then the next head's copy and its
+      // first tile's Q (O of a pair is written only by the workgroup that owns the pair, after its Q is read)
+      __builtin_amdgcn_sched_barrier(0);
+      gload(next < BH ? next : bh);
+      if (next < BH) qload(next, max(qt0, 0), qn);
+      __builtin_amdgcn_sched_barrier(0);
+      if (qt0 >= 0) process_tile(qt0, qf);
+      // further tiles (more than 4 per head): Q read at the start of the tile
+      for (int kt = 1;; ++kt) {
+        const int qt = tile_of(kt);
+        if (qt < 0) break;
+        qload(bh, qt, qf);
+        process_tile(qt, qf);
+      }
+      if (next >= BH) break;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) qf[c] = qn[c];
+    } else {
+      // A wave's first two tiles (all of them while q_len <= 512) have their Q requested before the next
+      // head's copy, which then overlaps the whole head: memory reads complete in issue order for the
+      // wait counter, so waiting for Q does not wait for the copy.  The code is straight-line up to the
+      // second tile so that the compiler's waits count exactly; scheduling barriers keep the issue order.
+      qload(bh, max(qt0, 0), qf);
+      qload(bh, qt1 >= 0 ? qt1 : max(qt0, 0), qn);
+      __builtin_amdgcn_sched_barrier(0);
+      gload(next < BH ? next : bh);  // in flight while this head is computed (the last head re-reads itself)
+      __builtin_amdgcn_sched_barrier(0);
+      if (qt0 >= 0) process_tile(qt0, qf);
+      if (qt1 >= 0) process_tile(qt1, qn);
+      // tiles past the second (q_len > 512): Q read at the start of the tile
+      for (int kt = 2;; ++kt) {
+        const int qt = tile_of(kt);
+        if (qt < 0) break;
+        qload(bh, qt, qf);
+        process_tile(qt, qf);
+      }
+      if (next >= BH) break;
     }
-    if (next >= BH) break;
     bh = next;
   }
 }
@@ -1604,10 +1634,10 @@ static bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 // which streams K and V^T from memory.
 constexpr int64_t kAttnLdsMax = (int64_t)kAttnLdsMaxKeys * 256;
 
-// Launches attn_lds_kernel<NP> on a persistent grid: as many workgroups as fit
-// on the device at once, each walking (sample, head) pairs.  The LDS limit is
-// raised above the default 64 KiB once per process, device and instance.
-template <int NP>
+// Launches attn_lds_kernel<NP, NW> on a persistent grid: as many workgroups as
+// fit on the device at once, each walking (sample, head) pairs.  The LDS limit
+// is raised above the default 64 KiB once per process, device and instance.
+template <int NP, int NW>
 static int launch_attn_lds(const AttnArgs& aa, int64_t lds, hipStream_t s) {
   static std::once_flag once[64];
   static hipError_t err[64];
@@ -1616,17 +1646,21 @@ static int launch_attn_lds(const AttnArgs& aa, int64_t lds, hipStream_t s) {
   PDM_CHECK_HIP(hipGetDevice(&dev));
   PDM_CHECK_ARG(dev >= 0 && dev < 64, "device index out of range");
   std::call_once(once[dev], [&] {
-    err[dev] = hipFuncSetAttribute(reinterpret_cast<const void*>(attn_lds_kernel<NP>),
+    err[dev] = hipFuncSetAttribute(reinterpret_cast<const void*>(attn_lds_kernel<NP, NW>),
                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)kAttnLdsMax);
     if (err[dev] == hipSuccess) err[dev] = hipDeviceGetAttribute(&ncu[dev], hipDeviceAttributeMultiprocessorCount, dev);
   });
   PDM_CHECK_HIP(err[dev]);
+  // the copy rounds must cover the kv_pad K rows (NW * 8 per round) and the kv_pad / 8 pieces of each of the
+  // 64 V^T rows (8 pieces of NW * 8 rows per round)
+  constexpr int RPR = NW * 8;
+  PDM_CHECK_ARG(aa.kv_pad <= RPR * NP && aa.kv_pad / 8 <= 8 * (NP / (64 / RPR)), "attention copy rounds too few");
   int per_cu = 0;
-  PDM_CHECK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, attn_lds_kernel<NP>, 512, (size_t)lds));
+  PDM_CHECK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, attn_lds_kernel<NP, NW>, NW * 64, (size_t)lds));
   const int64_t bh = (int64_t)aa.B * aa.H;
   PDM_CHECK_ARG(bh < (int64_t(1) << 31), "batch * heads too large");
   const int64_t grid = std::min<int64_t>(bh, (int64_t)std::max(ncu[dev], 1) * std::max(per_cu, 1));
-  hipLaunchKernelGGL(attn_lds_kernel<NP>, dim3((unsigned)grid), dim3(512), (unsigned)lds, s, aa);
+  hipLaunchKernelGGL((attn_lds_kernel<NP, NW>), dim3((unsigned)grid), dim3(NW * 64), (unsigned)lds, s, aa);
   PDM_CHECK_LAUNCH();
   return PDM_OK;
 }
@@ -1699,11 +1733,18 @@ static int block_fwd(const pdm_block_desc& d, const float* x, const pdm_block_we
     const int64_t gy = (int64_t)B * H;
     const int64_t lds = (int64_t)L.kv_pad * 256;  // K rows (128 B) + V^T rows (2 B per key) of one head
     if (lds <= kAttnLdsMax) {
-      const int np = (L.kv_pad * 8 + 511) / 512;
-      if (np <= 2) st = launch_attn_lds<2>(aa, lds, s);
-      else if (np <= 4) st = launch_attn_lds<4>(aa, lds, s);
-      else if (np <= 7) st = launch_attn_lds<7>(aa, lds, s);
-      else st = launch_attn_lds<(kAttnLdsMaxKeys * 8 + 511) / 512>(aa, lds, s);
+      const int np = (L.kv_pad * 8 + 511) / 512;      // copy rounds of 8 waves
+      const int np4 = 2 * ((L.kv_pad + 63) / 64);      // and of 4 (two rounds per 64 keys of V^T)
+      if ((ql + 31) / 32 <= 4 && np4 <= 8) {
+        // at most 4 query tiles per head: workgroups of 4 waves, two per CU on two heads
+        if (np4 <= 2) st = launch_attn_lds<2, 4>(aa, lds, s);
+        else if (np4 <= 4) st = launch_attn_lds<4, 4>(aa, lds, s);
+        else if (np4 <= 6) st = launch_attn_lds<6, 4>(aa, lds, s);
+        else st = launch_attn_lds<8, 4>(aa, lds, s);
+      } else if (np <= 2) st = launch_attn_lds<2, 8>(aa, lds, s);
+      else if (np <= 4) st = launch_attn_lds<4, 8>(aa, lds, s);
+      else if (np <= 7) st = launch_attn_lds<7, 8>(aa, lds, s);
+      else st = launch_attn_lds<(kAttnLdsMaxKeys * 8 + 511) / 512, 8>(aa, lds, s);
       if (st != PDM_OK) return st;
     } else {
       PDM_CHECK_ARG(gy < 65536, "batch * heads must be < 65536");
