@@ -1368,7 +1368,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_lds_kernel(AttnArgs a) {
   char* sK = smem;                           // kvp rows x 128 bytes
   char* sV = smem + (int64_t)kvp * 128;      // 64 rows x 2*kvp bytes
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
+  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int fr = lane & 31, hf = lane >> 5;
   const int D = a.H * 64;
   const int BH = a.B * a.H;
@@ -1466,8 +1466,10 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_lds_kernel(AttnArgs a) {
         process_tile(qt, qf);
       }
       if (next >= BH) break;
-#pragma unroll
-      for (int c = 0; c < 4; ++c) qf[c] = qn[c];
+      qf[0] = qn[0];
+      qf[1] = qn[1];
+      qf[2] = qn[2];
+      qf[3] = qn[3];
     } else {
       // A wave's first two tiles (all of them while q_len <= 512) have their Q requested before the next
       // head's copy, which then overlaps the whole head: memory reads complete in issue order for the
