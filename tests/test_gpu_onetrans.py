@@ -95,6 +95,7 @@ def _run_case(pdm, dev, B, kv, q_len, n_ns, D=256, F=1024, seed=0, x_std=1.0, w_
     (2, 33, 16, 16),     # q_len == n_ns: no S-token query
     (130, 48, 48, 2),    # B > one GEMM row tile of NS tokens
     (4, 64, 20, 0),      # no NS tokens
+    (6, 240, 100, 16),   # 4 query tiles over 240 keys: the 4-wave attention with 8 copy rounds
 ])
 def test_block_matches_oracle(pdm, dev, B, kv, q_len, n_ns):
     _run_case(pdm, dev, B, kv, q_len, n_ns, seed=B + kv)
