@@ -1092,6 +1092,7 @@ struct AttnArgs {
   uint16_t* o;
   int B, H, q_len, kv, kv_pad;
   float scale_log2;  // log2(e) / sqrt(64)
+  int q_lds;         // attn_lds_kernel with 8 waves: Q of a head staged in LDS after K and V^T
 };
 
 __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
@@ -1367,6 +1368,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_lds_kernel(AttnArgs a) {
   const int kvp = a.kv_pad;                  // keys held (multiple of 32, <= kAttnLdsMaxKeys)
   char* sK = smem;                           // kvp rows x 128 bytes
   char* sV = smem + (int64_t)kvp * 128;      // 64 rows x 2*kvp bytes
+  char* sQ = smem + (int64_t)kvp * 256;      // with q_lds: the head's Q rows, ntiles * 32 x 128 bytes
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int fr = lane & 31, hf = lane >> 5;
@@ -1434,16 +1436,40 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_lds_kernel(AttnArgs a) {
 #pragma unroll
     for (int c = 0; c < 4; ++c) f[c] = *reinterpret_cast<const u32x4_t*>(qbase + (int64_t)qi * D + c * 16);
   };
+  // With q_lds, Q of head p goes to sQ by LDS DMA in 1 KB chunks of 8 rows: lane l of a chunk fills slot l
+  // (row 8c + l / 8, position l % 8), which holds 16-byte piece (l % 8) ^ ((row >> 1) & 7) of the row, so
+  // that a tile's fragment reads (32 rows, one piece each) spread over the banks; rows past q_len hold row
+  // q_len - 1.  The wave's fragments of tile qt are then read from LDS.
+  auto qdma = [&](int p) {
+    const int b = p / a.H, h = p - (p / a.H) * a.H;
+    const uint64_t qb = (uint64_t)(uintptr_t)(a.q + (int64_t)b * a.q_len * D + h * 64);
+    const int r = lane >> 3, pos = lane & 7;
+    for (int c = wave; c < ntiles * 4; c += NW) {
+      const int row = 8 * c + r;
+      const uint32_t off = (uint32_t)((min(row, a.q_len - 1) * D + ((pos ^ ((row >> 1) & 7)) << 3)) * 2);
+      lds_dma16(qb, off, (uint32_t)(uintptr_t)(sQ + c * 1024));
+    }
+  };
+  auto qread = [&](int qt, u32x4_t (&f)[4]) {
+    const int row = qt * 32 + fr;
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      f[c] = *reinterpret_cast<const u32x4_t*>(sQ + row * 128 + (((2 * c + hf) ^ ((row >> 1) & 7)) << 4));
+  };
   // With 4 waves (heads of at most 4 query tiles: one tile per wave) the wave's tile of the next head has its
   // Q requested during this head, like the next head's K and V^T.
   constexpr bool kQNext = NW == 4;
   int bh = blockIdx.x;
   u32x4_t qf[4], qn[4];
+  const bool q_lds = !kQNext && a.q_lds;
   if constexpr (kQNext) qload(bh, max(tile_of(0), 0), qf);
+  if (q_lds) qdma(bh);
   gload(bh);
   for (;;) {
     __syncthreads();  // every wave is done with the previous head's LDS
     sstore();
+    // Q of this head, requested before this head's copy, has landed (the copy's registers are consumed)
+    if (q_lds) __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
     __syncthreads();
     const int b = bh / a.H, h = bh - (bh / a.H) * a.H;
     const int next = bh + (int)gridDim.x;
@@ -1475,11 +1501,20 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_lds_kernel(AttnArgs a) {
       // head's copy, which then overlaps the whole head: memory reads complete in issue order for the
       // wait counter, so waiting for Q does not wait for the copy.  The code is straight-line up to the
       // second tile so that the compiler's waits count exactly; scheduling barriers keep the issue order.
-      qload(bh, max(qt0, 0), qf);
-      qload(bh, qt1 >= 0 ? qt1 : max(qt0, 0), qn);
-      __builtin_amdgcn_sched_barrier(0);
-      gload(next < BH ? next : bh);  // in flight while this head is computed (the last head re-reads itself)
-      __builtin_amdgcn_sched_barrier(0);
+      if (q_lds) {
+        // every wave has at most two tiles: both read from LDS, then sQ is refilled with the next head's Q
+        qread(max(qt0, 0), qf);
+        qread(qt1 >= 0 ? qt1 : max(qt0, 0), qn);
+        __syncthreads();
+        if (next < BH) qdma(next);
+        gload(next < BH ? next : bh);
+      } else {
+        qload(bh, max(qt0, 0), qf);
+        qload(bh, qt1 >= 0 ? qt1 : max(qt0, 0), qn);
+        __builtin_amdgcn_sched_barrier(0);
+        gload(next < BH ? next : bh);  // in flight while this head is computed (the last head re-reads itself)
+        __builtin_amdgcn_sched_barrier(0);
+      }
       if (qt0 >= 0) process_tile(qt0, qf);
       if (qt1 >= 0) process_tile(qt1, qn);
       // tiles past the second (q_len > 512): Q read at the start of the tile
@@ -1635,6 +1670,8 @@ static bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 // Largest LDS footprint of attn_lds_kernel; longer sequences run attn_kernel,
 // which streams K and V^T from memory.
 constexpr int64_t kAttnLdsMax = (int64_t)kAttnLdsMaxKeys * 256;
+// LDS of one workgroup on gfx950: K, V^T and, when it fits, the head's Q
+constexpr int64_t kAttnLdsLimit = 160 * 1024;
 
 // Launches attn_lds_kernel<NP, NW> on a persistent grid: as many workgroups as
 // fit on the device at once, each walking (sample, head) pairs.  The LDS limit
@@ -1649,7 +1686,7 @@ static int launch_attn_lds(const AttnArgs& aa, int64_t lds, hipStream_t s) {
   PDM_CHECK_ARG(dev >= 0 && dev < 64, "device index out of range");
   std::call_once(once[dev], [&] {
     err[dev] = hipFuncSetAttribute(reinterpret_cast<const void*>(attn_lds_kernel<NP, NW>),
-                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)kAttnLdsMax);
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)kAttnLdsLimit);
     if (err[dev] == hipSuccess) err[dev] = hipDeviceGetAttribute(&ncu[dev], hipDeviceAttributeMultiprocessorCount, dev);
   });
   PDM_CHECK_HIP(err[dev]);
@@ -1743,10 +1780,16 @@ static int block_fwd(const pdm_block_desc& d, const float* x, const pdm_block_we
         else if (np4 <= 4) st = launch_attn_lds<4, 4>(aa, lds, s);
         else if (np4 <= 6) st = launch_attn_lds<6, 4>(aa, lds, s);
         else st = launch_attn_lds<8, 4>(aa, lds, s);
-      } else if (np <= 2) st = launch_attn_lds<2, 8>(aa, lds, s);
-      else if (np <= 4) st = launch_attn_lds<4, 8>(aa, lds, s);
-      else if (np <= 7) st = launch_attn_lds<7, 8>(aa, lds, s);
-      else st = launch_attn_lds<(kAttnLdsMaxKeys * 8 + 511) / 512, 8>(aa, lds, s);
+      } else {
+        // 8 waves: with at most 16 query tiles (two per wave) and room in LDS, Q is staged there too
+        const int64_t lds_q = lds + (int64_t)((ql + 31) / 32) * 32 * 128;
+        aa.q_lds = (ql + 31) / 32 <= 16 && lds_q <= kAttnLdsLimit;
+        const int64_t lds8 = aa.q_lds ? lds_q : lds;
+        if (np <= 2) st = launch_attn_lds<2, 8>(aa, lds8, s);
+        else if (np <= 4) st = launch_attn_lds<4, 8>(aa, lds8, s);
+        else if (np <= 7) st = launch_attn_lds<7, 8>(aa, lds8, s);
+        else st = launch_attn_lds<(kAttnLdsMaxKeys * 8 + 511) / 512, 8>(aa, lds8, s);
+      }
       if (st != PDM_OK) return st;
     } else {
       PDM_CHECK_ARG(gy < 65536, "batch * heads must be < 65536");
