@@ -21,8 +21,11 @@
 //    MFMAs whose weight operands are named registers (the compiler otherwise copies AGPR-held operands
 //    into VGPRs before every MFMA) and whose tile operands are read four k steps ahead.  Q and K come out
 //    token-per-lane (acc = W . h^T) and leave through a per-wave LDS staging tile as 128-byte row segments;
-//    V comes out column-per-lane (acc = h . W^T) and leaves as 64-byte V^T segments of 32 tokens.
-// Measured on one MI355X (B=1024, 400 tokens, d_model 256): 286 us against 315 us for the row GEMM
+//    V comes out column-per-lane (acc = h . W^T) and leaves as 64-byte V^T segments of 32 tokens.  The Q and K
+//    stores, whole 128-byte lines, are non-temporal (2.97 -> 2.91 ms per 4-layer step); the V^T segments are
+//    half lines that the L2 joins with the next tile's halves, and stay cached stores (non-temporal as well:
+//    2.94 ms).
+// Measured on one MI355X (B=1024, 400 tokens, d_model 256): 245 us against 315 us for the row GEMM
 // (A-stationary, weights streamed through LDS) it replaces.
 #include "block_kernels.h"
 #include "mfma_common.h"
@@ -295,7 +298,7 @@ __global__ __launch_bounds__(256, 1) void qkv_stationary_kernel(QkvArgs a) {
         for (int i = 0; i < 4; ++i) {
           const int r = (ln >> 3) + 8 * i;
           const u32x4_t v = *reinterpret_cast<const u32x4_t*>(stage + r * kQkStride + (ln & 7) * 16);
-          if (r < T.nrows && r >= r0) *reinterpret_cast<u32x4_t*>(base + (r - r0) * rstride) = v;
+          if (r < T.nrows && r >= r0) __builtin_nontemporal_store(v, reinterpret_cast<u32x4_t*>(base + (r - r0) * rstride));
         }
       } else {
         // feature bb*32 + lfr of head `wave`, tokens 8g + 4lhf .. +3: staged as 64 feature rows of the tile's
