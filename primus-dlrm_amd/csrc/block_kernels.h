@@ -18,7 +18,7 @@ struct QkvArgs {
   uint16_t* q;            // [B, q_len, D]
   uint16_t* k;            // [B, kv, D]
   uint16_t* vt;           // [B, D / 64, 64, kv_pad]
-  int B, kv, q_len, n_ns, kv_pad;
+  int B, kv, q_len, n_ns, kv_pad;  // kv_pad: V^T row stride, a multiple of 64
   // filled by the launcher: S tokens per sample, row tiles per sample / per NS token, all tiles
   int n_s, tps, tpg;
   int64_t n_tiles;

@@ -122,7 +122,7 @@ struct GemmArgs {
   uint16_t* q;
   uint16_t* k;
   uint16_t* vt;
-  int kv, q_len, kv_pad, D;
+  int kv, q_len, kv_pad, D;  // kv_pad: V^T row stride
   // row-stationary kernels: fp32 A rows normalised on load (RMSNorm weight norm_w), FFN weights
   const float* A32;
   const float* norm_w;
@@ -1090,7 +1090,8 @@ struct AttnArgs {
   const uint16_t* k;
   const uint16_t* vt;
   uint16_t* o;
-  int B, H, q_len, kv, kv_pad;
+  int B, H, q_len, kv, kv_pad;  // kv_pad: keys held in LDS (kv rounded up to 32)
+  int vt_ld;                     // V^T row stride in memory (kv rounded up to 64)
   float scale_log2;  // log2(e) / sqrt(64)
   int q_lds;         // attn_lds_kernel with 8 waves: Q of a head staged in LDS after K and V^T
 };
@@ -1123,7 +1124,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
   float m = -INFINITY, l = 0.0f;
 
   const uint16_t* kbase = a.k + (int64_t)b * a.kv * D + h * 64 + hf * 8;
-  const uint16_t* vbase = a.vt + ((int64_t)b * a.H + h) * 64 * a.kv_pad;
+  const uint16_t* vbase = a.vt + ((int64_t)b * a.H + h) * 64 * a.vt_ld;
 
   for (int j0 = 0; j0 < kv_end; j0 += 32) {
     // S^T[kv][q] = K . Q^T
@@ -1170,7 +1171,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
       const int jb = j0 + 16 * c2 + hf * 4;
 #pragma unroll
       for (int db = 0; db < 2; ++db) {
-        const uint16_t* vrow = vbase + (int64_t)(db * 32 + fr) * a.kv_pad + jb;
+        const uint16_t* vrow = vbase + (int64_t)(db * 32 + fr) * a.vt_ld + jb;
         u32x2_t lo = *reinterpret_cast<const u32x2_t*>(vrow);
         u32x2_t hi = *reinterpret_cast<const u32x2_t*>(vrow + 8);
         if (tail) {
@@ -1392,11 +1393,11 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_lds_kernel(AttnArgs a) {
   auto gload = [&](int bh) {
     const int b = bh / a.H, h = bh - (bh / a.H) * a.H;
     const uint16_t* ksrc = a.k + (int64_t)b * a.kv * D + h * 64 + p0 * 8;
-    const uint16_t* vsrc = a.vt + ((int64_t)bh * 64 + m0) * kvp;
+    const uint16_t* vsrc = a.vt + ((int64_t)bh * 64 + m0) * a.vt_ld;
 #pragma unroll
     for (int i = 0; i < NP; ++i) {
       kr[i] = *reinterpret_cast<const u32x4_t*>(ksrc + (int64_t)min(RPR * i + key0, a.kv - 1) * D);
-      vr[i] = *reinterpret_cast<const u32x4_t*>(vsrc + (int64_t)RPR * (i % VRS) * kvp + min(8 * (i / VRS) + p0, ppr - 1) * 8);
+      vr[i] = *reinterpret_cast<const u32x4_t*>(vsrc + (int64_t)RPR * (i % VRS) * a.vt_ld + min(8 * (i / VRS) + p0, ppr - 1) * 8);
     }
   };
   auto sstore = [&]() {
@@ -1536,7 +1537,8 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_lds_kernel(AttnArgs a) {
 
 struct BlockLayout {
   int64_t h = 0, q = 0, k = 0, vt = 0, g = 0, total = 0;
-  int kv_pad = 0;
+  int kv_pad = 0;  // keys of a head held by the attention (kv rounded up to 32)
+  int vt_ld = 0;   // V^T row stride (kv rounded up to 64: rows start on 128-byte lines)
 };
 
 static int64_t align256(int64_t v) { return (v + 255) & ~int64_t(255); }
@@ -1551,10 +1553,11 @@ static BlockLayout block_layout(const pdm_block_desc& d) {
   const int64_t B = d.batch, D = d.d_model;
   const bool fused = fused_path(d);
   L.kv_pad = (d.kv_len + 31) & ~31;
+  L.vt_ld = (d.kv_len + 63) & ~63;
   int64_t off = 0;
   L.q = off; off = align256(off + B * d.q_len * D * 2);                 // Q, later attention output
   L.k = off; off = align256(off + B * d.kv_len * D * 2);                // K
-  L.vt = off; off = align256(off + B * (D / 64) * 64 * (int64_t)L.kv_pad * 2);  // V^T per head
+  L.vt = off; off = align256(off + B * (D / 64) * 64 * (int64_t)L.vt_ld * 2);  // V^T per head
   if (!fused) {
     L.h = off; off = align256(off + B * d.kv_len * D * 2);                // h1, later h2
     L.g = off; off = align256(off + B * d.q_len * (int64_t)d.ffn_dim * 2);  // GELU(FFN-up)
@@ -1740,7 +1743,7 @@ static int block_fwd(const pdm_block_desc& d, const float* x, const pdm_block_we
     qa.W = reinterpret_cast<const uint16_t*>(w->s_qkv_w);
     qa.W_ns = reinterpret_cast<const uint16_t*>(w->ns_qkv_w);
     qa.q = q; qa.k = k; qa.vt = vt;
-    qa.B = B; qa.kv = kv; qa.q_len = ql; qa.n_ns = nns; qa.kv_pad = L.kv_pad;
+    qa.B = B; qa.kv = kv; qa.q_len = ql; qa.n_ns = nns; qa.kv_pad = L.vt_ld;
     if ((st = launch_qkv_stationary(qa, D, s)) != PDM_OK) return st;
   } else if (fused_path(d)) {
     // 1. Q (tail rows), K, V^T = RMSNorm1(x) . Wqkv^T  (norm fused into the GEMM)
@@ -1749,7 +1752,7 @@ static int block_fwd(const pdm_block_desc& d, const float* x, const pdm_block_we
     g0.W = reinterpret_cast<const uint16_t*>(w->s_qkv_w);
     g0.W_ns = reinterpret_cast<const uint16_t*>(w->ns_qkv_w);
     g0.B = B; g0.n_s = kv - nns; g0.n_ns = nns; g0.N = 3 * D; g0.K = D;
-    g0.q = q; g0.k = k; g0.vt = vt; g0.kv = kv; g0.q_len = ql; g0.kv_pad = L.kv_pad; g0.D = D;
+    g0.q = q; g0.k = k; g0.vt = vt; g0.kv = kv; g0.q_len = ql; g0.kv_pad = L.vt_ld; g0.D = D;
     if ((st = launch_rowgemm<EPI_QKV, true>(g0, D, s)) != PDM_OK) return st;
   } else {
     // 1. h1 = RMSNorm1(x)  [B, kv, D]
@@ -1760,14 +1763,14 @@ static int block_fwd(const pdm_block_desc& d, const float* x, const pdm_block_we
     g0.W = reinterpret_cast<const uint16_t*>(w->s_qkv_w);
     g0.W_ns = reinterpret_cast<const uint16_t*>(w->ns_qkv_w);
     g0.B = B; g0.n_s = kv - nns; g0.n_ns = nns; g0.N = 3 * D; g0.K = D;
-    g0.q = q; g0.k = k; g0.vt = vt; g0.kv = kv; g0.q_len = ql; g0.kv_pad = L.kv_pad; g0.D = D;
+    g0.q = q; g0.k = k; g0.vt = vt; g0.kv = kv; g0.q_len = ql; g0.kv_pad = L.vt_ld; g0.D = D;
     if ((st = launch_gemm<EPI_QKV>(g0, s)) != PDM_OK) return st;
   }
   // 3. attention -> O (written over Q: each wave reads its Q rows before writing them)
   {
     AttnArgs aa{};
     aa.q = q; aa.k = k; aa.vt = vt; aa.o = q;
-    aa.B = B; aa.H = H; aa.q_len = ql; aa.kv = kv; aa.kv_pad = L.kv_pad;
+    aa.B = B; aa.H = H; aa.q_len = ql; aa.kv = kv; aa.kv_pad = L.kv_pad; aa.vt_ld = L.vt_ld;
     aa.scale_log2 = 1.4426950408889634f / 8.0f;
     const int64_t gy = (int64_t)B * H;
     const int64_t lds = (int64_t)L.kv_pad * 256;  // K rows (128 B) + V^T rows (2 B per key) of one head

@@ -50,7 +50,6 @@ struct QkvTile {
   int wset;      // 0: shared weight, 1 + g: NS token g
   bool ns;
   bool need_q;   // some row is a kept query token
-  bool regular;  // S tile of 32 tokens whose rows all or none need Q
 };
 
 
@@ -120,6 +119,7 @@ __global__ __launch_bounds__(256, 1) void qkv_stationary_kernel(QkvArgs a) {
   __shared__ __attribute__((aligned(16))) float sNw[kD];
   __shared__ __attribute__((aligned(16))) char sNorm[2][32 * kNormStride];
   __shared__ __attribute__((aligned(16))) char sStage[4][kStageBytes];
+  __shared__ __attribute__((aligned(16))) char sVFirst[4][kStageBytes];  // V^T of the first tile of a pair
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -169,13 +169,11 @@ __global__ __launch_bounds__(256, 1) void qkv_stationary_kernel(QkvArgs a) {
       T.wset = 0;
       T.ns = false;
       T.need_q = t + T.nrows > qlo;
-      T.regular = T.nrows == 32 && (t >= qlo || !T.need_q);
     } else {
       T.nrows = min(32, a.B - b);
       T.wset = 1 + (t - a.n_s);
       T.ns = true;
       T.need_q = true;
-      T.regular = false;
     }
     return T;
   };
@@ -301,17 +299,38 @@ __global__ __launch_bounds__(256, 1) void qkv_stationary_kernel(QkvArgs a) {
           if (r < T.nrows && r >= r0) __builtin_nontemporal_store(v, reinterpret_cast<u32x4_t*>(base + (r - r0) * rstride));
         }
       } else {
+        // Two consecutive full S tiles of 64-aligned tokens t0 (first) and t0 + 32 (second) that this workgroup
+        // takes one after the other make a pair: the first keeps its V^T staged, the second writes both as whole
+        // 128-byte V^T lines (rows start on lines: the row stride is a multiple of 64 keys) with non-temporal
+        // stores.  Other tiles write their own 64-byte segments.
+        const bool full = !T.ns && T.nrows == 32;
+        const bool first = full && (T.t0 & 63) == 0 && T.t0 + 64 <= a.n_s && it + 1 < n_s_own;
+        const bool second = full && (T.t0 & 63) == 32 && it >= 1;  // its predecessor was a first
+        char* vst = first ? sVFirst[wave] : stage;
         // feature bb*32 + lfr of head `wave`, tokens 8g + 4lhf .. +3: staged as 64 feature rows of the tile's
         // 32 rows
 #pragma unroll
         for (int bb = 0; bb < 2; ++bb)
 #pragma unroll
           for (int g = 0; g < 4; ++g)
-            *reinterpret_cast<u32x2_t*>(stage + (bb * 32 + lfr) * kVStride + (8 * g + 4 * lhf) * 2) =
+            *reinterpret_cast<u32x2_t*>(vst + (bb * 32 + lfr) * kVStride + (8 * g + 4 * lhf) * 2) =
                 u32x2_t{pack_bf16x2(acc[bb][4 * g], acc[bb][4 * g + 1]),
                         pack_bf16x2(acc[bb][4 * g + 2], acc[bb][4 * g + 3])};
         uint16_t* vrow0 = a.vt + ((int64_t)T.b * (kD / 64) + wave) * 64 * a.kv_pad;
-        if (T.regular) {
+        if (first) {
+          // written with the second tile of the pair
+        } else if (second) {
+          // lane l stores 16-byte piece l % 8 (8 tokens) of feature rows l / 8 + 8 i, tokens t0 - 32 .. t0 + 31:
+          // pieces 0-3 from the first tile's staging, 4-7 from this tile's
+          const char* vfirst = sVFirst[wave];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const int d = (ln >> 3) + 8 * i, pc = ln & 7;
+            const char* src = (pc < 4 ? vfirst + pc * 16 : stage + (pc - 4) * 16) + d * kVStride;
+            __builtin_nontemporal_store(*reinterpret_cast<const u32x4_t*>(src),
+                                        reinterpret_cast<u32x4_t*>(vrow0 + d * a.kv_pad + (T.t0 - 32) + pc * 8));
+          }
+        } else if (full) {
           // lane l stores 16-byte piece l % 4 (8 tokens) of feature rows l / 4 + 16 i: 64-byte V^T segments
 #pragma unroll
           for (int i = 0; i < 4; ++i) {

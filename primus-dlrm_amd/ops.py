@@ -648,12 +648,12 @@ def onetrans_workspace_layout(B: int, kv: int, q_len: int, D: int, F: int) -> Di
     """Byte (offset, size) of each region of the block workspace, as laid out by
     pdm_onetrans_block_fwd: q (Q tail rows [B, q_len, D] bf16, later the
     attention output), k ([B, kv, D] bf16), vt (V transposed per head [B, D/64,
-    64, kv_pad] bf16, kv_pad = kv rounded up to 32).  d_model 128 and 256 run
+    64, kv_ld] bf16, kv_ld = kv rounded up to 64).  d_model 128 and 256 run
     fused kernels; other widths also hold h (normalised rows [B, kv, D] bf16)
     and g (GELU of the FFN-up GEMM [B, q_len, F] bf16)."""
     a = lambda v: (v + 255) // 256 * 256  # noqa: E731
-    kv_pad = (kv + 31) // 32 * 32
-    sizes = [("q", B * q_len * D * 2), ("k", B * kv * D * 2), ("vt", B * D * kv_pad * 2)]
+    kv_ld = (kv + 63) // 64 * 64
+    sizes = [("q", B * q_len * D * 2), ("k", B * kv * D * 2), ("vt", B * D * kv_ld * 2)]
     if D not in (128, 256):
         sizes += [("h", B * kv * D * 2), ("g", B * q_len * F * 2)]
     out, off = {}, 0

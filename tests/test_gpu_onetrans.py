@@ -65,8 +65,8 @@ def _check_layer(pdm, dev, x, w, q_len, label=""):
     torch.cuda.synchronize()
     # intermediates still held by the workspace: K, V^T, the attention output, GELU activations
     k = _ws_view(ws, layout, "k", (B, kv, D))
-    kv_pad = (kv + 31) // 32 * 32
-    vt = _ws_view(ws, layout, "vt", (B, H, 64, kv_pad))[..., :kv]
+    kv_ld = (kv + 63) // 64 * 64  # V^T row stride: rows start on 128-byte lines
+    vt = _ws_view(ws, layout, "vt", (B, H, 64, kv_ld))[..., :kv]
     v = vt.permute(0, 3, 1, 2).reshape(B, kv, D)
     o = _ws_view(ws, layout, "q", (B, q_len, D))
     _close("k", k, parts["k"], terms["k"])
