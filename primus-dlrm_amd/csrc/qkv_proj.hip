@@ -21,10 +21,10 @@
 //    MFMAs whose weight operands are named registers (the compiler otherwise copies AGPR-held operands
 //    into VGPRs before every MFMA) and whose tile operands are read four k steps ahead.  Q and K come out
 //    token-per-lane (acc = W . h^T) and leave through a per-wave LDS staging tile as 128-byte row segments;
-//    V comes out column-per-lane (acc = h . W^T) and leaves as 64-byte V^T segments of 32 tokens.  The Q and K
-//    stores, whole 128-byte lines, are non-temporal (2.97 -> 2.91 ms per 4-layer step); the V^T segments are
-//    half lines that the L2 joins with the next tile's halves, and stay cached stores (non-temporal as well:
-//    2.94 ms).
+//    V comes out column-per-lane (acc = h . W^T) and leaves as V^T rows of 32 tokens.  The Q and K stores,
+//    whole 128-byte lines, are non-temporal (2.97 -> 2.91 ms per 4-layer step).  Two consecutive tiles of a
+//    sample write their V^T together as whole 128-byte lines, non-temporal too; a tile without its partner
+//    writes 64-byte half lines with cached stores, which the L2 joins (non-temporal half lines: 2.94 ms).
 // Measured on one MI355X (B=1024, 400 tokens, d_model 256): 245 us against 315 us for the row GEMM
 // (A-stationary, weights streamed through LDS) it replaces.
 #include "block_kernels.h"
