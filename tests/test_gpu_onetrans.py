@@ -126,6 +126,14 @@ def test_block_batch1024_short_sequence(pdm, dev):
     _run_case(pdm, dev, 1024, 48, 32, 16, seed=12, norm_std=0.1)
 
 
+def test_block_vt_paired_tiles(pdm, dev):
+    """Batch 160 with 128 S tokens: 640 S tiles over the Q/K/V projection's 256 workgroups, shares of 2 or 3
+    consecutive tiles, so some workgroups write two tiles' V^T as whole lines together and others write a
+    tile alone (a share starting at token 64 pairs it with token 96; a share's last tile at token 0 goes
+    alone)."""
+    _run_case(pdm, dev, 160, 144, 32, 16, seed=14, norm_std=0.1)
+
+
 def test_block_ns_tiles_cross_tokens(pdm, dev):
     """Batch 1100 with 16 NS tokens: 35 row tiles of 32 samples per NS token (the last partial), 560 NS
     tiles over the Q/K/V projection's persistent grid, so workgroups' shares start and end inside a token's
