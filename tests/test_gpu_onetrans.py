@@ -134,6 +134,12 @@ def test_block_vt_paired_tiles(pdm, dev):
     _run_case(pdm, dev, 160, 144, 32, 16, seed=14, norm_std=0.1)
 
 
+def test_block_ffn_ns_last_round(pdm, dev):
+    """Batch 1024 keeping 80 of 96 tokens: 640 FFN row tiles of 128 rows, one whole round of 512 resident
+    workgroups (256 CUs x 2) on the S tiles and a last round holding the 128 NS tiles (per-token weights)."""
+    _run_case(pdm, dev, 1024, 96, 80, 16, seed=15, norm_std=0.1)
+
+
 def test_block_ns_tiles_cross_tokens(pdm, dev):
     """Batch 1100 with 16 NS tokens: 35 row tiles of 32 samples per NS token (the last partial), 560 NS
     tiles over the Q/K/V projection's persistent grid, so workgroups' shares start and end inside a token's
