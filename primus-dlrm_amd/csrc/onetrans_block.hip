@@ -980,7 +980,7 @@ __global__ __launch_bounds__(NW * 64, WPS) void ffn_kernel(GemmArgs a) {
         for (int s = 0; s < KS; ++s)
 #pragma unroll
           for (int rb = 0; rb < RB; ++rb) u[rb] = mfma32x32x16(wf[s], hfr[rb][s], u[rb]);
-        if constexpr (RB == 1) sched_mfma_ds_pipeline<KS, 4>();
+        if constexpr (RB == 1) sched_mfma_ds_pipeline<KS, 3>();
       }
       // G = bf16(gelu(bf16(U))): u[rb][e] is hidden unit (e/4)*8 + hf*4 + e%4 (LDS row order) of token fr;
       // two halves of 8 values bound the registers the table reads hold in flight
@@ -1015,7 +1015,7 @@ __global__ __launch_bounds__(NW * 64, WPS) void ffn_kernel(GemmArgs a) {
               const u32x4_t gb = {gp[rb][4 * c2], gp[rb][4 * c2 + 1], gp[rb][4 * c2 + 2], gp[rb][4 * c2 + 3]};
               y[rb][db] = mfma32x32x16(wf[c2 * DB + db], gb, y[rb][db]);
             }
-        if constexpr (RB == 1) sched_mfma_ds_pipeline<DB * 2, 4>();
+        if constexpr (RB == 1) sched_mfma_ds_pipeline<DB * 2, 3>();
       }
     }
   }
