@@ -11,7 +11,10 @@
 //   y  = z + FFN(RMSNorm2(z)), FFN = W2 gelu_erf(W1 .), S shared / NS per token (:172-204)
 // Every GEMM takes bf16 operands, accumulates in fp32 and rounds its output
 // to bf16 (autocast), GELU runs in fp32 on the bf16 GEMM output and rounds
-// to bf16, the residual additions run in fp32.
+// to bf16, the residual additions run in fp32.  Exception (d_model 128/256,
+// the fused FFN): the FFN-down accumulates on top of z in fp32, so its output
+// is not rounded to bf16 before the residual addition (at most half a bf16
+// ulp of the FFN output away from the autocast result).
 //
 // Launches per block: rmsnorm, QKV GEMM (writes Q tail rows, K, and V
 // transposed per head), attention, out-proj GEMM (+x tail -> z in y),
@@ -130,6 +133,7 @@ struct GemmArgs {
   const uint16_t* W2_ns;  // [n_ns, D, F]
   const uint16_t* bias;   // EPI_BIAS_*: bf16 [N]
   const uint16_t* Wo;     // FFN with the out-projection in front: Wout [D, D], shared by every token
+  int stagger;            // persistent FFN: start delay of the second half of the grid, in units of 8192 cycles
 };
 
 // Stores one GEMM output element (b, t, n) with the epilogue EPI.
@@ -725,20 +729,26 @@ __global__ __launch_bounds__(256, EPI == EPI_QKV ? PDM_QKV_WPS : 2) void rowgemm
 // accumulator row e/4*8 + (l/32)*4 + e%4 of a 16-unit half must meet hidden
 // unit (l/32)*8 + e%8 for the W2 operand to be one contiguous 16-byte read,
 // so LDS row r of the W1 chunk holds hidden unit r with bits 2 and 3 swapped.
-// W1 and W2 chunks stream through an NST-stage LDS ring: chunk c + NST - 1 is
-// read into registers in two halves (W1 during the FFN-up MFMAs, W2 during
-// GELU and FFN-down) and written to the stage chunk c - 1 used.  The
-// epilogue adds z (fp32) to the bf16-rounded FFN output.
+// W1 and W2 chunks go global -> LDS by LDS DMA into an NST-stage ring, chunk
+// c + NST - 1 issued right after the barrier that publishes chunk c.  Without
+// OPROJ the epilogue adds z (fp32, read from the residual rows) to the
+// bf16-rounded FFN output.
 //
 // OPROJ: the out-projection runs in front, z = bf16(O . Wout^T) + x, so z is
-// produced on chip instead of being read back from memory.  z^T = Wout . O^T
-// accumulates straight into the y registers (the same layout: lane l holds
-// row l%32), the O fragments stream from memory one 64-column chunk ahead and
-// the Wout chunks (D rows x 64 columns, exactly one ring stage) go through the
-// same ring in front of the FFN chunks.  z is added to the residual x, written
-// to the output rows (the epilogue reads it back there), and normalised in
-// registers; the RMSNorm2 values reach the B-operand layout of the FFN-up
-// with one exchange of two words per 16-column step between the half-waves.
+// produced on chip.  z^T = Wout . O^T accumulates straight into the y
+// registers (the same layout: lane l holds row l%32), every O fragment of the
+// lane's row is requested up front and the Wout chunks (D rows x 64 columns,
+// exactly one ring stage) go through the same ring in front of the FFN chunks.
+// z is added to the residual x and normalised in registers; the RMSNorm2
+// values reach the B-operand layout of the FFN-up with one exchange of two
+// words per 16-column step between the half-waves.  The FFN-down then
+// accumulates on top of z, so y = z + FFN leaves the registers once and z never
+// goes to memory.  The one difference from the reference's autocast rounding
+// points: the FFN-down output is added to z in fp32 instead of being rounded
+// to bf16 first, a difference of at most half a bf16 ulp of the FFN output.
+//
+// The grid is persistent: WPS workgroups per CU walk the row tiles
+// blockIdx.x, blockIdx.x + gridDim.x, ...
 // ---------------------------------------------------------------------------
 template <int D, int RB, int NW, int NST, int WPS, bool OPROJ>
 __global__ __launch_bounds__(NW * 64, WPS) void ffn_kernel(GemmArgs a) {
@@ -757,17 +767,30 @@ __global__ __launch_bounds__(NW * 64, WPS) void ffn_kernel(GemmArgs a) {
   __shared__ int s_rb[TROWS];
   __shared__ int s_rt[TROWS];
   __shared__ float sGelu[GELU_T_N];
+  __shared__ __attribute__((aligned(16))) float sNw[OPROJ ? D : 4];  // RMSNorm2 weight
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int fr = lane & 31, hf = lane >> 5;
-  const int mt = blockIdx.x;
-  for (int i = tid; i < TROWS; i += NT) tile_row(a, mt, TROWS, i, s_rb[i], s_rt[i]);
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   gelu_table_fill(sGelu, tid, NT);
+  if constexpr (OPROJ)
+    for (int i = tid; i < D; i += NT) sNw[i] = a.norm_w[i];
   const int F = a.N;
-  const int64_t gsel = mt < a.tiles_s ? -1 : (mt - a.tiles_s) / a.tiles_b;
-  const uint16_t* W1 = gsel < 0 ? a.W : a.W_ns + gsel * (int64_t)F * D;
-  const uint16_t* W2 = gsel < 0 ? a.W2 : a.W2_ns + gsel * (int64_t)D * F;
+  const uint16_t* W1 = a.W;
+  const uint16_t* W2 = a.W2;
+  // OPROJ: the O fragments of a tile's rows, the out-projection's B operand: lane (fr, hf) holds row
+  // wave * 32 + fr, columns 16 s + hf * 8 .. + 8 of 64-column chunk kc
+  constexpr int DWO = D / 64;
+  u32x4_t ofr[OPROJ ? DWO : 1][4];
+  auto load_o = [&](int mt_, int fr_, int hf_) {
+    int b, t;
+    tile_row(a, mt_, TROWS, wave * 32 + fr_, b, t);
+    // rows past the end read row 0, unused
+    const uint16_t* orow = a.A + (b >= 0 ? (int64_t)b * a.a_bstride + (int64_t)t * D : 0) + hf_ * 8;
+#pragma unroll
+    for (int kc = 0; kc < DWO; ++kc)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) ofr[kc][s] = *reinterpret_cast<const u32x4_t*>(orow + kc * 64 + s * 16);
+  };
 
   // Weight chunk c goes from global memory straight into LDS (global_load_lds_dwordx4: lane l of a wave
   // writes the 16 bytes at the wave's LDS base + 16 l), so LDS piece o of a stage is loaded by thread
@@ -778,20 +801,25 @@ __global__ __launch_bounds__(NW * 64, WPS) void ffn_kernel(GemmArgs a) {
   constexpr int L1 = W1_BYTES / 16 / NT;     // pieces per thread of a W1 chunk
   constexpr int L2 = W2_BYTES / 16 / NT;     // and of a W2 chunk
   static_assert(L1 * NT * 16 == W1_BYTES && L2 * NT * 16 == W2_BYTES, "chunk pieces must cover the threads");
-  // per-thread byte offsets of its pieces within chunk 0 (the chunk adds a uniform offset)
-  uint32_t off1[L1], off2[L2];
+  // Per-thread byte offsets of its pieces within chunk 0 (the chunk adds a uniform offset).  Piece p of a
+  // thread is row p * RP + r0 of the stage (RP = NT / (D / 8) rows per round of pieces, r0 = tid / (D / 8)):
+  // the multiple of 16 in that row index only moves the source by whole rows, so it goes into the scalar
+  // base and the thread keeps one offset per distinct (p * RP) mod 16.  W2 pieces differ by whole groups of
+  // NT / 4 rows (a scalar offset) and share one per-thread offset.
+  constexpr int RP = NT / (D / 8);
+  static_assert(RP * (D / 8) == NT && (RP >= 16 ? RP % 16 == 0 : 16 % RP == 0), "W1 piece rows");
+  constexpr int NLO = RP >= 16 ? 1 : 16 / RP;  // distinct (p * RP) mod 16
+  static_assert(NT % 64 == 0, "W2 pieces");
+  uint32_t off1[NLO];
+  {
+    const int r0 = tid / (D / 8), slot = tid % (D / 8);
 #pragma unroll
-  for (int p = 0; p < L1; ++p) {
-    const int o = p * NT + tid;              // piece index in the stage
-    const int r = o / (D / 8), slot = o % (D / 8);  // a row is D / 8 pieces
-    off1[p] = (uint32_t)((((r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1)) * D + ((slot ^ (r & 15)) << 3)) * 2);
+    for (int j = 0; j < NLO; ++j) {
+      const int r = j * RP + r0;  // < 16
+      off1[j] = (uint32_t)((((r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1)) * D + ((slot ^ (r & 15)) << 3)) * 2);
+    }
   }
-#pragma unroll
-  for (int p = 0; p < L2; ++p) {
-    const int q = p * NT + tid;
-    const int d = q >> 2, v = (q & 3) ^ ((d >> 2) & 3);
-    off2[p] = (uint32_t)((d * F + v * 8) * 2);
-  }
+  const uint32_t off2 = (uint32_t)(((tid >> 2) * F + (((tid & 3) ^ ((tid >> 4) & 3)) * 8)) * 2);
   // The DMA is issued from inline assembly: the compiler's own tracking of LDS DMA makes every later LDS
   // read wait for it.  Its completion is awaited explicitly (s_waitcnt vmcnt(0) before the barrier that
   // publishes a chunk and before the epilogue reuses the ring); the compiler's own vmcnt waits stay
@@ -801,14 +829,36 @@ __global__ __launch_bounds__(NW * 64, WPS) void ffn_kernel(GemmArgs a) {
     const uint64_t b2 = (uint64_t)(uintptr_t)W2 + (uint64_t)c * 32 * 2;
 #pragma unroll
     for (int p = 0; p < L1; ++p)
-      lds_dma16(b1, off1[p], (uint32_t)(uintptr_t)(sW1[stg] + (p * NT + wave * 64) * 16));
+      lds_dma16(b1 + (uint64_t)(((p * RP) & ~15) * D * 2), off1[((p * RP) & 15) / (RP >= 16 ? 16 : RP)],
+                (uint32_t)(uintptr_t)(sW1[stg] + (p * NT + wave * 64) * 16));
 #pragma unroll
     for (int p = 0; p < L2; ++p)
-      lds_dma16(b2, off2[p], (uint32_t)(uintptr_t)(sW2[stg] + (p * NT + wave * 64) * 16));
+      lds_dma16(b2 + (uint64_t)p * (NT / 4) * F * 2, off2, (uint32_t)(uintptr_t)(sW2[stg] + (p * NT + wave * 64) * 16));
   };
   const int nchunks = F / 32;
   constexpr unsigned kWaitDma = 0x0F70u | (unsigned)((PF - 1) * (L1 + L2));
   static_assert((PF - 1) * (L1 + L2) < 16, "vmcnt immediate");
+  // Persistent: the workgroup walks the row tiles blockIdx.x, blockIdx.x + gridDim.x, ...  With a.stagger, the
+  // second half of the grid (the second workgroup of each CU when the dispatcher fills the CUs in order) starts
+  // a.stagger * 8192 cycles later, so the two workgroups of a CU do not wait for their tiles' first rows and
+  // residuals at the same time: one's memory-bound prologue then runs beside the other's MFMAs.
+  if (a.stagger > 0 && (int)blockIdx.x >= (int)(gridDim.x / 2))
+    for (int i = 0; i < a.stagger; ++i) __builtin_amdgcn_s_sleep(127);
+  for (int mt = blockIdx.x; mt < a.total_blocks; mt += gridDim.x) {
+  // The lane's LDS and global offsets below derive from an opaque copy of the lane index taken per tile, so
+  // the compiler recomputes them in each tile instead of holding them in registers through the prologue and
+  // epilogue, where every register is taken.
+  int lane;
+  asm volatile("v_and_b32 %0, 63, %1" : "=v"(lane) : "v"(tid));
+  const int fr = lane & 31, hf = lane >> 5;
+  // every wave is done with the previous tile's staging tile (the ring) and row map
+  __syncthreads();
+  for (int i = tid; i < TROWS; i += NT) tile_row(a, mt, TROWS, i, s_rb[i], s_rt[i]);
+  {
+    const int64_t gsel = mt < a.tiles_s ? -1 : (mt - a.tiles_s) / a.tiles_b;
+    W1 = gsel < 0 ? a.W : a.W_ns + gsel * (int64_t)F * D;
+    W2 = gsel < 0 ? a.W2 : a.W2_ns + gsel * (int64_t)D * F;
+  }
   __syncthreads();
   u32x4_t hfr[RB][KS];
   f32x16_t y[RB][DB];
@@ -818,35 +868,29 @@ __global__ __launch_bounds__(NW * 64, WPS) void ffn_kernel(GemmArgs a) {
     static_assert(DW % NST == 0, "FFN chunk c must keep stage c % NST");
     // Wout chunk kc: LDS row r (output feature) = Wout[r, kc*64 .. +64), rows 0 .. D/2 - 1 in the W1 part of
     // the stage, the rest in its W2 part; 16-byte piece v of a row at slot v ^ (r & 7)
-    uint32_t offw[L1 + L2];
-#pragma unroll
-    for (int p = 0; p < L1 + L2; ++p) {
-      const int o = p * NT + tid, r = o >> 3;
-      offw[p] = (uint32_t)((r * D + (((o & 7) ^ (r & 7)) << 3)) * 2);
-    }
+    // piece p of a thread is row p * NT / 8 + tid / 8 (rows of 8 pieces, NT / 8 a multiple of 8): one
+    // per-thread offset, the row group in the scalar base
+    static_assert((NT / 8) % 8 == 0, "Wout pieces");
+    const uint32_t offw = (uint32_t)(((tid >> 3) * D + (((tid & 7) ^ ((tid >> 3) & 7)) << 3)) * 2);
     auto dma_wo = [&](int kc, int stg) {
       const uint64_t b = (uint64_t)(uintptr_t)a.Wo + (uint64_t)kc * 128;
 #pragma unroll
       for (int p = 0; p < L1; ++p)
-        lds_dma16(b, offw[p], (uint32_t)(uintptr_t)(sW1[stg] + (p * NT + wave * 64) * 16));
+        lds_dma16(b + (uint64_t)p * (NT / 8) * D * 2, offw, (uint32_t)(uintptr_t)(sW1[stg] + (p * NT + wave * 64) * 16));
 #pragma unroll
       for (int p = L1; p < L1 + L2; ++p)
-        lds_dma16(b, offw[p], (uint32_t)(uintptr_t)(sW2[stg] + ((p - L1) * NT + wave * 64) * 16));
+        lds_dma16(b + (uint64_t)p * (NT / 8) * D * 2, offw,
+                  (uint32_t)(uintptr_t)(sW2[stg] + ((p - L1) * NT + wave * 64) * 16));
     };
     const int row = wave * 32 + fr;
     const int b = s_rb[row], t = s_rt[row];
     const bool valid = b >= 0;
-    // O row of this lane (columns hf*8 .. of each 16-column step); rows past the end read row 0 unused
-    const uint16_t* orow = a.A + (valid ? (int64_t)b * a.a_bstride + (int64_t)t * D : 0) + hf * 8;
+    static_assert(DW == DWO, "Wout chunks");
     // every O fragment of the row (4 per Wout chunk) is requested up front, after the DMA of the first two
     // Wout chunks (both ring stages are free), so one memory latency covers the whole out-projection
-    u32x4_t ofr[DW][4];
     dma_wo(0, 0);
     dma_wo(1, 1);
-#pragma unroll
-    for (int kc = 0; kc < DW; ++kc)
-#pragma unroll
-      for (int s = 0; s < 4; ++s) ofr[kc][s] = *reinterpret_cast<const u32x4_t*>(orow + kc * 64 + s * 16);
+    load_o(mt, fr, hf);
     const float* xrow = a.res + (valid ? (int64_t)b * a.res_bstride + (int64_t)(t + a.res_toff) * D : 0) + hf * 4;
     f32x4_t xv[DB][4];
 #pragma unroll
@@ -888,9 +932,8 @@ __global__ __launch_bounds__(NW * 64, WPS) void ffn_kernel(GemmArgs a) {
         for (int db = 0; db < DB; ++db) y[0][db] = mfma32x32x16(wf[s * DB + db], ofr[kc][s], y[0][db]);
       sched_mfma_ds_pipeline<4 * DB, 4>();
     }
-    // z = bf16(O . Wout^T) + x[:, t + res_toff] in y (lane: row fr, outputs db*32 + g*8 + hf*4 + 0..3), written
-    // to the output rows, where the epilogue reads it back
-    float* zrow = reinterpret_cast<float*>(a.out) + (valid ? (int64_t)b * a.out_bstride + (int64_t)t * D : 0) + hf * 4;
+    // z = bf16(O . Wout^T) + x[:, t + res_toff] in y (lane: row fr, outputs db*32 + g*8 + hf*4 + 0..3): the FFN
+    // accumulates on top of it, so z never leaves the registers
     float ss = 0.0f;
 #pragma unroll
     for (int db = 0; db < DB; ++db) {
@@ -908,9 +951,6 @@ __global__ __launch_bounds__(NW * 64, WPS) void ffn_kernel(GemmArgs a) {
           y[0][db][4 * g + j] = z;
           ss += z * z;
         }
-        if (valid)
-          *reinterpret_cast<f32x4_t*>(zrow + db * 32 + g * 8) =
-              f32x4_t{y[0][db][4 * g], y[0][db][4 * g + 1], y[0][db][4 * g + 2], y[0][db][4 * g + 3]};
       }
     }
     ss += __shfl_xor(ss, 32, 64);
@@ -918,7 +958,7 @@ __global__ __launch_bounds__(NW * 64, WPS) void ffn_kernel(GemmArgs a) {
     // RMSNorm2 -> the FFN-up B operand: 16-column step s (block db = s / 2, groups g0 = 2 (s % 2) and g0 + 1)
     // needs columns 16s + hf*8 + 0..7 in lane (fr, hf); the lane holds g0*8 + hf*4 + 0..3 and (g0+1)*8 + hf*4
     // + 0..3, so the half-waves swap one 4-column group
-    const float* nw = a.norm_w + hf * 4;
+    const float* nw = sNw + hf * 4;
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
       const int db = s >> 1, g0 = 2 * (s & 1);
@@ -939,14 +979,13 @@ __global__ __launch_bounds__(NW * 64, WPS) void ffn_kernel(GemmArgs a) {
     for (int c = 0; c < PF; ++c)
       if (c < nchunks) dma(c, c);
     load_row_fragments<D, RB, true>(a, s_rb, s_rt, wave, fr, hf, hfr);
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) y[rb][db][e] = 0.0f;
   }
-
-#pragma unroll
-  for (int rb = 0; rb < RB; ++rb)
-#pragma unroll
-    for (int db = 0; db < DB; ++db)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) y[rb][db][e] = 0.0f;
 
   // The chunk loop is unrolled by the ring depth so that every stage index is a constant: the LDS reads of
   // stage k and the LDS DMA into stage (k + PF) % NST are then distinct objects to the compiler.
@@ -1020,18 +1059,19 @@ __global__ __launch_bounds__(NW * 64, WPS) void ffn_kernel(GemmArgs a) {
     }
   }
 
-  // Epilogue y = z + bf16(FFN).  y[rb][db][e] is output d = db*32 + (e/4)*8 + hf*4 + e%4 of row
-  // wave*RB*32 + rb*32 + fr.  The values go through LDS (the weight ring is free now) SEG outputs at a
-  // time, so that z is read and y written as whole row segments of SEG outputs, with
-  // non-temporal stores (y is streamed to memory; the next kernel reads it from there).  The z segments
-  // of the first two passes are requested before the last DMA is awaited, each later pass's when the
-  // pass two before it is done, so the passes do not wait for memory one after another.
+  // Epilogue.  y[rb][db][e] is output d = db*32 + (e/4)*8 + hf*4 + e%4 of row wave*RB*32 + rb*32 + fr.
+  // OPROJ: y already holds z + FFN (the FFN-down accumulated on top of z).  Otherwise y = z + bf16(FFN) with
+  // z the residual rows read here.  The values go through LDS (the weight ring is free now) SEG outputs at
+  // a time, so that y is written (and z read) as whole row segments of SEG outputs, with non-temporal stores
+  // (y is streamed to memory; the next kernel reads it from there).  The z segments of the first two
+  // passes are requested before the last DMA is awaited, each later pass's when the pass two before it is
+  // done, so the passes do not wait for memory one after another.
   constexpr int SEG = NW * RB * 32 * (64 * 4 + 16) <= RING_BYTES ? 64 : 32;  // outputs per pass
   constexpr int SROW = SEG * 4 + 16;       // LDS row stride (bytes), padded against bank conflicts
   constexpr int NQ = D / SEG;              // passes
   constexpr int EK = RB * 32 * (SEG / 4) / 64;  // 16-byte pieces per lane and pass
   static_assert(NW * RB * 32 * SROW <= RING_BYTES, "epilogue staging must fit the weight ring");
-  const float* zsrc = OPROJ ? reinterpret_cast<const float*>(a.out) : a.res;
+  const float* zsrc = a.res;
   int64_t eoff[EK];  // piece k of this lane: its row's output offset + its 4 columns (pass 0), or -1
 #pragma unroll
   for (int k = 0; k < EK; ++k) {
@@ -1041,11 +1081,13 @@ __global__ __launch_bounds__(NW * 64, WPS) void ffn_kernel(GemmArgs a) {
     const int b = s_rb[row];
     eoff[k] = b < 0 ? -1 : (int64_t)b * a.out_bstride + (int64_t)s_rt[row] * D + c4 * 4;
   }
-  f32x4_t zv[2][EK];
+  f32x4_t zv[OPROJ ? 1 : 2][EK];
   auto zload = [&](int q) {
+    if constexpr (!OPROJ) {
 #pragma unroll
-    for (int k = 0; k < EK; ++k)
-      zv[q & 1][k] = *reinterpret_cast<const f32x4_t*>(zsrc + (eoff[k] < 0 ? 0 : eoff[k] + q * SEG));
+      for (int k = 0; k < EK; ++k)
+        zv[q & 1][k] = *reinterpret_cast<const f32x4_t*>(zsrc + (eoff[k] < 0 ? 0 : eoff[k] + q * SEG));
+    }
   };
   zload(0);
   if (NQ > 1) zload(1);
@@ -1061,7 +1103,8 @@ __global__ __launch_bounds__(NW * 64, WPS) void ffn_kernel(GemmArgs a) {
         const int db = q * (SEG / 32) + db2;
 #pragma unroll
         for (int g = 0; g < 4; ++g)
-          *reinterpret_cast<f32x4_t*>(stage + (rb * 32 + fr) * SROW + (db2 * 32 + g * 8 + hf * 4) * 4) =
+          *reinterpret_cast<f32x4_t*>(stage + (rb * 32 + fr) * SROW + (db2 * 32 + g * 8 + hf * 4) * 4) = OPROJ ?
+              f32x4_t{y[rb][db][4 * g], y[rb][db][4 * g + 1], y[rb][db][4 * g + 2], y[rb][db][4 * g + 3]} :
               f32x4_t{bf16_round(y[rb][db][4 * g]), bf16_round(y[rb][db][4 * g + 1]),
                       bf16_round(y[rb][db][4 * g + 2]), bf16_round(y[rb][db][4 * g + 3])};
       }
@@ -1071,13 +1114,14 @@ __global__ __launch_bounds__(NW * 64, WPS) void ffn_kernel(GemmArgs a) {
       const int piece = k * 64 + lane;
       const int r = piece / (SEG / 4), c4 = piece - (piece / (SEG / 4)) * (SEG / 4);
       const f32x4_t v = *reinterpret_cast<const f32x4_t*>(stage + r * SROW + c4 * 16);
-      const f32x4_t z = zv[q & 1][k];
+      const f32x4_t z = OPROJ ? f32x4_t{0.0f, 0.0f, 0.0f, 0.0f} : zv[q & 1][k];
       if (eoff[k] >= 0)
-        __builtin_nontemporal_store(f32x4_t{z.x + v.x, z.y + v.y, z.z + v.z, z.w + v.w},
+        __builtin_nontemporal_store(OPROJ ? v : f32x4_t{z.x + v.x, z.y + v.y, z.z + v.z, z.w + v.w},
                                     reinterpret_cast<f32x4_t*>(reinterpret_cast<float*>(a.out) + eoff[k] + q * SEG));
     }
     if (q + 2 < NQ) zload(q + 2);
   }
+  }  // row tiles
 }
 
 // ---------------------------------------------------------------------------
@@ -1640,14 +1684,37 @@ static int launch_rowgemm(GemmArgs& g, int D, hipStream_t s) {
 #ifndef PDM_FFN_OPROJ
 #define PDM_FFN_OPROJ 1
 #endif
+// The FFN grid is persistent (WPS workgroups per CU walk the row tiles; 0: one workgroup per tile), and with
+// PDM_FFN_STAGGER > 0 the second half of the grid starts that many 8192-cycle units later.
+#ifndef PDM_FFN_PERSIST
+#define PDM_FFN_PERSIST 1
+#endif
+#ifndef PDM_FFN_STAGGER
+#define PDM_FFN_STAGGER 0
+#endif
 template <bool OPROJ>
 static int launch_ffn(GemmArgs& g, int D, hipStream_t s) {
   constexpr int RB = PDM_FFN_RB, NW = PDM_FFN_NW, NST = PDM_FFN_NST, WPS = PDM_FFN_WPS;
   const int64_t tiles = row_tiles(g, NW * RB * 32);
   if (tiles == 0) return PDM_OK;
   PDM_CHECK_ARG(tiles < (int64_t(1) << 31), "FFN grid too large");
-  if (D == 256) hipLaunchKernelGGL((ffn_kernel<256, RB, NW, NST, WPS, OPROJ>), dim3((unsigned)tiles), dim3(NW * 64), 0, s, g);
-  else hipLaunchKernelGGL((ffn_kernel<128, RB, NW, NST, WPS, OPROJ>), dim3((unsigned)tiles), dim3(NW * 64), 0, s, g);
+  g.total_blocks = tiles;
+  int64_t grid = tiles;
+  g.stagger = 0;
+  if (PDM_FFN_PERSIST) {
+    static std::once_flag once[64];
+    static hipError_t err[64];
+    static int ncu[64];
+    int dev = 0;
+    PDM_CHECK_HIP(hipGetDevice(&dev));
+    PDM_CHECK_ARG(dev >= 0 && dev < 64, "device index out of range");
+    std::call_once(once[dev], [&] { err[dev] = hipDeviceGetAttribute(&ncu[dev], hipDeviceAttributeMultiprocessorCount, dev); });
+    PDM_CHECK_HIP(err[dev]);
+    grid = std::min<int64_t>(tiles, (int64_t)std::max(ncu[dev], 1) * WPS);
+    g.stagger = grid == (int64_t)std::max(ncu[dev], 1) * WPS ? PDM_FFN_STAGGER : 0;
+  }
+  if (D == 256) hipLaunchKernelGGL((ffn_kernel<256, RB, NW, NST, WPS, OPROJ>), dim3((unsigned)grid), dim3(NW * 64), 0, s, g);
+  else hipLaunchKernelGGL((ffn_kernel<128, RB, NW, NST, WPS, OPROJ>), dim3((unsigned)grid), dim3(NW * 64), 0, s, g);
   PDM_CHECK_LAUNCH();
   return PDM_OK;
 }
