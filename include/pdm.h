@@ -476,7 +476,9 @@ int pdm_kjt_from_dense(const void* const* ids, const int32_t* row_len,
  * library-owned static device array (512 KiB per device, held until the
  * process ends), so F * B must not exceed PDM_KJT_NOALLOC_MAX_ROWS (larger
  * inputs return PDM_ERR_INVALID), and calls that overlap on one GPU (on
- * different streams) race on that array.  Arguments and results are those of
+ * different streams) race on that array.  The first call on a device looks
+ * up the array's address (hipGetSymbolAddress): under graph capture, make one
+ * call on the device before capturing.  Arguments and results are those of
  * pdm_kjt_from_dense. */
 #define PDM_KJT_NOALLOC_MAX_ROWS 67108864
 int pdm_kjt_from_dense_noalloc(const void* const* ids, const int32_t* row_len,

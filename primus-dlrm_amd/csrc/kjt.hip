@@ -326,6 +326,8 @@ int kjt_from_dense_impl(const void* const* ids, const int32_t* row_len, int32_t 
   PDM_CHECK_ARG(num_features >= 0 && num_features <= PDM_KJT_MAX_FEATURES, "num_features out of range");
   PDM_CHECK_ARG(index_bits == 32 || index_bits == 64, "index_bits must be 32 or 64");
   PDM_CHECK_ARG(batch_size >= 0, "batch_size < 0");
+  // the row count num_features * batch_size must be representable (checked before it is formed)
+  PDM_CHECK_ARG(num_features == 0 || batch_size <= INT64_MAX / num_features, "num_features * batch_size overflows");
   PDM_CHECK_ARG(offsets != nullptr, "null offsets");
   auto s = reinterpret_cast<hipStream_t>(stream);
   const int64_t rows = (int64_t)num_features * batch_size;
@@ -452,7 +454,16 @@ extern "C" int pdm_kjt_from_dense_noalloc(const void* const* ids, const int32_t*
                                           int64_t batch_size, int32_t index_bits, int64_t padding_idx,
                                           void* values, int32_t* lengths, int64_t* offsets, pdm_stream_t stream) {
   clear_error();
-  PDM_CHECK_ARG(num_features >= 0 && batch_size >= 0, "negative size");
+  PDM_CHECK_ARG(num_features >= 0 && num_features <= PDM_KJT_MAX_FEATURES, "num_features out of range");
+  PDM_CHECK_ARG(batch_size >= 0, "batch_size < 0");
+  // with at least one feature the row count is at least batch_size, so this bound keeps the product below
+  // 64 * PDM_KJT_NOALLOC_MAX_ROWS (no overflow) before it is formed
+  if (num_features > 0 && batch_size > PDM_KJT_NOALLOC_MAX_ROWS) {
+    set_error("pdm_kjt_from_dense_noalloc: batch_size " + std::to_string(batch_size) +
+              " exceeds the no-allocation limit of " + std::to_string((int64_t)PDM_KJT_NOALLOC_MAX_ROWS) +
+              " rows (use pdm_kjt_from_dense with a workspace)");
+    return PDM_ERR_INVALID;
+  }
   const int64_t rows = (int64_t)num_features * batch_size;
   if (rows > PDM_KJT_NOALLOC_MAX_ROWS) {
     set_error("pdm_kjt_from_dense_noalloc: " + std::to_string(rows) + " rows exceed the no-allocation limit of " +
@@ -474,6 +485,7 @@ extern "C" int pdm_kjt_permute(const void* values, int32_t index_bits, const int
   PDM_CHECK_ARG(index_bits == 32 || index_bits == 64, "index_bits must be 32 or 64");
   PDM_CHECK_ARG(num_keys >= 0 && num_out >= 0 && num_out <= PDM_KJT_MAX_FEATURES, "key counts out of range");
   PDM_CHECK_ARG(batch_size >= 0, "batch_size < 0");
+  PDM_CHECK_ARG(num_out == 0 || batch_size <= INT64_MAX / num_out, "num_out * batch_size overflows");
   PDM_CHECK_ARG(out_offsets != nullptr, "null out_offsets");
   auto s = reinterpret_cast<hipStream_t>(stream);
   const int64_t rows = (int64_t)num_out * batch_size;

@@ -89,30 +89,46 @@ def ebc_fp32(scale_rows: float = 1.0, batch: int = 2048) -> PooledWorkload:
                           np.concatenate(idx), offsets_from_lengths(np.concatenate(lens)), "uniform0.01")
 
 
-def single_hot_bf16(batch: int = 65_536, max_rows: Optional[int] = None) -> PooledWorkload:
-    """26 tables, rows log-uniform in [1e3, 4e7], dim 128 bf16, one id per bag, Zipf(1.05), sum, fp32 out."""
+def draw_rows(g: np.random.Generator, n: int, rows: int, alpha: float, ids: str) -> np.ndarray:
+    """``n`` row ids of a table of ``rows`` rows: Zipf(alpha) (``ids="zipf"``) or uniform (``ids="uniform"``,
+    the control distribution whose rows mostly miss every cache)."""
+    if ids == "zipf":
+        return zipf_rows(g, n, rows, alpha)
+    if ids == "uniform":
+        return g.integers(0, rows, n, dtype=np.int64)
+    raise ValueError(f"ids must be 'zipf' or 'uniform', got {ids!r}")
+
+
+def _ids_suffix(ids: str) -> str:
+    return "" if ids == "zipf" else "_" + ids
+
+
+def single_hot_bf16(batch: int = 65_536, max_rows: Optional[int] = None, ids: str = "zipf") -> PooledWorkload:
+    """26 tables, rows log-uniform in [1e3, 4e7], dim 128 bf16, one id per bag, Zipf(1.05) (or uniform) ids,
+    sum, fp32 out."""
     T = 26
     g0 = rng(2, 1000)
     rows = [int(round(math.exp(g0.uniform(math.log(1e3), math.log(4e7))))) for _ in range(T)]
     if max_rows is not None:
         rows = [min(r, max_rows) for r in rows]
-    idx = [zipf_rows(rng(2, t), batch, rows[t], 1.05) for t in range(T)]
+    idx = [draw_rows(rng(2, t), batch, rows[t], 1.05, ids) for t in range(T)]
     offsets = np.arange(T * batch + 1, dtype=np.int64)
-    return PooledWorkload("tbe_bf16_single_hot_26t_d128_b65536", rows, 128, "bf16", "sum", "fp32", batch,
-                          np.concatenate(idx), offsets, "normal0.02")
+    return PooledWorkload("tbe_bf16_single_hot_26t_d128_b65536" + _ids_suffix(ids), rows, 128, "bf16", "sum",
+                          "fp32", batch, np.concatenate(idx), offsets, "normal0.02")
 
 
-def int8_mean(batch: int = 16_384, rows: int = 5_000_000, tables: int = 64) -> PooledWorkload:
+def int8_mean(batch: int = 16_384, rows: int = 5_000_000, tables: int = 64, ids: str = "zipf") -> PooledWorkload:
     """64 tables x 5,000,000 x 128 int8 rowwise (from N(0, 0.05)), lengths Poisson(20) in [1, 100],
-    Zipf(1.2), mean, fp16 out."""
+    Zipf(1.2) (or uniform) ids, mean, fp16 out."""
     idx, lens = [], []
     for t in range(tables):
         g = rng(3, t)
         ln = poisson_lengths(g, batch, 20.0, 1, 100)
         lens.append(ln)
-        idx.append(zipf_rows(g, int(ln.sum()), rows, 1.2))
-    return PooledWorkload("tbe_int8_mean_64t_5m_d128_b16384", [rows] * tables, 128, "int8", "mean", "fp16",
-                          batch, np.concatenate(idx), offsets_from_lengths(np.concatenate(lens)), "normal0.05")
+        idx.append(draw_rows(g, int(ln.sum()), rows, 1.2, ids))
+    return PooledWorkload("tbe_int8_mean_64t_5m_d128_b16384" + _ids_suffix(ids), [rows] * tables, 128, "int8",
+                          "mean", "fp16", batch, np.concatenate(idx), offsets_from_lengths(np.concatenate(lens)),
+                          "normal0.05")
 
 
 @dataclass
@@ -140,18 +156,19 @@ def item_to_album(items: np.ndarray, n_album: int) -> np.ndarray:
 
 
 def seq_gather(batch: int = 1024, item_rows: int = 10_000_000, artist_rows: int = 1_000_000,
-               album_rows: int = 2_000_000, means=(150.0, 40.0, 80.0), max_len: int = 256) -> SeqWorkload:
-    """3 pools with lengths Poisson(150/40/80) clipped to [0, 256]; items Zipf(1.1) over 10M x 256 bf16,
-    artist (1M x 64) and album (2M x 64) ids from fixed maps of the item id."""
-    ids, offs = [], []
+               album_rows: int = 2_000_000, means=(150.0, 40.0, 80.0), max_len: int = 256,
+               ids: str = "zipf") -> SeqWorkload:
+    """3 pools with lengths Poisson(150/40/80) clipped to [0, 256]; items Zipf(1.1) (or uniform) over 10M x 256
+    bf16, artist (1M x 64) and album (2M x 64) ids from fixed maps of the item id."""
+    out_ids, offs = [], []
     for p, mean in enumerate(means):
         g = rng(4, p)
         ln = poisson_lengths(g, batch, mean, 0, max_len)
-        items = zipf_rows(g, int(ln.sum()), item_rows, 1.1)
-        ids.append([items, item_to_artist(items, artist_rows), item_to_album(items, album_rows)])
+        items = draw_rows(g, int(ln.sum()), item_rows, 1.1, ids)
+        out_ids.append([items, item_to_artist(items, artist_rows), item_to_album(items, album_rows)])
         offs.append(offsets_from_lengths(ln))
-    return SeqWorkload("seq_gather_3pools_b1024", batch, [max_len] * len(means),
-                       [item_rows, artist_rows, album_rows], [256, 64, 64], ids, offs)
+    return SeqWorkload("seq_gather_3pools_b1024" + _ids_suffix(ids), batch, [max_len] * len(means),
+                       [item_rows, artist_rows, album_rows], [256, 64, 64], out_ids, offs)
 
 
 @dataclass

@@ -132,3 +132,23 @@ def test_stack_workspace_size(pdm):
     assert size(B, kv, D, Fd, ns, []) == L.PDM_ERR_INVALID
     d = L.BlockDesc(B, D, D // 64, ns, Fd, kv, 0, 0)
     assert L.lib().pdm_onetrans_stack_workspace_size(ctypes.byref(d), None, 2) == L.PDM_ERR_INVALID
+
+
+def test_kjt_row_count_overflow_is_rejected(pdm):
+    """num_features * batch_size (and num_out * batch_size) must be checked before the product is formed: a
+    huge batch_size would otherwise wrap the int64 row count and pass the limits."""
+    L = pdm._lib
+    lib = L.lib()
+    F = 64
+    ids = (ctypes.c_void_p * F)(*([1] * F))
+    lens = (ctypes.c_int32 * F)(*([4] * F))
+    huge = 1 << 58
+    assert lib.pdm_kjt_from_dense(ids, lens, F, huge, 64, 0, None, None, None, None, 0, None) == L.PDM_ERR_INVALID
+    assert "overflow" in L.last_error()
+    assert lib.pdm_kjt_from_dense_noalloc(ids, lens, F, huge, 64, 0, None, None, None, None) == L.PDM_ERR_INVALID
+    assert "no-allocation limit" in L.last_error()
+    assert lib.pdm_kjt_from_dense_noalloc(ids, lens, F + 1, 1, 64, 0, None, None, None, None) == L.PDM_ERR_INVALID
+    assert "num_features" in L.last_error()
+    perm = (ctypes.c_int32 * F)(*range(F))
+    assert lib.pdm_kjt_permute(None, 64, None, F, huge, perm, F, None, None, None, None, 0, None) == L.PDM_ERR_INVALID
+    assert "overflow" in L.last_error()

@@ -96,6 +96,9 @@ def _run_case(pdm, dev, B, kv, q_len, n_ns, D=256, F=1024, seed=0, x_std=1.0, w_
     (130, 48, 48, 2),    # B > one GEMM row tile of NS tokens
     (4, 64, 20, 0),      # no NS tokens
     (6, 240, 100, 16),   # 4 query tiles over 240 keys: the 4-wave attention with 8 copy rounds
+    (2, 600, 600, 16),   # 19 query tiles over 608 padded keys: 8 waves, Q read from memory, <10,8>
+    (3, 500, 300, 16),   # 10 query tiles over 512 padded keys: Q does not fit beside K/V^T in LDS, <10,8>
+    (4, 250, 200, 16),   # 7 query tiles over 256 padded keys: the <4,8> instance
 ])
 def test_block_matches_oracle(pdm, dev, B, kv, q_len, n_ns):
     _run_case(pdm, dev, B, kv, q_len, n_ns, seed=B + kv)

@@ -73,3 +73,57 @@ def test_noalloc_rejects_inputs_beyond_the_scratch(pdm, dev):
     st = lib.pdm_kjt_from_dense_noalloc(None, None, 64, too_many, 64, 0, None, None, None, None)
     assert st == L.PDM_ERR_INVALID
     assert "no-allocation limit" in L.last_error()
+
+
+def test_noalloc_under_graph_capture(pdm, dev):
+    """The no-allocation build captured in a HIP graph (torch.cuda.graph) after one eager call on the device
+    (the first call on a device looks up the scratch array's address), replayed three times on new ids
+    written into the same input buffers, with eager work and synchronisations between the replays: every
+    replay matches the workspace entry point on the same ids bit for bit."""
+    L = pdm._lib
+    lib = L.lib()
+    F, B, Lr = 3, 5000, 7
+    ids = [torch.zeros((B, Lr + f), dtype=torch.int64, device=dev) for f in range(F)]
+    cap = sum(t.numel() for t in ids)
+    values = torch.zeros(cap, dtype=torch.int64, device=dev)
+    lengths = torch.zeros(F * B, dtype=torch.int32, device=dev)
+    offsets = torch.zeros(F * B + 1, dtype=torch.int64, device=dev)
+    id_ptrs = (ctypes.c_void_p * F)(*[t.data_ptr() for t in ids])
+    row_len = (ctypes.c_int32 * F)(*[t.shape[1] for t in ids])
+
+    def call():
+        st = lib.pdm_kjt_from_dense_noalloc(id_ptrs, row_len, F, B, 64, 0, values.data_ptr(), lengths.data_ptr(),
+                                            offsets.data_ptr(), L.stream_ptr(dev))
+        L.check(st, "pdm_kjt_from_dense_noalloc")
+
+    def fill(seed):
+        for f, m in enumerate(_mats(seed, F, B, Lr, 0.4)):
+            ids[f].copy_(torch.from_numpy(m))
+        torch.cuda.synchronize()
+        return [t.cpu().numpy() for t in ids]
+
+    fill(1)
+    call()  # eager first call: resolves the scratch address outside the capture
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
+        call()
+    torch.cuda.current_stream(dev).wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        call()
+    for rep in range(3):
+        mats = fill(40 + rep)
+        values.fill_(-7)
+        lengths.fill_(-7)
+        offsets.fill_(-7)
+        print(f"kjt no-alloc graph replay {rep}", flush=True)
+        graph.replay()
+        torch.cuda.synchronize()
+        want = _build(pdm, dev, mats, 0, noalloc=False)
+        n = int(offsets[-1].item())
+        got = (values[:n].cpu(), lengths.cpu(), offsets.cpu())
+        for name, a, b in zip(("values", "lengths", "offsets"), got, want):
+            assert torch.equal(a, b), f"replay {rep}: {name} differ"
