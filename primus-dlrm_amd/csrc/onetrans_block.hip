@@ -1021,18 +1021,20 @@ __global__ __launch_bounds__(NW * 64, WPS) void ffn_kernel(GemmArgs a) {
           for (int rb = 0; rb < RB; ++rb) u[rb] = mfma32x32x16(wf[s], hfr[rb][s], u[rb]);
         if constexpr (RB == 1) sched_mfma_ds_pipeline<KS, 3>();
       }
-      // G = bf16(gelu(bf16(U))): u[rb][e] is hidden unit (e/4)*8 + hf*4 + e%4 (LDS row order) of token fr;
-      // two halves of 8 values bound the registers the table reads hold in flight
+      // G = bf16(gelu(bf16(U))): u[rb][e] is hidden unit (e/4)*8 + hf*4 + e%4 (LDS row order) of token fr.
+      // The first half (u[0..7], G^T chunk c2 = 0) is computed before the FFN-down; the second half between
+      // the c2 = 0 MFMAs, which do not need it
       uint32_t gp[RB][8];
+      auto gelu_half = [&](int h2) {
 #pragma unroll
-      for (int rb = 0; rb < RB; ++rb)
-#pragma unroll
-        for (int h2 = 0; h2 < 2; ++h2) {
+        for (int rb = 0; rb < RB; ++rb) {
           float uv[8];
 #pragma unroll
           for (int e = 0; e < 8; ++e) uv[e] = u[rb][8 * h2 + e];
           gelu_lut_pack<8>(sGelu, uv, gp[rb] + 4 * h2);
         }
+      };
+      gelu_half(0);
       // FFN-down: y^T[rb][db] += W2[db rows, chunk c] . G[rb]^T; chunk c2 of G^T holds hidden units
       // 16*c2 + hf*8 + 0..7, piece 2*c2 + hf of W2 row d, stored at (2*c2 + hf) ^ ((d >> 2) & 3)
       const char* w2 = sW2[k];
@@ -1045,8 +1047,11 @@ __global__ __launch_bounds__(NW * 64, WPS) void ffn_kernel(GemmArgs a) {
           for (int db = 0; db < DB; ++db)
             wf[c2 * DB + db] =
                 *reinterpret_cast<const u32x4_t*>(w2 + (db * 32 + fr) * 64 + (((2 * c2 + hf) ^ ((fr >> 2) & 3)) << 4));
+        // the second GELU half has no dependence on the c2 = 0 MFMAs: the compiler's schedule interleaves them
+        // (an explicit MFMA / DS / VALU group order kept more fragments live and spilled)
+        gelu_half(1);
 #pragma unroll
-        for (int c2 = 0; c2 < 2; ++c2)
+        for (int c2 = 0; c2 < 2; ++c2) {
 #pragma unroll
           for (int db = 0; db < DB; ++db)
 #pragma unroll
@@ -1054,7 +1059,7 @@ __global__ __launch_bounds__(NW * 64, WPS) void ffn_kernel(GemmArgs a) {
               const u32x4_t gb = {gp[rb][4 * c2], gp[rb][4 * c2 + 1], gp[rb][4 * c2 + 2], gp[rb][4 * c2 + 3]};
               y[rb][db] = mfma32x32x16(wf[c2 * DB + db], gb, y[rb][db]);
             }
-        if constexpr (RB == 1) sched_mfma_ds_pipeline<DB * 2, 3>();
+        }
       }
     }
   }
