@@ -185,7 +185,26 @@ struct SeqLinArgs {
   int32_t* err;
   int64_t num_tokens;    // B * S
   int32_t P, F, S, pad_zero, align_left;
+  int32_t row0_apart;    // lookups of row 0 are left out of the sort (the row-0 column sum covers them)
 };
+
+// Pool p of S-token slot s of a sample and the slot's event in that pool (the last min(len, L) events, right
+// or left aligned, exactly as the gather's forward places them), or -1 for a padding slot.  Malformed
+// offsets make every slot of the (sample, pool) padding and set bad.
+__device__ __forceinline__ int64_t seq_slot_event(const SeqLinArgs& a, int64_t tok, int& p, bool& bad) {
+  const int64_t b = tok / a.S;
+  const int s = (int)(tok - b * a.S);
+  p = 0;
+  while (p + 1 < a.P && s >= a.soff[p + 1]) ++p;
+  int64_t beg = a.offsets[p][b], end = a.offsets[p][b + 1];
+  if (beg < 0 || end < beg || end > a.num_ids[p]) {
+    bad = true;
+    beg = end = 0;
+  }
+  const int pos = s - a.soff[p], L = a.lmax[p];
+  const int n = (int)(end - beg < (int64_t)L ? end - beg : (int64_t)L);
+  return a.align_left ? (pos < n ? end - n + pos : -1) : (pos >= L - n ? end - n + (pos - (L - n)) : -1);
+}
 
 // One thread per S-token slot (sample b, slot s): the slot's event (the last
 // min(len, L) events of its pool, right or left aligned, exactly as the
@@ -194,22 +213,14 @@ struct SeqLinArgs {
 // token row `token`, columns of feature f.  A padding slot looks up row 0
 // (pad mode ROW0) or nothing (ZERO); ids outside the table and malformed
 // offsets are skipped and flagged, as the forward does.
+// With row0_apart, lookups of row 0 (every padding slot in ROW0 mode, and events whose id is 0) keep the
+// sentinel key: the row-0 column sum adds their gradients in token order instead of the sort.
 __global__ __launch_bounds__(256) void seq_linearize_kernel(SeqLinArgs a) {
   const int64_t tok = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (tok >= a.num_tokens) return;
-  const int64_t b = tok / a.S;
-  const int s = (int)(tok - b * a.S);
-  int p = 0;
-  while (p + 1 < a.P && s >= a.soff[p + 1]) ++p;
-  int64_t beg = a.offsets[p][b], end = a.offsets[p][b + 1];
   bool bad = false;
-  if (beg < 0 || end < beg || end > a.num_ids[p]) {
-    bad = true;
-    beg = end = 0;
-  }
-  const int pos = s - a.soff[p], L = a.lmax[p];
-  const int n = (int)(end - beg < (int64_t)L ? end - beg : (int64_t)L);
-  const int64_t ev = a.align_left ? (pos < n ? end - n + pos : -1) : (pos >= L - n ? end - n + (pos - (L - n)) : -1);
+  int p = 0;
+  const int64_t ev = seq_slot_event(a, tok, p, bad);
   for (int f = 0; f < a.F; ++f) {
     int64_t id = 0;
     if (ev < 0) {
@@ -222,11 +233,152 @@ __global__ __launch_bounds__(256) void seq_linearize_kernel(SeqLinArgs a) {
       bad = true;
       continue;
     }
+    if (a.row0_apart && id == 0) continue;
     const int64_t q = (int64_t)f * a.num_tokens + tok;
     a.keys[q] = (uint32_t)(sl.row_off + id);
     a.bags[q] = (uint32_t)q;
   }
   if (bad && a.err) *a.err = 1;
+}
+
+// ---- 1b. row 0 of each feature's table (sequence gather with row0_apart) -----------------
+
+// Token blocks of the first column-sum pass (one partial row per block).
+constexpr int kRow0Blocks = 1024;  // a multiple of 16 x 16
+
+struct Row0Args {
+  SeqLinArgs seq;
+  const float* grad;      // token gradient [num_tokens, C4 * 4]
+  float* part;            // [kRow0Blocks, C4 * 4] partial column sums
+  uint32_t* part_cnt;     // [kRow0Blocks, PDM_SEQ_MAX_FEATURES] row-0 lookups per feature
+  float* sum;             // [C4 * 4] column sums over every token
+  uint32_t* cnt;          // [PDM_SEQ_MAX_FEATURES]
+  int32_t col_beg[PDM_SEQ_MAX_FEATURES + 1];  // feature f owns columns col_beg[f] .. col_beg[f + 1] - 1
+  int32_t C4;             // float4 columns of a token row, <= 256
+  int64_t tokens_per_block;
+};
+
+// Pass 1: block g sums, over its tokens in order, the gradient columns of every feature whose lookup at that
+// token is row 0 (a padding slot in ROW0 mode, or an event with id 0).  Per chunk of 256 tokens each thread
+// classifies one token; the tokens with some row-0 lookup are compacted into an LDS list in token order.
+// Thread (phase, c4) then adds float4 column c4 of list entries phase, phase + NPH, ..., issuing kRow0U row
+// loads before adding them; the NPH phase sums are added in phase order at the end.  Only token rows with a
+// row-0 lookup are read, whole and in order.
+constexpr int kRow0U = 8;
+
+__global__ __launch_bounds__(256) void seq_row0_colsum_kernel(Row0Args r) {
+  __shared__ uint16_t s_list[256];
+  __shared__ uint8_t s_flag[256];
+  __shared__ uint32_t s_tmp[4];
+  __shared__ __attribute__((aligned(16))) f32x4_t s_acc[256];
+  __shared__ uint32_t s_cnt[PDM_SEQ_MAX_FEATURES];
+  const SeqLinArgs& a = r.seq;
+  const int tid = threadIdx.x;
+  const int C4 = r.C4, NPH = 256 / C4;
+  const int ph = tid / C4, c4 = tid - ph * C4;
+  int feat = 0;  // feature of this thread's columns
+  while (feat + 1 < a.F && c4 * 4 >= r.col_beg[feat + 1]) ++feat;
+  if (tid < PDM_SEQ_MAX_FEATURES) s_cnt[tid] = 0;
+  const int64_t t0 = (int64_t)blockIdx.x * r.tokens_per_block;
+  const int64_t t1 = t0 + r.tokens_per_block < a.num_tokens ? t0 + r.tokens_per_block : a.num_tokens;
+  const f32x4_t* g4 = reinterpret_cast<const f32x4_t*>(r.grad);
+  const f32x4_t zero = {0.0f, 0.0f, 0.0f, 0.0f};
+  f32x4_t acc = zero;
+  for (int64_t c0 = t0; c0 < t1; c0 += 256) {
+    const int n = (int)(t1 - c0 < 256 ? t1 - c0 : 256);
+    uint32_t fl = 0;
+    if (tid < n) {
+      bool bad = false;
+      int p = 0;
+      const int64_t ev = seq_slot_event(a, c0 + tid, p, bad);
+      for (int f = 0; f < a.F; ++f) {
+        int64_t id = 0;
+        if (ev < 0) {
+          if (a.pad_zero) continue;
+        } else {
+          id = a.ids[p * PDM_SEQ_MAX_FEATURES + f][ev];
+        }
+        if (id == 0 && a.slots[f].rows > 0) fl |= 1u << f;
+      }
+    }
+    for (int f = 0; f < a.F; ++f)
+      if ((fl >> f) & 1u) atomicAdd(&s_cnt[f], 1u);
+    uint32_t m = 0;
+    const uint32_t at = block_excl_scan256(fl != 0 ? 1u : 0u, s_tmp, m);  // synchronises: last chunk's list read
+    if (fl != 0) {
+      s_list[at] = (uint16_t)tid;
+      s_flag[at] = (uint8_t)fl;
+    }
+    __syncthreads();
+    if (ph < NPH) {
+      for (int j = ph; j < (int)m; j += NPH * kRow0U) {
+        f32x4_t v[kRow0U];
+        bool use[kRow0U];
+#pragma unroll
+        for (int u = 0; u < kRow0U; ++u) {
+          const int e = j + u * NPH;
+          const int ee = e < (int)m ? e : j;
+          use[u] = e < (int)m && ((s_flag[ee] >> feat) & 1u);
+          v[u] = g4[(c0 + s_list[ee]) * C4 + c4];
+        }
+#pragma unroll
+        for (int u = 0; u < kRow0U; ++u)
+          if (use[u]) acc = acc + v[u];
+      }
+    }
+    __syncthreads();  // the list is read before the next chunk's scan overwrites s_tmp and the list
+  }
+  // phase sums in phase order
+  if (ph < NPH) s_acc[tid] = acc;
+  __syncthreads();
+  if (tid < C4) {
+    f32x4_t t = s_acc[tid];
+    for (int q = 1; q < NPH; ++q) t = t + s_acc[q * C4 + tid];
+    reinterpret_cast<f32x4_t*>(r.part)[(int64_t)blockIdx.x * C4 + tid] = t;
+  }
+  if (tid < PDM_SEQ_MAX_FEATURES) r.part_cnt[blockIdx.x * PDM_SEQ_MAX_FEATURES + tid] = s_cnt[tid];
+}
+
+// Pass 2: a block owns 16 columns; thread (segment, column) adds the partial sums of blocks
+// segment * 64 .. + 63 in block order, and the 16 segment sums are then added in segment order.  Counts
+// likewise (block 0).
+constexpr int kRow0Seg = 16;  // kRow0Blocks / kRow0Seg blocks per segment
+__global__ __launch_bounds__(256) void seq_row0_sum_kernel(Row0Args r) {
+  __shared__ float s_seg[kRow0Seg][16];
+  const int cl = threadIdx.x & 15, sg = threadIdx.x >> 4;
+  const int c = blockIdx.x * 16 + cl;
+  const int64_t stride = (int64_t)r.C4 * 4;
+  constexpr int PER = kRow0Blocks / kRow0Seg;
+  float t = 0.0f;
+  if (c < stride) {
+    for (int g = sg * PER; g < (sg + 1) * PER; g += 16) {
+      float v[16];  // 16 loads in flight, then added in block order
+#pragma unroll
+      for (int u = 0; u < 16; ++u) v[u] = r.part[(int64_t)(g + u) * stride + c];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) t += v[u];
+    }
+  }
+  s_seg[sg][cl] = t;
+  __syncthreads();
+  if (sg == 0 && c < stride) {
+    float sum = s_seg[0][cl];
+    for (int q = 1; q < kRow0Seg; ++q) sum += s_seg[q][cl];
+    r.sum[c] = sum;
+  }
+  if (blockIdx.x == 0) {
+    // counts (integers: any order): thread t adds feature t % 8 of blocks t / 8, t / 8 + 32, ...
+    __shared__ uint32_t s_n[PDM_SEQ_MAX_FEATURES];
+    if (threadIdx.x < PDM_SEQ_MAX_FEATURES) s_n[threadIdx.x] = 0;
+    __syncthreads();
+    const int f = threadIdx.x % PDM_SEQ_MAX_FEATURES;
+    uint32_t n = 0;
+    for (int g = threadIdx.x / PDM_SEQ_MAX_FEATURES; g < kRow0Blocks; g += 256 / PDM_SEQ_MAX_FEATURES)
+      n += r.part_cnt[g * PDM_SEQ_MAX_FEATURES + f];
+    atomicAdd(&s_n[f], n);
+    __syncthreads();
+    if (threadIdx.x < PDM_SEQ_MAX_FEATURES) r.cnt[threadIdx.x] = s_n[threadIdx.x];
+  }
 }
 
 // ---- 2. radix sort ---------------------------------------------------------------
@@ -808,6 +960,49 @@ __global__ __launch_bounds__(256) void bwd_fixup_kernel(AccArgs a) {
 }
 
 // Distinct rows (of the key range) whose first entry lies in each chunk.
+// Row 0 of the tables of one dim group (sequence gather with row0_apart): block f serves feature f; the
+// first feature of each distinct row-0 key adds the column sums of every feature on that key, in feature
+// order, and applies the update, once, when some slot looked the row up.
+struct Row0Upd {
+  uint32_t key[PDM_SEQ_MAX_FEATURES];       // row id of row 0 of feature f's table
+  int32_t col_beg[PDM_SEQ_MAX_FEATURES];    // feature f's first gradient column
+  const float* sum;                         // row-0 column sums
+  const uint32_t* cnt;                      // row-0 lookups per feature
+  int32_t F;
+};
+
+template <int G, int VEC, int MODE>
+__global__ __launch_bounds__(64) void bwd_row0_update_kernel(AccArgs a, Row0Upd u) {
+  const int f = blockIdx.x;
+  if (f >= u.F) return;
+  const uint32_t key = u.key[f];
+  if (key < a.key_lo || key >= a.key_hi) return;
+  for (int e = 0; e < f; ++e)
+    if (u.key[e] == key) return;
+  uint32_t n = 0;
+  for (int e = f; e < u.F; ++e)
+    if (u.key[e] == key) n += u.cnt[e];
+  if (n == 0) return;
+  const int gl = threadIdx.x;
+  if (gl >= G) return;
+  const int D4 = a.D >> 2;
+  f32x4_t g[VEC];
+#pragma unroll
+  for (int v = 0; v < VEC; ++v) g[v] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  const f32x4_t* sum4 = reinterpret_cast<const f32x4_t*>(u.sum);
+  for (int e = f; e < u.F; ++e) {
+    if (u.key[e] != key) continue;
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) {
+      const int c = gl + v * G;
+      if (c < D4) g[v] = g[v] + sum4[(u.col_beg[e] >> 2) + c];
+    }
+  }
+  RowState<VEC> st;
+  load_state<G, VEC, MODE>(a, key, gl, st);
+  update_row<G, VEC, MODE>(a, key, g, st, gl, 0);
+}
+
 __global__ __launch_bounds__(256) void bwd_count_heads_kernel(const uint32_t* __restrict__ keys,
                                                               uint32_t* __restrict__ cnt, int64_t num_chunks,
                                                               uint32_t key_lo, uint32_t key_hi) {
@@ -831,6 +1026,7 @@ __global__ void write_i64_kernel(int64_t* p, int64_t v) {
 struct BwdLayout {
   int64_t n_pad, num_tiles, num_chunks, dmax;
   int64_t keys_a, keys_b, vals_a, vals_b, bag_scale, hist, totals, part_first, part_last, total;
+  int64_t row0_part, row0_part_cnt, row0_sum, row0_cnt;  // -1: the row-0 column sum does not fit this plan
   int32_t num_levels;
   int64_t level[kMaxLevels];  // byte offset of each level >= 1
 };
@@ -867,12 +1063,21 @@ BwdLayout bwd_layout(const pdm_tbe_plan_s* plan, int64_t n, int64_t batch_size) 
     ++L.num_levels;
     span *= 64;
   }
+  // the row-0 column sums of the sequence backward (token rows of at most 1024 columns)
+  L.row0_part = L.row0_part_cnt = L.row0_sum = L.row0_cnt = -1;
+  if (plan->total_dim <= 1024 && plan->total_dim % 4 == 0) {
+    L.row0_part = take((int64_t)kRow0Blocks * plan->total_dim * 4);
+    L.row0_part_cnt = take((int64_t)kRow0Blocks * PDM_SEQ_MAX_FEATURES * 4);
+    L.row0_sum = take(plan->total_dim * 4);
+    L.row0_cnt = take(PDM_SEQ_MAX_FEATURES * 4);
+  }
   L.total = off;
   return L;
 }
 
 using AccFn = void (*)(AccArgs);
 using FoldFn = void (*)(FoldArgs);
+using Row0Fn = void (*)(AccArgs, Row0Upd);
 
 // float4 columns per lane of a row update: fewer lanes per row put more rows
 // of a wavefront in flight (the update is latency-bound on its loads).
@@ -881,13 +1086,14 @@ using FoldFn = void (*)(FoldArgs);
 #endif
 
 template <int MODE>
-bool pick_acc(int D, AccFn& acc, AccFn& fix, FoldFn& fold) {
+bool pick_acc(int D, AccFn& acc, AccFn& fix, FoldFn& fold, Row0Fn& row0) {
   const int d4 = D / 4;
 #define PDM_ACC_CASE(G_, V_)                            \
   {                                                     \
     acc = bwd_accumulate_kernel<G_, V_, MODE>;          \
     fix = bwd_fixup_kernel<G_, V_, MODE>;               \
     fold = bwd_fold_kernel<G_, V_>;                     \
+    row0 = bwd_row0_update_kernel<G_, V_, MODE>;        \
     return true;                                        \
   }
   constexpr int V = PDM_BWD_VEC;
@@ -904,11 +1110,11 @@ bool pick_acc(int D, AccFn& acc, AccFn& fix, FoldFn& fold) {
   return false;
 }
 
-bool pick_acc_mode(int mode, int D, AccFn& acc, AccFn& fix, FoldFn& fold) {
+bool pick_acc_mode(int mode, int D, AccFn& acc, AccFn& fix, FoldFn& fold, Row0Fn& row0) {
   switch (mode) {
-    case MODE_ADAM: return pick_acc<MODE_ADAM>(D, acc, fix, fold);
-    case MODE_ADAGRAD: return pick_acc<MODE_ADAGRAD>(D, acc, fix, fold);
-    default: return pick_acc<MODE_GRAD>(D, acc, fix, fold);
+    case MODE_ADAM: return pick_acc<MODE_ADAM>(D, acc, fix, fold, row0);
+    case MODE_ADAGRAD: return pick_acc<MODE_ADAGRAD>(D, acc, fix, fold, row0);
+    default: return pick_acc<MODE_GRAD>(D, acc, fix, fold, row0);
   }
 }
 
@@ -1002,16 +1208,47 @@ int run_backward(const BwdCall& c) {
   hipLaunchKernelGGL(fill_u32_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, c.stream, keys_a, n4,
                      kSentinel);
   PDM_CHECK_LAUNCH();
+  // The sequence backward takes row 0 of every feature's table out of the sort (left padding makes it one
+  // run of most slots, read as random token rows): two column-sum passes add the gradients of the slots
+  // that look it up, in token order, and one small launch per dim group applies its update.
+  const bool row0_apart = c.seq != nullptr && c.mode != MODE_GRAD && L.row0_part >= 0 && c.grad_stride <= 1024;
+  Row0Upd r0u{};
   if (c.seq) {
     SeqLinArgs sa = *c.seq;
     sa.slots = plan->d_bwd_slots;
     sa.keys = keys_a;
     sa.bags = vals_a;
     sa.err = c.err;
+    sa.row0_apart = row0_apart ? 1 : 0;
     const int64_t blocks = (sa.num_tokens + 255) / 256;
     PDM_CHECK_ARG(blocks < (int64_t(1) << 31), "too many tokens for one launch");
     hipLaunchKernelGGL(seq_linearize_kernel, dim3((unsigned)blocks), dim3(256), 0, c.stream, sa);
     PDM_CHECK_LAUNCH();
+    if (row0_apart) {
+      Row0Args ra{};
+      ra.seq = sa;
+      ra.grad = c.grad;
+      ra.part = reinterpret_cast<float*>(ws + L.row0_part);
+      ra.part_cnt = reinterpret_cast<uint32_t*>(ws + L.row0_part_cnt);
+      ra.sum = reinterpret_cast<float*>(ws + L.row0_sum);
+      ra.cnt = reinterpret_cast<uint32_t*>(ws + L.row0_cnt);
+      ra.C4 = (int32_t)(c.grad_stride / 4);
+      ra.tokens_per_block = (sa.num_tokens + kRow0Blocks - 1) / kRow0Blocks;
+      for (int f = 0; f < sa.F; ++f) {
+        ra.col_beg[f] = plan->tables[f].out_offset;
+        // a table without rows has no row 0 (its row id would be the next table's first row)
+        r0u.key[f] = plan->tables[f].rows > 0 ? (uint32_t)plan->slot_row_off[f] : 0xFFFFFFFFu;
+        r0u.col_beg[f] = plan->tables[f].out_offset;
+      }
+      ra.col_beg[sa.F] = (int32_t)c.grad_stride;
+      r0u.sum = ra.sum;
+      r0u.cnt = ra.cnt;
+      r0u.F = sa.F;
+      hipLaunchKernelGGL(seq_row0_colsum_kernel, dim3(kRow0Blocks), dim3(256), 0, c.stream, ra);
+      PDM_CHECK_LAUNCH();
+      hipLaunchKernelGGL(seq_row0_sum_kernel, dim3((unsigned)((c.grad_stride + 15) / 16)), dim3(256), 0, c.stream, ra);
+      PDM_CHECK_LAUNCH();
+    }
   } else {
     bool has_mean = false;
     for (const auto& d : plan->tables) has_mean = has_mean || d.pooling == PDM_POOL_MEAN;
@@ -1097,7 +1334,8 @@ int run_backward(const BwdCall& c) {
     }
     AccFn acc = nullptr, fix = nullptr;
     FoldFn fold = nullptr;
-    if (!pick_acc_mode(c.mode, g.dim, acc, fix, fold)) {
+    Row0Fn row0 = nullptr;
+    if (!pick_acc_mode(c.mode, g.dim, acc, fix, fold, row0)) {
       set_error("pdm_tbe_backward: unsupported dim " + std::to_string(g.dim));
       return PDM_ERR_UNSUPPORTED;
     }
@@ -1130,6 +1368,10 @@ int run_backward(const BwdCall& c) {
     }
     hipLaunchKernelGGL(fix, dim3((unsigned)acc_blocks), dim3(256), 0, c.stream, a);
     PDM_CHECK_LAUNCH();
+    if (row0_apart) {
+      hipLaunchKernelGGL(row0, dim3((unsigned)r0u.F), dim3(64), 0, c.stream, a, r0u);
+      PDM_CHECK_LAUNCH();
+    }
   }
   return PDM_OK;
 }

@@ -36,7 +36,8 @@ def _pools(g, B, pools, specs, zipf=None):
     return ids, offs
 
 
-def _run(pdm, dev, specs, pools, B, optimizer, pad_mode="row0", align="right", steps=2, zipf=None, bad_id=False):
+def _run(pdm, dev, specs, pools, B, optimizer, pad_mode="row0", align="right", steps=2, zipf=None, bad_id=False,
+         ids_fn=None):
     L = pdm._lib
     g = np.random.default_rng(17)
     slots, flat = _tables(g, specs)
@@ -55,6 +56,8 @@ def _run(pdm, dev, specs, pools, B, optimizer, pad_mode="row0", align="right", s
     bad = 0
     for step in range(1, steps + 1):
         ids, offs = _pools(g, B, pools, specs, zipf)
+        if ids_fn is not None:
+            ids = ids_fn(g, ids)
         if bad_id:
             ids[0][1][3] = specs[1][0] + 5
         G = g.normal(0, 1, (B, S, Dt)).astype(np.float32)
@@ -97,6 +100,43 @@ def test_seq_backward_hot_rows_and_invalid_ids(pdm, dev):
                                                  zipf=1.3, bad_id=True)
     assert err == 1 and bad == 2
     _close(w, ww, "weights")
+
+
+@pytest.mark.parametrize("optimizer", [o.ADAM, o.ROWWISE_ADAGRAD])
+def test_seq_backward_row0_only_when_looked_up(pdm, dev, optimizer):
+    """Row 0 of a table takes the update only when some slot looks it up.  ZERO padding with every id >= 1:
+    row 0 and its state keep their bits exactly.  ROW0 padding with a tenth of the events forced to id 0:
+    row 0's gradient adds padding slots and events (the oracle's row-0 sum), matching the oracle."""
+    specs = [(700, 32), (90, 16), (60, 16)]
+
+    def no_zero(g, ids):
+        return [[1 + a % (r - 1) for a, (r, _) in zip(row, specs)] for row in ids]
+
+    def some_zero(g, ids):
+        out = []
+        for row in ids:
+            z = g.random(row[0].size) < 0.1
+            out.append([np.where(z, 0, a) for a in row])
+        return out
+
+    (w, m1, m2, err), (ww, wm1, wm2, bad) = _run(pdm, dev, specs, [(24, 12.0), (16, 20.0)], 64, optimizer,
+                                                 "zero", "right", ids_fn=no_zero)
+    assert err == 0 and bad == 0
+    _close(w, ww, "weights")
+    g0 = np.random.default_rng(17)
+    slots, flat0 = _tables(g0, specs)
+    for sl in slots:
+        r0 = slice(sl["weights_offset"] // 4, sl["weights_offset"] // 4 + sl["dim"])
+        assert np.array_equal(w[r0], flat0[r0]), "row 0 changed without a lookup"
+        if optimizer == o.ADAM:
+            assert not m1[r0].any() and not m2[r0].any()
+    (w, m1, m2, err), (ww, wm1, wm2, bad) = _run(pdm, dev, specs, [(24, 12.0), (16, 20.0)], 64, optimizer,
+                                                 "row0", "right", ids_fn=some_zero)
+    assert err == 0 and bad == 0
+    _close(w, ww, "weights")
+    _close(m1, wm1, "state 1", atol=1e-6)
+    if optimizer == o.ADAM:
+        _close(m2, wm2, "state 2", atol=1e-6)
 
 
 def _seq_module(pdm, dev, optim_cls, kw):
