@@ -196,6 +196,34 @@ __device__ __forceinline__ void tile_row(const GemmArgs& a, int mt, int rows_per
   }
 }
 
+// NS tiles in XCD-major order for a persistent grid of a multiple of 8 workgroups, which the dispatcher deals
+// round-robin over the 8 XCDs (tile mt runs on XCD mt % 8): the NS tile that runs at position mt is the
+// rank-th tile of the list sorted by (token % 8, token, tile), where rank is mt's place among the NS
+// positions sorted by (mt % 8, mt).  When the counts agree (16 NS tokens, 8 tiles each), every tile of a
+// token runs on one XCD, whose L2 then fetches the token's weights once instead of every XCD fetching every
+// token's.  A bijection on the NS tiles for any sizes; S tiles are unchanged.
+__device__ __forceinline__ int ns_tile_xcd_major(const GemmArgs& a, int mt) {
+  if (mt < a.tiles_s) return mt;
+  const int nt = a.n_ns * a.tiles_b;
+  const int p = mt - a.tiles_s, cp = mt & 7;
+  int rank = 0;
+  for (int c = 0; c < cp; ++c) {
+    const int q = (c - a.tiles_s) & 7;
+    rank += q < nt ? (nt - 1 - q) / 8 + 1 : 0;
+  }
+  rank += (p - ((cp - a.tiles_s) & 7)) / 8;
+  int pre = 0;
+  for (int k = 0; k < 8; ++k) {
+    const int ck = (k < a.n_ns ? (a.n_ns - 1 - k) / 8 + 1 : 0) * a.tiles_b;
+    if (rank < pre + ck) {
+      const int q = rank - pre;
+      return a.tiles_s + (k + 8 * (q / a.tiles_b)) * a.tiles_b + q % a.tiles_b;
+    }
+    pre += ck;
+  }
+  return mt;  // not reached
+}
+
 template <int EPI>
 __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t sA[2][GBM][GBK + GPAD];
@@ -844,7 +872,8 @@ __global__ __launch_bounds__(NW * 64, WPS) void ffn_kernel(GemmArgs a) {
   // residuals at the same time: one's memory-bound prologue then runs beside the other's MFMAs.
   if (a.stagger > 0 && (int)blockIdx.x >= (int)(gridDim.x / 2))
     for (int i = 0; i < a.stagger; ++i) __builtin_amdgcn_s_sleep(127);
-  for (int mt = blockIdx.x; mt < a.total_blocks; mt += gridDim.x) {
+  for (int mt_run = blockIdx.x; mt_run < a.total_blocks; mt_run += gridDim.x) {
+  const int mt = ns_tile_xcd_major(a, mt_run);
   // The lane's LDS and global offsets below derive from an opaque copy of the lane index taken per tile, so
   // the compiler recomputes them in each tile instead of holding them in registers through the prologue and
   // epilogue, where every register is taken.
