@@ -79,11 +79,48 @@ def _check_stream(x: torch.Tensor) -> None:
 
 def build_pyramid_mask(q_len: int, kv_len: int, device: torch.device) -> torch.Tensor:
     """Bottom-right causal mask ``[q_len, kv_len]``: query i sees keys
-    j <= i + (kv_len - q_len) (onetrans.py:62-67)."""
+    j <= i + (kv_len - q_len) (onetrans.py:62-67).  The mask is tagged as the pyramid mask of its shape, so
+    ``OneTransBlock.forward`` accepts it without comparing its values (inference tensors, which keep no
+    version counter, are compared on every call)."""
     offset = kv_len - q_len
     q_idx = torch.arange(q_len, device=device).unsqueeze(1) + offset
     kv_idx = torch.arange(kv_len, device=device).unsqueeze(0)
-    return kv_idx <= q_idx
+    mask = kv_idx <= q_idx
+    _tag_pyramid(mask, q_len, kv_len)
+    return mask
+
+
+def _version_of(t: torch.Tensor) -> Optional[int]:
+    try:
+        return t._version
+    except RuntimeError:  # inference tensors keep no version counter
+        return None
+
+
+def _tag_pyramid(mask: torch.Tensor, q_len: int, kv_len: int) -> None:
+    version = _version_of(mask)
+    if version is not None and not torch.compiler.is_compiling() and not isinstance(mask, torch.fx.Proxy):
+        mask._pdm_pyramid = (q_len, kv_len, version)
+
+
+def check_pyramid_mask(mask: torch.Tensor, q_len: int, kv_len: int) -> None:
+    """The kernels apply the pyramid mask (``build_pyramid_mask(q_len, kv_len)``, the only mask the
+    reference's backbone passes, onetrans.py:568-582) whatever mask they are given, so any other mask is
+    rejected here.  A mask made by ``build_pyramid_mask`` and not modified since passes at once; any other
+    tensor is compared with the pyramid mask (one device-to-host sync) and, when equal, tagged so that later
+    calls with the same unmodified tensor pass at once."""
+    if tuple(mask.shape) != (q_len, kv_len):
+        raise ValueError(f"mask must be [q_len, kv_len] = [{q_len}, {kv_len}]")
+    if mask.dtype != torch.bool:
+        raise ValueError("mask must be a bool mask (True = the query attends to the key), as build_pyramid_mask "
+                         "makes it")
+    version = _version_of(mask)
+    if version is not None and getattr(mask, "_pdm_pyramid", None) == (q_len, kv_len, version):
+        return
+    if not torch.equal(mask, build_pyramid_mask(q_len, kv_len, mask.device)):
+        raise ValueError("only the pyramid mask build_pyramid_mask(q_len, kv_len) is supported: the kernels "
+                         "apply the bottom-right causal mask; run the reference's attention for other masks")
+    _tag_pyramid(mask, q_len, kv_len)
 
 
 class RMSNorm(nn.Module):
@@ -138,8 +175,8 @@ class OneTransBlock(nn.Module):
 
     Forward only (inference / evaluation); dropout must be inactive.  ``x``
     is the fp32 residual stream ``[B, kv_len, D]`` whose last ``n_ns`` tokens
-    are the NS-tokens; ``mask`` must be ``build_pyramid_mask(q_len, kv_len)``
-    (only its shape is checked, so no host sync happens).
+    are the NS-tokens; ``mask`` must be ``build_pyramid_mask(q_len, kv_len)`` or None
+    (``check_pyramid_mask``: other masks raise ``ValueError``; checked eagerly, not inside a compiled graph).
     """
 
     def __init__(self, d_model: int, n_heads: int, n_ns_tokens: int, ffn_mult: int = 4,
@@ -161,8 +198,8 @@ class OneTransBlock(nn.Module):
                 raise ValueError(f"n_s_tokens ({n_s_tokens}) must equal kv_len - n_ns ({kv_len - self.attn.n_ns})")
             # (not while compiling: the mask is no graph input, and equating q_len with its size would leave
             # q_len bound to a symbol the compiled graph does not receive)
-            if mask is not None and not torch.compiler.is_compiling() and tuple(mask.shape) != (q_len, kv_len):
-                raise ValueError(f"mask must be [q_len, kv_len] = [{q_len}, {kv_len}]")
+            if mask is not None and not torch.compiler.is_compiling():
+                check_pyramid_mask(mask, q_len, kv_len)
             _check_stream(x)
         return torch.ops.pdm.onetrans_block_fwd(x.contiguous(), *self.kernel_weights(), self.attn.n_heads, q_len)
 

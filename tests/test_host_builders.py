@@ -143,6 +143,38 @@ def test_pyramid_mask_product_matches_bruteforce(pdm):
         assert torch.equal(m, want)
 
 
+def test_block_rejects_masks_other_than_the_pyramid(pdm):
+    """The kernels always apply the bottom-right pyramid mask, so the block refuses any other mask before it
+    launches anything (the checks run on the host, so CPU tensors reach them)."""
+    from primus_dlrm_amd.onetrans import check_pyramid_mask
+    q, kv, n_ns = 6, 10, 2
+    blk = pdm.OneTransBlock(16, 2, n_ns).eval()
+    x = torch.zeros(1, kv, 16)
+    good = torch.tensor([[j <= i + kv - q for j in range(kv)] for i in range(q)])  # not made by the builder
+    check_pyramid_mask(good, q, kv)  # equal values pass, and the tensor is tagged
+    assert good._pdm_pyramid == (q, kv, good._version)
+    good[0, 0] = True  # an in-place change bumps the version: compared again, still the pyramid mask
+    check_pyramid_mask(good, q, kv)
+    wrong = [
+        torch.ones(q, kv, dtype=torch.bool),                                  # no mask at all
+        torch.tensor([[j <= i for j in range(kv)] for i in range(q)]),        # top-left causal
+        good.float(),                                                          # additive / float masks
+        pdm.build_pyramid_mask(q, kv + 1, torch.device("cpu")),               # another shape
+    ]
+    flipped = pdm.build_pyramid_mask(q, kv, torch.device("cpu"))
+    flipped[q - 1, 0] = False  # modified after it was built: the tag no longer applies
+    wrong.append(flipped)
+    for m in wrong:
+        with pytest.raises(ValueError):
+            blk(x, m, q, kv - n_ns)
+    with torch.inference_mode():
+        inf = pdm.build_pyramid_mask(q, kv, torch.device("cpu"))  # no version counter: compared each call
+        check_pyramid_mask(inf, q, kv)
+        inf[0, kv - 1] = True
+        with pytest.raises(ValueError):
+            check_pyramid_mask(inf, q, kv)
+
+
 # ---- synthetic generators ------------------------------------------------------------------
 
 def test_zipf_rank_to_row_is_a_bijection(pdm):
