@@ -16,6 +16,7 @@
 // [0, num_indices) of the index array: offending entries are skipped and
 // reported through an optional device flag.
 #include <algorithm>
+#include <cstdlib>
 #include <memory>
 #include <type_traits>
 #include <vector>
@@ -377,6 +378,134 @@ __global__ __launch_bounds__(256) void tbe_pooled_kernel(TbeArgs a) {
 #pragma unroll
   for (int r = 0; r < R; ++r)
     if (r < nb) store_bag<WT, OT, VB, NC>(a, m, b0 + r, lpb, j, acc[r], count[r]);
+  if (bad && a.err) a.err[0] = 1;
+}
+
+// Small launches of multi-id bags (a few thousand bags per table group), where a lane group walking its bag
+// U rows at a time spends most of the launch in dependent memory round trips (offsets, then ids, then one
+// round per U rows of its longest bag).  A workgroup of 256 threads pools BPW = 256 / LPB consecutive bags of
+// one table, whose ids form one contiguous range of the index array: it reads the bags' offsets, then the ids
+// of up to P = 4096 / LPB positions (P / 256 per thread), then every row piece of those positions at once
+// (16 loads of 16 bytes per thread, all in flight), so a round costs three memory latencies whatever the bag
+// lengths.  The pieces go through LDS in two halves of P / 2 rows (32 KB), and the LPB lanes of each bag add
+// its rows from there in bag order: every sum is the sequential fp32 sum, as in tbe_pooled_kernel.  A
+// workgroup whose bag ranges are not valid pools each bag on its own, skipping invalid entries, and reports
+// them.  Row payload = LPB x 16 bytes of fp32, fp16 or bf16 values.
+constexpr int kStagedPieces = 16;  // row pieces per thread and round
+
+template <int WT, int OT, int LPB>
+__global__ __launch_bounds__(256) void tbe_staged_kernel(TbeArgs a) {
+  constexpr int BPW = 256 / LPB;
+  constexpr int P = 256 * kStagedPieces / LPB;  // positions per round
+  constexpr int EPV = epv<WT, 16>();
+  __shared__ int64_t s_off[BPW + 1];
+  __shared__ int32_t s_row[P];  // table row of a position of the round, -1: none (padding, invalid, past the end)
+  __shared__ __attribute__((aligned(16))) u32x4_t s_data[P / 2 * LPB];
+  __shared__ int s_bad;
+  const int tid = threadIdx.x;
+  const int g = tid / LPB, j = tid % LPB;
+  const int64_t tl = (int64_t)blockIdx.x / a.chunks_per_table;
+  const int64_t b0 = ((int64_t)blockIdx.x - tl * a.chunks_per_table) * BPW;
+  const int nb = (int)min((int64_t)BPW, a.B - b0);
+  const int t = a.table_base >= 0 ? a.table_base + (int)tl : a.group_tables[tl];
+  const TbeMeta m = a.meta[t];
+  const int64_t bag0 = (int64_t)t * a.B + b0;
+  if (tid <= BPW) s_off[tid] = a.offsets[bag0 + (tid <= nb ? tid : nb)];
+  if (tid == 0) s_bad = 0;
+  __syncthreads();
+  // every bag of the workgroup has a valid, ordered range (then their ids are one contiguous range)
+  if (tid < nb && !(s_off[tid] >= 0 && s_off[tid + 1] >= s_off[tid] && s_off[tid + 1] <= a.num_indices)) s_bad = 1;
+  __syncthreads();
+  float acc[EPV];
+#pragma unroll
+  for (int e = 0; e < EPV; ++e) acc[e] = 0.0f;
+  int count = 0;
+  bool bad = false;
+  const char* wbase = a.weights + m.w_off;
+  if (s_bad) {
+    // some range is invalid: each group pools its own bag one row at a time, the invalid one to 0
+    if (g < nb) {
+      int64_t s0 = s_off[g], e0 = s_off[g + 1];
+      if (s0 < 0 || e0 < s0 || e0 > a.num_indices) {
+        s0 = e0 = 0;
+        bad = true;
+      }
+      for (int64_t pos = s0; pos < e0; ++pos) {
+        const int64_t idx = load_index(a, pos);
+        if (a.padding_idx >= 0 && idx == a.padding_idx) continue;
+        if (idx < 0 || idx >= m.rows) {
+          bad = true;
+          continue;
+        }
+        if (j < a.payload_vecs) {
+          uint32_t w[4];
+          load_words<16>(wbase + idx * (int64_t)m.row_bytes + j * 16, w);
+          accumulate<WT, 16>(acc, w, 0.0f, 0.0f);
+        }
+        ++count;
+      }
+    }
+  } else {
+    const int64_t s = s_off[0], e = s_off[nb];
+    const int64_t gs = g < nb ? s_off[g] : e, ge = g < nb ? s_off[g + 1] : e;  // this group's bag
+    for (int64_t base = s; base < e; base += P) {
+      const int n = (int)min((int64_t)P, e - base);
+      __syncthreads();  // the previous round's s_row is no longer read
+#pragma unroll
+      for (int k = 0; k < P / 256; ++k) {
+        const int i = tid + 256 * k;
+        int32_t r = -1;
+        if (i < n) {
+          const int64_t idx = load_index(a, base + i);
+          const bool live = !(a.padding_idx >= 0 && idx == a.padding_idx);
+          const bool ok = idx >= 0 && idx < m.rows;
+          bad |= live && !ok;
+          r = live && ok ? (int32_t)idx : -1;
+        }
+        s_row[i] = r;
+      }
+      __syncthreads();
+      // every piece of the round's rows: piece q = tid + 256 k is part q % LPB of position q / LPB
+      u32x4_t v[kStagedPieces];
+#pragma unroll
+      for (int k = 0; k < kStagedPieces; ++k) {
+        const int q = tid + 256 * k;
+        const int r = s_row[q / LPB];
+        v[k] = u32x4_t{0u, 0u, 0u, 0u};
+        if (r >= 0) {
+          uint32_t w[4];
+          load_words<16>(wbase + (int64_t)r * m.row_bytes + (q % LPB) * 16, w);
+          v[k] = u32x4_t{w[0], w[1], w[2], w[3]};
+        }
+      }
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        if (h == 1) __syncthreads();  // the first half has been read
+#pragma unroll
+        for (int k = 0; k < kStagedPieces / 2; ++k) s_data[tid + 256 * k] = v[h * (kStagedPieces / 2) + k];
+        __syncthreads();
+        // this group's positions within the half, in bag order
+        const int64_t h0 = base + (int64_t)h * (P / 2);
+        const int64_t lo = gs > h0 ? gs : h0;
+        const int64_t hi0 = h0 + P / 2 < base + n ? h0 + P / 2 : base + n;
+        const int64_t hi = ge < hi0 ? ge : hi0;
+        for (int64_t pos = lo; pos < hi; ++pos) {
+          const int li = (int)(pos - h0);
+          if (s_row[h * (P / 2) + li] < 0) continue;
+          const u32x4_t d = s_data[li * LPB + j];
+          const uint32_t w[4] = {d.x, d.y, d.z, d.w};
+          accumulate<WT, 16>(acc, w, 0.0f, 0.0f);
+          ++count;
+        }
+      }
+    }
+  }
+  if (g < nb && j < a.payload_vecs) {
+    float acc1[1][EPV];
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) acc1[0][e] = acc[e];
+    store_bag<WT, OT, 16, 1>(a, m, b0 + g, LPB, j, acc1, count);
+  }
   if (bad && a.err) a.err[0] = 1;
 }
 
@@ -872,6 +1001,45 @@ int bags_per_group_rt(int wt, int vb, int nc, bool multi) {
   return r < 1 ? 1 : (r > 8 ? 8 : r);
 }
 
+// Staged kernel for small launches of multi-id bags: fp32 / fp16 / bf16 rows of 64, 128 or 256 bytes.
+template <int WT>
+KernelFn pick_staged_ot(int ot, int lpb) {
+  auto by_lpb = [&](auto ot_tag) -> KernelFn {
+    constexpr int OT = decltype(ot_tag)::value;
+    switch (lpb) {
+      case 4: return tbe_staged_kernel<WT, OT, 4>;
+      case 8: return tbe_staged_kernel<WT, OT, 8>;
+      case 16: return tbe_staged_kernel<WT, OT, 16>;
+      default: return nullptr;
+    }
+  };
+  switch (ot) {
+    case PDM_F32: return by_lpb(std::integral_constant<int, PDM_F32>{});
+    case PDM_F16: return by_lpb(std::integral_constant<int, PDM_F16>{});
+    case PDM_BF16: return by_lpb(std::integral_constant<int, PDM_BF16>{});
+    default: return nullptr;
+  }
+}
+
+KernelFn pick_staged(int wt, int ot, int payload) {
+  if (payload % 16 != 0) return nullptr;
+  const int lpb = payload / 16;
+  switch (wt) {
+    case PDM_F32: return pick_staged_ot<PDM_F32>(ot, lpb);
+    case PDM_F16: return pick_staged_ot<PDM_F16>(ot, lpb);
+    case PDM_BF16: return pick_staged_ot<PDM_BF16>(ot, lpb);
+    default: return nullptr;
+  }
+}
+
+// Bags (tables x batch) up to which a launch of multi-id bags takes the staged kernel; PDM_TBE_STAGED_MAX_BAGS
+// overrides it (0: never).
+constexpr int64_t kStagedMaxBags = 131072;
+int64_t staged_max_bags() {
+  const char* e = std::getenv("PDM_TBE_STAGED_MAX_BAGS");
+  return e && *e ? std::atoll(e) : kStagedMaxBags;
+}
+
 KernelFn pick_kernel(int wt, int ot, int vb, int nc, bool multi, int lpb, bool& sp) {
   switch (wt) {
     case PDM_F32: return pick_ot<PDM_F32>(ot, vb, nc, multi, lpb, sp);
@@ -918,6 +1086,38 @@ extern "C" int pdm_tbe_pooled_fwd(pdm_tbe_plan plan, const void* weights, const 
     const bool multi = num_indices <= 2 * T * batch_size;
     bool short_path = false;
     KernelFn fn = nullptr;
+    if (!multi && (int64_t)g.count * batch_size <= staged_max_bags()) {
+      if (KernelFn st = pick_staged(g.dtype, out_dtype, payload)) {
+        const int slpb = payload / 16, bpw = 256 / slpb;
+        const int64_t store_bytes = std::min<int64_t>(16, (int64_t)(g.dtype == PDM_F32 ? 4 : 8) * osize);
+        TbeArgs a{};
+        a.weights = reinterpret_cast<const char*>(weights);
+        a.indices = indices;
+        a.offsets = offsets;
+        a.meta = plan->d_meta;
+        a.group_tables = plan->d_group_tables + g.first;
+        a.table_base = g.table_base;
+        a.out = out;
+        a.err = err_flag;
+        a.num_indices = num_indices;
+        a.B = batch_size;
+        a.chunks_per_table = (batch_size + bpw - 1) / bpw;
+        a.group_count = g.count;
+        a.num_groups = (int64_t)g.count * a.chunks_per_table;
+        a.padding_idx = padding_idx;
+        a.out_stride = out_row_stride;
+        a.lpb_shift = 0;
+        a.payload_vecs = slpb;
+        a.out_vec_ok = pow2_align((int64_t)(uintptr_t)out) >= store_bytes &&
+                       pow2_align(out_row_stride * osize) >= store_bytes &&
+                       pow2_align((int64_t)g.out_col_align * osize) >= store_bytes;
+        a.index_bits = index_bits;
+        PDM_CHECK_ARG(a.num_groups < (int64_t(1) << 31), "too many bags for one launch");
+        hipLaunchKernelGGL(st, dim3((unsigned)a.num_groups), dim3(256), 0, reinterpret_cast<hipStream_t>(stream), a);
+        PDM_CHECK_LAUNCH();
+        continue;
+      }
+    }
     if (multi) {
       int svb = 0, slpb = 0, snc = 0;
       if ((fn = pick_short_kernel(g.dtype, out_dtype, payload, osize, svb, slpb, snc)) != nullptr) {

@@ -61,6 +61,15 @@ def _run(pdm, dev, flat_dev, host, slots, indices, offsets, B, out_dtype="fp32",
     return got_np, want, int(err.item()), bad
 
 
+@pytest.fixture(params=["staged", "lane-group"])
+def tbe_path(request, monkeypatch):
+    """Launches of multi-id bags up to PDM_TBE_STAGED_MAX_BAGS bags take the LDS-staged kernel; 0 forces the
+    lane-group kernel that larger launches use, so both run on the same small cases."""
+    if request.param == "lane-group":
+        monkeypatch.setenv("PDM_TBE_STAGED_MAX_BAGS", "0")
+    return request.param
+
+
 def _assert_bits(got, want):
     if got.dtype == np.float32:
         mism = got.view(np.uint32) != want.view(np.uint32)
@@ -72,7 +81,7 @@ def _assert_bits(got, want):
 @pytest.mark.parametrize("dtype", ["fp32", "fp16", "bf16", "int8"])
 @pytest.mark.parametrize("pooling", ["sum", "mean"])
 @pytest.mark.parametrize("out_dtype", ["fp32", "fp16", "bf16"])
-def test_pooled_dtypes_bitexact(pdm, dev, dtype, pooling, out_dtype):
+def test_pooled_dtypes_bitexact(pdm, dev, dtype, pooling, out_dtype, tbe_path):
     g = np.random.default_rng(11)
     specs = [(1000, 64, dtype, pooling), (333, 128, dtype, pooling), (97, 16, dtype, pooling)]
     flat, host, slots = _make_tables(g, specs, dev)
@@ -87,7 +96,7 @@ def test_pooled_dtypes_bitexact(pdm, dev, dtype, pooling, out_dtype):
 
 @pytest.mark.parametrize("dim", [4, 8, 12, 20, 36, 256, 512, 1024])
 @pytest.mark.parametrize("dtype", ["fp32", "bf16"])
-def test_pooled_dims(pdm, dev, dim, dtype):
+def test_pooled_dims(pdm, dev, dim, dtype, tbe_path):
     g = np.random.default_rng(dim)
     specs = [(200, dim, dtype, "sum"), (300, dim, dtype, "mean")]
     flat, host, slots = _make_tables(g, specs, dev)
@@ -100,7 +109,7 @@ def test_pooled_dims(pdm, dev, dim, dtype):
 
 
 @pytest.mark.parametrize("index_dtype", [np.int32, np.int64])
-def test_pooled_padding_long_bags_and_empty(pdm, dev, index_dtype):
+def test_pooled_padding_long_bags_and_empty(pdm, dev, index_dtype, tbe_path):
     g = np.random.default_rng(5)
     specs = [(500, 64, "fp32", "mean"), (500, 128, "bf16", "sum")]
     flat, host, slots = _make_tables(g, specs, dev)
@@ -115,7 +124,7 @@ def test_pooled_padding_long_bags_and_empty(pdm, dev, index_dtype):
     assert err == 0 and bad == 0
 
 
-def test_pooled_invalid_ids_and_offsets_flagged(pdm, dev):
+def test_pooled_invalid_ids_and_offsets_flagged(pdm, dev, tbe_path):
     g = np.random.default_rng(6)
     specs = [(50, 32, "fp32", "sum")]
     flat, host, slots = _make_tables(g, specs, dev)
@@ -128,6 +137,37 @@ def test_pooled_invalid_ids_and_offsets_flagged(pdm, dev):
     got, want, err, bad = _run(pdm, dev, flat, host, slots, idx, off, 3)
     _assert_bits(got, want)
     assert err == 1 and bad >= 2
+
+
+@pytest.mark.parametrize("lpb_case", [("fp32", 16), ("fp32", 32), ("fp32", 64), ("bf16", 32), ("fp16", 64),
+                                      ("bf16", 128)])
+@pytest.mark.parametrize("pooling", ["sum", "mean"])
+def test_pooled_staged_rounds_bitexact(pdm, dev, lpb_case, pooling):
+    """The staged kernel (rows of 64, 128 and 256 bytes: 4, 8 or 16 lanes per bag): workgroups whose ids
+    span several rounds (bags of up to 1,500 ids), empty bags, padding and out-of-range ids, a batch that is
+    not a multiple of the bags per workgroup, and a workgroup with a backwards bag (pooled bag by bag)."""
+    dtype, dim = lpb_case
+    g = np.random.default_rng(dim + len(pooling))
+    specs = [(3000, dim, dtype, pooling), (700, dim, dtype, pooling)]
+    flat, host, slots = _make_tables(g, specs, dev)
+    B = 101
+    lens = g.integers(0, 40, 2 * B)
+    lens[3] = 1500
+    lens[B + 7] = 600
+    lens[10:14] = 0
+    idx = np.concatenate([g.integers(0, specs[t][0], lens[t * B:(t + 1) * B].sum()) for t in range(2)])
+    idx[g.random(idx.size) < 0.05] = 9  # padding id
+    idx[g.choice(idx.size, 4, replace=False)] = 10 ** 6
+    for out_dtype in ("fp32", "bf16"):
+        got, want, err, bad = _run(pdm, dev, flat, host, slots, idx, o.offsets_np(lens), B, out_dtype=out_dtype,
+                                   padding_idx=9)
+        _assert_bits(got, want)
+        assert err == 1 and bad == 4
+    off = o.offsets_np(lens)
+    off[B + 40] = off[B + 42] + 3  # bag B + 39 ends past bag B + 40's end: ranges run backwards there
+    got, want, err, bad = _run(pdm, dev, flat, host, slots, idx, off, B, padding_idx=9)
+    _assert_bits(got, want)
+    assert err == 1
 
 
 def test_pooled_misaligned_weights_base_uses_narrow_loads(pdm, dev):
@@ -234,7 +274,7 @@ def test_int8_quantizer_bitexact(pdm, dev):
         assert np.array_equal(got, want), f"dim {dim}: {(got != want).sum()} bytes differ"
 
 
-def test_workload_ebc_fp32_full_size_bitexact(pdm, dev):
+def test_workload_ebc_fp32_full_size_bitexact(pdm, dev, tbe_path):
     import primus_dlrm_amd.synthetic as syn
     w = syn.ebc_fp32()
     g = np.random.default_rng(1001)
