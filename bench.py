@@ -916,14 +916,14 @@ def onetrans_config(w, alg, causal):
             "gflop_per_step": round(alg / 1e9, 1), "causal_gflop_per_step": round(causal / 1e9, 1)}
 
 
-ONETRANS_CPU_BATCH = 16
+ONETRANS_CPU_BATCH = 1024
 
 
 def onetrans_cpu_baseline(torch, w, threads: int):
     sec, reps = cpu_onetrans(torch, w, threads, ONETRANS_CPU_BATCH)
     return cpu_result(ONETRANS_CPU_BATCH / sec, "samples/s", threads, "torch fp32 OneTransBlock x4 (Linear, einsum, "
                       "SDPA with the bool pyramid mask, RMSNorm, GELU)",
-                      f"the 4-layer stack at batch {ONETRANS_CPU_BATCH}", sec, reps)
+                      f"the 4-layer stack on the full batch of {ONETRANS_CPU_BATCH} samples", sec, reps)
 
 
 def block_leg(pdm, torch, dev, stream, args, threads: int):
@@ -1028,13 +1028,13 @@ def main() -> int:
                "out": [w.batch, S, TOK_D], "mlp_gflop_per_step": round(flops / 1e9, 2),
                "timed": "whole fused call (list build, MLP over kept events, padding fill)"}
         cfg["unfused_same_gpu_ms"] = round(unfused_tokenize_ms(pdm, torch, keep, w), 4)
-        cpu_b = 256
+        cpu_b = w.batch
 
         def cpu_fn():
             sec, reps = cpu_tokenize(torch, w, threads, cpu_b)
             return cpu_result(cpu_b * S / sec, unit, threads, "torch fp32: padded lookups + cat, per pool "
                               "Linear / GELU / Linear + pos_emb (SequentialTokenizer), cat",
-                              f"the first {cpu_b} samples ({cpu_b * S} slots) on full-size fp32 tables", sec, reps)
+                              f"the full batch of {cpu_b} samples ({cpu_b * S} slots) on full-size fp32 tables", sec, reps)
     elif args.workload == "ns_tokenize":
         B_ = 1024
         step, alg, K_, N_, keep = setup_ns(pdm, torch, dev, B_)
@@ -1066,7 +1066,7 @@ def main() -> int:
         alg, units, unit, bound, dtype = n_rows * 24, n_rows, "hashes/s", "hbm", "int64"
         cfg = {"workload": "cross_hash_uid_x_artist_16m", "rows": n_rows, "keys": 2, "table_size": table_size,
                "salt": 0}
-        cpu_rows = 200_000
+        cpu_rows = 1 << 22
 
         def cpu_fn():
             sec, reps, path = cpu_cross_hash(uid[:cpu_rows], artist[:cpu_rows], table_size)
