@@ -1098,7 +1098,7 @@ def main() -> int:
                "distinct_rows": distinct, "pad": "row0 (pad slots update row 0, as the reference's pad id 0)",
                "optimizer": "adam", "lr": 0.01, "eps": 1e-8, "weight_decay": 1e-5,
                "timed": "whole fused gather backward"}
-        cpu_b, cpu_cap = 256, 1_000_000
+        cpu_b, cpu_cap = w.batch, 1_000_000
 
         def cpu_fn():
             n, sec, reps = cpu_train_seq(torch, w, cpu_b, cpu_cap, threads)
