@@ -133,7 +133,6 @@ struct GemmArgs {
   const uint16_t* W2_ns;  // [n_ns, D, F]
   const uint16_t* bias;   // EPI_BIAS_*: bf16 [N]
   const uint16_t* Wo;     // FFN with the out-projection in front: Wout [D, D], shared by every token
-  int stagger;            // persistent FFN: start delay of the second half of the grid, in units of 8192 cycles
 };
 
 // Stores one GEMM output element (b, t, n) with the epilogue EPI.
@@ -866,12 +865,7 @@ __global__ __launch_bounds__(NW * 64, WPS) void ffn_kernel(GemmArgs a) {
   const int nchunks = F / 32;
   constexpr unsigned kWaitDma = 0x0F70u | (unsigned)((PF - 1) * (L1 + L2));
   static_assert((PF - 1) * (L1 + L2) < 16, "vmcnt immediate");
-  // Persistent: the workgroup walks the row tiles blockIdx.x, blockIdx.x + gridDim.x, ...  With a.stagger, the
-  // second half of the grid (the second workgroup of each CU when the dispatcher fills the CUs in order) starts
-  // a.stagger * 8192 cycles later, so the two workgroups of a CU do not wait for their tiles' first rows and
-  // residuals at the same time: one's memory-bound prologue then runs beside the other's MFMAs.
-  if (a.stagger > 0 && (int)blockIdx.x >= (int)(gridDim.x / 2))
-    for (int i = 0; i < a.stagger; ++i) __builtin_amdgcn_s_sleep(127);
+  // Persistent: the workgroup walks the row tiles blockIdx.x, blockIdx.x + gridDim.x, ...
   for (int mt_run = blockIdx.x; mt_run < a.total_blocks; mt_run += gridDim.x) {
   const int mt = ns_tile_xcd_major(a, mt_run);
   // The lane's LDS and global offsets below derive from an opaque copy of the lane index taken per tile, so
@@ -1718,13 +1712,9 @@ static int launch_rowgemm(GemmArgs& g, int D, hipStream_t s) {
 #ifndef PDM_FFN_OPROJ
 #define PDM_FFN_OPROJ 1
 #endif
-// The FFN grid is persistent (WPS workgroups per CU walk the row tiles; 0: one workgroup per tile), and with
-// PDM_FFN_STAGGER > 0 the second half of the grid starts that many 8192-cycle units later.
+// The FFN grid is persistent (WPS workgroups per CU walk the row tiles; 0: one workgroup per tile).
 #ifndef PDM_FFN_PERSIST
 #define PDM_FFN_PERSIST 1
-#endif
-#ifndef PDM_FFN_STAGGER
-#define PDM_FFN_STAGGER 0
 #endif
 template <bool OPROJ>
 static int launch_ffn(GemmArgs& g, int D, hipStream_t s) {
@@ -1734,7 +1724,6 @@ static int launch_ffn(GemmArgs& g, int D, hipStream_t s) {
   PDM_CHECK_ARG(tiles < (int64_t(1) << 31), "FFN grid too large");
   g.total_blocks = tiles;
   int64_t grid = tiles;
-  g.stagger = 0;
   if (PDM_FFN_PERSIST) {
     static std::once_flag once[64];
     static hipError_t err[64];
@@ -1745,7 +1734,6 @@ static int launch_ffn(GemmArgs& g, int D, hipStream_t s) {
     std::call_once(once[dev], [&] { err[dev] = hipDeviceGetAttribute(&ncu[dev], hipDeviceAttributeMultiprocessorCount, dev); });
     PDM_CHECK_HIP(err[dev]);
     grid = std::min<int64_t>(tiles, (int64_t)std::max(ncu[dev], 1) * WPS);
-    g.stagger = grid == (int64_t)std::max(ncu[dev], 1) * WPS ? PDM_FFN_STAGGER : 0;
   }
   if (D == 256) hipLaunchKernelGGL((ffn_kernel<256, RB, NW, NST, WPS, OPROJ>), dim3((unsigned)grid), dim3(NW * 64), 0, s, g);
   else hipLaunchKernelGGL((ffn_kernel<128, RB, NW, NST, WPS, OPROJ>), dim3((unsigned)grid), dim3(NW * 64), 0, s, g);
