@@ -17,13 +17,17 @@
 //                        tokens in sample order (output slot and the validated
 //                        row id of every feature).
 //   3. tok_mlp_kernel    persistent workgroups of 8 waves take passes of 128
-//                        list entries (entry 0 of a pool is its padding
-//                        token) from an atomic counter; Linear -> GELU ->
-//                        Linear on bf16 MFMAs; token rows written (the padding
-//                        token's row goes to the workspace).
-//   4. tok_fill_kernel   a workgroup per (pool, sample): its run of padding
-//                        slots gets the pool's padding row + pos[l]; every
-//                        slot gets its mask byte.
+//                        list entries from an atomic counter; Linear -> GELU
+//                        -> Linear on bf16 MFMAs; token rows written.
+//   4. tok_pad_kernel    a workgroup per pool: the padding token's row (the
+//                        MLP of row 0 of every table, or of zeros).
+//   5. tok_fill_kernel   a few persistent workgroups: every padding slot gets
+//                        its pool's padding row + pos[l]; every slot gets its
+//                        mask byte.
+// Kernels 4 and 5 run on a second stream beside 2 and 3 (forked after the
+// scan, joined at the end): the fill is bound by memory writes, the MLP by
+// MFMA and LDS work, so the fill's workgroups take a few CUs and the MLP's
+// persistent grid the others.
 #include <algorithm>
 #include <mutex>
 
@@ -63,7 +67,7 @@ struct TokArgs {
   uint8_t* mask;
   int32_t* err;
   // workspace
-  uint32_t* counter;  // next pass of the MLP kernel
+  uint32_t* counter;  // [0]: next pass of the MLP kernel, [1]: next item of the fill kernel
   int32_t* cnt;       // [P][B + 1] exclusive scan of n_b
   int32_t* tok_slot;  // pool p's list at B * soff[p]: b * L + l
   int32_t* tok_id;    // [F][B * S]: row of feature f of each entry, -1 for an id outside the table
@@ -173,7 +177,7 @@ __device__ __forceinline__ u32x4_t bias_gelu_pack8(const f32x4_t& u0, const f32x
 
 // One pass's list entries as seen by a thread of the first kTokRows.
 struct TokEntry {
-  int sl;  // slot b * L + l; -1: no entry, -2: the pool's padding token
+  int sl;  // slot b * L + l; -1: no entry
   int id[kTokMaxFeatures];  // row per feature, -1: zeros
 };
 
@@ -261,7 +265,7 @@ __global__ __launch_bounds__(kTokNW * 64, 1) void tok_mlp_kernel(TokArgs a) {
       s_np[p] = np;
       const int tot = a.cnt[(int64_t)p * (a.B + 1) + a.B];
       s_tot[p] = tot;
-      np += a.lmax[p] > 0 ? (tot + 1 + ROWS - 1) / ROWS : 0;
+      np += a.lmax[p] > 0 ? (tot + ROWS - 1) / ROWS : 0;
     }
     s_np[a.P] = np;
     s_q[0] = (int)atomicAdd(a.counter, 1u);
@@ -292,12 +296,8 @@ __global__ __launch_bounds__(kTokNW * 64, 1) void tok_mlp_kernel(TokArgs a) {
     en.sl = -1;
 #pragma unroll
     for (int f = 0; f < kTokMaxFeatures; ++f) en.id[f] = -1;
-    if (i == 0) {
-      en.sl = -2;
-#pragma unroll
-      for (int f = 0; f < kTokMaxFeatures; ++f) en.id[f] = a.pad_zero ? -1 : 0;
-    } else if (i - 1 < s_tot[p]) {
-      const int64_t base = a.B * a.soff[p] + (i - 1);
+    if (i < s_tot[p]) {
+      const int64_t base = a.B * a.soff[p] + i;
       en.sl = a.tok_slot[base];
 #pragma unroll
       for (int f = 0; f < kTokMaxFeatures; ++f)
@@ -311,7 +311,7 @@ __global__ __launch_bounds__(kTokNW * 64, 1) void tok_mlp_kernel(TokArgs a) {
       else if (t < D / 4) *reinterpret_cast<u32x4_t*>(&s_b2[buf][(t - D / 8) * 8]) = bias_piece;
       return;
     }
-    int64_t o = en.sl == -2 ? -2 : -1;
+    int64_t o = -1;
     int l = 0;
     if (en.sl >= 0) {
       const int L = a.lmax[p];
@@ -448,7 +448,6 @@ __global__ __launch_bounds__(kTokNW * 64, 1) void tok_mlp_kernel(TokArgs a) {
     }
 
     const float* pos = a.pos[p];
-    float* ypad = a.y_pad + (int64_t)p * D;
     char* stage = sStage + wave * (16 * SROW);
 #pragma unroll
     for (int h = 0; h < NH; ++h) {
@@ -520,12 +519,8 @@ __global__ __launch_bounds__(kTokNW * 64, 1) void tok_mlp_kernel(TokArgs a) {
           if (o == -1) continue;
           const int col = col0 + c4 * 4;
           const f32x4_t v = *reinterpret_cast<const f32x4_t*>(stage + r * SROW + c4 * 16);
-          if (o == -2) {
-            *reinterpret_cast<f32x4_t*>(ypad + col) = v;
-          } else {
-            const f32x4_t w = {v.x + pe[sq][it].x, v.y + pe[sq][it].y, v.z + pe[sq][it].z, v.w + pe[sq][it].w};
-            __builtin_nontemporal_store(w, reinterpret_cast<f32x4_t*>(a.out + o + col));
-          }
+          const f32x4_t w = {v.x + pe[sq][it].x, v.y + pe[sq][it].y, v.z + pe[sq][it].z, v.w + pe[sq][it].w};
+          __builtin_nontemporal_store(w, reinterpret_cast<f32x4_t*>(a.out + o + col));
         }
       }
     }
@@ -539,40 +534,170 @@ __global__ __launch_bounds__(kTokNW * 64, 1) void tok_mlp_kernel(TokArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// 4. A workgroup per (pool, sample): the run of padding slots (positions
-//    [0, L - n) right aligned, [n, L) left aligned) is contiguous in out and
-//    gets the pool's padding row + pos[l]; the L mask bytes are written.
+// 4. The padding token of each pool (a workgroup per pool): its raw row (row 0
+//    of every table, or zeros) through the pool's MLP with the MLP kernel's
+//    rounding points (bf16 after the Linear 1 bias, bf16 GELU, bf16 after the
+//    Linear 2 bias).  A thread per hidden unit, then per output, reads its
+//    weight row in 16-byte pieces, all requested before the first is used, and
+//    sums in fp32 (the bf16 products are exact in fp32).
 // ---------------------------------------------------------------------------
-template <int D>
-__global__ __launch_bounds__(256) void tok_fill_kernel(TokArgs a) {
-  const int64_t w = blockIdx.x;
-  const int p = (int)(w / a.B);
-  const int64_t b = w - p * a.B;
-  const int L = a.lmax[p];
-  if (L == 0) return;
-  const int32_t* cnt = a.cnt + (int64_t)p * (a.B + 1);
-  const int n = cnt[b + 1] - cnt[b];
-  const int l0 = a.align_left ? n : 0;
-  const int s0 = a.soff[p];
-  if (a.mask) {
-    for (int t = threadIdx.x; t < L; t += 256) {
-      const bool real = a.align_left ? t < n : t >= L - n;
-      a.mask[b * a.S + s0 + t] = real ? 1 : 0;
+constexpr int kPadThreads = 512;
+
+__device__ __forceinline__ float bf16_at(const uint16_t* p, int64_t i) { return __uint_as_float((uint32_t)p[i] << 16); }
+
+// dot of the bf16 row w[0 .. N) with the fp32 vector x (LDS), 8 columns per 16-byte piece
+template <int N>
+__device__ __forceinline__ float dot_bf16_row(const uint16_t* __restrict__ w, const float* x) {
+  u32x4_t pc[N / 8];
+#pragma unroll
+  for (int c = 0; c < N / 8; ++c) pc[c] = *reinterpret_cast<const u32x4_t*>(w + c * 8);
+  float acc = 0.0f;
+#pragma unroll
+  for (int c = 0; c < N / 8; ++c) {
+    const uint32_t wd[4] = {pc[c].x, pc[c].y, pc[c].z, pc[c].w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      acc = __builtin_fmaf(x[c * 8 + 2 * e], __uint_as_float(wd[e] << 16), acc);
+      acc = __builtin_fmaf(x[c * 8 + 2 * e + 1], __uint_as_float(wd[e] & 0xffff0000u), acc);
     }
   }
-  const float* pos = a.pos[p];
-  const float* yp = a.y_pad + (int64_t)p * D;
-  float* dst = a.out + b * a.out_bstride + (int64_t)(s0 + l0) * D;
-  constexpr int PR = D / 4;  // 16-byte pieces per row
-  const int pieces = (L - n) * PR;
-  for (int k = threadIdx.x; k < pieces; k += 256) {
-    const int i = k / PR, c = (k - i * PR) * 4;
-    f32x4_t v = *reinterpret_cast<const f32x4_t*>(yp + c);
-    if (pos) {
-      const f32x4_t pe = *reinterpret_cast<const f32x4_t*>(pos + (int64_t)(l0 + i) * D + c);
-      v = f32x4_t{v.x + pe.x, v.y + pe.y, v.z + pe.z, v.w + pe.w};
+  return acc;
+}
+
+template <int K, int D, bool F32>
+__global__ __launch_bounds__(kPadThreads) void tok_pad_kernel(TokArgs a) {
+  static_assert(D <= kPadThreads && K % 8 == 0 && D % 8 == 0, "a thread per hidden unit and output");
+  __shared__ __attribute__((aligned(16))) float s_raw[K];
+  __shared__ __attribute__((aligned(16))) float s_g[D];
+  const int p = blockIdx.x;
+  const int tid = threadIdx.x;
+  if (p == 0 && tid == 0) a.counter[1] = 0u;  // the fill kernel runs after this one, on the same stream
+  if (a.lmax[p] == 0) return;
+  for (int k = tid; k < K; k += kPadThreads) {
+    float v = 0.0f;
+    if (!a.pad_zero) {
+      int f = 0;
+      while (f + 1 < a.F && k >= a.col[f + 1]) ++f;
+      const int c = k - a.col[f];
+      v = F32 ? bf16_round(reinterpret_cast<const float*>(a.tables[f])[c])
+              : bf16_at(reinterpret_cast<const uint16_t*>(a.tables[f]), c);
     }
-    __builtin_nontemporal_store(v, reinterpret_cast<f32x4_t*>(dst + (int64_t)i * D + c));
+    s_raw[k] = v;
+  }
+  __syncthreads();
+  if (tid < D) {
+    const float u = dot_bf16_row<K>(a.w1[p] + (int64_t)tid * K, s_raw);
+    s_g[tid] = bf16_round(gelu_erf(bf16_round(u + bf16_at(a.b1[p], tid))));
+  }
+  __syncthreads();
+  if (tid < D) {
+    const float y = dot_bf16_row<D>(a.w2[p] + (int64_t)tid * D, s_g);
+    a.y_pad[(int64_t)p * D + tid] = bf16_round(y + bf16_at(a.b2[p], tid));
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 5. The padding slots and the mask.  The rows to write depend only on (pool,
+//    slot): the pool's padding row + pos[l].  An item is (pool, 32 slots, 64
+//    samples): the workgroup stages its 32 rows in LDS once and writes them to
+//    every sample of the item whose padding run ([0, L - n) right aligned,
+//    [n, L) left aligned) covers them, with non-temporal stores; the items of
+//    the first 32 slots also write their samples' L mask bytes.  A persistent
+//    grid of a few workgroups takes the items (pool-major, then slot chunk,
+//    then sample chunk) from an atomic counter, so the fill occupies only
+//    those CUs and a workgroup that shares its CU takes fewer items.
+// ---------------------------------------------------------------------------
+constexpr int kFillSamples = 64;
+constexpr int kFillThreads = 1024;
+constexpr int kFillRows = 32;  // a thread holds D / 128 pieces of the item's rows
+
+__host__ __device__ inline int64_t fill_items_of_pool(int L, int64_t B) {
+  return (int64_t)((L + kFillRows - 1) / kFillRows) * ((B + kFillSamples - 1) / kFillSamples);
+}
+
+template <int D>
+__global__ __launch_bounds__(kFillThreads) void tok_fill_kernel(TokArgs a) {
+  constexpr int PR = D / 4;                                // 16-byte pieces per row
+  constexpr int PPT = kFillRows * PR / kFillThreads;       // pieces of the item's rows per thread
+  static_assert(PPT * kFillThreads == kFillRows * PR && kFillSamples == 64, "fill item shape");
+  __shared__ __attribute__((aligned(16))) float s_t[kFillRows * D];
+  __shared__ int s_n[kFillSamples];
+  __shared__ uint64_t s_pad[kFillRows];  // bit sm: slot l0 + r is padding for sample b0 + sm
+  __shared__ uint32_t s_item;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t nbc = (a.B + kFillSamples - 1) / kFillSamples;
+  for (;;) {
+    if (tid == 0) s_item = atomicAdd(a.counter + 1, 1u);
+    __syncthreads();  // also: the previous item's rows and masks are read
+    const int64_t it = s_item;
+    int p = 0;
+    int64_t r = it;
+    for (; p < a.P; ++p) {
+      const int64_t n = fill_items_of_pool(a.lmax[p], a.B);
+      if (r < n) break;
+      r -= n;
+    }
+    if (p >= a.P) break;  // uniform
+    const int L = a.lmax[p];
+    const int lc = (int)(r / nbc);
+    const int64_t b0 = (r - lc * nbc) * kFillSamples;
+    const int l0 = lc * kFillRows, nr = min(kFillRows, L - l0);
+    const int nb = (int)min<int64_t>(kFillSamples, a.B - b0);
+    const float* pos = a.pos[p];
+    const float* yp = a.y_pad + (int64_t)p * D;
+    for (int k = tid; k < nr * PR; k += kFillThreads) {
+      const int rr = k / PR, c = (k - rr * PR) * 4;
+      f32x4_t v = *reinterpret_cast<const f32x4_t*>(yp + c);
+      if (pos) {
+        const f32x4_t pe = *reinterpret_cast<const f32x4_t*>(pos + (int64_t)(l0 + rr) * D + c);
+        v = f32x4_t{v.x + pe.x, v.y + pe.y, v.z + pe.z, v.w + pe.w};
+      }
+      *reinterpret_cast<f32x4_t*>(s_t + rr * D + c) = v;
+    }
+    const int32_t* cnt = a.cnt + (int64_t)p * (a.B + 1);
+    if (tid < nb) s_n[tid] = cnt[b0 + tid + 1] - cnt[b0 + tid];
+    __syncthreads();
+    // per slot, the samples it pads: lane = sample
+    for (int rr = wave; rr < kFillRows; rr += kFillThreads / 64) {
+      const int l = l0 + rr;
+      bool pad = false;
+      if (rr < nr && lane < nb) {
+        const int n = s_n[lane];
+        pad = a.align_left ? l >= n : l < L - n;
+      }
+      const uint64_t m = __ballot(pad);
+      if (lane == 0) s_pad[rr] = m;
+    }
+    const int s0 = a.soff[p];
+    if (lc == 0 && a.mask) {
+      for (int k = tid; k < nb * L; k += kFillThreads) {
+        const int sm = k / L, t = k - sm * L;
+        const int n = s_n[sm];
+        const bool real = a.align_left ? t < n : t >= L - n;
+        a.mask[(b0 + sm) * a.S + s0 + t] = real ? 1 : 0;
+      }
+    }
+    __syncthreads();
+    // each thread keeps its PPT pieces of the item's rows in registers and stores them to every sample the
+    // slot pads: the loop has stores only, no memory waits
+    f32x4_t v[PPT];
+    uint64_t m[PPT];
+    int64_t off[PPT];
+#pragma unroll
+    for (int j = 0; j < PPT; ++j) {
+      const int pi = j * kFillThreads + tid;
+      const int rr = pi / PR, c = (pi - rr * PR) * 4;
+      v[j] = *reinterpret_cast<const f32x4_t*>(s_t + rr * D + c);
+      m[j] = s_pad[rr];  // 0 for rows past the pool's end
+      off[j] = (int64_t)(s0 + l0 + rr) * D + c;
+    }
+    float* dst = a.out + b0 * a.out_bstride;
+    for (int sm = 0; sm < nb; ++sm) {
+#pragma unroll
+      for (int j = 0; j < PPT; ++j)
+        if ((m[j] >> sm) & 1u) __builtin_nontemporal_store(v[j], reinterpret_cast<f32x4_t*>(dst + off[j]));
+      dst += a.out_bstride;
+    }
   }
 }
 
@@ -601,6 +726,54 @@ TokLayout tok_layout(int64_t P, int64_t F, int64_t B, int64_t S, int64_t D) {
 
 using MlpFn = void (*)(TokArgs);
 
+// Workgroups of the fill kernel alone (no side stream).  Beside the MLP it takes one CU in eight, a
+// multiple of 8: workgroups go to the 8 XCDs in turn, so the MLP's grid leaves each XCD as many free CUs as
+// the fill places there.
+constexpr int kFillWgsAlone = 1024;
+inline int fill_wgs_beside(int ncus) { return std::max(8, ncus / 64 * 8); }
+
+// The library's second stream on one device (default priority, non-blocking) and a ring of fork / join
+// event pairs: a call records the next pair, so an event is recorded again only kSideEvents calls later,
+// long after its last wait.
+constexpr int kSideEvents = 16;
+struct SideStream {
+  hipStream_t s = nullptr;
+  hipEvent_t fork[kSideEvents] = {}, join[kSideEvents] = {};
+  int next = 0;
+  bool failed = false;
+};
+std::mutex g_side_mu;
+SideStream g_side[64];
+
+// The side stream of device dev, created on first use outside a stream capture; nullptr when it cannot be
+// made (then every kernel runs on the caller's stream).  Called with g_side_mu held.
+SideStream* side_stream(int dev, hipStream_t caller) {
+  SideStream& ss = g_side[dev];
+  if (ss.s) return &ss;
+  if (ss.failed) return nullptr;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(caller, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return nullptr;
+  bool ok = hipStreamCreateWithFlags(&ss.s, hipStreamNonBlocking) == hipSuccess;
+  for (int i = 0; ok && i < kSideEvents; ++i)
+    ok = hipEventCreateWithFlags(&ss.fork[i], hipEventDisableTiming) == hipSuccess &&
+         hipEventCreateWithFlags(&ss.join[i], hipEventDisableTiming) == hipSuccess;
+  if (!ok) {
+    for (int i = 0; i < kSideEvents; ++i) {
+      if (ss.fork[i]) (void)hipEventDestroy(ss.fork[i]);
+      if (ss.join[i]) (void)hipEventDestroy(ss.join[i]);
+      ss.fork[i] = ss.join[i] = nullptr;
+    }
+    if (ss.s) (void)hipStreamDestroy(ss.s);
+    ss.s = nullptr;
+    (void)hipGetLastError();
+    ss.failed = true;
+    return nullptr;
+  }
+  return &ss;
+}
+
+using FillFn = void (*)(TokArgs);
+
 template <int D, bool F32>
 MlpFn pick_mlp_k(int K) {
   switch (K) {
@@ -610,6 +783,23 @@ MlpFn pick_mlp_k(int K) {
     case 384: return tok_mlp_kernel<384, D, F32>;
     default: return nullptr;
   }
+}
+
+template <int D, bool F32>
+MlpFn pick_pad_k(int K) {
+  switch (K) {
+    case 128: return tok_pad_kernel<128, D, F32>;
+    case 192: return tok_pad_kernel<192, D, F32>;
+    case 256: return tok_pad_kernel<256, D, F32>;
+    case 384: return tok_pad_kernel<384, D, F32>;
+    default: return nullptr;
+  }
+}
+
+MlpFn pick_pad(int K, int D, bool f32) {
+  if (D == 384) return f32 ? pick_pad_k<384, true>(K) : pick_pad_k<384, false>(K);
+  if (D == 256) return f32 ? pick_pad_k<256, true>(K) : pick_pad_k<256, false>(K);
+  return f32 ? pick_pad_k<128, true>(K) : pick_pad_k<128, false>(K);
 }
 
 MlpFn pick_mlp(int K, int D, bool f32) {
@@ -745,18 +935,47 @@ extern "C" int pdm_seq_tokenize_fwd(const pdm_seq_desc* desc, const void* const*
   });
   PDM_CHECK_HIP(cu_err[dev]);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(tok_scan_kernel, dim3(a.P), dim3(kScanThreads), 0, s, a);
-  PDM_CHECK_LAUNCH();
   const int64_t pairs = (int64_t)a.P * a.B;
   PDM_CHECK_ARG(pairs < (int64_t(1) << 31), "pools * batch_size too large");
+  FillFn pad = pick_pad(K, d_model, f32);
+  FillFn fill = d_model == 384 ? tok_fill_kernel<384> : d_model == 256 ? tok_fill_kernel<256> : tok_fill_kernel<128>;
+  int64_t fill_items = 0;
+  for (int p = 0; p < a.P; ++p) fill_items += fill_items_of_pool(a.lmax[p], a.B);
+  const int ncus = std::max(ncu[dev], 1);
+  const int fill_beside = fill_wgs_beside(ncus);
+  hipLaunchKernelGGL(tok_scan_kernel, dim3(a.P), dim3(kScanThreads), 0, s, a);
+  PDM_CHECK_LAUNCH();
+  std::lock_guard<std::mutex> lk(g_side_mu);
+  SideStream* side = side_stream(dev, s);
+  const int ev = side ? side->next : 0;
+  if (side) {
+    side->next = (side->next + 1) % kSideEvents;
+    // fork after the scan: the padding rows and the fill on the side stream, the list and the MLP here
+    PDM_CHECK_HIP(hipEventRecord(side->fork[ev], s));
+    PDM_CHECK_HIP(hipStreamWaitEvent(side->s, side->fork[ev], 0));
+    hipLaunchKernelGGL(pad, dim3(a.P), dim3(kPadThreads), 0, side->s, a);
+    PDM_CHECK_LAUNCH();
+    const int64_t fg = std::max<int64_t>(1, std::min<int64_t>(fill_items, fill_beside));
+    hipLaunchKernelGGL(fill, dim3((unsigned)fg), dim3(kFillThreads), 0, side->s, a);
+    PDM_CHECK_LAUNCH();
+    PDM_CHECK_HIP(hipEventRecord(side->join[ev], side->s));
+  } else {
+    hipLaunchKernelGGL(pad, dim3(a.P), dim3(kPadThreads), 0, s, a);
+    PDM_CHECK_LAUNCH();
+  }
   hipLaunchKernelGGL(tok_list_kernel, dim3((unsigned)((pairs + 3) / 4)), dim3(256), 0, s, a);
   PDM_CHECK_LAUNCH();
-  const int64_t grid = std::max<int64_t>(1, std::min<int64_t>(passes_max, std::max(ncu[dev], 1)));
+  // the MLP's persistent grid leaves the fill its CUs (an MLP workgroup fills a CU's registers)
+  const int64_t cus = side ? std::max(ncus - fill_beside, 1) : ncus;
+  const int64_t grid = std::max<int64_t>(1, std::min<int64_t>(passes_max, cus));
   hipLaunchKernelGGL(mlp, dim3((unsigned)grid), dim3(kTokNW * 64), 0, s, a);
   PDM_CHECK_LAUNCH();
-  if (d_model == 384) hipLaunchKernelGGL(tok_fill_kernel<384>, dim3((unsigned)pairs), dim3(256), 0, s, a);
-  else if (d_model == 256) hipLaunchKernelGGL(tok_fill_kernel<256>, dim3((unsigned)pairs), dim3(256), 0, s, a);
-  else hipLaunchKernelGGL(tok_fill_kernel<128>, dim3((unsigned)pairs), dim3(256), 0, s, a);
-  PDM_CHECK_LAUNCH();
+  if (side) {
+    PDM_CHECK_HIP(hipStreamWaitEvent(s, side->join[ev], 0));
+  } else {
+    const int64_t fg = std::max<int64_t>(1, std::min<int64_t>(fill_items, kFillWgsAlone));
+    hipLaunchKernelGGL(fill, dim3((unsigned)fg), dim3(kFillThreads), 0, s, a);
+    PDM_CHECK_LAUNCH();
+  }
   return PDM_OK;
 }

@@ -148,6 +148,44 @@ def test_writes_into_block_input_rows(pdm, dev):
     _check(buf[:, :16].cpu(), tabs, ids, offs, max_len, ws, 0, 0, mask)
 
 
+def test_captured_in_a_graph(pdm, dev):
+    """The padding fill runs on the library's second stream beside the MLP (fork after the scan, join at the
+    end); under HIP graph capture both streams' kernels become nodes of the graph.  Every replay, with eager
+    calls on other inputs in between, must give the eager output bit for bit."""
+    g = np.random.default_rng(21)
+    specs, pools, d = [(900, 256), (90, 64), (120, 64)], [(64, 40), (24, 12), (40, 20)], 256
+    B = 200
+    args = []
+    for seed in (0, 1):
+        tabs, ids, offs = _inputs(np.random.default_rng(seed), B, pools, specs, "bf16")
+        args.append((_dev_tables(tabs, dev), [[torch.from_numpy(a).to(dev) for a in r] for r in ids],
+                     [torch.from_numpy(x).to(dev) for x in offs]))
+    max_len = [L for L, _ in pools]
+    ws = [ot.random_tokenizer_weights(384, d, 64, seed=30 + i) for i in range(3)]
+    wd = [{k: (v.to(torch.bfloat16) if k != "pos" else v).contiguous().to(dev) for k, v in w.items()} for w in ws]
+    out = torch.empty(B, sum(max_len), d, device=dev)
+    other = torch.empty_like(out)
+    work = pdm.ops.seq_tokenize_workspace(*args[0], max_len, d)
+    work2 = torch.empty_like(work)
+    pdm.ops.seq_tokenize_raw(*args[0], max_len, wd, out=out, workspace=work)  # eager first: the side stream exists
+    torch.cuda.synchronize()
+    want = out.clone()
+    out.fill_(-1.0)
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            pdm.ops.seq_tokenize_raw(*args[0], max_len, wd, out=out, workspace=work)
+    torch.cuda.synchronize()
+    for r in range(3):
+        out.fill_(-1.0)
+        pdm.ops.seq_tokenize_raw(*args[1], max_len, wd, out=other, workspace=work2)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), f"replay {r}"
+
+
 def test_bad_ids_and_offsets_raise_the_flag(pdm, dev):
     g = np.random.default_rng(4)
     specs, pools, d = [(100, 64), (30, 64)], [(8, 5)], 128
