@@ -36,6 +36,23 @@ void clear_error();
 // Checks the launch just enqueued; returns PDM_ERR_HIP on a launch error.
 #define PDM_CHECK_LAUNCH() PDM_CHECK_HIP(hipGetLastError())
 
+// ---- the library's second stream ------------------------------------------
+// Work that runs beside the caller's stream inside one entry point: side_fork records an event on the
+// caller's stream and makes the library's second stream of the current device (default priority,
+// non-blocking) wait for it; the entry point launches its side work on f.side; side_join records an event on
+// the side stream and makes the caller's stream wait for it.  Under HIP graph capture the pair brings the
+// side stream into the capture and back.  The side stream is made on a device's first fork outside a
+// stream capture; when it does not exist (first use inside a capture, or it could not be made) f.side is
+// null and the entry point launches everything on the caller's stream.  Fork / join event pairs rotate
+// through a ring, so an event is recorded again only many calls after its last wait.
+struct SideFork {
+  hipStream_t side = nullptr;
+  int dev = 0;
+  int ev = 0;
+};
+int side_fork(hipStream_t caller, SideFork& f);       // PDM_OK or PDM_ERR_HIP (f.side may be null)
+int side_join(hipStream_t caller, const SideFork& f);  // no-op when f.side is null
+
 inline int dtype_size(int dt) {
   switch (dt) {
     case PDM_F32: return 4;

@@ -732,46 +732,6 @@ using MlpFn = void (*)(TokArgs);
 constexpr int kFillWgsAlone = 1024;
 inline int fill_wgs_beside(int ncus) { return std::max(8, ncus / 64 * 8); }
 
-// The library's second stream on one device (default priority, non-blocking) and a ring of fork / join
-// event pairs: a call records the next pair, so an event is recorded again only kSideEvents calls later,
-// long after its last wait.
-constexpr int kSideEvents = 16;
-struct SideStream {
-  hipStream_t s = nullptr;
-  hipEvent_t fork[kSideEvents] = {}, join[kSideEvents] = {};
-  int next = 0;
-  bool failed = false;
-};
-std::mutex g_side_mu;
-SideStream g_side[64];
-
-// The side stream of device dev, created on first use outside a stream capture; nullptr when it cannot be
-// made (then every kernel runs on the caller's stream).  Called with g_side_mu held.
-SideStream* side_stream(int dev, hipStream_t caller) {
-  SideStream& ss = g_side[dev];
-  if (ss.s) return &ss;
-  if (ss.failed) return nullptr;
-  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-  if (hipStreamIsCapturing(caller, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return nullptr;
-  bool ok = hipStreamCreateWithFlags(&ss.s, hipStreamNonBlocking) == hipSuccess;
-  for (int i = 0; ok && i < kSideEvents; ++i)
-    ok = hipEventCreateWithFlags(&ss.fork[i], hipEventDisableTiming) == hipSuccess &&
-         hipEventCreateWithFlags(&ss.join[i], hipEventDisableTiming) == hipSuccess;
-  if (!ok) {
-    for (int i = 0; i < kSideEvents; ++i) {
-      if (ss.fork[i]) (void)hipEventDestroy(ss.fork[i]);
-      if (ss.join[i]) (void)hipEventDestroy(ss.join[i]);
-      ss.fork[i] = ss.join[i] = nullptr;
-    }
-    if (ss.s) (void)hipStreamDestroy(ss.s);
-    ss.s = nullptr;
-    (void)hipGetLastError();
-    ss.failed = true;
-    return nullptr;
-  }
-  return &ss;
-}
-
 using FillFn = void (*)(TokArgs);
 
 template <int D, bool F32>
@@ -945,20 +905,15 @@ extern "C" int pdm_seq_tokenize_fwd(const pdm_seq_desc* desc, const void* const*
   const int fill_beside = fill_wgs_beside(ncus);
   hipLaunchKernelGGL(tok_scan_kernel, dim3(a.P), dim3(kScanThreads), 0, s, a);
   PDM_CHECK_LAUNCH();
-  std::lock_guard<std::mutex> lk(g_side_mu);
-  SideStream* side = side_stream(dev, s);
-  const int ev = side ? side->next : 0;
-  if (side) {
-    side->next = (side->next + 1) % kSideEvents;
-    // fork after the scan: the padding rows and the fill on the side stream, the list and the MLP here
-    PDM_CHECK_HIP(hipEventRecord(side->fork[ev], s));
-    PDM_CHECK_HIP(hipStreamWaitEvent(side->s, side->fork[ev], 0));
-    hipLaunchKernelGGL(pad, dim3(a.P), dim3(kPadThreads), 0, side->s, a);
+  // fork after the scan: the padding rows and the fill on the side stream, the list and the MLP here
+  SideFork side;
+  if (int st = side_fork(s, side)) return st;
+  if (side.side) {
+    hipLaunchKernelGGL(pad, dim3(a.P), dim3(kPadThreads), 0, side.side, a);
     PDM_CHECK_LAUNCH();
     const int64_t fg = std::max<int64_t>(1, std::min<int64_t>(fill_items, fill_beside));
-    hipLaunchKernelGGL(fill, dim3((unsigned)fg), dim3(kFillThreads), 0, side->s, a);
+    hipLaunchKernelGGL(fill, dim3((unsigned)fg), dim3(kFillThreads), 0, side.side, a);
     PDM_CHECK_LAUNCH();
-    PDM_CHECK_HIP(hipEventRecord(side->join[ev], side->s));
   } else {
     hipLaunchKernelGGL(pad, dim3(a.P), dim3(kPadThreads), 0, s, a);
     PDM_CHECK_LAUNCH();
@@ -966,12 +921,12 @@ extern "C" int pdm_seq_tokenize_fwd(const pdm_seq_desc* desc, const void* const*
   hipLaunchKernelGGL(tok_list_kernel, dim3((unsigned)((pairs + 3) / 4)), dim3(256), 0, s, a);
   PDM_CHECK_LAUNCH();
   // the MLP's persistent grid leaves the fill its CUs (an MLP workgroup fills a CU's registers)
-  const int64_t cus = side ? std::max(ncus - fill_beside, 1) : ncus;
+  const int64_t cus = side.side ? std::max(ncus - fill_beside, 1) : ncus;
   const int64_t grid = std::max<int64_t>(1, std::min<int64_t>(passes_max, cus));
   hipLaunchKernelGGL(mlp, dim3((unsigned)grid), dim3(kTokNW * 64), 0, s, a);
   PDM_CHECK_LAUNCH();
-  if (side) {
-    PDM_CHECK_HIP(hipStreamWaitEvent(s, side->join[ev], 0));
+  if (side.side) {
+    if (int st = side_join(s, side)) return st;
   } else {
     const int64_t fg = std::max<int64_t>(1, std::min<int64_t>(fill_items, kFillWgsAlone));
     hipLaunchKernelGGL(fill, dim3((unsigned)fg), dim3(kFillThreads), 0, s, a);
