@@ -306,7 +306,14 @@ int pdm_seq_gather_backward_fused(pdm_tbe_plan plan, const pdm_seq_desc* desc,
  *          optional).  B * S < 2^31.
  * workspace: 256-byte aligned, >= pdm_seq_tokenize_workspace_size(desc,
  *          d_model) bytes; no initialisation needed; calls sharing one
- *          workspace must not overlap. */
+ *          workspace must not overlap.
+ * Streams: the padding rows and the mask are written on the library's own
+ * second stream of the device (default priority), forked from `stream` after
+ * the first kernel and joined back into it before the call returns, so work
+ * queued on `stream` afterwards sees the whole output.  The library makes that
+ * stream on a device's first call outside a stream capture; a first call
+ * inside a capture runs everything on `stream`.  Under HIP graph capture the
+ * fork and join become graph edges. */
 typedef struct {
   const uint16_t* w1;
   const uint16_t* b1;
