@@ -995,7 +995,8 @@ def main() -> int:
         dtype = {"bf16": "bf16->f32", "fp32": "f32", "int8": "u8->f32"}[w.dtype]
         cfg = {"workload": w.name, "tables": w.num_tables, "rows_total": int(sum(w.rows)), "dim": w.dim,
                "batch": w.batch, "lookups_per_batch": w.num_lookups, "pooling": w.pooling,
-               "weights": w.dtype, "out": w.out_dtype, "ids": args.ids}
+               "weights": w.dtype, "out": w.out_dtype,
+               "ids": "uniform" if args.workload == "ebc_fp32" else args.ids}  # the EBC workload's ids are uniform
         if args.workload == "ebc_fp32":
             def graph_fn():
                 return graph_steady_state(torch, dev, step, GRAPH_BATCHES)
