@@ -186,6 +186,65 @@ def test_captured_in_a_graph(pdm, dev):
         assert torch.equal(out, want), f"replay {r}"
 
 
+_FIRST_CALL_CAPTURED = r"""
+import sys
+import numpy as np
+import torch
+sys.path.insert(0, {root!r})
+import __graft_entry__
+pdm = __graft_entry__.pdm_import()
+from oracle import onetrans as ot
+dev = torch.device("cuda:0")
+g = np.random.default_rng(3)
+B, specs, pools, d = 90, [(500, 256), (60, 64), (80, 64)], [(40, 25), (16, 8), (24, 12)], 256
+tabs = [torch.from_numpy(g.normal(0, 0.5, (r, c)).astype(np.float32)).to(torch.bfloat16).to(dev) for r, c in specs]
+ids, offs = [], []
+for L, mean in pools:
+    ln = g.poisson(mean, B)
+    it = g.integers(0, specs[0][0], int(ln.sum()))
+    ids.append([torch.from_numpy(a).to(dev) for a in [it] + [it % r for r, _ in specs[1:]]])
+    offs.append(torch.from_numpy(np.concatenate([[0], np.cumsum(ln)]).astype(np.int64)).to(dev))
+max_len = [L for L, _ in pools]
+ws = [ot.random_tokenizer_weights(384, d, 48, seed=40 + i) for i in range(3)]
+wd = [{{k: (v.to(torch.bfloat16) if k != "pos" else v).contiguous().to(dev) for k, v in w.items()}} for w in ws]
+out = torch.empty(B, sum(max_len), d, device=dev)
+work = pdm.ops.seq_tokenize_workspace(tabs, ids, offs, max_len, d)
+stream = torch.cuda.Stream()
+stream.wait_stream(torch.cuda.current_stream())
+graph = torch.cuda.CUDAGraph()
+with torch.cuda.stream(stream):
+    with torch.cuda.graph(graph, stream=stream):  # the library's first tokenizer call: inside the capture
+        pdm.ops.seq_tokenize_raw(tabs, ids, offs, max_len, wd, out=out, workspace=work)
+torch.cuda.synchronize()
+out.fill_(-1.0)
+graph.replay()
+torch.cuda.synchronize()
+captured = out.clone()
+eager = torch.empty_like(out)
+for _ in range(2):  # eager calls: the first makes the second stream, both use it
+    pdm.ops.seq_tokenize_raw(tabs, ids, offs, max_len, wd, out=eager, workspace=work)
+    torch.cuda.synchronize()
+    assert torch.equal(eager, captured)
+graph.replay()
+torch.cuda.synchronize()
+assert torch.equal(out, captured)
+print("FIRST_CALL_CAPTURED_OK")
+"""
+
+
+def test_first_call_inside_a_capture(dev):
+    """In a fresh process whose first tokenizer call is captured into a graph (before the library has its
+    second stream, which is made outside captures only), the call runs on the capturing stream alone; the
+    eager calls after it make the second stream and give the graph's output bit for bit."""
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, "-c", _FIRST_CALL_CAPTURED.format(root=root)], capture_output=True,
+                       text=True, timeout=240)
+    assert r.returncode == 0 and "FIRST_CALL_CAPTURED_OK" in r.stdout, r.stdout[-2000:] + r.stderr[-2000:]
+
+
 def test_bad_ids_and_offsets_raise_the_flag(pdm, dev):
     g = np.random.default_rng(4)
     specs, pools, d = [(100, 64), (30, 64)], [(8, 5)], 128
