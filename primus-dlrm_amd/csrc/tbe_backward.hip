@@ -12,11 +12,13 @@
 // Design (one stream, no host synchronisation, deterministic):
 //  1. linearise: each lookup becomes a 32-bit row-space key (sentinel for
 //     padding / invalid ids) and an 8-byte record {gradient row, scale};
-//  2. stable LSD radix sort of (key, lookup position), 8 bits per pass over
-//     only the bits the row space needs.  A tile of 4096 keys is ranked per
+//  2. stable LSD radix sort of (key, lookup position), up to 9 bits per pass
+//     over only the bits the row space needs.  A tile of 4096 keys is ranked per
 //     wavefront with ballots (stable: lanes and rounds follow positions),
 //     then staged in LDS in sorted order so the scatter writes contiguous
-//     runs per digit;
+//     runs per digit.  Sentinel keys are not moved: every pass writes the
+//     sorted keys to the front and the sentinel behind them, and later passes
+//     skip the all-sentinel tiles;
 //  3. accumulate: a wavefront owns 64 consecutive sorted entries; lane groups
 //     of D/4 lanes (one float4 of the row per lane) sum the runs of equal keys
 //     in position order and apply the optimizer to the row in registers.  A
@@ -39,7 +41,14 @@ namespace {
 constexpr int kSortThreads = 256;
 constexpr int kSortItems = 16;
 constexpr int kTile = kSortThreads * kSortItems;  // keys per sort tile
-constexpr int kBins = 256;                         // 8-bit digits
+// Digits of up to PDM_SORT_DIGIT_BITS bits: the row space's bits are split evenly over the fewest passes
+// (a 27-bit row space of 80 M rows sorts in 3 passes of 9 bits).
+#ifndef PDM_SORT_DIGIT_BITS
+#define PDM_SORT_DIGIT_BITS 9
+#endif
+constexpr int kDigitBits = PDM_SORT_DIGIT_BITS;
+static_assert(kDigitBits >= 8 && kDigitBits <= 9, "digits of 8 or 9 bits");
+constexpr int kBins = 1 << kDigitBits;
 constexpr int kChunk = 64;                         // sorted entries per accumulating wavefront
 constexpr uint32_t kSentinel = 0xFFFFFFFFu;
 constexpr int kMaxLevels = 6;  // chunk partial sums folded 64 at a time: 64^5 chunks cover any 32-bit key count
@@ -383,28 +392,63 @@ __global__ __launch_bounds__(256) void seq_row0_sum_kernel(Row0Args r) {
 
 // ---- 2. radix sort ---------------------------------------------------------------
 
-// Per-tile digit counts, stored digit-major: hist[d * num_tiles + tile].
+// The sentinel key (padding, invalid ids, and with the sequence layout every row-0 lookup) is left out of the
+// sort: no pass counts, ranks or moves it.  Each pass writes the K sorted non-sentinel keys to positions
+// [0, K) and the sentinel to [K, n_pad) of its output, so the sorted keys end with the sentinel run the later
+// stages expect, and the input of every pass after the first is compacted: a tile whose first key is the
+// sentinel holds nothing else.
+
+// Tile of workgroup b when the tiles that hold keys are the first n (n = num_tiles for the first pass, the
+// tiles below the K sorted keys after it).  Workgroups go to the 8 XCDs in turn (b % 8), so XCD x takes the
+// contiguous tiles x * q + min(x, r) .. of the n = 8 q + r: a digit's runs from consecutive tiles then meet
+// in one XCD's L2, which joins the partial lines at their boundaries, and every XCD has a share of the keys.
+// Workgroups b >= n take tile b (all sentinel).
+__device__ __forceinline__ int64_t sort_tile(int64_t b, int64_t n) {
+  if (b >= n) return b;
+  const int64_t q = n >> 3, r = n & 7, x = b & 7;
+  return x * q + (x < r ? x : r) + (b >> 3);
+}
+
+// Tiles that hold keys: all of them in the first pass, those below the sorted keys' count after it.
+__device__ __forceinline__ int64_t keyed_tiles(int compacted, const uint32_t* nkeys, int64_t num_tiles) {
+  return compacted ? ((int64_t)*nkeys + kTile - 1) / kTile : num_tiles;
+}
+
+// Per-tile digit counts of the non-sentinel keys, stored digit-major: hist[d * num_tiles + tile] for the
+// 2^nbits digits of the pass.
 __global__ __launch_bounds__(kSortThreads) void radix_count_kernel(const uint32_t* __restrict__ keys,
                                                                    uint32_t* __restrict__ hist, int shift,
-                                                                   uint32_t mask, int64_t num_tiles) {
+                                                                   int nbits, int64_t num_tiles, int compacted,
+                                                                   const uint32_t* __restrict__ nkeys) {
   __shared__ uint32_t cnt[4][kBins];
   const int tid = threadIdx.x, w = tid >> 6;
+  const int nbins = 1 << nbits;
+  const uint32_t mask = (uint32_t)nbins - 1u;
+  const int64_t tile = sort_tile(blockIdx.x, keyed_tiles(compacted, nkeys, num_tiles));
+  const uint32_t* tk = keys + tile * kTile;
+  if (compacted && tk[0] == kSentinel) {
+    for (int d = tid; d < nbins; d += kSortThreads) hist[(int64_t)d * num_tiles + tile] = 0;
+    return;
+  }
 #pragma unroll
-  for (int i = 0; i < 4; ++i) cnt[i][tid] = 0;
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int d = tid; d < kBins; d += kSortThreads) cnt[i][d] = 0;
   __syncthreads();
-  const uint4* k4 = reinterpret_cast<const uint4*>(keys + (int64_t)blockIdx.x * kTile);
+  const uint4* k4 = reinterpret_cast<const uint4*>(tk);
   uint4 k[kSortItems / 4];
 #pragma unroll
   for (int i = 0; i < kSortItems / 4; ++i) k[i] = k4[i * kSortThreads + tid];
 #pragma unroll
   for (int i = 0; i < kSortItems / 4; ++i) {
-    atomicAdd(&cnt[w][(k[i].x >> shift) & mask], 1u);
-    atomicAdd(&cnt[w][(k[i].y >> shift) & mask], 1u);
-    atomicAdd(&cnt[w][(k[i].z >> shift) & mask], 1u);
-    atomicAdd(&cnt[w][(k[i].w >> shift) & mask], 1u);
+    if (k[i].x != kSentinel) atomicAdd(&cnt[w][(k[i].x >> shift) & mask], 1u);
+    if (k[i].y != kSentinel) atomicAdd(&cnt[w][(k[i].y >> shift) & mask], 1u);
+    if (k[i].z != kSentinel) atomicAdd(&cnt[w][(k[i].z >> shift) & mask], 1u);
+    if (k[i].w != kSentinel) atomicAdd(&cnt[w][(k[i].w >> shift) & mask], 1u);
   }
   __syncthreads();
-  hist[(int64_t)tid * num_tiles + blockIdx.x] = cnt[0][tid] + cnt[1][tid] + cnt[2][tid] + cnt[3][tid];
+  for (int d = tid; d < nbins; d += kSortThreads)
+    hist[(int64_t)d * num_tiles + tile] = cnt[0][d] + cnt[1][d] + cnt[2][d] + cnt[3][d];
 }
 
 // Exclusive scan of each row of rows[gridDim.x][len] in place; totals[row] =
@@ -435,30 +479,55 @@ __global__ __launch_bounds__(256) void scan_rows_kernel(uint32_t* __restrict__ r
 // Stable scatter of one tile.  Wave w ranks the keys at tile positions
 // w*1024 + j*64 + lane, j = 0..15 (position order = (j, lane) order): lanes
 // with equal digits are found with one ballot per digit bit, and a per-wave
-// LDS counter per digit carries ranks across rounds.  Keys (and values) are
-// then placed in LDS in tile-sorted order and written out in that order, so
-// the global writes of a digit are contiguous.
+// LDS counter per digit carries ranks across rounds.  The keys are then placed
+// in LDS in tile-sorted order and written out in that order, so the global
+// writes of a digit are contiguous; the values follow through the same LDS
+// buffer.  One 16 KB staging buffer keeps five workgroups on a CU.
 __global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
     const uint32_t* __restrict__ keys_in, const uint32_t* __restrict__ vals_in, uint32_t* __restrict__ keys_out,
     uint32_t* __restrict__ vals_out, const uint32_t* __restrict__ hist, const uint32_t* __restrict__ totals,
-    int shift, int nbits, int64_t num_tiles, uint32_t n_pad) {
+    int shift, int nbits, int64_t num_tiles, int compacted, uint32_t* __restrict__ nkeys) {
   __shared__ uint32_t cnt[4][kBins];
   __shared__ uint32_t tstart[kBins];
   __shared__ uint32_t gbase[kBins];
   __shared__ uint32_t tmp[4];
-  __shared__ uint32_t sk[kTile];
-  __shared__ uint32_t sv[kTile];
+  __shared__ uint32_t stage[kTile];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const uint32_t mask = (1u << nbits) - 1u;
-  const int64_t tile = blockIdx.x;
+  const int nbins = 1 << nbits;
+  const uint32_t mask = (uint32_t)nbins - 1u;
+  const int64_t tile = sort_tile(blockIdx.x, keyed_tiles(compacted, nkeys, num_tiles));
+  const int64_t t0 = tile * kTile;
+  if (compacted && keys_in[t0] == kSentinel) {  // every key of the tile is the sentinel, and so is its output
+    const uint4 s4 = make_uint4(kSentinel, kSentinel, kSentinel, kSentinel);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) cnt[i][tid] = 0;
-  {
-    uint32_t total;
-    const uint32_t dpre = block_excl_scan256(totals[tid], tmp, total);
-    gbase[tid] = dpre + hist[(int64_t)tid * num_tiles + tile];
+    for (int i = 0; i < kSortItems / 4; ++i)
+      reinterpret_cast<uint4*>(keys_out + t0)[i * kSortThreads + tid] = s4;
+    return;
   }
-  const int64_t p0 = tile * kTile + w * (kTile / 4);
+  // thread t owns digits dp = DPT * t .. DPT * t + DPT - 1 in the scans over digits
+  constexpr int DPT = kBins / kSortThreads;
+  const int dp = DPT * tid;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int e = 0; e < DPT; ++e) cnt[i][dp + e] = 0;
+  uint32_t num_keys;  // non-sentinel keys of the whole input
+  {
+    uint32_t tv[DPT], sum = 0;
+#pragma unroll
+    for (int e = 0; e < DPT; ++e) {
+      tv[e] = dp + e < nbins ? totals[dp + e] : 0u;
+      sum += tv[e];
+    }
+    uint32_t run = block_excl_scan256(sum, tmp, num_keys);
+#pragma unroll
+    for (int e = 0; e < DPT; ++e) {
+      if (dp + e < nbins) gbase[dp + e] = run + hist[(int64_t)(dp + e) * num_tiles + tile];
+      run += tv[e];
+    }
+    if (!compacted && blockIdx.x == 0 && tid == 0) *nkeys = num_keys;  // read by the later passes
+  }
+  const int64_t p0 = t0 + w * (kTile / 4);
   uint32_t key[kSortItems], val[kSortItems], rank[kSortItems];
 #pragma unroll
   for (int j = 0; j < kSortItems; ++j) {
@@ -469,52 +538,80 @@ __global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
   const uint64_t lt = lanemask_lt(lane);
 #pragma unroll
   for (int j = 0; j < kSortItems; ++j) {
+    const bool valid = key[j] != kSentinel;
     const uint32_t d = (key[j] >> shift) & mask;
-    uint64_t peers = ~uint64_t(0);
+    uint64_t peers = __ballot(valid);
 #pragma unroll
-    for (int b = 0; b < 8; ++b) {
+    for (int b = 0; b < kDigitBits; ++b) {
       if (b < nbits) {
         const bool bit = (d >> b) & 1u;
         const uint64_t bal = __ballot(bit);
         peers &= bit ? bal : ~bal;
       }
     }
-    const uint32_t before = cnt[w][d];
-    rank[j] = before + (uint32_t)__popcll(peers & lt);
-    if ((peers & lt) == 0) cnt[w][d] = before + (uint32_t)__popcll(peers);
+    if (valid) {
+      const uint32_t before = cnt[w][d];
+      rank[j] = before + (uint32_t)__popcll(peers & lt);
+      if ((peers & lt) == 0) cnt[w][d] = before + (uint32_t)__popcll(peers);
+    }
   }
   __syncthreads();
+  uint32_t tile_keys;  // non-sentinel keys of this tile
   {
-    const uint32_t c0 = cnt[0][tid], c1 = cnt[1][tid], c2 = cnt[2][tid], c3 = cnt[3][tid];
-    cnt[0][tid] = 0;
-    cnt[1][tid] = c0;
-    cnt[2][tid] = c0 + c1;
-    cnt[3][tid] = c0 + c1 + c2;
-    uint32_t total;
-    tstart[tid] = block_excl_scan256(c0 + c1 + c2 + c3, tmp, total);
+    uint32_t tc[DPT], sum = 0;
+#pragma unroll
+    for (int e = 0; e < DPT; ++e) {
+      const int d = dp + e;
+      const uint32_t c0 = cnt[0][d], c1 = cnt[1][d], c2 = cnt[2][d], c3 = cnt[3][d];
+      cnt[0][d] = 0;
+      cnt[1][d] = c0;
+      cnt[2][d] = c0 + c1;
+      cnt[3][d] = c0 + c1 + c2;
+      tc[e] = c0 + c1 + c2 + c3;
+      sum += tc[e];
+    }
+    uint32_t run = block_excl_scan256(sum, tmp, tile_keys);
+#pragma unroll
+    for (int e = 0; e < DPT; ++e) {
+      tstart[dp + e] = run;
+      run += tc[e];
+    }
   }
   __syncthreads();
+  uint32_t lpos[kSortItems];
 #pragma unroll
   for (int j = 0; j < kSortItems; ++j) {
     const uint32_t d = (key[j] >> shift) & mask;
-    const uint32_t lpos = tstart[d] + cnt[w][d] + rank[j];
-    if (lpos < (uint32_t)kTile) {
-      sk[lpos] = key[j];
-      sv[lpos] = val[j];
-    }
+    lpos[j] = key[j] != kSentinel ? tstart[d] + cnt[w][d] + rank[j] : 0xFFFFFFFFu;
+    if (lpos[j] < (uint32_t)kTile) stage[lpos[j]] = key[j];
   }
   __syncthreads();
+  uint32_t g[kSortItems];
 #pragma unroll
   for (int i = 0; i < kSortItems; ++i) {
     const uint32_t idx = i * kSortThreads + tid;
-    const uint32_t k = sk[idx];
-    const uint32_t d = (k >> shift) & mask;
-    const uint32_t g = gbase[d] + idx - tstart[d];
-    if (g < n_pad) {
-      keys_out[g] = k;
-      vals_out[g] = sv[idx];
+    g[i] = 0xFFFFFFFFu;
+    if (idx < tile_keys) {
+      const uint32_t k = stage[idx];
+      const uint32_t d = (k >> shift) & mask;
+      g[i] = gbase[d] + idx - tstart[d];
+      keys_out[g[i]] = k;
     }
   }
+  // positions of this tile's range at or beyond num_keys hold the sentinel
+#pragma unroll
+  for (int i = 0; i < kSortItems; ++i) {
+    const int64_t q = t0 + i * kSortThreads + tid;
+    if (q >= (int64_t)num_keys) keys_out[q] = kSentinel;
+  }
+  __syncthreads();  // keys read out of the staging buffer
+#pragma unroll
+  for (int j = 0; j < kSortItems; ++j)
+    if (lpos[j] < (uint32_t)kTile) stage[lpos[j]] = val[j];
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < kSortItems; ++i)
+    if (g[i] != 0xFFFFFFFFu) vals_out[g[i]] = stage[i * kSortThreads + tid];
 }
 
 // ---- 3. accumulate + optimizer ---------------------------------------------------
@@ -1053,7 +1150,7 @@ BwdLayout bwd_layout(const pdm_tbe_plan_s* plan, int64_t n, int64_t batch_size) 
   L.vals_b = take(L.n_pad * 4);
   L.bag_scale = take(std::max<int64_t>(num_bags, 1) * 4);
   L.hist = take(kBins * L.num_tiles * 4);
-  L.totals = take(kBins * 4);
+  L.totals = take((kBins + 1) * 4);  // digit totals, then the count of non-sentinel keys
   L.part_first = take(L.num_chunks * L.dmax * 4);
   L.part_last = take(L.num_chunks * L.dmax * 4);
   L.num_levels = 1;
@@ -1263,25 +1360,25 @@ int run_backward(const BwdCall& c) {
     PDM_CHECK_LAUNCH();
   }
 
-  // 2. sort (key, position) on the bits the row space needs
+  // 2. sort (key, position) on the bits the row space needs, in the fewest passes of at most kDigitBits
+  // bits, the first passes one bit wider where the bits do not divide evenly
   int bits = 1;
   while (bits < 32 && (int64_t(1) << bits) < plan->total_rows + 1) ++bits;
-  const int passes = (bits + 7) / 8;
+  const int passes = (bits + kDigitBits - 1) / kDigitBits;
   uint32_t *kin = keys_a, *kout = keys_b, *vin = vals_a, *vout = vals_b;
-  for (int p = 0; p < passes; ++p) {
-    const int shift = 8 * p;
-    const int nb = std::min(8, bits - shift);
-    const uint32_t mask = (1u << nb) - 1u;
+  for (int p = 0, shift = 0; p < passes; ++p) {
+    const int nb = bits / passes + (p < bits % passes ? 1 : 0);
     hipLaunchKernelGGL(radix_count_kernel, dim3((unsigned)L.num_tiles), dim3(kSortThreads), 0, c.stream, kin, hist,
-                       shift, mask, L.num_tiles);
+                       shift, nb, L.num_tiles, p > 0 ? 1 : 0, totals + kBins);
     PDM_CHECK_LAUNCH();
-    hipLaunchKernelGGL(scan_rows_kernel, dim3(kBins), dim3(256), 0, c.stream, hist, totals, L.num_tiles);
+    hipLaunchKernelGGL(scan_rows_kernel, dim3(1u << nb), dim3(256), 0, c.stream, hist, totals, L.num_tiles);
     PDM_CHECK_LAUNCH();
     hipLaunchKernelGGL(radix_scatter_kernel, dim3((unsigned)L.num_tiles), dim3(kSortThreads), 0, c.stream, kin,
-                       vin, kout, vout, hist, totals, shift, nb, L.num_tiles, (uint32_t)L.n_pad);
+                       vin, kout, vout, hist, totals, shift, nb, L.num_tiles, p > 0 ? 1 : 0, totals + kBins);
     PDM_CHECK_LAUNCH();
     std::swap(kin, kout);
     std::swap(vin, vout);
+    shift += nb;
   }
   // sorted data now in kin / vin
 
