@@ -17,6 +17,8 @@ mean pooling over Poisson(20) bags in [1, 100] of Zipf(1.2) ids, batch
   ns_tokenize NS tokens: uid/item/artist/album rows (1M/9.4M/1.3M/3.4M x 64 bf16) + dense parts 64/6/6/64 -> 396
               wide NS input -> AutoSplitTokenizer Linear(396, 4096) + GELU + Linear(4096, 4096), B=1024
   onetrans    4-layer OneTrans block stack, B=1024, 384 S + 16 NS tokens, d 256, schedule 384/256/128/64
+  onetrans_l  OneTransL: 8-layer stack, B=1024, 1500 S + 16 NS tokens, d 384, 6 heads, the pyramid schedule
+              1500 -> 16 (1500, 1288, 1076, 864, 652, 440, 228, 16)
   cross_hash  cross-feature ids: xxHash64 of (uid, artist_id) int64 pairs % 100,000,000, 16,777,216 rows
   train_adam  pooled backward + fused Adam (lr 1e-2, eps 1e-8, wd 1e-5): 8 tables x 10,000,000 x 64 fp32,
               sum, Poisson(10) bags in [0, 50], uniform ids, B=65,536 (about 5.2 M lookups)
@@ -810,7 +812,7 @@ def _torch_block(torch, x, w, q_len: int, n_heads: int):
 
 
 def cpu_onetrans(torch, w, threads: int, batch: int):
-    """The reference's 4-layer block stack (the block loop of onetrans.py:568-582) in fp32 torch on the CPU at
+    """The reference's block stack (the block loop of onetrans.py:568-582) in fp32 torch on the CPU at
     ``batch`` samples, N(0, 0.02) weights and inputs."""
     torch.set_num_threads(threads)
     g = torch.Generator().manual_seed(1005)
@@ -917,13 +919,16 @@ def onetrans_config(w, alg, causal):
 
 
 ONETRANS_CPU_BATCH = 1024
+ONETRANS_L_CPU_BATCH = 16  # OneTransL: 0.67 TFLOP per 16 samples
 
 
-def onetrans_cpu_baseline(torch, w, threads: int):
-    sec, reps = cpu_onetrans(torch, w, threads, ONETRANS_CPU_BATCH)
-    return cpu_result(ONETRANS_CPU_BATCH / sec, "samples/s", threads, "torch fp32 OneTransBlock x4 (Linear, einsum, "
+def onetrans_cpu_baseline(torch, w, threads: int, batch: int = ONETRANS_CPU_BATCH):
+    sec, reps = cpu_onetrans(torch, w, threads, batch)
+    n = len(w.schedule)
+    return cpu_result(batch / sec, "samples/s", threads, f"torch fp32 OneTransBlock x{n} (Linear, einsum, "
                       "SDPA with the bool pyramid mask, RMSNorm, GELU)",
-                      f"the 4-layer stack on the full batch of {ONETRANS_CPU_BATCH} samples", sec, reps)
+                      f"the {n}-layer stack on " + (f"the full batch of {batch} samples" if batch == w.batch else
+                                                    f"{batch} of the batch's {w.batch} samples"), sec, reps)
 
 
 def block_leg(pdm, torch, dev, stream, args, threads: int):
@@ -957,7 +962,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="int8_mean",
                     choices=["single_hot", "ebc_fp32", "int8_mean", "seq_gather", "seq_tokenize", "ns_tokenize",
-                             "onetrans",
+                             "onetrans", "onetrans_l",
                              "cross_hash",
                              "train_adam", "train_rowwise_adagrad", "train_seq_adam", "kjt_build", "copy_1gib"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -1149,13 +1154,14 @@ def main() -> int:
         alg, units, unit, bound, dtype = 2 << 30, 2 << 30, "bytes/s", "hbm", "f32"
         cfg = {"workload": "device_copy_1gib"}
     else:
-        w = syn.onetrans_block()
+        large = args.workload == "onetrans_l"
+        w = syn.onetrans_large() if large else syn.onetrans_block()
         step, alg, causal, keep = setup_onetrans(pdm, torch, dev, w)
         units, unit, bound, dtype = w.batch, "samples/s", "mfma", "bf16"
         cfg = onetrans_config(w, alg, causal)
 
         def cpu_fn():
-            return onetrans_cpu_baseline(torch, w, threads)
+            return onetrans_cpu_baseline(torch, w, threads, ONETRANS_L_CPU_BATCH if large else ONETRANS_CPU_BATCH)
 
     stream = torch.cuda.current_stream(dev)
     log(f"warmup {args.warmup} steps")
@@ -1166,7 +1172,7 @@ def main() -> int:
         roofline = hbm_roofline(alg, kernel_ms, args.workload if args.ids == "zipf" else args.workload + "_uniform")
     else:
         roofline = mfma_roofline(alg, kernel_ms, args.workload)
-        if args.workload == "onetrans":
+        if args.workload in ("onetrans", "onetrans_l"):
             roofline.update(causal_roofline(causal, kernel_ms))
     log(f"{value:.4g} {unit}, step {kernel_ms:.4f} ms, {roofline['achieved']:.1f} {roofline['unit']}")
     if graph_fn is not None:

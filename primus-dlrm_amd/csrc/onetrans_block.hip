@@ -1168,118 +1168,6 @@ struct AttnArgs {
   int q_lds;         // attn_lds_kernel with 8 waves: Q of a head staged in LDS after K and V^T
 };
 
-__global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int bh = blockIdx.y;
-  const int b = bh / a.H, h = bh - (bh / a.H) * a.H;
-  const int D = a.H * 64;
-  const int qi0 = blockIdx.x * 128 + wave * 32;
-  if (qi0 >= a.q_len) return;
-  const int fr = lane & 31, hf = lane >> 5;
-  const int off = a.kv - a.q_len;
-  const int qi = qi0 + fr;
-  const bool qvalid = qi < a.q_len;
-  const int p = qi + off;  // last key this query sees
-
-  u32x4_t qf[4];
-  const uint16_t* qrow = a.q + ((int64_t)b * a.q_len + qi) * D + h * 64 + hf * 8;
-#pragma unroll
-  for (int c = 0; c < 4; ++c) qf[c] = qvalid ? *reinterpret_cast<const u32x4_t*>(qrow + c * 16) : u32x4_t{0, 0, 0, 0};
-
-  const int q_last = min(qi0 + 31, a.q_len - 1);
-  const int kv_end = min(a.kv, q_last + off + 1);
-
-  f32x16_t o[2];
-#pragma unroll
-  for (int e = 0; e < 16; ++e) { o[0][e] = 0.0f; o[1][e] = 0.0f; }
-  float m = -INFINITY, l = 0.0f;
-
-  const uint16_t* kbase = a.k + (int64_t)b * a.kv * D + h * 64 + hf * 8;
-  const uint16_t* vbase = a.vt + ((int64_t)b * a.H + h) * 64 * a.vt_ld;
-
-  for (int j0 = 0; j0 < kv_end; j0 += 32) {
-    // S^T[kv][q] = K . Q^T
-    f32x16_t s;
-#pragma unroll
-    for (int e = 0; e < 16; ++e) s[e] = 0.0f;
-    const int jr = j0 + fr;
-    const uint16_t* krow = kbase + (int64_t)jr * D;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const u32x4_t kf = jr < a.kv ? *reinterpret_cast<const u32x4_t*>(krow + c * 16) : u32x4_t{0, 0, 0, 0};
-      s = mfma32x32x16(kf, qf[c], s);
-    }
-    // s[e] is key j0 + (e/4)*8 + hf*4 + e%4 of query qi
-    float mx = -INFINITY;
-#pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const int j = j0 + (e >> 2) * 8 + hf * 4 + (e & 3);
-      const float t = (j <= p && j < a.kv) ? s[e] * a.scale_log2 : -INFINITY;
-      s[e] = t;
-      mx = fmaxf(mx, t);
-    }
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float m_new = fmaxf(m, mx);
-    const float alpha = exp2f(m - m_new);
-    m = m_new;
-    float ps = 0.0f;
-    uint32_t pk[8];
-#pragma unroll
-    for (int e = 0; e < 16; e += 2) {
-      const float p0 = exp2f(s[e] - m_new);
-      const float p1 = exp2f(s[e + 1] - m_new);
-      ps += p0 + p1;
-      pk[e >> 1] = pack_bf16x2(p0, p1);
-    }
-    l = l * alpha + ps;
-#pragma unroll
-    for (int e = 0; e < 16; ++e) { o[0][e] *= alpha; o[1][e] *= alpha; }
-    // O^T[d][q] += V^T . P^T; P^T chunk c2 holds keys j0 + 16*c2 + (e/4)*8 + hf*4 + e%4, e = 0..7
-    const bool tail = j0 + 32 > a.kv;
-#pragma unroll
-    for (int c2 = 0; c2 < 2; ++c2) {
-      const u32x4_t pb = {pk[4 * c2], pk[4 * c2 + 1], pk[4 * c2 + 2], pk[4 * c2 + 3]};
-      const int jb = j0 + 16 * c2 + hf * 4;
-#pragma unroll
-      for (int db = 0; db < 2; ++db) {
-        const uint16_t* vrow = vbase + (int64_t)(db * 32 + fr) * a.vt_ld + jb;
-        u32x2_t lo = *reinterpret_cast<const u32x2_t*>(vrow);
-        u32x2_t hi = *reinterpret_cast<const u32x2_t*>(vrow + 8);
-        if (tail) {
-          // keys at or past kv hold no value: zero them so 0 * garbage cannot appear
-#pragma unroll
-          for (int w = 0; w < 2; ++w) {
-            const int j = jb + 2 * w;
-            if (j >= a.kv) lo[w] = 0u;
-            else if (j + 1 >= a.kv) lo[w] &= 0xffffu;
-            const int j2 = jb + 8 + 2 * w;
-            if (j2 >= a.kv) hi[w] = 0u;
-            else if (j2 + 1 >= a.kv) hi[w] &= 0xffffu;
-          }
-        }
-        const u32x4_t vf = {lo[0], lo[1], hi[0], hi[1]};
-        o[db] = mfma32x32x16(vf, pb, o[db]);
-      }
-    }
-  }
-  l += __shfl_xor(l, 32, 64);
-  if (!qvalid) return;
-  const float inv = 1.0f / l;
-  uint16_t* orow = a.o + ((int64_t)b * a.q_len + qi) * D + h * 64;
-  // o[db][e] is d = db*32 + (e/4)*8 + hf*4 + e%4
-#pragma unroll
-  for (int db = 0; db < 2; ++db)
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int d = db * 32 + g * 8 + hf * 4;
-      u32x2_t w;
-      w[0] = pack_bf16x2(o[db][4 * g] * inv, o[db][4 * g + 1] * inv);
-      w[1] = pack_bf16x2(o[db][4 * g + 2] * inv, o[db][4 * g + 3] * inv);
-      *reinterpret_cast<u32x2_t*>(orow + d) = w;
-    }
-}
-
 // ---------------------------------------------------------------------------
 // Persistent attention with the keys and values of a head resident in LDS.
 // Each workgroup of NW waves walks the (sample, head) pairs blockIdx.x,
@@ -1604,6 +1492,202 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_lds_kernel(AttnArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// Causal attention for heads whose keys do not fit in LDS (kv > kAttnLdsMaxKeys).  A workgroup of NW waves
+// owns 32 NW consecutive queries of one (sample, head), one 32-query tile per wave, and streams the head's
+// keys through LDS in chunks of 64: K rows and V^T rows in the layouts of attn_lds_kernel for 64 keys,
+// double-buffered, the next chunk read into registers while the waves compute on the current one and written
+// to the other buffer before the barrier that ends the chunk.  Each wave keeps its tile's online softmax
+// state (shift m, denominator share l, O^T accumulators) in registers across the chunks and skips the chunks
+// past its causal limit; the chunks stop at the workgroup's last visible key.  Workgroups take (sample, head,
+// query block) items XCD-contiguously (the 8 XCDs take the workgroups in turn), so the query blocks of a head
+// share one L2, and the longest query block of a head first.
+// ---------------------------------------------------------------------------
+constexpr int kStreamKeys = 64;  // keys per LDS chunk
+
+template <int NW>
+__global__ __launch_bounds__(NW * 64, 16 / NW) void attn_stream_kernel(AttnArgs a, int n_qb, int64_t n_items) {
+  constexpr int NT = NW * 64;
+  constexpr int PPT = kStreamKeys * 8 / NT;  // 16-byte pieces per thread of a chunk's K (and of its V^T)
+  static_assert(PPT >= 1 && PPT * NT == kStreamKeys * 8, "chunk pieces must split evenly over the threads");
+  __shared__ __attribute__((aligned(16))) char sbuf[2][2 * kStreamKeys * 128];  // per buffer: K 8 KB, V^T 8 KB
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int fr = lane & 31, hf = lane >> 5;
+  const int D = a.H * 64;
+  // item = bh * n_qb + (n_qb - 1 - query block): XCD x takes the contiguous items x * q + min(x, r) ..
+  int64_t item;
+  {
+    const int64_t id = blockIdx.x, q8 = n_items >> 3, r8 = n_items & 7, x = id & 7;
+    item = x * q8 + (x < r8 ? x : r8) + (id >> 3);
+  }
+  const int bh = (int)(item / n_qb);
+  const int qb = n_qb - 1 - (int)(item - (int64_t)bh * n_qb);
+  const int b = bh / a.H, h = bh - (bh / a.H) * a.H;
+  const int off = a.kv - a.q_len;
+  const int wq0 = qb * (32 * NW);
+  const int wq_last = min(wq0 + 32 * NW - 1, a.q_len - 1);
+  const int kv_end = min(a.kv, wq_last + off + 1);  // keys the workgroup's queries see
+  const int nchunks = (kv_end + kStreamKeys - 1) / kStreamKeys;
+  const int qi0 = wq0 + wave * 32;
+  const bool active = qi0 < a.q_len;  // wave-uniform
+  const int qi = qi0 + fr;
+  const int q_last = min(qi0 + 31, a.q_len - 1);
+  const int w_end = active ? min(a.kv, q_last + off + 1) : 0;  // keys this wave's queries see
+  const int p_last = qi + off;
+  // key kb + j0 + 16*(e/8) + hf*8 + e%8 of element e is visible iff 16*(e/8) + e%8 <= lim - kb - j0
+  const int lim = min(p_last, a.kv - 1) - hf * 8;
+
+  // chunk copy: piece u = i * NT + tid; K: LDS row m = u / 8 (chunk key (m & ~15) | swap23(m & 15)), piece
+  // u % 8 at position (u % 8) ^ ((m >> 1) & 7); V^T: row d = u / 8, piece pv = u % 8 (chunk keys 8 pv ..) at
+  // position pv ^ ((d >> 2) & 3).  Reads are unconditional (clamped rows); keys past kv are stored as zeros.
+  const uint16_t* kg = a.k + (int64_t)b * a.kv * D + h * 64;
+  const uint16_t* vg = a.vt + (int64_t)bh * 64 * a.vt_ld;
+  u32x4_t kr[PPT], vr[PPT];
+  auto cload = [&](int cb) {
+#pragma unroll
+    for (int i = 0; i < PPT; ++i) {
+      const int u = i * NT + tid, m = u >> 3, p = u & 7;
+      const int key = cb + ((m & ~15) | swap23(m & 15));
+      kr[i] = *reinterpret_cast<const u32x4_t*>(kg + (int64_t)min(key, a.kv - 1) * D + p * 8);
+      vr[i] = *reinterpret_cast<const u32x4_t*>(vg + (int64_t)m * a.vt_ld + cb + p * 8);
+    }
+  };
+  auto cstore = [&](int cb, int buf) {
+    char* sK = sbuf[buf];
+    char* sV = sbuf[buf] + kStreamKeys * 128;
+#pragma unroll
+    for (int i = 0; i < PPT; ++i) {
+      const int u = i * NT + tid, m = u >> 3, p = u & 7;
+      const int key = cb + ((m & ~15) | swap23(m & 15));
+      *reinterpret_cast<u32x4_t*>(sK + m * 128 + ((p ^ ((m >> 1) & 7)) << 4)) =
+          key < a.kv ? kr[i] : u32x4_t{0, 0, 0, 0};
+      u32x4_t v = vr[i];
+      if (cb + p * 8 + 8 > a.kv) {  // V^T beyond key kv - 1 is padding the Q/K/V projection never wrote
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const int k0 = cb + p * 8 + 2 * w;
+          if (k0 >= a.kv) v[w] = 0u;
+          else if (k0 + 1 >= a.kv) v[w] &= 0xffffu;
+        }
+      }
+      *reinterpret_cast<u32x4_t*>(sV + m * 128 + ((p ^ ((m >> 2) & 3)) << 4)) = v;
+    }
+  };
+
+  // the wave's Q fragments (rows past q_len read row q_len - 1, the wave's own last row; their outputs are
+  // never stored).  O is written over Q: each wave reads only its own rows, before it writes them.
+  u32x4_t qf[4] = {};
+  if (active) {
+    const uint16_t* qrow = a.q + ((int64_t)b * a.q_len + min(qi, a.q_len - 1)) * D + h * 64 + hf * 8;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) qf[c] = *reinterpret_cast<const u32x4_t*>(qrow + c * 16);
+  }
+  int kofs[4], vofs[2];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) kofs[c] = ((2 * c + hf) ^ ((fr >> 1) & 7)) << 4;
+#pragma unroll
+  for (int c2 = 0; c2 < 2; ++c2) vofs[c2] = ((2 * c2 + hf) ^ ((fr >> 2) & 3)) << 4;
+
+  f32x16_t o[2];
+#pragma unroll
+  for (int e = 0; e < 16; ++e) { o[0][e] = 0.0f; o[1][e] = 0.0f; }
+  // m: the shift of the exponentials (log2 units), shared by the two lanes of a query; raised only when a
+  // score exceeds it by more than 8 (the normalised output does not depend on it); l: this lane's share of
+  // the softmax denominator
+  float m = -INFINITY, l = 0.0f;
+
+  cload(0);
+  cstore(0, 0);
+  __syncthreads();
+  for (int c = 0; c < nchunks; ++c) {
+    const int buf = c & 1, cb = c * kStreamKeys;
+    if (c + 1 < nchunks) cload(cb + kStreamKeys);
+    if (cb < w_end) {
+      const char* kp = sbuf[buf] + fr * 128;
+      const char* vp0 = sbuf[buf] + kStreamKeys * 128 + fr * 128;
+      const char* vp1 = vp0 + 32 * 128;
+      for (int j0 = 0; j0 < kStreamKeys && cb + j0 < w_end; j0 += 32) {
+        u32x4_t kf[4], vf[4];
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc) kf[cc] = *reinterpret_cast<const u32x4_t*>(kp + j0 * 128 + kofs[cc]);
+#pragma unroll
+        for (int c2 = 0; c2 < 2; ++c2) {
+          vf[2 * c2] = *reinterpret_cast<const u32x4_t*>(vp0 + j0 * 2 + vofs[c2]);
+          vf[2 * c2 + 1] = *reinterpret_cast<const u32x4_t*>(vp1 + j0 * 2 + vofs[c2]);
+        }
+        // S^T[key][q] = K . Q^T; s[e] is key cb + j0 + 16*(e/8) + hf*8 + e%8
+        f32x16_t s;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) s[e] = 0.0f;
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc) s = mfma32x32x16(kf[cc], qf[cc], s);
+        const int jg = cb + j0;
+        if (jg + 31 > qi0 + off || jg + 32 > a.kv) {  // some key of the tile is masked for some query
+          const int r = lim - jg;
+#pragma unroll
+          for (int e = 0; e < 16; ++e) s[e] = (16 * (e >> 3) + (e & 7) <= r) ? s[e] : -INFINITY;
+        }
+        float mx = fmaxf(fmaxf(s[0], s[1]), s[2]);
+#pragma unroll
+        for (int e = 3; e < 15; e += 2) mx = fmaxf(fmaxf(mx, s[e]), s[e + 1]);
+        mx = fmaxf(mx, s[15]);
+        {  // max with the other half of the wave (lane l ^ 32 holds the same query)
+          const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+          mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+        }
+        const float mt = mx * a.scale_log2;
+        if (__builtin_amdgcn_ballot_w64(mt > m + 8.0f)) {
+          const float m_new = fmaxf(m, mt);
+          const float alpha = __builtin_amdgcn_exp2f(m - m_new);  // 0 on the first tile (m = -inf)
+          m = m_new;
+          l *= alpha;
+#pragma unroll
+          for (int e = 0; e < 16; ++e) { o[0][e] *= alpha; o[1][e] *= alpha; }
+        }
+        float ps = 0.0f;
+        uint32_t pk[8];
+#pragma unroll
+        for (int e = 0; e < 16; e += 2) {
+          const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[e], a.scale_log2, -m));
+          const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[e + 1], a.scale_log2, -m));
+          ps += p0 + p1;
+          pk[e >> 1] = pack_bf16x2(p0, p1);
+        }
+        l += ps;
+        // O^T[d][q] += V^T . P^T; chunk c2 of P^T holds keys j0 + 16*c2 + hf*8 + 0..7
+#pragma unroll
+        for (int c2 = 0; c2 < 2; ++c2) {
+          const u32x4_t pb = {pk[4 * c2], pk[4 * c2 + 1], pk[4 * c2 + 2], pk[4 * c2 + 3]};
+          o[0] = mfma32x32x16(vf[2 * c2], pb, o[0]);
+          o[1] = mfma32x32x16(vf[2 * c2 + 1], pb, o[1]);
+        }
+      }
+    }
+    if (c + 1 < nchunks) cstore(cb + kStreamKeys, buf ^ 1);
+    __syncthreads();
+  }
+  if (!active) return;
+  {
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(l), __float_as_uint(l), false, false);
+    l = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+  }
+  if (qi < a.q_len) {
+    const float inv = 1.0f / l;
+    uint16_t* orow = a.o + ((int64_t)b * a.q_len + qi) * D + h * 64;
+    // o[db][e] is d = db*32 + (e/4)*8 + hf*4 + e%4
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d = db * 32 + g * 8 + hf * 4;
+        u32x2_t w;
+        w[0] = pack_bf16x2(o[db][4 * g] * inv, o[db][4 * g + 1] * inv);
+        w[1] = pack_bf16x2(o[db][4 * g + 2] * inv, o[db][4 * g + 3] * inv);
+        *reinterpret_cast<u32x2_t*>(orow + d) = w;
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
 
@@ -1759,8 +1843,8 @@ static int launch_rmsnorm(const float* x, int64_t x_bstride, int T, int64_t B, i
 
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
-// Largest LDS footprint of attn_lds_kernel; longer sequences run attn_kernel,
-// which streams K and V^T from memory.
+// Largest LDS footprint of attn_lds_kernel; longer sequences run attn_stream_kernel,
+// which streams K and V^T through LDS in chunks.
 constexpr int64_t kAttnLdsMax = (int64_t)kAttnLdsMaxKeys * 256;
 // LDS of one workgroup on gfx950: K, V^T and, when it fits, the head's Q
 constexpr int64_t kAttnLdsLimit = 160 * 1024;
@@ -1884,8 +1968,12 @@ static int block_fwd(const pdm_block_desc& d, const float* x, const pdm_block_we
       }
       if (st != PDM_OK) return st;
     } else {
-      PDM_CHECK_ARG(gy < 65536, "batch * heads must be < 65536");
-      hipLaunchKernelGGL(attn_kernel, dim3((unsigned)((ql + 127) / 128), (unsigned)gy), dim3(256), 0, s, aa);
+      // keys streamed through LDS in chunks, 8 waves (256 queries) per workgroup
+      constexpr int kNW = 8;
+      const int n_qb = (ql + 32 * kNW - 1) / (32 * kNW);
+      const int64_t n_items = gy * n_qb;
+      PDM_CHECK_ARG(n_items < (int64_t(1) << 31), "batch * heads * query blocks must be < 2^31");
+      hipLaunchKernelGGL(attn_stream_kernel<kNW>, dim3((unsigned)n_items), dim3(kNW * 64), 0, s, aa, n_qb, n_items);
     }
     PDM_CHECK_LAUNCH();
   }

@@ -189,6 +189,14 @@ def onetrans_block(batch: int = 1024) -> BlockWorkload:
     return BlockWorkload("onetrans_4layer_b1024", batch, 384, 16, 256, 4, 4, [384, 256, 128, 64])
 
 
+def onetrans_large(batch: int = 1024) -> BlockWorkload:
+    """OneTransL (configs/bench_onetrans_large_synthetic.yaml:1-5,28-33): B=1024, 1500 S-tokens + 16 NS-tokens,
+    d 384, 6 heads x 64, FFN 4x, 8 layers, the reference's pyramid schedule 1500 -> 16
+    (pyramid_schedule(1500, 16, 8): 1500, 1288, 1076, 864, 652, 440, 228, 16), inputs and weights N(0, 0.02)."""
+    return BlockWorkload("onetransl_8layer_b1024", batch, 1500, 16, 384, 6, 4,
+                         [1500, 1288, 1076, 864, 652, 440, 228, 16])
+
+
 def block_flops(w: BlockWorkload) -> float:
     """Forward FLOPs by the reference's convention (onetrans.py:392-474 without the x3 for backward):
     S-token QKV on every kv S-token, attention counted full (no causal discount)."""
