@@ -752,7 +752,12 @@ __global__ __launch_bounds__(256, EPI == EPI_QKV ? PDM_QKV_WPS : 2) void rowgemm
 // on the columns, so lane l holds token row l%32 of each row block and 16
 // hidden units of it.  After GELU (fp32 on the bf16-rounded value, then bf16)
 // those values are the B operand of y^T += W2[:, c] . G^T without leaving
-// registers.  Every weight fragment read from LDS feeds RB MFMAs.  The
+// registers.  Every weight fragment read from LDS feeds RB MFMAs.  With
+// PDM_FFN_UP16 (the default) the FFN-up runs as 16x16x32 MFMAs into four
+// independent accumulators (two 16-unit hidden blocks x two 16-token blocks):
+// one exchange of the RMSNorm2 fragments per tile and one of the GELU values
+// per chunk (v_permlane16_swap) keep both sides' operand reads single 16-byte
+// LDS reads, and LDS row r of the W1 chunk holds hidden unit r.  Otherwise the
 // accumulator row e/4*8 + (l/32)*4 + e%4 of a 16-unit half must meet hidden
 // unit (l/32)*8 + e%8 for the W2 operand to be one contiguous 16-byte read,
 // so LDS row r of the W1 chunk holds hidden unit r with bits 2 and 3 swapped.
@@ -777,8 +782,15 @@ __global__ __launch_bounds__(256, EPI == EPI_QKV ? PDM_QKV_WPS : 2) void rowgemm
 // The grid is persistent: WPS workgroups per CU walk the row tiles
 // blockIdx.x, blockIdx.x + gridDim.x, ...
 // ---------------------------------------------------------------------------
+// PDM_FFN_UP16: the FFN-up runs as 16x16x32 MFMAs into four independent accumulators (no dependent chain of
+// KS MFMAs into one), with the operand exchanges described at their code; 0: one 32x32x16 chain.
+#ifndef PDM_FFN_UP16
+#define PDM_FFN_UP16 1
+#endif
+
 template <int D, int RB, int NW, int NST, int WPS, bool OPROJ>
 __global__ __launch_bounds__(NW * 64, WPS) void ffn_kernel(GemmArgs a) {
+  static_assert(!PDM_FFN_UP16 || RB == 1, "the 16x16x32 FFN-up assumes one row block per wave");
   constexpr int NT = NW * 64;                // threads
   constexpr int PF = NST - 1;                // chunks read ahead
   constexpr int KS = D / 16;
@@ -822,7 +834,8 @@ __global__ __launch_bounds__(NW * 64, WPS) void ffn_kernel(GemmArgs a) {
   // Weight chunk c goes from global memory straight into LDS (global_load_lds_dwordx4: lane l of a wave
   // writes the 16 bytes at the wave's LDS base + 16 l), so LDS piece o of a stage is loaded by thread
   // o mod NT, round o / NT, and the source address is what decides the layout.
-  // W1 stage: row r = hidden unit c*32 + swap23(r) (bits 2 and 3 swapped), D columns in 2D bytes,
+  // W1 stage: row r = hidden unit c*32 + r (c*32 + swap23(r), bits 2 and 3 swapped, without PDM_FFN_UP16),
+  // D columns in 2D bytes,
   // 16-byte piece v of the row at slot v ^ (r & 15), so the 32 rows of one fragment read hit distinct
   // bank groups.  W2 stage: W2[d, c*32 .. c*32+32) as D rows of 64 bytes, piece v at v ^ ((d >> 2) & 3).
   constexpr int L1 = W1_BYTES / 16 / NT;     // pieces per thread of a W1 chunk
@@ -843,7 +856,8 @@ __global__ __launch_bounds__(NW * 64, WPS) void ffn_kernel(GemmArgs a) {
 #pragma unroll
     for (int j = 0; j < NLO; ++j) {
       const int r = j * RP + r0;  // < 16
-      off1[j] = (uint32_t)((((r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1)) * D + ((slot ^ (r & 15)) << 3)) * 2);
+      const int hid = PDM_FFN_UP16 ? r : ((r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1));
+      off1[j] = (uint32_t)((hid * D + ((slot ^ (r & 15)) << 3)) * 2);
     }
   }
   const uint32_t off2 = (uint32_t)(((tid >> 2) * F + (((tid & 3) ^ ((tid >> 4) & 3)) * 8)) * 2);
@@ -1010,6 +1024,22 @@ __global__ __launch_bounds__(NW * 64, WPS) void ffn_kernel(GemmArgs a) {
         for (int e = 0; e < 16; ++e) y[rb][db][e] = 0.0f;
   }
 
+#if PDM_FFN_UP16
+  // hfr (lane l: token l % 32, columns 16 s + 8 (l / 32) .. + 7 of step s) -> the B operand of the 16x16x32
+  // FFN-up, two 16-token blocks tb: hfr[2 s2 + tb] of lane l then holds token 16 tb + l % 16, columns
+  // 32 s2 + 16 (G & 1) + 8 (G >> 1) .. + 7 with G = l / 16.  Lanes l and l ^ 16 (same half-wave, tokens of the
+  // two blocks) trade their pieces of odd and even steps: v_permlane16_swap exchanges the odd 16-lane rows
+  // of its first operand with the even rows of its second.
+#pragma unroll
+  for (int s2 = 0; s2 < KS / 2; ++s2)
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const auto sw = __builtin_amdgcn_permlane16_swap(hfr[0][2 * s2][w], hfr[0][2 * s2 + 1][w], false, false);
+      hfr[0][2 * s2][w] = sw[0];
+      hfr[0][2 * s2 + 1][w] = sw[1];
+    }
+#endif
+
   // The chunk loop is unrolled by the ring depth so that every stage index is a constant: the LDS reads of
   // stage k and the LDS DMA into stage (k + PF) % NST are then distinct objects to the compiler.
   for (int c0 = 0; c0 < nchunks; c0 += NST) {
@@ -1026,8 +1056,63 @@ __global__ __launch_bounds__(NW * 64, WPS) void ffn_kernel(GemmArgs a) {
       // issued unconditionally (a branch around it costs the compiler its stage tracking): past the last chunk
       // it reloads the last chunk into the stage just freed, which no later chunk reads
       dma(min(c + PF, nchunks - 1), (k + PF) % NST);
-      // FFN-up: U^T[rb] = W1_c . h[rb]^T, each W1 fragment feeding RB MFMAs
       const char* w1 = sW1[k];
+      uint32_t gp[RB][8];
+#if PDM_FFN_UP16
+      // FFN-up with 16x16x32 MFMAs into four independent accumulators u4[hb][tb]: hidden units 16 hb + 4 G
+      // + i (G = lane / 16, element i) of token 16 tb + lane % 16.  Step s2 takes the W1 fragment of row
+      // 16 hb + lane % 16, piece 4 s2 + 2 (G & 1) + (G >> 1) (the columns the lane's hfr pieces hold).
+      f32x4_t u4[2][2];
+#pragma unroll
+      for (int hb = 0; hb < 2; ++hb)
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb) u4[hb][tb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+      // G = bf16(gelu(bf16(U))), half h2 = hidden block hb: lane l holds hidden units 16 h2 + 4 G + 0..3 of its
+      // own token (block (l / 16) & 1) and of the token of lane l ^ 16; one exchange per word gives it hidden
+      // units 16 h2 + 8 (l / 32) + 0..7 of token l % 32, the FFN-down's B operand for chunk c2 = h2
+      auto gelu_half = [&](int h2) {
+        float uv[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          uv[i] = u4[h2][0][i];
+          uv[4 + i] = u4[h2][1][i];
+        }
+        uint32_t t[4];
+        gelu_lut_pack<8>(sGelu, uv, t);
+#pragma unroll
+        for (int w = 0; w < 2; ++w) {
+          const auto sw = __builtin_amdgcn_permlane16_swap(t[w], t[2 + w], false, false);
+          gp[0][4 * h2 + w] = sw[0];
+          gp[0][4 * h2 + 2 + w] = sw[1];
+        }
+      };
+      {
+        const int r16 = lane & 15, pofs = 2 * ((lane >> 4) & 1) + (lane >> 5);
+        u32x4_t wf[KS];
+#pragma unroll
+        for (int s2 = 0; s2 < KS / 2; ++s2)
+#pragma unroll
+          for (int hb = 0; hb < 2; ++hb)
+            wf[2 * s2 + hb] = *reinterpret_cast<const u32x4_t*>(w1 + (16 * hb + r16) * (2 * D) +
+                                                                (((4 * s2 + pofs) ^ r16) << 4));
+#pragma unroll
+        for (int s2 = 0; s2 < KS / 2; ++s2)
+#pragma unroll
+          for (int hb = 0; hb < 2; ++hb)
+#pragma unroll
+            for (int tb = 0; tb < 2; ++tb) u4[hb][tb] = mfma16x16x32(wf[2 * s2 + hb], hfr[0][2 * s2 + tb], u4[hb][tb]);
+        // 4 fragment reads ahead, then 4 MFMAs and the next step's 2 reads in turn
+        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+        for (int i = 0; i < KS / 2 - 2; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+          __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+      }
+      gelu_half(0);
+#else
+      // FFN-up: U^T[rb] = W1_c . h[rb]^T, each W1 fragment feeding RB MFMAs
       f32x16_t u[RB];
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb)
@@ -1045,9 +1130,6 @@ __global__ __launch_bounds__(NW * 64, WPS) void ffn_kernel(GemmArgs a) {
         if constexpr (RB == 1) sched_mfma_ds_pipeline<KS, 3>();
       }
       // G = bf16(gelu(bf16(U))): u[rb][e] is hidden unit (e/4)*8 + hf*4 + e%4 (LDS row order) of token fr.
-      // The first half (u[0..7], G^T chunk c2 = 0) is computed before the FFN-down; the second half between
-      // the c2 = 0 MFMAs, which do not need it
-      uint32_t gp[RB][8];
       auto gelu_half = [&](int h2) {
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) {
@@ -1057,7 +1139,12 @@ __global__ __launch_bounds__(NW * 64, WPS) void ffn_kernel(GemmArgs a) {
           gelu_lut_pack<8>(sGelu, uv, gp[rb] + 4 * h2);
         }
       };
+#endif
+      // The first half (G^T chunk c2 = 0) is computed before the FFN-down; the second half between the c2 = 0
+      // MFMAs, which do not need it
+#if !PDM_FFN_UP16
       gelu_half(0);
+#endif
       // FFN-down: y^T[rb][db] += W2[db rows, chunk c] . G[rb]^T; chunk c2 of G^T holds hidden units
       // 16*c2 + hf*8 + 0..7, piece 2*c2 + hf of W2 row d, stored at (2*c2 + hf) ^ ((d >> 2) & 3)
       const char* w2 = sW2[k];
