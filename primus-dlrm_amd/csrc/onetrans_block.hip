@@ -223,10 +223,20 @@ __device__ __forceinline__ int ns_tile_xcd_major(const GemmArgs& a, int mt) {
   return mt;  // not reached
 }
 
+// LDS stages of gemm_kernel: 2 (double buffer, two workgroups per CU) or 1 (the next step waits in
+// registers; up to four workgroups per CU), and the workgroups per CU its registers are sized for
+#ifndef PDM_GEMM_STAGES
+#define PDM_GEMM_STAGES 1
+#endif
+#ifndef PDM_GEMM_WPS
+#define PDM_GEMM_WPS 4
+#endif
+constexpr int kGemmStages = PDM_GEMM_STAGES;
+
 template <int EPI>
-__global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t sA[2][GBM][GBK + GPAD];
-  __shared__ __attribute__((aligned(16))) uint16_t sB[2][GBN][GBK + GPAD];
+__global__ __launch_bounds__(256, kGemmStages == 1 ? PDM_GEMM_WPS : 2) void gemm_kernel(GemmArgs a) {
+  __shared__ __attribute__((aligned(16))) uint16_t sA[kGemmStages][GBM][GBK + GPAD];
+  __shared__ __attribute__((aligned(16))) uint16_t sB[kGemmStages][GBN][GBK + GPAD];
   __shared__ int s_rb[GBM];  // sample of tile row i, -1 = no row
   __shared__ int s_rt[GBM];  // token of tile row i
 
@@ -256,25 +266,27 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
     }
   }
 
-  // global -> LDS assignment: 8 threads x 16 B per 64-element row slice, 32 rows per pass
+  // global -> LDS assignment: 8 threads x 16 B per 64-element row slice, 32 rows per pass.  Rows are 32-bit
+  // element offsets from the tile's first row (-1: no row), which launch_gemm bounds.
   const int lr = tid >> 3, lc = (tid & 7) * 8;
-  const uint16_t* arow[4];
-  const uint16_t* wrow[4];
+  const int b0 = s_rb[0];  // row 0 of every tile is a row
+  const uint16_t* abase = a.A + (int64_t)b0 * a.a_bstride;
+  int aoff[4], woff[4];
 #pragma unroll
   for (int p = 0; p < 4; ++p) {
     const int i = p * 32 + lr;
     const int b = s_rb[i];
-    arow[p] = b >= 0 ? a.A + (int64_t)b * a.a_bstride + (int64_t)s_rt[i] * a.K + lc : nullptr;
+    aoff[p] = b >= 0 ? (int)((int64_t)(b - b0) * a.a_bstride + (int64_t)s_rt[i] * a.K + lc) : -1;
     const int n = n0 + i;
-    wrow[p] = n < a.N ? W + (int64_t)n * a.K + lc : nullptr;
+    woff[p] = n < a.N ? n * a.K + lc : -1;
   }
 
   u32x4_t ra[4], rb[4];
   auto gload = [&](int k0) {
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
-      ra[p] = arow[p] ? *reinterpret_cast<const u32x4_t*>(arow[p] + k0) : u32x4_t{0, 0, 0, 0};
-      rb[p] = wrow[p] ? *reinterpret_cast<const u32x4_t*>(wrow[p] + k0) : u32x4_t{0, 0, 0, 0};
+      ra[p] = aoff[p] >= 0 ? *reinterpret_cast<const u32x4_t*>(abase + aoff[p] + k0) : u32x4_t{0, 0, 0, 0};
+      rb[p] = woff[p] >= 0 ? *reinterpret_cast<const u32x4_t*>(W + woff[p] + k0) : u32x4_t{0, 0, 0, 0};
     }
   };
   auto sstore = [&](int buf) {
@@ -299,7 +311,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
   __syncthreads();
   const int fr = lane & 31, fk = (lane >> 5) * 8;
   for (int kt = 0; kt < nk; ++kt) {
-    const int buf = kt & 1;
+    const int buf = kGemmStages == 1 ? 0 : kt & 1;
     if (kt + 1 < nk) gload((kt + 1) * GBK);
 #pragma unroll
     for (int ks = 0; ks < GBK / 16; ++ks) {
@@ -313,7 +325,12 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
 #pragma unroll
         for (int j = 0; j < 2; ++j) acc[i][j] = mfma32x32x16(af[i], bf[j], acc[i][j]);
     }
-    if (kt + 1 < nk) sstore(buf ^ 1);
+    if constexpr (kGemmStages == 1) {
+      __syncthreads();  // every wave is done with the step's tile
+      if (kt + 1 < nk) sstore(0);
+    } else if (kt + 1 < nk) {
+      sstore(buf ^ 1);
+    }
     __syncthreads();
   }
 
@@ -1833,6 +1850,9 @@ static int launch_gemm(GemmArgs& g, hipStream_t s) {
   gemm_tiles(g);
   if (g.total_blocks == 0) return PDM_OK;
   PDM_CHECK_ARG(g.total_blocks < (int64_t(1) << 31), "GEMM grid too large");
+  // 32-bit element offsets of a tile's A rows from its first row, and of the weight rows
+  PDM_CHECK_ARG((int64_t)GBM * g.a_bstride + g.a_bstride < (int64_t(1) << 31), "GEMM rows too far apart");
+  PDM_CHECK_ARG((int64_t)g.N * g.K < (int64_t(1) << 31), "GEMM weight too large");
   hipLaunchKernelGGL(gemm_kernel<EPI>, dim3((unsigned)g.total_blocks), dim3(256), 0, s, g);
   PDM_CHECK_LAUNCH();
   return PDM_OK;
