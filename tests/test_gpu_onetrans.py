@@ -151,12 +151,14 @@ def test_block_ns_tiles_cross_tokens(pdm, dev):
     _run_case(pdm, dev, 1100, 49, 20, 16, seed=13, norm_std=0.1)
 
 
-@pytest.mark.parametrize("B,kv,q_len", [
-    (2, 720, 300),       # above the LDS-resident attention's 608 keys: the streaming attention kernel
-    (1, 1516, 1516),     # the reference OneTransL's first layer (L_S = 1500 + 16 NS, full causal)
+@pytest.mark.parametrize("B,kv,q_len,D", [
+    (2, 720, 300, 256),    # above the LDS-resident attention's 608 keys: the streaming attention kernel
+    (1, 1516, 1516, 256),  # the reference OneTransL's first layer (L_S = 1500 + 16 NS, full causal)
+    (3, 1000, 700, 384),   # 6 heads: 18 (sample, head) pairs x 3 query blocks of 256, the last partial
+    (2, 650, 650, 384),    # just above 608 keys, full causal, tiled d_model 384 path
 ])
-def test_block_long_sequence_streaming_attention(pdm, dev, B, kv, q_len):
-    _run_case(pdm, dev, B, kv, q_len, 16, seed=kv, norm_std=0.1)
+def test_block_long_sequence_streaming_attention(pdm, dev, B, kv, q_len, D):
+    _run_case(pdm, dev, B, kv, q_len, 16, D=D, F=4 * D, seed=kv, norm_std=0.1)
 
 
 def _load_block(blk, w):
@@ -172,15 +174,16 @@ def _load_block(blk, w):
         blk.ffn.ns_w2.copy_(w["ns_w2"])
 
 
-@pytest.mark.parametrize("B,L_S,schedule", [
-    (16, 384, [384, 256, 128, 64]),   # the benchmark's 4-layer pyramid: (kv, q) = (400,400),(400,272),(272,144),(144,80)
-    (4, 96, [96, 64, 32, 0]),         # down to the NS tokens only
+@pytest.mark.parametrize("B,L_S,schedule,D", [
+    (16, 384, [384, 256, 128, 64], 256),  # the benchmark's 4-layer pyramid: (kv, q) = (400,400),(400,272),(272,144),(144,80)
+    (4, 96, [96, 64, 32, 0], 256),        # down to the NS tokens only
+    (2, 984, [984, 656, 328, 0], 384),    # d_model 384, 6 heads: streaming attention at kv 1000 and 672, then LDS
 ])
-def test_stack_pyramid_matches_oracle(pdm, dev, B, L_S, schedule):
+def test_stack_pyramid_matches_oracle(pdm, dev, B, L_S, schedule, D):
     """OneTransStack (the block loop of onetrans.py:568-582) with an explicit schedule.  Each layer is
     checked element-wise against the oracle on the GPU's own input to that layer; the stack's output
     equals the chained layers bit for bit, and stays within 1e-2 (relative L2) of the oracle's stack."""
-    D, F, n_ns, H = 256, 1024, 16, 4
+    F, n_ns, H = 4 * D, 16, D // 64
     stack = pdm.OneTransStack(D, H, n_ns, len(schedule), schedule=schedule).to(dev).eval()
     layers = []
     for i, blk in enumerate(stack.blocks):
