@@ -235,8 +235,12 @@ constexpr int kGemmStages = PDM_GEMM_STAGES;
 
 template <int EPI>
 __global__ __launch_bounds__(256, kGemmStages == 1 ? PDM_GEMM_WPS : 2) void gemm_kernel(GemmArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t sA[kGemmStages][GBM][GBK + GPAD];
-  __shared__ __attribute__((aligned(16))) uint16_t sB[kGemmStages][GBN][GBK + GPAD];
+  // the A and W tiles; after the k loop the Q/K/V epilogue stages a V^T tile (128 x 136 bf16) in the same bytes
+  constexpr int kTileElems = kGemmStages * GBM * (GBK + GPAD);
+  static_assert(2 * kTileElems >= GBN * (GBM + 8), "the V^T staging tile must fit in the A and W tiles");
+  __shared__ __attribute__((aligned(16))) uint16_t sAB[2 * kTileElems];
+  uint16_t (*sA)[GBM][GBK + GPAD] = reinterpret_cast<uint16_t (*)[GBM][GBK + GPAD]>(sAB);
+  uint16_t (*sB)[GBN][GBK + GPAD] = reinterpret_cast<uint16_t (*)[GBN][GBK + GPAD]>(sAB + kTileElems);
   __shared__ int s_rb[GBM];  // sample of tile row i, -1 = no row
   __shared__ int s_rt[GBM];  // token of tile row i
 
@@ -336,6 +340,42 @@ __global__ __launch_bounds__(256, kGemmStages == 1 ? PDM_GEMM_WPS : 2) void gemm
 
   // epilogue: acc[i][j][e] is row wm*64 + i*32 + (e/4)*8 + (lane/32)*4 + e%4, column n0 + wn*64 + j*32 + lane%32
   const int hf = lane >> 5;
+  if constexpr (EPI == EPI_QKV) {
+    if (n0 >= 2 * a.D) {
+      // a V tile (2 D is a multiple of 128): V^T rows (b, h, d) are contiguous in t, so the tile goes through
+      // LDS transposed, sT[column][row], and each store instruction writes 64 consecutive rows of one column
+      // (consecutive t of one sample) instead of one element of 64 columns.  The k loop ended with a barrier.
+      constexpr int TS = GBM + 8;  // sT row stride (bf16)
+      uint16_t* sT = sAB;
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int e = 0; e < 16; e += 2) {
+            const int row = wm * 64 + i * 32 + (e >> 2) * 8 + hf * 4 + (e & 3);
+            const int col = wn * 64 + j * 32 + fr;
+            *reinterpret_cast<uint32_t*>(sT + col * TS + row) = pack_bf16x2(acc[i][j][e], acc[i][j][e + 1]);
+          }
+      __syncthreads();
+      const int H = a.D >> 6;
+#pragma unroll 4
+      for (int cc = 0; cc < 32; ++cc) {
+        const int col = wave * 32 + cc;
+        const int c = n0 + col - 2 * a.D;
+        if (n0 + col >= a.N) break;  // wave-uniform
+        const int h = c >> 6, d = c & 63;
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+          const int row = half * 64 + lane;
+          const int b = s_rb[row];
+          if (b >= 0)
+            a.vt[(((int64_t)b * H + h) * 64 + d) * a.kv_pad + s_rt[row]] = sT[col * TS + row];
+        }
+      }
+      return;
+    }
+  }
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
 #pragma unroll
