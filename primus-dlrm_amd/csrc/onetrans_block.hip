@@ -232,17 +232,25 @@ __device__ __forceinline__ int ns_tile_xcd_major(const GemmArgs& a, int mt) {
 #define PDM_GEMM_WPS 4
 #endif
 constexpr int kGemmStages = PDM_GEMM_STAGES;
+// rows per tile of gemm_kernel: 128 (4 waves) or 256 (8 waves, each wave still 64 x 64)
+#ifndef PDM_GEMM_TM
+#define PDM_GEMM_TM 256
+#endif
 
-template <int EPI>
-__global__ __launch_bounds__(256, kGemmStages == 1 ? PDM_GEMM_WPS : 2) void gemm_kernel(GemmArgs a) {
-  // the A and W tiles; after the k loop the Q/K/V epilogue stages a V^T tile (128 x 136 bf16) in the same bytes
-  constexpr int kTileElems = kGemmStages * GBM * (GBK + GPAD);
-  static_assert(2 * kTileElems >= GBN * (GBM + 8), "the V^T staging tile must fit in the A and W tiles");
-  __shared__ __attribute__((aligned(16))) uint16_t sAB[2 * kTileElems];
-  uint16_t (*sA)[GBM][GBK + GPAD] = reinterpret_cast<uint16_t (*)[GBM][GBK + GPAD]>(sAB);
-  uint16_t (*sB)[GBN][GBK + GPAD] = reinterpret_cast<uint16_t (*)[GBN][GBK + GPAD]>(sAB + kTileElems);
-  __shared__ int s_rb[GBM];  // sample of tile row i, -1 = no row
-  __shared__ int s_rt[GBM];  // token of tile row i
+template <int EPI, int TM>
+__global__ __launch_bounds__(TM * 2, kGemmStages == 1 ? (TM == GBM ? PDM_GEMM_WPS : 4) : 2) void gemm_kernel(GemmArgs a) {
+  constexpr int NT = TM * 2;                 // threads: TM / 64 x 2 waves
+  constexpr int RPP = NT / 8;                // tile rows per pass of 16-byte loads
+  constexpr int PA = TM / RPP, PB = GBN / RPP;  // passes of the A and W tiles
+  // the A and W tiles; after the k loop the Q/K/V epilogue stages V^T (128 x 136 bf16 per 128 rows) in the
+  // same bytes
+  constexpr int kAElems = kGemmStages * TM * (GBK + GPAD), kBElems = kGemmStages * GBN * (GBK + GPAD);
+  static_assert(kAElems + kBElems >= GBN * (GBM + 8), "the V^T staging tile must fit in the A and W tiles");
+  __shared__ __attribute__((aligned(16))) uint16_t sAB[kAElems + kBElems];
+  uint16_t (*sA)[TM][GBK + GPAD] = reinterpret_cast<uint16_t (*)[TM][GBK + GPAD]>(sAB);
+  uint16_t (*sB)[GBN][GBK + GPAD] = reinterpret_cast<uint16_t (*)[GBN][GBK + GPAD]>(sAB + kAElems);
+  __shared__ int s_rb[TM];  // sample of tile row i, -1 = no row
+  __shared__ int s_rt[TM];  // token of tile row i
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -257,7 +265,7 @@ __global__ __launch_bounds__(256, kGemmStages == 1 ? PDM_GEMM_WPS : 2) void gemm
   const int n0 = (int)(bid - (int64_t)mt * a.n_tiles) * GBN;
 
   const uint16_t* W = a.W;
-  if (tid < GBM) tile_row(a, mt, GBM, tid, s_rb[tid], s_rt[tid]);
+  if (tid < TM) tile_row(a, mt, TM, tid, s_rb[tid], s_rt[tid]);
   if (mt >= a.tiles_s) W = a.W_ns + (int64_t)((mt - a.tiles_s) / a.tiles_b) * a.N * a.K;
   __syncthreads();
 
@@ -265,40 +273,43 @@ __global__ __launch_bounds__(256, kGemmStages == 1 ? PDM_GEMM_WPS : 2) void gemm
     // Q columns of S-token rows outside the kept tail are never read: skip the tile
     if (n0 < a.D) {
       const int thr = a.kv - a.q_len;
-      const int need = (tid < GBM && s_rb[tid] >= 0 && s_rt[tid] >= thr) ? 1 : 0;
+      const int need = (tid < TM && s_rb[tid] >= 0 && s_rt[tid] >= thr) ? 1 : 0;
       if (!__syncthreads_or(need)) return;
     }
   }
 
-  // global -> LDS assignment: 8 threads x 16 B per 64-element row slice, 32 rows per pass.  Rows are 32-bit
+  // global -> LDS assignment: 8 threads x 16 B per 64-element row slice, RPP rows per pass.  Rows are 32-bit
   // element offsets from the tile's first row (-1: no row), which launch_gemm bounds.
   const int lr = tid >> 3, lc = (tid & 7) * 8;
   const int b0 = s_rb[0];  // row 0 of every tile is a row
   const uint16_t* abase = a.A + (int64_t)b0 * a.a_bstride;
-  int aoff[4], woff[4];
+  int aoff[PA], woff[PB];
 #pragma unroll
-  for (int p = 0; p < 4; ++p) {
-    const int i = p * 32 + lr;
+  for (int p = 0; p < PA; ++p) {
+    const int i = p * RPP + lr;
     const int b = s_rb[i];
     aoff[p] = b >= 0 ? (int)((int64_t)(b - b0) * a.a_bstride + (int64_t)s_rt[i] * a.K + lc) : -1;
-    const int n = n0 + i;
+  }
+#pragma unroll
+  for (int p = 0; p < PB; ++p) {
+    const int n = n0 + p * RPP + lr;
     woff[p] = n < a.N ? n * a.K + lc : -1;
   }
 
-  u32x4_t ra[4], rb[4];
+  u32x4_t ra[PA], rb[PB];
   auto gload = [&](int k0) {
 #pragma unroll
-    for (int p = 0; p < 4; ++p) {
+    for (int p = 0; p < PA; ++p)
       ra[p] = aoff[p] >= 0 ? *reinterpret_cast<const u32x4_t*>(abase + aoff[p] + k0) : u32x4_t{0, 0, 0, 0};
+#pragma unroll
+    for (int p = 0; p < PB; ++p)
       rb[p] = woff[p] >= 0 ? *reinterpret_cast<const u32x4_t*>(W + woff[p] + k0) : u32x4_t{0, 0, 0, 0};
-    }
   };
   auto sstore = [&](int buf) {
 #pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      *reinterpret_cast<u32x4_t*>(&sA[buf][p * 32 + lr][lc]) = ra[p];
-      *reinterpret_cast<u32x4_t*>(&sB[buf][p * 32 + lr][lc]) = rb[p];
-    }
+    for (int p = 0; p < PA; ++p) *reinterpret_cast<u32x4_t*>(&sA[buf][p * RPP + lr][lc]) = ra[p];
+#pragma unroll
+    for (int p = 0; p < PB; ++p) *reinterpret_cast<u32x4_t*>(&sB[buf][p * RPP + lr][lc]) = rb[p];
   };
 
   f32x16_t acc[2][2];
@@ -345,33 +356,41 @@ __global__ __launch_bounds__(256, kGemmStages == 1 ? PDM_GEMM_WPS : 2) void gemm
       // a V tile (2 D is a multiple of 128): V^T rows (b, h, d) are contiguous in t, so the tile goes through
       // LDS transposed, sT[column][row], and each store instruction writes 64 consecutive rows of one column
       // (consecutive t of one sample) instead of one element of 64 columns.  The k loop ended with a barrier.
+      // 128 rows at a time (TM / 128 rounds)
       constexpr int TS = GBM + 8;  // sT row stride (bf16)
+      constexpr int CPW = GBN / (NT / 64);  // columns written out per wave
       uint16_t* sT = sAB;
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-          for (int e = 0; e < 16; e += 2) {
-            const int row = wm * 64 + i * 32 + (e >> 2) * 8 + hf * 4 + (e & 3);
-            const int col = wn * 64 + j * 32 + fr;
-            *reinterpret_cast<uint32_t*>(sT + col * TS + row) = pack_bf16x2(acc[i][j][e], acc[i][j][e + 1]);
-          }
-      __syncthreads();
       const int H = a.D >> 6;
-#pragma unroll 4
-      for (int cc = 0; cc < 32; ++cc) {
-        const int col = wave * 32 + cc;
-        const int c = n0 + col - 2 * a.D;
-        if (n0 + col >= a.N) break;  // wave-uniform
-        const int h = c >> 6, d = c & 63;
 #pragma unroll
-        for (int half = 0; half < 2; ++half) {
-          const int row = half * 64 + lane;
-          const int b = s_rb[row];
-          if (b >= 0)
-            a.vt[(((int64_t)b * H + h) * 64 + d) * a.kv_pad + s_rt[row]] = sT[col * TS + row];
+      for (int hv = 0; hv < TM / GBM; ++hv) {
+        if (wm / 2 == hv) {
+#pragma unroll
+          for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+              for (int e = 0; e < 16; e += 2) {
+                const int row = (wm & 1) * 64 + i * 32 + (e >> 2) * 8 + hf * 4 + (e & 3);
+                const int col = wn * 64 + j * 32 + fr;
+                *reinterpret_cast<uint32_t*>(sT + col * TS + row) = pack_bf16x2(acc[i][j][e], acc[i][j][e + 1]);
+              }
         }
+        __syncthreads();
+#pragma unroll 4
+        for (int cc = 0; cc < CPW; ++cc) {
+          const int col = wave * CPW + cc;
+          const int c = n0 + col - 2 * a.D;
+          if (n0 + col >= a.N) break;  // wave-uniform
+          const int h = c >> 6, d = c & 63;
+#pragma unroll
+          for (int half = 0; half < 2; ++half) {
+            const int row = half * 64 + lane;
+            const int b = s_rb[hv * GBM + row];
+            if (b >= 0)
+              a.vt[(((int64_t)b * H + h) * 64 + d) * a.kv_pad + s_rt[hv * GBM + row]] = sT[col * TS + row];
+          }
+        }
+        __syncthreads();  // sT is read before the next round writes it
       }
       return;
     }
@@ -1887,13 +1906,17 @@ static void gemm_tiles(GemmArgs& g) {
 
 template <int EPI>
 static int launch_gemm(GemmArgs& g, hipStream_t s) {
-  gemm_tiles(g);
+  constexpr int TM = PDM_GEMM_TM;
+  g.tiles_s = (int)(((int64_t)g.B * g.n_s + TM - 1) / TM);
+  g.tiles_b = (g.B + TM - 1) / TM;
+  g.n_tiles = (g.N + GBN - 1) / GBN;
+  g.total_blocks = ((int64_t)g.tiles_s + (int64_t)g.n_ns * g.tiles_b) * g.n_tiles;
   if (g.total_blocks == 0) return PDM_OK;
   PDM_CHECK_ARG(g.total_blocks < (int64_t(1) << 31), "GEMM grid too large");
   // 32-bit element offsets of a tile's A rows from its first row, and of the weight rows
-  PDM_CHECK_ARG((int64_t)GBM * g.a_bstride + g.a_bstride < (int64_t(1) << 31), "GEMM rows too far apart");
+  PDM_CHECK_ARG((int64_t)TM * g.a_bstride + g.a_bstride < (int64_t(1) << 31), "GEMM rows too far apart");
   PDM_CHECK_ARG((int64_t)g.N * g.K < (int64_t(1) << 31), "GEMM weight too large");
-  hipLaunchKernelGGL(gemm_kernel<EPI>, dim3((unsigned)g.total_blocks), dim3(256), 0, s, g);
+  hipLaunchKernelGGL((gemm_kernel<EPI, TM>), dim3((unsigned)g.total_blocks), dim3(TM * 2), 0, s, g);
   PDM_CHECK_LAUNCH();
   return PDM_OK;
 }
