@@ -64,16 +64,18 @@ def test_int8_mean_full_size_sampled_bags(pdm, dev):
     torch.cuda.empty_cache()
 
 
-def test_onetrans_stack_b1024_sampled_samples(pdm, dev):
-    D, F, n_ns, H, B = 256, 1024, 16, 4, 1024
-    schedule = [384, 256, 128, 64]
-    layers = [ot.random_weights(D, F, n_ns, std=0.02, seed=300 + i, norm_std=0.1) for i in range(len(schedule))]
-    x = torch.randn(B, schedule[0] + n_ns, D, generator=torch.Generator().manual_seed(9))
-    sample = torch.from_numpy(np.sort(np.random.default_rng(34).choice(B, 16, replace=False)))
+def _stack_sampled(pdm, dev, D, F, n_ns, B, schedule, n_sample, seed):
+    """The full-batch stack on the GPU, layer by layer; each layer's K, V, attention output and update of
+    n_sample sampled samples checked against the oracle on the GPU's own input to that layer, then the
+    whole stack in one call equal to the chained layers bit for bit."""
+    H = D // 64
+    layers = [ot.random_weights(D, F, n_ns, std=0.02, seed=seed + i, norm_std=0.1) for i in range(len(schedule))]
+    x = torch.randn(B, schedule[0] + n_ns, D, generator=torch.Generator().manual_seed(seed))
+    sample = torch.from_numpy(np.sort(np.random.default_rng(seed + 25).choice(B, n_sample, replace=False)))
     h = x
     for i, (w, q_s) in enumerate(zip(layers, schedule)):
         kv, q_len = h.shape[1], q_s + n_ns
-        print(f"stack layer {i}: B={B} kv={kv} q_len={q_len}, 16 sampled samples", flush=True)
+        print(f"stack layer {i}: B={B} kv={kv} q_len={q_len} D={D}, {n_sample} sampled samples", flush=True)
         layout = pdm.ops.onetrans_workspace_layout(B, kv, q_len, D, F)
         ws = torch.empty(layout["total"][0], dtype=torch.uint8, device=dev)
         got = pdm.ops.onetrans_block_raw(h.to(dev), _gpu_weights(w, dev), H, q_len, workspace=ws)
@@ -95,10 +97,22 @@ def test_onetrans_stack_b1024_sampled_samples(pdm, dev):
         _close(f"layer {i} update y - x_tail", got[sample] - tail, want - tail, terms["y"])
         h = got
         del ws
-    stack = pdm.OneTransStack(D, H, n_ns, len(schedule), schedule=schedule).to(dev).eval()
+    stack = pdm.OneTransStack(D, H, n_ns, len(schedule), ffn_mult=F // D, schedule=schedule).to(dev).eval()
     for blk, w in zip(stack.blocks, layers):
         _load_block(blk, w)
     with torch.no_grad():
         out = stack(x.to(dev)).cpu()
     assert torch.equal(out, h)
+    del stack, out
     torch.cuda.empty_cache()
+
+
+def test_onetrans_stack_b1024_sampled_samples(pdm, dev):
+    """The benchmark's 4-layer stack at B = 1024 (3,200 FFN row tiles per layer at kv 400)."""
+    _stack_sampled(pdm, dev, 256, 1024, 16, 1024, [384, 256, 128, 64], 16, 300)
+
+
+def test_onetransl_stack_b1024_sampled_samples(pdm, dev):
+    """The reference's OneTransL shape at B = 1024: d_model 384 (tiled path), 1516 tokens, the 8-layer pyramid
+    1500 -> 16; layers 0-5 run the streaming attention (kv 1516 .. 668)."""
+    _stack_sampled(pdm, dev, 384, 1536, 16, 1024, [1500, 1288, 1076, 864, 652, 440, 228, 16], 4, 700)
