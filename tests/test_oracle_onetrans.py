@@ -155,7 +155,7 @@ def test_autocast_mode_close_to_fp64_and_rounds_like_bf16():
 
     # the 4-layer benchmark stack: B=1024, L_S=384, 16 NS, d 256, FFN 1024, schedule 384/256/128/64
 def test_block_flops_reference_convention():
-    # BASELINE workload: B=1024, L_S=384, 16 NS, d 256, FFN 1024, schedule 384/256/128/64
+    # the benchmark workload: B=1024, L_S=384, 16 NS, d 256, FFN 1024, schedule 384/256/128/64
     tot, kv = 0.0, 400
     for q_s in (384, 256, 128, 64):
         tot += ot.block_flops(1024, kv, q_s + 16, 256, 1024, 16)
