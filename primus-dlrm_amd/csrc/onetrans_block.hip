@@ -236,6 +236,11 @@ constexpr int kGemmStages = PDM_GEMM_STAGES;
 #ifndef PDM_GEMM_TM
 #define PDM_GEMM_TM 256
 #endif
+// PDM_GEMM_STAGED_EPI: the residual and GELU epilogues write 64-row slices of the tile through LDS as
+// 16-byte / 8-byte row segments
+#ifndef PDM_GEMM_STAGED_EPI
+#define PDM_GEMM_STAGED_EPI 1
+#endif
 
 template <int EPI, int TM>
 __global__ __launch_bounds__(TM * 2, kGemmStages == 1 ? (TM == GBM ? PDM_GEMM_WPS : 4) : 2) void gemm_kernel(GemmArgs a) {
@@ -395,6 +400,57 @@ __global__ __launch_bounds__(TM * 2, kGemmStages == 1 ? (TM == GBM ? PDM_GEMM_WP
       return;
     }
   }
+#if PDM_GEMM_STAGED_EPI
+  if constexpr (EPI == EPI_RESID || EPI == EPI_GELU) {
+    if (n0 + GBN <= a.N && (a.N & 3) == 0) {
+      // 64 rows at a time through LDS (fp32, rows of 128 + 4): the two waves that hold them write their
+      // accumulators, then every thread finishes 4 consecutive outputs of a row with one 16-byte residual read
+      // and one 16-byte (fp32) or 8-byte (bf16) store.  The k loop ended with a barrier.
+      constexpr int OS = GBN + 4;  // sO row stride (floats)
+      static_assert((kAElems + kBElems) * 2 >= 64 * OS * 4, "the staging rows must fit in the A and W tiles");
+      float* sO = reinterpret_cast<float*>(sAB);
+#pragma unroll
+      for (int rr = 0; rr < TM / 64; ++rr) {
+        if (wm == rr) {
+#pragma unroll
+          for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+              for (int e = 0; e < 16; ++e)
+                sO[(i * 32 + (e >> 2) * 8 + hf * 4 + (e & 3)) * OS + wn * 64 + j * 32 + fr] = acc[i][j][e];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int it = 0; it < 64 * (GBN / 4) / NT; ++it) {
+          const int idx = it * NT + tid;
+          const int rl = idx / (GBN / 4), c4 = idx % (GBN / 4);
+          const int row = rr * 64 + rl;
+          const int b = s_rb[row];
+          if (b < 0) continue;
+          const int t = s_rt[row];
+          const f32x4_t v = *reinterpret_cast<const f32x4_t*>(sO + rl * OS + c4 * 4);
+          const int64_t o = (int64_t)b * a.out_bstride + (int64_t)t * a.N + n0 + c4 * 4;
+          if constexpr (EPI == EPI_RESID) {
+            const f32x4_t r = *reinterpret_cast<const f32x4_t*>(
+                a.res + (int64_t)b * a.res_bstride + (int64_t)(t + a.res_toff) * a.N + n0 + c4 * 4);
+            *reinterpret_cast<f32x4_t*>(reinterpret_cast<float*>(a.out) + o) =
+                f32x4_t{bf16_round(v[0]) + r[0], bf16_round(v[1]) + r[1], bf16_round(v[2]) + r[2],
+                        bf16_round(v[3]) + r[3]};
+          } else {
+            *reinterpret_cast<u32x2_t*>(reinterpret_cast<uint16_t*>(a.out) + o) =
+                u32x2_t{(uint32_t)bf16_bits(gelu_erf(bf16_round(v[0]))) |
+                            ((uint32_t)bf16_bits(gelu_erf(bf16_round(v[1]))) << 16),
+                        (uint32_t)bf16_bits(gelu_erf(bf16_round(v[2]))) |
+                            ((uint32_t)bf16_bits(gelu_erf(bf16_round(v[3]))) << 16)};
+          }
+        }
+        __syncthreads();  // sO is read before the next round writes it
+      }
+      return;
+    }
+  }
+#endif
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
 #pragma unroll
