@@ -401,7 +401,9 @@ __global__ __launch_bounds__(TM * 2, kGemmStages == 1 ? (TM == GBM ? PDM_GEMM_WP
     }
   }
 #if PDM_GEMM_STAGED_EPI
-  if constexpr (EPI == EPI_RESID || EPI == EPI_GELU) {
+  if constexpr (EPI == EPI_RESID || EPI == EPI_GELU || EPI == EPI_QKV) {
+    // (the Q/K/V GEMM's V tiles returned above: here its tiles are all Q or all K columns, D being a multiple
+    // of 128)
     if (n0 + GBN <= a.N && (a.N & 3) == 0) {
       // 64 rows at a time through LDS (fp32, rows of 128 + 4): the two waves that hold them write their
       // accumulators, then every thread finishes 4 consecutive outputs of a row with one 16-byte residual read
@@ -437,6 +439,17 @@ __global__ __launch_bounds__(TM * 2, kGemmStages == 1 ? (TM == GBM ? PDM_GEMM_WP
             *reinterpret_cast<f32x4_t*>(reinterpret_cast<float*>(a.out) + o) =
                 f32x4_t{bf16_round(v[0]) + r[0], bf16_round(v[1]) + r[1], bf16_round(v[2]) + r[2],
                         bf16_round(v[3]) + r[3]};
+          } else if constexpr (EPI == EPI_QKV) {
+            const int n = n0 + c4 * 4;
+            uint16_t* dst;
+            if (n < a.D) {
+              const int tq = t - (a.kv - a.q_len);
+              if (tq < 0) continue;  // Q of a row outside the kept tail is never read
+              dst = a.q + ((int64_t)b * a.q_len + tq) * a.D + n;
+            } else {
+              dst = a.k + ((int64_t)b * a.kv + t) * a.D + (n - a.D);
+            }
+            *reinterpret_cast<u32x2_t*>(dst) = u32x2_t{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
           } else {
             *reinterpret_cast<u32x2_t*>(reinterpret_cast<uint16_t*>(a.out) + o) =
                 u32x2_t{(uint32_t)bf16_bits(gelu_erf(bf16_round(v[0]))) |
