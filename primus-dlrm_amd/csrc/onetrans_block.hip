@@ -404,11 +404,12 @@ __global__ __launch_bounds__(TM * 2, kGemmStages == 1 ? (TM == GBM ? PDM_GEMM_WP
   if constexpr (EPI == EPI_RESID || EPI == EPI_GELU || EPI == EPI_QKV) {
     // (the Q/K/V GEMM's V tiles returned above: here its tiles are all Q or all K columns, D being a multiple
     // of 128)
-    if (n0 + GBN <= a.N && (a.N & 3) == 0) {
+    if (n0 + GBN <= a.N && (a.N & 7) == 0) {
       // 64 rows at a time through LDS (fp32, rows of 128 + 4): the two waves that hold them write their
-      // accumulators, then every thread finishes 4 consecutive outputs of a row with one 16-byte residual read
-      // and one 16-byte (fp32) or 8-byte (bf16) store.  The k loop ended with a barrier.
+      // accumulators, then every thread finishes VPT consecutive outputs of a row: 4 fp32 with one 16-byte
+      // residual read and one 16-byte store, or 8 bf16 with one 16-byte store.  The k loop ended with a barrier.
       constexpr int OS = GBN + 4;  // sO row stride (floats)
+      constexpr int VPT = EPI == EPI_RESID ? 4 : 8;
       static_assert((kAElems + kBElems) * 2 >= 64 * OS * 4, "the staging rows must fit in the A and W tiles");
       float* sO = reinterpret_cast<float*>(sAB);
 #pragma unroll
@@ -424,38 +425,45 @@ __global__ __launch_bounds__(TM * 2, kGemmStages == 1 ? (TM == GBM ? PDM_GEMM_WP
         }
         __syncthreads();
 #pragma unroll
-        for (int it = 0; it < 64 * (GBN / 4) / NT; ++it) {
+        for (int it = 0; it < 64 * (GBN / VPT) / NT; ++it) {
           const int idx = it * NT + tid;
-          const int rl = idx / (GBN / 4), c4 = idx % (GBN / 4);
+          const int rl = idx / (GBN / VPT), cv = idx % (GBN / VPT);
           const int row = rr * 64 + rl;
           const int b = s_rb[row];
           if (b < 0) continue;
           const int t = s_rt[row];
-          const f32x4_t v = *reinterpret_cast<const f32x4_t*>(sO + rl * OS + c4 * 4);
-          const int64_t o = (int64_t)b * a.out_bstride + (int64_t)t * a.N + n0 + c4 * 4;
+          const int n = n0 + cv * VPT;
+          const f32x4_t v = *reinterpret_cast<const f32x4_t*>(sO + rl * OS + cv * VPT);
           if constexpr (EPI == EPI_RESID) {
             const f32x4_t r = *reinterpret_cast<const f32x4_t*>(
-                a.res + (int64_t)b * a.res_bstride + (int64_t)(t + a.res_toff) * a.N + n0 + c4 * 4);
-            *reinterpret_cast<f32x4_t*>(reinterpret_cast<float*>(a.out) + o) =
+                a.res + (int64_t)b * a.res_bstride + (int64_t)(t + a.res_toff) * a.N + n);
+            *reinterpret_cast<f32x4_t*>(reinterpret_cast<float*>(a.out) + (int64_t)b * a.out_bstride +
+                                        (int64_t)t * a.N + n) =
                 f32x4_t{bf16_round(v[0]) + r[0], bf16_round(v[1]) + r[1], bf16_round(v[2]) + r[2],
                         bf16_round(v[3]) + r[3]};
-          } else if constexpr (EPI == EPI_QKV) {
-            const int n = n0 + c4 * 4;
-            uint16_t* dst;
-            if (n < a.D) {
-              const int tq = t - (a.kv - a.q_len);
-              if (tq < 0) continue;  // Q of a row outside the kept tail is never read
-              dst = a.q + ((int64_t)b * a.q_len + tq) * a.D + n;
-            } else {
-              dst = a.k + ((int64_t)b * a.kv + t) * a.D + (n - a.D);
-            }
-            *reinterpret_cast<u32x2_t*>(dst) = u32x2_t{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
           } else {
-            *reinterpret_cast<u32x2_t*>(reinterpret_cast<uint16_t*>(a.out) + o) =
-                u32x2_t{(uint32_t)bf16_bits(gelu_erf(bf16_round(v[0]))) |
-                            ((uint32_t)bf16_bits(gelu_erf(bf16_round(v[1]))) << 16),
-                        (uint32_t)bf16_bits(gelu_erf(bf16_round(v[2]))) |
-                            ((uint32_t)bf16_bits(gelu_erf(bf16_round(v[3]))) << 16)};
+            const f32x4_t v2 = *reinterpret_cast<const f32x4_t*>(sO + rl * OS + cv * VPT + 4);
+            uint16_t* dst;
+            u32x4_t w;
+            if constexpr (EPI == EPI_QKV) {
+              if (n < a.D) {
+                const int tq = t - (a.kv - a.q_len);
+                if (tq < 0) continue;  // Q of a row outside the kept tail is never read
+                dst = a.q + ((int64_t)b * a.q_len + tq) * a.D + n;
+              } else {
+                dst = a.k + ((int64_t)b * a.kv + t) * a.D + (n - a.D);
+              }
+              w = u32x4_t{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v2[0], v2[1]),
+                          pack_bf16x2(v2[2], v2[3])};
+            } else {
+              dst = reinterpret_cast<uint16_t*>(a.out) + (int64_t)b * a.out_bstride + (int64_t)t * a.N + n;
+              auto g2 = [](float x0, float x1) {
+                return (uint32_t)bf16_bits(gelu_erf(bf16_round(x0))) |
+                       ((uint32_t)bf16_bits(gelu_erf(bf16_round(x1))) << 16);
+              };
+              w = u32x4_t{g2(v[0], v[1]), g2(v[2], v[3]), g2(v2[0], v2[1]), g2(v2[2], v2[3])};
+            }
+            *reinterpret_cast<u32x4_t*>(dst) = w;
           }
         }
         __syncthreads();  // sO is read before the next round writes it
