@@ -412,6 +412,11 @@ __global__ __launch_bounds__(TM * 2, kGemmStages == 1 ? (TM == GBM ? PDM_GEMM_WP
       constexpr int VPT = EPI == EPI_RESID ? 4 : 8;
       static_assert((kAElems + kBElems) * 2 >= 64 * OS * 4, "the staging rows must fit in the A and W tiles");
       float* sO = reinterpret_cast<float*>(sAB);
+      // GELU: the table of gelu_lut after the staging rows, filled once here (published by the first round's
+      // barrier, only read afterwards)
+      constexpr bool kLut = EPI == EPI_GELU && (kAElems + kBElems) * 2 >= (64 * OS + GELU_T_N) * 4;
+      float* const sG = sO + 64 * OS;
+      if constexpr (kLut) gelu_table_fill(sG, tid, NT);
 #pragma unroll
       for (int rr = 0; rr < TM / 64; ++rr) {
         if (wm == rr) {
@@ -457,11 +462,18 @@ __global__ __launch_bounds__(TM * 2, kGemmStages == 1 ? (TM == GBM ? PDM_GEMM_WP
                           pack_bf16x2(v2[2], v2[3])};
             } else {
               dst = reinterpret_cast<uint16_t*>(a.out) + (int64_t)b * a.out_bstride + (int64_t)t * a.N + n;
-              auto g2 = [](float x0, float x1) {
-                return (uint32_t)bf16_bits(gelu_erf(bf16_round(x0))) |
-                       ((uint32_t)bf16_bits(gelu_erf(bf16_round(x1))) << 16);
-              };
-              w = u32x4_t{g2(v[0], v[1]), g2(v[2], v[3]), g2(v2[0], v2[1]), g2(v2[2], v2[3])};
+              if constexpr (kLut) {
+                const float u8[8] = {v[0], v[1], v[2], v[3], v2[0], v2[1], v2[2], v2[3]};
+                uint32_t gw[4];
+                gelu_lut_pack<8>(sG, u8, gw);
+                w = u32x4_t{gw[0], gw[1], gw[2], gw[3]};
+              } else {
+                auto g2 = [](float x0, float x1) {
+                  return (uint32_t)bf16_bits(gelu_erf(bf16_round(x0))) |
+                         ((uint32_t)bf16_bits(gelu_erf(bf16_round(x1))) << 16);
+                };
+                w = u32x4_t{g2(v[0], v[1]), g2(v[2], v[3]), g2(v2[0], v2[1]), g2(v2[2], v2[3])};
+              }
             }
             *reinterpret_cast<u32x4_t*>(dst) = w;
           }
