@@ -359,11 +359,12 @@ __global__ __launch_bounds__(TM * 2, kGemmStages == 1 ? (TM == GBM ? PDM_GEMM_WP
   if constexpr (EPI == EPI_QKV) {
     if (n0 >= 2 * a.D) {
       // a V tile (2 D is a multiple of 128): V^T rows (b, h, d) are contiguous in t, so the tile goes through
-      // LDS transposed, sT[column][row], and each store instruction writes 64 consecutive rows of one column
-      // (consecutive t of one sample) instead of one element of 64 columns.  The k loop ended with a barrier.
-      // 128 rows at a time (TM / 128 rounds)
+      // LDS transposed, sT[column][row], and each thread stores 8 consecutive rows of one column (consecutive t
+      // of one sample) with one 16-byte store, or two 8-byte stores where t is a multiple of 4 but not of 8;
+      // 16 lanes cover the 128 rows of a column.  Runs of 8 rows that are not 8 consecutive tokens of one
+      // sample (sample boundaries, the NS groups, padding rows) store element by element.  The k loop ended
+      // with a barrier.  128 rows at a time (TM / 128 rounds).
       constexpr int TS = GBM + 8;  // sT row stride (bf16)
-      constexpr int CPW = GBN / (NT / 64);  // columns written out per wave
       uint16_t* sT = sAB;
       const int H = a.D >> 6;
 #pragma unroll
@@ -381,18 +382,32 @@ __global__ __launch_bounds__(TM * 2, kGemmStages == 1 ? (TM == GBM ? PDM_GEMM_WP
               }
         }
         __syncthreads();
-#pragma unroll 4
-        for (int cc = 0; cc < CPW; ++cc) {
-          const int col = wave * CPW + cc;
+        static_assert(GBN * (GBM / 8) % NT == 0, "pieces per thread");
+#pragma unroll 1
+        for (int it = 0; it < GBN * (GBM / 8) / NT; ++it) {
+          const int idx = it * NT + tid;
+          const int col = idx >> 4, r0 = (idx & 15) * 8;
+          if (n0 + col >= a.N) continue;
           const int c = n0 + col - 2 * a.D;
-          if (n0 + col >= a.N) break;  // wave-uniform
           const int h = c >> 6, d = c & 63;
+          const u32x4_t v = *reinterpret_cast<const u32x4_t*>(sT + col * TS + r0);
+          const int rr = hv * GBM + r0;
+          const int b = s_rb[rr], t = s_rt[rr];
+          if (b >= 0 && s_rb[rr + 7] == b && s_rt[rr + 7] == t + 7 && (t & 3) == 0 && (a.kv_pad & 7) == 0) {
+            uint16_t* dst = a.vt + (((int64_t)b * H + h) * 64 + d) * a.kv_pad + t;
+            if ((t & 7) == 0) {
+              *reinterpret_cast<u32x4_t*>(dst) = v;
+            } else {
+              *reinterpret_cast<u32x2_t*>(dst) = u32x2_t{v[0], v[1]};
+              *reinterpret_cast<u32x2_t*>(dst + 4) = u32x2_t{v[2], v[3]};
+            }
+          } else {
 #pragma unroll
-          for (int half = 0; half < 2; ++half) {
-            const int row = half * 64 + lane;
-            const int b = s_rb[hv * GBM + row];
-            if (b >= 0)
-              a.vt[(((int64_t)b * H + h) * 64 + d) * a.kv_pad + s_rt[hv * GBM + row]] = sT[col * TS + row];
+            for (int e = 0; e < 8; ++e) {
+              const int be = s_rb[rr + e];
+              if (be >= 0)
+                a.vt[(((int64_t)be * H + h) * 64 + d) * a.kv_pad + s_rt[rr + e]] = (uint16_t)(v[e >> 1] >> (16 * (e & 1)));
+            }
           }
         }
         __syncthreads();  // sT is read before the next round writes it
