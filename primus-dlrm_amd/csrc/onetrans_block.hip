@@ -1770,6 +1770,9 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_lds_kernel(AttnArgs a) {
 // share one L2, and the longest query block of a head first.
 // ---------------------------------------------------------------------------
 constexpr int kStreamKeys = 64;  // keys per LDS chunk
+#ifndef PDM_ATTN_STREAM_NW
+#define PDM_ATTN_STREAM_NW 8  // waves (32-query tiles) per workgroup
+#endif
 
 template <int NW>
 __global__ __launch_bounds__(NW * 64, 16 / NW) void attn_stream_kernel(AttnArgs a, int n_qb, int64_t n_items) {
@@ -2243,7 +2246,7 @@ static int block_fwd(const pdm_block_desc& d, const float* x, const pdm_block_we
       if (st != PDM_OK) return st;
     } else {
       // keys streamed through LDS in chunks, 8 waves (256 queries) per workgroup
-      constexpr int kNW = 8;
+      constexpr int kNW = PDM_ATTN_STREAM_NW;
       const int n_qb = (ql + 32 * kNW - 1) / (32 * kNW);
       const int64_t n_items = gy * n_qb;
       PDM_CHECK_ARG(n_items < (int64_t(1) << 31), "batch * heads * query blocks must be < 2^31");
