@@ -1460,6 +1460,61 @@ constexpr int kAttnLdsMaxKeys = 608;
 // piece p at position p ^ ((m >> 1) & 7)) and V^T rows at sV (row d, piece pv of keys 8 pv .. at position
 // pv ^ ((d >> 2) & 3)).  S^T = K Q^T per 32-key tile, online softmax in fp32, O^T += V^T P^T with P^T in
 // registers; qf holds the tile's Q fragments; writes the tile's O rows (bf16) at o + qi * D.
+// Softmax step of one 32-key tile: s holds the lane's 16 scores of its query (-inf where masked), m the
+// running shift of the exponentials (log2 units, shared by the two lanes of a query), l the lane's share of
+// the denominator, o the O^T accumulators.  The exponentials p = 2^(s * scale_log2 - m) go to pk as bf16
+// pairs and their sum is returned; the normalised output does not depend on the shift.
+//  LAZY = false: the tile's maximum first (16 values and the other half-wave's), m raised when it exceeds
+//    m + 8, so every exponential is <= 2^8.
+//  LAZY = true: the exponentials first; m is raised only when some lane's sum exceeds 2^16 or is not a
+//    number (the first tile, where m = -inf), and then O and l are rescaled and the exponentials recomputed.
+//    Every kept exponential is <= 2^16, and a tile with no new maximum costs no max reduction, at the cost
+//    of the scores staying live until the check (about 14 more registers).
+template <bool LAZY>
+__device__ __forceinline__ float attn_tile_softmax(const f32x16_t& s, float scale_log2, float& m, float& l,
+                                                   f32x16_t (&o)[2], uint32_t (&pk)[8]) {
+  auto expo = [&]() {
+    float ps = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 16; e += 2) {
+      const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[e], scale_log2, -m));
+      const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[e + 1], scale_log2, -m));
+      ps += p0 + p1;
+      pk[e >> 1] = pack_bf16x2(p0, p1);
+    }
+    return ps;
+  };
+  auto tile_max = [&]() {
+    float mx = fmaxf(fmaxf(s[0], s[1]), s[2]);
+#pragma unroll
+    for (int e = 3; e < 15; e += 2) mx = fmaxf(fmaxf(mx, s[e]), s[e + 1]);
+    mx = fmaxf(mx, s[15]);
+    {  // max with the other half of the wave (lane l ^ 32 holds the same query)
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+      mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+    }
+    return mx * scale_log2;  // scale_log2 > 0
+  };
+  auto rescale = [&](float mt) {
+    const float m_new = fmaxf(m, mt);
+    const float alpha = __builtin_amdgcn_exp2f(m - m_new);  // 0 on the first tile (m = -inf)
+    m = m_new;
+    l *= alpha;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) { o[0][e] *= alpha; o[1][e] *= alpha; }
+  };
+  if constexpr (LAZY) {
+    const float ps = expo();
+    if (!__builtin_amdgcn_ballot_w64(!(ps <= 0x1p16f))) return ps;
+    rescale(tile_max());
+    return expo();
+  } else {
+    const float mt = tile_max();
+    if (__builtin_amdgcn_ballot_w64(mt > m + 8.0f)) rescale(mt);
+    return expo();
+  }
+}
+
 struct AttnTile {
   const char* sK;
   const char* sV;
@@ -1468,6 +1523,7 @@ struct AttnTile {
   float scale_log2;
 };
 
+template <bool LAZY>
 __device__ __forceinline__ void attn_query_tile(const AttnTile& t, const int qt, const u32x4_t (&qf)[4], int fr,
                                                 int hf) {
   const int qi0 = qt * 32;
@@ -1481,9 +1537,7 @@ __device__ __forceinline__ void attn_query_tile(const AttnTile& t, const int qt,
 #pragma unroll
   for (int e = 0; e < 16; ++e) { o[0][e] = 0.0f; o[1][e] = 0.0f; }
   // m: the shift of the exponentials (log2 units), shared by the two lanes of a query; l: this lane's
-  // share of the softmax denominator.  m is raised only when a score exceeds it by more than 8, so
-  // every exponential stays <= 2^8 and the rescale of O is skipped for most key tiles; the
-  // normalised output does not depend on the shift.
+  // share of the softmax denominator (attn_tile_softmax raises m only when the exponentials grow past 2^16).
   float m = -INFINITY, l = 0.0f;
   // key j0 + 16*(e/8) + hf*8 + e%8 of element e is visible iff 16*(e/8) + e%8 <= lim - j0
   const int lim = min(p_last, t.kv - 1) - hf * 8;
@@ -1528,32 +1582,8 @@ __device__ __forceinline__ void attn_query_tile(const AttnTile& t, const int qt,
 #pragma unroll
       for (int e = 0; e < 16; ++e) s[e] = (16 * (e >> 3) + (e & 7) <= r) ? s[e] : -INFINITY;
     }
-    float mx = fmaxf(fmaxf(s[0], s[1]), s[2]);
-#pragma unroll
-    for (int e = 3; e < 15; e += 2) mx = fmaxf(fmaxf(mx, s[e]), s[e + 1]);
-    mx = fmaxf(mx, s[15]);
-    {  // max with the other half of the wave (lane l ^ 32 holds the same query)
-      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
-      mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
-    }
-    const float mt = mx * t.scale_log2;  // tile max in log2 units (scale_log2 > 0)
-    if (__builtin_amdgcn_ballot_w64(mt > m + 8.0f)) {
-      const float m_new = fmaxf(m, mt);
-      const float alpha = __builtin_amdgcn_exp2f(m - m_new);  // 0 on the first tile (m = -inf)
-      m = m_new;
-      l *= alpha;
-#pragma unroll
-      for (int e = 0; e < 16; ++e) { o[0][e] *= alpha; o[1][e] *= alpha; }
-    }
-    float ps = 0.0f;
     uint32_t pk[8];
-#pragma unroll
-    for (int e = 0; e < 16; e += 2) {
-      const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[e], t.scale_log2, -m));
-      const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[e + 1], t.scale_log2, -m));
-      ps += p0 + p1;
-      pk[e >> 1] = pack_bf16x2(p0, p1);
-    }
+    const float ps = attn_tile_softmax<LAZY>(s, t.scale_log2, m, l, o, pk);  // (rescales l and o first when m rises)
     l += ps;
 #pragma unroll
     for (int c2 = 0; c2 < 2; ++c2) {
@@ -1702,7 +1732,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_lds_kernel(AttnArgs a) {
     const int b = bh / a.H, h = bh - (bh / a.H) * a.H;
     const int next = bh + (int)gridDim.x;
     const AttnTile at{sK, sV, a.o + (int64_t)b * a.q_len * D + h * 64, kvp, a.q_len, a.kv, D, a.scale_log2};
-    auto process_tile = [&](const int qt, const u32x4_t (&qf)[4]) { attn_query_tile(at, qt, qf, fr, hf); };
+    auto process_tile = [&](const int qt, const u32x4_t (&qf)[4]) { attn_query_tile<(NP <= 8)>(at, qt, qf, fr, hf); };
     const int qt0 = tile_of(0), qt1 = tile_of(1);
     if constexpr (kQNext) {
       // this head's first tile was requested during the previous head; then the next head's copy and its
@@ -1860,9 +1890,9 @@ __global__ __launch_bounds__(NW * 64, 16 / NW) void attn_stream_kernel(AttnArgs 
   f32x16_t o[2];
 #pragma unroll
   for (int e = 0; e < 16; ++e) { o[0][e] = 0.0f; o[1][e] = 0.0f; }
-  // m: the shift of the exponentials (log2 units), shared by the two lanes of a query; raised only when a
-  // score exceeds it by more than 8 (the normalised output does not depend on it); l: this lane's share of
-  // the softmax denominator
+  // m: the shift of the exponentials (log2 units), shared by the two lanes of a query, raised by
+  // attn_tile_softmax only when the exponentials grow past 2^16 (the normalised output does not depend on
+  // it); l: this lane's share of the softmax denominator
   float m = -INFINITY, l = 0.0f;
 
   cload(0);
@@ -1896,32 +1926,9 @@ __global__ __launch_bounds__(NW * 64, 16 / NW) void attn_stream_kernel(AttnArgs 
 #pragma unroll
           for (int e = 0; e < 16; ++e) s[e] = (16 * (e >> 3) + (e & 7) <= r) ? s[e] : -INFINITY;
         }
-        float mx = fmaxf(fmaxf(s[0], s[1]), s[2]);
-#pragma unroll
-        for (int e = 3; e < 15; e += 2) mx = fmaxf(fmaxf(mx, s[e]), s[e + 1]);
-        mx = fmaxf(mx, s[15]);
-        {  // max with the other half of the wave (lane l ^ 32 holds the same query)
-          const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
-          mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
-        }
-        const float mt = mx * a.scale_log2;
-        if (__builtin_amdgcn_ballot_w64(mt > m + 8.0f)) {
-          const float m_new = fmaxf(m, mt);
-          const float alpha = __builtin_amdgcn_exp2f(m - m_new);  // 0 on the first tile (m = -inf)
-          m = m_new;
-          l *= alpha;
-#pragma unroll
-          for (int e = 0; e < 16; ++e) { o[0][e] *= alpha; o[1][e] *= alpha; }
-        }
-        float ps = 0.0f;
         uint32_t pk[8];
-#pragma unroll
-        for (int e = 0; e < 16; e += 2) {
-          const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[e], a.scale_log2, -m));
-          const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[e + 1], a.scale_log2, -m));
-          ps += p0 + p1;
-          pk[e >> 1] = pack_bf16x2(p0, p1);
-        }
+        // max first: the lazy form needs about 14 more registers than the 128 of four waves per SIMD
+        const float ps = attn_tile_softmax<false>(s, a.scale_log2, m, l, o, pk);
         l += ps;
         // O^T[d][q] += V^T . P^T; chunk c2 of P^T holds keys j0 + 16*c2 + hf*8 + 0..7
 #pragma unroll
