@@ -1464,8 +1464,8 @@ constexpr int kAttnLdsMaxKeys = 608;
 // running shift of the exponentials (log2 units, shared by the two lanes of a query), l the lane's share of
 // the denominator, o the O^T accumulators.  The exponentials p = 2^(s * scale_log2 - m) go to pk as bf16
 // pairs and their sum is returned; the normalised output does not depend on the shift.
-//  LAZY = false: the tile's maximum first (16 values and the other half-wave's), m raised when it exceeds
-//    m + 8, so every exponential is <= 2^8.
+//  LAZY = false: the tile's maximum first (the lane's 16 values; the other half-wave's only when m rises), m
+//    raised when it exceeds m + 8, so every exponential is <= 2^8.
 //  LAZY = true: the exponentials first; m is raised only when some lane's sum exceeds 2^16 or is not a
 //    number (the first tile, where m = -inf), and then O and l are rescaled and the exponentials recomputed.
 //    Every kept exponential is <= 2^16, and a tile with no new maximum costs no max reduction, at the cost
@@ -1484,16 +1484,15 @@ __device__ __forceinline__ float attn_tile_softmax(const f32x16_t& s, float scal
     }
     return ps;
   };
-  auto tile_max = [&]() {
+  auto lane_max = [&]() {  // the lane's 16 scores
     float mx = fmaxf(fmaxf(s[0], s[1]), s[2]);
 #pragma unroll
     for (int e = 3; e < 15; e += 2) mx = fmaxf(fmaxf(mx, s[e]), s[e + 1]);
-    mx = fmaxf(mx, s[15]);
-    {  // max with the other half of the wave (lane l ^ 32 holds the same query)
-      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
-      mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
-    }
-    return mx * scale_log2;  // scale_log2 > 0
+    return fmaxf(mx, s[15]);
+  };
+  auto query_max = [](float mx) {  // with the other half of the wave (lane l ^ 32 holds the same query)
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+    return fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
   };
   auto rescale = [&](float mt) {
     const float m_new = fmaxf(m, mt);
@@ -1503,14 +1502,17 @@ __device__ __forceinline__ float attn_tile_softmax(const f32x16_t& s, float scal
 #pragma unroll
     for (int e = 0; e < 16; ++e) { o[0][e] *= alpha; o[1][e] *= alpha; }
   };
+  // (scale_log2 > 0: the maximum of the scaled scores is the scaled maximum)
   if constexpr (LAZY) {
     const float ps = expo();
     if (!__builtin_amdgcn_ballot_w64(!(ps <= 0x1p16f))) return ps;
-    rescale(tile_max());
+    rescale(query_max(lane_max()) * scale_log2);
     return expo();
   } else {
-    const float mt = tile_max();
-    if (__builtin_amdgcn_ballot_w64(mt > m + 8.0f)) rescale(mt);
+    // a query's maximum exceeds m + 8 exactly when one of its two lanes' does, so the exchange between the
+    // half-waves is needed only when m rises
+    const float mx = lane_max();
+    if (__builtin_amdgcn_ballot_w64(mx * scale_log2 > m + 8.0f)) rescale(query_max(mx) * scale_log2);
     return expo();
   }
 }
